@@ -1,0 +1,63 @@
+/*
+ * hive_oracle.h -- C-ABI of the CPU oracle.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This library is the checker for the HIP
+ * product path: only tests/, __graft_entry__.smoke() and bench.py's
+ * cpu_baseline leg load it.  Nothing in hive_neuralnet_amd/ links or calls it.
+ *
+ * Byte formats are the reference's wire formats:
+ *   state : 3424 bytes, HiveState layout (hive_gpu/csrc/hive_state.cuh:239-269)
+ *   move  : 6 bytes {u8 type, u8 piece_type, u16 from, u16 to} little-endian
+ *           (hive_gpu/csrc/hive_state.cuh:228-233)
+ */
+#ifndef HIVE_ORACLE_H
+#define HIVE_ORACLE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define OR_STATE_BYTES 3424
+#define OR_MOVE_BYTES 6
+#define OR_MAX_LEGAL 256
+#define OR_FEAT_DIM 122
+
+int or_state_bytes(void);
+
+/* single-state primitives */
+void or_init_state(uint8_t* state, int expansion_mask);
+void or_apply_move(uint8_t* state, const uint8_t* move6);
+int or_legal_moves(const uint8_t* state, uint8_t* moves_out /* 256*6, fully written */);
+int or_fnn_feature_moves(const uint8_t* state, uint8_t* moves_out /* 256*6 */);
+void or_fnn_features(const uint8_t* state, const uint8_t* moves, int n, float* feat_out);
+void or_articulation(const uint8_t* state, uint64_t* ap_out /* 9 words */);
+void or_centroid(const uint8_t* state, int* cq, int* cr);
+int or_move_to_action(const uint8_t* move6, int cq, int cr);
+int or_queen_escape(const uint8_t* state);
+void or_neighbor_table(int16_t* out /* 529*6 */);
+
+/* batched helpers (threads <= 0 means 1) */
+void or_batch_legal_features_actions(const uint8_t* states, int64_t B,
+                                     uint8_t* moves_out, int32_t* n_out,
+                                     float* feat_out, int32_t* act_out,
+                                     int threads);
+void or_batch_successor_features(const uint8_t* states, const uint8_t* legal,
+                                 const int64_t* action_to_root,
+                                 const int64_t* move_indices, int64_t N,
+                                 float* feat_out, int full_list, int threads);
+void or_batch_queen_escape(const uint8_t* states, int64_t B, uint8_t* out, int threads);
+
+/* Philox4x32-10 and the seeded random-play position generator */
+void or_philox4x32_10(uint32_t key0, uint32_t key1, const uint32_t ctr[4], uint32_t out[4]);
+void or_generate_positions(int64_t B, int expansion_mask, int max_ply, uint32_t seed,
+                           uint8_t* states_out, int32_t* plies_out, int threads);
+void or_lockstep_selfplay(int64_t G, int expansion_mask, int max_ply, uint32_t seed,
+                          uint8_t* states_out, int32_t* plies_out, int threads);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif
