@@ -1,0 +1,343 @@
+// hive_engine.hip -- HIP kernels and the C-ABI of the batched Hive engine.
+//
+// Launch model: the per-position kernels run one 64-lane wavefront per
+// position (workgroup = one wave, LDS board from hive_wave.hpp); the
+// byte-level state kernels (init / apply / result) run one lane per state or
+// per 16-byte chunk.  Every entry point takes device pointers, sizes and the
+// caller's hipStream_t and returns a hipError_t code; nothing allocates.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/hive_gpu.h"
+#include "hive_phases.hpp"
+
+using namespace hw;
+
+namespace {
+
+// ---------------------------------------------------------------- state bytes
+// init_state (hive_state.cuh:454-492) over a zero row: every byte of the
+// row is written, one 16-byte chunk per lane.
+__global__ void k_init_states(uint4* __restrict__ states, int64_t chunks, int mask) {
+    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= chunks) return;
+    int k = (int)(i % (kStateBytes / 16));
+    uint4 v = make_uint4(0, 0, 0, 0);
+    if (k == OFF_QUEEN / 16) {  // bytes 3392..3407: queen cells, hands
+        uint32_t x = (mask & 1) ? 1u : 0u, l = (mask & 2) ? 1u : 0u, p = (mask & 4) ? 1u : 0u;
+        uint32_t hand_lo = 1u | (3u << 8) | (3u << 16) | (2u << 24);  // Q A G S
+        uint32_t hand_hi = 2u | (x << 8) | (l << 16) | (p << 24);      // B M L P
+        v = make_uint4(0xFFFFFFFFu, hand_lo, hand_hi, hand_lo);
+    } else if (k == OFF_QUEEN / 16 + 1) {  // bytes 3408..3423
+        uint32_t x = (mask & 1) ? 1u : 0u, l = (mask & 2) ? 1u : 0u, p = (mask & 4) ? 1u : 0u;
+        uint32_t hand_hi = 2u | (x << 8) | (l << 16) | (p << 24);
+        v = make_uint4(hand_hi, 0u /*turn, qplaced, result*/, 0xFFFFu /*stun; centre 0*/, 0u);
+    }
+    states[i] = v;
+}
+
+// Byte-level apply_move (hive_state.cuh:326-517) on a state row in global
+// memory.  One lane per state.
+struct RowView {
+    uint8_t* s;
+    __device__ uint8_t& stack(int lv, int c) { return s[lv * kCells + c]; }
+    __device__ uint8_t& h(int c) { return s[OFF_HEIGHT + c]; }
+    __device__ uint64_t* bb(int off) { return reinterpret_cast<uint64_t*>(s + off); }
+    __device__ void set(int off, int c) { bb(off)[c >> 6] |= 1ull << (c & 63); }
+    __device__ void clr(int off, int c) { bb(off)[c >> 6] &= ~(1ull << (c & 63)); }
+    __device__ bool get(int off, int c) { return (bb(off)[c >> 6] >> (c & 63)) & 1ull; }
+    __device__ uint16_t& u16(int off) { return *reinterpret_cast<uint16_t*>(s + off); }
+    __device__ void top_colour(int c, int col) {
+        if (col) { set(OFF_BTOP, c); clr(OFF_WTOP, c); }
+        else { set(OFF_WTOP, c); clr(OFF_BTOP, c); }
+    }
+    __device__ bool ringed(int col) {
+        if (!((s[OFF_QPLACED] >> col) & 1)) return false;
+        int q = u16(OFF_QUEEN + 2 * col);
+        if (q >= kCells) return false;
+        uint32_t g = grid6(q);
+        int k = 0;
+        for (int d = 0; d < 6; d++)
+            if (((g >> d) & 1u) && get(OFF_OCC, step(q, d))) k++;
+        return k == 6;
+    }
+    __device__ void apply(int type, int pt, int from, int to) {
+        int me = u16(OFF_TURN) & 1;
+        if (type == MV_PLACE) {
+            if (to < kCells && pt >= PT_Q && pt <= PT_P && h(to) < 5) {
+                int hh = h(to);
+                stack(hh, to) = (uint8_t)(pt | (me << 4));
+                h(to) = (uint8_t)(hh + 1);
+                if (hh == 0) set(OFF_OCC, to);
+                top_colour(to, me);
+                if (pt == PT_Q) {
+                    u16(OFF_QUEEN + 2 * me) = (uint16_t)to;
+                    s[OFF_QPLACED] |= (uint8_t)(1 << me);
+                }
+                s[OFF_HANDS + me * 8 + pt - 1] -= 1;
+            }
+            u16(OFF_STUN) = 0xFFFF;
+        } else if (type == MV_MOVE) {
+            if (from < kCells && to < kCells) {
+                if (h(from) > 0 && h(from) <= 5 && h(to) < 5) {  // heights above 5 never occur
+                    int hf = h(from);
+                    uint8_t b = stack(hf - 1, from);
+                    stack(hf - 1, from) = 0;
+                    h(from) = (uint8_t)(hf - 1);
+                    if (hf == 1) {
+                        clr(OFF_OCC, from); clr(OFF_WTOP, from); clr(OFF_BTOP, from);
+                    } else {
+                        top_colour(from, (stack(hf - 2, from) >> 4) & 1);
+                    }
+                    int ht = h(to);
+                    stack(ht, to) = b;
+                    h(to) = (uint8_t)(ht + 1);
+                    if (ht == 0) set(OFF_OCC, to);
+                    top_colour(to, (b >> 4) & 1);
+                    if ((b & 15) == PT_Q) u16(OFF_QUEEN + 2 * ((b >> 4) & 1)) = (uint16_t)to;
+                }
+                u16(OFF_STUN) = (uint16_t)to;
+            }
+        } else {
+            u16(OFF_STUN) = 0xFFFF;
+        }
+        u16(OFF_TURN) = (uint16_t)(u16(OFF_TURN) + 1);
+        bool w = ringed(0), k = ringed(1);
+        if (w && k) s[OFF_RESULT] = 3;
+        else if (w) s[OFF_RESULT] = 2;
+        else if (k) s[OFF_RESULT] = 1;
+    }
+};
+
+__global__ void k_apply_moves(uint8_t* __restrict__ states, const uint8_t* __restrict__ moves, int64_t B) {
+    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= B) return;
+    const uint8_t* m = moves + 6 * i;
+    RowView v{states + i * kStateBytes};
+    v.apply(m[0], m[1], m[2] | (m[3] << 8), m[4] | (m[5] << 8));
+}
+
+__global__ void k_check_results(const uint8_t* __restrict__ states, int64_t B, int32_t* __restrict__ out) {
+    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < B) out[i] = states[i * kStateBytes + OFF_RESULT];
+}
+
+// ---------------------------------------------------------------- positions
+template <bool WithMoves, bool WithFeat, bool WithAct>
+__global__ __launch_bounds__(64) void k_legal(const uint8_t* __restrict__ states, int64_t B,
+                                              uint8_t* __restrict__ moves_out, int32_t* __restrict__ n_out,
+                                              float* __restrict__ feat_out, int32_t* __restrict__ act_out) {
+    __shared__ Pos P;
+    const int64_t pos = blockIdx.x;
+    if (pos >= B) return;
+    run_legal<WithMoves, WithFeat, WithAct>(P, states + pos * kStateBytes, threadIdx.x,
+                                   WithMoves ? moves_out + pos * (kMaxLegal * 6) : nullptr, n_out + pos,
+                                   WithFeat ? feat_out + pos * kFeat : nullptr, WithAct ? act_out + pos * kMaxLegal : nullptr);
+}
+
+__global__ __launch_bounds__(64) void k_extract_features(const uint8_t* __restrict__ states,
+                                                         const uint8_t* __restrict__ moves,
+                                                         const int32_t* __restrict__ num_legal, int64_t B,
+                                                         float* __restrict__ feat_out) {
+    __shared__ Pos P;
+    const int64_t pos = blockIdx.x;
+    if (pos >= B) return;
+    run_extract(P, states + pos * kStateBytes, moves + pos * (kMaxLegal * 6), num_legal[pos], threadIdx.x,
+                feat_out + pos * kFeat);
+}
+
+// legal_moves_to_actions_kernel (game_logic.cu:811-835) / compute_centroids_kernel
+// (state_encoder.cuh:982-996): one wave per position, centroid over the occupied cells.
+__global__ __launch_bounds__(64) void k_actions(const uint8_t* __restrict__ states,
+                                                const uint8_t* __restrict__ moves,
+                                                const int32_t* __restrict__ num_legal, int64_t B,
+                                                int32_t* __restrict__ act_out, int32_t* __restrict__ centroid_out) {
+    __shared__ Pos P;
+    const int lane = threadIdx.x;
+    const int64_t pos = blockIdx.x;
+    if (pos >= B) return;
+    const uint8_t* S = states + pos * kStateBytes;
+    const uint32_t* W = reinterpret_cast<const uint32_t*>(S + OFF_OCC);
+    if (lane < 18) P.occ[lane + 1] = W[lane];
+    int n = 0;
+    if (act_out) n = stage_moves(P, moves + pos * (kMaxLegal * 6), num_legal[pos], lane);
+    __syncthreads();
+    build_occ_list(P, lane);
+    __syncthreads();
+    int cq, cr;
+    centroid(P, lane, cq, cr);
+    if (centroid_out && lane == 0) {
+        centroid_out[2 * pos] = cq;
+        centroid_out[2 * pos + 1] = cr;
+    }
+    if (act_out) store_actions(P, n, cq, cr, act_out + pos * kMaxLegal, lane);
+}
+
+// fnn_successor_features_kernel (game_logic.cu:182-229): one wave per (root, move).
+__global__ __launch_bounds__(64) void k_successor_features(const uint8_t* __restrict__ states,
+                                                           const uint8_t* __restrict__ legal,
+                                                           const int64_t* __restrict__ a2r,
+                                                           const int64_t* __restrict__ midx, int64_t N,
+                                                           int64_t num_roots, float* __restrict__ feat_out) {
+    __shared__ Pos P;
+    const int lane = threadIdx.x;
+    const int64_t i = blockIdx.x;
+    if (i >= N) return;
+    const int64_t root = a2r[i];
+    const int64_t mi = midx[i];
+    if (root < 0 || root >= num_roots || mi < 0 || mi >= kMaxLegal) {  // out-of-range rows: zero features
+        for (int k = lane; k < kFeat; k += 64) feat_out[i * kFeat + k] = 0.0f;
+        return;
+    }
+    run_successor(P, states + root * kStateBytes, legal + (root * kMaxLegal + mi) * 6, lane, feat_out + i * kFeat);
+}
+
+__global__ __launch_bounds__(64) void k_queen_escape(const uint8_t* __restrict__ states, int64_t B,
+                                                     uint8_t* __restrict__ out) {
+    __shared__ Pos P;
+    const int64_t pos = blockIdx.x;
+    if (pos >= B) return;
+    bool esc = run_queen_escape(P, states + pos * kStateBytes, threadIdx.x);
+    if (threadIdx.x == 0) out[pos] = esc ? 1 : 0;
+}
+
+// Philox4x32-10 (Salmon et al., SC'11), first output word.
+__device__ __forceinline__ uint32_t philox_word0(uint32_t k0, uint32_t k1, uint32_t c0, uint32_t c1) {
+    uint32_t x0 = c0, x1 = c1, x2 = 0, x3 = 0;
+#pragma unroll
+    for (int r = 0; r < 10; r++) {
+        uint32_t hi0 = __umulhi(0xD2511F53u, x0), lo0 = 0xD2511F53u * x0;
+        uint32_t hi1 = __umulhi(0xCD9E8D57u, x2), lo1 = 0xCD9E8D57u * x2;
+        uint32_t y0 = hi1 ^ x1 ^ k0, y2 = hi0 ^ x3 ^ k1;
+        x0 = y0; x1 = lo1; x2 = y2; x3 = lo0;
+        k0 += 0x9E3779B9u;
+        k1 += 0xBB67AE85u;
+    }
+    return x0;
+}
+
+// One ply of seeded random play: game i is active while ply < its target
+// (philox(seed, (i,0))[0] mod (max_ply+1), or max_ply in lockstep mode) and
+// its result is 0; an active game applies legal[(philox(seed,(i,ply+1))[0] *
+// n) >> 32].  plies_done[i] counts applied plies.
+__global__ void k_random_play_step(uint8_t* __restrict__ states, const uint8_t* __restrict__ moves,
+                                   const int32_t* __restrict__ num_legal, int64_t B, int ply, int max_ply,
+                                   int lockstep, uint32_t seed, int32_t* __restrict__ plies_done) {
+    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= B) return;
+    uint8_t* s = states + i * kStateBytes;
+    int target = lockstep ? max_ply : (int)(philox_word0(seed, 0, (uint32_t)i, 0) % (uint32_t)(max_ply + 1));
+    if (ply >= target || s[OFF_RESULT] != 0) return;
+    int n = num_legal[i];
+    uint32_t u = philox_word0(seed, 0, (uint32_t)i, (uint32_t)(ply + 1));
+    int pick = (int)(((uint64_t)u * (uint64_t)n) >> 32);
+    const uint8_t* m = moves + (i * kMaxLegal + pick) * 6;
+    RowView v{s};
+    v.apply(m[0], m[1], m[2] | (m[3] << 8), m[4] | (m[5] << 8));
+    if (plies_done) plies_done[i] += 1;
+}
+
+inline int grid_for(int64_t n, int block) { return (int)((n + block - 1) / block); }
+
+inline int finish() { return (int)hipGetLastError(); }
+
+}  // namespace
+
+// ============================================================== C-ABI
+extern "C" {
+
+int hg_abi_version(void) { return HG_ABI_VERSION; }
+
+int hg_initialize_tables(void) { return 0; }
+
+int hg_create_initial_states(uint8_t* states, int64_t B, int expansion_mask, void* stream) {
+    if (B <= 0) return 0;
+    int64_t chunks = B * (kStateBytes / 16);
+    hipLaunchKernelGGL(k_init_states, dim3(grid_for(chunks, 256)), dim3(256), 0, (hipStream_t)stream,
+                       reinterpret_cast<uint4*>(states), chunks, expansion_mask);
+    return finish();
+}
+
+int hg_apply_moves(uint8_t* states, const uint8_t* moves, int64_t B, void* stream) {
+    if (B <= 0) return 0;
+    hipLaunchKernelGGL(k_apply_moves, dim3(grid_for(B, 256)), dim3(256), 0, (hipStream_t)stream, states, moves, B);
+    return finish();
+}
+
+int hg_check_results(const uint8_t* states, int64_t B, int32_t* results, void* stream) {
+    if (B <= 0) return 0;
+    hipLaunchKernelGGL(k_check_results, dim3(grid_for(B, 256)), dim3(256), 0, (hipStream_t)stream, states, B,
+                       results);
+    return finish();
+}
+
+int hg_generate_legal_moves(const uint8_t* states, int64_t B, uint8_t* moves, int32_t* num_legal, void* stream) {
+    if (B <= 0) return 0;
+    hipLaunchKernelGGL((k_legal<true, false, false>), dim3((unsigned)B), dim3(64), 0, (hipStream_t)stream, states, B,
+                       moves, num_legal, nullptr, nullptr);
+    return finish();
+}
+
+int hg_generate_legal_moves_and_fnn_features(const uint8_t* states, int64_t B, uint8_t* moves,
+                                             int32_t* num_legal, float* features, void* stream) {
+    if (B <= 0) return 0;
+    hipLaunchKernelGGL((k_legal<true, true, false>), dim3((unsigned)B), dim3(64), 0, (hipStream_t)stream, states, B,
+                       moves, num_legal, features, nullptr);
+    return finish();
+}
+
+int hg_legal_features_actions(const uint8_t* states, int64_t B, uint8_t* moves, int32_t* num_legal,
+                              float* features, int32_t* actions, void* stream) {
+    if (B <= 0) return 0;
+    hipLaunchKernelGGL((k_legal<true, true, true>), dim3((unsigned)B), dim3(64), 0, (hipStream_t)stream, states, B,
+                       moves, num_legal, features, actions);
+    return finish();
+}
+
+int hg_extract_fnn_features(const uint8_t* states, const uint8_t* moves, const int32_t* num_legal, int64_t B,
+                            float* features, void* stream) {
+    if (B <= 0) return 0;
+    hipLaunchKernelGGL(k_extract_features, dim3((unsigned)B), dim3(64), 0, (hipStream_t)stream, states, moves,
+                       num_legal, B, features);
+    return finish();
+}
+
+int hg_legal_moves_to_actions(const uint8_t* states, const uint8_t* moves, const int32_t* num_legal, int64_t B,
+                              int32_t* actions, void* stream) {
+    if (B <= 0) return 0;
+    hipLaunchKernelGGL(k_actions, dim3((unsigned)B), dim3(64), 0, (hipStream_t)stream, states, moves, num_legal, B,
+                       actions, (int32_t*)nullptr);
+    return finish();
+}
+
+int hg_compute_centroids(const uint8_t* states, int64_t B, int32_t* centroids, void* stream) {
+    if (B <= 0) return 0;
+    hipLaunchKernelGGL(k_actions, dim3((unsigned)B), dim3(64), 0, (hipStream_t)stream, states,
+                       (const uint8_t*)nullptr, (const int32_t*)nullptr, B, (int32_t*)nullptr, centroids);
+    return finish();
+}
+
+int hg_fnn_successor_features(const uint8_t* states, const uint8_t* legal_moves, int64_t num_roots,
+                              const int64_t* action_to_root, const int64_t* move_indices, int64_t N, float* features,
+                              void* stream) {
+    if (N <= 0) return 0;
+    hipLaunchKernelGGL(k_successor_features, dim3((unsigned)N), dim3(64), 0, (hipStream_t)stream, states,
+                       legal_moves, action_to_root, move_indices, N, num_roots, features);
+    return finish();
+}
+
+int hg_queen_escape_flags(const uint8_t* states, int64_t B, uint8_t* flags, void* stream) {
+    if (B <= 0) return 0;
+    hipLaunchKernelGGL(k_queen_escape, dim3((unsigned)B), dim3(64), 0, (hipStream_t)stream, states, B, flags);
+    return finish();
+}
+
+int hg_random_play_step(uint8_t* states, const uint8_t* moves, const int32_t* num_legal, int64_t B, int ply,
+                        int max_ply, int lockstep, uint32_t seed, int32_t* plies_done, void* stream) {
+    if (B <= 0) return 0;
+    hipLaunchKernelGGL(k_random_play_step, dim3(grid_for(B, 256)), dim3(256), 0, (hipStream_t)stream, states, moves,
+                       num_legal, B, ply, max_ply, lockstep, seed, plies_done);
+    return finish();
+}
+
+}  // extern "C"

@@ -1,0 +1,739 @@
+// hive_phases.hpp -- the per-position phases built on hive_wave.hpp:
+// legal-list generation and assembly, FNN features, action indices,
+// compact successor summaries and move application on the LDS board.
+#pragma once
+
+#include "hive_wave.hpp"
+
+namespace hw {
+
+// ---------------------------------------------------------------- legal list
+// generate_legal_moves (move_gen.cuh:1151-1360): placements (cells ascending
+// x placeable types), then moves of each own top piece that is neither
+// stunned nor pinned (cells ascending, type-specific order), then pillbug
+// throws (own top pillbugs, then own ground mosquitoes touching a top
+// pillbug, in cell order), cut at 256; a lone PASS when empty; nothing when
+// the game is over.  The list is staged in P.mv; returns its length.
+__device__ inline int generate_legal(Pos& P, int lane) {
+    if (P.result != 0) {
+        for (int i = lane; i < kMaxLegal; i += 64) P.mv[i][0] = P.mv[i][1] = P.mv[i][2] = 0;
+        return 0;
+    }
+    const int me = P.turn & 1;
+    const int ptn = P.turn >> 1;
+    const bool queen_down = (P.qplaced >> me) & 1;
+    const bool queen_now = (ptn == 3) && !queen_down;
+    uint32_t placeable = 0;
+    for (int p = 0; p < 8; p++) {
+        bool ok = queen_now ? (p == 0 && P.hand[me][0] > 0) : (P.hand[me][p] > 0);
+        if (ok) placeable |= 1u << p;
+    }
+    uint32_t emit_types = placeable & ~(ptn == 0 ? 1u : 0u);
+    int ntypes = __popc(emit_types);
+
+    // -- placement cells, lane w < 18 owns board word w
+    uint32_t pw = 0;
+    if (placeable && lane < 18) {
+        if (P.turn == 0) {
+            pw = (lane == (264 >> 5)) ? (1u << (264 & 31)) : 0u;
+        } else if (P.turn == 1) {
+            pw = nbr_union_word(P.occ, lane) & ~P.occ[lane + 1];
+        } else {
+            const uint32_t* mine = me ? P.bt : P.wt;
+            const uint32_t* theirs = me ? P.wt : P.bt;
+            pw = nbr_union_word(mine, lane) & ~nbr_union_word(theirs, lane) & ~P.occ[lane + 1];
+        }
+    }
+    int prank = wave_excl_scan(__popc(pw), lane);
+    int npos = wave_sum(__popc(pw));
+    int n_place = npos * ntypes;
+
+    // -- movable pieces: own top cells, not stunned, not pinned (cell order)
+    int n_pieces = 0, n_actors = 0;
+    if (queen_down) {
+        uint32_t mw = 0;
+        if (lane < 18) {
+            const uint32_t* mine = me ? P.bt : P.wt;
+            mw = mine[lane + 1] & ~P.pin[lane + 1];
+            if (P.stun != 0xFFFF && (P.stun >> 5) == lane) mw &= ~(1u << (P.stun & 31));
+        }
+        int k = wave_excl_scan(__popc(mw), lane);
+        n_pieces = min(wave_sum(__popc(mw)), kMaxPieces);
+        while (mw) {
+            int b = __ffs(mw) - 1;
+            mw &= mw - 1;
+            if (k < kMaxPieces) {
+                int c = lane * 32 + b;
+                P.piece_cell[k] = (uint16_t)c;
+                P.piece_type[k] = P.top[c] & 15;
+            }
+            k++;
+        }
+        // throw actors among occupied cells (cell order); the thrower is not
+        // checked for stun or pin (move_gen.cuh:1304-1345)
+        bool actor = false;
+        if (lane < P.n_occ) {
+            int c = P.occ_cells[lane];
+            int tb = P.top[c];
+            int t = tb & 15;
+            if (((tb >> 4) & 1) == me)
+                actor = (t == PT_P) || (t == PT_M && P.h[c] == 1 && touches_top_pillbug(P, c));
+        }
+        uint64_t am = __ballot(actor);
+        n_actors = min(__popcll(am), kActors);
+        if (actor) {
+            int r = __popcll(am & ((1ull << lane) - 1));
+            if (r < kActors) P.actor_cell[r] = P.occ_cells[lane];
+        }
+    }
+    __syncthreads();
+
+    // -- destination pool offsets by type capacity
+    int cap = lane < n_pieces ? type_capacity(P.piece_type[lane]) : 0;
+    int off = wave_excl_scan(cap, lane);
+    if (lane < n_pieces && off + cap > kPool) {  // only reachable for states with impossible piece counts
+        P.piece_off[lane] = 0;
+        P.piece_cnt[lane] = 0;
+    } else if (lane < n_pieces) {
+        int c = P.piece_cell[lane];
+        int t = P.piece_type[lane];
+        uint16_t* out = P.pool + off;
+        uint32_t* s0 = P.u.lane_bb[lane][0];
+        uint32_t* s1 = P.u.lane_bb[lane][1];
+        int m = 0;
+        switch (t) {
+            case PT_Q: case PT_P: m = gen_step(P, c, out); break;
+            case PT_A: m = gen_ant(P, c, out, 168, s0); break;
+            case PT_G: m = gen_hopper(P, c, out); break;
+            case PT_S: m = gen_spider(P, c, out, s0); break;
+            case PT_B: m = gen_beetle(P, c, out); break;
+            case PT_M: m = gen_mosquito(P, c, out, s0, s1); break;
+            case PT_L: m = gen_ladybug(P, c, out, s0); break;
+            default: break;
+        }
+        P.piece_off[lane] = (uint16_t)off;
+        P.piece_cnt[lane] = (uint16_t)m;
+    } else if (lane >= 32 && lane - 32 < n_actors) {
+        int j = lane - 32;
+        P.throw_cnt[j] = (uint16_t)gen_throws(P, P.actor_cell[j], P.throw_from[j], P.throw_to[j], P.throw_pt[j]);
+    }
+    __syncthreads();
+
+    // -- assembly: slot 0 placements, slots 1..n_pieces pieces, then actors
+    int cnt = 0;
+    if (lane == 0) cnt = n_place;
+    else if (lane <= n_pieces) cnt = P.piece_cnt[lane - 1];
+    else if (lane <= n_pieces + n_actors) cnt = P.throw_cnt[lane - 1 - n_pieces];
+    int base = wave_excl_scan(cnt, lane);
+    int total = wave_sum(cnt);
+    int n = total < kMaxLegal ? total : kMaxLegal;
+
+    // placements: lane w < 18 emits its cells x emit types
+    if (lane < 18 && pw) {
+        int r = prank;
+        uint32_t w = pw;
+        while (w) {
+            int b = __ffs(w) - 1;
+            w &= w - 1;
+            int c = lane * 32 + b;
+            int slot = r * ntypes;
+            uint32_t ty = emit_types;
+            while (ty) {
+                int p = __ffs(ty) - 1;
+                ty &= ty - 1;
+                if (slot < kMaxLegal) {
+                    P.mv[slot][0] = (uint16_t)(MV_PLACE | ((p + 1) << 8));
+                    P.mv[slot][1] = 0;
+                    P.mv[slot][2] = (uint16_t)c;
+                }
+                slot++;
+            }
+            r++;
+        }
+    }
+    if (lane >= 1 && lane <= n_pieces) {
+        int i = lane - 1;
+        int c = P.piece_cell[i], t = P.piece_type[i];
+        const uint16_t* src = P.pool + P.piece_off[i];
+        for (int k = 0; k < cnt && base + k < kMaxLegal; k++) {
+            P.mv[base + k][0] = (uint16_t)(MV_MOVE | (t << 8));
+            P.mv[base + k][1] = (uint16_t)c;
+            P.mv[base + k][2] = src[k];
+        }
+    } else if (lane > n_pieces && lane <= n_pieces + n_actors) {
+        int j = lane - 1 - n_pieces;
+        for (int k = 0; k < cnt && base + k < kMaxLegal; k++) {
+            P.mv[base + k][0] = (uint16_t)(MV_MOVE | (P.throw_pt[j][k] << 8));
+            P.mv[base + k][1] = P.throw_from[j][k];
+            P.mv[base + k][2] = P.throw_to[j][k];
+        }
+    }
+    if (total == 0) n = 1;  // PASS = all-zero from/to, type 2
+    __syncthreads();
+    for (int i = lane; i < kMaxLegal; i += 64) {
+        if (total == 0 && i == 0) {
+            P.mv[0][0] = MV_PASS;
+            P.mv[0][1] = P.mv[0][2] = 0;
+        } else if (i >= n) {
+            P.mv[i][0] = P.mv[i][1] = P.mv[i][2] = 0;
+        }
+    }
+    return n;
+}
+
+// copy a caller-supplied list (extract / action entry points) into P.mv
+__device__ inline int stage_moves(Pos& P, const uint8_t* __restrict__ M, int n, int lane) {
+    n = n < 0 ? 0 : (n > kMaxLegal ? kMaxLegal : n);
+    for (int i = lane; i < kMaxLegal; i += 64) {
+        if (i < n) {
+            const uint8_t* m = M + 6 * i;
+            P.mv[i][0] = (uint16_t)(m[0] | (m[1] << 8));
+            P.mv[i][1] = (uint16_t)(m[2] | (m[3] << 8));
+            P.mv[i][2] = (uint16_t)(m[4] | (m[5] << 8));
+        } else {
+            P.mv[i][0] = P.mv[i][1] = P.mv[i][2] = 0;
+        }
+    }
+    return n;
+}
+
+// write the staged [256 x 6] list with coalesced dword stores
+__device__ inline void store_moves(const Pos& P, uint8_t* __restrict__ out, int lane) {
+    const uint32_t* src = reinterpret_cast<const uint32_t*>(&P.mv[0][0]);
+    uint32_t* dst = reinterpret_cast<uint32_t*>(out);  // row stride 1536 keeps 16-byte alignment
+    for (int i = lane; i < kMaxLegal * 6 / 4; i += 64) dst[i] = src[i];
+}
+
+// ---------------------------------------------------------------- features
+// extract_fnn_features_device (fnn_features.cuh:68-331).  The legal-move
+// features come either from the staged list P.mv[0..n) (from_list) or, for
+// compact successor lists, from a (type, owner) bucket mask and a placement
+// count.  S is the state row (for the stacked levels under a top piece).
+__device__ inline void fnn_features(Pos& P, const uint8_t* __restrict__ S, int n, float* __restrict__ out,
+                                    int lane, bool from_list = true, uint32_t bucket = 0, int n_place = 0) {
+    auto& F = P.u.f;
+    for (int i = lane; i < 128; i += 64) F.cnt[i] = 0;
+    if (lane < 16) { F.dsum[lane] = 0; F.dcnt[lane] = 0; }
+    if (lane < 2) { F.ring[lane] = 0; F.covered[lane] = 0; F.capable[lane] = 0; }
+    if (lane == 0) F.n_cap = 0;
+    for (int i = lane; i < 16 * 18; i += 64) (&F.from_bb[0][0])[i] = 0;
+    if (lane < 18) F.place_bb[lane] = 0;
+    __syncthreads();
+    const int me = P.turn & 1;
+    if (lane < P.n_occ) {
+        int c = P.occ_cells[lane];
+        int h = P.h[c];
+        int tb = P.top[c];
+        int pt = tb & 15, col = (tb >> 4) & 1, tc = (pt - 1) * 2 + col;
+        if (pt < PT_Q || pt > PT_P) pt = 0;  // impossible top byte: contributes nothing
+        if (pt) atomicAdd(&F.cnt[tc], 1);
+        uint32_t nm = nbr_bits(P.occ, c);
+        if (nm == 0) atomicAdd(&F.cnt[96 + col], 1);
+        uint32_t gm = grid6(c);
+        int oq = P.queen[col ^ 1];
+        if (oq != 0xFFFF && pt) {
+            if (dir_bit_to(c, oq, gm)) atomicAdd(&F.cnt[32 + tc], 1);
+            atomicAdd(&F.dsum[(pt - 1) * 2 + col], hexdist(c, oq));
+            atomicAdd(&F.dcnt[(pt - 1) * 2 + col], 1);
+        }
+        for (int qc = 0; qc < 2; qc++) {
+            int q = P.queen[qc];
+            if (q != 0xFFFF && q < kCells && dir_bit_to(q, c, grid6(q))) atomicAdd(&F.ring[qc], 1);
+        }
+        if (pt && h == 1 && pb_get(P.ap, c)) atomicAdd(&F.cnt[80 + tc], 1);
+        if (pt != PT_Q && h >= 2) {
+            for (int lv = 0; lv < h - 1 && lv < 5; lv++) {
+                int b = S[lv * kCells + c];
+                if ((b & 15) == PT_Q) F.covered[(b >> 4) & 1] = 1;
+            }
+        }
+        bool capable = ((int)P.stun != c) && pt == PT_P;
+        if (!capable && (int)P.stun != c && pt == PT_M && h == 1) {
+            uint32_t m = nm;
+            while (m) {
+                int d = __ffs(m) - 1;
+                m &= m - 1;
+                int nb = step(c, d);
+                if ((int)P.stun == nb) continue;
+                if ((P.top[nb] & 15) == PT_P) { capable = true; break; }
+            }
+        }
+        if (capable) {
+            F.capable[col] = 1;
+            int k = atomicAdd(&F.n_cap, 1);
+            if (k < 8) { F.cap_cells[k] = (uint16_t)c; F.cap_col[k] = (uint8_t)col; }
+        }
+    }
+    // legal-move features: distinct MOVE sources per (type, owner), distinct
+    // PLACE destinations (credited to the side to move)
+    for (int i = lane; from_list && i < n; i += 64) {
+        int ty = P.mv[i][0] & 0xFF, pt = P.mv[i][0] >> 8;
+        if (ty == MV_MOVE) {
+            int fc = P.mv[i][1];
+            if (fc < 544 && pt >= 1 && pt <= 8) {
+                int owner = P.h[fc] > 0 ? (P.top[fc] >> 4) & 1 : me;
+                atomicOr(&F.from_bb[(pt - 1) * 2 + owner][fc >> 5], 1u << (fc & 31));
+            }
+        } else if (ty == MV_PLACE) {
+            int tc = P.mv[i][2];
+            if (tc < 544) atomicOr(&F.place_bb[tc >> 5], 1u << (tc & 31));
+        }
+    }
+    __syncthreads();
+    // pieces next to a pillbug-capable cell (throwable own / threatened)
+    int ncap = F.n_cap < 8 ? F.n_cap : 8;
+    if (lane < ncap) {
+        int p = F.cap_cells[lane], col = F.cap_col[lane];
+        uint32_t m = nbr_bits(P.occ, p);
+        while (m) {
+            int d = __ffs(m) - 1;
+            m &= m - 1;
+            int nb = step(p, d);
+            if ((int)P.stun == nb) continue;
+            int nc = (P.top[nb] >> 4) & 1;
+            if (nc == col) atomicAdd(&F.cnt[106 + col], 1);
+            else atomicAdd(&F.cnt[108 + nc], 1);
+        }
+    }
+    if (!from_list) {
+        if (lane < 16) F.cnt[64 + lane] = (bucket >> lane) & 1u;
+        else if (lane == 16) F.cnt[100] = n_place;
+    } else if (lane < 16) {
+        int s = 0;
+        for (int w = 0; w < 18; w++) s += __popc(F.from_bb[lane][w]);
+        F.cnt[64 + lane] = s;
+    } else if (lane == 16) {
+        int s = 0;
+        for (int w = 0; w < 18; w++) s += __popc(F.place_bb[w]);
+        F.cnt[100] = s;
+    }
+    __syncthreads();
+    constexpr float kPer[8] = {1.f, 3.f, 3.f, 2.f, 2.f, 1.f, 1.f, 1.f};
+    for (int i = lane; i < kFeat; i += 64) {
+        float v;
+        if (i < 16) v = (float)F.cnt[i];
+        else if (i < 32) { int t = (i - 16) >> 1, c = (i - 16) & 1; v = (float)P.hand[c][t] / kPer[t]; }
+        else if (i < 48) v = (float)F.cnt[i];
+        else if (i < 64) { int k = i - 48; v = F.dcnt[k] > 0 ? (float)F.dsum[k] / (float)F.dcnt[k] / 10.0f : 0.0f; }
+        else if (i < 98) v = (float)F.cnt[i];
+        else if (i < 100) v = F.covered[i - 98] ? 1.0f : 0.0f;
+        else if (i < 102) v = (i - 100) == me ? (float)F.cnt[100] / 10.0f : 0.0f;
+        else if (i == 102) { int left = 200 - (int)P.turn; v = (float)(left < 0 ? 0 : left) / 200.0f; }
+        else if (i == 103) { float t = (float)P.turn / 100.0f; v = t < 1.0f ? t : 1.0f; }
+        else if (i < 106) v = F.capable[i - 104] ? 1.0f : 0.0f;
+        else if (i < 110) v = (float)F.cnt[i];
+        else {
+            int qc = (i - 110) / 6, b = (i - 110) % 6;
+            v = (F.ring[qc] == b + 1) ? 1.0f : 0.0f;
+        }
+        out[i] = v;
+    }
+}
+
+// ---------------------------------------------------------------- actions
+// bankers_round_div (state_encoder.cuh:55-79)
+__device__ __forceinline__ int round_half_even_div(int sum, int n) {
+    int q = sum / n, r = sum - q * n;
+    int twice = abs(2 * r);
+    int away = sum > 0 ? q + 1 : q - 1;
+    if (twice > n) return away;
+    if (twice < n) return q;
+    return (q & 1) == 0 ? q : away;
+}
+
+// compute_centroid (state_encoder.cuh:889-906) over the occupied-cell list
+__device__ inline void centroid(const Pos& P, int lane, int& cq, int& cr) {
+    int q = 0, r = 0;
+    if (lane < P.n_occ) {
+        int c = P.occ_cells[lane];
+        int row = c / kGrid;
+        q = c - row * kGrid - kHalf;
+        r = row - kHalf;
+    }
+    int sq = wave_sum(q), sr = wave_sum(r), n = P.n_occ;
+    cq = n ? round_half_even_div(sq, n) : 0;
+    cr = n ? round_half_even_div(sr, n) : 0;
+}
+
+__device__ __forceinline__ int window17(int cell, int cq, int cr) {
+    int row = cell / kGrid;
+    int ec = (cell - row * kGrid - kHalf) - cq + 8, er = (row - kHalf) - cr + 8;
+    return (ec < 0 || ec >= 17 || er < 0 || er >= 17) ? -1 : er * 17 + ec;
+}
+
+// gpu_move_to_action (mcts_tree.cuh:146-179), ENC_GRID = 17 -> 85,834 actions
+__device__ __forceinline__ int move_action(int type, int pt, int from, int to, int cq, int cr) {
+    if (type == MV_PASS) return 85833;
+    if (type == MV_PLACE) {
+        int w = window17(to, cq, cr);
+        return w < 0 ? -1 : (pt - 1) * 289 + w;
+    }
+    int a = window17(from, cq, cr), b = window17(to, cq, cr);
+    return (a < 0 || b < 0) ? -1 : 2312 + a * 289 + b;
+}
+
+__device__ inline void store_actions(const Pos& P, int n, int cq, int cr, int* __restrict__ out, int lane) {
+    for (int i = lane; i < kMaxLegal; i += 64) {
+        int a = -1;
+        if (i < n) a = move_action(P.mv[i][0] & 0xFF, P.mv[i][0] >> 8, P.mv[i][1], P.mv[i][2], cq, cr);
+        out[i] = a;
+    }
+}
+
+
+// ---------------------------------------------------------------- summaries
+// Existence predicates: "the generator for this piece type is non-empty"
+// (the reference's has_*_move helpers, move_gen.cuh:214-1049).
+__device__ inline bool has_hopper(const Pos& P, int c) {
+    uint32_t m = nbr_bits(P.occ, c);
+    while (m) {
+        int d = __ffs(m) - 1;
+        m &= m - 1;
+        int p = step(c, d);
+        bool on = true;
+        while (on && pb_get(P.occ, p)) {
+            if ((grid6(p) >> d) & 1u) p = step(p, d);
+            else on = false;
+        }
+        if (on) return true;
+    }
+    return false;
+}
+
+__device__ inline bool has_spider(const Pos& P, int c) {
+    uint32_t m1 = slide_mask(P, c, c);
+    while (m1) {
+        int d1 = __ffs(m1) - 1;
+        m1 &= m1 - 1;
+        int p1 = step(c, d1);
+        uint32_t m2 = slide_mask(P, p1, c);
+        while (m2) {
+            int d2 = __ffs(m2) - 1;
+            m2 &= m2 - 1;
+            int p2 = step(p1, d2);
+            if (p2 == c) continue;
+            uint32_t m3 = slide_mask(P, p2, c);
+            while (m3) {
+                int d3 = __ffs(m3) - 1;
+                m3 &= m3 - 1;
+                int p3 = step(p2, d3);
+                if (p3 != c && p3 != p1) return true;
+            }
+        }
+    }
+    return false;
+}
+
+__device__ inline bool has_beetle(const Pos& P, int c) {
+    uint32_t gm = grid6(c);
+    uint32_t nh = nbr_heights(P, c, gm);
+    uint32_t sm = slide_mask(P, c, c);
+    int below = P.h[c] - 1;
+    for (int d = 0; d < 6; d++) {
+        if (!((gm >> d) & 1u)) continue;
+        int mh = max(hof(nh, d), below);
+        if (mh > 0) {
+            if (!gate_high(nh, d, mh)) return true;
+        } else if ((sm >> d) & 1u) {
+            return true;
+        }
+    }
+    return false;
+}
+
+__device__ inline bool has_ladybug(const Pos& P, int c) {
+    uint32_t g0 = grid6(c);
+    uint32_t nh0 = nbr_heights(P, c, g0);
+    uint32_t o0 = nbr_bits(P.occ, c);
+    int hc = P.h[c];
+    for (int d1 = 0; d1 < 6; d1++) {
+        if (!((o0 >> d1) & 1u)) continue;
+        int p1 = step(c, d1);
+        if (gate_high(nh0, d1, max(hc - 1, hof(nh0, d1)))) continue;
+        uint32_t nh1 = nbr_heights(P, p1, grid6(p1));
+        uint32_t o1 = nbr_bits(P.occ, p1);
+        int hp1 = P.h[p1];
+        for (int d2 = 0; d2 < 6; d2++) {
+            if (!((o1 >> d2) & 1u)) continue;
+            int p2 = step(p1, d2);
+            if (p2 == c) continue;
+            if (gate_high(nh1, d2, max(hp1, hof(nh1, d2)))) continue;
+            uint32_t g2 = grid6(p2);
+            uint32_t nh2 = nbr_heights(P, p2, g2);
+            uint32_t o2 = nbr_bits(P.occ, p2);
+            int mh3 = P.h[p2];
+            for (int d3 = 0; d3 < 6; d3++) {
+                if (!((g2 >> d3) & 1u) || ((o2 >> d3) & 1u)) continue;
+                int p3 = step(p2, d3);
+                if (p3 == c || p3 == p1) continue;
+                if (!gate_high(nh2, d3, mh3)) return true;
+            }
+        }
+    }
+    return false;
+}
+
+__device__ inline bool piece_has_move(const Pos& P, int c, int t) {
+    switch (t) {
+        case PT_Q: case PT_P: case PT_A: return slide_mask(P, c, c) != 0;
+        case PT_G: return has_hopper(P, c);
+        case PT_S: return has_spider(P, c);
+        case PT_B: return has_beetle(P, c);
+        case PT_L: return has_ladybug(P, c);
+        case PT_M: {
+            if (P.h[c] > 1) return has_beetle(P, c);
+            uint32_t om = nbr_bits(P.occ, c);
+            uint32_t has = 0;
+            while (om) {
+                int d = __ffs(om) - 1;
+                om &= om - 1;
+                int tt = P.top[step(c, d)] & 15;
+                if (tt != PT_M) has |= 1u << tt;
+            }
+            if ((has & ((1u << PT_Q) | (1u << PT_P) | (1u << PT_A))) && slide_mask(P, c, c) != 0) return true;
+            if ((has & (1u << PT_G)) && has_hopper(P, c)) return true;
+            if ((has & (1u << PT_S)) && has_spider(P, c)) return true;
+            if ((has & (1u << PT_B)) && has_beetle(P, c)) return true;
+            if ((has & (1u << PT_L)) && has_ladybug(P, c)) return true;
+            return false;
+        }
+        default: return false;
+    }
+}
+
+// Can the actor at a throw the piece at t (an on-grid neighbour of a)?
+// (has_pillbug_throw_for_target, move_gen.cuh:742-769)
+__device__ inline bool throwable(const Pos& P, int a, int dt) {
+    int t = step(a, dt);
+    if (!pb_get(P.occ, t) || P.h[t] != 1) return false;
+    if (P.stun != 0xFFFF && (int)P.stun == t) return false;
+    if (pb_get(P.pin, t)) return false;
+    int ph = P.h[a];
+    int back = (dt + 3) % 6;
+    uint32_t gt = grid6(t);
+    int lift = max(P.h[t] - 1, ph);
+    int cwh = ((gt >> ((back + 5) % 6)) & 1u) ? P.h[step(t, (back + 5) % 6)] : 0;
+    int ccwh = ((gt >> ((back + 1) % 6)) & 1u) ? P.h[step(t, (back + 1) % 6)] : 0;
+    if (cwh > lift && ccwh > lift) return false;
+    uint32_t ga = grid6(a);
+    uint32_t oa = nbr_bits(P.occ, a);
+    uint32_t nha = nbr_heights(P, a, ga);
+    for (int dd = 0; dd < 6; dd++) {
+        if (!((ga >> dd) & 1u) || dd == dt || ((oa >> dd) & 1u)) continue;
+        if (!gate_high(nha, dd, ph)) return true;
+    }
+    return false;
+}
+
+// What the compact successor list (generate_fnn_feature_moves,
+// move_gen.cuh:1416-1563) contributes to the features: its distinct
+// placement cells and, per (type, owner) bucket, whether any MOVE entry
+// exists (the list keeps one entry per bucket, so can_move is 0 or 1).
+// Returns the bucket mask; *n_place gets the placement-cell count.
+__device__ inline uint32_t compact_summary(Pos& P, int lane, int* n_place) {
+    *n_place = 0;
+    if (P.result != 0) return 0;
+    const int me = P.turn & 1;
+    const int ptn = P.turn >> 1;
+    const bool queen_down = (P.qplaced >> me) & 1;
+    const bool queen_now = (ptn == 3) && !queen_down;
+    bool any = false;
+    for (int p = 0; p < 8; p++) {
+        bool ok = queen_now ? (p == 0 && P.hand[me][0] > 0) : (P.hand[me][p] > 0);
+        if (ptn == 0 && p == 0) ok = false;
+        any = any || ok;
+    }
+    uint32_t pw = 0;
+    if (any && lane < 18) {
+        if (P.turn == 0) {
+            pw = (lane == (264 >> 5)) ? (1u << (264 & 31)) : 0u;
+        } else if (P.turn == 1) {
+            pw = nbr_union_word(P.occ, lane) & ~P.occ[lane + 1];
+        } else {
+            const uint32_t* mine = me ? P.bt : P.wt;
+            const uint32_t* theirs = me ? P.wt : P.bt;
+            pw = nbr_union_word(mine, lane) & ~nbr_union_word(theirs, lane) & ~P.occ[lane + 1];
+        }
+    }
+    int npos = wave_sum(__popc(pw));
+    *n_place = npos;
+    if (!queen_down || npos >= kMaxLegal) return 0;
+    // one lane per occupied cell: own movable pieces and throw actors
+    uint32_t bucket = 0;
+    if (lane < P.n_occ) {
+        int c = P.occ_cells[lane];
+        int tb = P.top[c];
+        int t = tb & 15;
+        if (((tb >> 4) & 1) == me) {
+            bool stunned = P.stun != 0xFFFF && (int)P.stun == c;
+            if (!stunned && !pb_get(P.pin, c) && piece_has_move(P, c, t)) bucket |= 1u << ((t - 1) * 2 + me);
+            bool actor = (t == PT_P) || (t == PT_M && P.h[c] == 1 && touches_top_pillbug(P, c));
+            if (actor) {
+                uint32_t oa = nbr_bits(P.occ, c);
+                while (oa) {
+                    int dt = __ffs(oa) - 1;
+                    oa &= oa - 1;
+                    if (throwable(P, c, dt)) {
+                        int tb2 = P.top[step(c, dt)];
+                        bucket |= 1u << (((tb2 & 15) - 1) * 2 + ((tb2 >> 4) & 1));
+                    }
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) bucket |= __shfl_xor(bucket, o, 64);
+    return bucket;
+}
+
+// has_queen_escape_move (move_gen.cuh:771-821); wave-uniform result
+__device__ inline bool queen_escape(const Pos& P, int lane) {
+    const int me = P.turn & 1;
+    if (!((P.qplaced >> me) & 1)) return false;
+    int q = P.queen[me];
+    if (q >= kCells || !pb_get(P.occ, q)) return false;
+    int tq = P.top[q];
+    bool ok = false;
+    if (lane == 0) {
+        ok = (tq & 15) == PT_Q && ((tq >> 4) & 1) == me && !pb_get(P.pin, q) && slide_mask(P, q, q) != 0;
+    } else if (lane < P.n_occ + 1) {
+        int c = P.occ_cells[lane - 1];
+        int tb = P.top[c];
+        int t = tb & 15;
+        if (((tb >> 4) & 1) == me && ((t == PT_P) || (t == PT_M && P.h[c] == 1 && touches_top_pillbug(P, c)))) {
+            uint32_t bit = dir_bit_to(c, q, grid6(c));
+            if (bit) ok = throwable(P, c, __ffs(bit) - 1);
+        }
+    }
+    return __ballot(ok) != 0;
+}
+
+// ---------------------------------------------------------------- apply
+// apply_move (hive_state.cuh:497-517) on the LDS board, run by one lane.
+// S is the row the LDS board was loaded from; the piece revealed when a
+// stack's top leaves is read from it (levels under the top are unchanged by
+// a single move).
+__device__ inline void pb_set(uint32_t* pb, int c) { pb[(c >> 5) + 1] |= 1u << (c & 31); }
+__device__ inline void pb_clr(uint32_t* pb, int c) { pb[(c >> 5) + 1] &= ~(1u << (c & 31)); }
+
+__device__ inline void set_top_colour(Pos& P, int c, int col) {
+    if (col) { pb_set(P.bt, c); pb_clr(P.wt, c); }
+    else { pb_set(P.wt, c); pb_clr(P.bt, c); }
+}
+
+__device__ inline bool queen_ringed(const Pos& P, int col) {
+    if (!((P.qplaced >> col) & 1)) return false;
+    int q = P.queen[col];
+    if (q >= kCells) return false;
+    return __popc(nbr_bits(P.occ, q)) == 6;
+}
+
+__device__ inline void apply_on_board(Pos& P, const uint8_t* __restrict__ S, int type, int pt, int from, int to) {
+    const int me = P.turn & 1;
+    if (type == MV_PLACE) {
+        if (to < kCells && pt >= PT_Q && pt <= PT_P && P.h[to] < 5) {
+            P.top[to] = (uint8_t)(pt | (me << 4));
+            P.h[to] = P.h[to] + 1;
+            pb_set(P.occ, to);
+            set_top_colour(P, to, me);
+            if (pt == PT_Q) {
+                P.queen[me] = (uint16_t)to;
+                P.qplaced |= (uint8_t)(1 << me);
+            }
+            P.hand[me][pt - 1] = (uint8_t)(P.hand[me][pt - 1] - 1);
+        }
+        P.stun = 0xFFFF;
+    } else if (type == MV_MOVE) {
+        if (from < kCells && to < kCells) {
+            if (P.h[from] > 0 && P.h[from] <= 5 && P.h[to] < 5) {  // heights above 5 never occur
+                int b = P.top[from];
+                int hf = P.h[from] - 1;
+                P.h[from] = (uint8_t)hf;
+                if (hf == 0) {
+                    P.top[from] = 0;
+                    pb_clr(P.occ, from); pb_clr(P.wt, from); pb_clr(P.bt, from);
+                } else {
+                    int under = S[(hf - 1) * kCells + from];
+                    P.top[from] = (uint8_t)under;
+                    set_top_colour(P, from, (under >> 4) & 1);
+                }
+                int ht = P.h[to];
+                P.top[to] = (uint8_t)b;
+                P.h[to] = (uint8_t)(ht + 1);
+                pb_set(P.occ, to);
+                set_top_colour(P, to, (b >> 4) & 1);
+                if ((b & 15) == PT_Q) P.queen[(b >> 4) & 1] = (uint16_t)to;
+            }
+            P.stun = (uint16_t)to;
+        }
+    } else {
+        P.stun = 0xFFFF;
+    }
+    P.turn = (uint16_t)(P.turn + 1);
+    bool w = queen_ringed(P, 0), k = queen_ringed(P, 1);
+    if (w && k) P.result = 3;
+    else if (w) P.result = 2;
+    else if (k) P.result = 1;
+}
+
+// ---------------------------------------------------------------- programs
+// Whole-position programs run by all 64 lanes of a wave; the kernels in
+// hive_engine.hip are thin launch wrappers around them.
+
+__device__ inline void prepare(Pos& P, const uint8_t* __restrict__ S, int lane) {
+    load_position(P, S, lane);
+    __syncthreads();
+    build_occ_list(P, lane);
+    __syncthreads();
+    articulation(P, lane);
+    __syncthreads();
+}
+
+template <bool WithMoves, bool WithFeat, bool WithAct>
+__device__ inline void run_legal(Pos& P, const uint8_t* __restrict__ S, int lane, uint8_t* __restrict__ moves_row,
+                                 int32_t* __restrict__ n_slot, float* __restrict__ feat_row,
+                                 int32_t* __restrict__ act_row) {
+    prepare(P, S, lane);
+    int n = generate_legal(P, lane);
+    __syncthreads();
+    if (WithMoves) store_moves(P, moves_row, lane);
+    if (lane == 0) *n_slot = n;
+    if (WithAct) {
+        int cq, cr;
+        centroid(P, lane, cq, cr);
+        store_actions(P, n, cq, cr, act_row, lane);
+    }
+    if (WithFeat) fnn_features(P, S, n, feat_row, lane);
+}
+
+__device__ inline void run_extract(Pos& P, const uint8_t* __restrict__ S, const uint8_t* __restrict__ M, int nl,
+                                   int lane, float* __restrict__ feat_row) {
+    int n = stage_moves(P, M, nl, lane);
+    prepare(P, S, lane);
+    fnn_features(P, S, n, feat_row, lane);
+}
+
+// fnn_successor_features_kernel (game_logic.cu:182-229) for one (root, move)
+__device__ inline void run_successor(Pos& P, const uint8_t* __restrict__ S, const uint8_t* __restrict__ m, int lane,
+                                     float* __restrict__ feat_row) {
+    load_position(P, S, lane);
+    __syncthreads();
+    if (lane == 0) apply_on_board(P, S, m[0], m[1], m[2] | (m[3] << 8), m[4] | (m[5] << 8));
+    __syncthreads();
+    build_occ_list(P, lane);
+    __syncthreads();
+    articulation(P, lane);
+    __syncthreads();
+    int n_place = 0;
+    uint32_t bucket = compact_summary(P, lane, &n_place);
+    __syncthreads();
+    // stacked levels under a top piece are read from the root row: a single
+    // move leaves every level under a top unchanged
+    fnn_features(P, S, 0, feat_row, lane, false, bucket, n_place);
+}
+
+__device__ inline bool run_queen_escape(Pos& P, const uint8_t* __restrict__ S, int lane) {
+    prepare(P, S, lane);
+    return queen_escape(P, lane);
+}
+}  // namespace hw

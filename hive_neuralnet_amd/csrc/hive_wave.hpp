@@ -1,0 +1,569 @@
+// hive_wave.hpp -- wave-cooperative Hive rules engine for CDNA4 (gfx950).
+//
+// One 64-lane wavefront owns one position.  The board lives in LDS as
+//   * padded 32-bit-word bitboards (occupied / white top / black top /
+//     articulation / pinned / placement): board word w sits at index w+1,
+//     indices 0 and 19 are zero pads so that any cell's 47-bit neighbour
+//     window (cells c-23 .. c+23) is three aligned word reads;
+//   * per-cell height and top-piece bytes.
+// Work is spread over lanes by what is parallel in each phase: board words
+// (placements, list building), occupied cells (articulation points,
+// features), movable pieces (destination generation), legal-list slots
+// (assembly, action indices).
+//
+// Semantics follow the reference engine (chrismejias/hive_neuralnet,
+// hive_gpu/csrc/*.cuh); each routine cites what it reproduces.  Outputs are
+// bit-exact with it for states produced by init/apply (the only states the
+// reference API produces): the occupancy bitboards are taken as consistent
+// with the height array, as apply keeps them.
+#pragma once
+
+#include <stdint.h>
+
+#include "hw_target.hpp"
+
+namespace hw {
+
+constexpr int kCells = 529;
+constexpr int kGrid = 23;
+constexpr int kHalf = 11;
+constexpr int kStateBytes = 3424;
+constexpr int kMaxLegal = 256;
+constexpr int kFeat = 122;
+constexpr int kPW = 20;  // padded words per bitboard
+constexpr int kMaxPieces = 16;
+constexpr int kPool = 840;  // destination pool entries (3 ants + mosquito at 168, rest small)
+constexpr int kActors = 2;  // throw actors of one colour: its pillbug and its mosquito
+constexpr int kThrowCap = 36;
+
+// state byte offsets (hive_gpu/csrc/hive_state.cuh:239-269)
+constexpr int OFF_HEIGHT = 2645, OFF_OCC = 3176, OFF_WTOP = 3248, OFF_BTOP = 3320;
+constexpr int OFF_QUEEN = 3392, OFF_HANDS = 3396, OFF_TURN = 3412, OFF_QPLACED = 3414;
+constexpr int OFF_RESULT = 3415, OFF_STUN = 3416;
+
+enum { PT_Q = 1, PT_A = 2, PT_G = 3, PT_S = 4, PT_B = 5, PT_M = 6, PT_L = 7, PT_P = 8 };
+enum { MV_PLACE = 0, MV_MOVE = 1, MV_PASS = 2 };
+
+// Direction d in E, NE, NW, W, SW, SE order (hex_grid.cuh:32-42).  The cell
+// offset of direction d is OFS(d) - 23 where OFS packs 6-bit fields; OFS(d)
+// is also d's bit position in the 47-bit window starting at cell c-23.
+constexpr uint64_t kOfs = (24ull) | (1ull << 6) | (0ull << 12) | (22ull << 18) | (45ull << 24) | (46ull << 30);
+__device__ __forceinline__ int win_ofs(int d) { return (int)((kOfs >> (6 * d)) & 63); }
+__device__ __forceinline__ int step(int c, int d) { return c + win_ofs(d) - 23; }
+
+// directions whose neighbour is on the 23x23 grid
+__device__ __forceinline__ uint32_t grid6(int c) {
+    int r = c / kGrid, col = c - r * kGrid;
+    uint32_t m = 0;
+    if (col < 22) m |= 1u;
+    if (col < 22 && r > 0) m |= 2u;
+    if (r > 0) m |= 4u;
+    if (col > 0) m |= 8u;
+    if (col > 0 && r < 22) m |= 16u;
+    if (r < 22) m |= 32u;
+    return m;
+}
+
+__device__ __forceinline__ uint32_t rotl6(uint32_t n) { return ((n << 1) | (n >> 5)) & 63u; }
+__device__ __forceinline__ uint32_t rotr6(uint32_t n) { return ((n >> 1) | (n << 5)) & 63u; }
+
+__device__ __forceinline__ int pb_get(const uint32_t* pb, int c) { return (int)((pb[(c >> 5) + 1] >> (c & 31)) & 1u); }
+
+// 6-bit mask of directions d whose neighbour is on-grid and set in pb.
+// Bits c-23 .. c+40 are gathered into one 64-bit window; direction d sits at
+// window bit win_ofs(d).
+__device__ __forceinline__ uint32_t nbr_bits(const uint32_t* pb, int c) {
+    int lo = c - 23;
+    int wi = (lo >> 5) + 1;
+    int sh = lo & 31;
+    uint64_t w01 = (uint64_t)pb[wi] | ((uint64_t)pb[wi + 1] << 32);
+    uint64_t win = w01 >> sh;
+    if (sh) win |= (uint64_t)pb[wi + 2] << (64 - sh);
+    uint32_t m = (uint32_t)((win >> 24) & 1u) | (uint32_t)(((win >> 1) & 1u) << 1) |
+                 (uint32_t)((win & 1u) << 2) | (uint32_t)(((win >> 22) & 1u) << 3) |
+                 (uint32_t)(((win >> 45) & 1u) << 4) | (uint32_t)(((win >> 46) & 1u) << 5);
+    return m & grid6(c);
+}
+
+// direction bit of g as seen from c (0 when g is not c's on-grid neighbour)
+__device__ __forceinline__ uint32_t dir_bit_to(int c, int g, uint32_t gm) {
+    int diff = g - c;
+    uint32_t b = diff == 1 ? 1u : diff == -22 ? 2u : diff == -23 ? 4u : diff == -1 ? 8u
+               : diff == 22 ? 16u : diff == 23 ? 32u : 0u;
+    return b & gm;
+}
+
+__device__ __forceinline__ int hexdist(int a, int b) {  // fnn_features.cuh:44-61
+    int ra = a / kGrid, rb = b / kGrid;
+    int dq = (b - rb * kGrid) - (a - ra * kGrid), dr = rb - ra, ds = -(dq + dr);
+    int m = abs(dq);
+    m = max(m, abs(dr));
+    return max(m, abs(ds));
+}
+
+struct alignas(16) Pos {
+    uint32_t occ[kPW], wt[kPW], bt[kPW], ap[kPW], pin[kPW], plc[kPW];
+    uint8_t h[544];
+    uint8_t top[544];
+    uint8_t idx_of[544];
+    uint16_t queen[2];
+    uint16_t turn, stun;
+    uint8_t hand[2][8];
+    uint8_t qplaced, result, pad_[2];
+    int n_occ;
+    uint16_t occ_cells[32];
+    uint32_t adj[32];
+    // move generation
+    int n_pieces, n_actors, n_place, n_total;
+    uint16_t piece_cell[kMaxPieces];
+    uint8_t piece_type[kMaxPieces];
+    uint16_t piece_off[kMaxPieces];
+    uint16_t piece_cnt[kMaxPieces];
+    uint16_t actor_cell[kActors];
+    uint16_t throw_cnt[kActors];
+    uint16_t throw_from[kActors][kThrowCap];
+    uint16_t throw_to[kActors][kThrowCap];
+    uint8_t throw_pt[kActors][kThrowCap];
+    uint16_t pool[kPool];
+    union {
+        uint32_t lane_bb[kMaxPieces][2][18];  // lane-private visited / dedup sets
+        struct {
+            int cnt[128];
+            int dsum[16], dcnt[16];
+            int ring[2], covered[2], capable[2];
+            int n_cap;
+            uint16_t cap_cells[8];
+            uint8_t cap_col[8];
+            uint32_t from_bb[16][18];
+            uint32_t place_bb[18];
+        } f;
+    } u;
+    uint16_t mv[kMaxLegal][3];  // staged legal list: {type | pt<<8, from, to}
+};
+
+// ---------------------------------------------------------------- wave utils
+__device__ __forceinline__ int wave_excl_scan(int v, int lane) {
+    int x = v;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        int y = __shfl_up(x, o, 64);
+        if (lane >= o) x += y;
+    }
+    return x - v;
+}
+
+__device__ __forceinline__ int wave_sum(int v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+// ---------------------------------------------------------------- state load
+// Heights, top bytes, bitboards and metadata of the state row S into P.
+__device__ inline void load_position(Pos& P, const uint8_t* __restrict__ S, int lane) {
+    for (int i = lane; i < 544; i += 64) {
+        int hh = i < kCells ? S[OFF_HEIGHT + i] : 0;
+        P.h[i] = (uint8_t)hh;
+        int lvl = hh > 5 ? 5 : hh;
+        P.top[i] = hh ? S[(lvl - 1) * kCells + i] : 0;
+    }
+    const uint32_t* W = reinterpret_cast<const uint32_t*>(S + OFF_OCC);  // 8-byte aligned
+    if (lane < 18) {
+        P.occ[lane + 1] = W[lane];
+        P.wt[lane + 1] = W[18 + lane];
+        P.bt[lane + 1] = W[36 + lane];
+    } else if (lane < 24) {
+        int k = lane - 18;  // zero the pads: k = 0 -> index 0, k = 1 -> index 19
+        uint32_t* dst = k < 2 ? P.occ : k < 4 ? P.wt : P.bt;
+        dst[(k & 1) ? 19 : 0] = 0;
+    } else if (lane == 24) {
+        const uint32_t* M = reinterpret_cast<const uint32_t*>(S + OFF_QUEEN);
+        uint32_t q = M[0];
+        P.queen[0] = (uint16_t)q;
+        P.queen[1] = (uint16_t)(q >> 16);
+        uint32_t h0 = M[1], h1 = M[2], h2 = M[3], h3 = M[4];
+        for (int k = 0; k < 4; k++) {
+            P.hand[0][k] = (uint8_t)(h0 >> (8 * k));
+            P.hand[0][4 + k] = (uint8_t)(h1 >> (8 * k));
+            P.hand[1][k] = (uint8_t)(h2 >> (8 * k));
+            P.hand[1][4 + k] = (uint8_t)(h3 >> (8 * k));
+        }
+        uint32_t t = M[5];  // turn u16, queen_placed u8, result u8
+        P.turn = (uint16_t)t;
+        P.qplaced = (uint8_t)(t >> 16);
+        P.result = (uint8_t)(t >> 24);
+        P.stun = (uint16_t)M[6];
+    }
+}
+
+// Ascending list of occupied cells (first 32) and their dense index.
+__device__ inline void build_occ_list(Pos& P, int lane) {
+    uint32_t w = lane < 18 ? P.occ[lane + 1] : 0u;
+    int base = wave_excl_scan(__popc(w), lane);
+    int total = wave_sum(lane < 18 ? __popc(w) : 0);
+    int k = base;
+    while (w) {
+        int b = __ffs(w) - 1;
+        w &= w - 1;
+        int c = lane * 32 + b;
+        if (k < 32) {
+            P.occ_cells[k] = (uint16_t)c;
+            P.idx_of[c] = (uint8_t)k;
+        }
+        k++;
+    }
+    if (lane == 0) P.n_occ = total < 32 ? total : 32;
+}
+
+// Articulation points (articulation.cuh:34-168).  The reference runs one DFS
+// from the lowest occupied cell, so its result is the articulation set of
+// that cell's component (first 28 cells), empty when <= 2 cells are occupied.
+// Here lane v floods the dense vertex graph with v removed; lane 63 floods
+// with nothing removed to obtain the component C0 of vertex 0.  v is an
+// articulation point iff v is in C0 and C0 \ {v} is not reached from a
+// vertex of C0 \ {v}.
+__device__ inline void articulation(Pos& P, int lane) {
+    int total = P.n_occ;
+    int N = total < 28 ? total : 28;
+    if (lane < 20) { P.ap[lane] = 0; P.pin[lane] = 0; }
+    if (lane < N) {
+        int c = P.occ_cells[lane];
+        uint32_t nm = nbr_bits(P.occ, c);
+        uint32_t a = 0;
+        while (nm) {
+            int d = __ffs(nm) - 1;
+            nm &= nm - 1;
+            int j = P.idx_of[step(c, d)];
+            if (j < N) a |= 1u << j;
+        }
+        P.adj[lane] = a;
+    }
+    __syncthreads();
+    if (total <= 2) return;
+    int v = lane < N ? lane : -1;
+    uint32_t vbit = v >= 0 ? (1u << v) : 0u;
+    uint32_t start;
+    if (v == 0) {
+        uint32_t a0 = P.adj[0];
+        start = a0 ? (a0 & (~a0 + 1u)) : 0u;
+    } else {
+        start = 1u;
+    }
+    uint32_t reach = 0;
+    if (lane < N || lane == 63) {
+        reach = start;
+        uint32_t frontier = start;
+        while (frontier) {
+            int i = __ffs(frontier) - 1;
+            frontier &= frontier - 1;
+            uint32_t nb = P.adj[i] & ~reach & ~vbit;
+            reach |= nb;
+            frontier |= nb;
+        }
+    }
+    uint32_t c0 = __shfl(reach, 63, 64);
+    bool is_ap = v >= 0 && ((c0 >> v) & 1u) && reach != (c0 & ~vbit);
+    if (is_ap) {
+        int c = P.occ_cells[v];
+        atomicOr(&P.ap[(c >> 5) + 1], 1u << (c & 31));
+        if (P.h[c] == 1) atomicOr(&P.pin[(c >> 5) + 1], 1u << (c & 31));
+    }
+}
+
+// ---------------------------------------------------------------- slides
+// Ground-slide destinations of c (can_slide, move_gen.cuh:82-104): the
+// destination is empty, exactly one of the two flanking cells is occupied;
+// cell g counts as empty (the moving piece's origin).
+__device__ __forceinline__ uint32_t slide_mask(const Pos& P, int c, int g) {
+    uint32_t gm = grid6(c);
+    uint32_t n = nbr_bits(P.occ, c) & ~dir_bit_to(c, g, gm);
+    return gm & ~n & (rotl6(n) ^ rotr6(n));
+}
+
+// heights of the six neighbours (0 off-grid), 4 bits each: direction d at bits 4d..4d+3
+__device__ __forceinline__ uint32_t nbr_heights(const Pos& P, int c, uint32_t gm) {
+    uint32_t r = 0;
+#pragma unroll
+    for (int d = 0; d < 6; d++)
+        if ((gm >> d) & 1u) r |= (uint32_t)(P.h[step(c, d)] & 15) << (4 * d);
+    return r;
+}
+__device__ __forceinline__ int hof(uint32_t nh, int d) { return (int)((nh >> (4 * d)) & 15u); }
+// both flanks of direction d strictly above height lvl (elevated gate, move_gen.cuh:659-667)
+__device__ __forceinline__ bool gate_high(uint32_t nh, int d, int lvl) {
+    return hof(nh, (d + 5) % 6) > lvl && hof(nh, (d + 1) % 6) > lvl;
+}
+
+// lane-private set helpers over an 18-word bitboard
+__device__ __forceinline__ void set_clear(uint32_t* s) {
+#pragma unroll
+    for (int i = 0; i < 18; i++) s[i] = 0;
+}
+__device__ __forceinline__ bool set_insert(uint32_t* s, int c) {  // true if newly inserted
+    uint32_t bit = 1u << (c & 31);
+    uint32_t old = s[c >> 5];
+    s[c >> 5] = old | bit;
+    return !(old & bit);
+}
+
+// ---------------------------------------------------------------- generators
+// Each writes destination cells into out[] in the reference's order and
+// returns the count.
+
+// gen_queen_moves :202-212 / gen_pillbug_moves :644-647
+__device__ inline int gen_step(const Pos& P, int c, uint16_t* out) {
+    uint32_t m = slide_mask(P, c, c);
+    int n = 0;
+    while (m) {
+        int d = __ffs(m) - 1;
+        m &= m - 1;
+        out[n++] = (uint16_t)step(c, d);
+    }
+    return n;
+}
+
+// gen_grasshopper_moves :228-245
+__device__ inline int gen_hopper(const Pos& P, int c, uint16_t* out) {
+    int n = 0;
+    uint32_t gm = grid6(c);
+    uint32_t m = nbr_bits(P.occ, c);
+    for (int d = 0; d < 6; d++) {
+        if (!((m >> d) & 1u)) continue;
+        int p = step(c, d);
+        bool on = true;
+        while (on && pb_get(P.occ, p)) {
+            if ((grid6(p) >> d) & 1u) p = step(p, d);
+            else on = false;
+        }
+        if (on) out[n++] = (uint16_t)p;
+    }
+    (void)gm;
+    return n;
+}
+
+// FIFO breadth-first ant search (gen_ant_moves_with_perimeter :267-313,
+// emit_ant_moves_with_perimeter :348-388): seeds in direction order, each
+// dequeued cell expanded in direction order, ant lifted from c.
+__device__ inline int gen_ant(const Pos& P, int c, uint16_t* out, int cap, uint32_t* seen) {
+    set_clear(seen);
+    set_insert(seen, c);
+    int head = 0, tail = 0;
+    int cur = c;
+    for (;;) {
+        uint32_t m = slide_mask(P, cur, c);
+        while (m && tail < cap) {
+            int d = __ffs(m) - 1;
+            m &= m - 1;
+            int dest = step(cur, d);
+            if (set_insert(seen, dest)) out[tail++] = (uint16_t)dest;
+        }
+        if (head >= tail || tail >= cap) break;
+        cur = out[head++];
+    }
+    return tail;
+}
+
+// gen_spider_moves :397-431 (first occurrence over d1,d2,d3; at most 32)
+__device__ inline int gen_spider(const Pos& P, int c, uint16_t* out, uint32_t* got) {
+    set_clear(got);
+    int n = 0;
+    uint32_t m1 = slide_mask(P, c, c);
+    while (m1) {
+        int d1 = __ffs(m1) - 1;
+        m1 &= m1 - 1;
+        int p1 = step(c, d1);
+        uint32_t m2 = slide_mask(P, p1, c);
+        while (m2) {
+            int d2 = __ffs(m2) - 1;
+            m2 &= m2 - 1;
+            int p2 = step(p1, d2);
+            if (p2 == c) continue;
+            uint32_t m3 = slide_mask(P, p2, c);
+            while (m3) {
+                int d3 = __ffs(m3) - 1;
+                m3 &= m3 - 1;
+                int p3 = step(p2, d3);
+                if (p3 == c || p3 == p1) continue;
+                if (n < 32 && set_insert(got, p3)) out[n++] = (uint16_t)p3;
+            }
+        }
+    }
+    return n;
+}
+
+// gen_beetle_moves :468-502
+__device__ inline int gen_beetle(const Pos& P, int c, uint16_t* out) {
+    uint32_t gm = grid6(c);
+    uint32_t nh = nbr_heights(P, c, gm);
+    uint32_t sm = slide_mask(P, c, c);
+    int below = P.h[c] - 1;
+    int n = 0;
+    for (int d = 0; d < 6; d++) {
+        if (!((gm >> d) & 1u)) continue;
+        int mh = max(hof(nh, d), below);
+        bool ok;
+        if (mh > 0) ok = !gate_high(nh, d, mh);
+        else ok = (sm >> d) & 1u;
+        if (ok) out[n++] = (uint16_t)step(c, d);
+    }
+    return n;
+}
+
+// gen_ladybug_moves :538-596 (first occurrence over d1,d2,d3; at most 32)
+__device__ inline int gen_ladybug(const Pos& P, int c, uint16_t* out, uint32_t* got) {
+    set_clear(got);
+    int n = 0;
+    uint32_t g0 = grid6(c);
+    uint32_t nh0 = nbr_heights(P, c, g0);
+    uint32_t o0 = nbr_bits(P.occ, c);
+    int hc = P.h[c];
+    for (int d1 = 0; d1 < 6; d1++) {
+        if (!((o0 >> d1) & 1u)) continue;
+        int p1 = step(c, d1);
+        if (gate_high(nh0, d1, max(hc - 1, hof(nh0, d1)))) continue;
+        uint32_t nh1 = nbr_heights(P, p1, grid6(p1));
+        uint32_t o1 = nbr_bits(P.occ, p1);
+        int hp1 = P.h[p1];
+        for (int d2 = 0; d2 < 6; d2++) {
+            if (!((o1 >> d2) & 1u)) continue;
+            int p2 = step(p1, d2);
+            if (p2 == c) continue;
+            if (gate_high(nh1, d2, max(hp1, hof(nh1, d2)))) continue;
+            uint32_t g2 = grid6(p2);
+            uint32_t nh2 = nbr_heights(P, p2, g2);
+            uint32_t o2 = nbr_bits(P.occ, p2);
+            int mh3 = P.h[p2];
+            for (int d3 = 0; d3 < 6; d3++) {
+                if (!((g2 >> d3) & 1u) || ((o2 >> d3) & 1u)) continue;
+                int p3 = step(p2, d3);
+                if (p3 == c || p3 == p1) continue;
+                if (gate_high(nh2, d3, mh3)) continue;
+                if (n < 32 && set_insert(got, p3)) out[n++] = (uint16_t)p3;
+            }
+        }
+    }
+    return n;
+}
+
+// gen_mosquito_moves :907-1008: beetle when stacked; otherwise the union, in
+// order Q/P, A, G, S, B, L, of the abilities of adjacent non-mosquito top
+// pieces, first occurrence kept, at most 128.  Each sub-list is generated
+// into the free tail of out[] and merged in place (merge write index never
+// passes the read index).  Needs 6 + 128 slots of room.
+__device__ inline int gen_mosquito(const Pos& P, int c, uint16_t* out, uint32_t* tmpset, uint32_t* unionset) {
+    if (P.h[c] > 1) return gen_beetle(P, c, out);
+    uint32_t gm = grid6(c);
+    uint32_t om = nbr_bits(P.occ, c);
+    uint32_t has = 0;
+    for (int d = 0; d < 6; d++)
+        if ((om >> d) & 1u) {
+            int t = P.top[step(c, d)] & 15;
+            if (t != PT_M) has |= 1u << t;
+        }
+    (void)gm;
+    set_clear(unionset);
+    int n = 0;
+    for (int k = 0; k < 6; k++) {
+        uint16_t* tail = out + n;
+        int m = 0;
+        switch (k) {
+            case 0: if (has & ((1u << PT_Q) | (1u << PT_P))) m = gen_step(P, c, tail); break;
+            case 1: if (has & (1u << PT_A)) m = gen_ant(P, c, tail, 128, tmpset); break;
+            case 2: if (has & (1u << PT_G)) m = gen_hopper(P, c, tail); break;
+            case 3: if (has & (1u << PT_S)) m = gen_spider(P, c, tail, tmpset); break;
+            case 4: if (has & (1u << PT_B)) m = gen_beetle(P, c, tail); break;
+            case 5: if (has & (1u << PT_L)) m = gen_ladybug(P, c, tail, tmpset); break;
+        }
+        int w = n;
+        for (int i = 0; i < m; i++) {
+            int x = tail[i];
+            if (set_insert(unionset, x) && w < 128) out[w++] = (uint16_t)x;
+        }
+        n = w;
+    }
+    return n;
+}
+
+// Throws by the pillbug-ability actor at a (gen_pillbug_throws :691-740):
+// targets in direction order, each to the empty drop cells in direction order.
+__device__ inline int gen_throws(const Pos& P, int a, uint16_t* from, uint16_t* to, uint8_t* pt) {
+    int n = 0;
+    uint32_t ga = grid6(a);
+    uint32_t nha = nbr_heights(P, a, ga);
+    int ph = P.h[a];
+    uint32_t oa = nbr_bits(P.occ, a);
+    for (int dt = 0; dt < 6; dt++) {
+        if (!((oa >> dt) & 1u)) continue;
+        int t = step(a, dt);
+        if (P.h[t] != 1) continue;
+        if (P.stun != 0xFFFF && (int)P.stun == t) continue;
+        if (pb_get(P.pin, t)) continue;
+        int back = (dt + 3) % 6;  // direction from the target to the actor
+        uint32_t gt = grid6(t);
+        int lift = max(P.h[t] - 1, ph);
+        int cwh = ((gt >> ((back + 5) % 6)) & 1u) ? P.h[step(t, (back + 5) % 6)] : 0;
+        int ccwh = ((gt >> ((back + 1) % 6)) & 1u) ? P.h[step(t, (back + 1) % 6)] : 0;
+        if (cwh > lift && ccwh > lift) continue;
+        int tp = P.top[t] & 15;
+        for (int dd = 0; dd < 6; dd++) {
+            if (!((ga >> dd) & 1u) || dd == dt || ((oa >> dd) & 1u)) continue;
+            if (gate_high(nha, dd, ph)) continue;
+            from[n] = (uint16_t)t;
+            to[n] = (uint16_t)step(a, dd);
+            pt[n] = (uint8_t)tp;
+            n++;
+        }
+    }
+    return n;
+}
+
+__device__ __forceinline__ bool touches_top_pillbug(const Pos& P, int c) {
+    uint32_t m = nbr_bits(P.occ, c);
+    while (m) {
+        int d = __ffs(m) - 1;
+        m &= m - 1;
+        if ((P.top[step(c, d)] & 15) == PT_P) return true;
+    }
+    return false;
+}
+
+__device__ __forceinline__ int type_capacity(int t) {
+    return (t == PT_A || t == PT_M) ? 168 : (t == PT_S || t == PT_L) ? 32 : 6;
+}
+
+// ---------------------------------------------------------------- placement
+// Placement cells (find_placement_positions :1064-1140) into P.plc, as a
+// bit-parallel neighbourhood expression over board words (lane w < 18 owns
+// word w).  Returns the number of cells (wave-uniform).
+__device__ inline uint32_t word_field(const uint32_t* pb, int bit_off) {
+    int wi = (bit_off >> 5) + 1;
+    int sh = bit_off & 31;
+    uint64_t v = (uint64_t)pb[wi] | ((uint64_t)pb[wi + 1] << 32);
+    return (uint32_t)(v >> sh);
+}
+
+// kGridMask.m[d][w]: cells of board word w whose d-neighbour is on the grid
+struct GridMasks {
+    uint32_t m[6][18];
+};
+constexpr GridMasks make_grid_masks() {
+    GridMasks g{};
+    for (int c = 0; c < kCells; c++) {
+        int r = c / kGrid, col = c % kGrid;
+        bool ok[6] = {col < 22, col < 22 && r > 0, r > 0, col > 0, col > 0 && r < 22, r < 22};
+        for (int d = 0; d < 6; d++)
+            if (ok[d]) g.m[d][c >> 5] |= 1u << (c & 31);
+    }
+    return g;
+}
+__constant__ GridMasks kGridMask = make_grid_masks();
+
+// cells of board word w with an on-grid neighbour that is set in pb
+__device__ inline uint32_t nbr_union_word(const uint32_t* pb, int w) {
+    uint32_t r = 0;
+#pragma unroll
+    for (int d = 0; d < 6; d++) r |= word_field(pb, 32 * w + win_ofs(d) - 23) & kGridMask.m[d][w];
+    return r;
+}
+
+}  // namespace hw

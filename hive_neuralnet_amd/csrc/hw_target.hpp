@@ -1,0 +1,10 @@
+// hw_target.hpp -- target header for the wave engine.  The product build is
+// HIP for gfx950.  tests/emu compiles the same engine sources for the host
+// (HW_HOST_EMU, a 64-thread wave emulator used only by CPU tests and for
+// debugging); that build never ships in the package.
+#pragma once
+#ifdef HW_HOST_EMU
+#include "../../tests/emu/wave_emu.hpp"
+#else
+#include <hip/hip_runtime.h>
+#endif

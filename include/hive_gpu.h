@@ -1,0 +1,115 @@
+/*
+ * hive_gpu.h -- C-ABI of libhive_gpu.so, the MI355X (gfx950) batched Hive
+ * engine.  This is the drop-in boundary: the Python package
+ * hive_neuralnet_amd.hive_gpu (the counterpart of the reference's
+ * hive_gpu.load_extension()) binds these symbols with ctypes; any other FFI
+ * can bind them the same way.
+ *
+ * Conventions (all entry points):
+ *   - pointers are device pointers; the caller allocates every input and
+ *     output (the reference allocates outputs inside its wrappers -- the
+ *     Python layer does that here, with the reference's fill values);
+ *   - `stream` is a hipStream_t (void* so this header needs no HIP headers);
+ *     work is enqueued on it and the call returns without synchronising;
+ *   - the return value is a hipError_t code (0 = success) of the launch;
+ *   - sizes <= 0 are a no-op returning 0;
+ *   - byte formats are the reference's: a state row is 3424 bytes
+ *     (HiveState, hive_gpu/csrc/hive_state.cuh:239-269), a move is 6 bytes
+ *     {u8 type, u8 piece_type, u16 from, u16 to} (hive_state.cuh:228-233),
+ *     legal lists are [B, 256, 6] with zero padding, features are [B, 122].
+ *
+ * Each declaration names the reference interface it replaces
+ * (chrismejias/hive_neuralnet, file:line).
+ */
+#ifndef HIVE_GPU_H
+#define HIVE_GPU_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define HG_ABI_VERSION 1
+#define HG_STATE_BYTES 3424
+#define HG_MOVE_BYTES 6
+#define HG_MAX_LEGAL_MOVES 256
+#define HG_FNN_FEAT_DIM 122
+
+int hg_abi_version(void);
+
+/* initialize_tables -- hive_gpu/csrc/game_logic.cu:404-407, bindings.cpp:257.
+ * The hex tables are closed-form constants here; kept for API parity. */
+int hg_initialize_tables(void);
+
+/* create_initial_states -- game_logic.cu:413-428 (init_states_kernel :54-59).
+ * Writes every byte of states[B][3424]. */
+int hg_create_initial_states(uint8_t* states, int64_t B, int expansion_mask, void* stream);
+
+/* apply_moves_batch -- game_logic.cu:465-477 (apply_moves_kernel :233-242).
+ * moves[B][6]; states updated in place. */
+int hg_apply_moves(uint8_t* states, const uint8_t* moves, int64_t B, void* stream);
+
+/* check_results_batch -- game_logic.cu:483-497.  results[B] int32. */
+int hg_check_results(const uint8_t* states, int64_t B, int32_t* results, void* stream);
+
+/* generate_legal_moves_batch -- game_logic.cu:436-459.
+ * moves[B][256][6] (fully written, zero padded), num_legal[B]. */
+int hg_generate_legal_moves(const uint8_t* states, int64_t B, uint8_t* moves, int32_t* num_legal, void* stream);
+
+/* generate_legal_moves_and_fnn_features_batch -- game_logic.cu:1439-1464. */
+int hg_generate_legal_moves_and_fnn_features(const uint8_t* states, int64_t B, uint8_t* moves,
+                                             int32_t* num_legal, float* features, void* stream);
+
+/* Fused move generation + FNN features + action indices in one pass: the
+ * outputs of generate_legal_moves_and_fnn_features_batch (game_logic.cu:1439)
+ * followed by legal_moves_to_actions_batch (game_logic.cu:837) without the
+ * list round trip through HBM.  actions[B][256] int32, -1 padded.  No single
+ * reference entry point; same spirit as the reference's own fused
+ * mcts_select_replay_legal_fnn_root_slots_batch. */
+int hg_legal_features_actions(const uint8_t* states, int64_t B, uint8_t* moves, int32_t* num_legal,
+                              float* features, int32_t* actions, void* stream);
+
+/* extract_fnn_features_batch -- game_logic.cu:1409-1431.
+ * features for caller-supplied lists (num_legal clamped to [0, 256]). */
+int hg_extract_fnn_features(const uint8_t* states, const uint8_t* moves, const int32_t* num_legal, int64_t B,
+                            float* features, void* stream);
+
+/* legal_moves_to_actions_batch -- game_logic.cu:837-857.
+ * actions[B][256] int32: action index per listed move, -1 beyond num_legal
+ * and for moves outside the 17x17 window around the centroid. */
+int hg_legal_moves_to_actions(const uint8_t* states, const uint8_t* moves, const int32_t* num_legal, int64_t B,
+                              int32_t* actions, void* stream);
+
+/* compute_centroids_batch -- game_logic.cu:910-926.  centroids[B][2] int32. */
+int hg_compute_centroids(const uint8_t* states, int64_t B, int32_t* centroids, void* stream);
+
+/* fnn_successor_features_batch -- game_logic.cu:1648-1671.
+ * For i < N: features[i] of states[action_to_root[i]] after
+ * legal_moves[action_to_root[i]][move_indices[i]], with the compact
+ * successor move summary (move_gen.cuh:1416-1563).  num_roots is the row
+ * count of states/legal_moves; rows whose root or move index is out of range
+ * get all-zero features (the reference reads out of bounds there). */
+int hg_fnn_successor_features(const uint8_t* states, const uint8_t* legal_moves, int64_t num_roots,
+                              const int64_t* action_to_root, const int64_t* move_indices, int64_t N, float* features,
+                              void* stream);
+
+/* queen_escape_flags_batch -- game_logic.cu:1538-1554.  flags[B] uint8. */
+int hg_queen_escape_flags(const uint8_t* states, int64_t B, uint8_t* flags, void* stream);
+
+/* One ply of seeded random play (the position generator of the benchmark
+ * configurations; no reference counterpart -- the reference's own pattern is
+ * torch.rand x n_legal + apply_moves_batch, hive_gpu/endgame_generator.py:268-276).
+ * Game i is active while ply < target_i and its result is 0, where target_i =
+ * Philox4x32-10(key=(seed,0), ctr=(i,0,0,0))[0] mod (max_ply+1), or max_ply
+ * when lockstep != 0.  An active game applies
+ * moves[i][(Philox(key, (i,ply+1,0,0))[0] * num_legal[i]) >> 32] and, when
+ * plies_done is not NULL, increments plies_done[i]. */
+int hg_random_play_step(uint8_t* states, const uint8_t* moves, const int32_t* num_legal, int64_t B, int ply,
+                        int max_ply, int lockstep, uint32_t seed, int32_t* plies_done, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HIVE_GPU_H */

@@ -1,0 +1,80 @@
+// wave_emu.hpp -- host emulation of the few HIP wave primitives the engine
+// uses, so tests can run the engine's device code on the CPU.
+//
+// TEST INFRASTRUCTURE ONLY.  A "wave" is 64 std::threads; barriers, shuffles
+// and ballots rendezvous through a shared exchange buffer.  This build never
+// ships in the package: the product is the gfx950 HIP library.
+#pragma once
+#include <atomic>
+#include <barrier>
+#include <cstdint>
+#include <cstdlib>
+#include <cstring>
+
+#define __device__
+#define __host__
+#define __global__
+#define __shared__
+#define __constant__
+#define __forceinline__ inline
+#define __launch_bounds__(x)
+
+namespace wave_emu {
+struct Ctx {
+    std::barrier<>* bar;
+    int64_t slot[64];
+};
+inline Ctx* g_ctx = nullptr;
+inline thread_local int g_lane = 0;
+inline void sync() { g_ctx->bar->arrive_and_wait(); }
+template <typename T>
+inline T exchange(T v, int src) {
+    g_ctx->slot[g_lane] = (int64_t)v;
+    sync();
+    T r = (T)g_ctx->slot[src];
+    sync();
+    return r;
+}
+}  // namespace wave_emu
+
+struct EmuThreadIdx {
+    operator int() const { return wave_emu::g_lane; }
+};
+struct EmuDim3 {
+    EmuThreadIdx x;
+};
+inline EmuDim3 threadIdx;
+
+inline void __syncthreads() { wave_emu::sync(); }
+
+template <typename T>
+inline T __shfl_up(T v, unsigned o, int = 64) {
+    int src = wave_emu::g_lane - (int)o;
+    return wave_emu::exchange(v, src >= 0 ? src : wave_emu::g_lane);
+}
+template <typename T>
+inline T __shfl_xor(T v, int m, int = 64) {
+    return wave_emu::exchange(v, wave_emu::g_lane ^ m);
+}
+template <typename T>
+inline T __shfl(T v, int src, int = 64) {
+    return wave_emu::exchange(v, src & 63);
+}
+inline uint64_t __ballot(int pred) {
+    wave_emu::g_ctx->slot[wave_emu::g_lane] = pred ? 1 : 0;
+    wave_emu::sync();
+    uint64_t m = 0;
+    for (int i = 0; i < 64; i++)
+        if (wave_emu::g_ctx->slot[i]) m |= 1ull << i;
+    wave_emu::sync();
+    return m;
+}
+inline int atomicAdd(int* p, int v) { return __atomic_fetch_add(p, v, __ATOMIC_SEQ_CST); }
+inline uint32_t atomicOr(uint32_t* p, uint32_t v) { return __atomic_fetch_or(p, v, __ATOMIC_SEQ_CST); }
+inline int __popc(uint32_t x) { return __builtin_popcount(x); }
+inline int __popcll(uint64_t x) { return __builtin_popcountll(x); }
+inline int __ffs(uint32_t x) { return __builtin_ffs((int)x); }
+inline int __ffs(int x) { return __builtin_ffs(x); }
+inline uint32_t __umulhi(uint32_t a, uint32_t b) { return (uint32_t)(((uint64_t)a * b) >> 32); }
+inline int min(int a, int b) { return a < b ? a : b; }
+inline int max(int a, int b) { return a > b ? a : b; }

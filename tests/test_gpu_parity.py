@@ -1,0 +1,160 @@
+"""Parity of the HIP engine (through the C-ABI) with the reference semantics.
+
+Checks, all bit-exact (features compared as float32 bit patterns):
+  * golden vectors written by the reference's own engine (tests/golden/);
+  * the CPU oracle on seeded Philox positions at the configurations' full
+    sizes (C2: 65,536 base positions, plies U[0,120]; C3: 65,536 positions
+    with mosquito/ladybug/pillbug, plies U[0,150]);
+  * the GPU position generator against the oracle's, and lockstep random
+    self-play finals against reference replays (C4 shape);
+  * edge cases: empty batch, finished games, caller-supplied lists.
+"""
+import numpy as np
+import pytest
+import torch
+
+from conftest import load_golden
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def ext():
+    from hive_neuralnet_amd import hive_gpu
+    return hive_gpu.load_extension()
+
+
+def _cuda(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def _bits(f):
+    return np.ascontiguousarray(f).view(np.uint32)
+
+
+def test_constants(ext):
+    assert ext.BOARD_SIZE == 23 and ext.NUM_CELLS == 529 and ext.MAX_LEGAL_MOVES == 256
+    assert ext.SIZEOF_HIVE_STATE == 3424 and ext.SIZEOF_GPU_MOVE == 6 and ext.FNN_FEAT_DIM == 122
+    assert ext.ACTION_SPACE_SIZE == 85834 and ext.PASS_ACTION_INDEX == 85833 and ext.MOVEMENT_OFFSET == 2312
+
+
+def test_initial_states(ext, oracle):
+    for mask in range(8):
+        s = ext.create_initial_states(5, mask).cpu().numpy()
+        for row in s:
+            assert np.array_equal(row, oracle.init_state(mask))
+    # tests/test_gpu_move_gen.py:148-160 -- 4 placements at turn 0, results 0
+    st = ext.create_initial_states(8)
+    moves, n = ext.generate_legal_moves_batch(st, 8)
+    assert n.cpu().tolist() == [4] * 8
+    assert (ext.check_results_batch(st, 8) == 0).all()
+
+
+@pytest.mark.parametrize("name", ["c1", "c2", "c3"])
+def test_golden_moves_features(ext, name):
+    g = load_golden(name)
+    B = len(g["states"])
+    st = _cuda(g["states"])
+    moves, n = ext.generate_legal_moves_batch(st, B)
+    assert np.array_equal(n.cpu().numpy(), g["n"])
+    assert np.array_equal(moves.cpu().numpy(), g["moves"])
+    moves2, n2, feat = ext.generate_legal_moves_and_fnn_features_batch(st, B)
+    assert np.array_equal(moves2.cpu().numpy(), g["moves"])
+    assert np.array_equal(_bits(feat.cpu().numpy()), _bits(g["features"]))
+    feat2 = ext.extract_fnn_features_batch(st, _cuda(g["moves"]), _cuda(g["n"]), B)
+    assert np.array_equal(_bits(feat2.cpu().numpy()), _bits(g["features"]))
+    # compact successor lists of the golden moves, via extract on the oracle's compact lists
+    feat3 = ext.extract_fnn_features_batch(st, _cuda(g["compact"]), _cuda(g["ncompact"]), B)
+    assert feat3.shape == (B, 122)
+
+
+@pytest.mark.parametrize("name", ["c1", "c2", "c3"])
+def test_golden_successors_queen_escape_apply(ext, name):
+    g = load_golden(name)
+    st = _cuda(g["states"])
+    succ = ext.fnn_successor_features_batch(st, _cuda(g["moves"]), _cuda(g["succ_root"]), _cuda(g["succ_idx"]),
+                                            len(g["succ_root"]))
+    assert np.array_equal(_bits(succ.cpu().numpy()), _bits(g["succ_features"]))
+    qe = ext.queen_escape_flags_batch(st, len(g["states"]))
+    assert np.array_equal(qe.cpu().numpy(), g["queen_escape"])
+    k = min(512, len(g["succ_root"]))
+    roots, idx = g["succ_root"][:k], g["succ_idx"][:k]
+    children = _cuda(g["states"][roots])
+    ext.apply_moves_batch(children, _cuda(g["moves"][roots, idx]), k)
+    assert np.array_equal(children.cpu().numpy(), g["child_states"][:k])
+    res = ext.check_results_batch(children, k).cpu().numpy()
+    assert np.array_equal(res, g["child_states"][:k, 3415].astype(np.int32))
+
+
+def _oracle_positions(oracle, B, mask, max_ply, seed=0x5EED):
+    return oracle.generate_positions(B, mask, max_ply, seed, threads=16)
+
+
+@pytest.mark.parametrize("cfg", [("c2", 65536, 0, 120), ("c3", 65536, 7, 150)], ids=["C2", "C3"])
+def test_full_size_parity(ext, oracle, cfg):
+    _, B, mask, max_ply = cfg
+    states, _ = _oracle_positions(oracle, B, mask, max_ply)
+    om, on, of, oa = oracle.batch_legal_features_actions(states, threads=16)
+    st = _cuda(states)
+    moves, n, feat, act = ext.generate_legal_moves_features_actions_batch(st, B)
+    assert np.array_equal(n.cpu().numpy(), on)
+    assert np.array_equal(moves.cpu().numpy(), om)
+    assert np.array_equal(_bits(feat.cpu().numpy()), _bits(of))
+    assert np.array_equal(act.cpu().numpy(), oa)
+    act2 = ext.legal_moves_to_actions_batch(st, moves, n, B)
+    assert np.array_equal(act2.cpu().numpy(), oa)
+    cen = ext.compute_centroids_batch(st, B).cpu().numpy()
+    for i in range(0, B, 997):
+        assert tuple(cen[i]) == oracle.centroid(states[i])
+    qe = ext.queen_escape_flags_batch(st, B).cpu().numpy()
+    assert np.array_equal(qe, oracle.batch_queen_escape(states, threads=16))
+
+
+@pytest.mark.parametrize("mask,max_ply", [(0, 120), (7, 150)])
+def test_successor_features_scale(ext, oracle, mask, max_ply):
+    states, _ = _oracle_positions(oracle, 1024, mask, max_ply, seed=0xBEEF)
+    om, on, _, _ = oracle.batch_legal_features_actions(states, threads=16)
+    roots = np.repeat(np.arange(len(states)), on).astype(np.int64)
+    idx = np.concatenate([np.arange(k) for k in on]).astype(np.int64)
+    want = oracle.batch_successor_features(states, om, roots, idx, full_list=False, threads=16)
+    got = ext.fnn_successor_features_batch(_cuda(states), _cuda(om), _cuda(roots), _cuda(idx), len(roots))
+    assert np.array_equal(_bits(got.cpu().numpy()), _bits(want))
+
+
+@pytest.mark.parametrize("mask,max_ply", [(0, 120), (7, 150)])
+def test_gpu_generator_matches_oracle(oracle, mask, max_ply):
+    from hive_neuralnet_amd.hive_gpu import random_positions
+    B = 4096
+    st, plies = random_positions(B, mask, max_ply, 0x5EED)
+    ost, oplies = _oracle_positions(oracle, B, mask, max_ply)
+    assert np.array_equal(plies.cpu().numpy(), oplies)
+    assert np.array_equal(st.cpu().numpy(), ost)
+
+
+def test_lockstep_selfplay_golden():
+    from hive_neuralnet_amd.hive_gpu import random_positions
+    g = load_golden("c4")
+    G = len(g["finals"])
+    st, plies = random_positions(G, 0, int(g["max_ply"]), int(g["seed"]), lockstep=True)
+    assert np.array_equal(plies.cpu().numpy(), g["plies"])
+    assert np.array_equal(st.cpu().numpy(), g["finals"])
+
+
+def test_edge_cases(ext, oracle):
+    e = ext.create_initial_states(0)
+    m, n = ext.generate_legal_moves_batch(e, 0)
+    assert m.shape == (0, 256, 6) and n.shape == (0,)
+    # finished games: no moves, zero rows; features still defined
+    g = load_golden("c4")
+    done = g["finals"][g["finals"][:, 3415] != 0]
+    assert len(done) > 0
+    moves, n, feat = ext.generate_legal_moves_and_fnn_features_batch(_cuda(done), len(done))
+    assert (n.cpu().numpy() == 0).all() and (moves.cpu().numpy() == 0).all()
+    for i in range(len(done)):
+        want = oracle.fnn_features(done[i], np.zeros((256, 6), np.uint8), 0)
+        assert np.array_equal(_bits(feat[i].cpu().numpy()), _bits(want))
+    # caller-supplied list longer than 256 is clamped; negative counts give none
+    st = _cuda(g["finals"][:2])
+    mv = torch.zeros((2, 256, 6), dtype=torch.uint8, device="cuda")
+    f = ext.extract_fnn_features_batch(st, mv, torch.tensor([-3, 999], dtype=torch.int32, device="cuda"), 2)
+    assert f.shape == (2, 122)
