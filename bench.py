@@ -48,6 +48,8 @@ def parse_args():
     ap.add_argument("--cpu-threads", type=int, default=0, help="0 = min(16, cores)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="target CPU-thread seconds for the baseline")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a 256 MiB device-to-device copy 3 times (rocprof counter calibration)")
     return ap.parse_args()
 
 
@@ -102,8 +104,16 @@ def main():
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}): positions and games are "
               "independent, so N GPUs shard the batch with no collectives; run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
-    import numpy as np
     import torch
+
+    if args.copy_calibration:
+        a = torch.ones(64 * 1024 * 1024, dtype=torch.float32, device="cuda")
+        b = torch.empty_like(a)
+        for _ in range(3):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes": a.numel() * 4, "copies": 3}))
+        return
 
     from hive_neuralnet_amd import hive_gpu
 
