@@ -1,0 +1,549 @@
+// hive_mcts.hip -- MCTS tree kernels over the reference's structure-of-arrays
+// tree (mcts_tree.cuh:31-45): select with root slots / root mask, replay,
+// dense-prior expansion, fused expansion + backup, root noise.
+//
+// Order of effect.  The reference runs one thread per simulation with
+// atomics, so simulations of one game race on virtual-loss reads, on which
+// of them expands a shared leaf, on node-id allocation and on float
+// summation order (mcts_tree.cuh:773-786,1001-1020,1166-1186).  Here one
+// wavefront owns one game and applies that game's simulations in
+// simulation-index order (sim = k*B + game, k = 0, 1, ...): each selection
+// sees the virtual losses of earlier ones, the earliest simulation reaching
+// an unexpanded leaf expands it, node ids are handed out in that order and
+// every float update of a node happens in that order.  Within one
+// simulation the lanes split the per-child work (PUCT over a node's
+// children, initialising a new node's children).  With one simulation per
+// root candidate per call the result equals every interleaving of the
+// reference up to node numbering.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/hive_gpu.h"
+#include "hive_phases.hpp"
+
+using namespace hw;
+
+namespace {
+
+constexpr int kDepth = 128;  // MAX_TREE_DEPTH (mcts_tree.cuh:27)
+
+struct Tree {
+    int32_t* vc;
+    float* tv;
+    float* pr;
+    int32_t* pa;
+    float* vq;
+    uint8_t* mb;
+    int32_t* ai;
+    int32_t* fc;
+    int32_t* nc;
+    int8_t* it;
+    float* tval;
+    int32_t* cnt;
+    float* ciq;
+    int64_t M;
+};
+
+Tree to_tree(const hg_tree* t) {
+    return Tree{t->visit_count, t->total_value, t->prior, t->parent_idx, t->virtual_q_penalty, t->move_bytes,
+                t->action_idx, t->first_child, t->num_children, t->is_terminal, t->terminal_value,
+                t->node_count, t->child_init_q, t->max_nodes};
+}
+
+// puct_score (mcts_tree.cuh:55-67), evaluated in the same operation order
+__device__ __forceinline__ float puct(const Tree& T, int64_t pi, int64_t ci, float c_puct) {
+    int n = T.vc[ci];
+    float q = n > 0 ? (-T.tv[ci] / (float)n) : 0.0f;
+    q -= T.vq[ci];
+    float explore = c_puct * T.pr[ci] * sqrtf((float)T.vc[pi]) / (1.0f + (float)n);
+    return q + explore;
+}
+
+// first maximum of score over the lanes' candidates (score must beat -1e30)
+__device__ __forceinline__ int wave_argmax_first(float score, int idx) {
+    bool ok = score > -1e30f;  // NaN and the -1e30 floor never win (strict '>' from -1e30)
+    float s = ok ? score : -INFINITY;
+    int i = ok ? idx : 0x7fffffff;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        float s2 = __shfl_xor(s, o, 64);
+        int i2 = __shfl_xor(i, o, 64);
+        if (s2 > s || (s2 == s && i2 < i)) { s = s2; i = i2; }
+    }
+    return i == 0x7fffffff ? -1 : i;
+}
+
+// deterministic_completed_q_child (mcts_tree.cuh:77-143), one lane, child order
+__device__ int completed_q_child(const Tree& T, int64_t g0, int first, int count, float sigma) {
+    float sum_visits = 0.0f;
+    for (int c = 0; c < count; c++) {
+        if (first + c < 0 || first + c >= T.M) break;
+        sum_visits += (float)T.vc[g0 + first + c];
+    }
+    float mx = -1e30f;
+    for (int c = 0; c < count; c++) {
+        if (first + c < 0 || first + c >= T.M) break;
+        int64_t ci = g0 + first + c;
+        float visits = (float)T.vc[ci];
+        float q = visits > 0.0f ? (-T.tv[ci] / visits) : T.ciq[ci];
+        q -= T.vq[ci];
+        float lq = logf(fmaxf(T.pr[ci], 1e-20f)) + sigma * q;
+        if (lq > mx) mx = lq;
+    }
+    float se = 0.0f;
+    for (int c = 0; c < count; c++) {
+        if (first + c < 0 || first + c >= T.M) break;
+        int64_t ci = g0 + first + c;
+        float visits = (float)T.vc[ci];
+        float q = visits > 0.0f ? (-T.tv[ci] / visits) : T.ciq[ci];
+        q -= T.vq[ci];
+        se += expf(logf(fmaxf(T.pr[ci], 1e-20f)) + sigma * q - mx);
+    }
+    se = fmaxf(se, 1e-20f);
+    int best = -1;
+    float bs = -1e30f;
+    float denom = 1.0f + sum_visits;
+    for (int c = 0; c < count; c++) {
+        if (first + c < 0 || first + c >= T.M) break;
+        int64_t ci = g0 + first + c;
+        float visits = (float)T.vc[ci];
+        float q = visits > 0.0f ? (-T.tv[ci] / visits) : T.ciq[ci];
+        q -= T.vq[ci];
+        float pi0 = expf(logf(fmaxf(T.pr[ci], 1e-20f)) + sigma * q - mx) / se;
+        float score = pi0 - (visits / denom);
+        if (score > bs) { bs = score; best = first + c; }
+    }
+    return best;
+}
+
+struct SelectOut {
+    int32_t* leaf;
+    uint8_t* paths;
+    int32_t* plen;
+    int32_t* vl;
+    int32_t* vlen;
+};
+
+__device__ __forceinline__ void empty_sim(const SelectOut& O, int64_t sim, int lane) {
+    if (lane == 0) {
+        O.leaf[sim] = -1;
+        O.plen[sim] = 0;
+        O.vlen[sim] = 0;
+    }
+}
+
+// Enter `node` below the root (virtual loss or q penalty, path records).
+__device__ __forceinline__ void enter(const Tree& T, int64_t g0, int node, bool det, float q_penalty,
+                                      const SelectOut& O, int64_t sim, int& plen, int& vlen, int lane) {
+    if (lane == 0) {
+        int64_t ni = g0 + node;
+        if (det) {
+            T.vc[ni] += 1;
+            T.vq[ni] += q_penalty;
+        } else {
+            T.vc[ni] += 1;
+            T.tv[ni] += -1.0f;
+        }
+        if (vlen < kDepth) O.vl[sim * kDepth + vlen] = node;
+        if (plen < kDepth) {
+            const uint8_t* src = T.mb + ni * 6;
+            uint8_t* dst = O.paths + (sim * kDepth + plen) * 6;
+            for (int b = 0; b < 6; b++) dst[b] = src[b];
+        }
+    }
+    vlen = vlen < kDepth ? vlen + 1 : vlen;
+    plen = plen < kDepth ? plen + 1 : plen;
+    __syncthreads();  // later reads of this game's statistics see the update
+}
+
+// PUCT descent below `node` (mcts_tree.cuh:895-950 / 729-795 below the root).
+__device__ int descend(const Tree& T, int64_t g0, int node, int first_iter, float c_puct, bool det, float sigma,
+                       float q_penalty, const SelectOut& O, int64_t sim, int& plen, int& vlen, int lane) {
+    for (int it = first_iter; it < kDepth; it++) {
+        int64_t ni = g0 + node;
+        int cfc = T.fc[ni];
+        int cnc = T.nc[ni];
+        if (cfc < 0 || T.it[ni] || cnc == 0) break;
+        if (cnc <= 0 || cnc > 1024) break;
+        int best;
+        if (det) {
+            int b = 0;
+            if (lane == 0) b = completed_q_child(T, g0, cfc, cnc, sigma);
+            best = __shfl(b, 0, 64);
+        } else {
+            float bs = -INFINITY;
+            int bi = 0x7fffffff;
+            for (int c = lane; c < cnc; c += 64) {
+                int child = cfc + c;
+                if (child < 0 || child >= T.M) break;
+                float sc = puct(T, ni, g0 + child, c_puct);
+                if (sc > -1e30f && (sc > bs || (sc == bs && c < bi))) { bs = sc; bi = c; }
+            }
+            int c = wave_argmax_first(bs, bi);
+            best = c < 0 ? -1 : cfc + c;
+        }
+        if (best < 0) break;
+        node = best;
+        enter(T, g0, node, det, q_penalty, O, sim, plen, vlen, lane);
+    }
+    return node;
+}
+
+// mcts_select_with_root_slots_kernel (mcts_tree.cuh:811-955), one wave per game
+__global__ __launch_bounds__(64) void k_select_slots(Tree T, const int8_t* __restrict__ game_active,
+                                                     const int32_t* __restrict__ root_nodes,
+                                                     const int32_t* __restrict__ root_slots, int C, int max_root,
+                                                     float c_puct, int64_t B, int64_t total, int det, float sigma,
+                                                     float q_penalty, SelectOut O) {
+    const int64_t g = blockIdx.x;
+    const int lane = threadIdx.x;
+    if (g >= B) return;
+    const int64_t g0 = g * T.M;
+    for (int64_t sim = g; sim < total; sim += B) {
+        int cand = (int)((sim / B) % C);
+        if (!game_active[g]) { empty_sim(O, sim, lane); continue; }
+        int slot = root_slots[g * C + cand];
+        if (slot < 0 || slot >= max_root) { empty_sim(O, sim, lane); continue; }
+        int root = root_nodes[g];
+        int64_t ri = g0 + root;
+        int fc = T.fc[ri], nc = T.nc[ri];
+        if (fc < 0 || T.it[ri] || nc <= 0 || slot >= nc) { empty_sim(O, sim, lane); continue; }
+        int node = fc + slot;
+        if (node < 0 || node >= T.M) { empty_sim(O, sim, lane); continue; }
+        int plen = 0, vlen = 0;
+        if (!det) {
+            enter(T, g0, node, false, 0.0f, O, sim, plen, vlen, lane);
+        } else {  // the root child gets no penalty in this mode, only the path record
+            if (lane == 0) {
+                const uint8_t* src = T.mb + (g0 + node) * 6;
+                uint8_t* dst = O.paths + sim * kDepth * 6;
+                for (int b = 0; b < 6; b++) dst[b] = src[b];
+            }
+            plen = 1;
+        }
+        node = descend(T, g0, node, 1, c_puct, det, sigma, q_penalty, O, sim, plen, vlen, lane);
+        if (lane == 0) {
+            O.leaf[sim] = node;
+            O.plen[sim] = plen;
+            O.vlen[sim] = vlen;
+        }
+        __syncthreads();
+    }
+}
+
+// mcts_select_with_root_mask_kernel (mcts_tree.cuh:689-800), one wave per game
+__global__ __launch_bounds__(64) void k_select_mask(Tree T, const int8_t* __restrict__ game_active,
+                                                    const int32_t* __restrict__ root_nodes,
+                                                    const int8_t* __restrict__ alive, int max_root, float c_puct,
+                                                    int64_t B, int64_t total, int det, float sigma, float q_penalty,
+                                                    SelectOut O) {
+    const int64_t g = blockIdx.x;
+    const int lane = threadIdx.x;
+    if (g >= B) return;
+    const int64_t g0 = g * T.M;
+    for (int64_t sim = g; sim < total; sim += B) {
+        if (!game_active[g]) { empty_sim(O, sim, lane); continue; }
+        int root = root_nodes[g];
+        int node = root;
+        int plen = 0, vlen = 0;
+        int64_t ri = g0 + root;
+        int fc = T.fc[ri], nc = T.nc[ri];
+        bool go = !(fc < 0 || T.it[ri] || nc == 0) && !(nc <= 0 || nc > 1024);
+        int first_iter = 0;
+        if (go) {  // root level: PUCT over alive children
+            float bs = -INFINITY;
+            int bi = 0x7fffffff;
+            for (int c = lane; c < nc; c += 64) {
+                int child = fc + c;
+                if (child < 0 || child >= T.M) break;
+                if (c >= max_root || !alive[g * max_root + c]) continue;
+                float sc = puct(T, ri, g0 + child, c_puct);
+                if (sc > -1e30f && (sc > bs || (sc == bs && c < bi))) { bs = sc; bi = c; }
+            }
+            int c = wave_argmax_first(bs, bi);
+            if (c >= 0) {
+                node = fc + c;
+                enter(T, g0, node, false, 0.0f, O, sim, plen, vlen, lane);
+                first_iter = 1;
+            } else {
+                go = false;
+            }
+        }
+        if (go) node = descend(T, g0, node, first_iter, c_puct, det, sigma, q_penalty, O, sim, plen, vlen, lane);
+        if (lane == 0) {
+            O.leaf[sim] = node;
+            O.plen[sim] = plen;
+            O.vlen[sim] = vlen;
+        }
+        __syncthreads();
+    }
+}
+
+// mcts_replay_kernel (mcts_tree.cuh:298-320): leaf = root + path moves.  One
+// wave per simulation; the row is assembled in LDS and written once.
+__global__ __launch_bounds__(64) void k_replay(const uint8_t* __restrict__ roots, int64_t B,
+                                               uint8_t* __restrict__ leaves, const uint8_t* __restrict__ paths,
+                                               const int32_t* __restrict__ plen, const int32_t* __restrict__ leaf_idx,
+                                               int64_t total) {
+    __shared__ uint4 row[kStateBytes / 16];
+    const int64_t sim = blockIdx.x;
+    const int lane = threadIdx.x;
+    if (sim >= total || leaf_idx[sim] < 0) return;
+    const uint4* src = reinterpret_cast<const uint4*>(roots + (sim % B) * kStateBytes);
+    for (int i = lane; i < kStateBytes / 16; i += 64) row[i] = src[i];
+    __syncthreads();
+    if (lane == 0) {
+        RowView v{reinterpret_cast<uint8_t*>(row)};
+        int n = plen[sim];
+        const uint8_t* p = paths + sim * kDepth * 6;
+        for (int d = 0; d < n && d < kDepth; d++, p += 6) v.apply(p[0], p[1], p[2] | (p[3] << 8), p[4] | (p[5] << 8));
+    }
+    __syncthreads();
+    uint4* dst = reinterpret_cast<uint4*>(leaves + sim * kStateBytes);
+    for (int i = lane; i < kStateBytes / 16; i += 64) dst[i] = row[i];
+}
+
+// centroid of a state row (compute_centroid, state_encoder.cuh:889-906)
+__device__ void row_centroid(const uint8_t* __restrict__ S, int lane, int& cq, int& cr) {
+    int q = 0, r = 0, n = 0;
+    if (lane < 18) {
+        uint32_t w = reinterpret_cast<const uint32_t*>(S + OFF_OCC)[lane];
+        while (w) {
+            int c = lane * 32 + __ffs(w) - 1;
+            w &= w - 1;
+            int row = c / kGrid;
+            q += c - row * kGrid - kHalf;
+            r += row - kHalf;
+            n++;
+        }
+    }
+    int sq = wave_sum(q), sr = wave_sum(r), sn = wave_sum(n);
+    cq = sn ? round_half_even_div(sq, sn) : 0;
+    cr = sn ? round_half_even_div(sr, sn) : 0;
+}
+
+// result_to_value (mcts_tree.cuh:182-188)
+__device__ __forceinline__ float result_value(int result, int turn) {
+    if (result == 3) return 0.0f;
+    int player = turn & 1;
+    if (result == 1) return player == 0 ? 1.0f : -1.0f;
+    if (result == 2) return player == 0 ? -1.0f : 1.0f;
+    return 0.0f;
+}
+
+struct LeafIn {
+    const int32_t* leaf;
+    const uint8_t* states;
+    const uint8_t* legal;
+    const int32_t* nlegal;
+    const float* priors;
+    const float* childq;
+    const int32_t* results;
+};
+
+// Expansion of one simulation's leaf (mcts_expand_dense_priors_kernel
+// :971-1062 body); returns 1 when this simulation created the children.
+__device__ int expand_leaf(const Tree& T, int64_t g, int64_t sim, const LeafIn& L, int lane) {
+    const int64_t g0 = g * T.M;
+    int leaf = L.leaf[sim];
+    int64_t li = g0 + leaf;
+    const uint8_t* S = L.states + sim * kStateBytes;
+    int res = L.results[sim];
+    if (res != 0) {
+        if (lane == 0) {
+            T.it[li] = 1;
+            T.tval[li] = result_value(res, S[OFF_TURN] | (S[OFF_TURN + 1] << 8));
+        }
+        __syncthreads();
+        return 0;
+    }
+    if (T.fc[li] != -1) return 0;
+    int n = L.nlegal[sim];
+    if (n <= 0) return 0;
+    int base = T.cnt[g];
+    if ((int64_t)base + n > T.M) return 0;  // pool exhausted: leaf stays unexpanded
+    int cq, cr;
+    row_centroid(S, lane, cq, cr);
+    const uint8_t* mv = L.legal + sim * (kMaxLegal * 6);
+    const float* pri = L.priors + sim * kMaxLegal;
+    const float* cqv = L.childq + sim * kMaxLegal;
+    for (int m = lane; m < n; m += 64) {
+        const uint8_t* x = mv + 6 * m;
+        int64_t ci = g0 + base + m;
+        T.vc[ci] = 0;
+        T.tv[ci] = 0.0f;
+        T.pr[ci] = pri[m];
+        T.pa[ci] = leaf;
+        T.ai[ci] = move_action(x[0], x[1], x[2] | (x[3] << 8), x[4] | (x[5] << 8), cq, cr);
+        T.fc[ci] = -1;
+        T.nc[ci] = 0;
+        T.it[ci] = 0;
+        T.tval[ci] = 0.0f;
+        T.ciq[ci] = cqv[m];
+        uint8_t* d = T.mb + ci * 6;
+        for (int b = 0; b < 6; b++) d[b] = x[b];
+    }
+    if (lane == 0) {
+        T.cnt[g] = base + n;
+        T.nc[li] = n;
+        T.fc[li] = base;
+    }
+    __syncthreads();
+    return 1;
+}
+
+__global__ __launch_bounds__(64) void k_expand(Tree T, LeafIn L, int64_t B, int64_t total,
+                                               int8_t* __restrict__ was_expanded) {
+    const int64_t g = blockIdx.x;
+    const int lane = threadIdx.x;
+    if (g >= B) return;
+    for (int64_t sim = g; sim < total; sim += B) {
+        int e = 0;
+        if (L.leaf[sim] >= 0) e = expand_leaf(T, g, sim, L, lane);
+        if (lane == 0) was_expanded[sim] = (int8_t)e;
+    }
+}
+
+// mcts_expand_and_backprop_dense_priors_kernel (mcts_tree.cuh:1068-1187)
+__global__ __launch_bounds__(64) void k_expand_backprop(Tree T, LeafIn L, const float* __restrict__ nn_values,
+                                                        const int32_t* __restrict__ vl_paths,
+                                                        const int32_t* __restrict__ vl_lens, float q_penalty,
+                                                        int64_t B, int64_t total) {
+    const int64_t g = blockIdx.x;
+    const int lane = threadIdx.x;
+    if (g >= B) return;
+    const int64_t g0 = g * T.M;
+    for (int64_t sim = g; sim < total; sim += B) {
+        int leaf = L.leaf[sim];
+        if (leaf < 0) continue;
+        int e = expand_leaf(T, g, sim, L, lane);
+        if (lane == 0) {
+            int64_t li = g0 + leaf;
+            float v = T.it[li] ? T.tval[li] : (e ? nn_values[sim] : 0.0f);
+            int n = vl_lens[sim];
+            const int32_t* vp = vl_paths + sim * kDepth;
+            for (int k = 0; k < n && k < kDepth; k++) {
+                int64_t ni = g0 + vp[k];
+                if (q_penalty > 0.0f) {
+                    T.vq[ni] += -q_penalty;
+                } else {
+                    T.vc[ni] -= 1;
+                    T.tv[ni] += 1.0f;
+                }
+            }
+            int node = leaf;
+            for (int s = 0; s < kDepth + 1 && node >= 0; s++) {
+                int64_t ni = g0 + node;
+                T.vc[ni] += 1;
+                T.tv[ni] += v;
+                v = -v;
+                node = T.pa[ni];
+            }
+        }
+        __syncthreads();
+    }
+}
+
+// mcts_root_noise_kernel (mcts_tree.cuh:1192-1234), one lane per game
+__global__ void k_root_noise(Tree T, const float* __restrict__ noise, const int32_t* __restrict__ root_nodes,
+                             int pad, float eps, float temp, int64_t B) {
+    int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (g >= B) return;
+    const int64_t g0 = g * T.M;
+    int64_t ri = g0 + root_nodes[g];
+    int fc = T.fc[ri], nc = T.nc[ri];
+    if (fc < 0 || nc == 0) return;
+    const float* z = noise + g * pad;
+    if (temp > 1.0f) {
+        float inv = 1.0f / temp, sum = 0.0f;
+        for (int c = 0; c < nc; c++) {
+            float p = powf(T.pr[g0 + fc + c], inv);
+            T.pr[g0 + fc + c] = p;
+            sum += p;
+        }
+        if (sum > 0.0f)
+            for (int c = 0; c < nc; c++) T.pr[g0 + fc + c] /= sum;
+    }
+    if (eps > 0.0f) {
+        for (int c = 0; c < nc && c < pad; c++) {
+            float a = (1.0f - eps) * T.pr[g0 + fc + c];
+            float b = eps * z[c];
+            T.pr[g0 + fc + c] = a + b;
+        }
+    }
+}
+
+inline int finish() { return (int)hipGetLastError(); }
+
+}  // namespace
+
+extern "C" {
+
+int hg_mcts_select_root_slots(const hg_tree* tree, const int8_t* game_active, const int32_t* root_nodes,
+                              const int32_t* root_slots, int num_candidates, int max_root_children, float c_puct,
+                              int64_t B, int W, int deterministic_non_root, float non_root_sigma, float q_penalty,
+                              int32_t* leaf_idx, uint8_t* move_paths, int32_t* path_lens, int32_t* vl_paths,
+                              int32_t* vl_lens, void* stream) {
+    if (B <= 0 || W <= 0 || num_candidates <= 0) return 0;
+    int64_t total = (int64_t)W * num_candidates * B;
+    SelectOut O{leaf_idx, move_paths, path_lens, vl_paths, vl_lens};
+    hipLaunchKernelGGL(k_select_slots, dim3((unsigned)B), dim3(64), 0, (hipStream_t)stream, to_tree(tree),
+                       game_active, root_nodes, root_slots, num_candidates, max_root_children, c_puct, B, total,
+                       deterministic_non_root, non_root_sigma, q_penalty, O);
+    return finish();
+}
+
+int hg_mcts_select_root_mask(const hg_tree* tree, const int8_t* game_active, const int32_t* root_nodes,
+                             const int8_t* alive_mask, int max_root_children, float c_puct, int64_t B, int W,
+                             int deterministic_non_root, float non_root_sigma, float q_penalty, int32_t* leaf_idx,
+                             uint8_t* move_paths, int32_t* path_lens, int32_t* vl_paths, int32_t* vl_lens,
+                             void* stream) {
+    if (B <= 0 || W <= 0) return 0;
+    int64_t total = (int64_t)W * B;
+    SelectOut O{leaf_idx, move_paths, path_lens, vl_paths, vl_lens};
+    hipLaunchKernelGGL(k_select_mask, dim3((unsigned)B), dim3(64), 0, (hipStream_t)stream, to_tree(tree),
+                       game_active, root_nodes, alive_mask, max_root_children, c_puct, B, total,
+                       deterministic_non_root, non_root_sigma, q_penalty, O);
+    return finish();
+}
+
+int hg_mcts_replay(const uint8_t* root_states, int64_t B, uint8_t* leaf_states, const uint8_t* move_paths,
+                   const int32_t* path_lens, const int32_t* leaf_idx, int64_t total, void* stream) {
+    if (B <= 0 || total <= 0) return 0;
+    hipLaunchKernelGGL(k_replay, dim3((unsigned)total), dim3(64), 0, (hipStream_t)stream, root_states, B,
+                       leaf_states, move_paths, path_lens, leaf_idx, total);
+    return finish();
+}
+
+int hg_mcts_expand_dense(const hg_tree* tree, const float* child_q_values, const int32_t* leaf_idx,
+                         const uint8_t* leaf_states, const uint8_t* legal_moves, const int32_t* num_legal,
+                         const float* priors_per_legal, const int32_t* results, int64_t B, int64_t total,
+                         int8_t* was_expanded, void* stream) {
+    if (B <= 0 || total <= 0) return 0;
+    LeafIn L{leaf_idx, leaf_states, legal_moves, num_legal, priors_per_legal, child_q_values, results};
+    hipLaunchKernelGGL(k_expand, dim3((unsigned)B), dim3(64), 0, (hipStream_t)stream, to_tree(tree), L, B, total,
+                       was_expanded);
+    return finish();
+}
+
+int hg_mcts_expand_backprop_dense(const hg_tree* tree, const float* child_q_values, const int32_t* leaf_idx,
+                                  const uint8_t* leaf_states, const uint8_t* legal_moves, const int32_t* num_legal,
+                                  const float* priors_per_legal, const int32_t* results, const float* nn_values,
+                                  const int32_t* vl_paths, const int32_t* vl_lens, float q_penalty, int64_t B,
+                                  int64_t total, void* stream) {
+    if (B <= 0 || total <= 0) return 0;
+    LeafIn L{leaf_idx, leaf_states, legal_moves, num_legal, priors_per_legal, child_q_values, results};
+    hipLaunchKernelGGL(k_expand_backprop, dim3((unsigned)B), dim3(64), 0, (hipStream_t)stream, to_tree(tree), L,
+                       nn_values, vl_paths, vl_lens, q_penalty, B, total);
+    return finish();
+}
+
+int hg_mcts_root_noise(const hg_tree* tree, const float* noise, const int32_t* root_nodes, int max_children_pad,
+                       float dir_eps, float root_policy_temp, int64_t B, void* stream) {
+    if (B <= 0) return 0;
+    hipLaunchKernelGGL(k_root_noise, dim3((unsigned)((B + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                       to_tree(tree), noise, root_nodes, max_children_pad, dir_eps, root_policy_temp, B);
+    return finish();
+}
+
+}  // extern "C"

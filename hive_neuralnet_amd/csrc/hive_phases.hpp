@@ -736,4 +736,78 @@ __device__ inline bool run_queen_escape(Pos& P, const uint8_t* __restrict__ S, i
     prepare(P, S, lane);
     return queen_escape(P, lane);
 }
+// ---------------------------------------------------------------- rows
+// Byte-level apply_move (hive_state.cuh:326-517) on a state row in global
+// memory or LDS, run by one lane.
+struct RowView {
+    uint8_t* s;
+    __device__ uint8_t& stack(int lv, int c) { return s[lv * kCells + c]; }
+    __device__ uint8_t& h(int c) { return s[OFF_HEIGHT + c]; }
+    __device__ uint64_t* bb(int off) { return reinterpret_cast<uint64_t*>(s + off); }
+    __device__ void set(int off, int c) { bb(off)[c >> 6] |= 1ull << (c & 63); }
+    __device__ void clr(int off, int c) { bb(off)[c >> 6] &= ~(1ull << (c & 63)); }
+    __device__ bool get(int off, int c) { return (bb(off)[c >> 6] >> (c & 63)) & 1ull; }
+    __device__ uint16_t& u16(int off) { return *reinterpret_cast<uint16_t*>(s + off); }
+    __device__ void top_colour(int c, int col) {
+        if (col) { set(OFF_BTOP, c); clr(OFF_WTOP, c); }
+        else { set(OFF_WTOP, c); clr(OFF_BTOP, c); }
+    }
+    __device__ bool ringed(int col) {
+        if (!((s[OFF_QPLACED] >> col) & 1)) return false;
+        int q = u16(OFF_QUEEN + 2 * col);
+        if (q >= kCells) return false;
+        uint32_t g = grid6(q);
+        int k = 0;
+        for (int d = 0; d < 6; d++)
+            if (((g >> d) & 1u) && get(OFF_OCC, step(q, d))) k++;
+        return k == 6;
+    }
+    __device__ void apply(int type, int pt, int from, int to) {
+        int me = u16(OFF_TURN) & 1;
+        if (type == MV_PLACE) {
+            if (to < kCells && pt >= PT_Q && pt <= PT_P && h(to) < 5) {
+                int hh = h(to);
+                stack(hh, to) = (uint8_t)(pt | (me << 4));
+                h(to) = (uint8_t)(hh + 1);
+                if (hh == 0) set(OFF_OCC, to);
+                top_colour(to, me);
+                if (pt == PT_Q) {
+                    u16(OFF_QUEEN + 2 * me) = (uint16_t)to;
+                    s[OFF_QPLACED] |= (uint8_t)(1 << me);
+                }
+                s[OFF_HANDS + me * 8 + pt - 1] -= 1;
+            }
+            u16(OFF_STUN) = 0xFFFF;
+        } else if (type == MV_MOVE) {
+            if (from < kCells && to < kCells) {
+                if (h(from) > 0 && h(from) <= 5 && h(to) < 5) {  // heights above 5 never occur
+                    int hf = h(from);
+                    uint8_t b = stack(hf - 1, from);
+                    stack(hf - 1, from) = 0;
+                    h(from) = (uint8_t)(hf - 1);
+                    if (hf == 1) {
+                        clr(OFF_OCC, from); clr(OFF_WTOP, from); clr(OFF_BTOP, from);
+                    } else {
+                        top_colour(from, (stack(hf - 2, from) >> 4) & 1);
+                    }
+                    int ht = h(to);
+                    stack(ht, to) = b;
+                    h(to) = (uint8_t)(ht + 1);
+                    if (ht == 0) set(OFF_OCC, to);
+                    top_colour(to, (b >> 4) & 1);
+                    if ((b & 15) == PT_Q) u16(OFF_QUEEN + 2 * ((b >> 4) & 1)) = (uint16_t)to;
+                }
+                u16(OFF_STUN) = (uint16_t)to;
+            }
+        } else {
+            u16(OFF_STUN) = 0xFFFF;
+        }
+        u16(OFF_TURN) = (uint16_t)(u16(OFF_TURN) + 1);
+        bool w = ringed(0), k = ringed(1);
+        if (w && k) s[OFF_RESULT] = 3;
+        else if (w) s[OFF_RESULT] = 2;
+        else if (k) s[OFF_RESULT] = 1;
+    }
+};
+
 }  // namespace hw

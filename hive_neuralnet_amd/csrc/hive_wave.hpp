@@ -556,7 +556,7 @@ constexpr GridMasks make_grid_masks() {
     }
     return g;
 }
-__constant__ GridMasks kGridMask = make_grid_masks();
+static __constant__ GridMasks kGridMask = make_grid_masks();
 
 // cells of board word w with an on-grid neighbour that is set in pb
 __device__ inline uint32_t nbr_union_word(const uint32_t* pb, int w) {

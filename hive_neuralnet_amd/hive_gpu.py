@@ -69,7 +69,64 @@ _SIGS = {
     "hg_queen_escape_flags": [_c_void_p, _c_i64, _c_void_p, _c_void_p],
     "hg_random_play_step": [_c_void_p, _c_void_p, _c_void_p, _c_i64, _c_int, _c_int, _c_int, ctypes.c_uint32,
                             _c_void_p, _c_void_p],
+    "hg_mcts_select_root_slots": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, ctypes.c_float, _c_i64,
+                                  _c_int, _c_int, ctypes.c_float, ctypes.c_float, _c_void_p, _c_void_p, _c_void_p,
+                                  _c_void_p, _c_void_p, _c_void_p],
+    "hg_mcts_select_root_mask": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, ctypes.c_float, _c_i64, _c_int,
+                                 _c_int, ctypes.c_float, ctypes.c_float, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+                                 _c_void_p, _c_void_p],
+    "hg_mcts_replay": [_c_void_p, _c_i64, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_i64, _c_void_p],
+    "hg_mcts_expand_dense": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+                             _c_i64, _c_i64, _c_void_p, _c_void_p],
+    "hg_mcts_expand_backprop_dense": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+                                      _c_void_p, _c_void_p, _c_void_p, _c_void_p, ctypes.c_float, _c_i64, _c_i64,
+                                      _c_void_p],
+    "hg_mcts_root_noise": [_c_void_p, _c_void_p, _c_void_p, _c_int, ctypes.c_float, ctypes.c_float, _c_i64,
+                           _c_void_p],
 }
+
+
+class HgTree(ctypes.Structure):
+    """C layout of `hg_tree` (include/hive_gpu.h)."""
+
+    _fields_ = [(name, ctypes.c_void_p) for name in (
+        "visit_count", "total_value", "prior", "parent_idx", "virtual_q_penalty", "move_bytes", "action_idx",
+        "first_child", "num_children", "is_terminal", "terminal_value", "node_count", "child_init_q")] + [
+        ("max_nodes", ctypes.c_int64)]
+
+
+_TREE_SPEC = [  # the 12 tree tensors in the reference's argument order (game_logic.cu:933-953)
+    ("vc", torch.int32), ("tv", torch.float32), ("pr", torch.float32), ("pa", torch.int32),
+    ("vq", torch.float32), ("mb", torch.uint8), ("ai", torch.int32), ("fc", torch.int32),
+    ("nc", torch.int32), ("it", torch.int8), ("tv2", torch.float32), ("cnt", torch.int32),
+]
+
+
+def _tree_struct(tensors, child_init_q, B: int, max_nodes: int) -> HgTree:
+    """Validate the 12 tree tensors + child_init_q and pack their pointers."""
+    if len(tensors) != 12:
+        raise ValueError("expected the 12 tree tensors")
+    ptrs = []
+    for (name, dtype), t in zip(_TREE_SPEC, tensors):
+        if name == "mb":
+            _dev(t, name, dtype, (max_nodes, SIZEOF_GPU_MOVE), B)
+        elif name == "cnt":
+            _dev(t, name, dtype, (), B)
+        else:
+            _dev(t, name, dtype, (max_nodes,), B)
+        ptrs.append(t.data_ptr())
+    _dev(child_init_q, "child_init_q", torch.float32, (max_nodes,), B)
+    vc, tv, pr, pa, vq, mb, ai, fc, nc, it, tv2, cnt = ptrs
+    return HgTree(vc, tv, pr, pa, vq, mb, ai, fc, nc, it, tv2, cnt, child_init_q.data_ptr(), int(max_nodes))
+
+
+def _select_outputs(T: int):
+    leaf = torch.zeros((T,), dtype=torch.int32, device="cuda")
+    paths = torch.zeros((T, MAX_TREE_DEPTH, SIZEOF_GPU_MOVE), dtype=torch.uint8, device="cuda")
+    plen = torch.zeros((T,), dtype=torch.int32, device="cuda")
+    vl = torch.zeros((T, MAX_TREE_DEPTH), dtype=torch.int32, device="cuda")
+    vlen = torch.zeros((T,), dtype=torch.int32, device="cuda")
+    return leaf, paths, plen, vl, vlen
 
 _lib = None
 _lib_lock = threading.Lock()
@@ -261,6 +318,128 @@ def random_positions(batch_size: int, expansion_mask: int, max_ply: int, seed: i
                                        1 if lockstep else 0, int(seed) & 0xFFFFFFFF, plies.data_ptr(), _stream()),
                "random_play_step")
     return states, plies
+
+
+def _mcts_methods():
+    """MCTS entry points, bound onto HiveGpuExtension below (reference
+    signatures: bindings.cpp:378-436)."""
+
+    def mcts_select_with_root_mask_batch(self, vc, tv, pr, pa, vq, mb, ai, fc, nc, it, tv2, cnt, child_init_q,
+                                         game_active, root_nodes, alive_mask, max_root_children, c_puct, B, W,
+                                         max_nodes, deterministic_non_root=False, non_root_sigma=4.0, q_penalty=0.0):
+        B, W, M = int(B), int(W), int(max_nodes)
+        tree = _tree_struct((vc, tv, pr, pa, vq, mb, ai, fc, nc, it, tv2, cnt), child_init_q, B, M)
+        _dev(game_active, "game_active", torch.int8, (), B)
+        _dev(root_nodes, "root_nodes", torch.int32, (), B)
+        _dev(alive_mask, "alive_mask", torch.int8, (int(max_root_children),), B)
+        T = W * B
+        out = _select_outputs(T)
+        _check(self._lib.hg_mcts_select_root_mask(
+            ctypes.byref(tree), game_active.data_ptr(), root_nodes.data_ptr(), alive_mask.data_ptr(),
+            int(max_root_children), float(c_puct), B, W, 1 if deterministic_non_root else 0, float(non_root_sigma),
+            float(q_penalty), *[o.data_ptr() for o in out], _stream()), "mcts_select_with_root_mask_batch")
+        return out
+
+    def mcts_select_with_root_slots_batch(self, vc, tv, pr, pa, vq, mb, ai, fc, nc, it, tv2, cnt, child_init_q,
+                                          game_active, root_nodes, root_slots, num_candidates, max_root_children,
+                                          c_puct, B, W, max_nodes, deterministic_non_root=False, non_root_sigma=4.0,
+                                          q_penalty=0.0):
+        B, W, C, M = int(B), int(W), int(num_candidates), int(max_nodes)
+        tree = _tree_struct((vc, tv, pr, pa, vq, mb, ai, fc, nc, it, tv2, cnt), child_init_q, B, M)
+        _dev(game_active, "game_active", torch.int8, (), B)
+        _dev(root_nodes, "root_nodes", torch.int32, (), B)
+        _dev(root_slots, "root_slots", torch.int32, (C,), B)
+        T = W * C * B
+        out = _select_outputs(T)
+        _check(self._lib.hg_mcts_select_root_slots(
+            ctypes.byref(tree), game_active.data_ptr(), root_nodes.data_ptr(), root_slots.data_ptr(), C,
+            int(max_root_children), float(c_puct), B, W, 1 if deterministic_non_root else 0, float(non_root_sigma),
+            float(q_penalty), *[o.data_ptr() for o in out], _stream()), "mcts_select_with_root_slots_batch")
+        return out
+
+    def mcts_replay_batch(self, root_states, leaf_states, move_paths, path_lengths, leaf_indices, B, total):
+        B, total = int(B), int(total)
+        _state_rows(root_states, B)
+        _state_rows(leaf_states, total)
+        _dev(move_paths, "move_paths", torch.uint8, (MAX_TREE_DEPTH, SIZEOF_GPU_MOVE), total)
+        _dev(path_lengths, "path_lengths", torch.int32, (), total)
+        _dev(leaf_indices, "leaf_indices", torch.int32, (), total)
+        _check(self._lib.hg_mcts_replay(root_states.data_ptr(), B, leaf_states.data_ptr(), move_paths.data_ptr(),
+                                        path_lengths.data_ptr(), leaf_indices.data_ptr(), total, _stream()),
+               "mcts_replay_batch")
+
+    def mcts_select_replay_legal_fnn_root_slots_batch(self, vc, tv, pr, pa, vq, mb, ai, fc, nc, it, tv2, cnt,
+                                                      child_init_q, root_states, game_active, root_nodes, root_slots,
+                                                      num_candidates, max_root_children, c_puct, B, W, max_nodes,
+                                                      deterministic_non_root=False, non_root_sigma=4.0,
+                                                      q_penalty=0.0):
+        """game_logic.cu:1183-1254: select -> replay -> results -> legal + features, 8-tuple."""
+        leaf_idx, paths, plen, vl, vlen = self.mcts_select_with_root_slots_batch(
+            vc, tv, pr, pa, vq, mb, ai, fc, nc, it, tv2, cnt, child_init_q, game_active, root_nodes, root_slots,
+            num_candidates, max_root_children, c_puct, B, W, max_nodes, deterministic_non_root, non_root_sigma,
+            q_penalty)
+        T = leaf_idx.shape[0]
+        leaf_states = torch.zeros((T, root_states.shape[1]), dtype=torch.uint8, device="cuda")
+        self.mcts_replay_batch(root_states, leaf_states, paths, plen, leaf_idx, B, T)
+        results = self.check_results_batch(leaf_states, T)
+        moves, n, feat = self.generate_legal_moves_and_fnn_features_batch(leaf_states, T)
+        return leaf_idx, leaf_states, moves, n, feat, results, vl, vlen
+
+    def _leaf_args(total, child_q_values, leaf_indices, leaf_states, legal_moves, num_legal, priors_per_legal,
+                   results):
+        _dev(child_q_values, "child_q_values", torch.float32, (MAX_LEGAL_MOVES,), total)
+        _dev(leaf_indices, "leaf_indices", torch.int32, (), total)
+        _state_rows(leaf_states, total)
+        _dev(legal_moves, "legal_moves", torch.uint8, (MAX_LEGAL_MOVES, SIZEOF_GPU_MOVE), total)
+        _dev(num_legal, "num_legal", torch.int32, (), total)
+        _dev(priors_per_legal, "priors_per_legal", torch.float32, (MAX_LEGAL_MOVES,), total)
+        _dev(results, "results", torch.int32, (), total)
+        return [child_q_values.data_ptr(), leaf_indices.data_ptr(), leaf_states.data_ptr(), legal_moves.data_ptr(),
+                num_legal.data_ptr(), priors_per_legal.data_ptr(), results.data_ptr()]
+
+    def mcts_expand_dense_priors_batch(self, vc, tv, pr, pa, vq, mb, ai, fc, nc, it, tv2, cnt, child_init_q,
+                                       child_q_values, leaf_indices, leaf_states, legal_moves, num_legal,
+                                       priors_per_legal, results, B, total, max_nodes):
+        B, total, M = int(B), int(total), int(max_nodes)
+        tree = _tree_struct((vc, tv, pr, pa, vq, mb, ai, fc, nc, it, tv2, cnt), child_init_q, B, M)
+        args = _leaf_args(total, child_q_values, leaf_indices, leaf_states, legal_moves, num_legal,
+                          priors_per_legal, results)
+        was = torch.zeros((total,), dtype=torch.int8, device="cuda")
+        _check(self._lib.hg_mcts_expand_dense(ctypes.byref(tree), *args, B, total, was.data_ptr(), _stream()),
+               "mcts_expand_dense_priors_batch")
+        return was
+
+    def mcts_expand_and_backprop_dense_priors_batch(self, vc, tv, pr, pa, vq, mb, ai, fc, nc, it, tv2, cnt,
+                                                    child_init_q, child_q_values, leaf_indices, leaf_states,
+                                                    legal_moves, num_legal, priors_per_legal, results, nn_values,
+                                                    vl_paths, vl_lengths, B, total, max_nodes, q_penalty):
+        B, total, M = int(B), int(total), int(max_nodes)
+        tree = _tree_struct((vc, tv, pr, pa, vq, mb, ai, fc, nc, it, tv2, cnt), child_init_q, B, M)
+        args = _leaf_args(total, child_q_values, leaf_indices, leaf_states, legal_moves, num_legal,
+                          priors_per_legal, results)
+        _dev(nn_values, "nn_values", torch.float32, (), total)
+        _dev(vl_paths, "vl_paths", torch.int32, (MAX_TREE_DEPTH,), total)
+        _dev(vl_lengths, "vl_lengths", torch.int32, (), total)
+        _check(self._lib.hg_mcts_expand_backprop_dense(
+            ctypes.byref(tree), *args, nn_values.data_ptr(), vl_paths.data_ptr(), vl_lengths.data_ptr(),
+            float(q_penalty), B, total, _stream()), "mcts_expand_and_backprop_dense_priors_batch")
+
+    def mcts_apply_root_noise(self, vc, tv, pr, pa, vq, mb, ai, fc, nc, it, tv2, cnt, noise, root_nodes,
+                              max_children_pad, dir_eps, root_policy_temp, B, max_nodes):
+        B, M, pad = int(B), int(max_nodes), int(max_children_pad)
+        # the noise kernel never touches child_init_q; any [B, M] f32 array fills the slot
+        tree = _tree_struct((vc, tv, pr, pa, vq, mb, ai, fc, nc, it, tv2, cnt), tv, B, M)
+        _dev(noise, "noise", torch.float32, (pad,), B)
+        _dev(root_nodes, "root_nodes", torch.int32, (), B)
+        _check(self._lib.hg_mcts_root_noise(ctypes.byref(tree), noise.data_ptr(), root_nodes.data_ptr(), pad,
+                                            float(dir_eps), float(root_policy_temp), B, _stream()),
+               "mcts_apply_root_noise")
+
+    return {k: v for k, v in locals().items() if k.startswith("mcts_")}
+
+
+for _name, _fn in _mcts_methods().items():
+    setattr(HiveGpuExtension, _name, _fn)
 
 
 _extension = None

@@ -108,6 +108,81 @@ int hg_queen_escape_flags(const uint8_t* states, int64_t B, uint8_t* flags, void
 int hg_random_play_step(uint8_t* states, const uint8_t* moves, const int32_t* num_legal, int64_t B, int ply,
                         int max_ply, int lockstep, uint32_t seed, int32_t* plies_done, void* stream);
 
+/* ---------------------------------------------------------------- MCTS tree
+ * The reference's structure-of-arrays tree (mcts_tree.cuh:31-45), one pool of
+ * max_nodes slots per game, arrays [B, max_nodes] (move_bytes [B, max_nodes, 6],
+ * node_count [B]); child_init_q is the extra [B, max_nodes] array the
+ * reference passes beside the struct.  Passed by host pointer.
+ *
+ * Order of effect: simulations of one game take effect in simulation-index
+ * order (sim = k*B + game): each selection sees earlier selections' virtual
+ * losses, the earliest simulation reaching an unexpanded leaf expands it,
+ * node ids are handed out in that order, float updates happen in that order.
+ * The reference applies the same updates with atomics in whatever order its
+ * threads run. */
+typedef struct hg_tree {
+    int32_t* visit_count;
+    float* total_value;
+    float* prior;
+    int32_t* parent_idx;
+    float* virtual_q_penalty;
+    uint8_t* move_bytes;
+    int32_t* action_idx;
+    int32_t* first_child;
+    int32_t* num_children;
+    int8_t* is_terminal;
+    float* terminal_value;
+    int32_t* node_count;
+    float* child_init_q;
+    int64_t max_nodes;
+} hg_tree;
+
+/* mcts_select_with_root_slots_batch -- game_logic.cu:1134-1175
+ * (mcts_select_with_root_slots_kernel, mcts_tree.cuh:811-955).
+ * T = W * num_candidates * B simulations, sim = (w*C + c)*B + game.
+ * Outputs (caller zero-fills move_paths/vl_paths): leaf_idx[T], move_paths[T][128][6],
+ * path_lens[T], vl_paths[T][128], vl_lens[T]. */
+int hg_mcts_select_root_slots(const hg_tree* tree, const int8_t* game_active, const int32_t* root_nodes,
+                              const int32_t* root_slots, int num_candidates, int max_root_children, float c_puct,
+                              int64_t B, int W, int deterministic_non_root, float non_root_sigma, float q_penalty,
+                              int32_t* leaf_idx, uint8_t* move_paths, int32_t* path_lens, int32_t* vl_paths,
+                              int32_t* vl_lens, void* stream);
+
+/* mcts_select_with_root_mask_batch -- game_logic.cu:1088-1129
+ * (mcts_select_with_root_mask_kernel, mcts_tree.cuh:689-800).  T = W * B. */
+int hg_mcts_select_root_mask(const hg_tree* tree, const int8_t* game_active, const int32_t* root_nodes,
+                             const int8_t* alive_mask, int max_root_children, float c_puct, int64_t B, int W,
+                             int deterministic_non_root, float non_root_sigma, float q_penalty, int32_t* leaf_idx,
+                             uint8_t* move_paths, int32_t* path_lens, int32_t* vl_paths, int32_t* vl_lens,
+                             void* stream);
+
+/* mcts_replay_batch -- game_logic.cu:1000-1015 (mcts_replay_kernel, mcts_tree.cuh:298-320).
+ * leaf_states[s] = root_states[s % B] with the path moves applied; rows with
+ * leaf_idx < 0 are left untouched. */
+int hg_mcts_replay(const uint8_t* root_states, int64_t B, uint8_t* leaf_states, const uint8_t* move_paths,
+                   const int32_t* path_lens, const int32_t* leaf_idx, int64_t total, void* stream);
+
+/* mcts_expand_dense_priors_batch -- game_logic.cu:1259-1288
+ * (mcts_expand_dense_priors_kernel, mcts_tree.cuh:971-1062).  was_expanded[total] int8. */
+int hg_mcts_expand_dense(const hg_tree* tree, const float* child_q_values, const int32_t* leaf_idx,
+                         const uint8_t* leaf_states, const uint8_t* legal_moves, const int32_t* num_legal,
+                         const float* priors_per_legal, const int32_t* results, int64_t B, int64_t total,
+                         int8_t* was_expanded, void* stream);
+
+/* mcts_expand_and_backprop_dense_priors_batch -- game_logic.cu:1293-1323
+ * (mcts_expand_and_backprop_dense_priors_kernel, mcts_tree.cuh:1068-1187). */
+int hg_mcts_expand_backprop_dense(const hg_tree* tree, const float* child_q_values, const int32_t* leaf_idx,
+                                  const uint8_t* leaf_states, const uint8_t* legal_moves, const int32_t* num_legal,
+                                  const float* priors_per_legal, const int32_t* results, const float* nn_values,
+                                  const int32_t* vl_paths, const int32_t* vl_lens, float q_penalty, int64_t B,
+                                  int64_t total, void* stream);
+
+/* mcts_apply_root_noise -- game_logic.cu:1384-1402 (mcts_root_noise_kernel,
+ * mcts_tree.cuh:1192-1234).  noise[B][max_children_pad]; children beyond the
+ * pad are left unchanged (the reference reads past the row there). */
+int hg_mcts_root_noise(const hg_tree* tree, const float* noise, const int32_t* root_nodes, int max_children_pad,
+                       float dir_eps, float root_policy_temp, int64_t B, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

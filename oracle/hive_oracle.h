@@ -56,6 +56,42 @@ void or_generate_positions(int64_t B, int expansion_mask, int max_ply, uint32_t 
 void or_lockstep_selfplay(int64_t G, int expansion_mask, int max_ply, uint32_t seed,
                           uint8_t* states_out, int32_t* plies_out, int threads);
 
+/* MCTS tree (hive_mcts_oracle.c): host arrays in the reference's SoA layout */
+typedef struct {
+    int32_t* vc;   /* visit_count [B, M] */
+    float* tv;     /* total_value */
+    float* pr;     /* prior */
+    int32_t* pa;   /* parent_idx */
+    float* vq;     /* virtual_q_penalty */
+    uint8_t* mb;   /* move_bytes [B, M, 6] */
+    int32_t* ai;   /* action_idx */
+    int32_t* fc;   /* first_child */
+    int32_t* nc;   /* num_children */
+    int8_t* it;    /* is_terminal */
+    float* tval;   /* terminal_value */
+    int32_t* cnt;  /* node_count [B] */
+    float* ciq;    /* child_init_q */
+    int64_t M;     /* max_nodes */
+} or_tree;
+
+void or_mcts_select_slots(const or_tree* t, const int8_t* active, const int32_t* roots, const int32_t* slots, int C,
+                          int max_root, float c_puct, int64_t B, int W, int det, float sigma, float qp,
+                          int32_t* leaf, uint8_t* paths, int32_t* plen, int32_t* vl, int32_t* vlen);
+void or_mcts_select_mask(const or_tree* t, const int8_t* active, const int32_t* roots, const int8_t* alive,
+                         int max_root, float c_puct, int64_t B, int W, int det, float sigma, float qp,
+                         int32_t* leaf, uint8_t* paths, int32_t* plen, int32_t* vl, int32_t* vlen);
+void or_mcts_replay(const uint8_t* roots, int64_t B, uint8_t* leaves, const uint8_t* paths, const int32_t* plen,
+                    const int32_t* leaf, int64_t total);
+void or_mcts_expand_dense(const or_tree* t, const float* child_q, const int32_t* leaf, const uint8_t* states,
+                          const uint8_t* legal, const int32_t* nlegal, const float* priors, const int32_t* results,
+                          int64_t B, int64_t total, int8_t* was);
+void or_mcts_expand_backprop_dense(const or_tree* t, const float* child_q, const int32_t* leaf, const uint8_t* states,
+                                   const uint8_t* legal, const int32_t* nlegal, const float* priors,
+                                   const int32_t* results, const float* values, const int32_t* vl,
+                                   const int32_t* vlen, float qp, int64_t B, int64_t total);
+void or_mcts_root_noise(const or_tree* t, const float* noise, const int32_t* roots, int pad, float eps, float temp,
+                        int64_t B);
+
 #ifdef __cplusplus
 }
 #endif

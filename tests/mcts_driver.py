@@ -1,0 +1,189 @@
+"""A small Gumbel-style search driver over the MCTS tree entry points.
+
+Test helper.  It runs the reference orchestrator's call sequence
+(hive_fnn/fnn_mcts_orchestrator.py:645-711,896-925,982-1055): root expansion
+with dense priors, root noise, then waves of root-slot selection, replay,
+results, legal lists, expansion + backup -- with the network replaced by
+seeded synthetic outputs computed on the host (record-and-replay), so the
+CPU oracle and the GPU engine receive identical inputs and their trees can
+be compared array by array.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+from oracle.mcts import TREE_KEYS, MctsOracle, new_tree
+
+MAX_LEGAL = 256
+
+
+def synthetic_eval(rng, n, total):
+    """Softmax priors over legal slots, values and child Q in [-1, 1]."""
+    valid = np.arange(MAX_LEGAL)[None, :] < n[:total, None]
+    logits = rng.standard_normal((total, MAX_LEGAL))
+    logits = np.where(valid, logits, -np.inf)
+    mx = np.max(np.where(valid, logits, -1e300), axis=1, keepdims=True)
+    e = np.where(valid, np.exp(logits - mx), 0.0)
+    s = e.sum(axis=1, keepdims=True)
+    pri = np.where(s > 0, e / np.where(s > 0, s, 1), 0.0).astype(np.float32)
+    vals = rng.uniform(-1, 1, total).astype(np.float32)
+    cq = np.where(valid, rng.uniform(-1, 1, (total, MAX_LEGAL)), 0.0).astype(np.float32)
+    return np.ascontiguousarray(pri), vals, np.ascontiguousarray(cq)
+
+
+class OracleEngine:
+    def __init__(self):
+        self.m = MctsOracle()
+        self.o = self.m.o
+
+    def tree(self, B, M):
+        return new_tree(B, M)
+
+    def to_np(self, t):
+        return t
+
+    def legal(self, states):
+        m, n, _, _ = self.o.batch_legal_features_actions(states, want_features=False, want_actions=False)
+        return m, n
+
+    def expand_dense(self, t, cq, leaf, states, legal, n, pri, results):
+        return self.m.expand_dense(t, cq, leaf, states, legal, n, pri, results)
+
+    def root_noise(self, t, noise, eps):
+        self.m.root_noise(t, noise, t["root_node"], eps)
+
+    def select_slots(self, t, active, slots, max_root, c_puct, W):
+        return self.m.select_slots(t, active, t["root_node"], slots, max_root, c_puct, W)
+
+    def select_mask(self, t, active, alive, c_puct, W):
+        return self.m.select_mask(t, active, t["root_node"], alive, c_puct, W)
+
+    def replay(self, roots, paths, plen, leaf):
+        leaves = np.zeros((leaf.shape[0], 3424), np.uint8)
+        self.m.replay(roots, leaves, paths, plen, leaf)
+        return leaves
+
+    def expand_backprop(self, t, cq, leaf, states, legal, n, pri, results, vals, vl, vlen):
+        self.m.expand_backprop_dense(t, cq, leaf, states, legal, n, pri, results, vals, vl, vlen)
+
+
+class GpuEngine:
+    """Same interface over hive_neuralnet_amd.hive_gpu (all device work through the C-ABI)."""
+
+    def __init__(self):
+        import torch
+        from hive_neuralnet_amd import hive_gpu
+        self.torch = torch
+        self.ext = hive_gpu.load_extension()
+
+    def c(self, a):
+        return self.torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+    def tree(self, B, M):
+        return {k: self.c(v) for k, v in new_tree(B, M).items()}
+
+    def to_np(self, t):
+        return {k: v.cpu().numpy() for k, v in t.items()}
+
+    def args(self, t):
+        return [t["visit_count"], t["total_value"], t["prior"], t["parent_idx"], t["virtual_q_penalty"],
+                t["move_bytes"], t["action_idx"], t["first_child"], t["num_children"], t["is_terminal"],
+                t["terminal_value"], t["node_count"]]
+
+    def M(self, t):
+        return t["visit_count"].shape[1]
+
+    def legal(self, states):
+        m, n = self.ext.generate_legal_moves_batch(self.c(states), states.shape[0])
+        return m.cpu().numpy(), n.cpu().numpy()
+
+    def expand_dense(self, t, cq, leaf, states, legal, n, pri, results):
+        B = t["node_count"].shape[0]
+        was = self.ext.mcts_expand_dense_priors_batch(
+            *self.args(t), t["child_init_q"], self.c(cq), self.c(leaf), self.c(states), self.c(legal), self.c(n),
+            self.c(pri), self.c(results), B, leaf.shape[0], self.M(t))
+        return was.cpu().numpy()
+
+    def root_noise(self, t, noise, eps):
+        B = t["node_count"].shape[0]
+        self.ext.mcts_apply_root_noise(*self.args(t), self.c(noise.astype(np.float32)), t["root_node"],
+                                       noise.shape[1], eps, 1.0, B, self.M(t))
+
+    def select_slots(self, t, active, slots, max_root, c_puct, W):
+        B, C = slots.shape
+        out = self.ext.mcts_select_with_root_slots_batch(
+            *self.args(t), t["child_init_q"], self.c(active.astype(np.int8)), t["root_node"],
+            self.c(slots.astype(np.int32)), C, max_root, c_puct, B, W, self.M(t))
+        return tuple(o.cpu().numpy() for o in out)
+
+    def select_mask(self, t, active, alive, c_puct, W):
+        B, max_root = alive.shape
+        out = self.ext.mcts_select_with_root_mask_batch(
+            *self.args(t), t["child_init_q"], self.c(active.astype(np.int8)), t["root_node"],
+            self.c(alive.astype(np.int8)), max_root, c_puct, B, W, self.M(t))
+        return tuple(o.cpu().numpy() for o in out)
+
+    def replay(self, roots, paths, plen, leaf):
+        total = leaf.shape[0]
+        leaves = self.torch.zeros((total, 3424), dtype=self.torch.uint8, device="cuda")
+        self.ext.mcts_replay_batch(self.c(roots), leaves, self.c(paths), self.c(plen), self.c(leaf),
+                                   roots.shape[0], total)
+        return leaves.cpu().numpy()
+
+    def expand_backprop(self, t, cq, leaf, states, legal, n, pri, results, vals, vl, vlen):
+        B = t["node_count"].shape[0]
+        self.ext.mcts_expand_and_backprop_dense_priors_batch(
+            *self.args(t), t["child_init_q"], self.c(cq), self.c(leaf), self.c(states), self.c(legal), self.c(n),
+            self.c(pri), self.c(results), self.c(vals), self.c(vl), self.c(vlen), B, leaf.shape[0], self.M(t), 0.0)
+
+
+def run_search(engine, roots, *, seed=1, M=4096, C=4, W=2, waves=6, c_puct=1.25, eps=0.25, mode="slots"):
+    """Root expand + noise + `waves` select/replay/legal/expand-backup rounds.
+
+    Returns (final tree as numpy, list of per-wave records)."""
+    rng = np.random.default_rng(seed)
+    B = roots.shape[0]
+    t = engine.tree(B, M)
+    legal, n = engine.legal(roots)
+    pri, _, cq = synthetic_eval(rng, n, B)
+    results = roots[:, 3415].astype(np.int32)
+    active = (results == 0) & (n > 0)
+    leaf0 = np.where(active, 0, -1).astype(np.int32)
+    was = engine.expand_dense(t, cq, leaf0, roots, legal, n, pri, results)
+    nc = np.maximum(n, 1)
+    noise = np.zeros((B, int(nc.max())), np.float32)
+    for i in range(B):
+        noise[i, : n[i]] = rng.dirichlet([0.3] * max(1, n[i]))[: n[i]]
+    engine.root_noise(t, noise, eps)
+    order = np.argsort(-pri, axis=1, kind="stable")[:, :C]
+    slots = np.where(np.arange(C)[None, :] < n[:, None], order, -1).astype(np.int32)
+    alive = np.zeros((B, MAX_LEGAL), np.int8)
+    for i in range(B):
+        alive[i, slots[i][slots[i] >= 0]] = 1
+    records = [{"was_root": was}]
+    for _ in range(waves):
+        if mode == "slots":
+            leaf, paths, plen, vl, vlen = engine.select_slots(t, active, slots, MAX_LEGAL, c_puct, W)
+        else:
+            leaf, paths, plen, vl, vlen = engine.select_mask(t, active, alive, c_puct, W)
+        leaves = engine.replay(roots, paths, plen, leaf)
+        res = leaves[:, 3415].astype(np.int32)
+        lm, ln = engine.legal(leaves)
+        p2, v2, q2 = synthetic_eval(rng, ln, leaf.shape[0])
+        mid = engine.to_np(t)
+        mid_visits, mid_total = mid["visit_count"].copy(), mid["total_value"].copy()
+        engine.expand_backprop(t, q2, leaf, leaves, lm, ln, p2, res, v2, vl, vlen)
+        records.append({"leaf": leaf, "paths": paths, "plen": plen, "vl": vl, "vlen": vlen, "leaves": leaves,
+                        "mid_visits": mid_visits, "mid_total": mid_total})
+    return engine.to_np(t), records
+
+
+def tree_equal(a, b):
+    bad = []
+    for k in TREE_KEYS + ["root_node"]:
+        x, y = a[k], b[k]
+        if x.dtype == np.float32:
+            x, y = x.view(np.uint32), y.view(np.uint32)
+        if not np.array_equal(x, y):
+            bad.append(k)
+    return bad

@@ -1,0 +1,141 @@
+"""Pins of the MCTS tree oracle (oracle/hive_mcts_oracle.c): invariants the
+reference's tree kernels guarantee (mcts_tree.cuh:689-1234) and hand-built
+trees with known answers.  No reference test pins these kernels."""
+import numpy as np
+import pytest
+
+from mcts_driver import OracleEngine, run_search
+from oracle.mcts import MctsOracle, new_tree
+
+
+@pytest.fixture(scope="module")
+def roots(oracle):
+    st, _ = oracle.generate_positions(12, 7, 40, 0xC0FFEE)
+    return st
+
+
+def _check_counts(t, records):
+    """N(node) = simulations ending at node + sum of children's N; no outstanding virtual loss."""
+    B, M = t["visit_count"].shape
+    ended = np.zeros((B, M), np.int64)
+    for r in records[1:]:
+        for s, leaf in enumerate(r["leaf"]):
+            if leaf >= 0:
+                ended[s % B, leaf] += 1
+    vc, fc, nc = t["visit_count"], t["first_child"], t["num_children"]
+    for g in range(B):
+        for u in range(int(t["node_count"][g])):
+            kids = vc[g, fc[g, u]: fc[g, u] + nc[g, u]].sum() if fc[g, u] >= 0 else 0
+            assert vc[g, u] == ended[g, u] + kids, (g, u)
+            assert abs(float(t["total_value"][g, u])) <= vc[g, u] + 1e-4
+    assert not t["virtual_q_penalty"].any()
+
+
+@pytest.mark.parametrize("mode,W", [("slots", 1), ("slots", 2), ("mask", 3)])
+def test_search_invariants(roots, mode, W):
+    t, rec = run_search(OracleEngine(), roots, W=W, mode=mode, waves=5)
+    _check_counts(t, rec)
+    B = roots.shape[0]
+    # node pool accounting: 1 + children of every expanded node
+    for g in range(B):
+        expanded = t["first_child"][g] >= 0
+        assert t["node_count"][g] == 1 + t["num_children"][g][expanded].sum()
+    # mid-wave: each selection adds one virtual visit to every node it entered
+    prev = None
+    for r in rec[1:]:
+        if prev is not None:
+            entered = np.zeros_like(prev)
+            for s in range(r["leaf"].shape[0]):
+                for k in range(r["vlen"][s]):
+                    entered[s % B, r["vl"][s, k]] += 1
+            assert np.array_equal(r["mid_visits"] - prev, entered)
+        prev = None
+
+
+def test_children_in_legal_order(oracle, roots):
+    t, rec = run_search(OracleEngine(), roots, W=2, waves=4)
+    for g in range(roots.shape[0]):
+        if t["first_child"][g, 0] < 0:
+            continue
+        moves, n = oracle.legal_moves(roots[g])
+        f = t["first_child"][g, 0]
+        assert t["num_children"][g, 0] == n
+        assert np.array_equal(t["move_bytes"][g, f:f + n], moves[:n])
+        assert (t["parent_idx"][g, f:f + n] == 0).all()
+        cq, cr = oracle.centroid(roots[g])
+        assert [oracle.move_to_action(moves[i], cq, cr) for i in range(n)] == list(t["action_idx"][g, f:f + n])
+
+
+def _tiny_tree(priors, M=16):
+    t = new_tree(1, M)
+    n = len(priors)
+    t["first_child"][0, 0] = 1
+    t["num_children"][0, 0] = n
+    t["node_count"][0] = 1 + n
+    t["prior"][0, 1:1 + n] = priors
+    t["parent_idx"][0, 1:1 + n] = 0
+    for i in range(n):
+        t["move_bytes"][0, 1 + i] = [2, 0, 0, 0, 0, 0]  # PASS moves
+    return t
+
+
+def test_puct_known_answers_and_sign_alternation(oracle):
+    m = MctsOracle(oracle)
+    t = _tiny_tree([0.1, 0.6, 0.3])
+    alive = np.zeros((1, 256), np.int8)
+    alive[0, :3] = 1
+    # an unvisited root has sqrt(N)=0: every score is 0 and the first child wins
+    leaf, _, _, _, _ = m.select_mask(t, np.ones(1, np.int8), np.zeros(1, np.int32), alive, 1.25, 1)
+    assert leaf[0] == 1
+    t = _tiny_tree([0.1, 0.6, 0.3])
+    t["visit_count"][0, 0] = 1
+    leaf, paths, plen, vl, vlen = m.select_mask(t, np.ones(1, np.int8), np.zeros(1, np.int32), alive, 1.25, 1)
+    assert leaf[0] == 2 and plen[0] == 1 and vl[0, 0] == 2  # max prior wins with no child visits
+    assert t["visit_count"][0, 2] == 1 and t["total_value"][0, 2] == -1.0  # virtual loss
+    st = oracle.init_state(0)
+    leaves = np.repeat(st[None], 1, axis=0)
+    legal, nl = oracle.legal_moves(st)
+    z = np.zeros((1, 256), np.float32)
+    m.expand_backprop_dense(t, z, leaf, leaves, legal[None], np.array([0], np.int32), z, np.zeros(1, np.int32),
+                            np.array([0.5], np.float32), vl, vlen)
+    # the leaf was not expanded (n=0 given), so 0.0 is backed up; virtual loss undone
+    assert t["visit_count"][0, 2] == 1 and t["total_value"][0, 2] == 0.0
+    assert t["visit_count"][0, 0] == 2
+    # second simulation: child 2 now has N=1, W=0 -> q=0; PUCT favours child 3 (prior 0.3) over 2?
+    leaf2, _, _, vl2, vlen2 = m.select_mask(t, np.ones(1, np.int8), np.zeros(1, np.int32), alive, 1.25, 1)
+    # scores: c2: 0 + (1.25*0.6)*sqrt2/2 ; c3: (1.25*0.3)*sqrt2/1 -- equal in float32; first wins (node 2)
+    assert leaf2[0] == 2
+    # expanding sim with value v: W(leaf) = v, W(parent) = -v (sign alternation)
+    legal, nl = oracle.legal_moves(st)
+    pri = np.zeros((1, 256), np.float32)
+    pri[0, :nl] = 1.0 / nl
+    m.expand_backprop_dense(t, z, leaf2, leaves, legal[None], np.array([nl], np.int32), pri,
+                            np.zeros(1, np.int32), np.array([0.5], np.float32), vl2, vlen2)
+    assert t["num_children"][0, 2] == nl and t["first_child"][0, 2] == 4
+    assert t["total_value"][0, 2] == 0.5 and t["total_value"][0, 0] == -0.5
+    assert t["node_count"][0] == 4 + nl
+
+
+def test_terminal_and_pool_exhaustion(oracle):
+    m = MctsOracle(oracle)
+    t = _tiny_tree([0.5, 0.5], M=5)
+    t["visit_count"][0, 0] = 1
+    alive = np.zeros((1, 256), np.int8)
+    alive[0, :2] = 1
+    leaf, _, _, vl, vlen = m.select_mask(t, np.ones(1, np.int8), np.zeros(1, np.int32), alive, 1.0, 1)
+    st = oracle.init_state(0)
+    legal, nl = oracle.legal_moves(st)  # 4 placements > 2 free slots: the pool cannot take them
+    pri = np.full((1, 256), 0.25, np.float32)
+    z = np.zeros((1, 256), np.float32)
+    m.expand_backprop_dense(t, z, leaf, st[None], legal[None], np.array([nl], np.int32), pri,
+                            np.zeros(1, np.int32), np.array([0.9], np.float32), vl, vlen)
+    assert t["first_child"][0, leaf[0]] == -1 and t["node_count"][0] == 3
+    assert t["total_value"][0, leaf[0]] == 0.0  # not expanded: 0.0 backed up
+    # terminal leaf: white to move (turn even) after white won -> +1 for the leaf's player
+    leaf, _, _, vl, vlen = m.select_mask(t, np.ones(1, np.int8), np.zeros(1, np.int32), alive, 1.0, 1)
+    won = st.copy()
+    won[3415] = 1
+    m.expand_backprop_dense(t, z, leaf, won[None], legal[None], np.array([nl], np.int32), pri,
+                            np.ones(1, np.int32), np.array([0.9], np.float32), vl, vlen)
+    assert t["is_terminal"][0, leaf[0]] == 1 and t["terminal_value"][0, leaf[0]] == 1.0
+    assert t["total_value"][0, leaf[0]] == 1.0
