@@ -48,6 +48,13 @@ def parse_args():
     ap.add_argument("--cpu-threads", type=int, default=0, help="0 = min(16, cores)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="target CPU-thread seconds for the baseline")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-mcts", action="store_true", help="skip the C5 Gumbel self-play leg")
+    ap.add_argument("--mcts-only", action="store_true", help="run only the C5 leg (its own JSON line)")
+    ap.add_argument("--mcts-games", type=int, default=512)
+    ap.add_argument("--mcts-sims", type=int, default=4096)
+    ap.add_argument("--mcts-plies", type=int, default=1, help="timed self-play plies")
+    ap.add_argument("--mcts-warmup", type=int, default=1, help="untimed self-play plies before timing")
+    ap.add_argument("--mcts-roots", choices=("empty", "midgame"), default="empty")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 256 MiB device-to-device copy 3 times (rocprof counter calibration)")
     return ap.parse_args()
@@ -98,6 +105,127 @@ def cpu_baseline(states_np, threads, target_s):
     return out
 
 
+def mcts_cpu_baseline(net, leaves_np, threads, target_s):
+    """Leaf evaluation on the host: legal moves + root features + successor
+    features of every legal move (oracle/hive_oracle.c, compact list as the GPU)
+    + the FNN forward in numpy fp32.  Tree select/backup are left out (well
+    under 1% of a simulation on the CPU), so this is an upper bound on CPU sims/s."""
+    import numpy as np
+    from oracle import Oracle
+    orc = Oracle()
+    W = {k: v.detach().float().cpu().numpy() for k, v in net.state_dict().items()}
+
+    def lin(x, name):
+        return x @ W[name + ".weight"].T + W[name + ".bias"]
+
+    def encode(x):
+        h = 1.0 / (1.0 + np.exp(-lin(x, "fc1")))
+        mu = h.mean(axis=1, keepdims=True)
+        var = ((h - mu) ** 2).mean(axis=1, keepdims=True)
+        h = (h - mu) / np.sqrt(var + 1e-5) * W["ln1.weight"] + W["ln1.bias"]
+        return lin(h, "fc2")
+
+    def evaluate(states):
+        moves, n, feat, _ = orc.batch_legal_features_actions(states, threads=threads, want_actions=False)
+        a2r = np.repeat(np.arange(states.shape[0]), n).astype(np.int64)
+        mi = np.concatenate([np.arange(k) for k in n]).astype(np.int64) if len(n) else np.zeros(0, np.int64)
+        succ = orc.batch_successor_features(states, moves, a2r, mi, threads=threads)
+        emb = encode(np.concatenate([feat, succ]).astype(np.float32))
+        r, sc = emb[: states.shape[0]], emb[states.shape[0]:]
+        np.tanh(lin(r, "value_fc"))
+        np.tanh(lin(sc, "value_fc"))
+        x = 1.0 / (1.0 + np.exp(-lin(np.concatenate([r[a2r], sc], axis=1), "action_fc1")))
+        return lin(x, "action_fc2")
+
+    L = leaves_np.shape[0]
+    t0 = time.perf_counter()
+    evaluate(leaves_np[: min(L, 512)])
+    one = (time.perf_counter() - t0) / min(L, 512)
+    count = int(max(256, min(L, target_s / max(one, 1e-9) / 3)))
+    sample = leaves_np[:count]
+    rates = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        evaluate(sample)
+        rates.append(count / (time.perf_counter() - t0))
+    return {
+        "value": statistics.median(rates), "unit": "sims/s", "cores": threads, "kind": "port",
+        "sample": f"{count} leaf states from the GPU search's last wave, 3 passes, median; leaf evaluation only "
+                  f"(legal list + features + successor features via oracle/hive_oracle.c with {threads} pthreads, "
+                  "FNN large in numpy fp32)",
+    }
+
+
+def mcts_leg(args):
+    """C5: Gumbel-root self-play over `--mcts-games` games with `--mcts-sims`
+    simulations per move, k=16, FNN `large` random init (torch.manual_seed)."""
+    import numpy as np
+    import torch
+    from hive_neuralnet_amd import hive_gpu
+    from hive_neuralnet_amd.fnn import seeded_large
+    from hive_neuralnet_amd.orchestrator import FNNMCTSConfig, FNNMCTSOrchestrator
+
+    G, S = args.mcts_games, args.mcts_sims
+    net = seeded_large(SEED)
+    cfg = FNNMCTSConfig(num_simulations=S, max_num_considered_actions=16, batch_size=G,
+                        max_tree_nodes=1 + S * 256)
+    orch = FNNMCTSOrchestrator(net, cfg)
+    ext = orch.ext
+    if args.mcts_roots == "empty":
+        states = ext.create_initial_states(G, 0)
+    else:
+        states, _ = hive_gpu.random_positions(G, 0, 120, SEED)
+    torch.manual_seed(SEED + 1)
+    np.random.seed(SEED & 0xFFFF)
+    tree = orch._alloc_tree(G)
+    active = torch.ones((G,), dtype=torch.bool, device="cuda")
+
+    def ply():
+        r = orch.search_ply(states, tree, active)
+        orch.apply_and_rebase(states, tree, r)
+        active.logical_and_(ext.check_results_batch(states, G) == 0)
+
+    for _ in range(args.mcts_warmup):
+        ply()
+    orch.enable_counters()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.mcts_plies):
+        ply()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    c = {k: int(v.item()) for k, v in orch.counters.items()}
+    sims = c["sims"]
+    Lm = c["leaf_legal"] / max(1, sims)
+    Dm = c["vl_len"] / max(1, sims)
+    b_sim = 5976 + 535 * Lm + 16 * Dm
+    value = sims / wall
+    achieved = b_sim * value / 1e9
+    out = {
+        "metric": "MCTS sims/sec at 512 games", "value": value, "unit": "sims/s", "plies": args.mcts_plies,
+        "warmup_plies": args.mcts_warmup, "ms_per_ply": wall / args.mcts_plies * 1e3,
+        "config": {"workload": f"C5: Gumbel-root self-play, {G} games from the "
+                               f"{'empty board' if args.mcts_roots == 'empty' else 'C2-style mid-game roots'}, "
+                               f"{S} sims/move, k=16, wave schedule (2,4,8,16), FNN large random init",
+                   "games": G, "sims_per_move": S, "max_tree_nodes": 1 + S * 256, "seed": SEED,
+                   "roots": args.mcts_roots},
+        "simulations": sims, "sim_rows": c["rows"], "mean_leaf_legal": Lm, "mean_vl_len": Dm,
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": None,
+                     "bytes_per_sim": b_sim, "formula": "5976 + 535*L + 16*D"},
+    }
+    if not args.no_cpu:
+        orch.keep_last_leaves = True
+        orch.counters = None
+        cfg.num_simulations = min(S, 256)
+        orch.search_ply(states, tree, active)
+        leaves = orch.last_leaves.cpu().numpy()
+        threads = args.cpu_threads or max(1, min(16, os.cpu_count() or 1))
+        out["cpu_baseline"] = mcts_cpu_baseline(net, leaves, threads, args.cpu_seconds)
+        out["gpu_over_cpu"] = value / out["cpu_baseline"]["value"]
+    return out
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
@@ -113,6 +241,10 @@ def main():
             b.copy_(a)
         torch.cuda.synchronize()
         print(json.dumps({"copy_bytes": a.numel() * 4, "copies": 3}))
+        return
+
+    if args.mcts_only:
+        print(json.dumps(mcts_leg(args)))
         return
 
     from hive_neuralnet_amd import hive_gpu
@@ -189,6 +321,8 @@ def main():
         threads = args.cpu_threads or max(1, min(16, os.cpu_count() or 1))
         result["cpu_baseline"] = cpu_baseline(states.cpu().numpy(), threads, args.cpu_seconds)
         result["gpu_over_cpu"] = value / result["cpu_baseline"]["value"]
+    if not args.no_mcts:
+        result["mcts"] = mcts_leg(args)
     print(json.dumps(result))
 
 

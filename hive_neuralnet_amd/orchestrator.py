@@ -1,0 +1,542 @@
+"""Gumbel-root MCTS self-play over the MI355X engine: the counterpart of the
+reference's FNNMCTSOrchestrator (hive_fnn/fnn_mcts_orchestrator.py).
+
+Per ply (self_play_batch, :561-875): legal lists + root features, leaf
+evaluation of every legal successor with the FNN (`_eval_states`,
+:243-316), immediate-win override (:446-493), root candidates by prior with
+queen-surround reserve slots (:384-444), root expansion (:888-902) and
+Dirichlet noise (:904-925), four sequential-halving rounds of waves of
+root-slot simulations (:670-711, :982-1055), final Gumbel argmax (:714-731),
+visited-only policy target with adaptive temperature (:144-191, :738-755),
+apply + rebase (:812-818, :1122-1142).
+
+Differences from the reference, all deliberate:
+  * ties in every top-k are broken by the lowest slot (a stable descending
+    sort) -- torch.topk's tie order is unspecified, so the reference's is not
+    reproducible;
+  * per-game Python loops (immediate wins, tree rebase, history) are
+    vectorised; the results are the same;
+  * the tree kernels apply each game's simulations in simulation order (see
+    include/hive_gpu.h), where the reference's atomics race.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+
+import numpy as np
+import torch
+
+from . import hive_gpu
+from .fnn import HiveFNN
+
+_OFF_TURN = 3412
+_OFF_HEIGHT = 2645
+_OFF_QUEEN_CELL = 3392
+_GUMBEL_ROUNDS = 4
+_GUMBEL_WAVE_SCHEDULE = (2, 4, 8, 16)
+_NUM_CELLS = 529
+
+
+@dataclass
+class FNNMCTSConfig:  # fnn_mcts_orchestrator.py:45-82 (same fields and defaults)
+    num_simulations: int = 128
+    max_num_considered_actions: int = 16
+    c_puct: float = 1.25
+    c_visit: float = 50.0
+    c_scale: float = 1.0
+    temperature: float = 1.0
+    temperature_drop_move: int = 20
+    batch_size: int = 128
+    max_game_length: int = 300
+    expansion_mask: int = 0
+    wave_parallel: bool = True
+    wave_size: int = 4
+    deterministic_non_root: bool = False
+    virtual_q_penalty: float = 0.25
+    non_root_sigma: float = 4.0
+    dirichlet_alpha: float = 0.3
+    dirichlet_epsilon: float = 0.25
+    max_tree_nodes: int = 65536
+    queen_surround_reserve_slots: int = 6
+    queen_surround_reserve_immobile_only: bool = True
+    root_q_min_visits: int = 0
+    short_forced_win_probe: bool = False
+    probe_win_in_one: bool = True
+    probe_check_opponent_wins: bool = True
+    probe_win_in_two: bool = True
+    policy_target_temperature: float = 1.0
+    adaptive_policy_target_temperature: bool = True
+    policy_target_top1_cap: float = 0.7
+    policy_target_min_temperature: float = 1.0
+    policy_target_max_temperature: float = 7.0
+    final_value_ply_count: int = 3
+    final_value_weight: float = 2.0
+    rebase_tree_each_move: bool = True
+
+
+@dataclass
+class FNNTrainingExample:  # hive_fnn/fnn_replay_buffer.py record shape
+    state_bytes: np.ndarray
+    policy_target: np.ndarray
+    value_target: float
+    use_for_policy: bool = True
+    use_for_value: bool = True
+    value_weight: float = 1.0
+
+
+@dataclass
+class PlyResult:
+    chosen_slot: torch.Tensor
+    legal_moves: torch.Tensor
+    num_legal: torch.Tensor
+    policy: torch.Tensor
+    slot_visits: torch.Tensor
+    has_actions: torch.Tensor
+    simulations: int = 0
+    stats: dict = field(default_factory=dict)
+
+
+def topk_stable(x: torch.Tensor, k: int):
+    """Top-k along dim 1, ties to the lowest index."""
+    vals, idx = torch.sort(x, dim=1, descending=True, stable=True)
+    return vals[:, :k], idx[:, :k]
+
+
+class FNNMCTSOrchestrator:
+    def __init__(self, net: HiveFNN, config: FNNMCTSConfig | None = None) -> None:
+        self.ext = hive_gpu.load_extension()
+        self.config = config or FNNMCTSConfig()
+        self.net = net
+        self._max_nodes = int(self.config.max_tree_nodes)
+        self._max_legal = int(self.ext.MAX_LEGAL_MOVES)
+        self._slot_idx = torch.arange(self._max_legal, device="cuda", dtype=torch.int64).unsqueeze(0)
+        self._neighbor_cells = self._build_neighbor_cells()
+        self.last_policy_temperature_stats: dict[str, float] = {}
+        # optional device-side counters (no host sync): simulations run, legal
+        # moves at their leaves, virtual-loss path lengths, successor rows
+        self.counters: dict[str, torch.Tensor] | None = None
+        self.keep_last_leaves = False
+        self.last_leaves: torch.Tensor | None = None
+
+    def enable_counters(self) -> None:
+        self.counters = {k: torch.zeros((), dtype=torch.int64, device="cuda")
+                         for k in ("sims", "leaf_legal", "vl_len", "rows")}
+
+    # ---- helpers -------------------------------------------------------
+    def _build_neighbor_cells(self) -> torch.Tensor:
+        cells = torch.arange(_NUM_CELLS)
+        row, col = cells // 23, cells % 23
+        out = torch.full((_NUM_CELLS, 6), -1, dtype=torch.int64)
+        for i, (dq, dr) in enumerate(((1, 0), (1, -1), (0, -1), (-1, 0), (-1, 1), (0, 1))):
+            nr, nc = row + dr, col + dq
+            ok = (nr >= 0) & (nr < 23) & (nc >= 0) & (nc < 23)
+            out[:, i] = torch.where(ok, nr * 23 + nc, torch.full_like(nr, -1))
+        return out.cuda()
+
+    def _rows(self, n: int) -> torch.Tensor:
+        return torch.arange(n, device="cuda", dtype=torch.int64).unsqueeze(1)
+
+    def _alloc_tree(self, B: int) -> dict:  # :195-214
+        M = self._max_nodes
+        z = lambda dt: torch.zeros(B, M, dtype=dt, device="cuda")  # noqa: E731
+        return {
+            "visit_count": z(torch.int32), "total_value": z(torch.float32), "prior": z(torch.float32),
+            "virtual_q_penalty": z(torch.float32),
+            "parent_idx": torch.full((B, M), -1, dtype=torch.int32, device="cuda"),
+            "move_bytes": torch.zeros(B, M, 6, dtype=torch.uint8, device="cuda"),
+            "action_idx": torch.full((B, M), -1, dtype=torch.int32, device="cuda"),
+            "first_child": torch.full((B, M), -1, dtype=torch.int32, device="cuda"),
+            "num_children": z(torch.int32), "is_terminal": z(torch.int8), "terminal_value": z(torch.float32),
+            "node_count": torch.ones(B, dtype=torch.int32, device="cuda"),
+            "root_node": torch.zeros(B, dtype=torch.int32, device="cuda"),
+            "child_init_q": z(torch.float32),
+        }
+
+    def _reset_rows(self, tree: dict, rows: torch.Tensor) -> None:  # _reroot_tree rebase, :1122-1142
+        if rows.numel() == 0:
+            return
+        for k, fill in (("visit_count", 0), ("total_value", 0), ("prior", 0), ("parent_idx", -1),
+                        ("move_bytes", 0), ("action_idx", -1), ("first_child", -1), ("num_children", 0),
+                        ("is_terminal", 0), ("terminal_value", 0), ("child_init_q", 0)):
+            tree[k][rows] = fill
+        tree["node_count"][rows] = 1
+        tree["root_node"][rows] = 0
+
+    def _tree_args(self, tree: dict) -> list:
+        return [tree["visit_count"], tree["total_value"], tree["prior"], tree["parent_idx"],
+                tree["virtual_q_penalty"], tree["move_bytes"], tree["action_idx"], tree["first_child"],
+                tree["num_children"], tree["is_terminal"], tree["terminal_value"], tree["node_count"]]
+
+    # ---- evaluation (:243-316) -----------------------------------------
+    def _eval_states(self, states, legal_moves, num_legal, total, root_features=None):
+        MAX_L = self._max_legal
+        n64 = num_legal.to(torch.int64)
+        if root_features is None:
+            root_features = self.ext.extract_fnn_features_batch(states, legal_moves, num_legal, total)
+        if total == 0:
+            empty = torch.zeros(0, MAX_L, dtype=torch.float32, device="cuda")
+            return empty, empty.new_zeros((0,)), empty
+        valid = self._slot_idx < n64.unsqueeze(1)
+        action_to_root = self._rows(total).expand_as(valid)[valid]
+        move_indices = self._slot_idx.expand_as(valid)[valid]
+        n_total = int(action_to_root.shape[0])
+        if n_total == 0:
+            with torch.inference_mode():
+                root_values = self.net.value_head(self.net.encode(root_features)).squeeze(-1).float()
+            z = torch.zeros(total, MAX_L, dtype=torch.float32, device="cuda")
+            return z, root_values, z.clone()
+        succ = self.ext.fnn_successor_features_batch(states, legal_moves, action_to_root, move_indices, n_total)
+        with torch.inference_mode():
+            emb = self.net.encode(torch.cat([root_features, succ], dim=0))
+            root_emb, succ_emb = emb[:total], emb[total:]
+            root_values = self.net.value_head(root_emb).squeeze(-1).float()
+            child_values = self.net.value_head(succ_emb).squeeze(-1).float()
+            logits = self.net.score_actions(root_emb[action_to_root], succ_emb).float()
+        legal_logits = torch.full((total, MAX_L), -1e30, dtype=torch.float32, device="cuda")
+        legal_logits[valid] = logits
+        prior = torch.softmax(legal_logits, dim=1).masked_fill(~valid, 0.0)
+        child_q = torch.zeros(total, MAX_L, dtype=torch.float32, device="cuda")
+        child_q[valid] = -child_values
+        return prior, root_values, child_q
+
+    # ---- root candidates (:318-444) ------------------------------------
+    def _queen_surround_count(self, states, queen_color):
+        rows = torch.arange(states.shape[0], device="cuda", dtype=torch.int64)
+        qbase = (_OFF_QUEEN_CELL + 2 * queen_color).to(torch.int64)
+        qcell = states[rows, qbase].to(torch.int32) | (states[rows, qbase + 1].to(torch.int32) << 8)
+        valid_queen = qcell != 0xFFFF
+        neigh = self._neighbor_cells[qcell.clamp(0, _NUM_CELLS - 1).to(torch.int64)]
+        heights = states[:, _OFF_HEIGHT:_OFF_HEIGHT + _NUM_CELLS].to(torch.int16)
+        nh = heights.gather(1, neigh.clamp(min=0))
+        surround = ((neigh >= 0) & (nh > 0)).sum(dim=1).to(torch.int32)
+        return torch.where(valid_queen, surround, torch.zeros_like(surround)), qcell
+
+    def _queen_surround_qualifying_mask(self, states, legal_moves, num_legal, total):
+        valid = self._slot_idx < num_legal.to(torch.int64).unsqueeze(1)
+        if total == 0 or not bool(valid.any().item()):
+            return torch.zeros((total, self._max_legal), dtype=torch.bool, device="cuda")
+        root_rows = self._rows(total).expand_as(valid)[valid]
+        move_indices = self._slot_idx.expand_as(valid)[valid]
+        n_total = int(root_rows.shape[0])
+        child = states[root_rows].clone()
+        self.ext.apply_moves_batch(child, legal_moves[root_rows, move_indices].contiguous(), n_total)
+        parent_turn = states[:, _OFF_TURN].to(torch.int32) | (states[:, _OFF_TURN + 1].to(torch.int32) << 8)
+        before, _ = self._queen_surround_count(states, ((parent_turn + 1) & 1).to(torch.int64))
+        child_turn = child[:, _OFF_TURN].to(torch.int32) | (child[:, _OFF_TURN + 1].to(torch.int32) << 8)
+        after, _ = self._queen_surround_count(child, (child_turn & 1).to(torch.int64))
+        qual_flat = after > before[root_rows]
+        if self.config.queen_surround_reserve_immobile_only and bool(qual_flat.any().item()):
+            qual_flat &= ~self.ext.queen_escape_flags_batch(child, n_total).to(torch.bool)
+        qual = torch.zeros((total, self._max_legal), dtype=torch.bool, device="cuda")
+        qual[valid] = qual_flat
+        return qual
+
+    def _root_candidate_slots(self, states, legal_moves, num_legal, priors, legal_logits, total,
+                              allowed_slot_mask=None):
+        max_legal = self._max_legal
+        k = min(int(self.config.max_num_considered_actions), max_legal)
+        valid = self._slot_idx < num_legal.to(torch.int64).unsqueeze(1)
+        if allowed_slot_mask is not None:
+            valid &= allowed_slot_mask
+        reserve = min(int(self.config.queen_surround_reserve_slots), k)
+        if reserve <= 0:
+            u = torch.rand(total, max_legal, device="cuda").clamp(1e-4, 1 - 1e-4)
+            g = torch.where(valid, -torch.log(-torch.log(u)), torch.full_like(u, -1e30))
+            return topk_stable(g + legal_logits, k)[1].to(torch.int32)
+        qual = self._queen_surround_qualifying_mask(states, legal_moves, num_legal, total)
+        reserve_scores = torch.where(qual, priors, torch.full_like(priors, -1e30))
+        reserve_per_game = qual.sum(dim=1).clamp(max=reserve)
+        _, reserve_order = topk_stable(reserve_scores, reserve)
+        reserve_valid = torch.arange(reserve, device="cuda").unsqueeze(0) < reserve_per_game.unsqueeze(1)
+        reserve_cand = torch.where(reserve_valid, reserve_order.to(torch.int32),
+                                   torch.full_like(reserve_order, -1, dtype=torch.int32))
+        chosen = torch.zeros((total, max_legal), dtype=torch.bool, device="cuda")
+        rows = self._rows(total).expand_as(reserve_valid)[reserve_valid]
+        chosen[rows, reserve_order[reserve_valid]] = True
+        fill_scores = torch.where(valid & ~chosen, priors, torch.full_like(priors, -1e30))
+        _, fill_order = topk_stable(fill_scores, k)
+        fill_keep = (k - reserve_per_game).clamp(min=0)
+        fill_valid = torch.arange(k, device="cuda").unsqueeze(0) < fill_keep.unsqueeze(1)
+        fill_cand = torch.where(fill_valid, fill_order.to(torch.int32), torch.full_like(fill_order, -1,
+                                                                                          dtype=torch.int32))
+        return torch.cat([reserve_cand, fill_cand], dim=1)[:, :k]
+
+    def _find_immediate_wins(self, states, legal_moves, num_legal, total):  # :446-493, vectorised
+        winners = torch.full((total,), -1, dtype=torch.int64, device="cuda")
+        valid = self._slot_idx < num_legal.to(torch.int64).unsqueeze(1)
+        if total == 0 or not bool(valid.any().item()):
+            return winners
+        a2r = self._rows(total).expand_as(valid)[valid]
+        mi = self._slot_idx.expand_as(valid)[valid]
+        n_total = int(a2r.shape[0])
+        child = states[a2r].clone()
+        self.ext.apply_moves_batch(child, legal_moves[a2r, mi].contiguous(), n_total)
+        results = self.ext.check_results_batch(child, n_total)
+        is_white = (states[a2r, _OFF_TURN].to(torch.int32) % 2) == 0
+        win = ((results == 1) & is_white) | ((results == 2) & ~is_white)
+        first = torch.full((total,), self._max_legal, dtype=torch.int64, device="cuda")
+        first.scatter_reduce_(0, a2r[win], mi[win], reduce="amin")
+        return torch.where(first < self._max_legal, first, winners)
+
+    # ---- tree steps ----------------------------------------------------
+    def _expand_root_if_needed(self, tree, states, legal_moves, num_legal, priors, child_q, game_active, B):
+        root = tree["root_node"]
+        fc = tree["first_child"][torch.arange(B, device="cuda"), root]
+        needs = (fc < 0) & game_active.to(torch.bool)
+        if not bool(needs.any().item()):
+            return
+        leaf = torch.where(needs, root.to(torch.int32), torch.full_like(root, -1, dtype=torch.int32))
+        results = self.ext.check_results_batch(states, B)
+        self.ext.mcts_expand_dense_priors_batch(*self._tree_args(tree), tree["child_init_q"], child_q, leaf, states,
+                                                legal_moves, num_legal, priors, results, B, B, self._max_nodes)
+
+    def _apply_root_dirichlet(self, tree, B, active):  # :904-925
+        cfg = self.config
+        nc = tree["num_children"][torch.arange(B, device="cuda"), tree["root_node"]].cpu().numpy()
+        act = active.cpu().numpy()
+        max_nc = int(nc.max()) if nc.size and nc.max() > 0 else 1
+        noise = np.zeros((B, max_nc), dtype=np.float32)
+        for i in range(B):
+            n = int(nc[i])
+            if n == 0 or not act[i]:
+                continue
+            alpha = max(0.03, min(cfg.dirichlet_alpha, 10.0 / n))
+            noise[i, :n] = np.random.dirichlet([alpha] * n)
+        self.ext.mcts_apply_root_noise(*self._tree_args(tree), torch.from_numpy(noise).cuda(), tree["root_node"],
+                                       max_nc, cfg.dirichlet_epsilon, 1.0, B, self._max_nodes)
+
+    def _run_simulations_for_root_slots(self, tree, root_states, game_active, root_slots, B, per_slot, wave_size):
+        cfg = self.config
+        C = int(root_slots.shape[1])
+        W = max(1, int(wave_size))
+        q_penalty = float(cfg.virtual_q_penalty) if cfg.deterministic_non_root and W > 1 else 0.0
+        sims = 0
+        for wave in range(math.ceil(per_slot / W)):
+            w = min(W, per_slot - wave * W)
+            total = w * C * B
+            (leaf_idx, leaf_states, legal, nl, feat, results, vl, vlen) = \
+                self.ext.mcts_select_replay_legal_fnn_root_slots_batch(
+                    *self._tree_args(tree), tree["child_init_q"], root_states, game_active, tree["root_node"],
+                    root_slots, C, self._max_legal, cfg.c_puct, B, w, self._max_nodes, cfg.deterministic_non_root,
+                    cfg.non_root_sigma, q_penalty)
+            if self.counters is not None:
+                live = leaf_idx >= 0
+                self.counters["sims"] += live.sum()
+                self.counters["leaf_legal"] += torch.where(live, nl, torch.zeros_like(nl)).sum()
+                self.counters["vl_len"] += torch.where(live, vlen, torch.zeros_like(vlen)).sum()
+                self.counters["rows"] += total
+            if self.keep_last_leaves:
+                self.last_leaves = leaf_states[leaf_idx >= 0]
+            priors, vals, child_q = self._eval_states(leaf_states, legal, nl, total, feat)
+            self.ext.mcts_expand_and_backprop_dense_priors_batch(
+                *self._tree_args(tree), tree["child_init_q"], child_q, leaf_idx, leaf_states, legal, nl, priors,
+                results, vals, vl, vlen, B, total, self._max_nodes, q_penalty)
+            sims += total
+        return sims
+
+    def _root_child_stats(self, tree, B, slots):  # _gather_root_candidate_stats / _gather_root_child_stats
+        row = torch.arange(B, device="cuda", dtype=torch.long)
+        root = tree["root_node"]
+        fc = tree["first_child"][row, root].to(torch.long)
+        nc = tree["num_children"][row, root].to(torch.long)
+        slots = slots.to(torch.long)
+        valid = (slots >= 0) & (fc.unsqueeze(1) >= 0) & (slots < nc.unsqueeze(1))
+        idx = (fc.unsqueeze(1) + slots.clamp(min=0)).clamp(0, self._max_nodes - 1)
+        r2 = row.unsqueeze(1).expand_as(idx)
+        v_raw = tree["visit_count"][r2, idx]
+        t_raw = tree["total_value"][r2, idx]
+        visits = torch.where(valid, v_raw, torch.zeros_like(v_raw))
+        q = torch.where(valid & (v_raw > int(self.config.root_q_min_visits)),
+                        -t_raw / v_raw.clamp(min=1).float(), torch.zeros_like(t_raw))
+        return visits, q
+
+    def _build_policy_target(self, sampled_logits, valid_slot):  # :144-191
+        cfg = self.config
+
+        def soft(temp):
+            p = torch.softmax(sampled_logits / temp, dim=1)
+            p = torch.where(valid_slot, p, torch.zeros_like(p))
+            return p / p.sum(dim=1, keepdim=True).clamp_min(1e-12)
+
+        if not cfg.adaptive_policy_target_temperature:
+            t = torch.full((sampled_logits.shape[0], 1), max(float(cfg.policy_target_temperature), 1e-6),
+                           dtype=sampled_logits.dtype, device=sampled_logits.device)
+            return soft(t), t.squeeze(1)
+        lo_t = max(float(cfg.policy_target_min_temperature), 1.0)
+        hi_t = max(float(cfg.policy_target_max_temperature), lo_t)
+        cap = min(max(float(cfg.policy_target_top1_cap), 0.0), 1.0)
+        base = torch.full((sampled_logits.shape[0], 1), lo_t, dtype=sampled_logits.dtype,
+                          device=sampled_logits.device)
+        probs = soft(base)
+        need = probs.max(dim=1, keepdim=True).values > cap
+        if not bool(need.any().item()) or hi_t <= lo_t:
+            return probs, base.squeeze(1)
+        low, high = base.clone(), torch.full_like(base, hi_t)
+        for _ in range(12):
+            mid = (low + high) * 0.5
+            sharp = soft(mid).max(dim=1, keepdim=True).values > cap
+            low = torch.where(need & sharp, mid, low)
+            high = torch.where(need & ~sharp, mid, high)
+        final = torch.where(need, high, base)
+        return soft(final), final.squeeze(1)
+
+    # ---- one ply of search ---------------------------------------------
+    def search_ply(self, states: torch.Tensor, tree: dict, active_mask: torch.Tensor) -> PlyResult:
+        """Root evaluation + Gumbel sequential halving for every active game (:589-755)."""
+        cfg = self.config
+        if cfg.short_forced_win_probe:
+            raise NotImplementedError("short_forced_win_probe (root tactical probes) is not part of this engine")
+        cfg.max_num_considered_actions = max(1, min(cfg.max_num_considered_actions, self._max_legal))
+        B = states.shape[0]
+        MAX_L = self._max_legal
+        legal, nl, root_feat = self.ext.generate_legal_moves_and_fnn_features_batch(states, B)
+        n64 = nl.to(torch.int64)
+        has_actions = active_mask & (n64 > 0)
+        priors, _, child_q = self._eval_states(states, legal, nl, B, root_feat)
+        valid_slot = self._slot_idx < n64.unsqueeze(1)
+        allowed = valid_slot
+        wins = self._find_immediate_wins(states, legal, nl, B)
+        has_win = wins >= 0
+        if bool(has_win.any().item()):
+            # the reference clears priors and child Q of EVERY game in the batch
+            # once any game has a winning move (fnn_mcts_orchestrator.py:624-627)
+            priors.zero_()
+            priors[has_win, wins[has_win]] = 1.0
+            child_q.zero_()
+        search_rows = has_actions & ~has_win
+        legal_logits = torch.where(allowed, priors.clamp(min=1e-20).log(), torch.full_like(priors, -1e30))
+        u = torch.rand(B, MAX_L, device="cuda").clamp(1e-4, 1 - 1e-4)
+        gumbel = torch.where(allowed, -torch.log(-torch.log(u)), torch.full_like(u, -1e30))
+        topk_slots = self._root_candidate_slots(states, legal, nl, priors, legal_logits, B, allowed)
+        game_active = search_rows.to(torch.int8)
+        self._expand_root_if_needed(tree, states, legal, nl, priors, child_q, game_active, B)
+        self._apply_root_dirichlet(tree, B, search_rows)
+        slot_visits = torch.zeros(B, MAX_L, dtype=torch.int32, device="cuda")
+        probs = torch.zeros(B, MAX_L, dtype=torch.float32, device="cuda")
+        chosen = torch.zeros((B,), dtype=torch.long, device="cuda")
+        sims = 0
+        stats: dict = {}
+        if bool(search_rows.any().item()):
+            cand = topk_slots.to(torch.int32)
+            cvalid = torch.gather(valid_slot, 1, cand.long().clamp(min=0)) & (cand >= 0)
+            cand = torch.where(cvalid, cand, torch.full_like(cand, -1))
+            per_round = max(1, cfg.num_simulations // _GUMBEL_ROUNDS)
+            for r in range(_GUMBEL_ROUNDS):
+                cvalid = cand >= 0
+                C = int(cand.shape[1])
+                wave = _GUMBEL_WAVE_SCHEDULE[min(r, len(_GUMBEL_WAVE_SCHEDULE) - 1)] if cfg.wave_parallel else 1
+                sims += self._run_simulations_for_root_slots(tree, states, game_active, cand, B,
+                                                             max(1, per_round // C), wave)
+                if C <= 1:
+                    continue
+                keep_n = (cvalid.sum(dim=1) // 2).clamp(min=1)
+                max_keep = C // 2
+                visits, q = self._root_child_stats(tree, B, cand)
+                sigma = (cfg.c_visit + visits.max()) * cfg.c_scale
+                score = (torch.gather(gumbel + legal_logits, 1, cand.long().clamp(min=0)) + sigma * q).float()
+                score = torch.where(cvalid, score, torch.full_like(score, -1e30))
+                _, keep_pos = topk_stable(score, max_keep)
+                keep_ok = torch.arange(max_keep, device="cuda").unsqueeze(0) < keep_n.unsqueeze(1)
+                cand = torch.where(keep_ok, torch.gather(cand, 1, keep_pos), torch.full_like(keep_pos, -1,
+                                                                                            dtype=torch.int32))
+            cvalid = cand >= 0
+            visits, q = self._root_child_stats(tree, B, cand)
+            sigma = (cfg.c_visit + visits.max()) * cfg.c_scale
+            final = (torch.gather(gumbel + legal_logits, 1, cand.long().clamp(min=0)) + sigma * q).float()
+            final = torch.where(cvalid, final, torch.full_like(final, -1e30))
+            pos = torch.argmax(final, dim=1)
+            chosen = torch.gather(cand, 1, pos.unsqueeze(1)).squeeze(1).clamp(min=0).to(torch.long)
+            slot_visits, slot_q = self._root_child_stats(tree, B, self._slot_idx.expand(B, -1))
+            visited = (slot_visits > 0) & valid_slot
+            max_n = slot_visits.float().max(dim=1, keepdim=True).values
+            sampled = torch.where(visited, legal_logits + (cfg.c_visit + max_n) * cfg.c_scale * slot_q,
+                                  torch.full_like(legal_logits, -1e30))
+            probs, temps = self._build_policy_target(sampled, valid_slot)
+            used = search_rows & visited.any(dim=1)
+            if bool(used.any().item()):
+                t = temps[used].detach().float().cpu().numpy()
+                stats = {"sum": float(t.sum()), "count": int(t.shape[0]), "min": float(t.min()),
+                         "max": float(t.max())}
+        if bool(has_win.any().item()):
+            slot_visits[has_win] = 0
+            slot_visits[has_win, wins[has_win]] = cfg.num_simulations
+            probs[has_win] = 0.0
+            probs[has_win, wins[has_win]] = 1.0
+            chosen = torch.where(has_win, wins, chosen)
+        return PlyResult(chosen, legal, nl, probs, slot_visits, has_actions, sims, stats)
+
+    def apply_and_rebase(self, states, tree, ply: PlyResult):
+        B = states.shape[0]
+        move = torch.zeros((B, 6), dtype=torch.uint8, device="cuda")
+        idx = torch.nonzero(ply.has_actions, as_tuple=False).squeeze(1)
+        if idx.numel():
+            move[idx] = ply.legal_moves[idx, ply.chosen_slot[idx].clamp(max=self._max_legal - 1)]
+        self.ext.apply_moves_batch(states, move, B)
+        fc = tree["first_child"][torch.arange(B, device="cuda"), tree["root_node"]]
+        moved = ply.has_actions & (fc >= 0)
+        if self.config.rebase_tree_each_move:
+            self._reset_rows(tree, torch.nonzero(moved, as_tuple=False).squeeze(1))
+            return
+        # keep the chosen child's subtree (fnn_mcts_orchestrator.py:1143-1153)
+        new_roots = torch.where(moved, (fc + ply.chosen_slot.to(torch.int32)).to(torch.int32), tree["root_node"])
+        tree["root_node"].copy_(new_roots)
+        tree["parent_idx"].scatter_(1, new_roots.long().unsqueeze(1),
+                                    torch.full((B, 1), -1, dtype=torch.int32, device="cuda"))
+
+    # ---- full games ----------------------------------------------------
+    def self_play_batch(self, start_states: torch.Tensor | None = None) -> list[list[FNNTrainingExample]]:
+        cfg = self.config
+        B = cfg.batch_size
+        states = start_states.cuda().contiguous() if start_states is not None else \
+            self.ext.create_initial_states(B, cfg.expansion_mask)
+        tree = self._alloc_tree(B)
+        active = torch.ones((B,), dtype=torch.bool, device="cuda")
+        moves_done = torch.zeros((B,), dtype=torch.int64, device="cuda")
+        histories: list[list] = [[] for _ in range(B)]
+        t_sum, t_count, t_min, t_max = 0.0, 0, float("inf"), 0.0
+        while bool(active.any().item()):
+            ply = self.search_ply(states, tree, active)
+            if ply.stats:
+                t_sum += ply.stats["sum"]
+                t_count += ply.stats["count"]
+                t_min = min(t_min, ply.stats["min"])
+                t_max = max(t_max, ply.stats["max"])
+            active &= ply.num_legal > 0
+            if not bool(ply.has_actions.any().item()):
+                break
+            has_cpu = ply.has_actions.cpu().numpy()
+            n_cpu = ply.num_legal.cpu().numpy()
+            st_cpu = states.cpu().numpy()
+            pr_cpu = ply.policy.cpu().numpy()
+            for i in np.nonzero(has_cpu)[0]:
+                histories[i].append((st_cpu[i].copy(), pr_cpu[i, : n_cpu[i]].astype(np.float32), True))
+            self.apply_and_rebase(states, tree, ply)
+            moves_done += ply.has_actions.to(torch.int64)
+            res = self.ext.check_results_batch(states, B)
+            active &= (res == 0) & (moves_done < cfg.max_game_length)
+        final = self.ext.check_results_batch(states, B).cpu().numpy()
+        out: list[list[FNNTrainingExample]] = [[] for _ in range(B)]
+        for i in range(B):
+            winner = int(final[i])
+            use_v = winner != 0
+            weighted_from = len(histories[i]) - max(0, int(cfg.final_value_ply_count))
+            for h, (sb, pi, use_p) in enumerate(histories[i]):
+                turn = int(sb[_OFF_TURN]) | (int(sb[_OFF_TURN + 1]) << 8)
+                value = self._result_to_value(winner, turn)
+                w = float(cfg.final_value_weight) if (use_v and h >= weighted_from) else 1.0
+                out[i].append(FNNTrainingExample(sb, pi, float(value), use_p, use_v, w))
+        if t_count:
+            self.last_policy_temperature_stats = {"mean": t_sum / t_count, "min": t_min, "max": t_max,
+                                                  "count": float(t_count)}
+        else:
+            lo = float(cfg.policy_target_min_temperature)
+            self.last_policy_temperature_stats = {"mean": lo, "min": lo, "max": lo, "count": 0.0}
+        return out
+
+    @staticmethod
+    def _result_to_value(result: int, turn: int) -> float:  # :1155-1161
+        if result == 0 or result == 3:
+            return 0.0
+        white = turn % 2 == 0
+        return 1.0 if (result == 1 and white) or (result == 2 and not white) else -1.0

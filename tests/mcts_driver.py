@@ -144,6 +144,7 @@ def run_search(engine, roots, *, seed=1, M=4096, C=4, W=2, waves=6, c_puct=1.25,
     rng = np.random.default_rng(seed)
     B = roots.shape[0]
     t = engine.tree(B, M)
+    start_visits = engine.to_np(t)["visit_count"].copy()
     legal, n = engine.legal(roots)
     pri, _, cq = synthetic_eval(rng, n, B)
     results = roots[:, 3415].astype(np.int32)
@@ -160,7 +161,7 @@ def run_search(engine, roots, *, seed=1, M=4096, C=4, W=2, waves=6, c_puct=1.25,
     alive = np.zeros((B, MAX_LEGAL), np.int8)
     for i in range(B):
         alive[i, slots[i][slots[i] >= 0]] = 1
-    records = [{"was_root": was}]
+    records = [{"was_root": was, "post_visits": engine.to_np(t)["visit_count"].copy(), "start": start_visits}]
     for _ in range(waves):
         if mode == "slots":
             leaf, paths, plen, vl, vlen = engine.select_slots(t, active, slots, MAX_LEGAL, c_puct, W)
@@ -173,8 +174,9 @@ def run_search(engine, roots, *, seed=1, M=4096, C=4, W=2, waves=6, c_puct=1.25,
         mid = engine.to_np(t)
         mid_visits, mid_total = mid["visit_count"].copy(), mid["total_value"].copy()
         engine.expand_backprop(t, q2, leaf, leaves, lm, ln, p2, res, v2, vl, vlen)
+        post_visits = engine.to_np(t)["visit_count"].copy()
         records.append({"leaf": leaf, "paths": paths, "plen": plen, "vl": vl, "vlen": vlen, "leaves": leaves,
-                        "mid_visits": mid_visits, "mid_total": mid_total})
+                        "mid_visits": mid_visits, "mid_total": mid_total, "post_visits": post_visits})
     return engine.to_np(t), records
 
 

@@ -1,0 +1,165 @@
+"""Gumbel self-play orchestrator on the GPU, every tree call shadowed by the oracle.
+
+A real search ply (FNN `large`, seeded) runs through
+hive_neuralnet_amd.orchestrator; each MCTS entry point it calls
+(root expansion, root noise, root-slot selection, replay, expansion + backup)
+is wrapped so that the same call, with the same inputs copied to the host, is
+applied to a host mirror of the tree by the C tree oracle.  Outputs and the
+whole tree must stay bit-identical after every call.  The network itself runs
+in torch fp32 on the GPU; its outputs are inputs of the shadowed calls, so the
+check covers the orchestrator's tree traffic exactly.
+"""
+import numpy as np
+import pytest
+
+from mcts_driver import tree_equal
+
+pytestmark = pytest.mark.gpu
+
+
+def _np(t):
+    return t.detach().cpu().numpy()
+
+
+class Shadow:
+    """Mirror of one orchestrator tree on the host, advanced by the oracle."""
+
+    def __init__(self, orch, tree, monkeypatch):
+        from oracle.mcts import MctsOracle
+        self.m = MctsOracle()
+        self.orch, self.tree = orch, tree
+        self.calls = {}
+        self.sync()
+        ext = orch.ext
+        for name in ("mcts_expand_dense_priors_batch", "mcts_apply_root_noise", "mcts_select_with_root_slots_batch",
+                     "mcts_replay_batch", "mcts_expand_and_backprop_dense_priors_batch"):
+            monkeypatch.setattr(ext, name, self._wrap(name, getattr(ext, name)), raising=False)
+
+    def sync(self):
+        self.ot = {k: _np(v).copy() for k, v in self.tree.items()}
+
+    def check_tree(self, where):
+        gt = {k: _np(v) for k, v in self.tree.items()}
+        bad = tree_equal(self.ot, gt)
+        assert bad == [], f"{where}: tree arrays differ: {bad}"
+
+    def _wrap(self, name, fn):
+        def call(*a):
+            out = fn(*a)
+            getattr(self, "_" + name)(a, out)
+            self.calls[name] = self.calls.get(name, 0) + 1
+            self.check_tree(name)
+            return out
+        return call
+
+    def _mcts_expand_dense_priors_batch(self, a, out):
+        cq, leaf, st, lm, nl, pri, res = [_np(x) for x in a[13:20]]
+        was = self.m.expand_dense(self.ot, cq, leaf, st, lm, nl, pri, res)
+        assert np.array_equal(was, _np(out))
+
+    def _mcts_apply_root_noise(self, a, out):
+        noise, roots = _np(a[12]), _np(a[13])
+        self.m.root_noise(self.ot, noise, roots, float(a[15]), float(a[16]))
+
+    def _mcts_select_with_root_slots_batch(self, a, out):
+        active, roots, slots = _np(a[13]), _np(a[14]), _np(a[15])
+        max_root, c_puct, W = int(a[17]), float(a[18]), int(a[20])
+        rest = list(a[22:]) + [False, 4.0, 0.0][len(a) - 22:]
+        exp = self.m.select_slots(self.ot, active, roots, slots, max_root, c_puct, W, bool(rest[0]),
+                                  float(rest[1]), float(rest[2]))
+        for e, g in zip(exp, out):
+            assert np.array_equal(e, _np(g))
+
+    def _mcts_replay_batch(self, a, out):
+        roots, leaves, paths, plen, leaf = [_np(x) for x in a[:5]]
+        exp = np.zeros_like(leaves)
+        self.m.replay(roots, exp, paths, plen, leaf)
+        assert np.array_equal(exp, leaves)
+
+    def _mcts_expand_and_backprop_dense_priors_batch(self, a, out):
+        cq, leaf, st, lm, nl, pri, res, vals, vl, vlen = [_np(x) for x in a[13:23]]
+        self.m.expand_backprop_dense(self.ot, cq, leaf, st, lm, nl, pri, res, vals, vl, vlen, float(a[26]))
+
+
+def _setup(B, sims, M, mask, max_ply, seed, **kw):
+    import torch
+    from hive_neuralnet_amd import hive_gpu
+    from hive_neuralnet_amd.fnn import seeded_large
+    from hive_neuralnet_amd.orchestrator import FNNMCTSConfig, FNNMCTSOrchestrator
+    net = seeded_large(seed)
+    cfg = FNNMCTSConfig(num_simulations=sims, batch_size=B, max_tree_nodes=M, **kw)
+    orch = FNNMCTSOrchestrator(net, cfg)
+    states, _ = hive_gpu.random_positions(B, mask, max_ply, seed)
+    torch.manual_seed(seed + 1)
+    np.random.seed(seed)
+    return orch, states, orch._alloc_tree(B)
+
+
+@pytest.mark.parametrize("sims,M,mask,max_ply,kw", [
+    (64, 4096, 7, 40, {}),
+    (64, 600, 0, 30, {}),                       # node pool runs out mid-search
+    (32, 4096, 7, 60, {"wave_parallel": False}),
+], ids=["schedule", "pool-exhaustion", "w1"])
+def test_search_ply_tree_calls_match_oracle(monkeypatch, sims, M, mask, max_ply, kw):
+    import torch
+    B = 12
+    orch, states, tree = _setup(B, sims, M, mask, max_ply, 11, **kw)
+    sh = Shadow(orch, tree, monkeypatch)
+    active = torch.ones((B,), dtype=torch.bool, device="cuda")
+    r = orch.search_ply(states, tree, active)
+    assert sh.calls.get("mcts_expand_and_backprop_dense_priors_batch", 0) > 0
+    assert sh.calls.get("mcts_replay_batch", 0) == sh.calls["mcts_select_with_root_slots_batch"]
+    sh.check_tree("end of ply")
+    # the chosen slot is a legal move and the policy is a distribution over legal slots
+    n = _np(r.num_legal)
+    has = _np(r.has_actions)
+    ch = _np(r.chosen_slot)
+    pol = _np(r.policy)
+    assert (ch[has] < n[has]).all()
+    for i in np.nonzero(has)[0]:
+        assert abs(pol[i].sum() - 1.0) < 1e-5
+        assert (pol[i, n[i]:] == 0).all()
+    # root visits = completed simulations through the root (pool exhaustion backs up too)
+    vc = _np(tree["visit_count"])
+    fc = _np(tree["first_child"])
+    sv = _np(r.slot_visits)
+    searched = has & (fc[:, 0] >= 0)
+    assert searched.any()
+    for i in np.nonzero(searched)[0]:
+        assert vc[i, 0] == sv[i].sum() > 0
+
+
+def test_two_plies_rebase_and_continue(monkeypatch):
+    import torch
+    B = 8
+    orch, states, tree = _setup(B, 32, 4096, 0, 20, 5)
+    sh = Shadow(orch, tree, monkeypatch)
+    active = torch.ones((B,), dtype=torch.bool, device="cuda")
+    for ply in range(2):
+        r = orch.search_ply(states, tree, active)
+        sh.check_tree(f"ply {ply}")
+        before = states.clone()
+        orch.apply_and_rebase(states, tree, r)
+        moved = _np(r.has_actions)
+        assert (_np(tree["node_count"])[moved] == 1).all()
+        assert (_np(tree["first_child"])[moved] == -1).all()
+        assert not torch.equal(before[torch.from_numpy(moved).cuda()], states[torch.from_numpy(moved).cuda()])
+        sh.sync()
+
+
+def test_self_play_batch_examples():
+    import torch
+    from hive_neuralnet_amd.fnn import seeded_large
+    from hive_neuralnet_amd.orchestrator import FNNMCTSConfig, FNNMCTSOrchestrator
+    net = seeded_large(3)
+    cfg = FNNMCTSConfig(num_simulations=16, batch_size=4, max_tree_nodes=2048, max_game_length=6)
+    torch.manual_seed(4)
+    np.random.seed(4)
+    ex = FNNMCTSOrchestrator(net, cfg).self_play_batch()
+    assert len(ex) == 4
+    for game in ex:
+        assert 1 <= len(game) <= 6
+        for e in game:
+            assert e.state_bytes.shape == (3424,) and e.state_bytes.dtype == np.uint8
+            assert abs(float(e.policy_target.sum()) - 1.0) < 1e-5
+            assert e.value_target in (-1.0, 0.0, 1.0)

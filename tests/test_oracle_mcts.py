@@ -41,15 +41,12 @@ def test_search_invariants(roots, mode, W):
         expanded = t["first_child"][g] >= 0
         assert t["node_count"][g] == 1 + t["num_children"][g][expanded].sum()
     # mid-wave: each selection adds one virtual visit to every node it entered
-    prev = None
-    for r in rec[1:]:
-        if prev is not None:
-            entered = np.zeros_like(prev)
-            for s in range(r["leaf"].shape[0]):
-                for k in range(r["vlen"][s]):
-                    entered[s % B, r["vl"][s, k]] += 1
-            assert np.array_equal(r["mid_visits"] - prev, entered)
-        prev = None
+    for before, r in zip(rec[:-1], rec[1:]):
+        entered = np.zeros_like(r["mid_visits"])
+        for s in range(r["leaf"].shape[0]):
+            for k in range(r["vlen"][s]):
+                entered[s % B, r["vl"][s, k]] += 1
+        assert np.array_equal(r["mid_visits"] - before["post_visits"], entered)
 
 
 def test_children_in_legal_order(oracle, roots):
