@@ -74,7 +74,7 @@ __device__ __forceinline__ int wave_argmax_first(float score, int idx) {
 }
 
 // deterministic_completed_q_child (mcts_tree.cuh:77-143), one lane, child order
-__device__ int completed_q_child(const Tree& T, int64_t g0, int first, int count, float sigma) {
+HW_INL int completed_q_child(const Tree& T, int64_t g0, int first, int count, float sigma) {
     float sum_visits = 0.0f;
     for (int c = 0; c < count; c++) {
         if (first + c < 0 || first + c >= T.M) break;
@@ -157,7 +157,7 @@ __device__ __forceinline__ void enter(const Tree& T, int64_t g0, int node, bool 
 }
 
 // PUCT descent below `node` (mcts_tree.cuh:895-950 / 729-795 below the root).
-__device__ int descend(const Tree& T, int64_t g0, int node, int first_iter, float c_puct, bool det, float sigma,
+HW_INL int descend(const Tree& T, int64_t g0, int node, int first_iter, float c_puct, bool det, float sigma,
                        float q_penalty, const SelectOut& O, int64_t sim, int& plen, int& vlen, int lane) {
     for (int it = first_iter; it < kDepth; it++) {
         int64_t ni = g0 + node;
@@ -304,7 +304,7 @@ __global__ __launch_bounds__(64) void k_replay(const uint8_t* __restrict__ roots
 }
 
 // centroid of a state row (compute_centroid, state_encoder.cuh:889-906)
-__device__ void row_centroid(const uint8_t* __restrict__ S, int lane, int& cq, int& cr) {
+HW_INL void row_centroid(const uint8_t* __restrict__ S, int lane, int& cq, int& cr) {
     int q = 0, r = 0, n = 0;
     if (lane < 18) {
         uint32_t w = reinterpret_cast<const uint32_t*>(S + OFF_OCC)[lane];
@@ -343,7 +343,7 @@ struct LeafIn {
 
 // Expansion of one simulation's leaf (mcts_expand_dense_priors_kernel
 // :971-1062 body); returns 1 when this simulation created the children.
-__device__ int expand_leaf(const Tree& T, int64_t g, int64_t sim, const LeafIn& L, int lane) {
+HW_INL int expand_leaf(const Tree& T, int64_t g, int64_t sim, const LeafIn& L, int lane) {
     const int64_t g0 = g * T.M;
     int leaf = L.leaf[sim];
     int64_t li = g0 + leaf;

@@ -14,7 +14,7 @@ namespace hw {
 // throws (own top pillbugs, then own ground mosquitoes touching a top
 // pillbug, in cell order), cut at 256; a lone PASS when empty; nothing when
 // the game is over.  The list is staged in P.mv; returns its length.
-__device__ inline int generate_legal(Pos& P, int lane) {
+HW_INL int generate_legal(Pos& P, int lane) {
     if (P.result != 0) {
         for (int i = lane; i < kMaxLegal; i += 64) P.mv[i][0] = P.mv[i][1] = P.mv[i][2] = 0;
         return 0;
@@ -182,7 +182,7 @@ __device__ inline int generate_legal(Pos& P, int lane) {
 }
 
 // copy a caller-supplied list (extract / action entry points) into P.mv
-__device__ inline int stage_moves(Pos& P, const uint8_t* __restrict__ M, int n, int lane) {
+HW_INL int stage_moves(Pos& P, const uint8_t* __restrict__ M, int n, int lane) {
     n = n < 0 ? 0 : (n > kMaxLegal ? kMaxLegal : n);
     for (int i = lane; i < kMaxLegal; i += 64) {
         if (i < n) {
@@ -198,7 +198,7 @@ __device__ inline int stage_moves(Pos& P, const uint8_t* __restrict__ M, int n, 
 }
 
 // write the staged [256 x 6] list with coalesced dword stores
-__device__ inline void store_moves(const Pos& P, uint8_t* __restrict__ out, int lane) {
+HW_INL void store_moves(const Pos& P, uint8_t* __restrict__ out, int lane) {
     const uint32_t* src = reinterpret_cast<const uint32_t*>(&P.mv[0][0]);
     uint32_t* dst = reinterpret_cast<uint32_t*>(out);  // row stride 1536 keeps 16-byte alignment
     for (int i = lane; i < kMaxLegal * 6 / 4; i += 64) dst[i] = src[i];
@@ -209,7 +209,7 @@ __device__ inline void store_moves(const Pos& P, uint8_t* __restrict__ out, int 
 // features come either from the staged list P.mv[0..n) (from_list) or, for
 // compact successor lists, from a (type, owner) bucket mask and a placement
 // count.  S is the state row (for the stacked levels under a top piece).
-__device__ inline void fnn_features(Pos& P, const uint8_t* __restrict__ S, int n, float* __restrict__ out,
+HW_INL void fnn_features(Pos& P, const uint8_t* __restrict__ S, int n, float* __restrict__ out,
                                     int lane, bool from_list = true, uint32_t bucket = 0, int n_place = 0) {
     auto& F = P.u.f;
     for (int i = lane; i < 128; i += 64) F.cnt[i] = 0;
@@ -342,7 +342,7 @@ __device__ __forceinline__ int round_half_even_div(int sum, int n) {
 }
 
 // compute_centroid (state_encoder.cuh:889-906) over the occupied-cell list
-__device__ inline void centroid(const Pos& P, int lane, int& cq, int& cr) {
+HW_INL void centroid(const Pos& P, int lane, int& cq, int& cr) {
     int q = 0, r = 0;
     if (lane < P.n_occ) {
         int c = P.occ_cells[lane];
@@ -372,7 +372,7 @@ __device__ __forceinline__ int move_action(int type, int pt, int from, int to, i
     return (a < 0 || b < 0) ? -1 : 2312 + a * 289 + b;
 }
 
-__device__ inline void store_actions(const Pos& P, int n, int cq, int cr, int* __restrict__ out, int lane) {
+HW_INL void store_actions(const Pos& P, int n, int cq, int cr, int* __restrict__ out, int lane) {
     for (int i = lane; i < kMaxLegal; i += 64) {
         int a = -1;
         if (i < n) a = move_action(P.mv[i][0] & 0xFF, P.mv[i][0] >> 8, P.mv[i][1], P.mv[i][2], cq, cr);
@@ -384,7 +384,7 @@ __device__ inline void store_actions(const Pos& P, int n, int cq, int cr, int* _
 // ---------------------------------------------------------------- summaries
 // Existence predicates: "the generator for this piece type is non-empty"
 // (the reference's has_*_move helpers, move_gen.cuh:214-1049).
-__device__ inline bool has_hopper(const Pos& P, int c) {
+HW_INL bool has_hopper(const Pos& P, int c) {
     uint32_t m = nbr_bits(P.occ, c);
     while (m) {
         int d = __ffs(m) - 1;
@@ -400,7 +400,7 @@ __device__ inline bool has_hopper(const Pos& P, int c) {
     return false;
 }
 
-__device__ inline bool has_spider(const Pos& P, int c) {
+HW_INL bool has_spider(const Pos& P, int c) {
     uint32_t m1 = slide_mask(P, c, c);
     while (m1) {
         int d1 = __ffs(m1) - 1;
@@ -424,7 +424,7 @@ __device__ inline bool has_spider(const Pos& P, int c) {
     return false;
 }
 
-__device__ inline bool has_beetle(const Pos& P, int c) {
+HW_INL bool has_beetle(const Pos& P, int c) {
     uint32_t gm = grid6(c);
     uint32_t nh = nbr_heights(P, c, gm);
     uint32_t sm = slide_mask(P, c, c);
@@ -441,7 +441,7 @@ __device__ inline bool has_beetle(const Pos& P, int c) {
     return false;
 }
 
-__device__ inline bool has_ladybug(const Pos& P, int c) {
+HW_INL bool has_ladybug(const Pos& P, int c) {
     uint32_t g0 = grid6(c);
     uint32_t nh0 = nbr_heights(P, c, g0);
     uint32_t o0 = nbr_bits(P.occ, c);
@@ -473,7 +473,7 @@ __device__ inline bool has_ladybug(const Pos& P, int c) {
     return false;
 }
 
-__device__ inline bool piece_has_move(const Pos& P, int c, int t) {
+HW_INL bool piece_has_move(const Pos& P, int c, int t) {
     switch (t) {
         case PT_Q: case PT_P: case PT_A: return slide_mask(P, c, c) != 0;
         case PT_G: return has_hopper(P, c);
@@ -503,7 +503,7 @@ __device__ inline bool piece_has_move(const Pos& P, int c, int t) {
 
 // Can the actor at a throw the piece at t (an on-grid neighbour of a)?
 // (has_pillbug_throw_for_target, move_gen.cuh:742-769)
-__device__ inline bool throwable(const Pos& P, int a, int dt) {
+HW_INL bool throwable(const Pos& P, int a, int dt) {
     int t = step(a, dt);
     if (!pb_get(P.occ, t) || P.h[t] != 1) return false;
     if (P.stun != 0xFFFF && (int)P.stun == t) return false;
@@ -530,7 +530,7 @@ __device__ inline bool throwable(const Pos& P, int a, int dt) {
 // placement cells and, per (type, owner) bucket, whether any MOVE entry
 // exists (the list keeps one entry per bucket, so can_move is 0 or 1).
 // Returns the bucket mask; *n_place gets the placement-cell count.
-__device__ inline uint32_t compact_summary(Pos& P, int lane, int* n_place) {
+HW_INL uint32_t compact_summary(Pos& P, int lane, int* n_place) {
     *n_place = 0;
     if (P.result != 0) return 0;
     const int me = P.turn & 1;
@@ -587,7 +587,7 @@ __device__ inline uint32_t compact_summary(Pos& P, int lane, int* n_place) {
 }
 
 // has_queen_escape_move (move_gen.cuh:771-821); wave-uniform result
-__device__ inline bool queen_escape(const Pos& P, int lane) {
+HW_INL bool queen_escape(const Pos& P, int lane) {
     const int me = P.turn & 1;
     if (!((P.qplaced >> me) & 1)) return false;
     int q = P.queen[me];
@@ -613,22 +613,22 @@ __device__ inline bool queen_escape(const Pos& P, int lane) {
 // S is the row the LDS board was loaded from; the piece revealed when a
 // stack's top leaves is read from it (levels under the top are unchanged by
 // a single move).
-__device__ inline void pb_set(uint32_t* pb, int c) { pb[(c >> 5) + 1] |= 1u << (c & 31); }
-__device__ inline void pb_clr(uint32_t* pb, int c) { pb[(c >> 5) + 1] &= ~(1u << (c & 31)); }
+HW_INL void pb_set(uint32_t* pb, int c) { pb[(c >> 5) + 1] |= 1u << (c & 31); }
+HW_INL void pb_clr(uint32_t* pb, int c) { pb[(c >> 5) + 1] &= ~(1u << (c & 31)); }
 
-__device__ inline void set_top_colour(Pos& P, int c, int col) {
+HW_INL void set_top_colour(Pos& P, int c, int col) {
     if (col) { pb_set(P.bt, c); pb_clr(P.wt, c); }
     else { pb_set(P.wt, c); pb_clr(P.bt, c); }
 }
 
-__device__ inline bool queen_ringed(const Pos& P, int col) {
+HW_INL bool queen_ringed(const Pos& P, int col) {
     if (!((P.qplaced >> col) & 1)) return false;
     int q = P.queen[col];
     if (q >= kCells) return false;
     return __popc(nbr_bits(P.occ, q)) == 6;
 }
 
-__device__ inline void apply_on_board(Pos& P, const uint8_t* __restrict__ S, int type, int pt, int from, int to) {
+HW_INL void apply_on_board(Pos& P, const uint8_t* __restrict__ S, int type, int pt, int from, int to) {
     const int me = P.turn & 1;
     if (type == MV_PLACE) {
         if (to < kCells && pt >= PT_Q && pt <= PT_P && P.h[to] < 5) {
@@ -680,7 +680,7 @@ __device__ inline void apply_on_board(Pos& P, const uint8_t* __restrict__ S, int
 // Whole-position programs run by all 64 lanes of a wave; the kernels in
 // hive_engine.hip are thin launch wrappers around them.
 
-__device__ inline void prepare(Pos& P, const uint8_t* __restrict__ S, int lane) {
+HW_INL void prepare(Pos& P, const uint8_t* __restrict__ S, int lane) {
     load_position(P, S, lane);
     __syncthreads();
     build_occ_list(P, lane);
@@ -690,7 +690,7 @@ __device__ inline void prepare(Pos& P, const uint8_t* __restrict__ S, int lane) 
 }
 
 template <bool WithMoves, bool WithFeat, bool WithAct>
-__device__ inline void run_legal(Pos& P, const uint8_t* __restrict__ S, int lane, uint8_t* __restrict__ moves_row,
+HW_INL void run_legal(Pos& P, const uint8_t* __restrict__ S, int lane, uint8_t* __restrict__ moves_row,
                                  int32_t* __restrict__ n_slot, float* __restrict__ feat_row,
                                  int32_t* __restrict__ act_row) {
     prepare(P, S, lane);
@@ -706,7 +706,7 @@ __device__ inline void run_legal(Pos& P, const uint8_t* __restrict__ S, int lane
     if (WithFeat) fnn_features(P, S, n, feat_row, lane);
 }
 
-__device__ inline void run_extract(Pos& P, const uint8_t* __restrict__ S, const uint8_t* __restrict__ M, int nl,
+HW_INL void run_extract(Pos& P, const uint8_t* __restrict__ S, const uint8_t* __restrict__ M, int nl,
                                    int lane, float* __restrict__ feat_row) {
     int n = stage_moves(P, M, nl, lane);
     prepare(P, S, lane);
@@ -714,7 +714,7 @@ __device__ inline void run_extract(Pos& P, const uint8_t* __restrict__ S, const 
 }
 
 // fnn_successor_features_kernel (game_logic.cu:182-229) for one (root, move)
-__device__ inline void run_successor(Pos& P, const uint8_t* __restrict__ S, const uint8_t* __restrict__ m, int lane,
+HW_INL void run_successor(Pos& P, const uint8_t* __restrict__ S, const uint8_t* __restrict__ m, int lane,
                                      float* __restrict__ feat_row) {
     load_position(P, S, lane);
     __syncthreads();
@@ -732,7 +732,7 @@ __device__ inline void run_successor(Pos& P, const uint8_t* __restrict__ S, cons
     fnn_features(P, S, 0, feat_row, lane, false, bucket, n_place);
 }
 
-__device__ inline bool run_queen_escape(Pos& P, const uint8_t* __restrict__ S, int lane) {
+HW_INL bool run_queen_escape(Pos& P, const uint8_t* __restrict__ S, int lane) {
     prepare(P, S, lane);
     return queen_escape(P, lane);
 }

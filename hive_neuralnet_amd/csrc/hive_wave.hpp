@@ -160,7 +160,7 @@ __device__ __forceinline__ int wave_sum(int v) {
 
 // ---------------------------------------------------------------- state load
 // Heights, top bytes, bitboards and metadata of the state row S into P.
-__device__ inline void load_position(Pos& P, const uint8_t* __restrict__ S, int lane) {
+HW_INL void load_position(Pos& P, const uint8_t* __restrict__ S, int lane) {
     for (int i = lane; i < 544; i += 64) {
         int hh = i < kCells ? S[OFF_HEIGHT + i] : 0;
         P.h[i] = (uint8_t)hh;
@@ -197,7 +197,7 @@ __device__ inline void load_position(Pos& P, const uint8_t* __restrict__ S, int 
 }
 
 // Ascending list of occupied cells (first 32) and their dense index.
-__device__ inline void build_occ_list(Pos& P, int lane) {
+HW_INL void build_occ_list(Pos& P, int lane) {
     uint32_t w = lane < 18 ? P.occ[lane + 1] : 0u;
     int base = wave_excl_scan(__popc(w), lane);
     int total = wave_sum(lane < 18 ? __popc(w) : 0);
@@ -222,7 +222,7 @@ __device__ inline void build_occ_list(Pos& P, int lane) {
 // with nothing removed to obtain the component C0 of vertex 0.  v is an
 // articulation point iff v is in C0 and C0 \ {v} is not reached from a
 // vertex of C0 \ {v}.
-__device__ inline void articulation(Pos& P, int lane) {
+HW_INL void articulation(Pos& P, int lane) {
     int total = P.n_occ;
     int N = total < 28 ? total : 28;
     if (lane < 20) { P.ap[lane] = 0; P.pin[lane] = 0; }
@@ -311,7 +311,7 @@ __device__ __forceinline__ bool set_insert(uint32_t* s, int c) {  // true if new
 // returns the count.
 
 // gen_queen_moves :202-212 / gen_pillbug_moves :644-647
-__device__ inline int gen_step(const Pos& P, int c, uint16_t* out) {
+HW_INL int gen_step(const Pos& P, int c, uint16_t* out) {
     uint32_t m = slide_mask(P, c, c);
     int n = 0;
     while (m) {
@@ -323,7 +323,7 @@ __device__ inline int gen_step(const Pos& P, int c, uint16_t* out) {
 }
 
 // gen_grasshopper_moves :228-245
-__device__ inline int gen_hopper(const Pos& P, int c, uint16_t* out) {
+HW_INL int gen_hopper(const Pos& P, int c, uint16_t* out) {
     int n = 0;
     uint32_t gm = grid6(c);
     uint32_t m = nbr_bits(P.occ, c);
@@ -344,7 +344,7 @@ __device__ inline int gen_hopper(const Pos& P, int c, uint16_t* out) {
 // FIFO breadth-first ant search (gen_ant_moves_with_perimeter :267-313,
 // emit_ant_moves_with_perimeter :348-388): seeds in direction order, each
 // dequeued cell expanded in direction order, ant lifted from c.
-__device__ inline int gen_ant(const Pos& P, int c, uint16_t* out, int cap, uint32_t* seen) {
+HW_INL int gen_ant(const Pos& P, int c, uint16_t* out, int cap, uint32_t* seen) {
     set_clear(seen);
     set_insert(seen, c);
     int head = 0, tail = 0;
@@ -364,7 +364,7 @@ __device__ inline int gen_ant(const Pos& P, int c, uint16_t* out, int cap, uint3
 }
 
 // gen_spider_moves :397-431 (first occurrence over d1,d2,d3; at most 32)
-__device__ inline int gen_spider(const Pos& P, int c, uint16_t* out, uint32_t* got) {
+HW_INL int gen_spider(const Pos& P, int c, uint16_t* out, uint32_t* got) {
     set_clear(got);
     int n = 0;
     uint32_t m1 = slide_mask(P, c, c);
@@ -392,7 +392,7 @@ __device__ inline int gen_spider(const Pos& P, int c, uint16_t* out, uint32_t* g
 }
 
 // gen_beetle_moves :468-502
-__device__ inline int gen_beetle(const Pos& P, int c, uint16_t* out) {
+HW_INL int gen_beetle(const Pos& P, int c, uint16_t* out) {
     uint32_t gm = grid6(c);
     uint32_t nh = nbr_heights(P, c, gm);
     uint32_t sm = slide_mask(P, c, c);
@@ -410,7 +410,7 @@ __device__ inline int gen_beetle(const Pos& P, int c, uint16_t* out) {
 }
 
 // gen_ladybug_moves :538-596 (first occurrence over d1,d2,d3; at most 32)
-__device__ inline int gen_ladybug(const Pos& P, int c, uint16_t* out, uint32_t* got) {
+HW_INL int gen_ladybug(const Pos& P, int c, uint16_t* out, uint32_t* got) {
     set_clear(got);
     int n = 0;
     uint32_t g0 = grid6(c);
@@ -450,7 +450,7 @@ __device__ inline int gen_ladybug(const Pos& P, int c, uint16_t* out, uint32_t* 
 // pieces, first occurrence kept, at most 128.  Each sub-list is generated
 // into the free tail of out[] and merged in place (merge write index never
 // passes the read index).  Needs 6 + 128 slots of room.
-__device__ inline int gen_mosquito(const Pos& P, int c, uint16_t* out, uint32_t* tmpset, uint32_t* unionset) {
+HW_INL int gen_mosquito(const Pos& P, int c, uint16_t* out, uint32_t* tmpset, uint32_t* unionset) {
     if (P.h[c] > 1) return gen_beetle(P, c, out);
     uint32_t gm = grid6(c);
     uint32_t om = nbr_bits(P.occ, c);
@@ -486,7 +486,7 @@ __device__ inline int gen_mosquito(const Pos& P, int c, uint16_t* out, uint32_t*
 
 // Throws by the pillbug-ability actor at a (gen_pillbug_throws :691-740):
 // targets in direction order, each to the empty drop cells in direction order.
-__device__ inline int gen_throws(const Pos& P, int a, uint16_t* from, uint16_t* to, uint8_t* pt) {
+HW_INL int gen_throws(const Pos& P, int a, uint16_t* from, uint16_t* to, uint8_t* pt) {
     int n = 0;
     uint32_t ga = grid6(a);
     uint32_t nha = nbr_heights(P, a, ga);
@@ -535,7 +535,7 @@ __device__ __forceinline__ int type_capacity(int t) {
 // Placement cells (find_placement_positions :1064-1140) into P.plc, as a
 // bit-parallel neighbourhood expression over board words (lane w < 18 owns
 // word w).  Returns the number of cells (wave-uniform).
-__device__ inline uint32_t word_field(const uint32_t* pb, int bit_off) {
+HW_INL uint32_t word_field(const uint32_t* pb, int bit_off) {
     int wi = (bit_off >> 5) + 1;
     int sh = bit_off & 31;
     uint64_t v = (uint64_t)pb[wi] | ((uint64_t)pb[wi + 1] << 32);
@@ -559,7 +559,7 @@ constexpr GridMasks make_grid_masks() {
 static __constant__ GridMasks kGridMask = make_grid_masks();
 
 // cells of board word w with an on-grid neighbour that is set in pb
-__device__ inline uint32_t nbr_union_word(const uint32_t* pb, int w) {
+HW_INL uint32_t nbr_union_word(const uint32_t* pb, int w) {
     uint32_t r = 0;
 #pragma unroll
     for (int d = 0; d < 6; d++) r |= word_field(pb, 32 * w + win_ofs(d) - 23) & kGridMask.m[d][w];

@@ -8,3 +8,8 @@
 #else
 #include <hip/hip_runtime.h>
 #endif
+
+// Every engine routine is inlined into its kernel: a device-side call makes
+// the whole kernel allocate for the call ABI (twice the registers, half the
+// occupancy of the inlined form for k_legal).
+#define HW_INL __device__ __attribute__((always_inline)) inline
