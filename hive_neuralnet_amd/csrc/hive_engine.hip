@@ -87,7 +87,10 @@ __global__ __launch_bounds__(64) void k_actions(const uint8_t* __restrict__ stat
     const uint32_t* W = reinterpret_cast<const uint32_t*>(S + OFF_OCC);
     if (lane < 18) P.occ[lane + 1] = W[lane];
     int n = 0;
-    if (act_out) n = stage_moves(P, moves + pos * (kMaxLegal * 6), num_legal[pos], lane);
+    if (act_out) {
+        n = num_legal[pos];
+        n = n < 0 ? 0 : (n > kMaxLegal ? kMaxLegal : n);
+    }
     __syncthreads();
     build_occ_list(P, lane);
     __syncthreads();
@@ -97,7 +100,7 @@ __global__ __launch_bounds__(64) void k_actions(const uint8_t* __restrict__ stat
         centroid_out[2 * pos] = cq;
         centroid_out[2 * pos + 1] = cr;
     }
-    if (act_out) store_actions(P, n, cq, cr, act_out + pos * kMaxLegal, lane);
+    if (act_out) list_actions(moves + pos * (kMaxLegal * 6), n, cq, cr, act_out + pos * kMaxLegal, lane);
 }
 
 // fnn_successor_features_kernel (game_logic.cu:182-229): one wave per (root, move).

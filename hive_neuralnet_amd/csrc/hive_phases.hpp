@@ -13,12 +13,27 @@ namespace hw {
 // stunned nor pinned (cells ascending, type-specific order), then pillbug
 // throws (own top pillbugs, then own ground mosquitoes touching a top
 // pillbug, in cell order), cut at 256; a lone PASS when empty; nothing when
-// the game is over.  The list is staged in P.mv; returns its length.
-HW_INL int generate_legal(Pos& P, int lane) {
-    if (P.result != 0) {
-        for (int i = lane; i < kMaxLegal; i += 64) P.mv[i][0] = P.mv[i][1] = P.mv[i][2] = 0;
-        return 0;
-    }
+// the game is over.
+//
+// The list is not materialised in LDS: generate_legal leaves the placement
+// cells (P.plc, P.plc_pre), the per-piece destination lists (P.pool), the
+// throw lists and the segment starts (P.seg_base: placements, one segment
+// per piece, one per throw actor, end) on the board; list_slot() decodes any
+// slot from them, so that slots are written to memory lane-parallel.
+struct ListInfo {
+    int n;          // list length after the cut (1 for a lone PASS, 0 when the game is over)
+    int total;      // entries before the cut
+    int n_place;    // placement entries (npos * ntypes)
+    int npos;       // placement cells
+    int ntypes;     // placeable types emitted per cell
+    int n_pieces;   // piece segments
+    int nseg;       // segments before the end marker
+    uint32_t emit_types;
+};
+
+HW_INL ListInfo generate_legal(Pos& P, int lane) {
+    ListInfo L{0, 0, 0, 0, 0, 0, 0, 0u};
+    if (P.result != 0) return L;
     const int me = P.turn & 1;
     const int ptn = P.turn >> 1;
     const bool queen_down = (P.qplaced >> me) & 1;
@@ -46,6 +61,10 @@ HW_INL int generate_legal(Pos& P, int lane) {
     }
     int prank = wave_excl_scan(__popc(pw), lane);
     int npos = wave_sum(__popc(pw));
+    if (lane < 18) {
+        P.plc[lane + 1] = pw;
+        P.plc_pre[lane] = (uint16_t)prank;
+    }
     int n_place = npos * ntypes;
 
     // -- movable pieces: own top cells, not stunned, not pinned (cell order)
@@ -59,14 +78,12 @@ HW_INL int generate_legal(Pos& P, int lane) {
         }
         int k = wave_excl_scan(__popc(mw), lane);
         n_pieces = min(wave_sum(__popc(mw)), kMaxPieces);
-        while (mw) {
+        while (mw && k < kMaxPieces) {
             int b = __ffs(mw) - 1;
             mw &= mw - 1;
-            if (k < kMaxPieces) {
-                int c = lane * 32 + b;
-                P.piece_cell[k] = (uint16_t)c;
-                P.piece_type[k] = P.top[c] & 15;
-            }
+            int c = lane * 32 + b;
+            P.piece_cell[k] = (uint16_t)c;
+            P.piece_type[k] = P.top[c] & 15;
             k++;
         }
         // throw actors among occupied cells (cell order); the thrower is not
@@ -119,98 +136,89 @@ HW_INL int generate_legal(Pos& P, int lane) {
     }
     __syncthreads();
 
-    // -- assembly: slot 0 placements, slots 1..n_pieces pieces, then actors
+    // -- segment starts: lane 0 placements, lanes 1..n_pieces pieces, then actors, then the end
     int cnt = 0;
     if (lane == 0) cnt = n_place;
     else if (lane <= n_pieces) cnt = P.piece_cnt[lane - 1];
     else if (lane <= n_pieces + n_actors) cnt = P.throw_cnt[lane - 1 - n_pieces];
     int base = wave_excl_scan(cnt, lane);
     int total = wave_sum(cnt);
-    int n = total < kMaxLegal ? total : kMaxLegal;
-
-    // placements: lane w < 18 emits its cells x emit types
-    if (lane < 18 && pw) {
-        int r = prank;
-        uint32_t w = pw;
-        while (w) {
-            int b = __ffs(w) - 1;
-            w &= w - 1;
-            int c = lane * 32 + b;
-            int slot = r * ntypes;
-            uint32_t ty = emit_types;
-            while (ty) {
-                int p = __ffs(ty) - 1;
-                ty &= ty - 1;
-                if (slot < kMaxLegal) {
-                    P.mv[slot][0] = (uint16_t)(MV_PLACE | ((p + 1) << 8));
-                    P.mv[slot][1] = 0;
-                    P.mv[slot][2] = (uint16_t)c;
-                }
-                slot++;
-            }
-            r++;
-        }
-    }
-    if (lane >= 1 && lane <= n_pieces) {
-        int i = lane - 1;
-        int c = P.piece_cell[i], t = P.piece_type[i];
-        const uint16_t* src = P.pool + P.piece_off[i];
-        for (int k = 0; k < cnt && base + k < kMaxLegal; k++) {
-            P.mv[base + k][0] = (uint16_t)(MV_MOVE | (t << 8));
-            P.mv[base + k][1] = (uint16_t)c;
-            P.mv[base + k][2] = src[k];
-        }
-    } else if (lane > n_pieces && lane <= n_pieces + n_actors) {
-        int j = lane - 1 - n_pieces;
-        for (int k = 0; k < cnt && base + k < kMaxLegal; k++) {
-            P.mv[base + k][0] = (uint16_t)(MV_MOVE | (P.throw_pt[j][k] << 8));
-            P.mv[base + k][1] = P.throw_from[j][k];
-            P.mv[base + k][2] = P.throw_to[j][k];
-        }
-    }
-    if (total == 0) n = 1;  // PASS = all-zero from/to, type 2
+    int nseg = 1 + n_pieces + n_actors;
+    if (lane <= nseg) P.seg_base[lane] = (int16_t)min(base, 32767);
     __syncthreads();
-    for (int i = lane; i < kMaxLegal; i += 64) {
-        if (total == 0 && i == 0) {
-            P.mv[0][0] = MV_PASS;
-            P.mv[0][1] = P.mv[0][2] = 0;
-        } else if (i >= n) {
-            P.mv[i][0] = P.mv[i][1] = P.mv[i][2] = 0;
-        }
-    }
-    return n;
+    L.total = total;
+    L.n = total == 0 ? 1 : (total < kMaxLegal ? total : kMaxLegal);  // PASS = all-zero from/to, type 2
+    L.n_place = n_place;
+    L.npos = npos;
+    L.ntypes = ntypes;
+    L.n_pieces = n_pieces;
+    L.nseg = nseg;
+    L.emit_types = emit_types;
+    return L;
 }
 
-// copy a caller-supplied list (extract / action entry points) into P.mv
-HW_INL int stage_moves(Pos& P, const uint8_t* __restrict__ M, int n, int lane) {
-    n = n < 0 ? 0 : (n > kMaxLegal ? kMaxLegal : n);
-    for (int i = lane; i < kMaxLegal; i += 64) {
-        if (i < n) {
-            const uint8_t* m = M + 6 * i;
-            P.mv[i][0] = (uint16_t)(m[0] | (m[1] << 8));
-            P.mv[i][1] = (uint16_t)(m[2] | (m[3] << 8));
-            P.mv[i][2] = (uint16_t)(m[4] | (m[5] << 8));
-        } else {
-            P.mv[i][0] = P.mv[i][1] = P.mv[i][2] = 0;
-        }
-    }
-    return n;
+// position of the r-th set bit of x (r < popc(x))
+__device__ __forceinline__ int select_bit(uint32_t x, int r) {
+    int pos = 0;
+    int c = __popc(x & 0xFFFFu);
+    if (r >= c) { r -= c; x >>= 16; pos += 16; }
+    c = __popc(x & 0xFFu);
+    if (r >= c) { r -= c; x >>= 8; pos += 8; }
+    c = __popc(x & 0xFu);
+    if (r >= c) { r -= c; x >>= 4; pos += 4; }
+    c = __popc(x & 0x3u);
+    if (r >= c) { r -= c; x >>= 2; pos += 2; }
+    c = (int)(x & 1u);
+    if (r >= c) pos += 1;
+    return pos;
 }
 
-// write the staged [256 x 6] list with coalesced dword stores
-HW_INL void store_moves(const Pos& P, uint8_t* __restrict__ out, int lane) {
-    const uint32_t* src = reinterpret_cast<const uint32_t*>(&P.mv[0][0]);
-    uint32_t* dst = reinterpret_cast<uint32_t*>(out);  // row stride 1536 keeps 16-byte alignment
-    for (int i = lane; i < kMaxLegal * 6 / 4; i += 64) dst[i] = src[i];
+// Slot i (i < L.n, L.total > 0) of the generated list as (type | pt << 8, from, to).
+HW_INL void list_slot(const Pos& P, const ListInfo& L, int i, int& tp, int& from, int& to, int& seg) {
+    int lo = 0, hi = L.nseg - 1;  // last segment starting at or before i
+    while (lo < hi) {
+        int mid = (lo + hi + 1) >> 1;
+        if (P.seg_base[mid] <= i) lo = mid;
+        else hi = mid - 1;
+    }
+    seg = lo;
+    int k = i - P.seg_base[lo];
+    if (lo == 0) {  // placement: cell k / ntypes, type (k % ntypes)-th of emit_types
+        int r = k / L.ntypes;
+        int ti = k - r * L.ntypes;
+        int wl = 0, wh = 17;  // last board word whose placement prefix is <= r
+        while (wl < wh) {
+            int mid = (wl + wh + 1) >> 1;
+            if (P.plc_pre[mid] <= r) wl = mid;
+            else wh = mid - 1;
+        }
+        to = wl * 32 + select_bit(P.plc[wl + 1], r - P.plc_pre[wl]);
+        from = 0;
+        tp = MV_PLACE | ((select_bit(L.emit_types, ti) + 1) << 8);
+    } else if (lo <= L.n_pieces) {
+        int j = lo - 1;
+        from = P.piece_cell[j];
+        to = P.pool[P.piece_off[j] + k];
+        tp = MV_MOVE | (P.piece_type[j] << 8);
+    } else {
+        int j = lo - 1 - L.n_pieces;
+        from = P.throw_from[j][k];
+        to = P.throw_to[j][k];
+        tp = MV_MOVE | (P.throw_pt[j][k] << 8);
+    }
 }
 
 // ---------------------------------------------------------------- features
 // extract_fnn_features_device (fnn_features.cuh:68-331).  The legal-move
-// features come either from the staged list P.mv[0..n) (from_list) or, for
-// compact successor lists, from a (type, owner) bucket mask and a placement
-// count.  S is the state row (for the stacked levels under a top piece).
-HW_INL void fnn_features(Pos& P, const uint8_t* __restrict__ S, int n, float* __restrict__ out,
-                                    int lane, bool from_list = true, uint32_t bucket = 0, int n_place = 0) {
+// features (distinct MOVE sources per (type, owner), distinct PLACE
+// destinations) come from the from_bb / place_bb sets filled while a list is
+// written or read (kFeatList, kFeatGen: place count given), or, for compact
+// successor lists, from a (type, owner) bucket mask and a placement count
+// (kFeatBucket).  S is the state row (for the stacked levels under a top
+// piece).
+enum { kFeatList = 0, kFeatGen = 1, kFeatBucket = 2 };
+
+HW_INL void features_clear(Pos& P, int lane) {
     auto& F = P.u.f;
     for (int i = lane; i < 128; i += 64) F.cnt[i] = 0;
     if (lane < 16) { F.dsum[lane] = 0; F.dcnt[lane] = 0; }
@@ -218,7 +226,33 @@ HW_INL void fnn_features(Pos& P, const uint8_t* __restrict__ S, int n, float* __
     if (lane == 0) F.n_cap = 0;
     for (int i = lane; i < 16 * 18; i += 64) (&F.from_bb[0][0])[i] = 0;
     if (lane < 18) F.place_bb[lane] = 0;
-    __syncthreads();
+}
+
+// MOVE source / PLACE destination sets of a caller-supplied list (global memory)
+HW_INL void list_sources(Pos& P, const uint8_t* __restrict__ M, int n, int lane) {
+    auto& F = P.u.f;
+    const int me = P.turn & 1;
+    for (int i = lane; i < n; i += 64) {
+        const uint8_t* m = M + 6 * i;
+        int ty = m[0], pt = m[1];
+        if (ty == MV_MOVE) {
+            int fc = m[2] | (m[3] << 8);
+            if (fc < 544 && pt >= 1 && pt <= 8) {
+                int owner = P.h[fc] > 0 ? (P.top[fc] >> 4) & 1 : me;
+                atomicOr(&F.from_bb[(pt - 1) * 2 + owner][fc >> 5], 1u << (fc & 31));
+            }
+        } else if (ty == MV_PLACE) {
+            int tc = m[4] | (m[5] << 8);
+            if (tc < 544) atomicOr(&F.place_bb[tc >> 5], 1u << (tc & 31));
+        }
+    }
+}
+
+// Needs features_clear and the legal-move sets (modes kFeatList / kFeatGen)
+// complete, behind a barrier.
+HW_INL void features_finish(Pos& P, const uint8_t* __restrict__ S, float* __restrict__ out, int lane, int mode,
+                            uint32_t bucket, int n_place) {
+    auto& F = P.u.f;
     const int me = P.turn & 1;
     if (lane < P.n_occ) {
         int c = P.occ_cells[lane];
@@ -227,7 +261,7 @@ HW_INL void fnn_features(Pos& P, const uint8_t* __restrict__ S, int n, float* __
         int pt = tb & 15, col = (tb >> 4) & 1, tc = (pt - 1) * 2 + col;
         if (pt < PT_Q || pt > PT_P) pt = 0;  // impossible top byte: contributes nothing
         if (pt) atomicAdd(&F.cnt[tc], 1);
-        uint32_t nm = nbr_bits(P.occ, c);
+        uint32_t nm = P.nb[c];
         if (nm == 0) atomicAdd(&F.cnt[96 + col], 1);
         uint32_t gm = grid6(c);
         int oq = P.queen[col ^ 1];
@@ -264,27 +298,12 @@ HW_INL void fnn_features(Pos& P, const uint8_t* __restrict__ S, int n, float* __
             if (k < 8) { F.cap_cells[k] = (uint16_t)c; F.cap_col[k] = (uint8_t)col; }
         }
     }
-    // legal-move features: distinct MOVE sources per (type, owner), distinct
-    // PLACE destinations (credited to the side to move)
-    for (int i = lane; from_list && i < n; i += 64) {
-        int ty = P.mv[i][0] & 0xFF, pt = P.mv[i][0] >> 8;
-        if (ty == MV_MOVE) {
-            int fc = P.mv[i][1];
-            if (fc < 544 && pt >= 1 && pt <= 8) {
-                int owner = P.h[fc] > 0 ? (P.top[fc] >> 4) & 1 : me;
-                atomicOr(&F.from_bb[(pt - 1) * 2 + owner][fc >> 5], 1u << (fc & 31));
-            }
-        } else if (ty == MV_PLACE) {
-            int tc = P.mv[i][2];
-            if (tc < 544) atomicOr(&F.place_bb[tc >> 5], 1u << (tc & 31));
-        }
-    }
     __syncthreads();
     // pieces next to a pillbug-capable cell (throwable own / threatened)
     int ncap = F.n_cap < 8 ? F.n_cap : 8;
     if (lane < ncap) {
         int p = F.cap_cells[lane], col = F.cap_col[lane];
-        uint32_t m = nbr_bits(P.occ, p);
+        uint32_t m = P.nb[p];
         while (m) {
             int d = __ffs(m) - 1;
             m &= m - 1;
@@ -295,7 +314,7 @@ HW_INL void fnn_features(Pos& P, const uint8_t* __restrict__ S, int n, float* __
             else atomicAdd(&F.cnt[108 + nc], 1);
         }
     }
-    if (!from_list) {
+    if (mode == kFeatBucket) {
         if (lane < 16) F.cnt[64 + lane] = (bucket >> lane) & 1u;
         else if (lane == 16) F.cnt[100] = n_place;
     } else if (lane < 16) {
@@ -303,8 +322,11 @@ HW_INL void fnn_features(Pos& P, const uint8_t* __restrict__ S, int n, float* __
         for (int w = 0; w < 18; w++) s += __popc(F.from_bb[lane][w]);
         F.cnt[64 + lane] = s;
     } else if (lane == 16) {
-        int s = 0;
-        for (int w = 0; w < 18; w++) s += __popc(F.place_bb[w]);
+        int s = n_place;
+        if (mode == kFeatList) {
+            s = 0;
+            for (int w = 0; w < 18; w++) s += __popc(F.place_bb[w]);
+        }
         F.cnt[100] = s;
     }
     __syncthreads();
@@ -372,11 +394,50 @@ __device__ __forceinline__ int move_action(int type, int pt, int from, int to, i
     return (a < 0 || b < 0) ? -1 : 2312 + a * 289 + b;
 }
 
-HW_INL void store_actions(const Pos& P, int n, int cq, int cr, int* __restrict__ out, int lane) {
+// action indices of a caller-supplied list (global memory), -1 padded
+HW_INL void list_actions(const uint8_t* __restrict__ M, int n, int cq, int cr, int* __restrict__ out, int lane) {
     for (int i = lane; i < kMaxLegal; i += 64) {
         int a = -1;
-        if (i < n) a = move_action(P.mv[i][0] & 0xFF, P.mv[i][0] >> 8, P.mv[i][1], P.mv[i][2], cq, cr);
+        if (i < n) {
+            const uint8_t* m = M + 6 * i;
+            a = move_action(m[0], m[1], m[2] | (m[3] << 8), m[4] | (m[5] << 8), cq, cr);
+        }
         out[i] = a;
+    }
+}
+
+// Writes the generated list: moves (zero padded), action indices (-1
+// padded), and the MOVE-source sets of the features (one bit per piece
+// segment that is inside the cut, one per throw entry).
+template <bool WithMoves, bool WithAct, bool WithFeat>
+HW_INL void emit_list(Pos& P, const ListInfo& L, int lane, uint8_t* __restrict__ moves_row,
+                      int32_t* __restrict__ act_row, int cq, int cr) {
+    const int me = P.turn & 1;
+    uint16_t* row16 = reinterpret_cast<uint16_t*>(moves_row);
+    for (int i = lane; i < kMaxLegal; i += 64) {
+        int tp = 0, from = 0, to = 0;
+        if (i < L.n) {
+            if (L.total == 0) {
+                tp = MV_PASS;
+            } else {
+                int seg;
+                list_slot(P, L, i, tp, from, to, seg);
+                if (WithFeat && seg > 0) {
+                    bool thr = seg > L.n_pieces;
+                    int pt = tp >> 8;
+                    if ((thr || i == P.seg_base[seg]) && from < 544 && pt >= 1 && pt <= 8) {
+                        int owner = thr ? (P.top[from] >> 4) & 1 : me;
+                        atomicOr(&P.u.f.from_bb[(pt - 1) * 2 + owner][from >> 5], 1u << (from & 31));
+                    }
+                }
+            }
+        }
+        if (WithMoves) {
+            row16[3 * i] = (uint16_t)tp;
+            row16[3 * i + 1] = (uint16_t)from;
+            row16[3 * i + 2] = (uint16_t)to;
+        }
+        if (WithAct) act_row[i] = i < L.n ? move_action(tp & 0xFF, tp >> 8, from, to, cq, cr) : -1;
     }
 }
 
@@ -385,7 +446,7 @@ HW_INL void store_actions(const Pos& P, int n, int cq, int cr, int* __restrict__
 // Existence predicates: "the generator for this piece type is non-empty"
 // (the reference's has_*_move helpers, move_gen.cuh:214-1049).
 HW_INL bool has_hopper(const Pos& P, int c) {
-    uint32_t m = nbr_bits(P.occ, c);
+    uint32_t m = P.nb[c];
     while (m) {
         int d = __ffs(m) - 1;
         m &= m - 1;
@@ -444,14 +505,14 @@ HW_INL bool has_beetle(const Pos& P, int c) {
 HW_INL bool has_ladybug(const Pos& P, int c) {
     uint32_t g0 = grid6(c);
     uint32_t nh0 = nbr_heights(P, c, g0);
-    uint32_t o0 = nbr_bits(P.occ, c);
+    uint32_t o0 = P.nb[c];
     int hc = P.h[c];
     for (int d1 = 0; d1 < 6; d1++) {
         if (!((o0 >> d1) & 1u)) continue;
         int p1 = step(c, d1);
         if (gate_high(nh0, d1, max(hc - 1, hof(nh0, d1)))) continue;
         uint32_t nh1 = nbr_heights(P, p1, grid6(p1));
-        uint32_t o1 = nbr_bits(P.occ, p1);
+        uint32_t o1 = P.nb[p1];
         int hp1 = P.h[p1];
         for (int d2 = 0; d2 < 6; d2++) {
             if (!((o1 >> d2) & 1u)) continue;
@@ -460,7 +521,7 @@ HW_INL bool has_ladybug(const Pos& P, int c) {
             if (gate_high(nh1, d2, max(hp1, hof(nh1, d2)))) continue;
             uint32_t g2 = grid6(p2);
             uint32_t nh2 = nbr_heights(P, p2, g2);
-            uint32_t o2 = nbr_bits(P.occ, p2);
+            uint32_t o2 = P.nb[p2];
             int mh3 = P.h[p2];
             for (int d3 = 0; d3 < 6; d3++) {
                 if (!((g2 >> d3) & 1u) || ((o2 >> d3) & 1u)) continue;
@@ -482,7 +543,7 @@ HW_INL bool piece_has_move(const Pos& P, int c, int t) {
         case PT_L: return has_ladybug(P, c);
         case PT_M: {
             if (P.h[c] > 1) return has_beetle(P, c);
-            uint32_t om = nbr_bits(P.occ, c);
+            uint32_t om = P.nb[c];
             uint32_t has = 0;
             while (om) {
                 int d = __ffs(om) - 1;
@@ -516,7 +577,7 @@ HW_INL bool throwable(const Pos& P, int a, int dt) {
     int ccwh = ((gt >> ((back + 1) % 6)) & 1u) ? P.h[step(t, (back + 1) % 6)] : 0;
     if (cwh > lift && ccwh > lift) return false;
     uint32_t ga = grid6(a);
-    uint32_t oa = nbr_bits(P.occ, a);
+    uint32_t oa = P.nb[a];
     uint32_t nha = nbr_heights(P, a, ga);
     for (int dd = 0; dd < 6; dd++) {
         if (!((ga >> dd) & 1u) || dd == dt || ((oa >> dd) & 1u)) continue;
@@ -569,7 +630,7 @@ HW_INL uint32_t compact_summary(Pos& P, int lane, int* n_place) {
             if (!stunned && !pb_get(P.pin, c) && piece_has_move(P, c, t)) bucket |= 1u << ((t - 1) * 2 + me);
             bool actor = (t == PT_P) || (t == PT_M && P.h[c] == 1 && touches_top_pillbug(P, c));
             if (actor) {
-                uint32_t oa = nbr_bits(P.occ, c);
+                uint32_t oa = P.nb[c];
                 while (oa) {
                     int dt = __ffs(oa) - 1;
                     oa &= oa - 1;
@@ -684,6 +745,7 @@ HW_INL void prepare(Pos& P, const uint8_t* __restrict__ S, int lane) {
     load_position(P, S, lane);
     __syncthreads();
     build_occ_list(P, lane);
+    build_cell_masks(P, lane);
     __syncthreads();
     articulation(P, lane);
     __syncthreads();
@@ -691,45 +753,52 @@ HW_INL void prepare(Pos& P, const uint8_t* __restrict__ S, int lane) {
 
 template <bool WithMoves, bool WithFeat, bool WithAct>
 HW_INL void run_legal(Pos& P, const uint8_t* __restrict__ S, int lane, uint8_t* __restrict__ moves_row,
-                                 int32_t* __restrict__ n_slot, float* __restrict__ feat_row,
-                                 int32_t* __restrict__ act_row) {
+                      int32_t* __restrict__ n_slot, float* __restrict__ feat_row, int32_t* __restrict__ act_row) {
     prepare(P, S, lane);
-    int n = generate_legal(P, lane);
+    ListInfo L = generate_legal(P, lane);
+    if (WithFeat) features_clear(P, lane);
+    int cq = 0, cr = 0;
+    if (WithAct) centroid(P, lane, cq, cr);
     __syncthreads();
-    if (WithMoves) store_moves(P, moves_row, lane);
-    if (lane == 0) *n_slot = n;
-    if (WithAct) {
-        int cq, cr;
-        centroid(P, lane, cq, cr);
-        store_actions(P, n, cq, cr, act_row, lane);
+    emit_list<WithMoves, WithAct, WithFeat>(P, L, lane, moves_row, act_row, cq, cr);
+    if (lane == 0) *n_slot = L.n;
+    if (WithFeat) {
+        __syncthreads();
+        int m = L.total > 0 ? min(L.n, L.n_place) : 0;
+        features_finish(P, S, feat_row, lane, kFeatGen, 0u, L.ntypes ? (m + L.ntypes - 1) / L.ntypes : 0);
     }
-    if (WithFeat) fnn_features(P, S, n, feat_row, lane);
 }
 
 HW_INL void run_extract(Pos& P, const uint8_t* __restrict__ S, const uint8_t* __restrict__ M, int nl,
-                                   int lane, float* __restrict__ feat_row) {
-    int n = stage_moves(P, M, nl, lane);
+                        int lane, float* __restrict__ feat_row) {
+    int n = nl < 0 ? 0 : (nl > kMaxLegal ? kMaxLegal : nl);
     prepare(P, S, lane);
-    fnn_features(P, S, n, feat_row, lane);
+    features_clear(P, lane);
+    __syncthreads();
+    list_sources(P, M, n, lane);
+    __syncthreads();
+    features_finish(P, S, feat_row, lane, kFeatList, 0u, 0);
 }
 
 // fnn_successor_features_kernel (game_logic.cu:182-229) for one (root, move)
 HW_INL void run_successor(Pos& P, const uint8_t* __restrict__ S, const uint8_t* __restrict__ m, int lane,
-                                     float* __restrict__ feat_row) {
+                          float* __restrict__ feat_row) {
     load_position(P, S, lane);
     __syncthreads();
     if (lane == 0) apply_on_board(P, S, m[0], m[1], m[2] | (m[3] << 8), m[4] | (m[5] << 8));
     __syncthreads();
     build_occ_list(P, lane);
+    build_cell_masks(P, lane);
     __syncthreads();
     articulation(P, lane);
     __syncthreads();
     int n_place = 0;
     uint32_t bucket = compact_summary(P, lane, &n_place);
+    features_clear(P, lane);
     __syncthreads();
     // stacked levels under a top piece are read from the root row: a single
     // move leaves every level under a top unchanged
-    fnn_features(P, S, 0, feat_row, lane, false, bucket, n_place);
+    features_finish(P, S, feat_row, lane, kFeatBucket, bucket, n_place);
 }
 
 HW_INL bool run_queen_escape(Pos& P, const uint8_t* __restrict__ S, int lane) {

@@ -5,7 +5,10 @@
 //     articulation / pinned / placement): board word w sits at index w+1,
 //     indices 0 and 19 are zero pads so that any cell's 47-bit neighbour
 //     window (cells c-23 .. c+23) is three aligned word reads;
-//   * per-cell height and top-piece bytes.
+//   * per-cell height and top-piece bytes, and per-cell 6-bit direction
+//     masks of occupied neighbours (nb) and of ground-slide exits (sm),
+//     built once per board so that the generators' inner loops read one
+//     byte instead of rebuilding a neighbour window.
 // Work is spread over lanes by what is parallel in each phase: board words
 // (placements, list building), occupied cells (articulation points,
 // features), movable pieces (destination generation), legal-list slots
@@ -35,6 +38,7 @@ constexpr int kMaxPieces = 16;
 constexpr int kPool = 840;  // destination pool entries (3 ants + mosquito at 168, rest small)
 constexpr int kActors = 2;  // throw actors of one colour: its pillbug and its mosquito
 constexpr int kThrowCap = 36;
+constexpr int kSegs = 1 + kMaxPieces + kActors + 1;  // placements, pieces, actors, end
 
 // state byte offsets (hive_gpu/csrc/hive_state.cuh:239-269)
 constexpr int OFF_HEIGHT = 2645, OFF_OCC = 3176, OFF_WTOP = 3248, OFF_BTOP = 3320;
@@ -72,7 +76,7 @@ __device__ __forceinline__ int pb_get(const uint32_t* pb, int c) { return (int)(
 // 6-bit mask of directions d whose neighbour is on-grid and set in pb.
 // Bits c-23 .. c+40 are gathered into one 64-bit window; direction d sits at
 // window bit win_ofs(d).
-__device__ __forceinline__ uint32_t nbr_bits(const uint32_t* pb, int c) {
+__device__ __forceinline__ uint32_t nbr_bits_raw(const uint32_t* pb, int c) {
     int lo = c - 23;
     int wi = (lo >> 5) + 1;
     int sh = lo & 31;
@@ -82,8 +86,9 @@ __device__ __forceinline__ uint32_t nbr_bits(const uint32_t* pb, int c) {
     uint32_t m = (uint32_t)((win >> 24) & 1u) | (uint32_t)(((win >> 1) & 1u) << 1) |
                  (uint32_t)((win & 1u) << 2) | (uint32_t)(((win >> 22) & 1u) << 3) |
                  (uint32_t)(((win >> 45) & 1u) << 4) | (uint32_t)(((win >> 46) & 1u) << 5);
-    return m & grid6(c);
+    return m;
 }
+__device__ __forceinline__ uint32_t nbr_bits(const uint32_t* pb, int c) { return nbr_bits_raw(pb, c) & grid6(c); }
 
 // direction bit of g as seen from c (0 when g is not c's on-grid neighbour)
 __device__ __forceinline__ uint32_t dir_bit_to(int c, int g, uint32_t gm) {
@@ -105,7 +110,11 @@ struct alignas(16) Pos {
     uint32_t occ[kPW], wt[kPW], bt[kPW], ap[kPW], pin[kPW], plc[kPW];
     uint8_t h[544];
     uint8_t top[544];
-    uint8_t idx_of[544];
+    uint8_t nb[544];  // occupied on-grid neighbours of each cell (direction mask)
+    uint8_t sm[544];  // ground-slide exits of each cell with nothing lifted
+    uint16_t occ_pre[20];  // occupied cells in board words before word w
+    uint16_t plc_pre[20];  // placement cells in board words before word w
+    int16_t seg_base[kSegs];  // legal-list segment starts (placements, pieces, actors, end)
     uint16_t queen[2];
     uint16_t turn, stun;
     uint8_t hand[2][8];
@@ -138,7 +147,6 @@ struct alignas(16) Pos {
             uint32_t place_bb[18];
         } f;
     } u;
-    uint16_t mv[kMaxLegal][3];  // staged legal list: {type | pt<<8, from, to}
 };
 
 // ---------------------------------------------------------------- wave utils
@@ -161,11 +169,26 @@ __device__ __forceinline__ int wave_sum(int v) {
 // ---------------------------------------------------------------- state load
 // Heights, top bytes, bitboards and metadata of the state row S into P.
 HW_INL void load_position(Pos& P, const uint8_t* __restrict__ S, int lane) {
-    for (int i = lane; i < 544; i += 64) {
-        int hh = i < kCells ? S[OFF_HEIGHT + i] : 0;
-        P.h[i] = (uint8_t)hh;
-        int lvl = hh > 5 ? 5 : hh;
-        P.top[i] = hh ? S[(lvl - 1) * kCells + i] : 0;
+    // heights and level-0 bytes are independent loads, issued together; the
+    // top byte of a stack (height > 1) is a second, rare, dependent load
+    uint32_t hv[9], tv[9];
+#pragma unroll
+    for (int k = 0; k < 9; k++) {
+        int i = lane + 64 * k;
+        bool on = i < kCells;
+        hv[k] = on ? S[OFF_HEIGHT + i] : 0u;
+        tv[k] = on ? S[i] : 0u;
+    }
+#pragma unroll
+    for (int k = 0; k < 9; k++) {
+        int i = lane + 64 * k;
+        if (i < 544) {
+            int hh = (int)hv[k];
+            int t = (int)tv[k];
+            if (hh > 1) t = S[((hh > 5 ? 5 : hh) - 1) * kCells + i];
+            P.h[i] = (uint8_t)hh;
+            P.top[i] = hh ? (uint8_t)t : 0;
+        }
     }
     const uint32_t* W = reinterpret_cast<const uint32_t*>(S + OFF_OCC);  // 8-byte aligned
     if (lane < 18) {
@@ -196,23 +219,38 @@ HW_INL void load_position(Pos& P, const uint8_t* __restrict__ S, int lane) {
     }
 }
 
-// Ascending list of occupied cells (first 32) and their dense index.
+// Ascending list of occupied cells (first 32) and per-word occupied-cell
+// prefix counts.
 HW_INL void build_occ_list(Pos& P, int lane) {
     uint32_t w = lane < 18 ? P.occ[lane + 1] : 0u;
     int base = wave_excl_scan(__popc(w), lane);
     int total = wave_sum(lane < 18 ? __popc(w) : 0);
+    if (lane < 18) P.occ_pre[lane] = (uint16_t)base;
     int k = base;
-    while (w) {
+    while (w && k < 32) {
         int b = __ffs(w) - 1;
         w &= w - 1;
-        int c = lane * 32 + b;
-        if (k < 32) {
-            P.occ_cells[k] = (uint16_t)c;
-            P.idx_of[c] = (uint8_t)k;
-        }
+        P.occ_cells[k] = (uint16_t)(lane * 32 + b);
         k++;
     }
     if (lane == 0) P.n_occ = total < 32 ? total : 32;
+}
+
+// Per-cell occupied-neighbour and ground-slide direction masks of the
+// current occupancy (P.occ with zero pads).
+HW_INL void build_cell_masks(Pos& P, int lane) {
+    for (int c = lane; c < kCells; c += 64) {
+        uint32_t gm = grid6(c);
+        uint32_t n = nbr_bits_raw(P.occ, c) & gm;
+        P.nb[c] = (uint8_t)n;
+        P.sm[c] = (uint8_t)(gm & ~n & (rotl6(n) ^ rotr6(n)));
+    }
+}
+
+// index of occupied cell c in ascending cell order
+HW_INL int occ_rank(const Pos& P, int c) {
+    int w = c >> 5;
+    return P.occ_pre[w] + __popc(P.occ[w + 1] & ((1u << (c & 31)) - 1u));
 }
 
 // Articulation points (articulation.cuh:34-168).  The reference runs one DFS
@@ -228,12 +266,12 @@ HW_INL void articulation(Pos& P, int lane) {
     if (lane < 20) { P.ap[lane] = 0; P.pin[lane] = 0; }
     if (lane < N) {
         int c = P.occ_cells[lane];
-        uint32_t nm = nbr_bits(P.occ, c);
+        uint32_t nm = P.nb[c];
         uint32_t a = 0;
         while (nm) {
             int d = __ffs(nm) - 1;
             nm &= nm - 1;
-            int j = P.idx_of[step(c, d)];
+            int j = occ_rank(P, step(c, d));
             if (j < N) a |= 1u << j;
         }
         P.adj[lane] = a;
@@ -275,9 +313,14 @@ HW_INL void articulation(Pos& P, int lane) {
 // destination is empty, exactly one of the two flanking cells is occupied;
 // cell g counts as empty (the moving piece's origin).
 __device__ __forceinline__ uint32_t slide_mask(const Pos& P, int c, int g) {
-    uint32_t gm = grid6(c);
-    uint32_t n = nbr_bits(P.occ, c) & ~dir_bit_to(c, g, gm);
-    return gm & ~n & (rotl6(n) ^ rotr6(n));
+    uint32_t s = P.sm[c];
+    int dlt = g - c;
+    if (dlt != 0 && dlt >= -23 && dlt <= 23) {  // g may be a neighbour: recompute with g empty
+        uint32_t gm = grid6(c);
+        uint32_t n = P.nb[c] & ~dir_bit_to(c, g, gm);
+        s = gm & ~n & (rotl6(n) ^ rotr6(n));
+    }
+    return s;
 }
 
 // heights of the six neighbours (0 off-grid), 4 bits each: direction d at bits 4d..4d+3
@@ -326,7 +369,7 @@ HW_INL int gen_step(const Pos& P, int c, uint16_t* out) {
 HW_INL int gen_hopper(const Pos& P, int c, uint16_t* out) {
     int n = 0;
     uint32_t gm = grid6(c);
-    uint32_t m = nbr_bits(P.occ, c);
+    uint32_t m = P.nb[c];
     for (int d = 0; d < 6; d++) {
         if (!((m >> d) & 1u)) continue;
         int p = step(c, d);
@@ -415,14 +458,14 @@ HW_INL int gen_ladybug(const Pos& P, int c, uint16_t* out, uint32_t* got) {
     int n = 0;
     uint32_t g0 = grid6(c);
     uint32_t nh0 = nbr_heights(P, c, g0);
-    uint32_t o0 = nbr_bits(P.occ, c);
+    uint32_t o0 = P.nb[c];
     int hc = P.h[c];
     for (int d1 = 0; d1 < 6; d1++) {
         if (!((o0 >> d1) & 1u)) continue;
         int p1 = step(c, d1);
         if (gate_high(nh0, d1, max(hc - 1, hof(nh0, d1)))) continue;
         uint32_t nh1 = nbr_heights(P, p1, grid6(p1));
-        uint32_t o1 = nbr_bits(P.occ, p1);
+        uint32_t o1 = P.nb[p1];
         int hp1 = P.h[p1];
         for (int d2 = 0; d2 < 6; d2++) {
             if (!((o1 >> d2) & 1u)) continue;
@@ -431,7 +474,7 @@ HW_INL int gen_ladybug(const Pos& P, int c, uint16_t* out, uint32_t* got) {
             if (gate_high(nh1, d2, max(hp1, hof(nh1, d2)))) continue;
             uint32_t g2 = grid6(p2);
             uint32_t nh2 = nbr_heights(P, p2, g2);
-            uint32_t o2 = nbr_bits(P.occ, p2);
+            uint32_t o2 = P.nb[p2];
             int mh3 = P.h[p2];
             for (int d3 = 0; d3 < 6; d3++) {
                 if (!((g2 >> d3) & 1u) || ((o2 >> d3) & 1u)) continue;
@@ -453,7 +496,7 @@ HW_INL int gen_ladybug(const Pos& P, int c, uint16_t* out, uint32_t* got) {
 HW_INL int gen_mosquito(const Pos& P, int c, uint16_t* out, uint32_t* tmpset, uint32_t* unionset) {
     if (P.h[c] > 1) return gen_beetle(P, c, out);
     uint32_t gm = grid6(c);
-    uint32_t om = nbr_bits(P.occ, c);
+    uint32_t om = P.nb[c];
     uint32_t has = 0;
     for (int d = 0; d < 6; d++)
         if ((om >> d) & 1u) {
@@ -491,7 +534,7 @@ HW_INL int gen_throws(const Pos& P, int a, uint16_t* from, uint16_t* to, uint8_t
     uint32_t ga = grid6(a);
     uint32_t nha = nbr_heights(P, a, ga);
     int ph = P.h[a];
-    uint32_t oa = nbr_bits(P.occ, a);
+    uint32_t oa = P.nb[a];
     for (int dt = 0; dt < 6; dt++) {
         if (!((oa >> dt) & 1u)) continue;
         int t = step(a, dt);
@@ -518,7 +561,7 @@ HW_INL int gen_throws(const Pos& P, int a, uint16_t* from, uint16_t* to, uint8_t
 }
 
 __device__ __forceinline__ bool touches_top_pillbug(const Pos& P, int c) {
-    uint32_t m = nbr_bits(P.occ, c);
+    uint32_t m = P.nb[c];
     while (m) {
         int d = __ffs(m) - 1;
         m &= m - 1;
