@@ -745,8 +745,8 @@ HW_INL void prepare(Pos& P, const uint8_t* __restrict__ S, int lane) {
     load_position(P, S, lane);
     __syncthreads();
     build_occ_list(P, lane);
-    build_cell_masks(P, lane);
     __syncthreads();
+    build_cell_masks(P, lane);
     articulation(P, lane);
     __syncthreads();
 }
@@ -788,8 +788,8 @@ HW_INL void run_successor(Pos& P, const uint8_t* __restrict__ S, const uint8_t* 
     if (lane == 0) apply_on_board(P, S, m[0], m[1], m[2] | (m[3] << 8), m[4] | (m[5] << 8));
     __syncthreads();
     build_occ_list(P, lane);
-    build_cell_masks(P, lane);
     __syncthreads();
+    build_cell_masks(P, lane);
     articulation(P, lane);
     __syncthreads();
     int n_place = 0;

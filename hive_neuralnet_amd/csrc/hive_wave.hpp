@@ -90,6 +90,14 @@ __device__ __forceinline__ uint32_t nbr_bits_raw(const uint32_t* pb, int c) {
 }
 __device__ __forceinline__ uint32_t nbr_bits(const uint32_t* pb, int c) { return nbr_bits_raw(pb, c) & grid6(c); }
 
+// 32 board bits starting at bit_off (>= -32) of a padded bitboard
+__device__ __forceinline__ uint32_t word_field(const uint32_t* pb, int bit_off) {
+    int wi = (bit_off >> 5) + 1;
+    int sh = bit_off & 31;
+    uint64_t v = (uint64_t)pb[wi] | ((uint64_t)pb[wi + 1] << 32);
+    return (uint32_t)(v >> sh);
+}
+
 // direction bit of g as seen from c (0 when g is not c's on-grid neighbour)
 __device__ __forceinline__ uint32_t dir_bit_to(int c, int g, uint32_t gm) {
     int diff = g - c;
@@ -237,13 +245,36 @@ HW_INL void build_occ_list(Pos& P, int lane) {
 }
 
 // Per-cell occupied-neighbour and ground-slide direction masks of the
-// current occupancy (P.occ with zero pads).
+// current occupancy (P.occ with zero pads), for the cells of the hive's
+// bounding box grown by one row and column: every hex neighbour of an
+// occupied cell lies in it.  Readers only look at occupied cells and their
+// neighbours; the other entries are left unwritten.
 HW_INL void build_cell_masks(Pos& P, int lane) {
-    for (int c = lane; c < kCells; c += 64) {
-        uint32_t gm = grid6(c);
-        uint32_t n = nbr_bits_raw(P.occ, c) & gm;
-        P.nb[c] = (uint8_t)n;
-        P.sm[c] = (uint8_t)(gm & ~n & (rotl6(n) ^ rotr6(n)));
+    uint32_t rowbits = lane < kGrid ? (word_field(P.occ, kGrid * lane) & 0x7FFFFFu) : 0u;
+    uint64_t rows = __ballot(rowbits != 0);
+    if (rows == 0) return;
+    uint32_t cols = rowbits;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) cols |= __shfl_xor(cols, o, 64);
+    int r0 = __ffsll((unsigned long long)rows) - 1, r1 = 63 - __clzll((long long)rows);
+    int c0 = __ffs(cols) - 1, c1 = 31 - __clz(cols);
+    int rlo = r0 > 0 ? r0 - 1 : 0, rhi = r1 < kGrid - 1 ? r1 + 1 : kGrid - 1;
+    int clo = c0 > 0 ? c0 - 1 : 0, chi = c1 < kGrid - 1 ? c1 + 1 : kGrid - 1;
+    int bw = chi - clo + 1, n = bw * (rhi - rlo + 1);
+    for (int k = lane; k < n; k += 64) {
+        int rr = k / bw;
+        int row = rlo + rr, col = clo + (k - rr * bw);
+        int c = row * kGrid + col;
+        uint32_t gm = 0;
+        if (col < 22) gm |= 1u;
+        if (col < 22 && row > 0) gm |= 2u;
+        if (row > 0) gm |= 4u;
+        if (col > 0) gm |= 8u;
+        if (col > 0 && row < 22) gm |= 16u;
+        if (row < 22) gm |= 32u;
+        uint32_t nm = nbr_bits_raw(P.occ, c) & gm;
+        P.nb[c] = (uint8_t)nm;
+        P.sm[c] = (uint8_t)(gm & ~nm & (rotl6(nm) ^ rotr6(nm)));
     }
 }
 
@@ -266,7 +297,7 @@ HW_INL void articulation(Pos& P, int lane) {
     if (lane < 20) { P.ap[lane] = 0; P.pin[lane] = 0; }
     if (lane < N) {
         int c = P.occ_cells[lane];
-        uint32_t nm = P.nb[c];
+        uint32_t nm = nbr_bits(P.occ, c);
         uint32_t a = 0;
         while (nm) {
             int d = __ffs(nm) - 1;
@@ -575,15 +606,9 @@ __device__ __forceinline__ int type_capacity(int t) {
 }
 
 // ---------------------------------------------------------------- placement
-// Placement cells (find_placement_positions :1064-1140) into P.plc, as a
+// Placement cells (find_placement_positions :1064-1140) are computed as a
 // bit-parallel neighbourhood expression over board words (lane w < 18 owns
-// word w).  Returns the number of cells (wave-uniform).
-HW_INL uint32_t word_field(const uint32_t* pb, int bit_off) {
-    int wi = (bit_off >> 5) + 1;
-    int sh = bit_off & 31;
-    uint64_t v = (uint64_t)pb[wi] | ((uint64_t)pb[wi + 1] << 32);
-    return (uint32_t)(v >> sh);
-}
+// word w) from nbr_union_word below.
 
 // kGridMask.m[d][w]: cells of board word w whose d-neighbour is on the grid
 struct GridMasks {

@@ -20,53 +20,60 @@
 #define __launch_bounds__(x)
 
 namespace wave_emu {
+// A workgroup of up to 4 waves: shuffles and ballots rendezvous per wave,
+// __syncthreads across the workgroup.
 struct Ctx {
-    std::barrier<>* bar;
-    int64_t slot[64];
+    std::barrier<>* wave_bar[4];
+    std::barrier<>* group_bar;
+    int64_t slot[256];
 };
 inline Ctx* g_ctx = nullptr;
-inline thread_local int g_lane = 0;
-inline void sync() { g_ctx->bar->arrive_and_wait(); }
+inline thread_local int g_tid = 0;
+inline int lane() { return g_tid & 63; }
+inline int wave() { return g_tid >> 6; }
+inline void wave_sync() { g_ctx->wave_bar[wave()]->arrive_and_wait(); }
+inline void group_sync() { g_ctx->group_bar->arrive_and_wait(); }
 template <typename T>
 inline T exchange(T v, int src) {
-    g_ctx->slot[g_lane] = (int64_t)v;
-    sync();
-    T r = (T)g_ctx->slot[src];
-    sync();
+    g_ctx->slot[g_tid] = (int64_t)v;
+    wave_sync();
+    T r = (T)g_ctx->slot[(wave() << 6) | (src & 63)];
+    wave_sync();
     return r;
 }
 }  // namespace wave_emu
 
 struct EmuThreadIdx {
-    operator int() const { return wave_emu::g_lane; }
+    operator int() const { return wave_emu::g_tid; }
 };
 struct EmuDim3 {
     EmuThreadIdx x;
 };
 inline EmuDim3 threadIdx;
 
-inline void __syncthreads() { wave_emu::sync(); }
+inline void __syncthreads() { wave_emu::group_sync(); }
 
 template <typename T>
 inline T __shfl_up(T v, unsigned o, int = 64) {
-    int src = wave_emu::g_lane - (int)o;
-    return wave_emu::exchange(v, src >= 0 ? src : wave_emu::g_lane);
+    int src = wave_emu::lane() - (int)o;
+    return wave_emu::exchange(v, src >= 0 ? src : wave_emu::lane());
 }
 template <typename T>
 inline T __shfl_xor(T v, int m, int = 64) {
-    return wave_emu::exchange(v, wave_emu::g_lane ^ m);
+    return wave_emu::exchange(v, wave_emu::lane() ^ m);
 }
 template <typename T>
 inline T __shfl(T v, int src, int = 64) {
     return wave_emu::exchange(v, src & 63);
 }
 inline uint64_t __ballot(int pred) {
-    wave_emu::g_ctx->slot[wave_emu::g_lane] = pred ? 1 : 0;
-    wave_emu::sync();
+    wave_emu::g_ctx->slot[wave_emu::g_tid] = pred ? 1 : 0;
+    wave_emu::wave_sync();
     uint64_t m = 0;
+    int base = wave_emu::wave() << 6;
     for (int i = 0; i < 64; i++)
-        if (wave_emu::g_ctx->slot[i]) m |= 1ull << i;
-    wave_emu::sync();
+        if (wave_emu::g_ctx->slot[base + i]) m |= 1ull << i;
+    wave_emu::wave_sync();
     return m;
 }
 inline int atomicAdd(int* p, int v) { return __atomic_fetch_add(p, v, __ATOMIC_SEQ_CST); }
@@ -75,6 +82,9 @@ inline int __popc(uint32_t x) { return __builtin_popcount(x); }
 inline int __popcll(uint64_t x) { return __builtin_popcountll(x); }
 inline int __ffs(uint32_t x) { return __builtin_ffs((int)x); }
 inline int __ffs(int x) { return __builtin_ffs(x); }
+inline int __ffsll(unsigned long long x) { return __builtin_ffsll((long long)x); }
+inline int __clz(uint32_t x) { return x ? __builtin_clz(x) : 32; }
+inline int __clzll(long long x) { return x ? __builtin_clzll((unsigned long long)x) : 64; }
 inline uint32_t __umulhi(uint32_t a, uint32_t b) { return (uint32_t)(((uint64_t)a * b) >> 32); }
 inline int min(int a, int b) { return a < b ? a : b; }
 inline int max(int a, int b) { return a > b ? a : b; }

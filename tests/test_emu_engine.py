@@ -31,7 +31,7 @@ def _p(a):
 @pytest.mark.parametrize("name", ["c1", "c2", "c3"])
 def test_emulated_legal_features(emu, oracle, name):
     g = load_golden(name)
-    st = np.ascontiguousarray(g["states"][:48])
+    st = np.ascontiguousarray(g["states"][:47])
     B = len(st)
     mv = np.zeros((B, 256, 6), np.uint8)
     n = np.zeros(B, np.int32)

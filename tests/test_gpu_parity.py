@@ -68,6 +68,19 @@ def test_golden_moves_features(ext, name):
     assert feat3.shape == (B, 122)
 
 
+@pytest.mark.parametrize("B", [1, 2, 3, 5, 7, 130])
+def test_small_batches(ext, B):
+    """Small and odd batch sizes, fused entry point against the golden lists."""
+    g = load_golden("c3")
+    st = _cuda(g["states"][1:B + 1])
+    moves, n, feat, act = ext.generate_legal_moves_features_actions_batch(st, B)
+    assert np.array_equal(n.cpu().numpy(), g["n"][1:B + 1])
+    assert np.array_equal(moves.cpu().numpy(), g["moves"][1:B + 1])
+    assert np.array_equal(_bits(feat.cpu().numpy()), _bits(g["features"][1:B + 1]))
+    act2 = ext.legal_moves_to_actions_batch(st, moves, n, B)
+    assert torch.equal(act, act2)
+
+
 @pytest.mark.parametrize("name", ["c1", "c2", "c3"])
 def test_golden_successors_queen_escape_apply(ext, name):
     g = load_golden(name)
