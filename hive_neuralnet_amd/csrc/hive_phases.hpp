@@ -198,7 +198,7 @@ HW_INL void list_slot(const Pos& P, const ListInfo& L, int i, int& tp, int& from
     } else if (lo <= L.n_pieces) {
         int j = lo - 1;
         from = P.piece_cell[j];
-        to = P.pool[P.piece_off[j] + k];
+        to = P.pool[P.piece_off[j] + k] & kCellMask;
         tp = MV_MOVE | (P.piece_type[j] << 8);
     } else {
         int j = lo - 1 - L.n_pieces;

@@ -98,11 +98,14 @@ __device__ __forceinline__ uint32_t word_field(const uint32_t* pb, int bit_off) 
     return (uint32_t)(v >> sh);
 }
 
+// window positions (cell offset + 23) of the six directions, as a bit set
+constexpr uint64_t kRingWin = (1ull << 24) | (1ull << 1) | (1ull << 0) | (1ull << 22) | (1ull << 45) | (1ull << 46);
+
 // direction bit of g as seen from c (0 when g is not c's on-grid neighbour)
 __device__ __forceinline__ uint32_t dir_bit_to(int c, int g, uint32_t gm) {
-    int diff = g - c;
-    uint32_t b = diff == 1 ? 1u : diff == -22 ? 2u : diff == -23 ? 4u : diff == -1 ? 8u
-               : diff == 22 ? 16u : diff == 23 ? 32u : 0u;
+    int w = g - c + 23;
+    uint32_t b = (uint32_t)(w == 24) | ((uint32_t)(w == 1) << 1) | ((uint32_t)(w == 0) << 2) |
+                 ((uint32_t)(w == 22) << 3) | ((uint32_t)(w == 45) << 4) | ((uint32_t)(w == 46) << 5);
     return b & gm;
 }
 
@@ -158,21 +161,26 @@ struct alignas(16) Pos {
 };
 
 // ---------------------------------------------------------------- wave utils
-__device__ __forceinline__ int wave_excl_scan(int v, int lane) {
-    int x = v;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        int y = __shfl_up(x, o, 64);
-        if (lane >= o) x += y;
-    }
-    return x - v;
+// Inclusive prefix sum over the 64 lanes with DPP lane moves: shifts by 1,
+// 2, 4, 8 within each 16-lane row, then the row totals carried by
+// row_bcast:15 (into rows 1, 3) and row_bcast:31 (into rows 2, 3).
+// Lanes a move has no source for add 0 (bound_ctrl), so do disabled rows.
+__device__ __forceinline__ int wave_incl_scan(int x) {
+    x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, true);  // row_shr:1
+    x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, true);  // row_shr:2
+    x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, true);  // row_shr:4
+    x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, true);  // row_shr:8
+    x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xa, 0xf, true);  // row_bcast:15
+    x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xc, 0xf, true);  // row_bcast:31
+    return x;
 }
 
-__device__ __forceinline__ int wave_sum(int v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
+__device__ __forceinline__ int wave_excl_scan(int v, int lane) {
+    (void)lane;
+    return wave_incl_scan(v) - v;
 }
+
+__device__ __forceinline__ int wave_sum(int v) { return __builtin_amdgcn_readlane(wave_incl_scan(v), 63); }
 
 // ---------------------------------------------------------------- state load
 // Heights, top bytes, bitboards and metadata of the state row S into P.
@@ -345,8 +353,8 @@ HW_INL void articulation(Pos& P, int lane) {
 // cell g counts as empty (the moving piece's origin).
 __device__ __forceinline__ uint32_t slide_mask(const Pos& P, int c, int g) {
     uint32_t s = P.sm[c];
-    int dlt = g - c;
-    if (dlt != 0 && dlt >= -23 && dlt <= 23) {  // g may be a neighbour: recompute with g empty
+    uint32_t w = (uint32_t)(g - c + 23);
+    if (w < 47u && ((kRingWin >> w) & 1ull)) {  // g may be a neighbour: recompute with g empty
         uint32_t gm = grid6(c);
         uint32_t n = P.nb[c] & ~dir_bit_to(c, g, gm);
         s = gm & ~n & (rotl6(n) ^ rotr6(n));
@@ -375,9 +383,7 @@ __device__ __forceinline__ void set_clear(uint32_t* s) {
 }
 __device__ __forceinline__ bool set_insert(uint32_t* s, int c) {  // true if newly inserted
     uint32_t bit = 1u << (c & 31);
-    uint32_t old = s[c >> 5];
-    s[c >> 5] = old | bit;
-    return !(old & bit);
+    return !(atomicOr(&s[c >> 5], bit) & bit);
 }
 
 // ---------------------------------------------------------------- generators
@@ -417,22 +423,30 @@ HW_INL int gen_hopper(const Pos& P, int c, uint16_t* out) {
 
 // FIFO breadth-first ant search (gen_ant_moves_with_perimeter :267-313,
 // emit_ant_moves_with_perimeter :348-388): seeds in direction order, each
-// dequeued cell expanded in direction order, ant lifted from c.
+// dequeued cell expanded in direction order, ant lifted from c.  An entry
+// is the cell | arrival direction << kDirShift (readers mask with kCellMask):
+// the exit back to the parent leads to a visited cell and is skipped.
+constexpr int kDirShift = 10;
+constexpr int kCellMask = (1 << kDirShift) - 1;
 HW_INL int gen_ant(const Pos& P, int c, uint16_t* out, int cap, uint32_t* seen) {
     set_clear(seen);
     set_insert(seen, c);
     int head = 0, tail = 0;
     int cur = c;
+    uint32_t back = 0;
     for (;;) {
-        uint32_t m = slide_mask(P, cur, c);
+        uint32_t m = slide_mask(P, cur, c) & ~back;
         while (m && tail < cap) {
             int d = __ffs(m) - 1;
             m &= m - 1;
             int dest = step(cur, d);
-            if (set_insert(seen, dest)) out[tail++] = (uint16_t)dest;
+            if (set_insert(seen, dest)) out[tail++] = (uint16_t)(dest | (d << kDirShift));
         }
         if (head >= tail || tail >= cap) break;
-        cur = out[head++];
+        int e = out[head++];
+        cur = e & kCellMask;
+        int d = e >> kDirShift;
+        back = 1u << (d >= 3 ? d - 3 : d + 3);
     }
     return tail;
 }
@@ -550,7 +564,7 @@ HW_INL int gen_mosquito(const Pos& P, int c, uint16_t* out, uint32_t* tmpset, ui
         }
         int w = n;
         for (int i = 0; i < m; i++) {
-            int x = tail[i];
+            int x = tail[i] & kCellMask;
             if (set_insert(unionset, x) && w < 128) out[w++] = (uint16_t)x;
         }
         n = w;

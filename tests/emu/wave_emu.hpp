@@ -76,6 +76,27 @@ inline uint64_t __ballot(int pred) {
     wave_emu::wave_sync();
     return m;
 }
+// DPP lane moves used by the engine's prefix sums: row_shr:1..15, row_bcast:15,
+// row_bcast:31 (GFX9 semantics).  Every lane of the wave calls it.
+inline int __builtin_amdgcn_update_dpp(int old, int src, int ctrl, int row_mask, int bank_mask, bool bound_ctrl) {
+    int l = wave_emu::lane(), row = l >> 4, r = l & 15, bank = r >> 2;
+    int from = -1;
+    if (ctrl >= 0x111 && ctrl <= 0x11F) {
+        int n = ctrl - 0x110;
+        if (r >= n) from = l - n;
+    } else if (ctrl == 0x142) {
+        if (row >= 1) from = (row - 1) * 16 + 15;
+    } else if (ctrl == 0x143) {
+        if (row >= 2) from = 31;
+    } else {
+        abort();
+    }
+    int v = wave_emu::exchange(src, from >= 0 ? from : l);
+    if (!((row_mask >> row) & 1) || !((bank_mask >> bank) & 1)) return old;
+    if (from < 0) return bound_ctrl ? 0 : old;
+    return v;
+}
+inline int __builtin_amdgcn_readlane(int v, int l) { return wave_emu::exchange(v, l); }
 inline int atomicAdd(int* p, int v) { return __atomic_fetch_add(p, v, __ATOMIC_SEQ_CST); }
 inline uint32_t atomicOr(uint32_t* p, uint32_t v) { return __atomic_fetch_or(p, v, __ATOMIC_SEQ_CST); }
 inline int __popc(uint32_t x) { return __builtin_popcount(x); }
