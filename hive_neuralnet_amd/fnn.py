@@ -54,6 +54,20 @@ class HiveFNN(nn.Module):
         self.action_fc1 = nn.Linear(c.embed_dim * 2, c.action_hidden)
         self.action_fc2 = nn.Linear(c.action_hidden, 1)
 
+    def load_state_dict(self, state_dict, strict: bool = True, assign: bool = False):
+        """Loads checkpoints whose fc1 was trained on a different feature count
+        (fnn_network.py:74-94): the overlapping block of fc1.weight is kept and the
+        rest drawn from N(0, 1e-3)."""
+        state = dict(state_dict)
+        cur = self.fc1.weight
+        old = state.get("fc1.weight")
+        if old is not None and old.shape != cur.shape:
+            grown = torch.empty_like(cur).normal_(mean=0.0, std=1e-3)
+            r, c = min(old.shape[0], cur.shape[0]), min(old.shape[1], cur.shape[1])
+            grown[:r, :c] = old[:r, :c].to(grown)
+            state["fc1.weight"] = grown
+        return super().load_state_dict(state, strict=strict, assign=assign)
+
     def encode(self, features: torch.Tensor) -> torch.Tensor:
         return self.fc2(self.ln1(torch.sigmoid(self.fc1(features))))
 

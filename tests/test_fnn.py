@@ -50,3 +50,15 @@ def test_forward_against_numpy_float64():
     np.testing.assert_allclose(emb.numpy(), e, rtol=1e-5, atol=1e-5)
     np.testing.assert_allclose(vals[:, 0].numpy(), v, rtol=1e-5, atol=1e-6)
     np.testing.assert_allclose(logits.numpy(), logit, rtol=1e-5, atol=1e-5)
+
+
+def test_load_state_dict_grows_fc1():
+    """A checkpoint trained on fewer features loads: the known block is kept."""
+    net = seeded_large(1, device="cpu")
+    sd = {k: v.clone() for k, v in net.state_dict().items()}
+    sd["fc1.weight"] = sd["fc1.weight"][:, :100].clone()
+    other = seeded_large(2, device="cpu")
+    other.load_state_dict(sd)
+    assert torch.equal(other.fc1.weight[:, :100], net.fc1.weight[:, :100])
+    assert other.fc1.weight[:, 100:].abs().max() < 0.01
+    assert torch.equal(other.fc2.weight, net.fc2.weight)
