@@ -16,7 +16,7 @@ namespace hw {
 // the game is over.
 //
 // The list is not materialised in LDS: generate_legal leaves the placement
-// cells (P.plc, P.plc_pre), the per-piece destination lists (P.pool), the
+// cells (P.plc, P.plc_pre), the per-piece destination lists (P.u2.pool), the
 // throw lists and the segment starts (P.seg_base: placements, one segment
 // per piece, one per throw actor, end) on the board; list_slot() decodes any
 // slot from them, so that slots are written to memory lane-parallel.
@@ -83,7 +83,7 @@ HW_INL ListInfo generate_legal(Pos& P, int lane) {
             mw &= mw - 1;
             int c = lane * 32 + b;
             P.piece_cell[k] = (uint16_t)c;
-            P.piece_type[k] = P.top[c] & 15;
+            P.piece_type[k] = P.tp(c) & 15;
             k++;
         }
         // throw actors among occupied cells (cell order); the thrower is not
@@ -91,10 +91,10 @@ HW_INL ListInfo generate_legal(Pos& P, int lane) {
         bool actor = false;
         if (lane < P.n_occ) {
             int c = P.occ_cells[lane];
-            int tb = P.top[c];
+            int tb = P.tp(c);
             int t = tb & 15;
             if (((tb >> 4) & 1) == me)
-                actor = (t == PT_P) || (t == PT_M && P.h[c] == 1 && touches_top_pillbug(P, c));
+                actor = (t == PT_P) || (t == PT_M && P.hgt(c) == 1 && touches_top_pillbug(P, c));
         }
         uint64_t am = __ballot(actor);
         n_actors = min(__popcll(am), kActors);
@@ -105,22 +105,24 @@ HW_INL ListInfo generate_legal(Pos& P, int lane) {
     }
     __syncthreads();
 
-    // -- destination pool offsets by type capacity
+    // -- destination pool offsets by type capacity, visited sets by need
     int cap = lane < n_pieces ? type_capacity(P.piece_type[lane]) : 0;
     int off = wave_excl_scan(cap, lane);
-    if (lane < n_pieces && off + cap > kPool) {  // only reachable for states with impossible piece counts
+    int nsets = lane < n_pieces ? type_sets(P.piece_type[lane]) : 0;
+    int set0 = wave_excl_scan(nsets, lane);
+    if (lane < n_pieces && (off + cap > kPool || set0 + nsets > kSets)) {  // impossible piece counts
         P.piece_off[lane] = 0;
         P.piece_cnt[lane] = 0;
     } else if (lane < n_pieces) {
         int c = P.piece_cell[lane];
         int t = P.piece_type[lane];
-        uint16_t* out = P.pool + off;
-        uint32_t* s0 = P.u.lane_bb[lane][0];
-        uint32_t* s1 = P.u.lane_bb[lane][1];
+        uint16_t* out = P.u2.pool + off;
+        uint32_t* s0 = P.u1.sets[set0 < kSets ? set0 : 0];
+        uint32_t* s1 = P.u1.sets[set0 + 1 < kSets ? set0 + 1 : 0];
         int m = 0;
         switch (t) {
             case PT_Q: case PT_P: m = gen_step(P, c, out); break;
-            case PT_A: m = gen_ant(P, c, out, 168, s0); break;
+            case PT_A: m = gen_ant(P, c, out, 64, s0); break;
             case PT_G: m = gen_hopper(P, c, out); break;
             case PT_S: m = gen_spider(P, c, out, s0); break;
             case PT_B: m = gen_beetle(P, c, out); break;
@@ -198,7 +200,7 @@ HW_INL void list_slot(const Pos& P, const ListInfo& L, int i, int& tp, int& from
     } else if (lo <= L.n_pieces) {
         int j = lo - 1;
         from = P.piece_cell[j];
-        to = P.pool[P.piece_off[j] + k] & kCellMask;
+        to = P.u2.pool[P.piece_off[j] + k] & kCellMask;
         tp = MV_MOVE | (P.piece_type[j] << 8);
     } else {
         int j = lo - 1 - L.n_pieces;
@@ -218,19 +220,24 @@ HW_INL void list_slot(const Pos& P, const ListInfo& L, int i, int& tp, int& from
 // piece).
 enum { kFeatList = 0, kFeatGen = 1, kFeatBucket = 2 };
 
-HW_INL void features_clear(Pos& P, int lane) {
-    auto& F = P.u.f;
+// The list's source sets (u1: after destination generation) ...
+HW_INL void sources_clear(Pos& P, int lane) {
+    auto& S = P.u1.s;
+    for (int i = lane; i < 16 * 18; i += 64) (&S.from_bb[0][0])[i] = 0;
+    if (lane < 18) S.place_bb[lane] = 0;
+}
+// ... and the feature counters (u2: after list emission).
+HW_INL void counters_clear(Pos& P, int lane) {
+    auto& F = P.u2.c;
     for (int i = lane; i < 128; i += 64) F.cnt[i] = 0;
     if (lane < 16) { F.dsum[lane] = 0; F.dcnt[lane] = 0; }
     if (lane < 2) { F.ring[lane] = 0; F.covered[lane] = 0; F.capable[lane] = 0; }
     if (lane == 0) F.n_cap = 0;
-    for (int i = lane; i < 16 * 18; i += 64) (&F.from_bb[0][0])[i] = 0;
-    if (lane < 18) F.place_bb[lane] = 0;
 }
 
 // MOVE source / PLACE destination sets of a caller-supplied list (global memory)
 HW_INL void list_sources(Pos& P, const uint8_t* __restrict__ M, int n, int lane) {
-    auto& F = P.u.f;
+    auto& F = P.u1.s;
     const int me = P.turn & 1;
     for (int i = lane; i < n; i += 64) {
         const uint8_t* m = M + 6 * i;
@@ -238,7 +245,7 @@ HW_INL void list_sources(Pos& P, const uint8_t* __restrict__ M, int n, int lane)
         if (ty == MV_MOVE) {
             int fc = m[2] | (m[3] << 8);
             if (fc < 544 && pt >= 1 && pt <= 8) {
-                int owner = P.h[fc] > 0 ? (P.top[fc] >> 4) & 1 : me;
+                int owner = P.hgt(fc) > 0 ? (P.tp(fc) >> 4) & 1 : me;
                 atomicOr(&F.from_bb[(pt - 1) * 2 + owner][fc >> 5], 1u << (fc & 31));
             }
         } else if (ty == MV_PLACE) {
@@ -248,16 +255,17 @@ HW_INL void list_sources(Pos& P, const uint8_t* __restrict__ M, int n, int lane)
     }
 }
 
-// Needs features_clear and the legal-move sets (modes kFeatList / kFeatGen)
+// Needs sources_clear / counters_clear and the legal-move sets (modes kFeatList / kFeatGen)
 // complete, behind a barrier.
 HW_INL void features_finish(Pos& P, const uint8_t* __restrict__ S, float* __restrict__ out, int lane, int mode,
                             uint32_t bucket, int n_place) {
-    auto& F = P.u.f;
+    auto& F = P.u2.c;
+    const auto& SB = P.u1.s;
     const int me = P.turn & 1;
     if (lane < P.n_occ) {
         int c = P.occ_cells[lane];
-        int h = P.h[c];
-        int tb = P.top[c];
+        int h = P.hgt(c);
+        int tb = P.tp(c);
         int pt = tb & 15, col = (tb >> 4) & 1, tc = (pt - 1) * 2 + col;
         if (pt < PT_Q || pt > PT_P) pt = 0;  // impossible top byte: contributes nothing
         if (pt) atomicAdd(&F.cnt[tc], 1);
@@ -289,7 +297,7 @@ HW_INL void features_finish(Pos& P, const uint8_t* __restrict__ S, float* __rest
                 m &= m - 1;
                 int nb = step(c, d);
                 if ((int)P.stun == nb) continue;
-                if ((P.top[nb] & 15) == PT_P) { capable = true; break; }
+                if ((P.tp(nb) & 15) == PT_P) { capable = true; break; }
             }
         }
         if (capable) {
@@ -309,7 +317,7 @@ HW_INL void features_finish(Pos& P, const uint8_t* __restrict__ S, float* __rest
             m &= m - 1;
             int nb = step(p, d);
             if ((int)P.stun == nb) continue;
-            int nc = (P.top[nb] >> 4) & 1;
+            int nc = (P.tp(nb) >> 4) & 1;
             if (nc == col) atomicAdd(&F.cnt[106 + col], 1);
             else atomicAdd(&F.cnt[108 + nc], 1);
         }
@@ -319,13 +327,13 @@ HW_INL void features_finish(Pos& P, const uint8_t* __restrict__ S, float* __rest
         else if (lane == 16) F.cnt[100] = n_place;
     } else if (lane < 16) {
         int s = 0;
-        for (int w = 0; w < 18; w++) s += __popc(F.from_bb[lane][w]);
+        for (int w = 0; w < 18; w++) s += __popc(SB.from_bb[lane][w]);
         F.cnt[64 + lane] = s;
     } else if (lane == 16) {
         int s = n_place;
         if (mode == kFeatList) {
             s = 0;
-            for (int w = 0; w < 18; w++) s += __popc(F.place_bb[w]);
+            for (int w = 0; w < 18; w++) s += __popc(SB.place_bb[w]);
         }
         F.cnt[100] = s;
     }
@@ -426,8 +434,8 @@ HW_INL void emit_list(Pos& P, const ListInfo& L, int lane, uint8_t* __restrict__
                     bool thr = seg > L.n_pieces;
                     int pt = tp >> 8;
                     if ((thr || i == P.seg_base[seg]) && from < 544 && pt >= 1 && pt <= 8) {
-                        int owner = thr ? (P.top[from] >> 4) & 1 : me;
-                        atomicOr(&P.u.f.from_bb[(pt - 1) * 2 + owner][from >> 5], 1u << (from & 31));
+                        int owner = thr ? (P.tp(from) >> 4) & 1 : me;
+                        atomicOr(&P.u1.s.from_bb[(pt - 1) * 2 + owner][from >> 5], 1u << (from & 31));
                     }
                 }
             }
@@ -489,7 +497,7 @@ HW_INL bool has_beetle(const Pos& P, int c) {
     uint32_t gm = grid6(c);
     uint32_t nh = nbr_heights(P, c, gm);
     uint32_t sm = slide_mask(P, c, c);
-    int below = P.h[c] - 1;
+    int below = P.hgt(c) - 1;
     for (int d = 0; d < 6; d++) {
         if (!((gm >> d) & 1u)) continue;
         int mh = max(hof(nh, d), below);
@@ -506,14 +514,14 @@ HW_INL bool has_ladybug(const Pos& P, int c) {
     uint32_t g0 = grid6(c);
     uint32_t nh0 = nbr_heights(P, c, g0);
     uint32_t o0 = P.nb[c];
-    int hc = P.h[c];
+    int hc = P.hgt(c);
     for (int d1 = 0; d1 < 6; d1++) {
         if (!((o0 >> d1) & 1u)) continue;
         int p1 = step(c, d1);
         if (gate_high(nh0, d1, max(hc - 1, hof(nh0, d1)))) continue;
         uint32_t nh1 = nbr_heights(P, p1, grid6(p1));
         uint32_t o1 = P.nb[p1];
-        int hp1 = P.h[p1];
+        int hp1 = P.hgt(p1);
         for (int d2 = 0; d2 < 6; d2++) {
             if (!((o1 >> d2) & 1u)) continue;
             int p2 = step(p1, d2);
@@ -522,7 +530,7 @@ HW_INL bool has_ladybug(const Pos& P, int c) {
             uint32_t g2 = grid6(p2);
             uint32_t nh2 = nbr_heights(P, p2, g2);
             uint32_t o2 = P.nb[p2];
-            int mh3 = P.h[p2];
+            int mh3 = P.hgt(p2);
             for (int d3 = 0; d3 < 6; d3++) {
                 if (!((g2 >> d3) & 1u) || ((o2 >> d3) & 1u)) continue;
                 int p3 = step(p2, d3);
@@ -542,13 +550,13 @@ HW_INL bool piece_has_move(const Pos& P, int c, int t) {
         case PT_B: return has_beetle(P, c);
         case PT_L: return has_ladybug(P, c);
         case PT_M: {
-            if (P.h[c] > 1) return has_beetle(P, c);
+            if (P.hgt(c) > 1) return has_beetle(P, c);
             uint32_t om = P.nb[c];
             uint32_t has = 0;
             while (om) {
                 int d = __ffs(om) - 1;
                 om &= om - 1;
-                int tt = P.top[step(c, d)] & 15;
+                int tt = P.tp(step(c, d)) & 15;
                 if (tt != PT_M) has |= 1u << tt;
             }
             if ((has & ((1u << PT_Q) | (1u << PT_P) | (1u << PT_A))) && slide_mask(P, c, c) != 0) return true;
@@ -566,15 +574,15 @@ HW_INL bool piece_has_move(const Pos& P, int c, int t) {
 // (has_pillbug_throw_for_target, move_gen.cuh:742-769)
 HW_INL bool throwable(const Pos& P, int a, int dt) {
     int t = step(a, dt);
-    if (!pb_get(P.occ, t) || P.h[t] != 1) return false;
+    if (!pb_get(P.occ, t) || P.hgt(t) != 1) return false;
     if (P.stun != 0xFFFF && (int)P.stun == t) return false;
     if (pb_get(P.pin, t)) return false;
-    int ph = P.h[a];
+    int ph = P.hgt(a);
     int back = (dt + 3) % 6;
     uint32_t gt = grid6(t);
-    int lift = max(P.h[t] - 1, ph);
-    int cwh = ((gt >> ((back + 5) % 6)) & 1u) ? P.h[step(t, (back + 5) % 6)] : 0;
-    int ccwh = ((gt >> ((back + 1) % 6)) & 1u) ? P.h[step(t, (back + 1) % 6)] : 0;
+    int lift = max(P.hgt(t) - 1, ph);
+    int cwh = ((gt >> ((back + 5) % 6)) & 1u) ? P.hgt(step(t, (back + 5) % 6)) : 0;
+    int ccwh = ((gt >> ((back + 1) % 6)) & 1u) ? P.hgt(step(t, (back + 1) % 6)) : 0;
     if (cwh > lift && ccwh > lift) return false;
     uint32_t ga = grid6(a);
     uint32_t oa = P.nb[a];
@@ -623,19 +631,19 @@ HW_INL uint32_t compact_summary(Pos& P, int lane, int* n_place) {
     uint32_t bucket = 0;
     if (lane < P.n_occ) {
         int c = P.occ_cells[lane];
-        int tb = P.top[c];
+        int tb = P.tp(c);
         int t = tb & 15;
         if (((tb >> 4) & 1) == me) {
             bool stunned = P.stun != 0xFFFF && (int)P.stun == c;
             if (!stunned && !pb_get(P.pin, c) && piece_has_move(P, c, t)) bucket |= 1u << ((t - 1) * 2 + me);
-            bool actor = (t == PT_P) || (t == PT_M && P.h[c] == 1 && touches_top_pillbug(P, c));
+            bool actor = (t == PT_P) || (t == PT_M && P.hgt(c) == 1 && touches_top_pillbug(P, c));
             if (actor) {
                 uint32_t oa = P.nb[c];
                 while (oa) {
                     int dt = __ffs(oa) - 1;
                     oa &= oa - 1;
                     if (throwable(P, c, dt)) {
-                        int tb2 = P.top[step(c, dt)];
+                        int tb2 = P.tp(step(c, dt));
                         bucket |= 1u << (((tb2 & 15) - 1) * 2 + ((tb2 >> 4) & 1));
                     }
                 }
@@ -653,15 +661,15 @@ HW_INL bool queen_escape(const Pos& P, int lane) {
     if (!((P.qplaced >> me) & 1)) return false;
     int q = P.queen[me];
     if (q >= kCells || !pb_get(P.occ, q)) return false;
-    int tq = P.top[q];
+    int tq = P.tp(q);
     bool ok = false;
     if (lane == 0) {
         ok = (tq & 15) == PT_Q && ((tq >> 4) & 1) == me && !pb_get(P.pin, q) && slide_mask(P, q, q) != 0;
     } else if (lane < P.n_occ + 1) {
         int c = P.occ_cells[lane - 1];
-        int tb = P.top[c];
+        int tb = P.tp(c);
         int t = tb & 15;
-        if (((tb >> 4) & 1) == me && ((t == PT_P) || (t == PT_M && P.h[c] == 1 && touches_top_pillbug(P, c)))) {
+        if (((tb >> 4) & 1) == me && ((t == PT_P) || (t == PT_M && P.hgt(c) == 1 && touches_top_pillbug(P, c)))) {
             uint32_t bit = dir_bit_to(c, q, grid6(c));
             if (bit) ok = throwable(P, c, __ffs(bit) - 1);
         }
@@ -692,9 +700,8 @@ HW_INL bool queen_ringed(const Pos& P, int col) {
 HW_INL void apply_on_board(Pos& P, const uint8_t* __restrict__ S, int type, int pt, int from, int to) {
     const int me = P.turn & 1;
     if (type == MV_PLACE) {
-        if (to < kCells && pt >= PT_Q && pt <= PT_P && P.h[to] < 5) {
-            P.top[to] = (uint8_t)(pt | (me << 4));
-            P.h[to] = P.h[to] + 1;
+        if (to < kCells && pt >= PT_Q && pt <= PT_P && P.hgt(to) < 5) {
+            P.set_cell(to, P.hgt(to) + 1, pt | (me << 4));
             pb_set(P.occ, to);
             set_top_colour(P, to, me);
             if (pt == PT_Q) {
@@ -706,21 +713,19 @@ HW_INL void apply_on_board(Pos& P, const uint8_t* __restrict__ S, int type, int 
         P.stun = 0xFFFF;
     } else if (type == MV_MOVE) {
         if (from < kCells && to < kCells) {
-            if (P.h[from] > 0 && P.h[from] <= 5 && P.h[to] < 5) {  // heights above 5 never occur
-                int b = P.top[from];
-                int hf = P.h[from] - 1;
-                P.h[from] = (uint8_t)hf;
+            if (P.hgt(from) > 0 && P.hgt(from) <= 5 && P.hgt(to) < 5) {  // heights above 5 never occur
+                int b = P.tp(from);
+                int hf = P.hgt(from) - 1;
                 if (hf == 0) {
-                    P.top[from] = 0;
+                    P.set_cell(from, 0, 0);
                     pb_clr(P.occ, from); pb_clr(P.wt, from); pb_clr(P.bt, from);
                 } else {
                     int under = S[(hf - 1) * kCells + from];
-                    P.top[from] = (uint8_t)under;
+                    P.set_cell(from, hf, under);
                     set_top_colour(P, from, (under >> 4) & 1);
                 }
-                int ht = P.h[to];
-                P.top[to] = (uint8_t)b;
-                P.h[to] = (uint8_t)(ht + 1);
+                int ht = P.hgt(to);
+                P.set_cell(to, ht + 1, b);
                 pb_set(P.occ, to);
                 set_top_colour(P, to, (b >> 4) & 1);
                 if ((b & 15) == PT_Q) P.queen[(b >> 4) & 1] = (uint16_t)to;
@@ -756,13 +761,15 @@ HW_INL void run_legal(Pos& P, const uint8_t* __restrict__ S, int lane, uint8_t* 
                       int32_t* __restrict__ n_slot, float* __restrict__ feat_row, int32_t* __restrict__ act_row) {
     prepare(P, S, lane);
     ListInfo L = generate_legal(P, lane);
-    if (WithFeat) features_clear(P, lane);
+    if (WithFeat) sources_clear(P, lane);
     int cq = 0, cr = 0;
     if (WithAct) centroid(P, lane, cq, cr);
     __syncthreads();
     emit_list<WithMoves, WithAct, WithFeat>(P, L, lane, moves_row, act_row, cq, cr);
     if (lane == 0) *n_slot = L.n;
     if (WithFeat) {
+        __syncthreads();
+        counters_clear(P, lane);
         __syncthreads();
         int m = L.total > 0 ? min(L.n, L.n_place) : 0;
         features_finish(P, S, feat_row, lane, kFeatGen, 0u, L.ntypes ? (m + L.ntypes - 1) / L.ntypes : 0);
@@ -773,7 +780,8 @@ HW_INL void run_extract(Pos& P, const uint8_t* __restrict__ S, const uint8_t* __
                         int lane, float* __restrict__ feat_row) {
     int n = nl < 0 ? 0 : (nl > kMaxLegal ? kMaxLegal : nl);
     prepare(P, S, lane);
-    features_clear(P, lane);
+    sources_clear(P, lane);
+    counters_clear(P, lane);
     __syncthreads();
     list_sources(P, M, n, lane);
     __syncthreads();
@@ -794,7 +802,8 @@ HW_INL void run_successor(Pos& P, const uint8_t* __restrict__ S, const uint8_t* 
     __syncthreads();
     int n_place = 0;
     uint32_t bucket = compact_summary(P, lane, &n_place);
-    features_clear(P, lane);
+    sources_clear(P, lane);
+    counters_clear(P, lane);
     __syncthreads();
     // stacked levels under a top piece are read from the root row: a single
     // move leaves every level under a top unchanged

@@ -35,9 +35,19 @@ constexpr int kMaxLegal = 256;
 constexpr int kFeat = 122;
 constexpr int kPW = 20;  // padded words per bitboard
 constexpr int kMaxPieces = 16;
-constexpr int kPool = 840;  // destination pool entries (3 ants + mosquito at 168, rest small)
+// Destination pool entries for one side's pieces at type_capacity() each:
+// 3 ants x 64 + mosquito 128 + 2 spiders x 32 + ladybug 32 + 8 others x 6.
+// Capacities are bounds for states built by init/apply: a connected hive of
+// n cells has at most 2n + 4 empty neighbour cells (each cell added next to
+// the hive removes one and adds at most three), every ant destination is
+// one of them with n <= 27 (the ant lifted), so an ant has < 64; a
+// mosquito's union adds at most its 6 neighbours.
+constexpr int kPool = 464;
 constexpr int kActors = 2;  // throw actors of one colour: its pillbug and its mosquito
-constexpr int kThrowCap = 36;
+// throws of one actor: targets are occupied and drops empty neighbours of
+// the actor, so targets x drops <= 3 x 3
+constexpr int kThrowCap = 12;
+constexpr int kSets = 8;  // visited / dedup sets: 3 ants, 2 spiders, 1 ladybug, 1 mosquito (2)
 constexpr int kSegs = 1 + kMaxPieces + kActors + 1;  // placements, pieces, actors, end
 
 // state byte offsets (hive_gpu/csrc/hive_state.cuh:239-269)
@@ -119,8 +129,7 @@ __device__ __forceinline__ int hexdist(int a, int b) {  // fnn_features.cuh:44-6
 
 struct alignas(16) Pos {
     uint32_t occ[kPW], wt[kPW], bt[kPW], ap[kPW], pin[kPW], plc[kPW];
-    uint8_t h[544];
-    uint8_t top[544];
+    uint8_t cell[544];  // top piece byte (type | colour << 4) in bits 0-4, stack height in bits 5-7
     uint8_t nb[544];  // occupied on-grid neighbours of each cell (direction mask)
     uint8_t sm[544];  // ground-slide exits of each cell with nothing lifted
     uint16_t occ_pre[20];  // occupied cells in board words before word w
@@ -139,14 +148,23 @@ struct alignas(16) Pos {
     uint8_t piece_type[kMaxPieces];
     uint16_t piece_off[kMaxPieces];
     uint16_t piece_cnt[kMaxPieces];
+    uint8_t piece_set[kMaxPieces];  // first visited set of a piece that needs sets
     uint16_t actor_cell[kActors];
     uint16_t throw_cnt[kActors];
     uint16_t throw_from[kActors][kThrowCap];
     uint16_t throw_to[kActors][kThrowCap];
     uint8_t throw_pt[kActors][kThrowCap];
-    uint16_t pool[kPool];
+    // generation: visited sets; emission and features: the list's source sets
     union {
-        uint32_t lane_bb[kMaxPieces][2][18];  // lane-private visited / dedup sets
+        uint32_t sets[kSets][18];
+        struct {
+            uint32_t from_bb[16][18];  // MOVE sources per (type, owner)
+            uint32_t place_bb[18];     // PLACE destinations
+        } s;
+    } u1;
+    // generation and emission: destinations; features (after emission): counters
+    union {
+        uint16_t pool[kPool];
         struct {
             int cnt[128];
             int dsum[16], dcnt[16];
@@ -154,10 +172,13 @@ struct alignas(16) Pos {
             int n_cap;
             uint16_t cap_cells[8];
             uint8_t cap_col[8];
-            uint32_t from_bb[16][18];
-            uint32_t place_bb[18];
-        } f;
-    } u;
+        } c;
+    } u2;
+    __device__ __forceinline__ int hgt(int c) const { return cell[c] >> 5; }
+    __device__ __forceinline__ int tp(int c) const { return cell[c] & 31; }
+    __device__ __forceinline__ void set_cell(int c, int h, int top) {
+        cell[c] = (uint8_t)((h << 5) | (h ? (top & 31) : 0));
+    }
 };
 
 // ---------------------------------------------------------------- wave utils
@@ -202,8 +223,7 @@ HW_INL void load_position(Pos& P, const uint8_t* __restrict__ S, int lane) {
             int hh = (int)hv[k];
             int t = (int)tv[k];
             if (hh > 1) t = S[((hh > 5 ? 5 : hh) - 1) * kCells + i];
-            P.h[i] = (uint8_t)hh;
-            P.top[i] = hh ? (uint8_t)t : 0;
+            P.set_cell(i, hh > 7 ? 7 : hh, t);
         }
     }
     const uint32_t* W = reinterpret_cast<const uint32_t*>(S + OFF_OCC);  // 8-byte aligned
@@ -343,7 +363,7 @@ HW_INL void articulation(Pos& P, int lane) {
     if (is_ap) {
         int c = P.occ_cells[v];
         atomicOr(&P.ap[(c >> 5) + 1], 1u << (c & 31));
-        if (P.h[c] == 1) atomicOr(&P.pin[(c >> 5) + 1], 1u << (c & 31));
+        if (P.hgt(c) == 1) atomicOr(&P.pin[(c >> 5) + 1], 1u << (c & 31));
     }
 }
 
@@ -367,7 +387,7 @@ __device__ __forceinline__ uint32_t nbr_heights(const Pos& P, int c, uint32_t gm
     uint32_t r = 0;
 #pragma unroll
     for (int d = 0; d < 6; d++)
-        if ((gm >> d) & 1u) r |= (uint32_t)(P.h[step(c, d)] & 15) << (4 * d);
+        if ((gm >> d) & 1u) r |= (uint32_t)(P.hgt(step(c, d)) & 15) << (4 * d);
     return r;
 }
 __device__ __forceinline__ int hof(uint32_t nh, int d) { return (int)((nh >> (4 * d)) & 15u); }
@@ -484,7 +504,7 @@ HW_INL int gen_beetle(const Pos& P, int c, uint16_t* out) {
     uint32_t gm = grid6(c);
     uint32_t nh = nbr_heights(P, c, gm);
     uint32_t sm = slide_mask(P, c, c);
-    int below = P.h[c] - 1;
+    int below = P.hgt(c) - 1;
     int n = 0;
     for (int d = 0; d < 6; d++) {
         if (!((gm >> d) & 1u)) continue;
@@ -504,14 +524,14 @@ HW_INL int gen_ladybug(const Pos& P, int c, uint16_t* out, uint32_t* got) {
     uint32_t g0 = grid6(c);
     uint32_t nh0 = nbr_heights(P, c, g0);
     uint32_t o0 = P.nb[c];
-    int hc = P.h[c];
+    int hc = P.hgt(c);
     for (int d1 = 0; d1 < 6; d1++) {
         if (!((o0 >> d1) & 1u)) continue;
         int p1 = step(c, d1);
         if (gate_high(nh0, d1, max(hc - 1, hof(nh0, d1)))) continue;
         uint32_t nh1 = nbr_heights(P, p1, grid6(p1));
         uint32_t o1 = P.nb[p1];
-        int hp1 = P.h[p1];
+        int hp1 = P.hgt(p1);
         for (int d2 = 0; d2 < 6; d2++) {
             if (!((o1 >> d2) & 1u)) continue;
             int p2 = step(p1, d2);
@@ -520,7 +540,7 @@ HW_INL int gen_ladybug(const Pos& P, int c, uint16_t* out, uint32_t* got) {
             uint32_t g2 = grid6(p2);
             uint32_t nh2 = nbr_heights(P, p2, g2);
             uint32_t o2 = P.nb[p2];
-            int mh3 = P.h[p2];
+            int mh3 = P.hgt(p2);
             for (int d3 = 0; d3 < 6; d3++) {
                 if (!((g2 >> d3) & 1u) || ((o2 >> d3) & 1u)) continue;
                 int p3 = step(p2, d3);
@@ -539,13 +559,13 @@ HW_INL int gen_ladybug(const Pos& P, int c, uint16_t* out, uint32_t* got) {
 // into the free tail of out[] and merged in place (merge write index never
 // passes the read index).  Needs 6 + 128 slots of room.
 HW_INL int gen_mosquito(const Pos& P, int c, uint16_t* out, uint32_t* tmpset, uint32_t* unionset) {
-    if (P.h[c] > 1) return gen_beetle(P, c, out);
+    if (P.hgt(c) > 1) return gen_beetle(P, c, out);
     uint32_t gm = grid6(c);
     uint32_t om = P.nb[c];
     uint32_t has = 0;
     for (int d = 0; d < 6; d++)
         if ((om >> d) & 1u) {
-            int t = P.top[step(c, d)] & 15;
+            int t = P.tp(step(c, d)) & 15;
             if (t != PT_M) has |= 1u << t;
         }
     (void)gm;
@@ -556,7 +576,7 @@ HW_INL int gen_mosquito(const Pos& P, int c, uint16_t* out, uint32_t* tmpset, ui
         int m = 0;
         switch (k) {
             case 0: if (has & ((1u << PT_Q) | (1u << PT_P))) m = gen_step(P, c, tail); break;
-            case 1: if (has & (1u << PT_A)) m = gen_ant(P, c, tail, 128, tmpset); break;
+            case 1: if (has & (1u << PT_A)) m = gen_ant(P, c, tail, 128 - n, tmpset); break;
             case 2: if (has & (1u << PT_G)) m = gen_hopper(P, c, tail); break;
             case 3: if (has & (1u << PT_S)) m = gen_spider(P, c, tail, tmpset); break;
             case 4: if (has & (1u << PT_B)) m = gen_beetle(P, c, tail); break;
@@ -578,24 +598,24 @@ HW_INL int gen_throws(const Pos& P, int a, uint16_t* from, uint16_t* to, uint8_t
     int n = 0;
     uint32_t ga = grid6(a);
     uint32_t nha = nbr_heights(P, a, ga);
-    int ph = P.h[a];
+    int ph = P.hgt(a);
     uint32_t oa = P.nb[a];
     for (int dt = 0; dt < 6; dt++) {
         if (!((oa >> dt) & 1u)) continue;
         int t = step(a, dt);
-        if (P.h[t] != 1) continue;
+        if (P.hgt(t) != 1) continue;
         if (P.stun != 0xFFFF && (int)P.stun == t) continue;
         if (pb_get(P.pin, t)) continue;
         int back = (dt + 3) % 6;  // direction from the target to the actor
         uint32_t gt = grid6(t);
-        int lift = max(P.h[t] - 1, ph);
-        int cwh = ((gt >> ((back + 5) % 6)) & 1u) ? P.h[step(t, (back + 5) % 6)] : 0;
-        int ccwh = ((gt >> ((back + 1) % 6)) & 1u) ? P.h[step(t, (back + 1) % 6)] : 0;
+        int lift = max(P.hgt(t) - 1, ph);
+        int cwh = ((gt >> ((back + 5) % 6)) & 1u) ? P.hgt(step(t, (back + 5) % 6)) : 0;
+        int ccwh = ((gt >> ((back + 1) % 6)) & 1u) ? P.hgt(step(t, (back + 1) % 6)) : 0;
         if (cwh > lift && ccwh > lift) continue;
-        int tp = P.top[t] & 15;
+        int tp = P.tp(t) & 15;
         for (int dd = 0; dd < 6; dd++) {
             if (!((ga >> dd) & 1u) || dd == dt || ((oa >> dd) & 1u)) continue;
-            if (gate_high(nha, dd, ph)) continue;
+            if (gate_high(nha, dd, ph) || n >= kThrowCap) continue;
             from[n] = (uint16_t)t;
             to[n] = (uint16_t)step(a, dd);
             pt[n] = (uint8_t)tp;
@@ -610,13 +630,16 @@ __device__ __forceinline__ bool touches_top_pillbug(const Pos& P, int c) {
     while (m) {
         int d = __ffs(m) - 1;
         m &= m - 1;
-        if ((P.top[step(c, d)] & 15) == PT_P) return true;
+        if ((P.tp(step(c, d)) & 15) == PT_P) return true;
     }
     return false;
 }
 
 __device__ __forceinline__ int type_capacity(int t) {
-    return (t == PT_A || t == PT_M) ? 168 : (t == PT_S || t == PT_L) ? 32 : 6;
+    return t == PT_A ? 64 : t == PT_M ? 128 : (t == PT_S || t == PT_L) ? 32 : 6;
+}
+__device__ __forceinline__ int type_sets(int t) {
+    return t == PT_M ? 2 : (t == PT_A || t == PT_S || t == PT_L) ? 1 : 0;
 }
 
 // ---------------------------------------------------------------- placement
