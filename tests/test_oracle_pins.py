@@ -247,3 +247,44 @@ def test_pillbug_throws_enemy_and_mosquito_copies(oracle):
     hb.set_turn(m, 4)
     moves, n = oracle.legal_moves(m)
     assert len(hb.dests_of(moves, n, hb.cell(-1, 0))) > 2
+
+
+def test_site_perimeter_bound():
+    """A connected n-cell hive has at most 2n + 4 empty neighbour cells.
+
+    The engine sizes its per-piece destination buffers with this bound (an
+    ant's destinations are such cells of the hive without the ant)."""
+    rng = random.Random(7)
+    worst = {}
+    for _ in range(3000):
+        n = rng.randint(1, 27)
+        cells = set(_random_hive(rng, n))
+        per = {(q + dq, r + dr) for q, r in cells for dq, dr in hb.DIRS} - cells
+        assert len(per) <= 2 * n + 4
+        worst[n] = max(worst.get(n, 0), len(per))
+    # a straight line reaches the bound
+    line = {(i, 0) for i in range(10)}
+    assert len({(q + dq, r + dr) for q, r in line for dq, dr in hb.DIRS} - line) == 24
+
+
+def test_destination_counts_within_buffers(oracle):
+    """Legal lists of seeded random-play positions: per-piece destination
+    counts stay inside the engine's buffers (ant < 64, mosquito <= 128,
+    spider / ladybug <= 32).  A piece's own moves are one contiguous run of
+    MOVE entries with its cell as source (throws come after all pieces)."""
+    worst = {}
+    for mask, max_ply in ((0, 120), (7, 150)):
+        st, _ = oracle.generate_positions(4096, mask, max_ply, 0xB0B)
+        moves, n, _, _ = oracle.batch_legal_features_actions(st, want_features=False, want_actions=False)
+        for i in range(st.shape[0]):
+            m = moves[i, :n[i]]
+            key = [(int(r[1]), int(r[2]) | (int(r[3]) << 8)) if r[0] == 1 else None for r in m]
+            run, seen = 0, set()
+            for j, k in enumerate(key):
+                run = run + 1 if j > 0 and k is not None and k == key[j - 1] else 1
+                if k is not None and (j + 1 == len(key) or key[j + 1] != k) and k not in seen:
+                    seen.add(k)
+                    worst[k[0]] = max(worst.get(k[0], 0), run)
+    assert worst.get(2, 0) < 64 and worst.get(6, 0) <= 128
+    assert worst.get(4, 0) <= 32 and worst.get(7, 0) <= 32
+    assert worst.get(2, 0) > 20  # the sample does exercise long ant searches
