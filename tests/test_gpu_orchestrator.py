@@ -163,3 +163,60 @@ def test_self_play_batch_examples():
             assert e.state_bytes.shape == (3424,) and e.state_bytes.dtype == np.uint8
             assert abs(float(e.policy_target.sum()) - 1.0) < 1e-5
             assert e.value_target in (-1.0, 0.0, 1.0)
+
+
+@pytest.mark.parametrize("sims,mask,max_ply,seed,kw", [
+    (64, 7, 40, 21, {}),
+    (48, 0, 80, 22, {}),
+    (32, 7, 60, 23, {"wave_parallel": False}),
+], ids=["mask7", "mask0-late", "w1"])
+def test_search_ply_matches_numpy_orchestrator(monkeypatch, sims, mask, max_ply, seed, kw):
+    """The torch orchestrator's host logic against oracle/orchestrator.py (numpy),
+    fed the same recorded network outputs, Gumbel draws and Dirichlet noise.
+
+    The seeded cases cover queen-surround reserve slots (6-8 games per case),
+    a finished game (mask0-late), and an immediate win, which also clears
+    every other game's priors (w1)."""
+    import torch
+    from oracle.orchestrator import SearchPlyOracle
+    B = 12
+    orch, states, tree = _setup(B, sims, 1 << 15, mask, max_ply, seed, **kw)
+    evals, uniforms, noises = [], [], []
+    real_eval = orch._eval_states
+
+    def rec_eval(*a, **k):
+        out = real_eval(*a, **k)
+        evals.append(tuple(_np(x).copy() for x in out))
+        return out
+
+    real_rand = torch.rand
+
+    def rec_rand(*a, **k):
+        out = real_rand(*a, **k)
+        uniforms.append(_np(out).copy())
+        return out
+
+    ext = orch.ext
+    real_noise = ext.mcts_apply_root_noise
+
+    def rec_noise(*a):
+        noises.append(_np(a[12]).copy())
+        return real_noise(*a)
+
+    monkeypatch.setattr(orch, "_eval_states", rec_eval)
+    monkeypatch.setattr(torch, "rand", rec_rand)
+    monkeypatch.setattr(ext, "mcts_apply_root_noise", rec_noise, raising=False)
+    t0 = {k: _np(v).copy() for k, v in tree.items()}
+    st = _np(states).copy()
+    active = torch.ones((B,), dtype=torch.bool, device="cuda")
+    r = orch.search_ply(states, tree, active)
+    assert len(uniforms) == 1 and len(noises) == 1 and len(evals) >= 2
+
+    ref = SearchPlyOracle(orch.config)
+    legal, n, _, _ = ref.o.batch_legal_features_actions(st, want_features=False, want_actions=False)
+    assert np.array_equal(legal, _np(r.legal_moves)) and np.array_equal(n, _np(r.num_legal))
+    chosen, probs, visits = ref.run(t0, st, np.ones(B, bool), legal, n, evals[0], uniforms[0], noises[0], evals[1:])
+    assert np.array_equal(chosen, _np(r.chosen_slot))
+    assert np.array_equal(visits, _np(r.slot_visits))
+    np.testing.assert_allclose(probs, _np(r.policy), atol=2e-6, rtol=0)
+    assert tree_equal(t0, {k: _np(v) for k, v in tree.items()}) == []
