@@ -50,42 +50,55 @@ __global__ void k_check_results(const uint8_t* __restrict__ states, int64_t B, i
 }
 
 // ---------------------------------------------------------------- positions
+// Two positions per 64-lane workgroup (lane groups of kW = 32).  A group
+// whose item index is past the end works on the last item and writes
+// nothing, so that both groups reach every barrier.
+__device__ __forceinline__ int64_t item_of(int64_t n, bool& live) {
+    const int64_t i = (int64_t)blockIdx.x * kPosPerWave + (threadIdx.x >> 5);
+    live = i < n;
+    return live ? i : n - 1;
+}
+
 template <bool WithMoves, bool WithFeat, bool WithAct>
 __global__ __launch_bounds__(64) void k_legal(const uint8_t* __restrict__ states, int64_t B,
                                               uint8_t* __restrict__ moves_out, int32_t* __restrict__ n_out,
                                               float* __restrict__ feat_out, int32_t* __restrict__ act_out) {
-    __shared__ Pos P;
-    const int64_t pos = blockIdx.x;
-    if (pos >= B) return;
-    run_legal<WithMoves, WithFeat, WithAct>(P, states + pos * kStateBytes, threadIdx.x,
-                                   WithMoves ? moves_out + pos * (kMaxLegal * 6) : nullptr, n_out + pos,
-                                   WithFeat ? feat_out + pos * kFeat : nullptr, WithAct ? act_out + pos * kMaxLegal : nullptr);
+    __shared__ Pos PS[kPosPerWave];
+    bool live;
+    const int64_t pos = item_of(B, live);
+    run_legal<WithMoves, WithFeat, WithAct>(PS[threadIdx.x >> 5], states + pos * kStateBytes, threadIdx.x,
+                                            live ? moves_out + pos * (kMaxLegal * 6) : nullptr,
+                                            live ? n_out + pos : nullptr,
+                                            WithFeat && live ? feat_out + pos * kFeat : nullptr,
+                                            WithAct && live ? act_out + pos * kMaxLegal : nullptr);
 }
 
 __global__ __launch_bounds__(64) void k_extract_features(const uint8_t* __restrict__ states,
                                                          const uint8_t* __restrict__ moves,
                                                          const int32_t* __restrict__ num_legal, int64_t B,
                                                          float* __restrict__ feat_out) {
-    __shared__ Pos P;
-    const int64_t pos = blockIdx.x;
-    if (pos >= B) return;
-    run_extract(P, states + pos * kStateBytes, moves + pos * (kMaxLegal * 6), num_legal[pos], threadIdx.x,
-                feat_out + pos * kFeat);
+    __shared__ Pos PS[kPosPerWave];
+    bool live;
+    const int64_t pos = item_of(B, live);
+    run_extract(PS[threadIdx.x >> 5], states + pos * kStateBytes, moves + pos * (kMaxLegal * 6), num_legal[pos],
+                threadIdx.x, live ? feat_out + pos * kFeat : nullptr);
 }
 
 // legal_moves_to_actions_kernel (game_logic.cu:811-835) / compute_centroids_kernel
-// (state_encoder.cuh:982-996): one wave per position, centroid over the occupied cells.
+// (state_encoder.cuh:982-996): centroid over the occupied cells, one lane per list slot.
 __global__ __launch_bounds__(64) void k_actions(const uint8_t* __restrict__ states,
                                                 const uint8_t* __restrict__ moves,
                                                 const int32_t* __restrict__ num_legal, int64_t B,
                                                 int32_t* __restrict__ act_out, int32_t* __restrict__ centroid_out) {
-    __shared__ Pos P;
+    __shared__ Pos PS[kPosPerWave];
     const int lane = threadIdx.x;
-    const int64_t pos = blockIdx.x;
-    if (pos >= B) return;
+    const int l = gl(lane);
+    bool live;
+    const int64_t pos = item_of(B, live);
+    Pos& P = PS[lane >> 5];
     const uint8_t* S = states + pos * kStateBytes;
     const uint32_t* W = reinterpret_cast<const uint32_t*>(S + OFF_OCC);
-    if (lane < 18) P.occ[lane + 1] = W[lane];
+    if (l < 18) P.occ[l + 1] = W[l];
     int n = 0;
     if (act_out) {
         n = num_legal[pos];
@@ -96,39 +109,44 @@ __global__ __launch_bounds__(64) void k_actions(const uint8_t* __restrict__ stat
     __syncthreads();
     int cq, cr;
     centroid(P, lane, cq, cr);
-    if (centroid_out && lane == 0) {
+    if (centroid_out && live && l == 0) {
         centroid_out[2 * pos] = cq;
         centroid_out[2 * pos + 1] = cr;
     }
-    if (act_out) list_actions(moves + pos * (kMaxLegal * 6), n, cq, cr, act_out + pos * kMaxLegal, lane);
+    if (act_out && live) list_actions(moves + pos * (kMaxLegal * 6), n, cq, cr, act_out + pos * kMaxLegal, lane);
 }
 
-// fnn_successor_features_kernel (game_logic.cu:182-229): one wave per (root, move).
+// a zero state and move for rows that reference no valid (root, move)
+__device__ const uint8_t kZeroRow[kStateBytes] = {};
+
+// fnn_successor_features_kernel (game_logic.cu:182-229): one lane group per (root, move).
 __global__ __launch_bounds__(64) void k_successor_features(const uint8_t* __restrict__ states,
                                                            const uint8_t* __restrict__ legal,
                                                            const int64_t* __restrict__ a2r,
                                                            const int64_t* __restrict__ midx, int64_t N,
                                                            int64_t num_roots, float* __restrict__ feat_out) {
-    __shared__ Pos P;
+    __shared__ Pos PS[kPosPerWave];
     const int lane = threadIdx.x;
-    const int64_t i = blockIdx.x;
-    if (i >= N) return;
+    bool live;
+    const int64_t i = item_of(N, live);
     const int64_t root = a2r[i];
     const int64_t mi = midx[i];
-    if (root < 0 || root >= num_roots || mi < 0 || mi >= kMaxLegal) {  // out-of-range rows: zero features
-        for (int k = lane; k < kFeat; k += 64) feat_out[i * kFeat + k] = 0.0f;
-        return;
-    }
-    run_successor(P, states + root * kStateBytes, legal + (root * kMaxLegal + mi) * 6, lane, feat_out + i * kFeat);
+    const bool valid = root >= 0 && root < num_roots && mi >= 0 && mi < kMaxLegal;
+    const uint8_t* S = valid ? states + root * kStateBytes : kZeroRow;
+    const uint8_t* m = valid ? legal + (root * kMaxLegal + mi) * 6 : kZeroRow;
+    float* out = live ? feat_out + i * kFeat : nullptr;
+    run_successor(PS[lane >> 5], S, m, lane, valid ? out : nullptr);
+    if (live && !valid)  // out-of-range rows: zero features
+        for (int k = gl(lane); k < kFeat; k += kW) out[k] = 0.0f;
 }
 
 __global__ __launch_bounds__(64) void k_queen_escape(const uint8_t* __restrict__ states, int64_t B,
                                                      uint8_t* __restrict__ out) {
-    __shared__ Pos P;
-    const int64_t pos = blockIdx.x;
-    if (pos >= B) return;
-    bool esc = run_queen_escape(P, states + pos * kStateBytes, threadIdx.x);
-    if (threadIdx.x == 0) out[pos] = esc ? 1 : 0;
+    __shared__ Pos PS[kPosPerWave];
+    bool live;
+    const int64_t pos = item_of(B, live);
+    bool esc = run_queen_escape(PS[threadIdx.x >> 5], states + pos * kStateBytes, threadIdx.x);
+    if (live && gl(threadIdx.x) == 0) out[pos] = esc ? 1 : 0;
 }
 
 // Philox4x32-10 (Salmon et al., SC'11), first output word.
@@ -203,7 +221,7 @@ int hg_check_results(const uint8_t* states, int64_t B, int32_t* results, void* s
 
 int hg_generate_legal_moves(const uint8_t* states, int64_t B, uint8_t* moves, int32_t* num_legal, void* stream) {
     if (B <= 0) return 0;
-    hipLaunchKernelGGL((k_legal<true, false, false>), dim3((unsigned)B), dim3(64), 0, (hipStream_t)stream, states, B,
+    hipLaunchKernelGGL((k_legal<true, false, false>), dim3((unsigned)grid_for(B, kPosPerWave)), dim3(64), 0, (hipStream_t)stream, states, B,
                        moves, num_legal, nullptr, nullptr);
     return finish();
 }
@@ -211,7 +229,7 @@ int hg_generate_legal_moves(const uint8_t* states, int64_t B, uint8_t* moves, in
 int hg_generate_legal_moves_and_fnn_features(const uint8_t* states, int64_t B, uint8_t* moves,
                                              int32_t* num_legal, float* features, void* stream) {
     if (B <= 0) return 0;
-    hipLaunchKernelGGL((k_legal<true, true, false>), dim3((unsigned)B), dim3(64), 0, (hipStream_t)stream, states, B,
+    hipLaunchKernelGGL((k_legal<true, true, false>), dim3((unsigned)grid_for(B, kPosPerWave)), dim3(64), 0, (hipStream_t)stream, states, B,
                        moves, num_legal, features, nullptr);
     return finish();
 }
@@ -219,7 +237,7 @@ int hg_generate_legal_moves_and_fnn_features(const uint8_t* states, int64_t B, u
 int hg_legal_features_actions(const uint8_t* states, int64_t B, uint8_t* moves, int32_t* num_legal,
                               float* features, int32_t* actions, void* stream) {
     if (B <= 0) return 0;
-    hipLaunchKernelGGL((k_legal<true, true, true>), dim3((unsigned)B), dim3(64), 0, (hipStream_t)stream, states, B,
+    hipLaunchKernelGGL((k_legal<true, true, true>), dim3((unsigned)grid_for(B, kPosPerWave)), dim3(64), 0, (hipStream_t)stream, states, B,
                        moves, num_legal, features, actions);
     return finish();
 }
@@ -227,7 +245,7 @@ int hg_legal_features_actions(const uint8_t* states, int64_t B, uint8_t* moves, 
 int hg_extract_fnn_features(const uint8_t* states, const uint8_t* moves, const int32_t* num_legal, int64_t B,
                             float* features, void* stream) {
     if (B <= 0) return 0;
-    hipLaunchKernelGGL(k_extract_features, dim3((unsigned)B), dim3(64), 0, (hipStream_t)stream, states, moves,
+    hipLaunchKernelGGL(k_extract_features, dim3((unsigned)grid_for(B, kPosPerWave)), dim3(64), 0, (hipStream_t)stream, states, moves,
                        num_legal, B, features);
     return finish();
 }
@@ -235,14 +253,14 @@ int hg_extract_fnn_features(const uint8_t* states, const uint8_t* moves, const i
 int hg_legal_moves_to_actions(const uint8_t* states, const uint8_t* moves, const int32_t* num_legal, int64_t B,
                               int32_t* actions, void* stream) {
     if (B <= 0) return 0;
-    hipLaunchKernelGGL(k_actions, dim3((unsigned)B), dim3(64), 0, (hipStream_t)stream, states, moves, num_legal, B,
+    hipLaunchKernelGGL(k_actions, dim3((unsigned)grid_for(B, kPosPerWave)), dim3(64), 0, (hipStream_t)stream, states, moves, num_legal, B,
                        actions, (int32_t*)nullptr);
     return finish();
 }
 
 int hg_compute_centroids(const uint8_t* states, int64_t B, int32_t* centroids, void* stream) {
     if (B <= 0) return 0;
-    hipLaunchKernelGGL(k_actions, dim3((unsigned)B), dim3(64), 0, (hipStream_t)stream, states,
+    hipLaunchKernelGGL(k_actions, dim3((unsigned)grid_for(B, kPosPerWave)), dim3(64), 0, (hipStream_t)stream, states,
                        (const uint8_t*)nullptr, (const int32_t*)nullptr, B, (int32_t*)nullptr, centroids);
     return finish();
 }
@@ -251,14 +269,14 @@ int hg_fnn_successor_features(const uint8_t* states, const uint8_t* legal_moves,
                               const int64_t* action_to_root, const int64_t* move_indices, int64_t N, float* features,
                               void* stream) {
     if (N <= 0) return 0;
-    hipLaunchKernelGGL(k_successor_features, dim3((unsigned)N), dim3(64), 0, (hipStream_t)stream, states,
+    hipLaunchKernelGGL(k_successor_features, dim3((unsigned)grid_for(N, kPosPerWave)), dim3(64), 0, (hipStream_t)stream, states,
                        legal_moves, action_to_root, move_indices, N, num_roots, features);
     return finish();
 }
 
 int hg_queen_escape_flags(const uint8_t* states, int64_t B, uint8_t* flags, void* stream) {
     if (B <= 0) return 0;
-    hipLaunchKernelGGL(k_queen_escape, dim3((unsigned)B), dim3(64), 0, (hipStream_t)stream, states, B, flags);
+    hipLaunchKernelGGL(k_queen_escape, dim3((unsigned)grid_for(B, kPosPerWave)), dim3(64), 0, (hipStream_t)stream, states, B, flags);
     return finish();
 }
 

@@ -32,8 +32,9 @@ struct ListInfo {
 };
 
 HW_INL ListInfo generate_legal(Pos& P, int lane) {
+    const int l = gl(lane);
     ListInfo L{0, 0, 0, 0, 0, 0, 0, 0u};
-    if (P.result != 0) return L;
+    const bool go = P.result == 0;  // barriers below are reached by both positions of the wave
     const int me = P.turn & 1;
     const int ptn = P.turn >> 1;
     const bool queen_down = (P.qplaced >> me) & 1;
@@ -41,47 +42,47 @@ HW_INL ListInfo generate_legal(Pos& P, int lane) {
     uint32_t placeable = 0;
     for (int p = 0; p < 8; p++) {
         bool ok = queen_now ? (p == 0 && P.hand[me][0] > 0) : (P.hand[me][p] > 0);
-        if (ok) placeable |= 1u << p;
+        if (ok && go) placeable |= 1u << p;
     }
     uint32_t emit_types = placeable & ~(ptn == 0 ? 1u : 0u);
     int ntypes = __popc(emit_types);
 
     // -- placement cells, lane w < 18 owns board word w
     uint32_t pw = 0;
-    if (placeable && lane < 18) {
+    if (placeable && l < 18) {
         if (P.turn == 0) {
-            pw = (lane == (264 >> 5)) ? (1u << (264 & 31)) : 0u;
+            pw = (l == (264 >> 5)) ? (1u << (264 & 31)) : 0u;
         } else if (P.turn == 1) {
-            pw = nbr_union_word(P.occ, lane) & ~P.occ[lane + 1];
+            pw = nbr_union_word(P.occ, l) & ~P.occ[l + 1];
         } else {
             const uint32_t* mine = me ? P.bt : P.wt;
             const uint32_t* theirs = me ? P.wt : P.bt;
-            pw = nbr_union_word(mine, lane) & ~nbr_union_word(theirs, lane) & ~P.occ[lane + 1];
+            pw = nbr_union_word(mine, l) & ~nbr_union_word(theirs, l) & ~P.occ[l + 1];
         }
     }
-    int prank = wave_excl_scan(__popc(pw), lane);
-    int npos = wave_sum(__popc(pw));
-    if (lane < 18) {
-        P.plc[lane + 1] = pw;
-        P.plc_pre[lane] = (uint16_t)prank;
+    int prank = grp_excl_scan(__popc(pw));
+    int npos = grp_sum(__popc(pw), lane);
+    if (l < 18) {
+        P.plc[l + 1] = pw;
+        P.plc_pre[l] = (uint16_t)prank;
     }
     int n_place = npos * ntypes;
 
     // -- movable pieces: own top cells, not stunned, not pinned (cell order)
     int n_pieces = 0, n_actors = 0;
-    if (queen_down) {
+    if (go && queen_down) {
         uint32_t mw = 0;
-        if (lane < 18) {
+        if (l < 18) {
             const uint32_t* mine = me ? P.bt : P.wt;
-            mw = mine[lane + 1] & ~P.pin[lane + 1];
-            if (P.stun != 0xFFFF && (P.stun >> 5) == lane) mw &= ~(1u << (P.stun & 31));
+            mw = mine[l + 1] & ~P.pin[l + 1];
+            if (P.stun != 0xFFFF && (P.stun >> 5) == l) mw &= ~(1u << (P.stun & 31));
         }
-        int k = wave_excl_scan(__popc(mw), lane);
-        n_pieces = min(wave_sum(__popc(mw)), kMaxPieces);
+        int k = grp_excl_scan(__popc(mw));
+        n_pieces = min(grp_sum(__popc(mw), lane), kMaxPieces);
         while (mw && k < kMaxPieces) {
             int b = __ffs(mw) - 1;
             mw &= mw - 1;
-            int c = lane * 32 + b;
+            int c = l * 32 + b;
             P.piece_cell[k] = (uint16_t)c;
             P.piece_type[k] = P.tp(c) & 15;
             k++;
@@ -89,33 +90,34 @@ HW_INL ListInfo generate_legal(Pos& P, int lane) {
         // throw actors among occupied cells (cell order); the thrower is not
         // checked for stun or pin (move_gen.cuh:1304-1345)
         bool actor = false;
-        if (lane < P.n_occ) {
-            int c = P.occ_cells[lane];
+        if (l < P.n_occ) {
+            int c = P.occ_cells[l];
             int tb = P.tp(c);
             int t = tb & 15;
             if (((tb >> 4) & 1) == me)
                 actor = (t == PT_P) || (t == PT_M && P.hgt(c) == 1 && touches_top_pillbug(P, c));
         }
-        uint64_t am = __ballot(actor);
-        n_actors = min(__popcll(am), kActors);
+        uint32_t am = grp_ballot(actor, lane);
+        n_actors = min(__popc(am), kActors);
         if (actor) {
-            int r = __popcll(am & ((1ull << lane) - 1));
-            if (r < kActors) P.actor_cell[r] = P.occ_cells[lane];
+            int r = __popc(am & ((1u << l) - 1u));
+            if (r < kActors) P.actor_cell[r] = P.occ_cells[l];
         }
     }
     __syncthreads();
 
-    // -- destination pool offsets by type capacity, visited sets by need
-    int cap = lane < n_pieces ? type_capacity(P.piece_type[lane]) : 0;
-    int off = wave_excl_scan(cap, lane);
-    int nsets = lane < n_pieces ? type_sets(P.piece_type[lane]) : 0;
-    int set0 = wave_excl_scan(nsets, lane);
-    if (lane < n_pieces && (off + cap > kPool || set0 + nsets > kSets)) {  // impossible piece counts
-        P.piece_off[lane] = 0;
-        P.piece_cnt[lane] = 0;
-    } else if (lane < n_pieces) {
-        int c = P.piece_cell[lane];
-        int t = P.piece_type[lane];
+    // -- destination pool offsets by type capacity, visited sets by need;
+    // lanes 0..15 run the pieces, lanes 16, 17 the throw actors
+    int cap = l < n_pieces ? type_capacity(P.piece_type[l]) : 0;
+    int off = grp_excl_scan(cap);
+    int nsets = l < n_pieces ? type_sets(P.piece_type[l]) : 0;
+    int set0 = grp_excl_scan(nsets);
+    if (l < n_pieces && (off + cap > kPool || set0 + nsets > kSets)) {  // impossible piece counts
+        P.piece_off[l] = 0;
+        P.piece_cnt[l] = 0;
+    } else if (l < n_pieces) {
+        int c = P.piece_cell[l];
+        int t = P.piece_type[l];
         uint16_t* out = P.u2.pool + off;
         uint32_t* s0 = P.u1.sets[set0 < kSets ? set0 : 0];
         uint32_t* s1 = P.u1.sets[set0 + 1 < kSets ? set0 + 1 : 0];
@@ -130,24 +132,25 @@ HW_INL ListInfo generate_legal(Pos& P, int lane) {
             case PT_L: m = gen_ladybug(P, c, out, s0); break;
             default: break;
         }
-        P.piece_off[lane] = (uint16_t)off;
-        P.piece_cnt[lane] = (uint16_t)m;
-    } else if (lane >= 32 && lane - 32 < n_actors) {
-        int j = lane - 32;
+        P.piece_off[l] = (uint16_t)off;
+        P.piece_cnt[l] = (uint16_t)m;
+    } else if (l >= kMaxPieces && l - kMaxPieces < n_actors) {
+        int j = l - kMaxPieces;
         P.throw_cnt[j] = (uint16_t)gen_throws(P, P.actor_cell[j], P.throw_from[j], P.throw_to[j], P.throw_pt[j]);
     }
     __syncthreads();
 
     // -- segment starts: lane 0 placements, lanes 1..n_pieces pieces, then actors, then the end
     int cnt = 0;
-    if (lane == 0) cnt = n_place;
-    else if (lane <= n_pieces) cnt = P.piece_cnt[lane - 1];
-    else if (lane <= n_pieces + n_actors) cnt = P.throw_cnt[lane - 1 - n_pieces];
-    int base = wave_excl_scan(cnt, lane);
-    int total = wave_sum(cnt);
+    if (l == 0) cnt = n_place;
+    else if (l <= n_pieces) cnt = P.piece_cnt[l - 1];
+    else if (l <= n_pieces + n_actors) cnt = P.throw_cnt[l - 1 - n_pieces];
+    int base = grp_excl_scan(cnt);
+    int total = grp_sum(cnt, lane);
     int nseg = 1 + n_pieces + n_actors;
-    if (lane <= nseg) P.seg_base[lane] = (int16_t)min(base, 32767);
+    if (l <= nseg) P.seg_base[l] = (int16_t)min(base, 32767);
     __syncthreads();
+    if (!go) return L;
     L.total = total;
     L.n = total == 0 ? 1 : (total < kMaxLegal ? total : kMaxLegal);  // PASS = all-zero from/to, type 2
     L.n_place = n_place;
@@ -222,24 +225,26 @@ enum { kFeatList = 0, kFeatGen = 1, kFeatBucket = 2 };
 
 // The list's source sets (u1: after destination generation) ...
 HW_INL void sources_clear(Pos& P, int lane) {
+    const int l = gl(lane);
     auto& S = P.u1.s;
-    for (int i = lane; i < 16 * 18; i += 64) (&S.from_bb[0][0])[i] = 0;
-    if (lane < 18) S.place_bb[lane] = 0;
+    for (int i = l; i < 16 * 18; i += kW) (&S.from_bb[0][0])[i] = 0;
+    if (l < 18) S.place_bb[l] = 0;
 }
 // ... and the feature counters (u2: after list emission).
 HW_INL void counters_clear(Pos& P, int lane) {
+    const int l = gl(lane);
     auto& F = P.u2.c;
-    for (int i = lane; i < 128; i += 64) F.cnt[i] = 0;
-    if (lane < 16) { F.dsum[lane] = 0; F.dcnt[lane] = 0; }
-    if (lane < 2) { F.ring[lane] = 0; F.covered[lane] = 0; F.capable[lane] = 0; }
-    if (lane == 0) F.n_cap = 0;
+    for (int i = l; i < 128; i += kW) F.cnt[i] = 0;
+    if (l < 16) { F.dsum[l] = 0; F.dcnt[l] = 0; }
+    if (l < 2) { F.ring[l] = 0; F.covered[l] = 0; F.capable[l] = 0; }
+    if (l == 0) F.n_cap = 0;
 }
 
 // MOVE source / PLACE destination sets of a caller-supplied list (global memory)
 HW_INL void list_sources(Pos& P, const uint8_t* __restrict__ M, int n, int lane) {
     auto& F = P.u1.s;
     const int me = P.turn & 1;
-    for (int i = lane; i < n; i += 64) {
+    for (int i = gl(lane); i < n; i += kW) {
         const uint8_t* m = M + 6 * i;
         int ty = m[0], pt = m[1];
         if (ty == MV_MOVE) {
@@ -259,11 +264,12 @@ HW_INL void list_sources(Pos& P, const uint8_t* __restrict__ M, int n, int lane)
 // complete, behind a barrier.
 HW_INL void features_finish(Pos& P, const uint8_t* __restrict__ S, float* __restrict__ out, int lane, int mode,
                             uint32_t bucket, int n_place) {
+    const int l = gl(lane);
     auto& F = P.u2.c;
     const auto& SB = P.u1.s;
     const int me = P.turn & 1;
-    if (lane < P.n_occ) {
-        int c = P.occ_cells[lane];
+    if (l < P.n_occ) {
+        int c = P.occ_cells[l];
         int h = P.hgt(c);
         int tb = P.tp(c);
         int pt = tb & 15, col = (tb >> 4) & 1, tc = (pt - 1) * 2 + col;
@@ -309,8 +315,8 @@ HW_INL void features_finish(Pos& P, const uint8_t* __restrict__ S, float* __rest
     __syncthreads();
     // pieces next to a pillbug-capable cell (throwable own / threatened)
     int ncap = F.n_cap < 8 ? F.n_cap : 8;
-    if (lane < ncap) {
-        int p = F.cap_cells[lane], col = F.cap_col[lane];
+    if (l < ncap) {
+        int p = F.cap_cells[l], col = F.cap_col[l];
         uint32_t m = P.nb[p];
         while (m) {
             int d = __ffs(m) - 1;
@@ -323,13 +329,13 @@ HW_INL void features_finish(Pos& P, const uint8_t* __restrict__ S, float* __rest
         }
     }
     if (mode == kFeatBucket) {
-        if (lane < 16) F.cnt[64 + lane] = (bucket >> lane) & 1u;
-        else if (lane == 16) F.cnt[100] = n_place;
-    } else if (lane < 16) {
+        if (l < 16) F.cnt[64 + l] = (bucket >> l) & 1u;
+        else if (l == 16) F.cnt[100] = n_place;
+    } else if (l < 16) {
         int s = 0;
-        for (int w = 0; w < 18; w++) s += __popc(SB.from_bb[lane][w]);
-        F.cnt[64 + lane] = s;
-    } else if (lane == 16) {
+        for (int w = 0; w < 18; w++) s += __popc(SB.from_bb[l][w]);
+        F.cnt[64 + l] = s;
+    } else if (l == 16) {
         int s = n_place;
         if (mode == kFeatList) {
             s = 0;
@@ -339,7 +345,7 @@ HW_INL void features_finish(Pos& P, const uint8_t* __restrict__ S, float* __rest
     }
     __syncthreads();
     constexpr float kPer[8] = {1.f, 3.f, 3.f, 2.f, 2.f, 1.f, 1.f, 1.f};
-    for (int i = lane; i < kFeat; i += 64) {
+    for (int i = l; i < kFeat; i += kW) {
         float v;
         if (i < 16) v = (float)F.cnt[i];
         else if (i < 32) { int t = (i - 16) >> 1, c = (i - 16) & 1; v = (float)P.hand[c][t] / kPer[t]; }
@@ -356,7 +362,7 @@ HW_INL void features_finish(Pos& P, const uint8_t* __restrict__ S, float* __rest
             int qc = (i - 110) / 6, b = (i - 110) % 6;
             v = (F.ring[qc] == b + 1) ? 1.0f : 0.0f;
         }
-        out[i] = v;
+        if (out) out[i] = v;
     }
 }
 
@@ -373,14 +379,15 @@ __device__ __forceinline__ int round_half_even_div(int sum, int n) {
 
 // compute_centroid (state_encoder.cuh:889-906) over the occupied-cell list
 HW_INL void centroid(const Pos& P, int lane, int& cq, int& cr) {
+    const int l = gl(lane);
     int q = 0, r = 0;
-    if (lane < P.n_occ) {
-        int c = P.occ_cells[lane];
+    if (l < P.n_occ) {
+        int c = P.occ_cells[l];
         int row = c / kGrid;
         q = c - row * kGrid - kHalf;
         r = row - kHalf;
     }
-    int sq = wave_sum(q), sr = wave_sum(r), n = P.n_occ;
+    int sq = grp_sum(q, lane), sr = grp_sum(r, lane), n = P.n_occ;
     cq = n ? round_half_even_div(sq, n) : 0;
     cr = n ? round_half_even_div(sr, n) : 0;
 }
@@ -404,7 +411,7 @@ __device__ __forceinline__ int move_action(int type, int pt, int from, int to, i
 
 // action indices of a caller-supplied list (global memory), -1 padded
 HW_INL void list_actions(const uint8_t* __restrict__ M, int n, int cq, int cr, int* __restrict__ out, int lane) {
-    for (int i = lane; i < kMaxLegal; i += 64) {
+    for (int i = gl(lane); i < kMaxLegal; i += kW) {
         int a = -1;
         if (i < n) {
             const uint8_t* m = M + 6 * i;
@@ -422,7 +429,7 @@ HW_INL void emit_list(Pos& P, const ListInfo& L, int lane, uint8_t* __restrict__
                       int32_t* __restrict__ act_row, int cq, int cr) {
     const int me = P.turn & 1;
     uint16_t* row16 = reinterpret_cast<uint16_t*>(moves_row);
-    for (int i = lane; i < kMaxLegal; i += 64) {
+    for (int i = gl(lane); i < kMaxLegal; i += kW) {
         int tp = 0, from = 0, to = 0;
         if (i < L.n) {
             if (L.total == 0) {
@@ -612,25 +619,26 @@ HW_INL uint32_t compact_summary(Pos& P, int lane, int* n_place) {
         if (ptn == 0 && p == 0) ok = false;
         any = any || ok;
     }
+    const int l = gl(lane);
     uint32_t pw = 0;
-    if (any && lane < 18) {
+    if (any && l < 18) {
         if (P.turn == 0) {
-            pw = (lane == (264 >> 5)) ? (1u << (264 & 31)) : 0u;
+            pw = (l == (264 >> 5)) ? (1u << (264 & 31)) : 0u;
         } else if (P.turn == 1) {
-            pw = nbr_union_word(P.occ, lane) & ~P.occ[lane + 1];
+            pw = nbr_union_word(P.occ, l) & ~P.occ[l + 1];
         } else {
             const uint32_t* mine = me ? P.bt : P.wt;
             const uint32_t* theirs = me ? P.wt : P.bt;
-            pw = nbr_union_word(mine, lane) & ~nbr_union_word(theirs, lane) & ~P.occ[lane + 1];
+            pw = nbr_union_word(mine, l) & ~nbr_union_word(theirs, l) & ~P.occ[l + 1];
         }
     }
-    int npos = wave_sum(__popc(pw));
+    int npos = grp_sum(__popc(pw), lane);
     *n_place = npos;
     if (!queen_down || npos >= kMaxLegal) return 0;
     // one lane per occupied cell: own movable pieces and throw actors
     uint32_t bucket = 0;
-    if (lane < P.n_occ) {
-        int c = P.occ_cells[lane];
+    if (l < P.n_occ) {
+        int c = P.occ_cells[l];
         int tb = P.tp(c);
         int t = tb & 15;
         if (((tb >> 4) & 1) == me) {
@@ -650,9 +658,7 @@ HW_INL uint32_t compact_summary(Pos& P, int lane, int* n_place) {
             }
         }
     }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) bucket |= __shfl_xor(bucket, o, 64);
-    return bucket;
+    return grp_or(bucket);
 }
 
 // has_queen_escape_move (move_gen.cuh:771-821); wave-uniform result
@@ -662,11 +668,12 @@ HW_INL bool queen_escape(const Pos& P, int lane) {
     int q = P.queen[me];
     if (q >= kCells || !pb_get(P.occ, q)) return false;
     int tq = P.tp(q);
+    const int l = gl(lane);
     bool ok = false;
-    if (lane == 0) {
+    if (l == 0) {
         ok = (tq & 15) == PT_Q && ((tq >> 4) & 1) == me && !pb_get(P.pin, q) && slide_mask(P, q, q) != 0;
-    } else if (lane < P.n_occ + 1) {
-        int c = P.occ_cells[lane - 1];
+    } else if (l < P.n_occ + 1) {
+        int c = P.occ_cells[l - 1];
         int tb = P.tp(c);
         int t = tb & 15;
         if (((tb >> 4) & 1) == me && ((t == PT_P) || (t == PT_M && P.hgt(c) == 1 && touches_top_pillbug(P, c)))) {
@@ -674,7 +681,7 @@ HW_INL bool queen_escape(const Pos& P, int lane) {
             if (bit) ok = throwable(P, c, __ffs(bit) - 1);
         }
     }
-    return __ballot(ok) != 0;
+    return grp_ballot(ok, lane) != 0;
 }
 
 // ---------------------------------------------------------------- apply
@@ -765,8 +772,8 @@ HW_INL void run_legal(Pos& P, const uint8_t* __restrict__ S, int lane, uint8_t* 
     int cq = 0, cr = 0;
     if (WithAct) centroid(P, lane, cq, cr);
     __syncthreads();
-    emit_list<WithMoves, WithAct, WithFeat>(P, L, lane, moves_row, act_row, cq, cr);
-    if (lane == 0) *n_slot = L.n;
+    if (moves_row) emit_list<WithMoves, WithAct, WithFeat>(P, L, lane, moves_row, act_row, cq, cr);
+    if (gl(lane) == 0 && n_slot) *n_slot = L.n;
     if (WithFeat) {
         __syncthreads();
         counters_clear(P, lane);
@@ -793,7 +800,7 @@ HW_INL void run_successor(Pos& P, const uint8_t* __restrict__ S, const uint8_t* 
                           float* __restrict__ feat_row) {
     load_position(P, S, lane);
     __syncthreads();
-    if (lane == 0) apply_on_board(P, S, m[0], m[1], m[2] | (m[3] << 8), m[4] | (m[5] << 8));
+    if (gl(lane) == 0) apply_on_board(P, S, m[0], m[1], m[2] | (m[3] << 8), m[4] | (m[5] << 8));
     __syncthreads();
     build_occ_list(P, lane);
     __syncthreads();

@@ -1,6 +1,9 @@
 // hive_wave.hpp -- wave-cooperative Hive rules engine for CDNA4 (gfx950).
 //
-// One 64-lane wavefront owns one position.  The board lives in LDS as
+// A group of kW = 32 lanes owns one position; a 64-lane wavefront works on
+// two positions side by side (lanes 0-31 and 32-63), so the sequential
+// parts of a position (searches of single pieces, floods, per-word loops)
+// are paid once per two positions.  The board lives in LDS as
 //   * padded 32-bit-word bitboards (occupied / white top / black top /
 //     articulation / pinned / placement): board word w sits at index w+1,
 //     indices 0 and 19 are zero pads so that any cell's 47-bit neighbour
@@ -49,6 +52,8 @@ constexpr int kActors = 2;  // throw actors of one colour: its pillbug and its m
 constexpr int kThrowCap = 12;
 constexpr int kSets = 8;  // visited / dedup sets: 3 ants, 2 spiders, 1 ladybug, 1 mosquito (2)
 constexpr int kSegs = 1 + kMaxPieces + kActors + 1;  // placements, pieces, actors, end
+constexpr int kW = 32;               // lanes per position
+constexpr int kPosPerWave = 64 / kW;  // positions per wavefront
 
 // state byte offsets (hive_gpu/csrc/hive_state.cuh:239-269)
 constexpr int OFF_HEIGHT = 2645, OFF_OCC = 3176, OFF_WTOP = 3248, OFF_BTOP = 3320;
@@ -203,39 +208,71 @@ __device__ __forceinline__ int wave_excl_scan(int v, int lane) {
 
 __device__ __forceinline__ int wave_sum(int v) { return __builtin_amdgcn_readlane(wave_incl_scan(v), 63); }
 
+// ---- lane-group (one position) versions; `lane` is the wavefront lane
+__device__ __forceinline__ int gl(int lane) { return lane & (kW - 1); }
+
+// inclusive prefix sum within each 32-lane group: row shifts, then the row
+// total of rows 0 / 2 carried into rows 1 / 3 (row_bcast:15)
+__device__ __forceinline__ int grp_incl_scan(int x) {
+    x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, true);  // row_shr:1
+    x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, true);  // row_shr:2
+    x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, true);  // row_shr:4
+    x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, true);  // row_shr:8
+    x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xa, 0xf, true);  // row_bcast:15
+    return x;
+}
+__device__ __forceinline__ int grp_excl_scan(int v) { return grp_incl_scan(v) - v; }
+template <typename T>
+__device__ __forceinline__ T grp_shfl(T v, int src, int lane) { return __shfl(v, (lane & ~(kW - 1)) | src, 64); }
+__device__ __forceinline__ int grp_sum(int v, int lane) { return grp_shfl(grp_incl_scan(v), kW - 1, lane); }
+__device__ __forceinline__ uint32_t grp_ballot(bool p, int lane) {
+    return (uint32_t)(__ballot(p) >> (lane & ~(kW - 1)));
+}
+__device__ __forceinline__ uint32_t grp_or(uint32_t v) {
+#pragma unroll
+    for (int o = kW / 2; o > 0; o >>= 1) v |= __shfl_xor(v, o, 64);
+    return v;
+}
+
 // ---------------------------------------------------------------- state load
 // Heights, top bytes, bitboards and metadata of the state row S into P.
+// Lane l handles cells 4j .. 4j+3 (j = l, l + 32, ...): one aligned dword
+// of level-0 bytes and the two aligned dwords holding their heights (which
+// start at the odd offset 2645); the top byte of a stack (height > 1) is a
+// second, rare, dependent load.
 HW_INL void load_position(Pos& P, const uint8_t* __restrict__ S, int lane) {
-    // heights and level-0 bytes are independent loads, issued together; the
-    // top byte of a stack (height > 1) is a second, rare, dependent load
-    uint32_t hv[9], tv[9];
+    const int l = gl(lane);
+    const uint32_t* S32 = reinterpret_cast<const uint32_t*>(S);
+    uint32_t* cell32 = reinterpret_cast<uint32_t*>(P.cell);
+    for (int j = l; j < 136; j += kW) {
+        uint32_t packed = 0;
+        if (j < 133) {
+            uint32_t lv0 = S32[j];
+            uint32_t h0 = S32[(OFF_HEIGHT - 1) / 4 + j], h1 = S32[(OFF_HEIGHT - 1) / 4 + j + 1];
+            uint32_t hts = __builtin_amdgcn_alignbyte(h1, h0, 1);  // bytes 2645+4j .. 2648+4j
 #pragma unroll
-    for (int k = 0; k < 9; k++) {
-        int i = lane + 64 * k;
-        bool on = i < kCells;
-        hv[k] = on ? S[OFF_HEIGHT + i] : 0u;
-        tv[k] = on ? S[i] : 0u;
-    }
-#pragma unroll
-    for (int k = 0; k < 9; k++) {
-        int i = lane + 64 * k;
-        if (i < 544) {
-            int hh = (int)hv[k];
-            int t = (int)tv[k];
-            if (hh > 1) t = S[((hh > 5 ? 5 : hh) - 1) * kCells + i];
-            P.set_cell(i, hh > 7 ? 7 : hh, t);
+            for (int k = 0; k < 4; k++) {
+                int c = 4 * j + k;
+                int hh = (int)((hts >> (8 * k)) & 0xFFu);
+                int t = (int)((lv0 >> (8 * k)) & 0xFFu);
+                if (c >= kCells) hh = 0;
+                if (hh > 1) t = S[((hh > 5 ? 5 : hh) - 1) * kCells + c];
+                int h7 = hh > 7 ? 7 : hh;
+                packed |= (uint32_t)((h7 << 5) | (h7 ? (t & 31) : 0)) << (8 * k);
+            }
         }
+        cell32[j] = packed;
     }
     const uint32_t* W = reinterpret_cast<const uint32_t*>(S + OFF_OCC);  // 8-byte aligned
-    if (lane < 18) {
-        P.occ[lane + 1] = W[lane];
-        P.wt[lane + 1] = W[18 + lane];
-        P.bt[lane + 1] = W[36 + lane];
-    } else if (lane < 24) {
-        int k = lane - 18;  // zero the pads: k = 0 -> index 0, k = 1 -> index 19
+    if (l < 18) {
+        P.occ[l + 1] = W[l];
+        P.wt[l + 1] = W[18 + l];
+        P.bt[l + 1] = W[36 + l];
+    } else if (l < 24) {
+        int k = l - 18;  // zero the pads: k = 0 -> index 0, k = 1 -> index 19
         uint32_t* dst = k < 2 ? P.occ : k < 4 ? P.wt : P.bt;
         dst[(k & 1) ? 19 : 0] = 0;
-    } else if (lane == 24) {
+    } else if (l == 24) {
         const uint32_t* M = reinterpret_cast<const uint32_t*>(S + OFF_QUEEN);
         uint32_t q = M[0];
         P.queen[0] = (uint16_t)q;
@@ -258,18 +295,19 @@ HW_INL void load_position(Pos& P, const uint8_t* __restrict__ S, int lane) {
 // Ascending list of occupied cells (first 32) and per-word occupied-cell
 // prefix counts.
 HW_INL void build_occ_list(Pos& P, int lane) {
-    uint32_t w = lane < 18 ? P.occ[lane + 1] : 0u;
-    int base = wave_excl_scan(__popc(w), lane);
-    int total = wave_sum(lane < 18 ? __popc(w) : 0);
-    if (lane < 18) P.occ_pre[lane] = (uint16_t)base;
+    const int l = gl(lane);
+    uint32_t w = l < 18 ? P.occ[l + 1] : 0u;
+    int base = grp_excl_scan(__popc(w));
+    int total = grp_sum(__popc(w), lane);
+    if (l < 18) P.occ_pre[l] = (uint16_t)base;
     int k = base;
     while (w && k < 32) {
         int b = __ffs(w) - 1;
         w &= w - 1;
-        P.occ_cells[k] = (uint16_t)(lane * 32 + b);
+        P.occ_cells[k] = (uint16_t)(l * 32 + b);
         k++;
     }
-    if (lane == 0) P.n_occ = total < 32 ? total : 32;
+    if (l == 0) P.n_occ = total < 32 ? total : 32;
 }
 
 // Per-cell occupied-neighbour and ground-slide direction masks of the
@@ -278,18 +316,17 @@ HW_INL void build_occ_list(Pos& P, int lane) {
 // occupied cell lies in it.  Readers only look at occupied cells and their
 // neighbours; the other entries are left unwritten.
 HW_INL void build_cell_masks(Pos& P, int lane) {
-    uint32_t rowbits = lane < kGrid ? (word_field(P.occ, kGrid * lane) & 0x7FFFFFu) : 0u;
-    uint64_t rows = __ballot(rowbits != 0);
+    const int l = gl(lane);
+    uint32_t rowbits = l < kGrid ? (word_field(P.occ, kGrid * l) & 0x7FFFFFu) : 0u;
+    uint32_t rows = grp_ballot(rowbits != 0, lane);
+    uint32_t cols = grp_or(rowbits);
     if (rows == 0) return;
-    uint32_t cols = rowbits;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) cols |= __shfl_xor(cols, o, 64);
-    int r0 = __ffsll((unsigned long long)rows) - 1, r1 = 63 - __clzll((long long)rows);
+    int r0 = __ffs(rows) - 1, r1 = 31 - __clz(rows);
     int c0 = __ffs(cols) - 1, c1 = 31 - __clz(cols);
     int rlo = r0 > 0 ? r0 - 1 : 0, rhi = r1 < kGrid - 1 ? r1 + 1 : kGrid - 1;
     int clo = c0 > 0 ? c0 - 1 : 0, chi = c1 < kGrid - 1 ? c1 + 1 : kGrid - 1;
     int bw = chi - clo + 1, n = bw * (rhi - rlo + 1);
-    for (int k = lane; k < n; k += 64) {
+    for (int k = l; k < n; k += kW) {
         int rr = k / bw;
         int row = rlo + rr, col = clo + (k - rr * bw);
         int c = row * kGrid + col;
@@ -315,16 +352,17 @@ HW_INL int occ_rank(const Pos& P, int c) {
 // Articulation points (articulation.cuh:34-168).  The reference runs one DFS
 // from the lowest occupied cell, so its result is the articulation set of
 // that cell's component (first 28 cells), empty when <= 2 cells are occupied.
-// Here lane v floods the dense vertex graph with v removed; lane 63 floods
+// Here lane v floods the dense vertex graph with v removed; lane 31 floods
 // with nothing removed to obtain the component C0 of vertex 0.  v is an
 // articulation point iff v is in C0 and C0 \ {v} is not reached from a
 // vertex of C0 \ {v}.
 HW_INL void articulation(Pos& P, int lane) {
+    const int l = gl(lane);
     int total = P.n_occ;
     int N = total < 28 ? total : 28;
-    if (lane < 20) { P.ap[lane] = 0; P.pin[lane] = 0; }
-    if (lane < N) {
-        int c = P.occ_cells[lane];
+    if (l < 20) { P.ap[l] = 0; P.pin[l] = 0; }
+    if (l < N) {
+        int c = P.occ_cells[l];
         uint32_t nm = nbr_bits(P.occ, c);
         uint32_t a = 0;
         while (nm) {
@@ -333,11 +371,11 @@ HW_INL void articulation(Pos& P, int lane) {
             int j = occ_rank(P, step(c, d));
             if (j < N) a |= 1u << j;
         }
-        P.adj[lane] = a;
+        P.adj[l] = a;
     }
     __syncthreads();
     if (total <= 2) return;
-    int v = lane < N ? lane : -1;
+    int v = l < N ? l : -1;
     uint32_t vbit = v >= 0 ? (1u << v) : 0u;
     uint32_t start;
     if (v == 0) {
@@ -347,7 +385,7 @@ HW_INL void articulation(Pos& P, int lane) {
         start = 1u;
     }
     uint32_t reach = 0;
-    if (lane < N || lane == 63) {
+    if (l < N || l == kW - 1) {
         reach = start;
         uint32_t frontier = start;
         while (frontier) {
@@ -358,7 +396,7 @@ HW_INL void articulation(Pos& P, int lane) {
             frontier |= nb;
         }
     }
-    uint32_t c0 = __shfl(reach, 63, 64);
+    uint32_t c0 = grp_shfl(reach, kW - 1, lane);
     bool is_ap = v >= 0 && ((c0 >> v) & 1u) && reach != (c0 & ~vbit);
     if (is_ap) {
         int c = P.occ_cells[v];

@@ -3,6 +3,7 @@
 // used by tests/test_emu_engine.py to check the device logic on the CPU and
 // to debug it there.
 #define HW_HOST_EMU 1
+#include <memory>
 #include <thread>
 #include <vector>
 
@@ -12,49 +13,63 @@ using namespace hw;
 
 namespace {
 // Runs body(i, tid) for i in [0, count) on one emulated workgroup of
-// `waves` waves, one item after another.
+// `threads` threads (2 positions per 64), one item after another.
 template <typename F>
-void run_group(int waves, int64_t count, F&& body) {
-    std::barrier<> gbar(waves * 64);
-    std::barrier<> wb0(64), wb1(64), wb2(64), wb3(64);
+void run_group(int threads, int64_t count, F&& body) {
+    std::barrier<> wg(threads);
+    std::vector<std::unique_ptr<std::barrier<>>> groups;
     wave_emu::Ctx ctx;
-    ctx.wave_bar[0] = &wb0; ctx.wave_bar[1] = &wb1; ctx.wave_bar[2] = &wb2; ctx.wave_bar[3] = &wb3;
-    ctx.group_bar = &gbar;
+    for (int g = 0; g < threads / wave_emu::kGroupLanes; g++) {
+        groups.emplace_back(new std::barrier<>(wave_emu::kGroupLanes));
+        ctx.group_bar[g] = groups.back().get();
+    }
+    ctx.wg_bar = &wg;
     wave_emu::g_ctx = &ctx;
-    std::vector<std::thread> threads;
-    for (int t = 0; t < waves * 64; t++) {
-        threads.emplace_back([&, t] {
+    std::vector<std::thread> th;
+    for (int t = 0; t < threads; t++) {
+        th.emplace_back([&, t] {
             wave_emu::g_tid = t;
             for (int64_t i = 0; i < count; i++) {
                 body(i, t);
-                wave_emu::group_sync();
+                wave_emu::wg_sync();
             }
         });
     }
-    for (auto& th : threads) th.join();
+    for (auto& x : th) x.join();
     wave_emu::g_ctx = nullptr;
 }
-static Pos g_one;
+static Pos g_pos[kPosPerWave];
 }  // namespace
 
 extern "C" {
+// one emulated wave per kPosPerWave items, as the kernels launch them
 void emu_legal(const uint8_t* states, int64_t B, uint8_t* moves, int32_t* n, float* feat, int32_t* act) {
-    run_group(1, B, [&](int64_t i, int l) {
-        run_legal<true, true, true>(g_one, states + i * kStateBytes, l, moves + i * 1536, n + i, feat + i * kFeat,
-                                    act + i * kMaxLegal);
+    run_group(64, (B + kPosPerWave - 1) / kPosPerWave, [&](int64_t w, int t) {
+        int64_t i = w * kPosPerWave + t / kW;
+        bool live = i < B;
+        if (!live) i = B - 1;
+        run_legal<true, true, true>(g_pos[t / kW], states + i * kStateBytes, t, live ? moves + i * 1536 : nullptr,
+                                    live ? n + i : nullptr, live ? feat + i * kFeat : nullptr,
+                                    live ? act + i * kMaxLegal : nullptr);
     });
 }
 void emu_successor(const uint8_t* states, const uint8_t* legal, const int64_t* a2r, const int64_t* midx, int64_t N,
                    float* feat) {
-    run_group(1, N, [&](int64_t i, int l) {
-        run_successor(g_one, states + a2r[i] * kStateBytes, legal + (a2r[i] * kMaxLegal + midx[i]) * 6, l,
-                      feat + i * kFeat);
+    run_group(64, (N + kPosPerWave - 1) / kPosPerWave, [&](int64_t w, int t) {
+        int64_t i = w * kPosPerWave + t / kW;
+        bool live = i < N;
+        if (!live) i = N - 1;
+        run_successor(g_pos[t / kW], states + a2r[i] * kStateBytes, legal + (a2r[i] * kMaxLegal + midx[i]) * 6, t,
+                      live ? feat + i * kFeat : nullptr);
     });
 }
 void emu_queen_escape(const uint8_t* states, int64_t B, uint8_t* out) {
-    run_group(1, B, [&](int64_t i, int l) {
-        bool e = run_queen_escape(g_one, states + i * kStateBytes, l);
-        if (l == 0) out[i] = e ? 1 : 0;
+    run_group(64, (B + kPosPerWave - 1) / kPosPerWave, [&](int64_t w, int t) {
+        int64_t i = w * kPosPerWave + t / kW;
+        bool live = i < B;
+        if (!live) i = B - 1;
+        bool e = run_queen_escape(g_pos[t / kW], states + i * kStateBytes, t);
+        if (live && t % kW == 0) out[i] = e ? 1 : 0;
     });
 }
 }

@@ -20,25 +20,32 @@
 #define __launch_bounds__(x)
 
 namespace wave_emu {
-// A workgroup of up to 4 waves: shuffles and ballots rendezvous per wave,
-// __syncthreads across the workgroup.
+// A workgroup of one or more waves.  The engine's cross-lane operations stay
+// inside a lane group of kGroupLanes (one position); they rendezvous per
+// group, so a group may take a branch the other group of its wave skips.
+// __syncthreads synchronises the whole workgroup.
+constexpr int kGroupLanes = 32;
 struct Ctx {
-    std::barrier<>* wave_bar[4];
-    std::barrier<>* group_bar;
+    std::barrier<>* group_bar[8];
+    std::barrier<>* wg_bar;
     int64_t slot[256];
 };
 inline Ctx* g_ctx = nullptr;
 inline thread_local int g_tid = 0;
 inline int lane() { return g_tid & 63; }
-inline int wave() { return g_tid >> 6; }
-inline void wave_sync() { g_ctx->wave_bar[wave()]->arrive_and_wait(); }
-inline void group_sync() { g_ctx->group_bar->arrive_and_wait(); }
+inline int group() { return g_tid / kGroupLanes; }
+inline int group_base() { return g_tid & ~(kGroupLanes - 1); }
+inline void group_sync() { g_ctx->group_bar[group()]->arrive_and_wait(); }
+inline void wg_sync() { g_ctx->wg_bar->arrive_and_wait(); }
+// value of v at wave lane src, which must be in the caller's group
 template <typename T>
 inline T exchange(T v, int src) {
+    int s = (g_tid & ~63) | (src & 63);
+    if ((s & ~(kGroupLanes - 1)) != group_base()) abort();
     g_ctx->slot[g_tid] = (int64_t)v;
-    wave_sync();
-    T r = (T)g_ctx->slot[(wave() << 6) | (src & 63)];
-    wave_sync();
+    group_sync();
+    T r = (T)g_ctx->slot[s];
+    group_sync();
     return r;
 }
 }  // namespace wave_emu
@@ -50,8 +57,11 @@ struct EmuDim3 {
     EmuThreadIdx x;
 };
 inline EmuDim3 threadIdx;
+struct EmuBlockIdx {
+    operator int() const { return 0; }
+};
 
-inline void __syncthreads() { wave_emu::group_sync(); }
+inline void __syncthreads() { wave_emu::wg_sync(); }
 
 template <typename T>
 inline T __shfl_up(T v, unsigned o, int = 64) {
@@ -66,20 +76,25 @@ template <typename T>
 inline T __shfl(T v, int src, int = 64) {
     return wave_emu::exchange(v, src & 63);
 }
+// the caller's group bits, at their wave positions
 inline uint64_t __ballot(int pred) {
     wave_emu::g_ctx->slot[wave_emu::g_tid] = pred ? 1 : 0;
-    wave_emu::wave_sync();
+    wave_emu::group_sync();
     uint64_t m = 0;
-    int base = wave_emu::wave() << 6;
-    for (int i = 0; i < 64; i++)
-        if (wave_emu::g_ctx->slot[base + i]) m |= 1ull << i;
-    wave_emu::wave_sync();
+    int base = wave_emu::group_base();
+    for (int i = 0; i < wave_emu::kGroupLanes; i++)
+        if (wave_emu::g_ctx->slot[base + i]) m |= 1ull << ((base & 63) + i);
+    wave_emu::group_sync();
     return m;
+}
+inline uint32_t __builtin_amdgcn_alignbyte(uint32_t hi, uint32_t lo, uint32_t s) {
+    return (uint32_t)(((((uint64_t)hi) << 32) | lo) >> (8 * (s & 3)));
 }
 // DPP lane moves used by the engine's prefix sums: row_shr:1..15, row_bcast:15,
 // row_bcast:31 (GFX9 semantics).  Every lane of the wave calls it.
 inline int __builtin_amdgcn_update_dpp(int old, int src, int ctrl, int row_mask, int bank_mask, bool bound_ctrl) {
     int l = wave_emu::lane(), row = l >> 4, r = l & 15, bank = r >> 2;
+    bool enabled = ((row_mask >> row) & 1) && ((bank_mask >> bank) & 1);
     int from = -1;
     if (ctrl >= 0x111 && ctrl <= 0x11F) {
         int n = ctrl - 0x110;
@@ -91,8 +106,9 @@ inline int __builtin_amdgcn_update_dpp(int old, int src, int ctrl, int row_mask,
     } else {
         abort();
     }
+    if (!enabled) from = -1;
     int v = wave_emu::exchange(src, from >= 0 ? from : l);
-    if (!((row_mask >> row) & 1) || !((bank_mask >> bank) & 1)) return old;
+    if (!enabled) return old;
     if (from < 0) return bound_ctrl ? 0 : old;
     return v;
 }
