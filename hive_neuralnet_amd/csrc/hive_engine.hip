@@ -59,8 +59,10 @@ __device__ __forceinline__ int64_t item_of(int64_t n, bool& live) {
     return live ? i : n - 1;
 }
 
+// 6 waves per SIMD: the register cap (80 VGPRs, a few bytes of spill) pays
+// for itself, the kernel is bound by issue and latency, not by registers
 template <bool WithMoves, bool WithFeat, bool WithAct>
-__global__ __launch_bounds__(64) void k_legal(const uint8_t* __restrict__ states, int64_t B,
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(6))) void k_legal(const uint8_t* __restrict__ states, int64_t B,
                                               uint8_t* __restrict__ moves_out, int32_t* __restrict__ n_out,
                                               float* __restrict__ feat_out, int32_t* __restrict__ act_out) {
     __shared__ Pos PS[kPosPerWave];
@@ -78,10 +80,11 @@ __global__ __launch_bounds__(64) void k_extract_features(const uint8_t* __restri
                                                          const int32_t* __restrict__ num_legal, int64_t B,
                                                          float* __restrict__ feat_out) {
     __shared__ Pos PS[kPosPerWave];
+    __shared__ ListSets XS[kPosPerWave];
     bool live;
     const int64_t pos = item_of(B, live);
-    run_extract(PS[threadIdx.x >> 5], states + pos * kStateBytes, moves + pos * (kMaxLegal * 6), num_legal[pos],
-                threadIdx.x, live ? feat_out + pos * kFeat : nullptr);
+    run_extract(PS[threadIdx.x >> 5], XS[threadIdx.x >> 5], states + pos * kStateBytes,
+                moves + pos * (kMaxLegal * 6), num_legal[pos], threadIdx.x, live ? feat_out + pos * kFeat : nullptr);
 }
 
 // legal_moves_to_actions_kernel (game_logic.cu:811-835) / compute_centroids_kernel

@@ -223,12 +223,15 @@ HW_INL void list_slot(const Pos& P, const ListInfo& L, int i, int& tp, int& from
 // piece).
 enum { kFeatList = 0, kFeatGen = 1, kFeatBucket = 2 };
 
-// The list's source sets (u1: after destination generation) ...
-HW_INL void sources_clear(Pos& P, int lane) {
+// The list's source sets (u1: after destination generation; X: a
+// caller-supplied list's cell sets) ...
+HW_INL void sources_clear(Pos& P, int lane, ListSets* X = nullptr) {
     const int l = gl(lane);
-    auto& S = P.u1.s;
-    for (int i = l; i < 16 * 18; i += kW) (&S.from_bb[0][0])[i] = 0;
-    if (l < 18) S.place_bb[l] = 0;
+    if (l < 16) P.u1.from_d[l] = 0;
+    if (X) {
+        for (int i = l; i < 16 * 18; i += kW) (&X->from_bb[0][0])[i] = 0;
+        if (l < 18) X->place_bb[l] = 0;
+    }
 }
 // ... and the feature counters (u2: after list emission).
 HW_INL void counters_clear(Pos& P, int lane) {
@@ -241,8 +244,7 @@ HW_INL void counters_clear(Pos& P, int lane) {
 }
 
 // MOVE source / PLACE destination sets of a caller-supplied list (global memory)
-HW_INL void list_sources(Pos& P, const uint8_t* __restrict__ M, int n, int lane) {
-    auto& F = P.u1.s;
+HW_INL void list_sources(Pos& P, const uint8_t* __restrict__ M, int n, int lane, ListSets& F) {
     const int me = P.turn & 1;
     for (int i = gl(lane); i < n; i += kW) {
         const uint8_t* m = M + 6 * i;
@@ -263,10 +265,9 @@ HW_INL void list_sources(Pos& P, const uint8_t* __restrict__ M, int n, int lane)
 // Needs sources_clear / counters_clear and the legal-move sets (modes kFeatList / kFeatGen)
 // complete, behind a barrier.
 HW_INL void features_finish(Pos& P, const uint8_t* __restrict__ S, float* __restrict__ out, int lane, int mode,
-                            uint32_t bucket, int n_place) {
+                            uint32_t bucket, int n_place, const ListSets* X = nullptr) {
     const int l = gl(lane);
     auto& F = P.u2.c;
-    const auto& SB = P.u1.s;
     const int me = P.turn & 1;
     if (l < P.n_occ) {
         int c = P.occ_cells[l];
@@ -275,7 +276,7 @@ HW_INL void features_finish(Pos& P, const uint8_t* __restrict__ S, float* __rest
         int pt = tb & 15, col = (tb >> 4) & 1, tc = (pt - 1) * 2 + col;
         if (pt < PT_Q || pt > PT_P) pt = 0;  // impossible top byte: contributes nothing
         if (pt) atomicAdd(&F.cnt[tc], 1);
-        uint32_t nm = P.nb[c];
+        uint32_t nm = P.nbd[l];
         if (nm == 0) atomicAdd(&F.cnt[96 + col], 1);
         uint32_t gm = grid6(c);
         int oq = P.queen[col ^ 1];
@@ -317,7 +318,7 @@ HW_INL void features_finish(Pos& P, const uint8_t* __restrict__ S, float* __rest
     int ncap = F.n_cap < 8 ? F.n_cap : 8;
     if (l < ncap) {
         int p = F.cap_cells[l], col = F.cap_col[l];
-        uint32_t m = P.nb[p];
+        uint32_t m = nbo(P, p);
         while (m) {
             int d = __ffs(m) - 1;
             m &= m - 1;
@@ -331,17 +332,20 @@ HW_INL void features_finish(Pos& P, const uint8_t* __restrict__ S, float* __rest
     if (mode == kFeatBucket) {
         if (l < 16) F.cnt[64 + l] = (bucket >> l) & 1u;
         else if (l == 16) F.cnt[100] = n_place;
-    } else if (l < 16) {
-        int s = 0;
-        for (int w = 0; w < 18; w++) s += __popc(SB.from_bb[l][w]);
-        F.cnt[64 + l] = s;
-    } else if (l == 16) {
-        int s = n_place;
-        if (mode == kFeatList) {
-            s = 0;
-            for (int w = 0; w < 18; w++) s += __popc(SB.place_bb[w]);
+    } else if (mode == kFeatList) {
+        if (l < 16) {
+            int s = 0;
+            for (int w = 0; w < 18; w++) s += __popc(X->from_bb[l][w]);
+            F.cnt[64 + l] = s;
+        } else if (l == 16) {
+            int s = 0;
+            for (int w = 0; w < 18; w++) s += __popc(X->place_bb[w]);
+            F.cnt[100] = s;
         }
-        F.cnt[100] = s;
+    } else if (l < 16) {
+        F.cnt[64 + l] = __popc(P.u1.from_d[l]);
+    } else if (l == 16) {
+        F.cnt[100] = n_place;
     }
     __syncthreads();
     constexpr float kPer[8] = {1.f, 3.f, 3.f, 2.f, 2.f, 1.f, 1.f, 1.f};
@@ -440,9 +444,10 @@ HW_INL void emit_list(Pos& P, const ListInfo& L, int lane, uint8_t* __restrict__
                 if (WithFeat && seg > 0) {
                     bool thr = seg > L.n_pieces;
                     int pt = tp >> 8;
-                    if ((thr || i == P.seg_base[seg]) && from < 544 && pt >= 1 && pt <= 8) {
+                    if ((thr || i == P.seg_base[seg]) && from < kCells && pt >= 1 && pt <= 8) {
                         int owner = thr ? (P.tp(from) >> 4) & 1 : me;
-                        atomicOr(&P.u1.s.from_bb[(pt - 1) * 2 + owner][from >> 5], 1u << (from & 31));
+                        int r = occ_rank(P, from);  // sources of generated moves are occupied
+                        if (r < 32) atomicOr(&P.u1.from_d[(pt - 1) * 2 + owner], 1u << r);
                     }
                 }
             }
@@ -461,7 +466,7 @@ HW_INL void emit_list(Pos& P, const ListInfo& L, int lane, uint8_t* __restrict__
 // Existence predicates: "the generator for this piece type is non-empty"
 // (the reference's has_*_move helpers, move_gen.cuh:214-1049).
 HW_INL bool has_hopper(const Pos& P, int c) {
-    uint32_t m = P.nb[c];
+    uint32_t m = nbo(P, c);
     while (m) {
         int d = __ffs(m) - 1;
         m &= m - 1;
@@ -520,14 +525,14 @@ HW_INL bool has_beetle(const Pos& P, int c) {
 HW_INL bool has_ladybug(const Pos& P, int c) {
     uint32_t g0 = grid6(c);
     uint32_t nh0 = nbr_heights(P, c, g0);
-    uint32_t o0 = P.nb[c];
+    uint32_t o0 = nbo(P, c);
     int hc = P.hgt(c);
     for (int d1 = 0; d1 < 6; d1++) {
         if (!((o0 >> d1) & 1u)) continue;
         int p1 = step(c, d1);
         if (gate_high(nh0, d1, max(hc - 1, hof(nh0, d1)))) continue;
         uint32_t nh1 = nbr_heights(P, p1, grid6(p1));
-        uint32_t o1 = P.nb[p1];
+        uint32_t o1 = nbo(P, p1);
         int hp1 = P.hgt(p1);
         for (int d2 = 0; d2 < 6; d2++) {
             if (!((o1 >> d2) & 1u)) continue;
@@ -536,7 +541,7 @@ HW_INL bool has_ladybug(const Pos& P, int c) {
             if (gate_high(nh1, d2, max(hp1, hof(nh1, d2)))) continue;
             uint32_t g2 = grid6(p2);
             uint32_t nh2 = nbr_heights(P, p2, g2);
-            uint32_t o2 = P.nb[p2];
+            uint32_t o2 = nbo(P, p2);
             int mh3 = P.hgt(p2);
             for (int d3 = 0; d3 < 6; d3++) {
                 if (!((g2 >> d3) & 1u) || ((o2 >> d3) & 1u)) continue;
@@ -558,7 +563,7 @@ HW_INL bool piece_has_move(const Pos& P, int c, int t) {
         case PT_L: return has_ladybug(P, c);
         case PT_M: {
             if (P.hgt(c) > 1) return has_beetle(P, c);
-            uint32_t om = P.nb[c];
+            uint32_t om = nbo(P, c);
             uint32_t has = 0;
             while (om) {
                 int d = __ffs(om) - 1;
@@ -592,7 +597,7 @@ HW_INL bool throwable(const Pos& P, int a, int dt) {
     int ccwh = ((gt >> ((back + 1) % 6)) & 1u) ? P.hgt(step(t, (back + 1) % 6)) : 0;
     if (cwh > lift && ccwh > lift) return false;
     uint32_t ga = grid6(a);
-    uint32_t oa = P.nb[a];
+    uint32_t oa = nbo(P, a);
     uint32_t nha = nbr_heights(P, a, ga);
     for (int dd = 0; dd < 6; dd++) {
         if (!((ga >> dd) & 1u) || dd == dt || ((oa >> dd) & 1u)) continue;
@@ -646,7 +651,7 @@ HW_INL uint32_t compact_summary(Pos& P, int lane, int* n_place) {
             if (!stunned && !pb_get(P.pin, c) && piece_has_move(P, c, t)) bucket |= 1u << ((t - 1) * 2 + me);
             bool actor = (t == PT_P) || (t == PT_M && P.hgt(c) == 1 && touches_top_pillbug(P, c));
             if (actor) {
-                uint32_t oa = P.nb[c];
+                uint32_t oa = nbo(P, c);
                 while (oa) {
                     int dt = __ffs(oa) - 1;
                     oa &= oa - 1;
@@ -783,16 +788,16 @@ HW_INL void run_legal(Pos& P, const uint8_t* __restrict__ S, int lane, uint8_t* 
     }
 }
 
-HW_INL void run_extract(Pos& P, const uint8_t* __restrict__ S, const uint8_t* __restrict__ M, int nl,
+HW_INL void run_extract(Pos& P, ListSets& X, const uint8_t* __restrict__ S, const uint8_t* __restrict__ M, int nl,
                         int lane, float* __restrict__ feat_row) {
     int n = nl < 0 ? 0 : (nl > kMaxLegal ? kMaxLegal : nl);
     prepare(P, S, lane);
-    sources_clear(P, lane);
+    sources_clear(P, lane, &X);
     counters_clear(P, lane);
     __syncthreads();
-    list_sources(P, M, n, lane);
+    list_sources(P, M, n, lane, X);
     __syncthreads();
-    features_finish(P, S, feat_row, lane, kFeatList, 0u, 0);
+    features_finish(P, S, feat_row, lane, kFeatList, 0u, 0, &X);
 }
 
 // fnn_successor_features_kernel (game_logic.cu:182-229) for one (root, move)

@@ -135,7 +135,6 @@ __device__ __forceinline__ int hexdist(int a, int b) {  // fnn_features.cuh:44-6
 struct alignas(16) Pos {
     uint32_t occ[kPW], wt[kPW], bt[kPW], ap[kPW], pin[kPW], plc[kPW];
     uint8_t cell[544];  // top piece byte (type | colour << 4) in bits 0-4, stack height in bits 5-7
-    uint8_t nb[544];  // occupied on-grid neighbours of each cell (direction mask)
     uint8_t sm[544];  // ground-slide exits of each cell with nothing lifted
     uint16_t occ_pre[20];  // occupied cells in board words before word w
     uint16_t plc_pre[20];  // placement cells in board words before word w
@@ -146,26 +145,24 @@ struct alignas(16) Pos {
     uint8_t qplaced, result, pad_[2];
     int n_occ;
     uint16_t occ_cells[32];
-    uint32_t adj[32];
+    uint8_t nbd[32];  // occupied on-grid neighbours (direction mask) of the occupied cells, by rank
     // move generation
     int n_pieces, n_actors, n_place, n_total;
     uint16_t piece_cell[kMaxPieces];
     uint8_t piece_type[kMaxPieces];
     uint16_t piece_off[kMaxPieces];
     uint16_t piece_cnt[kMaxPieces];
-    uint8_t piece_set[kMaxPieces];  // first visited set of a piece that needs sets
     uint16_t actor_cell[kActors];
     uint16_t throw_cnt[kActors];
     uint16_t throw_from[kActors][kThrowCap];
     uint16_t throw_to[kActors][kThrowCap];
     uint8_t throw_pt[kActors][kThrowCap];
-    // generation: visited sets; emission and features: the list's source sets
+    // articulation: dense adjacency; generation: visited sets; emission and
+    // features: the generated list's MOVE sources per (type, owner), by rank
     union {
+        uint32_t adj[32];
         uint32_t sets[kSets][18];
-        struct {
-            uint32_t from_bb[16][18];  // MOVE sources per (type, owner)
-            uint32_t place_bb[18];     // PLACE destinations
-        } s;
+        uint32_t from_d[16];
     } u1;
     // generation and emission: destinations; features (after emission): counters
     union {
@@ -184,6 +181,13 @@ struct alignas(16) Pos {
     __device__ __forceinline__ void set_cell(int c, int h, int top) {
         cell[c] = (uint8_t)((h << 5) | (h ? (top & 31) : 0));
     }
+};
+
+// MOVE sources per (type, owner) and PLACE destinations of a caller-supplied
+// list, as bitboards over all cells (the list may name any cell)
+struct ListSets {
+    uint32_t from_bb[16][18];
+    uint32_t place_bb[18];
 };
 
 // ---------------------------------------------------------------- wave utils
@@ -310,11 +314,24 @@ HW_INL void build_occ_list(Pos& P, int lane) {
     if (l == 0) P.n_occ = total < 32 ? total : 32;
 }
 
-// Per-cell occupied-neighbour and ground-slide direction masks of the
-// current occupancy (P.occ with zero pads), for the cells of the hive's
-// bounding box grown by one row and column: every hex neighbour of an
-// occupied cell lies in it.  Readers only look at occupied cells and their
-// neighbours; the other entries are left unwritten.
+// index of occupied cell c in ascending cell order
+HW_INL int occ_rank(const Pos& P, int c) {
+    int w = c >> 5;
+    return P.occ_pre[w] + __popc(P.occ[w + 1] & ((1u << (c & 31)) - 1u));
+}
+
+// occupied-neighbour direction mask of an occupied cell
+HW_INL uint32_t nbo(const Pos& P, int c) {
+    int r = occ_rank(P, c);
+    return r < 32 ? (uint32_t)P.nbd[r] : nbr_bits(P.occ, c);
+}
+
+// Ground-slide direction masks of the current occupancy (P.occ with zero
+// pads) for the cells of the hive's bounding box grown by one row and
+// column (every hex neighbour of an occupied cell lies in it; readers only
+// look at occupied cells and their neighbours, other entries are left
+// unwritten), and the occupied-neighbour masks of the occupied cells (nbd,
+// by rank; needs occ_pre).
 HW_INL void build_cell_masks(Pos& P, int lane) {
     const int l = gl(lane);
     uint32_t rowbits = l < kGrid ? (word_field(P.occ, kGrid * l) & 0x7FFFFFu) : 0u;
@@ -338,16 +355,14 @@ HW_INL void build_cell_masks(Pos& P, int lane) {
         if (col > 0 && row < 22) gm |= 16u;
         if (row < 22) gm |= 32u;
         uint32_t nm = nbr_bits_raw(P.occ, c) & gm;
-        P.nb[c] = (uint8_t)nm;
         P.sm[c] = (uint8_t)(gm & ~nm & (rotl6(nm) ^ rotr6(nm)));
+        if (pb_get(P.occ, c)) {
+            int r = occ_rank(P, c);
+            if (r < 32) P.nbd[r] = (uint8_t)nm;
+        }
     }
 }
 
-// index of occupied cell c in ascending cell order
-HW_INL int occ_rank(const Pos& P, int c) {
-    int w = c >> 5;
-    return P.occ_pre[w] + __popc(P.occ[w + 1] & ((1u << (c & 31)) - 1u));
-}
 
 // Articulation points (articulation.cuh:34-168).  The reference runs one DFS
 // from the lowest occupied cell, so its result is the articulation set of
@@ -371,7 +386,7 @@ HW_INL void articulation(Pos& P, int lane) {
             int j = occ_rank(P, step(c, d));
             if (j < N) a |= 1u << j;
         }
-        P.adj[l] = a;
+        P.u1.adj[l] = a;
     }
     __syncthreads();
     if (total <= 2) return;
@@ -379,7 +394,7 @@ HW_INL void articulation(Pos& P, int lane) {
     uint32_t vbit = v >= 0 ? (1u << v) : 0u;
     uint32_t start;
     if (v == 0) {
-        uint32_t a0 = P.adj[0];
+        uint32_t a0 = P.u1.adj[0];
         start = a0 ? (a0 & (~a0 + 1u)) : 0u;
     } else {
         start = 1u;
@@ -391,7 +406,7 @@ HW_INL void articulation(Pos& P, int lane) {
         while (frontier) {
             int i = __ffs(frontier) - 1;
             frontier &= frontier - 1;
-            uint32_t nb = P.adj[i] & ~reach & ~vbit;
+            uint32_t nb = P.u1.adj[i] & ~reach & ~vbit;
             reach |= nb;
             frontier |= nb;
         }
@@ -414,7 +429,7 @@ __device__ __forceinline__ uint32_t slide_mask(const Pos& P, int c, int g) {
     uint32_t w = (uint32_t)(g - c + 23);
     if (w < 47u && ((kRingWin >> w) & 1ull)) {  // g may be a neighbour: recompute with g empty
         uint32_t gm = grid6(c);
-        uint32_t n = P.nb[c] & ~dir_bit_to(c, g, gm);
+        uint32_t n = nbr_bits(P.occ, c) & ~dir_bit_to(c, g, gm);
         s = gm & ~n & (rotl6(n) ^ rotr6(n));
     }
     return s;
@@ -464,7 +479,7 @@ HW_INL int gen_step(const Pos& P, int c, uint16_t* out) {
 HW_INL int gen_hopper(const Pos& P, int c, uint16_t* out) {
     int n = 0;
     uint32_t gm = grid6(c);
-    uint32_t m = P.nb[c];
+    uint32_t m = nbo(P, c);
     for (int d = 0; d < 6; d++) {
         if (!((m >> d) & 1u)) continue;
         int p = step(c, d);
@@ -561,14 +576,14 @@ HW_INL int gen_ladybug(const Pos& P, int c, uint16_t* out, uint32_t* got) {
     int n = 0;
     uint32_t g0 = grid6(c);
     uint32_t nh0 = nbr_heights(P, c, g0);
-    uint32_t o0 = P.nb[c];
+    uint32_t o0 = nbo(P, c);
     int hc = P.hgt(c);
     for (int d1 = 0; d1 < 6; d1++) {
         if (!((o0 >> d1) & 1u)) continue;
         int p1 = step(c, d1);
         if (gate_high(nh0, d1, max(hc - 1, hof(nh0, d1)))) continue;
         uint32_t nh1 = nbr_heights(P, p1, grid6(p1));
-        uint32_t o1 = P.nb[p1];
+        uint32_t o1 = nbo(P, p1);
         int hp1 = P.hgt(p1);
         for (int d2 = 0; d2 < 6; d2++) {
             if (!((o1 >> d2) & 1u)) continue;
@@ -577,7 +592,7 @@ HW_INL int gen_ladybug(const Pos& P, int c, uint16_t* out, uint32_t* got) {
             if (gate_high(nh1, d2, max(hp1, hof(nh1, d2)))) continue;
             uint32_t g2 = grid6(p2);
             uint32_t nh2 = nbr_heights(P, p2, g2);
-            uint32_t o2 = P.nb[p2];
+            uint32_t o2 = nbo(P, p2);
             int mh3 = P.hgt(p2);
             for (int d3 = 0; d3 < 6; d3++) {
                 if (!((g2 >> d3) & 1u) || ((o2 >> d3) & 1u)) continue;
@@ -599,7 +614,7 @@ HW_INL int gen_ladybug(const Pos& P, int c, uint16_t* out, uint32_t* got) {
 HW_INL int gen_mosquito(const Pos& P, int c, uint16_t* out, uint32_t* tmpset, uint32_t* unionset) {
     if (P.hgt(c) > 1) return gen_beetle(P, c, out);
     uint32_t gm = grid6(c);
-    uint32_t om = P.nb[c];
+    uint32_t om = nbo(P, c);
     uint32_t has = 0;
     for (int d = 0; d < 6; d++)
         if ((om >> d) & 1u) {
@@ -637,7 +652,7 @@ HW_INL int gen_throws(const Pos& P, int a, uint16_t* from, uint16_t* to, uint8_t
     uint32_t ga = grid6(a);
     uint32_t nha = nbr_heights(P, a, ga);
     int ph = P.hgt(a);
-    uint32_t oa = P.nb[a];
+    uint32_t oa = nbo(P, a);
     for (int dt = 0; dt < 6; dt++) {
         if (!((oa >> dt) & 1u)) continue;
         int t = step(a, dt);
@@ -664,7 +679,7 @@ HW_INL int gen_throws(const Pos& P, int a, uint16_t* from, uint16_t* to, uint8_t
 }
 
 __device__ __forceinline__ bool touches_top_pillbug(const Pos& P, int c) {
-    uint32_t m = P.nb[c];
+    uint32_t m = nbo(P, c);
     while (m) {
         int d = __ffs(m) - 1;
         m &= m - 1;
