@@ -67,6 +67,9 @@ _SIGS = {
     "hg_fnn_successor_features": [_c_void_p, _c_void_p, _c_i64, _c_void_p, _c_void_p, _c_i64, _c_void_p,
                                   _c_void_p],
     "hg_queen_escape_flags": [_c_void_p, _c_i64, _c_void_p, _c_void_p],
+    "hg_fnn_sigmoid_layernorm": [_c_void_p, _c_void_p, _c_void_p, _c_i64, _c_void_p],
+    "hg_fnn_leaf_heads": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_i64, _c_void_p, ctypes.c_float,
+                          _c_void_p, ctypes.c_float, _c_void_p, _c_void_p, _c_void_p, _c_void_p],
     "hg_random_play_step": [_c_void_p, _c_void_p, _c_void_p, _c_i64, _c_int, _c_int, _c_int, ctypes.c_uint32,
                             _c_void_p, _c_void_p],
     "hg_mcts_select_root_slots": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, ctypes.c_float, _c_i64,
@@ -279,18 +282,54 @@ class HiveGpuExtension:
         return out
 
     def fnn_successor_features_batch(self, states, legal_moves, action_to_root, move_indices,
-                                     num_actions: int) -> torch.Tensor:
+                                     num_actions: int, out: torch.Tensor | None = None) -> torch.Tensor:
+        """`out` (extension): an existing [N, 122] float32 buffer to write into."""
         N = int(num_actions)
         states = _dev(states, "states", torch.uint8, (SIZEOF_HIVE_STATE,), 0)
         legal_moves = _dev(legal_moves, "legal_moves", torch.uint8, (MAX_LEGAL_MOVES, SIZEOF_GPU_MOVE), 0)
         action_to_root = _dev(action_to_root, "action_to_root", torch.int64, (), N)
         move_indices = _dev(move_indices, "move_indices", torch.int64, (), N)
-        feat = torch.empty((N, FNN_FEAT_DIM), dtype=torch.float32, device="cuda")
+        if out is None:
+            feat = torch.empty((N, FNN_FEAT_DIM), dtype=torch.float32, device="cuda")
+        else:
+            feat = _dev(out, "out", torch.float32, (FNN_FEAT_DIM,), N)
         roots = min(states.numel() // SIZEOF_HIVE_STATE, legal_moves.numel() // (MAX_LEGAL_MOVES * SIZEOF_GPU_MOVE))
         _check(self._lib.hg_fnn_successor_features(states.data_ptr(), legal_moves.data_ptr(), roots,
                                                    action_to_root.data_ptr(), move_indices.data_ptr(), N,
                                                    feat.data_ptr(), _stream()), "fnn_successor_features_batch")
         return feat
+
+    # ---- fused FNN leaf evaluation (no reference counterpart; see include/hive_gpu.h)
+    def fnn_sigmoid_layernorm_(self, h: torch.Tensor, gamma: torch.Tensor, beta: torch.Tensor) -> torch.Tensor:
+        """h[rows, 64] <- LayerNorm(sigmoid(h)) in place; returns h."""
+        rows = h.shape[0]
+        h = _dev(h, "h", torch.float32, (64,), rows)
+        gamma = _dev(gamma, "gamma", torch.float32, (), 64)
+        beta = _dev(beta, "beta", torch.float32, (), 64)
+        _check(self._lib.hg_fnn_sigmoid_layernorm(h.data_ptr(), gamma.data_ptr(), beta.data_ptr(), rows, _stream()),
+               "fnn_sigmoid_layernorm_")
+        return h
+
+    def fnn_leaf_heads(self, emb, succ_half, root_half, offsets, num_legal, T: int, value_w, value_b: float,
+                       action_w, action_b: float):
+        """(priors [T, 256], root values [T], child_q [T, 256]) of the leaves."""
+        T = int(T)
+        N = succ_half.shape[0]
+        emb = _dev(emb, "emb", torch.float32, (64,), T + N)
+        succ_half = _dev(succ_half, "succ_half", torch.float32, (64,), N)
+        root_half = _dev(root_half, "root_half", torch.float32, (64,), T)
+        offsets = _dev(offsets, "offsets", torch.int64, (), T)
+        num_legal = _dev(num_legal, "num_legal", torch.int32, (), T)
+        value_w = _dev(value_w, "value_w", torch.float32, (), 64)
+        action_w = _dev(action_w, "action_w", torch.float32, (), 64)
+        priors = torch.empty((T, MAX_LEGAL_MOVES), dtype=torch.float32, device="cuda")
+        child_q = torch.empty((T, MAX_LEGAL_MOVES), dtype=torch.float32, device="cuda")
+        values = torch.empty((T,), dtype=torch.float32, device="cuda")
+        _check(self._lib.hg_fnn_leaf_heads(emb.data_ptr(), succ_half.data_ptr(), root_half.data_ptr(),
+                                           offsets.data_ptr(), num_legal.data_ptr(), T, value_w.data_ptr(),
+                                           float(value_b), action_w.data_ptr(), float(action_b), priors.data_ptr(),
+                                           values.data_ptr(), child_q.data_ptr(), _stream()), "fnn_leaf_heads")
+        return priors, values, child_q
 
     def queen_escape_flags_batch(self, states: torch.Tensor, batch_size: int) -> torch.Tensor:
         B = int(batch_size)

@@ -169,7 +169,49 @@ class FNNMCTSOrchestrator:
                 tree["num_children"], tree["is_terminal"], tree["terminal_value"], tree["node_count"]]
 
     # ---- evaluation (:243-316) -----------------------------------------
+    def _fused_eval_ok(self) -> bool:
+        c = self.net.config
+        return c.hidden_dim == 64 and c.embed_dim == 64 and c.action_hidden == 64
+
     def _eval_states(self, states, legal_moves, num_legal, total, root_features=None):
+        """(priors [total, 256], leaf values [total], child Q [total, 256]).
+
+        The 64-wide presets run the fused path: successor features written
+        straight into the encoder input, fc1 / fc2 / action-tower GEMMs on
+        hipBLASLt, and two kernels for everything else
+        (hg_fnn_sigmoid_layernorm, hg_fnn_leaf_heads).  Other widths run the
+        torch composition of the reference (_eval_states_torch)."""
+        if not self._fused_eval_ok():
+            return self._eval_states_torch(states, legal_moves, num_legal, total, root_features)
+        MAX_L = self._max_legal
+        if root_features is None:
+            root_features = self.ext.extract_fnn_features_batch(states, legal_moves, num_legal, total)
+        if total == 0:
+            empty = torch.zeros(0, MAX_L, dtype=torch.float32, device="cuda")
+            return empty, empty.new_zeros((0,)), empty
+        net = self.net
+        n64 = num_legal.to(torch.int64).clamp(0, MAX_L)
+        ends = torch.cumsum(n64, 0)
+        N = int(ends[-1].item())
+        offsets = ends - n64
+        X = torch.empty((total + N, root_features.shape[1]), dtype=torch.float32, device="cuda")
+        X[:total] = root_features
+        if N > 0:
+            a2r = torch.repeat_interleave(torch.arange(total, device="cuda"), n64, output_size=N)
+            mi = torch.arange(N, device="cuda") - offsets[a2r]
+            self.ext.fnn_successor_features_batch(states, legal_moves, a2r, mi, N, out=X[total:])
+        with torch.no_grad():  # not inference_mode: the caller updates the outputs in place
+            H = torch.addmm(net.fc1.bias, X, net.fc1.weight.t())
+            self.ext.fnn_sigmoid_layernorm_(H, net.ln1.weight, net.ln1.bias)
+            E = torch.addmm(net.fc2.bias, H, net.fc2.weight.t())
+            W = net.action_fc1.weight
+            R = torch.addmm(net.action_fc1.bias, E[:total], W[:, :64].t())
+            S = (E[total:] @ W[:, 64:].t()).contiguous()
+            vb, ab = self._head_biases
+            return self.ext.fnn_leaf_heads(E, S, R, offsets, num_legal, total, net.value_fc.weight.reshape(-1), vb,
+                                           net.action_fc2.weight.reshape(-1), ab)
+
+    def _eval_states_torch(self, states, legal_moves, num_legal, total, root_features=None):
         MAX_L = self._max_legal
         n64 = num_legal.to(torch.int64)
         if root_features is None:
@@ -391,6 +433,7 @@ class FNNMCTSOrchestrator:
         B = states.shape[0]
         MAX_L = self._max_legal
         legal, nl, root_feat = self.ext.generate_legal_moves_and_fnn_features_batch(states, B)
+        self._head_biases = (float(self.net.value_fc.bias.item()), float(self.net.action_fc2.bias.item()))
         n64 = nl.to(torch.int64)
         has_actions = active_mask & (n64 > 0)
         priors, _, child_q = self._eval_states(states, legal, nl, B, root_feat)

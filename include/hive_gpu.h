@@ -94,6 +94,29 @@ int hg_fnn_successor_features(const uint8_t* states, const uint8_t* legal_moves,
                               const int64_t* action_to_root, const int64_t* move_indices, int64_t N, float* features,
                               void* stream);
 
+/* FNN leaf evaluation, fused (restates the torch chain of the reference's
+ * FNNMCTSOrchestrator._eval_states, hive_fnn/fnn_mcts_orchestrator.py:243-316,
+ * over HiveFNN.encode / value_head / score_actions, hive_fnn/fnn_network.py:
+ * 175-220; the reference has no kernel for it).  The GEMMs stay with the
+ * caller (hipBLASLt); these two kernels do everything between them.
+ *
+ * hg_fnn_sigmoid_layernorm: h[rows][64] <- LayerNorm(sigmoid(h)) in place
+ * (eps 1e-5, biased variance, affine gamma/beta[64]). */
+int hg_fnn_sigmoid_layernorm(float* h, const float* gamma, const float* beta, int64_t rows, void* stream);
+
+/* hg_fnn_leaf_heads: per leaf t < T, with emb[T+N][64] (leaf rows first, then
+ * the successor rows of leaf t at T + offsets[t] .. + num_legal[t]),
+ * succ_half[N][64] = successor rows x action_fc1.weight[:, 64:]^T,
+ * root_half[T][64] = leaf rows x action_fc1.weight[:, :64]^T + action_fc1.bias:
+ *   root_values[t]   = tanh(emb[t] . value_w + value_b)
+ *   child_q[t][i]    = -tanh(emb[T+offsets[t]+i] . value_w + value_b)
+ *   logit_i          = action_w . sigmoid(succ_half[offsets[t]+i] + root_half[t]) + action_b
+ *   priors[t][i]     = softmax over i < num_legal[t] of logit_i
+ * priors and child_q are [T][256], zero beyond num_legal[t]. */
+int hg_fnn_leaf_heads(const float* emb, const float* succ_half, const float* root_half, const int64_t* offsets,
+                      const int32_t* num_legal, int64_t T, const float* value_w, float value_b, const float* action_w,
+                      float action_b, float* priors, float* root_values, float* child_q, void* stream);
+
 /* queen_escape_flags_batch -- game_logic.cu:1538-1554.  flags[B] uint8. */
 int hg_queen_escape_flags(const uint8_t* states, int64_t B, uint8_t* flags, void* stream);
 

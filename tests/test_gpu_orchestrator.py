@@ -220,3 +220,28 @@ def test_search_ply_matches_numpy_orchestrator(monkeypatch, sims, mask, max_ply,
     assert np.array_equal(visits, _np(r.slot_visits))
     np.testing.assert_allclose(probs, _np(r.policy), atol=2e-6, rtol=0)
     assert tree_equal(t0, {k: _np(v) for k, v in tree.items()}) == []
+
+
+@pytest.mark.parametrize("mask,max_ply", [(0, 120), (7, 150)])
+def test_fused_leaf_evaluation_matches_torch(mask, max_ply):
+    """hg_fnn_sigmoid_layernorm + hg_fnn_leaf_heads (with the GEMMs on
+    hipBLASLt) against the reference's torch composition over HiveFNN, on
+    the same leaves: priors, values and child Q within fp32 rounding."""
+    import torch
+    from hive_neuralnet_amd import hive_gpu
+    B = 300
+    orch, _, _ = _setup(4, 8, 256, mask, max_ply, 31)
+    ext = orch.ext
+    states, _ = hive_gpu.random_positions(B, mask, max_ply, 77)
+    legal, nl, feat = ext.generate_legal_moves_and_fnn_features_batch(states, B)
+    orch._head_biases = (float(orch.net.value_fc.bias.item()), float(orch.net.action_fc2.bias.item()))
+    p1, v1, q1 = orch._eval_states(states, legal, nl, B, feat)
+    p2, v2, q2 = orch._eval_states_torch(states, legal, nl, B, feat)
+    torch.testing.assert_close(p1, p2, atol=2e-6, rtol=1e-4)
+    torch.testing.assert_close(v1, v2, atol=2e-6, rtol=1e-4)
+    torch.testing.assert_close(q1, q2, atol=2e-6, rtol=1e-4)
+    n = nl.cpu().numpy()
+    pr = p1.cpu().numpy()
+    assert (pr[np.arange(256)[None, :] >= n[:, None]] == 0).all()
+    live = n > 0
+    np.testing.assert_allclose(pr[live].sum(axis=1), 1.0, atol=1e-5)
