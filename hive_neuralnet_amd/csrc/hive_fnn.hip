@@ -5,22 +5,42 @@
 // masks, row lists, successor features, concatenation, fc1, sigmoid,
 // LayerNorm, fc2, value head, action tower over [root | successor]
 // embeddings, scatter into [T, 256] logits, softmax, child-Q scatter.  Here
-// the GEMMs stay with hipBLASLt (torch.addmm) and the rest collapses into
-// two kernels:
+// the whole network runs in one kernel per row kind, with the weights held in
+// LDS and the three layer products on fp32 matrix cores:
 //
-//   k_sigmoid_layernorm  h <- LayerNorm(sigmoid(h)) in place, per 64-wide row
-//                        (fnn_network.py:175-187, eps 1e-5, biased variance);
-//   k_leaf_heads         per leaf: child values tanh(e_succ . wv + bv), action
-//                        logits a2 . sigmoid(S_succ + R_root) + b2 (the action
-//                        tower's first layer split into its successor half S
-//                        and root half R, fnn_network.py:204-220), softmax
-//                        over the leaf's legal slots, priors / child Q
-//                        (= -child value) written as [T, 256] rows with zero
-//                        padding, and the leaf's own value.
+//   k_leaf_mlp<root>   per leaf row: embedding e = fc2(LN(sigmoid(fc1 x))),
+//                      value tanh(value_fc e), and the root half of the
+//                      action tower's first layer r = Wr e + b (Wr =
+//                      action_fc1.weight[:, :64]), kept as [T][64];
+//   k_leaf_mlp<succ>   per successor row: e as above, child value
+//                      tanh(value_fc e), and the action logit
+//                      action_fc2(sigmoid(Ws e + r[leaf])) (Ws =
+//                      action_fc1.weight[:, 64:]), so [root | successor] is
+//                      never materialised;
+//   k_leaf_softmax     per leaf: softmax of its logits over its legal slots,
+//                      priors / child Q (= -child value) as [T][256] rows,
+//                      zero beyond the legal count.
 //
-// Floating point: fp32 throughout with the same operations as the torch
-// path; summation orders differ (GEMM split, reductions), so results agree
-// with the torch path to ~1e-6 relative, not bit for bit.
+// Matrix-core layout (v_mfma_f32_16x16x4f32, D = A.B + C, A 16x4, B 4x16):
+// lane l holds A[l%16][l/16], B[l/16][l%16] and D[4(l/16)+i][l%16] in its
+// four accumulator registers i.  A wave evaluates 16 rows at a time and
+// computes every layer transposed, out^T = W . in^T: A = 16 output units of
+// W, B = the inputs of the 16 rows, so after a layer lane l holds, for row
+// l%16, the 16 units {16t + 4(l/16) + i : t, i < 4} of its output.  Those are
+// exactly the B operands the next layer needs when the K index of step s for
+// lane group g = l/16 is 16(s/4) + 4g + s%4: no transposes, no LDS traffic
+// between layers.  The weights are stored in LDS pre-permuted to that K
+// order ([step][lane][tile] float4 per lane, conflict-free 16-byte reads).
+// The first layer reads the features in their natural order, K index 32g + s
+// for lane group g (a lane loads 32 consecutive features of its row).
+//
+// LayerNorm, value and logit reductions over the 64 units of a row are a
+// sum over the lane's 16 units plus two cross-lane steps (lanes l, l^16,
+// l^32, l^48 share a row).
+//
+// Floating point: fp32 throughout with the reference's operations (eps 1e-5,
+// biased variance); summation orders differ from torch's GEMMs, so results
+// agree with the torch composition to ~1e-6 relative, not bit for bit.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -28,8 +48,208 @@
 
 namespace {
 
-constexpr int kE = 64;  // embedding / hidden width of the FNN presets this kernel serves
-constexpr int kSlots = 256;
+constexpr int kE = 64;       // hidden / embedding / action-tower width served here
+constexpr int kFMax = 128;   // feature rows up to 128 wide (Hive FNN: 122)
+constexpr int kSlots = 256;  // legal-slot rows of priors / child Q
+constexpr int kBlockWaves = 4;
+constexpr int kMaxBlocks = 512;  // 2 resident blocks (67 KB LDS each) on each of 256 CUs
+
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+struct MlpLds {
+    f4 w1[32][64];  // fc1, step s = K index 32g + s
+    f4 w2[16][64];  // fc2, step s = K index 16(s/4) + 4g + s%4
+    f4 w3[16][64];  // action_fc1 root half (root rows) or successor half (successor rows)
+    float vec[7][kE];
+};
+enum { kB1, kLnW, kLnB, kB2, kWv, kWa2, kBa1 };
+
+__device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+// sum over the four lanes l, l^16, l^32, l^48 (one row)
+__device__ __forceinline__ float row_sum(float v) {
+    v += __shfl_xor(v, 16, 64);
+    v += __shfl_xor(v, 32, 64);
+    return v;
+}
+
+__device__ __forceinline__ f4 mfma(float a, float b, f4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ f4 vec4(const MlpLds& L, int which, int t, int g) {
+    return *reinterpret_cast<const f4*>(&L.vec[which][16 * t + 4 * g]);
+}
+
+// X: [rows][F] features (F even, <= 128, 8-byte aligned rows).
+// kRoot: R[rows][64] <- Wr e + b_a1, value[rows] <- tanh(wv . e + bv).
+// !kRoot: row -> leaf = succ_leaf[row]; value[rows] <- tanh(wv . e + bv),
+//         logit[rows] <- wa2 . sigmoid(Ws e + R[leaf]) + ba2.
+template <bool kRoot>
+__global__ __launch_bounds__(256) void k_leaf_mlp(const float* __restrict__ X, int64_t rows, int F,
+                                                  const int64_t* __restrict__ succ_leaf, int64_t T,
+                                                  const float* __restrict__ w1, const float* __restrict__ b1,
+                                                  const float* __restrict__ lnw, const float* __restrict__ lnb,
+                                                  const float* __restrict__ w2, const float* __restrict__ b2,
+                                                  const float* __restrict__ wv, float bv, const float* __restrict__ a1w,
+                                                  const float* __restrict__ a1b, const float* __restrict__ a2w, float ba2,
+                                                  float* __restrict__ R, float* __restrict__ value,
+                                                  float* __restrict__ logit) {
+    __shared__ MlpLds L;
+    // permuted weights into LDS: element i of a [step][lane][tile] array is
+    // unit m = 16 tile + lane%16 and step/lane group dependent K index k
+    float* l1 = reinterpret_cast<float*>(&L.w1[0][0]);
+    for (int i = threadIdx.x; i < 32 * 64 * 4; i += blockDim.x) {
+        const int t = i & 3, l = (i >> 2) & 63, s = i >> 8;
+        const int m = 16 * t + (l & 15), k = 32 * (l >> 4) + s;
+        l1[i] = k < F ? w1[m * F + k] : 0.0f;
+    }
+    float* l2 = reinterpret_cast<float*>(&L.w2[0][0]);
+    float* l3 = reinterpret_cast<float*>(&L.w3[0][0]);
+    for (int i = threadIdx.x; i < 16 * 64 * 4; i += blockDim.x) {
+        const int t = i & 3, l = (i >> 2) & 63, s = i >> 8;
+        const int m = 16 * t + (l & 15), k = 16 * (s >> 2) + 4 * (l >> 4) + (s & 3);
+        l2[i] = w2[m * kE + k];
+        l3[i] = a1w[m * 2 * kE + (kRoot ? 0 : kE) + k];
+    }
+    if (threadIdx.x < kE) {
+        const int u = threadIdx.x;
+        L.vec[kB1][u] = b1[u];
+        L.vec[kLnW][u] = lnw[u];
+        L.vec[kLnB][u] = lnb[u];
+        L.vec[kB2][u] = b2[u];
+        L.vec[kWv][u] = wv[u];
+        L.vec[kWa2][u] = a2w[u];
+        L.vec[kBa1][u] = a1b[u];
+    }
+    __syncthreads();
+
+    const int lane = threadIdx.x & 63, g = lane >> 4;
+    const int64_t ntiles = (rows + 15) >> 4;
+    for (int64_t tile = (int64_t)blockIdx.x * kBlockWaves + (threadIdx.x >> 6); tile < ntiles;
+         tile += (int64_t)gridDim.x * kBlockWaves) {
+        // the weights are re-read from LDS in every tile: hoisted out of the
+        // loop they would take ~400 registers and leave one wave per SIMD
+        __asm__ volatile("" ::: "memory");
+        const int64_t row = tile * 16 + (lane & 15);
+        const bool ok = row < rows;
+        // successor rows: the leaf's root half of the action tower, fetched first
+        f4 rh[4];
+        if constexpr (!kRoot) {
+            int64_t leaf = ok ? succ_leaf[row] : 0;
+            leaf = leaf < 0 ? 0 : (leaf >= T ? T - 1 : leaf);
+#pragma unroll
+            for (int t = 0; t < 4; t++) rh[t] = *reinterpret_cast<const f4*>(R + leaf * kE + 16 * t + 4 * g);
+        }
+        // features 32g .. 32g+31 of this lane's row
+        float x[32];
+        const float* xr = X + (ok ? row : 0) * F + 32 * g;
+#pragma unroll
+        for (int p = 0; p < 16; p++) {
+            float2 v = make_float2(0.0f, 0.0f);
+            if (ok && 32 * g + 2 * p < F) v = *reinterpret_cast<const float2*>(xr + 2 * p);
+            x[2 * p] = v.x;
+            x[2 * p + 1] = v.y;
+        }
+        // fc1
+        f4 acc[4];
+#pragma unroll
+        for (int t = 0; t < 4; t++) acc[t] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int s = 0; s < 32; s++) {
+            const f4 a = L.w1[s][lane];
+            acc[0] = mfma(a.x, x[s], acc[0]);
+            acc[1] = mfma(a.y, x[s], acc[1]);
+            acc[2] = mfma(a.z, x[s], acc[2]);
+            acc[3] = mfma(a.w, x[s], acc[3]);
+        }
+        // sigmoid + LayerNorm over the row's 64 units
+        float sum = 0.0f;
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const f4 b = vec4(L, kB1, t, g);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                acc[t][i] = sigmoidf_(acc[t][i] + b[i]);
+                sum += acc[t][i];
+            }
+        }
+        const float mean = row_sum(sum) / (float)kE;
+        float sq = 0.0f;
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                acc[t][i] -= mean;
+                sq += acc[t][i] * acc[t][i];
+            }
+        const float rstd = 1.0f / sqrtf(row_sum(sq) / (float)kE + 1e-5f);
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const f4 w = vec4(L, kLnW, t, g), b = vec4(L, kLnB, t, g);
+#pragma unroll
+            for (int i = 0; i < 4; i++) acc[t][i] = acc[t][i] * rstd * w[i] + b[i];
+        }
+        // fc2 -> embedding
+        f4 e[4];
+#pragma unroll
+        for (int t = 0; t < 4; t++) e[t] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int s = 0; s < 16; s++) {
+            const f4 a = L.w2[s][lane];
+            const float b = acc[s >> 2][s & 3];
+            e[0] = mfma(a.x, b, e[0]);
+            e[1] = mfma(a.y, b, e[1]);
+            e[2] = mfma(a.z, b, e[2]);
+            e[3] = mfma(a.w, b, e[3]);
+        }
+        float v = 0.0f;
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const f4 b = vec4(L, kB2, t, g), w = vec4(L, kWv, t, g);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                e[t][i] += b[i];
+                v += e[t][i] * w[i];
+            }
+        }
+        v = tanhf(row_sum(v) + bv);
+        // action tower, first layer (root or successor half)
+        f4 h[4];
+#pragma unroll
+        for (int t = 0; t < 4; t++) h[t] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int s = 0; s < 16; s++) {
+            const f4 a = L.w3[s][lane];
+            const float b = e[s >> 2][s & 3];
+            h[0] = mfma(a.x, b, h[0]);
+            h[1] = mfma(a.y, b, h[1]);
+            h[2] = mfma(a.z, b, h[2]);
+            h[3] = mfma(a.w, b, h[3]);
+        }
+        if constexpr (kRoot) {
+            if (ok) {
+#pragma unroll
+                for (int t = 0; t < 4; t++)
+                    *reinterpret_cast<f4*>(R + row * kE + 16 * t + 4 * g) = h[t] + vec4(L, kBa1, t, g);
+                if (g == 0) value[row] = v;
+            }
+        } else {
+            float a = 0.0f;
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                const f4 w = vec4(L, kWa2, t, g);
+#pragma unroll
+                for (int i = 0; i < 4; i++) a += sigmoidf_(h[t][i] + rh[t][i]) * w[i];
+            }
+            a = row_sum(a) + ba2;
+            if (ok && g == 0) {
+                value[row] = v;
+                logit[row] = a;
+            }
+        }
+    }
+}
 
 __device__ __forceinline__ float wave_sum_f(float v) {
 #pragma unroll
@@ -41,110 +261,74 @@ __device__ __forceinline__ float wave_max_f(float v) {
     for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
     return v;
 }
-__device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf(-x)); }
 
-// one 64-lane wave per row, lane = column
-__global__ __launch_bounds__(256) void k_sigmoid_layernorm(float* __restrict__ h, const float* __restrict__ gamma,
-                                                           const float* __restrict__ beta, int64_t rows) {
+// One wave per leaf t: softmax of logit[offsets[t] .. + n) into priors[t],
+// child_q[t][i] = -child value; zero beyond n.
+__global__ __launch_bounds__(256) void k_leaf_softmax(const float* __restrict__ logit, const float* __restrict__ cval,
+                                                      const int64_t* __restrict__ offsets,
+                                                      const int32_t* __restrict__ nlegal, int64_t T,
+                                                      float* __restrict__ priors, float* __restrict__ child_q) {
     const int lane = threadIdx.x & 63;
-    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (row >= rows) return;
-    float* x = h + row * kE;
-    float v = sigmoidf_(x[lane]);
-    float mean = wave_sum_f(v) / (float)kE;
-    float d = v - mean;
-    float var = wave_sum_f(d * d) / (float)kE;
-    x[lane] = d / sqrtf(var + 1e-5f) * gamma[lane] + beta[lane];
-}
-
-// One wave per leaf t.  E: [T + N, 64] embeddings (leaf rows 0..T-1, successor
-// rows T..T+N-1); S: [N, 64] successor halves of the action tower's first
-// layer (no bias); R: [T, 64] root halves with the bias; offsets[t] = first
-// successor row of leaf t, n[t] its legal-slot count.
-__global__ __launch_bounds__(256) void k_leaf_heads(const float* __restrict__ E, const float* __restrict__ S,
-                                                    const float* __restrict__ R, const int64_t* __restrict__ offsets,
-                                                    const int32_t* __restrict__ nlegal, int64_t T,
-                                                    const float* __restrict__ wv, float bv,
-                                                    const float* __restrict__ wa2, float ba2,
-                                                    float* __restrict__ priors, float* __restrict__ root_values,
-                                                    float* __restrict__ child_q) {
-    __shared__ float sR[4][kE], sWv[kE], sWa[kE];
-    const int lane = threadIdx.x & 63, wv_i = threadIdx.x >> 6;
-    const int64_t t = (int64_t)blockIdx.x * 4 + wv_i;
-    if (threadIdx.x < kE) {
-        sWv[threadIdx.x] = wv[threadIdx.x];
-        sWa[threadIdx.x] = wa2[threadIdx.x];
-    }
-    if (t < T) sR[wv_i][lane] = R[t * kE + lane];
-    __syncthreads();
+    const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (t >= T) return;
-    // the leaf's own value
-    float rv = wave_sum_f(E[t * kE + lane] * sWv[lane]);
-    if (lane == 0) root_values[t] = tanhf(rv + bv);
     int n = nlegal[t];
     n = n < 0 ? 0 : (n > kSlots ? kSlots : n);
     const int64_t base = offsets[t];
-    // lane i handles slots i, i + 64, ...: child value and action logit
-    float logit[4], cv[4];
+    float lg[4], cv[4];
 #pragma unroll
     for (int k = 0; k < 4; k++) {
-        int i = lane + 64 * k;
-        logit[k] = -INFINITY;
-        cv[k] = 0.0f;
-        if (i < n) {
-            const float4* e4 = reinterpret_cast<const float4*>(E + (T + base + i) * kE);
-            const float4* s4 = reinterpret_cast<const float4*>(S + (base + i) * kE);
-            float v = 0.0f, a = 0.0f;
-#pragma unroll
-            for (int j = 0; j < kE / 4; j++) {
-                float4 e = e4[j], s = s4[j];
-                v += e.x * sWv[4 * j] + e.y * sWv[4 * j + 1] + e.z * sWv[4 * j + 2] + e.w * sWv[4 * j + 3];
-                a += sigmoidf_(s.x + sR[wv_i][4 * j]) * sWa[4 * j] + sigmoidf_(s.y + sR[wv_i][4 * j + 1]) * sWa[4 * j + 1] +
-                     sigmoidf_(s.z + sR[wv_i][4 * j + 2]) * sWa[4 * j + 2] +
-                     sigmoidf_(s.w + sR[wv_i][4 * j + 3]) * sWa[4 * j + 3];
-            }
-            cv[k] = tanhf(v + bv);
-            logit[k] = a + ba2;
-        }
+        const int i = lane + 64 * k;
+        lg[k] = i < n ? logit[base + i] : -INFINITY;
+        cv[k] = i < n ? cval[base + i] : 0.0f;
     }
-    float m = fmaxf(fmaxf(logit[0], logit[1]), fmaxf(logit[2], logit[3]));
-    m = wave_max_f(m);
+    const float m = wave_max_f(fmaxf(fmaxf(lg[0], lg[1]), fmaxf(lg[2], lg[3])));
     float ex[4], s = 0.0f;
 #pragma unroll
     for (int k = 0; k < 4; k++) {
-        int i = lane + 64 * k;
-        ex[k] = i < n ? expf(logit[k] - m) : 0.0f;
+        ex[k] = lane + 64 * k < n ? expf(lg[k] - m) : 0.0f;
         s += ex[k];
     }
     s = wave_sum_f(s);
 #pragma unroll
     for (int k = 0; k < 4; k++) {
-        int i = lane + 64 * k;
+        const int i = lane + 64 * k;
         priors[t * kSlots + i] = i < n ? ex[k] / s : 0.0f;
         child_q[t * kSlots + i] = i < n ? -cv[k] : 0.0f;
     }
 }
 
 inline int grid_for(int64_t n, int per) { return (int)((n + per - 1) / per); }
+inline int mlp_blocks(int64_t rows) {
+    const int64_t b = ((rows + 15) / 16 + kBlockWaves - 1) / kBlockWaves;
+    return (int)(b < kMaxBlocks ? b : kMaxBlocks);
+}
 
 }  // namespace
 
 extern "C" {
 
-int hg_fnn_sigmoid_layernorm(float* h, const float* gamma, const float* beta, int64_t rows, void* stream) {
-    if (rows <= 0) return 0;
-    hipLaunchKernelGGL(k_sigmoid_layernorm, dim3(grid_for(rows, 4)), dim3(256), 0, (hipStream_t)stream, h, gamma,
-                       beta, rows);
-    return (int)hipGetLastError();
-}
-
-int hg_fnn_leaf_heads(const float* emb, const float* succ_half, const float* root_half, const int64_t* offsets,
-                      const int32_t* num_legal, int64_t T, const float* value_w, float value_b, const float* action_w,
-                      float action_b, float* priors, float* root_values, float* child_q, void* stream) {
-    if (T <= 0) return 0;
-    hipLaunchKernelGGL(k_leaf_heads, dim3(grid_for(T, 4)), dim3(256), 0, (hipStream_t)stream, emb, succ_half,
-                       root_half, offsets, num_legal, T, value_w, value_b, action_w, action_b, priors, root_values,
-                       child_q);
+int hg_fnn_leaf_eval(const float* features, int64_t T, int64_t N, int F, const int64_t* offsets,
+                     const int32_t* num_legal, const int64_t* succ_leaf, const float* fc1_w, const float* fc1_b,
+                     const float* ln_w, const float* ln_b, const float* fc2_w, const float* fc2_b,
+                     const float* value_w, float value_b, const float* action1_w, const float* action1_b,
+                     const float* action2_w, float action2_b, float* workspace, float* priors, float* root_values,
+                     float* child_q, void* stream) {
+    if (T < 0 || N < 0 || F <= 0 || F > kFMax || (F & 1)) return (int)hipErrorInvalidValue;
+    if (((uintptr_t)features & 7) || ((uintptr_t)workspace & 15)) return (int)hipErrorInvalidValue;
+    if (T == 0) return 0;
+    hipStream_t st = (hipStream_t)stream;
+    float* R = workspace;           // [T][64]
+    float* logit = R + T * kE;      // [N]
+    float* cval = logit + N;        // [N]
+    hipLaunchKernelGGL(k_leaf_mlp<true>, dim3(mlp_blocks(T)), dim3(64 * kBlockWaves), 0, st, features, T, F,
+                       nullptr, T, fc1_w, fc1_b, ln_w, ln_b, fc2_w, fc2_b, value_w, value_b, action1_w, action1_b,
+                       action2_w, action2_b, R, root_values, nullptr);
+    if (N > 0)
+        hipLaunchKernelGGL(k_leaf_mlp<false>, dim3(mlp_blocks(N)), dim3(64 * kBlockWaves), 0, st, features + T * F,
+                           N, F, succ_leaf, T, fc1_w, fc1_b, ln_w, ln_b, fc2_w, fc2_b, value_w, value_b, action1_w,
+                           action1_b, action2_w, action2_b, R, cval, logit);
+    hipLaunchKernelGGL(k_leaf_softmax, dim3(grid_for(T, 4)), dim3(256), 0, st, logit, cval, offsets, num_legal, T,
+                       priors, child_q);
     return (int)hipGetLastError();
 }
 

@@ -67,9 +67,10 @@ _SIGS = {
     "hg_fnn_successor_features": [_c_void_p, _c_void_p, _c_i64, _c_void_p, _c_void_p, _c_i64, _c_void_p,
                                   _c_void_p],
     "hg_queen_escape_flags": [_c_void_p, _c_i64, _c_void_p, _c_void_p],
-    "hg_fnn_sigmoid_layernorm": [_c_void_p, _c_void_p, _c_void_p, _c_i64, _c_void_p],
-    "hg_fnn_leaf_heads": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_i64, _c_void_p, ctypes.c_float,
-                          _c_void_p, ctypes.c_float, _c_void_p, _c_void_p, _c_void_p, _c_void_p],
+    "hg_fnn_leaf_eval": [_c_void_p, _c_i64, _c_i64, ctypes.c_int, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+                         _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, ctypes.c_float,
+                         _c_void_p, _c_void_p, _c_void_p, ctypes.c_float, _c_void_p, _c_void_p, _c_void_p,
+                         _c_void_p, _c_void_p],
     "hg_random_play_step": [_c_void_p, _c_void_p, _c_void_p, _c_i64, _c_int, _c_int, _c_int, ctypes.c_uint32,
                             _c_void_p, _c_void_p],
     "hg_mcts_select_root_slots": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, ctypes.c_float, _c_i64,
@@ -300,35 +301,42 @@ class HiveGpuExtension:
         return feat
 
     # ---- fused FNN leaf evaluation (no reference counterpart; see include/hive_gpu.h)
-    def fnn_sigmoid_layernorm_(self, h: torch.Tensor, gamma: torch.Tensor, beta: torch.Tensor) -> torch.Tensor:
-        """h[rows, 64] <- LayerNorm(sigmoid(h)) in place; returns h."""
-        rows = h.shape[0]
-        h = _dev(h, "h", torch.float32, (64,), rows)
-        gamma = _dev(gamma, "gamma", torch.float32, (), 64)
-        beta = _dev(beta, "beta", torch.float32, (), 64)
-        _check(self._lib.hg_fnn_sigmoid_layernorm(h.data_ptr(), gamma.data_ptr(), beta.data_ptr(), rows, _stream()),
-               "fnn_sigmoid_layernorm_")
-        return h
-
-    def fnn_leaf_heads(self, emb, succ_half, root_half, offsets, num_legal, T: int, value_w, value_b: float,
-                       action_w, action_b: float):
-        """(priors [T, 256], root values [T], child_q [T, 256]) of the leaves."""
+    def fnn_leaf_eval(self, features, T: int, offsets, num_legal, succ_leaf, net, head_biases=None):
+        """(priors [T, 256], leaf values [T], child Q [T, 256]) from the feature
+        rows [T + N, F] (leaf rows, then successor rows grouped by leaf) through
+        the 64-wide HiveFNN `net` (fc1, ln1, fc2, value_fc, action_fc1, action_fc2).
+        `head_biases` = (value_fc.bias, action_fc2.bias) as floats, when the
+        caller already holds them on the host (saves two device reads)."""
         T = int(T)
-        N = succ_half.shape[0]
-        emb = _dev(emb, "emb", torch.float32, (64,), T + N)
-        succ_half = _dev(succ_half, "succ_half", torch.float32, (64,), N)
-        root_half = _dev(root_half, "root_half", torch.float32, (64,), T)
+        F = features.shape[1]
+        N = features.shape[0] - T
+        features = _dev(features, "features", torch.float32, (F,), T + N)
         offsets = _dev(offsets, "offsets", torch.int64, (), T)
         num_legal = _dev(num_legal, "num_legal", torch.int32, (), T)
-        value_w = _dev(value_w, "value_w", torch.float32, (), 64)
-        action_w = _dev(action_w, "action_w", torch.float32, (), 64)
+        succ_leaf = _dev(succ_leaf, "succ_leaf", torch.int64, (), N)
+        spec = ((net.fc1.weight, "fc1.weight", 64 * F), (net.fc1.bias, "fc1.bias", 64),
+                (net.ln1.weight, "ln1.weight", 64), (net.ln1.bias, "ln1.bias", 64),
+                (net.fc2.weight, "fc2.weight", 64 * 64), (net.fc2.bias, "fc2.bias", 64),
+                (net.value_fc.weight, "value_fc.weight", 64), (net.action_fc1.weight, "action_fc1.weight", 64 * 128),
+                (net.action_fc1.bias, "action_fc1.bias", 64), (net.action_fc2.weight, "action_fc2.weight", 64))
+        w = []
+        for t, name, n in spec:
+            if t.numel() != n:
+                raise ValueError(f"fnn_leaf_eval serves 64-wide networks: {name} has {t.numel()} values, need {n}")
+            w.append(_dev(t.detach().reshape(-1), name, torch.float32, (), n))
+        if head_biases is None:
+            head_biases = (net.value_fc.bias.detach().reshape(-1)[0].item(),
+                           net.action_fc2.bias.detach().reshape(-1)[0].item())
+        vb, ab = float(head_biases[0]), float(head_biases[1])
+        ws = torch.empty((T * 64 + 2 * N,), dtype=torch.float32, device="cuda")
         priors = torch.empty((T, MAX_LEGAL_MOVES), dtype=torch.float32, device="cuda")
         child_q = torch.empty((T, MAX_LEGAL_MOVES), dtype=torch.float32, device="cuda")
         values = torch.empty((T,), dtype=torch.float32, device="cuda")
-        _check(self._lib.hg_fnn_leaf_heads(emb.data_ptr(), succ_half.data_ptr(), root_half.data_ptr(),
-                                           offsets.data_ptr(), num_legal.data_ptr(), T, value_w.data_ptr(),
-                                           float(value_b), action_w.data_ptr(), float(action_b), priors.data_ptr(),
-                                           values.data_ptr(), child_q.data_ptr(), _stream()), "fnn_leaf_heads")
+        _check(self._lib.hg_fnn_leaf_eval(
+            features.data_ptr(), T, N, F, offsets.data_ptr(), num_legal.data_ptr(), succ_leaf.data_ptr(),
+            w[0].data_ptr(), w[1].data_ptr(), w[2].data_ptr(), w[3].data_ptr(), w[4].data_ptr(), w[5].data_ptr(),
+            w[6].data_ptr(), vb, w[7].data_ptr(), w[8].data_ptr(), w[9].data_ptr(), ab, ws.data_ptr(),
+            priors.data_ptr(), values.data_ptr(), child_q.data_ptr(), _stream()), "fnn_leaf_eval")
         return priors, values, child_q
 
     def queen_escape_flags_batch(self, states: torch.Tensor, batch_size: int) -> torch.Tensor:

@@ -118,6 +118,8 @@ class FNNMCTSOrchestrator:
         self.counters: dict[str, torch.Tensor] | None = None
         self.keep_last_leaves = False
         self.last_leaves: torch.Tensor | None = None
+        # (value_fc.bias, action_fc2.bias) on the host, read once per search ply
+        self._head_biases: tuple[float, float] | None = None
 
     def enable_counters(self) -> None:
         self.counters = {k: torch.zeros((), dtype=torch.int64, device="cuda")
@@ -177,10 +179,10 @@ class FNNMCTSOrchestrator:
         """(priors [total, 256], leaf values [total], child Q [total, 256]).
 
         The 64-wide presets run the fused path: successor features written
-        straight into the encoder input, fc1 / fc2 / action-tower GEMMs on
-        hipBLASLt, and two kernels for everything else
-        (hg_fnn_sigmoid_layernorm, hg_fnn_leaf_heads).  Other widths run the
-        torch composition of the reference (_eval_states_torch)."""
+        straight into the network input, then hg_fnn_leaf_eval (the whole
+        network and the heads on matrix cores, softmax and the [T, 256]
+        scatter).  Other widths run the torch composition of the reference
+        (_eval_states_torch)."""
         if not self._fused_eval_ok():
             return self._eval_states_torch(states, legal_moves, num_legal, total, root_features)
         MAX_L = self._max_legal
@@ -189,7 +191,6 @@ class FNNMCTSOrchestrator:
         if total == 0:
             empty = torch.zeros(0, MAX_L, dtype=torch.float32, device="cuda")
             return empty, empty.new_zeros((0,)), empty
-        net = self.net
         n64 = num_legal.to(torch.int64).clamp(0, MAX_L)
         ends = torch.cumsum(n64, 0)
         N = int(ends[-1].item())
@@ -200,16 +201,9 @@ class FNNMCTSOrchestrator:
             a2r = torch.repeat_interleave(torch.arange(total, device="cuda"), n64, output_size=N)
             mi = torch.arange(N, device="cuda") - offsets[a2r]
             self.ext.fnn_successor_features_batch(states, legal_moves, a2r, mi, N, out=X[total:])
-        with torch.no_grad():  # not inference_mode: the caller updates the outputs in place
-            H = torch.addmm(net.fc1.bias, X, net.fc1.weight.t())
-            self.ext.fnn_sigmoid_layernorm_(H, net.ln1.weight, net.ln1.bias)
-            E = torch.addmm(net.fc2.bias, H, net.fc2.weight.t())
-            W = net.action_fc1.weight
-            R = torch.addmm(net.action_fc1.bias, E[:total], W[:, :64].t())
-            S = (E[total:] @ W[:, 64:].t()).contiguous()
-            vb, ab = self._head_biases
-            return self.ext.fnn_leaf_heads(E, S, R, offsets, num_legal, total, net.value_fc.weight.reshape(-1), vb,
-                                           net.action_fc2.weight.reshape(-1), ab)
+        else:
+            a2r = torch.empty((0,), dtype=torch.int64, device="cuda")
+        return self.ext.fnn_leaf_eval(X, total, offsets, num_legal, a2r, self.net, self._head_biases)
 
     def _eval_states_torch(self, states, legal_moves, num_legal, total, root_features=None):
         MAX_L = self._max_legal

@@ -94,28 +94,34 @@ int hg_fnn_successor_features(const uint8_t* states, const uint8_t* legal_moves,
                               const int64_t* action_to_root, const int64_t* move_indices, int64_t N, float* features,
                               void* stream);
 
-/* FNN leaf evaluation, fused (restates the torch chain of the reference's
- * FNNMCTSOrchestrator._eval_states, hive_fnn/fnn_mcts_orchestrator.py:243-316,
- * over HiveFNN.encode / value_head / score_actions, hive_fnn/fnn_network.py:
- * 175-220; the reference has no kernel for it).  The GEMMs stay with the
- * caller (hipBLASLt); these two kernels do everything between them.
+/* hg_fnn_leaf_eval -- FNN leaf evaluation, fused (restates the torch chain of
+ * the reference's FNNMCTSOrchestrator._eval_states,
+ * hive_fnn/fnn_mcts_orchestrator.py:243-316, over HiveFNN.encode / value_head /
+ * score_actions, hive_fnn/fnn_network.py:175-220; the reference has no kernel
+ * for it).  Network widths: hidden = embedding = action tower = 64, F <= 128
+ * features (even).  Weights are the nn.Linear / nn.LayerNorm tensors as
+ * stored (row-major [out][in]).
  *
- * hg_fnn_sigmoid_layernorm: h[rows][64] <- LayerNorm(sigmoid(h)) in place
- * (eps 1e-5, biased variance, affine gamma/beta[64]). */
-int hg_fnn_sigmoid_layernorm(float* h, const float* gamma, const float* beta, int64_t rows, void* stream);
-
-/* hg_fnn_leaf_heads: per leaf t < T, with emb[T+N][64] (leaf rows first, then
- * the successor rows of leaf t at T + offsets[t] .. + num_legal[t]),
- * succ_half[N][64] = successor rows x action_fc1.weight[:, 64:]^T,
- * root_half[T][64] = leaf rows x action_fc1.weight[:, :64]^T + action_fc1.bias:
- *   root_values[t]   = tanh(emb[t] . value_w + value_b)
- *   child_q[t][i]    = -tanh(emb[T+offsets[t]+i] . value_w + value_b)
- *   logit_i          = action_w . sigmoid(succ_half[offsets[t]+i] + root_half[t]) + action_b
- *   priors[t][i]     = softmax over i < num_legal[t] of logit_i
- * priors and child_q are [T][256], zero beyond num_legal[t]. */
-int hg_fnn_leaf_heads(const float* emb, const float* succ_half, const float* root_half, const int64_t* offsets,
-                      const int32_t* num_legal, int64_t T, const float* value_w, float value_b, const float* action_w,
-                      float action_b, float* priors, float* root_values, float* child_q, void* stream);
+ * features[T + N][F]: the T leaf rows, then the successor rows; the
+ * successor rows of leaf t are T + offsets[t] .. + num_legal[t], and
+ * succ_leaf[i] = t for successor row i (i < N).  With
+ *   e(x)          = fc2(LayerNorm(sigmoid(fc1 x)))     (eps 1e-5)
+ *   root_values[t] = tanh(value_w . e(leaf t) + value_b)
+ *   child_q[t][i]  = -tanh(value_w . e(successor i of t) + value_b)
+ *   logit_i        = action2_w . sigmoid(action1_w [e(leaf t) | e(succ i)]
+ *                                        + action1_b) + action2_b
+ *   priors[t][i]   = softmax over i < num_legal[t] of logit_i
+ * priors and child_q are [T][256], zero beyond num_legal[t].
+ * workspace: T * 64 + 2 * N floats, 16-byte aligned (the root half of the
+ * action tower per leaf, then logits and child values per successor row);
+ * features must be 8-byte aligned.  Returns hipErrorInvalidValue for other
+ * shapes or alignments. */
+int hg_fnn_leaf_eval(const float* features, int64_t T, int64_t N, int F, const int64_t* offsets,
+                     const int32_t* num_legal, const int64_t* succ_leaf, const float* fc1_w, const float* fc1_b,
+                     const float* ln_w, const float* ln_b, const float* fc2_w, const float* fc2_b,
+                     const float* value_w, float value_b, const float* action1_w, const float* action1_b,
+                     const float* action2_w, float action2_b, float* workspace, float* priors, float* root_values,
+                     float* child_q, void* stream);
 
 /* queen_escape_flags_batch -- game_logic.cu:1538-1554.  flags[B] uint8. */
 int hg_queen_escape_flags(const uint8_t* states, int64_t B, uint8_t* flags, void* stream);

@@ -224,9 +224,9 @@ def test_search_ply_matches_numpy_orchestrator(monkeypatch, sims, mask, max_ply,
 
 @pytest.mark.parametrize("mask,max_ply", [(0, 120), (7, 150)])
 def test_fused_leaf_evaluation_matches_torch(mask, max_ply):
-    """hg_fnn_sigmoid_layernorm + hg_fnn_leaf_heads (with the GEMMs on
-    hipBLASLt) against the reference's torch composition over HiveFNN, on
-    the same leaves: priors, values and child Q within fp32 rounding."""
+    """hg_fnn_leaf_eval (network and heads on fp32 matrix cores) against the
+    reference's torch composition over HiveFNN, on the same leaves: priors,
+    values and child Q within fp32 rounding."""
     import torch
     from hive_neuralnet_amd import hive_gpu
     B = 300
