@@ -475,6 +475,46 @@ __global__ void k_root_noise(Tree T, const float* __restrict__ noise, const int3
 
 inline int finish() { return (int)hipGetLastError(); }
 
+
+// Hard rebase of the games with reset[g] != 0 (_reroot_tree,
+// fnn_mcts_orchestrator.py:1122-1142): the reference refills all max_nodes
+// entries of the game's rows; nodes at or beyond node_count[g] have never
+// been written since the game's last reset (expansion hands out ids below
+// node_count only), so refilling the used prefix [0, node_count) gives the
+// same arrays.  grid (x, B): the x blocks of game g stride over its prefix.
+// node_count / root_node are reset by k_reset_counts after this kernel.
+__global__ __launch_bounds__(256) void k_reset_nodes(Tree T, const int8_t* __restrict__ reset, int64_t B) {
+    const int64_t g = blockIdx.y;
+    if (g >= B || !reset[g]) return;
+    int64_t cnt = T.cnt[g];
+    cnt = cnt < 0 ? 0 : (cnt > T.M ? T.M : cnt);
+    const int64_t base = g * T.M;
+    for (int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; j < cnt; j += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t n = base + j;
+        T.vc[n] = 0;
+        T.tv[n] = 0.0f;
+        T.pr[n] = 0.0f;
+        T.pa[n] = -1;
+        T.ai[n] = -1;
+        T.fc[n] = -1;
+        T.nc[n] = 0;
+        T.it[n] = 0;
+        T.tval[n] = 0.0f;
+        T.ciq[n] = 0.0f;
+        uint8_t* mb = T.mb + n * 6;
+#pragma unroll
+        for (int b = 0; b < 6; b++) mb[b] = 0;
+    }
+}
+
+__global__ void k_reset_counts(int32_t* __restrict__ cnt, int32_t* __restrict__ root_node,
+                               const int8_t* __restrict__ reset, int64_t B) {
+    const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (g < B && reset[g]) {
+        cnt[g] = 1;
+        root_node[g] = 0;
+    }
+}
 }  // namespace
 
 extern "C" {
@@ -543,6 +583,16 @@ int hg_mcts_root_noise(const hg_tree* tree, const float* noise, const int32_t* r
     if (B <= 0) return 0;
     hipLaunchKernelGGL(k_root_noise, dim3((unsigned)((B + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
                        to_tree(tree), noise, root_nodes, max_children_pad, dir_eps, root_policy_temp, B);
+    return finish();
+}
+
+int hg_mcts_reset_trees(const hg_tree* tree, const int8_t* reset, int32_t* root_node, int64_t B, void* stream) {
+    if (B <= 0) return 0;
+    if (B > 65535) return (int)hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_reset_nodes, dim3(64, (unsigned)B), dim3(256), 0, (hipStream_t)stream, to_tree(tree), reset,
+                       B);
+    hipLaunchKernelGGL(k_reset_counts, dim3((unsigned)((B + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                       tree->node_count, root_node, reset, B);
     return finish();
 }
 

@@ -87,6 +87,7 @@ _SIGS = {
                                       _c_void_p],
     "hg_mcts_root_noise": [_c_void_p, _c_void_p, _c_void_p, _c_int, ctypes.c_float, ctypes.c_float, _c_i64,
                            _c_void_p],
+    "hg_mcts_reset_trees": [_c_void_p, _c_void_p, _c_void_p, _c_i64, _c_void_p],
 }
 
 
@@ -481,6 +482,19 @@ def _mcts_methods():
         _check(self._lib.hg_mcts_root_noise(ctypes.byref(tree), noise.data_ptr(), root_nodes.data_ptr(), pad,
                                             float(dir_eps), float(root_policy_temp), B, _stream()),
                "mcts_apply_root_noise")
+
+    def mcts_reset_trees(self, vc, tv, pr, pa, vq, mb, ai, fc, nc, it, tv2, cnt, child_init_q, reset, root_node,
+                         B, max_nodes):
+        """Hard rebase (_reroot_tree, fnn_mcts_orchestrator.py:1122-1142) of
+        the games with reset[g] (bool or int8 [B]); extension entry point."""
+        B, M = int(B), int(max_nodes)
+        tree = _tree_struct((vc, tv, pr, pa, vq, mb, ai, fc, nc, it, tv2, cnt), child_init_q, B, M)
+        if reset.dtype == torch.bool:
+            reset = reset.view(torch.int8)
+        _dev(reset, "reset", torch.int8, (), B)
+        _dev(root_node, "root_node", torch.int32, (), B)
+        _check(self._lib.hg_mcts_reset_trees(ctypes.byref(tree), reset.data_ptr(), root_node.data_ptr(), B,
+                                             _stream()), "mcts_reset_trees")
 
     return {k: v for k, v in locals().items() if k.startswith("mcts_")}
 

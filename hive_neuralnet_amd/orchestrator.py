@@ -155,15 +155,11 @@ class FNNMCTSOrchestrator:
             "child_init_q": z(torch.float32),
         }
 
-    def _reset_rows(self, tree: dict, rows: torch.Tensor) -> None:  # _reroot_tree rebase, :1122-1142
-        if rows.numel() == 0:
-            return
-        for k, fill in (("visit_count", 0), ("total_value", 0), ("prior", 0), ("parent_idx", -1),
-                        ("move_bytes", 0), ("action_idx", -1), ("first_child", -1), ("num_children", 0),
-                        ("is_terminal", 0), ("terminal_value", 0), ("child_init_q", 0)):
-            tree[k][rows] = fill
-        tree["node_count"][rows] = 1
-        tree["root_node"][rows] = 0
+    def _reset_games(self, tree: dict, games: torch.Tensor) -> None:  # _reroot_tree rebase, :1122-1142
+        """Hard rebase of the games flagged in `games` (bool [B])."""
+        B = games.shape[0]
+        self.ext.mcts_reset_trees(*self._tree_args(tree), tree["child_init_q"], games.contiguous(), tree["root_node"],
+                                  B, self._max_nodes)
 
     def _tree_args(self, tree: dict) -> list:
         return [tree["visit_count"], tree["total_value"], tree["prior"], tree["parent_idx"],
@@ -513,7 +509,7 @@ class FNNMCTSOrchestrator:
         fc = tree["first_child"][torch.arange(B, device="cuda"), tree["root_node"]]
         moved = ply.has_actions & (fc >= 0)
         if self.config.rebase_tree_each_move:
-            self._reset_rows(tree, torch.nonzero(moved, as_tuple=False).squeeze(1))
+            self._reset_games(tree, moved)
             return
         # keep the chosen child's subtree (fnn_mcts_orchestrator.py:1143-1153)
         new_roots = torch.where(moved, (fc + ply.chosen_slot.to(torch.int32)).to(torch.int32), tree["root_node"])

@@ -166,6 +166,16 @@ typedef struct hg_tree {
     int64_t max_nodes;
 } hg_tree;
 
+/* Hard tree rebase of FNNMCTSOrchestrator._reroot_tree
+ * (hive_fnn/fnn_mcts_orchestrator.py:1122-1142, rebase_tree_each_move): for
+ * each game g with reset[g] != 0, every node of the game's rows returns to
+ * its initial fill (visit/value/prior/children/terminal/child_init_q 0,
+ * parent/action/first_child -1, move bytes 0; virtual_q_penalty untouched,
+ * as in the reference), node_count[g] = 1, root_node[g] = 0.  Only the used
+ * prefix [0, node_count[g]) is written: the nodes beyond it still hold the
+ * initial fill.  B <= 65535. */
+int hg_mcts_reset_trees(const hg_tree* tree, const int8_t* reset, int32_t* root_node, int64_t B, void* stream);
+
 /* mcts_select_with_root_slots_batch -- game_logic.cu:1134-1175
  * (mcts_select_with_root_slots_kernel, mcts_tree.cuh:811-955).
  * T = W * num_candidates * B simulations, sim = (w*C + c)*B + game.

@@ -245,3 +245,28 @@ def test_fused_leaf_evaluation_matches_torch(mask, max_ply):
     assert (pr[np.arange(256)[None, :] >= n[:, None]] == 0).all()
     live = n > 0
     np.testing.assert_allclose(pr[live].sum(axis=1), 1.0, atol=1e-5)
+
+
+@pytest.mark.parametrize("M", [4096, 600], ids=["roomy", "pool-exhausted"])
+def test_reset_trees_equals_full_refill(M):
+    """hg_mcts_reset_trees (used prefix only) against the reference's hard
+    rebase, which refills every node of the reset games' rows
+    (fnn_mcts_orchestrator.py:1122-1142), on trees left by a real search ply."""
+    import torch
+    B = 8
+    orch, states, tree = _setup(B, 64, M, 7, 40, 13)
+    active = torch.ones((B,), dtype=torch.bool, device="cuda")
+    orch.search_ply(states, tree, active)
+    cnt = _np(tree["node_count"])
+    assert (cnt > 1).all() and cnt.max() <= M
+    reset = torch.tensor([1, 0, 1, 1, 0, 1, 0, 1], dtype=torch.bool, device="cuda")
+    rows = torch.nonzero(reset).squeeze(1)
+    expect = {k: v.clone() for k, v in tree.items()}
+    for k, fill in (("visit_count", 0), ("total_value", 0), ("prior", 0), ("parent_idx", -1), ("move_bytes", 0),
+                    ("action_idx", -1), ("first_child", -1), ("num_children", 0), ("is_terminal", 0),
+                    ("terminal_value", 0), ("child_init_q", 0)):
+        expect[k][rows] = fill
+    expect["node_count"][rows] = 1
+    expect["root_node"][rows] = 0
+    orch._reset_games(tree, reset)
+    assert tree_equal({k: _np(v) for k, v in expect.items()}, {k: _np(v) for k, v in tree.items()}) == []
