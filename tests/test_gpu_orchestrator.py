@@ -246,6 +246,38 @@ def test_fused_leaf_evaluation_matches_torch(mask, max_ply):
     live = n > 0
     np.testing.assert_allclose(pr[live].sum(axis=1), 1.0, atol=1e-5)
 
+    # the fused fp32 outputs against the network restated in float64 numpy
+    # (fnn_network.py:175-220 over the same features): 1e-5 relative, with an
+    # absolute floor of 1e-7 for outputs that round to ~0
+    a2r = np.repeat(np.arange(B), n).astype(np.int64)
+    mi = np.concatenate([np.arange(k) for k in n]).astype(np.int64)
+    succ = ext.fnn_successor_features_batch(states, legal, torch.from_numpy(a2r).cuda(), torch.from_numpy(mi).cuda(),
+                                            len(a2r))
+    W = {k: v.detach().double().cpu().numpy() for k, v in orch.net.state_dict().items()}
+
+    def enc(x):
+        h = 1 / (1 + np.exp(-(x @ W["fc1.weight"].T + W["fc1.bias"])))
+        h = (h - h.mean(1, keepdims=True)) / np.sqrt(h.var(1, keepdims=True) + 1e-5)
+        return (h * W["ln1.weight"] + W["ln1.bias"]) @ W["fc2.weight"].T + W["fc2.bias"]
+
+    er, es = enc(_np(feat).astype(np.float64)), enc(_np(succ).astype(np.float64))
+    val = lambda e: np.tanh(e @ W["value_fc.weight"].T + W["value_fc.bias"])[:, 0]  # noqa: E731
+    z = 1 / (1 + np.exp(-(np.concatenate([er[a2r], es], 1) @ W["action_fc1.weight"].T + W["action_fc1.bias"])))
+    logit = (z @ W["action_fc2.weight"].T + W["action_fc2.bias"])[:, 0]
+    want_p = np.zeros((B, 256))
+    want_q = np.zeros((B, 256))
+    cv = -val(es)
+    offs = np.concatenate([[0], np.cumsum(n)])
+    for t in range(B):
+        s = slice(int(offs[t]), int(offs[t + 1]))
+        if n[t] > 0:
+            x = np.exp(logit[s] - logit[s].max())
+            want_p[t, :n[t]] = x / x.sum()
+            want_q[t, :n[t]] = cv[s]
+    np.testing.assert_allclose(_np(v1), val(er), rtol=1e-5, atol=1e-7)
+    np.testing.assert_allclose(pr, want_p, rtol=1e-5, atol=1e-7)
+    np.testing.assert_allclose(_np(q1), want_q, rtol=1e-5, atol=1e-7)
+
 
 @pytest.mark.parametrize("M", [4096, 600], ids=["roomy", "pool-exhausted"])
 def test_reset_trees_equals_full_refill(M):
