@@ -120,7 +120,7 @@ __global__ __launch_bounds__(64) void k_actions(const uint8_t* __restrict__ stat
 }
 
 // a zero state and move for rows that reference no valid (root, move)
-__device__ const uint8_t kZeroRow[kStateBytes] = {};
+__device__ __attribute__((aligned(16))) const uint8_t kZeroRow[kStateBytes] = {};
 
 // fnn_successor_features_kernel (game_logic.cu:182-229): one lane group per (root, move).
 __global__ __launch_bounds__(64) void k_successor_features(const uint8_t* __restrict__ states,

@@ -239,60 +239,108 @@ __device__ __forceinline__ uint32_t grp_or(uint32_t v) {
 }
 
 // ---------------------------------------------------------------- state load
+// Four cells' bytes (height in bits 5-7, clamped to 7; top piece in bits 0-4
+// when the stack is non-empty) from their heights and level-0 bytes; bit k of
+// *stacked is set for cell c0 + k when its top is above level 0.
+__device__ __forceinline__ uint32_t pack_cells4(uint32_t hts, uint32_t lv0, int c0, uint32_t& stacked) {
+    uint32_t packed = 0;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        int hh = (int)((hts >> (8 * k)) & 0xFFu);
+        if (c0 + k >= kCells) hh = 0;
+        int h7 = hh > 7 ? 7 : hh;
+        if (hh > 1) stacked |= 1u << k;
+        packed |= (uint32_t)((h7 << 5) | (h7 ? (int)((lv0 >> (8 * k)) & 31u) : 0)) << (8 * k);
+    }
+    return packed;
+}
+
 // Heights, top bytes, bitboards and metadata of the state row S into P.
-// Lane l handles cells 4j .. 4j+3 (j = l, l + 32, ...): one aligned dword
-// of level-0 bytes and the two aligned dwords holding their heights (which
-// start at the odd offset 2645); the top byte of a stack (height > 1) is a
-// second, rare, dependent load.
+// Lane l of the group takes the 16-cell chunks l and (l < 2) 32 + l: the
+// chunk's level-0 bytes (one 16-byte load) and its heights, which start at
+// the odd offset 2645 (a 16-byte and a 4-byte load, realigned in registers).
+// Every load of the position is issued before the first is used, so the
+// whole row costs one memory round trip; the top byte of a stack (height > 1)
+// is a second, rare, dependent load.
 HW_INL void load_position(Pos& P, const uint8_t* __restrict__ S, int lane) {
     const int l = gl(lane);
-    const uint32_t* S32 = reinterpret_cast<const uint32_t*>(S);
-    uint32_t* cell32 = reinterpret_cast<uint32_t*>(P.cell);
-    for (int j = l; j < 136; j += kW) {
-        uint32_t packed = 0;
-        if (j < 133) {
-            uint32_t lv0 = S32[j];
-            uint32_t h0 = S32[(OFF_HEIGHT - 1) / 4 + j], h1 = S32[(OFF_HEIGHT - 1) / 4 + j + 1];
-            uint32_t hts = __builtin_amdgcn_alignbyte(h1, h0, 1);  // bytes 2645+4j .. 2648+4j
-#pragma unroll
-            for (int k = 0; k < 4; k++) {
-                int c = 4 * j + k;
-                int hh = (int)((hts >> (8 * k)) & 0xFFu);
-                int t = (int)((lv0 >> (8 * k)) & 0xFFu);
-                if (c >= kCells) hh = 0;
-                if (hh > 1) t = S[((hh > 5 ? 5 : hh) - 1) * kCells + c];
-                int h7 = hh > 7 ? 7 : hh;
-                packed |= (uint32_t)((h7 << 5) | (h7 ? (t & 31) : 0)) << (8 * k);
-            }
-        }
-        cell32[j] = packed;
+    const bool two = l < 34 - kW;  // lanes 0, 1 also take chunks 32, 33
+    const int k1 = kW + l;
+    u32x4 lv_a = *reinterpret_cast<const u32x4*>(S + 16 * l);
+    u32x4 ht_a = *reinterpret_cast<const u32x4*>(S + (OFF_HEIGHT - 1) + 16 * l);
+    uint32_t ht_a4 = *reinterpret_cast<const uint32_t*>(S + (OFF_HEIGHT - 1) + 16 * l + 16);
+    u32x4 lv_b = {0u, 0u, 0u, 0u}, ht_b = {0u, 0u, 0u, 0u};
+    uint32_t ht_b4 = 0;
+    if (two) {
+        lv_b = *reinterpret_cast<const u32x4*>(S + 16 * k1);
+        ht_b = *reinterpret_cast<const u32x4*>(S + (OFF_HEIGHT - 1) + 16 * k1);
+        ht_b4 = *reinterpret_cast<const uint32_t*>(S + (OFF_HEIGHT - 1) + 16 * k1 + 16);
     }
     const uint32_t* W = reinterpret_cast<const uint32_t*>(S + OFF_OCC);  // 8-byte aligned
+    uint32_t occ_w = 0, wt_w = 0, bt_w = 0;
     if (l < 18) {
-        P.occ[l + 1] = W[l];
-        P.wt[l + 1] = W[18 + l];
-        P.bt[l + 1] = W[36 + l];
+        occ_w = W[l];
+        wt_w = W[18 + l];
+        bt_w = W[36 + l];
+    }
+    uint32_t m0 = 0, m1 = 0, m2 = 0, m3 = 0, m4 = 0, m5 = 0, m6 = 0;
+    if (l == 24) {
+        const uint32_t* M = reinterpret_cast<const uint32_t*>(S + OFF_QUEEN);
+        m0 = M[0]; m1 = M[1]; m2 = M[2]; m3 = M[3]; m4 = M[4]; m5 = M[5]; m6 = M[6];
+    }
+
+    uint32_t* cell32 = reinterpret_cast<uint32_t*>(P.cell);
+    uint32_t st_a = 0, st_b = 0;
+    {
+        u32x4 o;
+        uint32_t s;
+        s = 0; o[0] = pack_cells4(__builtin_amdgcn_alignbyte(ht_a[1], ht_a[0], 1), lv_a[0], 16 * l + 0, s); st_a |= s;
+        s = 0; o[1] = pack_cells4(__builtin_amdgcn_alignbyte(ht_a[2], ht_a[1], 1), lv_a[1], 16 * l + 4, s); st_a |= s << 4;
+        s = 0; o[2] = pack_cells4(__builtin_amdgcn_alignbyte(ht_a[3], ht_a[2], 1), lv_a[2], 16 * l + 8, s); st_a |= s << 8;
+        s = 0; o[3] = pack_cells4(__builtin_amdgcn_alignbyte(ht_a4, ht_a[3], 1), lv_a[3], 16 * l + 12, s); st_a |= s << 12;
+        *reinterpret_cast<u32x4*>(cell32 + 4 * l) = o;
+    }
+    if (two) {
+        u32x4 o;
+        uint32_t s;
+        s = 0; o[0] = pack_cells4(__builtin_amdgcn_alignbyte(ht_b[1], ht_b[0], 1), lv_b[0], 16 * k1 + 0, s); st_b |= s;
+        s = 0; o[1] = pack_cells4(__builtin_amdgcn_alignbyte(ht_b[2], ht_b[1], 1), lv_b[1], 16 * k1 + 4, s); st_b |= s << 4;
+        s = 0; o[2] = pack_cells4(__builtin_amdgcn_alignbyte(ht_b[3], ht_b[2], 1), lv_b[2], 16 * k1 + 8, s); st_b |= s << 8;
+        s = 0; o[3] = pack_cells4(__builtin_amdgcn_alignbyte(ht_b4, ht_b[3], 1), lv_b[3], 16 * k1 + 12, s); st_b |= s << 12;
+        *reinterpret_cast<u32x4*>(cell32 + 4 * k1) = o;
+    }
+    // stacked tops: level min(h, 5) - 1 of the cell (h is the clamped height)
+    uint32_t st = st_a | (st_b << 16);
+    while (st) {
+        int b = __ffs(st) - 1;
+        st &= st - 1;
+        int c = b < 16 ? 16 * l + b : 16 * k1 + (b - 16);
+        int h = P.cell[c] >> 5;
+        int t = S[((h > 5 ? 5 : h) - 1) * kCells + c];
+        P.cell[c] = (uint8_t)((h << 5) | (t & 31));
+    }
+
+    if (l < 18) {
+        P.occ[l + 1] = occ_w;
+        P.wt[l + 1] = wt_w;
+        P.bt[l + 1] = bt_w;
     } else if (l < 24) {
         int k = l - 18;  // zero the pads: k = 0 -> index 0, k = 1 -> index 19
         uint32_t* dst = k < 2 ? P.occ : k < 4 ? P.wt : P.bt;
         dst[(k & 1) ? 19 : 0] = 0;
     } else if (l == 24) {
-        const uint32_t* M = reinterpret_cast<const uint32_t*>(S + OFF_QUEEN);
-        uint32_t q = M[0];
-        P.queen[0] = (uint16_t)q;
-        P.queen[1] = (uint16_t)(q >> 16);
-        uint32_t h0 = M[1], h1 = M[2], h2 = M[3], h3 = M[4];
+        P.queen[0] = (uint16_t)m0;
+        P.queen[1] = (uint16_t)(m0 >> 16);
         for (int k = 0; k < 4; k++) {
-            P.hand[0][k] = (uint8_t)(h0 >> (8 * k));
-            P.hand[0][4 + k] = (uint8_t)(h1 >> (8 * k));
-            P.hand[1][k] = (uint8_t)(h2 >> (8 * k));
-            P.hand[1][4 + k] = (uint8_t)(h3 >> (8 * k));
+            P.hand[0][k] = (uint8_t)(m1 >> (8 * k));
+            P.hand[0][4 + k] = (uint8_t)(m2 >> (8 * k));
+            P.hand[1][k] = (uint8_t)(m3 >> (8 * k));
+            P.hand[1][4 + k] = (uint8_t)(m4 >> (8 * k));
         }
-        uint32_t t = M[5];  // turn u16, queen_placed u8, result u8
-        P.turn = (uint16_t)t;
-        P.qplaced = (uint8_t)(t >> 16);
-        P.result = (uint8_t)(t >> 24);
-        P.stun = (uint16_t)M[6];
+        P.turn = (uint16_t)m5;  // turn u16, queen_placed u8, result u8
+        P.qplaced = (uint8_t)(m5 >> 16);
+        P.result = (uint8_t)(m5 >> 24);
+        P.stun = (uint16_t)m6;
     }
 }
 

@@ -13,3 +13,10 @@
 // the whole kernel allocate for the call ABI (twice the registers, half the
 // occupancy of the inlined form for k_legal).
 #define HW_INL __device__ __attribute__((always_inline)) inline
+
+// four dwords loaded or stored together (16-byte access, 4-byte alignment)
+#ifdef HW_HOST_EMU
+typedef uint32_t u32x4 __attribute__((vector_size(16), aligned(4)));
+#else
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4), aligned(4)));
+#endif
