@@ -128,6 +128,11 @@ class Oracle(_Engine):
             ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_uint32, _u8p, _i32p, ctypes.c_int]
         lib.or_lockstep_selfplay.argtypes = lib.or_generate_positions.argtypes
         lib.or_philox4x32_10.argtypes = [ctypes.c_uint32, ctypes.c_uint32, _u32p, _u32p]
+        lib.or_batch_root_tactical_probe.argtypes = [
+            _u8p, _u8p, _i32p, _f32p, ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_int, _i64p, _u8p, _u8p,
+            ctypes.c_int]
+        lib.or_surround_count.restype = ctypes.c_int
+        lib.or_immediate_win.restype = ctypes.c_int
         super().__init__(lib)
         assert lib.or_state_bytes() == STATE_BYTES
 
@@ -199,6 +204,32 @@ class Oracle(_Engine):
                                        threads or default_threads())
         return out
 
+    def batch_root_tactical_probe(self, states, legal, num_legal, priors, win1=True, screen=True, win2=True,
+                                  threads: int | None = None):
+        """(winning [B] int64, allowed [B, 256] uint8, forced [B] uint8) of
+        root_tactical_probe_batch (game_logic.cu:290-397)."""
+        states = np.ascontiguousarray(states, dtype=np.uint8)
+        legal = np.ascontiguousarray(legal, dtype=np.uint8)
+        n = np.ascontiguousarray(np.clip(num_legal, -1, MAX_LEGAL), dtype=np.int32)
+        pr = np.ascontiguousarray(priors, dtype=np.float32)
+        B = states.shape[0]
+        win = np.zeros(B, np.int64)
+        allowed = np.zeros((B, MAX_LEGAL), np.uint8)
+        forced = np.zeros(B, np.uint8)
+        self.lib.or_batch_root_tactical_probe(_ptr(states, _u8p), _ptr(legal, _u8p), _ptr(n, _i32p),
+                                              _ptr(pr, _f32p), B, int(win1), int(screen), int(win2),
+                                              _ptr(win, _i64p), _ptr(allowed, _u8p), _ptr(forced, _u8p),
+                                              threads or default_threads())
+        return win, allowed, forced
+
+    def surround_count(self, state, colour: int) -> int:
+        s = np.ascontiguousarray(state, dtype=np.uint8)
+        return int(self.lib.or_surround_count(_ptr(s, _u8p), int(colour)))
+
+    def immediate_win(self, state) -> int:
+        s = np.ascontiguousarray(state, dtype=np.uint8)
+        return int(self.lib.or_immediate_win(_ptr(s, _u8p)))
+
 
 class Reference(_Engine):
     """The reference's own engine (compiled from /root/reference), or None."""
@@ -213,6 +244,9 @@ class Reference(_Engine):
         lib.ref_batch_legal_features.argtypes = [_u8p, ctypes.c_int64, _u8p, _i32p, _f32p, ctypes.c_int]
         lib.ref_batch_successor_features.argtypes = [
             _u8p, _u8p, _i64p, _i64p, ctypes.c_int64, _f32p, ctypes.c_int, ctypes.c_int]
+        lib.ref_root_tactical_probe.argtypes = [_u8p, _u8p, ctypes.c_int, _f32p, ctypes.c_int, ctypes.c_int,
+                                                ctypes.c_int, _i64p, _u8p, _u8p]
+        lib.ref_immediate_win.restype = ctypes.c_int
         super().__init__(lib)
         assert lib.ref_state_bytes() == STATE_BYTES
         lib.ref_init()
@@ -246,3 +280,19 @@ class Reference(_Engine):
                                               _ptr(mi, _i64p), a2r.shape[0], _ptr(out, _f32p),
                                               1 if full_list else 0, threads or default_threads())
         return out
+
+    def root_tactical_probe(self, state, legal, num_legal: int, priors, win1=True, screen=True, win2=True):
+        s = np.ascontiguousarray(state, dtype=np.uint8)
+        m = np.ascontiguousarray(legal, dtype=np.uint8)
+        p = np.ascontiguousarray(priors, dtype=np.float32)
+        win = np.zeros(1, np.int64)
+        allowed = np.zeros(MAX_LEGAL, np.uint8)
+        forced = np.zeros(1, np.uint8)
+        self.lib.ref_root_tactical_probe(_ptr(s, _u8p), _ptr(m, _u8p), int(num_legal), _ptr(p, _f32p), int(win1),
+                                         int(screen), int(win2), _ptr(win, _i64p), _ptr(allowed, _u8p),
+                                         _ptr(forced, _u8p))
+        return int(win[0]), allowed, int(forced[0])
+
+    def immediate_win(self, state) -> int:
+        s = np.ascontiguousarray(state, dtype=np.uint8)
+        return int(self.lib.ref_immediate_win(_ptr(s, _u8p)))

@@ -858,6 +858,116 @@ static int move_action(const hmove* m, int cq, int cr) { /* gpu_move_to_action m
 }
 
 /* ---- public single-state API ---- */
+/* ---- root tactical probe: game_logic.cu:257-397, move_gen.cuh:825-898 ---- */
+static int surround_count(const hstate* s, int colour) { /* queen_surround_count_for_color game_logic.cu:257-263 */
+    if (!queen_down(s, colour)) return 0;
+    return occupied_neighbours(s, s->queen[colour]);
+}
+
+static int lone_empty_neighbour(const hstate* s, int target) { /* lone_empty_neighbor_of_queen move_gen.cuh:833-851 */
+    if (!queen_down(s, target)) return -1;
+    int q = s->queen[target];
+    if (q >= NCELL) return -1;
+    if (occupied_neighbours(s, q) != 5) return -1;
+    int e = -1;
+    for (int d = 0; d < NDIR; d++) {
+        int nb = NB[q][d];
+        if (nb < 0) continue;
+        if (!occ_at(s, nb)) {
+            if (e >= 0) return -1;
+            e = nb;
+        }
+    }
+    return e;
+}
+
+static int wins_for(int result, int colour) { return result == (colour == 0 ? RES_WHITE : RES_BLACK); }
+
+/* has_immediate_surround_win_for_current_player, move_gen.cuh:853-874 */
+static int immediate_win(const hstate* s) {
+    int me = side_to_move(s);
+    int cell = lone_empty_neighbour(s, me ^ 1);
+    if (cell < 0) return 0;
+    hmove mv[MAXLEG];
+    int n = legal_moves(s, mv);
+    for (int i = 0; i < n; i++) {
+        if ((int)mv[i].to != cell) continue;
+        hstate c = *s;
+        apply(&c, &mv[i]);
+        if (wins_for(c.result, me)) return 1;
+    }
+    return 0;
+}
+
+/* root_tactical_probe_kernel, game_logic.cu:290-397, for one root */
+static void root_probe(const hstate* root, const hmove* moves, int nlegal, const float* priors, int win1,
+                       int screen, int win2, int64_t* win_out, uint8_t* allowed, uint8_t* forced) {
+    *win_out = -1;
+    *forced = 0;
+    for (int i = 0; i < MAXLEG; i++) allowed[i] = i < nlegal;
+    if (nlegal <= 0 || root->result != RES_NONE) return;
+    int me = side_to_move(root), opp = me ^ 1;
+    int opp_s = surround_count(root, opp), own_s = surround_count(root, me);
+    if (win1 && opp_s == 5) { /* 1: immediate win, best prior (first on ties) */
+        int best = -1;
+        float bp = -1e30f;
+        for (int i = 0; i < nlegal; i++) {
+            hstate c = *root;
+            apply(&c, &moves[i]);
+            if (wins_for(c.result, me) && (best < 0 || priors[i] > bp)) {
+                best = i;
+                bp = priors[i];
+            }
+        }
+        if (best >= 0) {
+            *win_out = best;
+            return;
+        }
+    }
+    if (screen && own_s == 5) { /* 2: moves after which the opponent wins at once are not allowed */
+        int any_safe = 0;
+        for (int i = 0; i < nlegal; i++) {
+            hstate c = *root;
+            apply(&c, &moves[i]);
+            int bad = immediate_win(&c);
+            allowed[i] = !bad;
+            any_safe |= !bad;
+        }
+        if (!any_safe) {
+            *forced = 1;
+            return;
+        }
+    }
+    if (!win2 || !(opp_s == 4 || opp_s == 5)) return;
+    for (int i = 0; i < nlegal; i++) { /* 3: surround-raising moves every reply to which loses at once */
+        if (!allowed[i]) continue;
+        hstate c = *root;
+        apply(&c, &moves[i]);
+        int cs = surround_count(&c, opp);
+        if (opp_s == 4 && cs <= opp_s) continue;
+        if (opp_s == 5 && cs < opp_s) continue;
+        hmove rep[MAXLEG];
+        int nr = legal_moves(&c, rep); /* generate_non_decreasing_surround_replies move_gen.cuh:876-898 */
+        int monotone = 1;
+        for (int r = 0; r < nr && monotone; r++) {
+            hstate g = c;
+            apply(&g, &rep[r]);
+            if (surround_count(&g, opp) < cs) monotone = 0;
+        }
+        if (!monotone) continue;
+        int ok = 1;
+        for (int r = 0; r < nr && ok; r++) {
+            hstate g = c;
+            apply(&g, &rep[r]);
+            if (!wins_for(g.result, me) && !immediate_win(&g)) ok = 0;
+        }
+        if (ok) {
+            *win_out = i;
+            return;
+        }
+    }
+}
+
 int or_state_bytes(void) { return (int)sizeof(hstate); }
 
 int or_legal_moves(const uint8_t* raw, uint8_t* out) {
@@ -1005,6 +1115,35 @@ void or_batch_queen_escape(const uint8_t* states, int64_t B, uint8_t* out, int t
 /* ---- Philox4x32-10 (Salmon et al., SC'11, "Parallel random numbers: as easy
  * as 1, 2, 3"), multipliers 0xD2511F53 / 0xCD9E8D57, Weyl keys
  * 0x9E3779B9 / 0xBB67AE85. ---- */
+typedef struct {
+    const uint8_t* states;
+    const uint8_t* legal;
+    const int32_t* nlegal;
+    const float* priors;
+    int f1, f2, f3;
+    int64_t* win;
+    uint8_t* allowed;
+    uint8_t* forced;
+} probe_ctx;
+
+static void probe_body(int64_t i, void* p) {
+    probe_ctx* c = (probe_ctx*)p;
+    hmove mv[MAXLEG];
+    memcpy(mv, c->legal + i * MAXLEG * OR_MOVE_BYTES, sizeof(mv));
+    root_probe((const hstate*)(c->states + i * OR_STATE_BYTES), mv, c->nlegal[i], c->priors + i * MAXLEG, c->f1,
+               c->f2, c->f3, c->win + i, c->allowed + i * MAXLEG, c->forced + i);
+}
+
+void or_batch_root_tactical_probe(const uint8_t* states, const uint8_t* legal, const int32_t* nlegal,
+                                  const float* priors, int64_t B, int win1, int screen, int win2, int64_t* win,
+                                  uint8_t* allowed, uint8_t* forced, int threads) {
+    probe_ctx c = {states, legal, nlegal, priors, win1, screen, win2, win, allowed, forced};
+    parallel_for(B, threads, probe_body, &c);
+}
+
+int or_surround_count(const uint8_t* raw, int colour) { return surround_count((const hstate*)raw, colour); }
+int or_immediate_win(const uint8_t* raw) { return immediate_win((const hstate*)raw); }
+
 void or_philox4x32_10(uint32_t k0, uint32_t k1, const uint32_t ctr[4], uint32_t out[4]) {
     uint32_t x0 = ctr[0], x1 = ctr[1], x2 = ctr[2], x3 = ctr[3];
     for (int r = 0; r < 10; r++) {

@@ -48,6 +48,12 @@ void or_batch_successor_features(const uint8_t* states, const uint8_t* legal,
                                  const int64_t* move_indices, int64_t N,
                                  float* feat_out, int full_list, int threads);
 void or_batch_queen_escape(const uint8_t* states, int64_t B, uint8_t* out, int threads);
+/* root_tactical_probe_batch (game_logic.cu:290-397): nlegal clamped by the caller to <= 256 */
+void or_batch_root_tactical_probe(const uint8_t* states, const uint8_t* legal, const int32_t* nlegal,
+                                  const float* priors, int64_t B, int win1, int screen, int win2, int64_t* win,
+                                  uint8_t* allowed, uint8_t* forced, int threads);
+int or_surround_count(const uint8_t* state, int colour);
+int or_immediate_win(const uint8_t* state);
 
 /* Philox4x32-10 and the seeded random-play position generator */
 void or_philox4x32_10(uint32_t key0, uint32_t key1, const uint32_t ctr[4], uint32_t out[4]);

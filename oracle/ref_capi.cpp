@@ -146,4 +146,88 @@ void ref_batch_successor_features(const uint8_t* states, const uint8_t* legal,
     });
 }
 
+// root_tactical_probe_kernel (game_logic.cu:290-397) for one root, composed
+// from the reference's own primitives (apply_move, generate_legal_moves,
+// has_immediate_surround_win_for_current_player,
+// generate_non_decreasing_surround_replies, queen_surround_count_for_color_device).
+// game_logic.cu is CUDA-only, so its loop is restated here around them.
+void ref_root_tactical_probe(const uint8_t* raw, const uint8_t* moves, int nlegal, const float* priors, int win1,
+                             int screen, int win2, int64_t* win_out, uint8_t* allowed, uint8_t* forced) {
+    using namespace hive_gpu;
+    init_cpu_tables_once();
+    HiveState root = load(raw);
+    std::vector<GPUMove> mv(MAX_LEGAL_MOVES);
+    std::memcpy(mv.data(), moves, sizeof(GPUMove) * MAX_LEGAL_MOVES);
+    *win_out = -1;
+    *forced = 0;
+    for (int i = 0; i < MAX_LEGAL_MOVES; ++i) allowed[i] = i < nlegal ? 1 : 0;
+    if (nlegal <= 0 || root.result != IN_PROGRESS) return;
+    Color me = current_player(root);
+    Color opp = me == WHITE ? BLACK : WHITE;
+    int opp_s = queen_surround_count_for_color_device(root, opp);
+    int own_s = queen_surround_count_for_color_device(root, me);
+    auto won = [&](const HiveState& s) {
+        return (me == WHITE && s.result == WHITE_WINS) || (me == BLACK && s.result == BLACK_WINS);
+    };
+    if (win1 && opp_s == 5) {
+        int best = -1;
+        float bp = -1e30f;
+        for (int i = 0; i < nlegal; ++i) {
+            HiveState c = root;
+            apply_move(c, mv[i]);
+            if (won(c) && (best < 0 || priors[i] > bp)) {
+                best = i;
+                bp = priors[i];
+            }
+        }
+        if (best >= 0) {
+            *win_out = best;
+            return;
+        }
+    }
+    if (screen && own_s == 5) {
+        bool any_safe = false;
+        for (int i = 0; i < nlegal; ++i) {
+            HiveState c = root;
+            apply_move(c, mv[i]);
+            bool bad = has_immediate_surround_win_for_current_player(c);
+            allowed[i] = bad ? 0 : 1;
+            any_safe |= !bad;
+        }
+        if (!any_safe) {
+            *forced = 1;
+            return;
+        }
+    }
+    if (!win2 || !(opp_s == 4 || opp_s == 5)) return;
+    std::vector<GPUMove> rep(MAX_LEGAL_MOVES);
+    for (int i = 0; i < nlegal; ++i) {
+        if (!allowed[i]) continue;
+        HiveState c = root;
+        apply_move(c, mv[i]);
+        int cs = queen_surround_count_for_color_device(c, opp);
+        if (opp_s == 4 && cs <= opp_s) continue;
+        if (opp_s == 5 && cs < opp_s) continue;
+        bool monotone = true;
+        int nr = generate_non_decreasing_surround_replies(c, opp, cs, rep.data(), monotone);
+        if (!monotone) continue;
+        bool ok = true;
+        for (int r = 0; r < nr && ok; ++r) {
+            HiveState g = c;
+            apply_move(g, rep[r]);
+            if (!won(g) && !has_immediate_surround_win_for_current_player(g)) ok = false;
+        }
+        if (ok) {
+            *win_out = i;
+            return;
+        }
+    }
+}
+
+int ref_immediate_win(const uint8_t* raw) {
+    hive_gpu::init_cpu_tables_once();
+    HiveState s = load(raw);
+    return hive_gpu::has_immediate_surround_win_for_current_player(s) ? 1 : 0;
+}
+
 }  // extern "C"

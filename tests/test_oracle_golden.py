@@ -57,3 +57,22 @@ def test_lockstep_selfplay_finals(oracle):
     finals, plies = oracle.lockstep_selfplay(len(g["finals"]), 0, int(g["max_ply"]), int(g["seed"]))
     assert np.array_equal(plies, g["plies"])
     assert np.array_equal(finals, g["finals"])
+
+
+def test_root_tactical_probe(oracle):
+    """root_tactical_probe_batch (game_logic.cu:290-397) on positions sampled by
+    outcome (no tactic, immediate win, two-move forced win, screened list,
+    forced random move, no gate), for four combinations of the enable flags."""
+    g = load_golden("probe")
+    kinds = set(g["kinds"].tolist())
+    assert {"none", "screened", "w1", "w2", "forced", "ungated"} <= kinds
+    for j, (f1, f2, f3) in enumerate(g["flags"]):
+        win, allowed, forced = oracle.batch_root_tactical_probe(g["states"], g["legal"], g["nlegal"], g["priors"],
+                                                                f1, f2, f3, threads=2)
+        assert np.array_equal(win, g["win"][j]), (f1, f2, f3)
+        assert np.array_equal(allowed, g["allowed"][j]), (f1, f2, f3)
+        assert np.array_equal(forced, g["forced"][j]), (f1, f2, f3)
+    kids = g["child_states"]
+    got = np.array([oracle.immediate_win(kids[i]) for i in range(len(kids))], np.uint8)
+    assert np.array_equal(got, g["child_immediate_win"])
+    assert got.any() and not got.all()
