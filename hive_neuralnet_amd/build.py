@@ -17,7 +17,7 @@ import sys
 PKG = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(PKG)
 LIB = os.path.join(PKG, "libhive_gpu.so")
-SOURCES = [os.path.join(PKG, "csrc", n) for n in ("hive_engine.hip", "hive_mcts.hip", "hive_fnn.hip")]
+SOURCES = [os.path.join(PKG, "csrc", n) for n in ("hive_engine.hip", "hive_mcts.hip", "hive_fnn.hip", "hive_probe.hip")]
 ARCH = os.environ.get("HIVE_GPU_ARCH", "gfx950")
 
 FLAGS = [

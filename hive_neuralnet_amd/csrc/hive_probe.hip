@@ -1,0 +1,167 @@
+// hive_probe.hip -- root_tactical_probe_batch (game_logic.cu:1579-1616 over
+// root_tactical_probe_kernel :290-397) as four launches on the caller's
+// stream, no host synchronisation:
+//
+//   k_probe_roots   one lane group per root (hive_probe.hpp probe_root):
+//                   allowed[] = legal slots, the immediate win, the gates of
+//                   the screen and two-move stages (kept in forced[] until
+//                   k_probe_finish), and the (root, move) jobs of both
+//                   stages appended to the workspace's job lists;
+//   k_probe_screen  one lane group per screen job: allowed[r][i] = 0 when
+//                   the opponent wins at once after move i;
+//   k_probe_win2    one lane group per two-move candidate still allowed:
+//                   the lowest passing slot of each root by atomic min
+//                   (winning[] holds kUndecided meanwhile);
+//   k_probe_finish  per root: kUndecided -> -1, forced = the screen ran and
+//                   left no move allowed.
+//
+// The job kernels stride over their list with a grid sized from the batch;
+// the list length is read on the device.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/hive_gpu.h"
+#include "hive_probe.hpp"
+
+using namespace hw;
+
+namespace {
+
+constexpr int64_t kUndecided = 1 << 20;  // above every slot; replaced by -1 at the end
+constexpr int kJobGrid = 4096;           // workgroups of the job kernels (two jobs each per pass)
+
+__global__ void k_probe_reset(int32_t* __restrict__ counters) {
+    if (threadIdx.x < 2) counters[threadIdx.x] = 0;
+}
+
+__global__ __launch_bounds__(64) void k_probe_roots(const uint8_t* __restrict__ states,
+                                                    const uint8_t* __restrict__ legal,
+                                                    const int32_t* __restrict__ num_legal,
+                                                    const float* __restrict__ priors, int64_t B, int win1, int screen,
+                                                    int win2, int64_t* __restrict__ winning,
+                                                    uint8_t* __restrict__ allowed, uint8_t* __restrict__ gate_out,
+                                                    int32_t* __restrict__ counters, int32_t* __restrict__ jobs_screen,
+                                                    int32_t* __restrict__ jobs_win2) {
+    __shared__ Pos PS[kPosPerWave];
+    const int lane = threadIdx.x, l = gl(lane);
+    const int64_t r0 = (int64_t)blockIdx.x * kPosPerWave + (lane >> 5);
+    const bool live = r0 < B;
+    const int64_t r = live ? r0 : B - 1;
+    RootProbe R = probe_root(PS[lane >> 5], states + r * kStateBytes, legal + r * (kMaxLegal * 6), num_legal[r],
+                             priors + r * kMaxLegal, win1 != 0, screen != 0, win2 != 0, lane);
+    if (!live) return;
+    for (int i = l; i < kMaxLegal; i += kW) allowed[r * kMaxLegal + i] = i < R.n ? 1 : 0;
+    if (l == 0) {
+        winning[r] = R.win >= 0 ? R.win : ((R.gate & kProbeWin2) ? kUndecided : -1);
+        gate_out[r] = (uint8_t)R.gate;
+    }
+    if (R.gate & kProbeScreen) {
+        int base = 0;
+        if (l == 0) base = atomicAdd(&counters[0], R.n);
+        base = grp_shfl(base, 0, lane);
+        for (int i = l; i < R.n; i += kW) jobs_screen[base + i] = (int32_t)(r * kMaxLegal + i);
+    }
+    if (R.gate & kProbeWin2) {
+        int nc = 0;
+        for (int k = 0; k < 8; k++) nc += __popc(R.cand[k]);
+        int base = 0;
+        if (l == 0 && nc) base = atomicAdd(&counters[1], nc);
+        base = grp_shfl(base, 0, lane);
+        if (l == 0) {
+            int j = base;
+            for (int k = 0; k < 8; k++)
+                for (uint32_t w = R.cand[k]; w; w &= w - 1) jobs_win2[j++] = (int32_t)(r * kMaxLegal + 32 * k + __ffs(w) - 1);
+        }
+    }
+}
+
+__global__ __launch_bounds__(64) void k_probe_screen(const uint8_t* __restrict__ states,
+                                                     const uint8_t* __restrict__ legal,
+                                                     const int32_t* __restrict__ counters,
+                                                     const int32_t* __restrict__ jobs, uint8_t* __restrict__ allowed) {
+    __shared__ Pos PS[kPosPerWave];
+    const int lane = threadIdx.x;
+    const int64_t count = counters[0];
+    for (int64_t p = blockIdx.x; 2 * p < count; p += gridDim.x) {  // uniform over the workgroup
+        const int64_t j0 = 2 * p + (lane >> 5);
+        const bool live = j0 < count;
+        const int job = jobs[live ? j0 : 2 * p];
+        const int64_t r = job / kMaxLegal, i = job % kMaxLegal;
+        bool bad = probe_screen(PS[lane >> 5], states + r * kStateBytes, legal + (r * kMaxLegal + i) * 6, lane);
+        if (live && gl(lane) == 0) allowed[job] = bad ? 0 : 1;
+        __syncthreads();
+    }
+}
+
+__global__ __launch_bounds__(64) void k_probe_win2(const uint8_t* __restrict__ states,
+                                                   const uint8_t* __restrict__ legal,
+                                                   const int32_t* __restrict__ counters,
+                                                   const int32_t* __restrict__ jobs,
+                                                   const uint8_t* __restrict__ allowed,
+                                                   int64_t* __restrict__ winning) {
+    __shared__ Pos PS[kPosPerWave];
+    __shared__ Replies RS[kPosPerWave];
+    const int lane = threadIdx.x;
+    const int64_t count = counters[1];
+    for (int64_t p = blockIdx.x; 2 * p < count; p += gridDim.x) {
+        const int64_t j0 = 2 * p + (lane >> 5);
+        const bool live = j0 < count;
+        const int job = jobs[live ? j0 : 2 * p];
+        const int64_t r = job / kMaxLegal, i = job % kMaxLegal;
+        const bool active = live && allowed[job] != 0;
+        bool ok = probe_win2(PS[lane >> 5], RS[lane >> 5], states + r * kStateBytes,
+                             legal + (r * kMaxLegal + i) * 6, active, lane);
+        if (active && ok && gl(lane) == 0)
+            atomicMin(reinterpret_cast<unsigned long long*>(winning + r), (unsigned long long)i);
+        __syncthreads();
+    }
+}
+
+__global__ void k_probe_finish(const int32_t* __restrict__ num_legal, int64_t B, int64_t* __restrict__ winning,
+                               const uint8_t* __restrict__ allowed, uint8_t* __restrict__ forced) {
+    const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (r >= B) return;
+    if (winning[r] == kUndecided) winning[r] = -1;
+    const int gate = forced[r];
+    uint8_t f = 0;
+    if (gate & kProbeScreen) {
+        int n = num_legal[r];
+        n = n < 0 ? 0 : (n > kMaxLegal ? kMaxLegal : n);
+        bool any = false;
+        for (int i = 0; i < n; i++) any |= allowed[r * kMaxLegal + i] != 0;
+        f = any ? 0 : 1;
+    }
+    forced[r] = f;
+}
+
+}  // namespace
+
+extern "C" {
+
+int64_t hg_root_tactical_probe_workspace(int64_t B) { return B <= 0 ? 0 : 2 + 2 * B * kMaxLegal; }
+
+int hg_root_tactical_probe(const uint8_t* states, const uint8_t* legal_moves, const int32_t* num_legal,
+                           const float* priors, int64_t B, int enable_win_in_one, int enable_check_opponent_wins,
+                           int enable_win_in_two, int64_t* winning, uint8_t* allowed, uint8_t* forced,
+                           int32_t* workspace, void* stream) {
+    if (B <= 0) return 0;
+    if (B > (int64_t)(INT32_MAX / kMaxLegal)) return (int)hipErrorInvalidValue;
+    hipStream_t s = (hipStream_t)stream;
+    int32_t* counters = workspace;
+    int32_t* jobs_screen = workspace + 2;
+    int32_t* jobs_win2 = jobs_screen + B * kMaxLegal;
+    hipLaunchKernelGGL(k_probe_reset, dim3(1), dim3(64), 0, s, counters);
+    hipLaunchKernelGGL(k_probe_roots, dim3((unsigned)((B + kPosPerWave - 1) / kPosPerWave)), dim3(64), 0, s, states,
+                       legal_moves, num_legal, priors, B, enable_win_in_one, enable_check_opponent_wins,
+                       enable_win_in_two, winning, allowed, forced, counters, jobs_screen, jobs_win2);
+    const int64_t pairs = (B * kMaxLegal + 1) / 2;
+    const unsigned grid = (unsigned)(pairs < kJobGrid ? pairs : kJobGrid);
+    hipLaunchKernelGGL(k_probe_screen, dim3(grid), dim3(64), 0, s, states, legal_moves, counters, jobs_screen, allowed);
+    hipLaunchKernelGGL(k_probe_win2, dim3(grid), dim3(64), 0, s, states, legal_moves, counters, jobs_win2, allowed,
+                       winning);
+    hipLaunchKernelGGL(k_probe_finish, dim3((unsigned)((B + 255) / 256)), dim3(256), 0, s, num_legal, B, winning,
+                       allowed, forced);
+    return (int)hipGetLastError();
+}
+
+}  // extern "C"

@@ -1,0 +1,295 @@
+// hive_probe.hpp -- root tactical probe (root_tactical_probe_kernel,
+// hive_gpu/csrc/game_logic.cu:290-397) as lane-group programs on the LDS
+// board of hive_wave.hpp / hive_phases.hpp.
+//
+// The reference runs the whole probe of a root on one thread: an
+// immediate-win scan, an opponent-immediate-win screen of every legal move
+// (one full move generation per child) and a two-move forced-win search
+// (one move generation per child and per reply).  Here each of those units
+// is a 32-lane group program, so the move generations run lane-parallel and
+// the (root, move) units of all roots run side by side (hive_probe.hip
+// launches them):
+//
+//   probe_root    one root: surround counts, the immediate-win scan (lanes
+//                 over the legal moves, each move's result decided from the
+//                 occupancy change and queen cells it causes), the gates of
+//                 the later stages and the two-move candidates;
+//   probe_screen  one (root, move): the child, then
+//                 has_immediate_surround_win_for_current_player on it;
+//   probe_win2    one (root, candidate move): the child's replies, the
+//                 non-decreasing-surround test over all of them, then the
+//                 immediate-win test of every grandchild the reply does not
+//                 already win.
+//
+// Every program reaches the same barriers in both groups of a wave: a group
+// without work runs on the data it has and its caller writes nothing.
+#pragma once
+
+#include "hive_phases.hpp"
+
+namespace hw {
+
+enum { kProbeScreen = 1, kProbeWin2 = 2 };
+
+// What a move changes that decides results and queen surround counts: the
+// cell that becomes occupied, the cell that becomes empty (a lone piece
+// leaving it) and the queen cells, as apply_on_board would leave them.
+struct MoveEffect {
+    int add, del;
+    int q[2];
+    uint32_t placed;
+};
+
+HW_INL MoveEffect move_effect(const Pos& P, int type, int pt, int from, int to) {
+    MoveEffect e{-1, -1, {(int)P.queen[0], (int)P.queen[1]}, (uint32_t)P.qplaced};
+    const int me = P.turn & 1;
+    if (type == MV_PLACE) {
+        if (to < kCells && pt >= PT_Q && pt <= PT_P && P.hgt(to) < 5) {
+            e.add = to;
+            if (pt == PT_Q) {
+                e.q[me] = to;
+                e.placed |= 1u << me;
+            }
+        }
+    } else if (type == MV_MOVE) {
+        if (from < kCells && to < kCells && P.hgt(from) > 0 && P.hgt(from) <= 5 && P.hgt(to) < 5) {
+            int b = P.tp(from);
+            if (P.hgt(from) == 1) e.del = from;
+            e.add = to;
+            if ((b & 15) == PT_Q) e.q[(b >> 4) & 1] = to;
+        }
+    }
+    return e;
+}
+
+// queen_surround_count_for_color (game_logic.cu:257-263) after the move
+HW_INL int surround_after(const Pos& P, const MoveEffect& e, int col) {
+    if (!((e.placed >> col) & 1u)) return 0;
+    int q = e.q[col];
+    if (q < 0 || q >= kCells) return 0;
+    uint32_t gm = grid6(q);
+    uint32_t nb = nbr_bits_raw(P.occ, q) & gm;
+    if (e.del >= 0) nb &= ~dir_bit_to(q, e.del, gm);
+    if (e.add >= 0) nb |= dir_bit_to(q, e.add, gm);
+    return __popc(nb);
+}
+
+HW_INL int surround_now(const Pos& P, int col) {
+    MoveEffect e{-1, -1, {(int)P.queen[0], (int)P.queen[1]}, (uint32_t)P.qplaced};
+    return surround_after(P, e, col);
+}
+
+// the result apply_move + check_game_over (hive_state.cuh:442-448,497-517) leave
+HW_INL int result_after(const Pos& P, const MoveEffect& e) {
+    bool w = surround_after(P, e, 0) == 6, b = surround_after(P, e, 1) == 6;
+    if (w && b) return 3;
+    if (w) return 2;
+    if (b) return 1;
+    return P.result;
+}
+
+// lone_empty_neighbor_of_queen (move_gen.cuh:833-851)
+HW_INL int lone_empty_cell(const Pos& P, int target) {
+    if (!((P.qplaced >> target) & 1)) return -1;
+    int q = P.queen[target];
+    if (q >= kCells) return -1;
+    uint32_t gm = grid6(q);
+    uint32_t nb = nbr_bits_raw(P.occ, q) & gm;
+    if (__popc(nb) != 5) return -1;
+    uint32_t e = gm & ~nb;
+    if (__popc(e) != 1) return -1;
+    return step(q, __ffs(e) - 1);
+}
+
+// has_immediate_surround_win_for_current_player (move_gen.cuh:853-874) on a
+// prepared board: some legal move to the lone empty neighbour of the
+// opponent's queen wins.  Uniform within the group.
+HW_INL bool immediate_win(Pos& P, int lane) {
+    const int me = P.turn & 1;
+    const int cell = lone_empty_cell(P, me ^ 1);
+    const bool any = hw_wave_any(cell >= 0);
+    if (!any) return false;  // neither group needs the list
+    ListInfo L = generate_legal(P, lane);
+    bool hit = false;
+    if (cell >= 0 && L.total > 0) {
+        for (int i = gl(lane); i < L.n; i += kW) {
+            int tp, from, to, seg;
+            list_slot(P, L, i, tp, from, to, seg);
+            if (to != cell) continue;
+            MoveEffect e = move_effect(P, tp & 0xFF, tp >> 8, from, to);
+            if (result_after(P, e) == (me ? 2 : 1)) hit = true;
+        }
+    }
+    return grp_ballot(hit, lane) != 0;
+}
+
+// board prepared for move generation (load_position done, moves applied)
+HW_INL void prepare_loaded(Pos& P, int lane) {
+    build_occ_list(P, lane);
+    __syncthreads();
+    build_cell_masks(P, lane);
+    articulation(P, lane);
+    __syncthreads();
+}
+
+struct RootProbe {
+    int win;        // immediate win found (slot), else -1
+    int gate;       // kProbeScreen | kProbeWin2: the later stages that run
+    int n;          // legal moves considered (num_legal clamped to 256)
+    int opp_s;      // the opponent's queen surround count
+    uint32_t cand[8];  // two-move candidates: moves that raise (opp_s 4) / keep (opp_s 5) it
+};
+
+// probe_root: stages 1 and the gates of 2 and 3 of root_tactical_probe_kernel.
+// M: the root's [256][6] legal list, n its count, pr its priors.
+HW_INL RootProbe probe_root(Pos& P, const uint8_t* __restrict__ S, const uint8_t* __restrict__ M, int n,
+                            const float* __restrict__ pr, bool win1, bool screen, bool win2, int lane) {
+    const int l = gl(lane);
+    load_position(P, S, lane);
+    __syncthreads();
+    RootProbe R{-1, 0, n < 0 ? 0 : (n > kMaxLegal ? kMaxLegal : n), 0, {0, 0, 0, 0, 0, 0, 0, 0}};
+    const bool go = R.n > 0 && P.result == 0;
+    const int me = P.turn & 1;
+    const int opp_s = surround_now(P, me ^ 1), own_s = surround_now(P, me);
+    R.opp_s = opp_s;
+    if (!go) return R;
+    if (win1 && opp_s == 5) {
+        uint32_t wins[8];
+        for (int k = 0; k < 8; k++) {
+            int i = 32 * k + l;
+            bool w = false;
+            if (i < R.n) {
+                const uint8_t* m = M + 6 * i;
+                MoveEffect e = move_effect(P, m[0], m[1], m[2] | (m[3] << 8), m[4] | (m[5] << 8));
+                w = result_after(P, e) == (me ? 2 : 1);
+            }
+            wins[k] = grp_ballot(w, lane);
+        }
+        // first winning slot, replaced only by a strictly higher prior
+        int best = -1;
+        float bp = -1e30f;
+        for (int k = 0; k < 8; k++) {
+            uint32_t w = wins[k];
+            while (w) {
+                int i = 32 * k + __ffs(w) - 1;
+                w &= w - 1;
+                float p = pr[i];
+                if (best < 0 || p > bp) {
+                    best = i;
+                    bp = p;
+                }
+            }
+        }
+        if (best >= 0) {
+            R.win = best;
+            return R;
+        }
+    }
+    if (screen && own_s == 5) R.gate |= kProbeScreen;
+    if (win2 && (opp_s == 4 || opp_s == 5)) {
+        R.gate |= kProbeWin2;
+        for (int k = 0; k < 8; k++) {
+            int i = 32 * k + l;
+            bool c = false;
+            if (i < R.n) {
+                const uint8_t* m = M + 6 * i;
+                MoveEffect e = move_effect(P, m[0], m[1], m[2] | (m[3] << 8), m[4] | (m[5] << 8));
+                int cs = surround_after(P, e, me ^ 1);
+                c = opp_s == 4 ? cs > opp_s : cs >= opp_s;
+            }
+            R.cand[k] = grp_ballot(c, lane);
+        }
+    }
+    return R;
+}
+
+// probe_screen: does the opponent win at once after the root move m?
+HW_INL bool probe_screen(Pos& P, const uint8_t* __restrict__ S, const uint8_t* __restrict__ m, int lane) {
+    load_position(P, S, lane);
+    __syncthreads();
+    if (gl(lane) == 0) apply_on_board(P, S, m[0], m[1], m[2] | (m[3] << 8), m[4] | (m[5] << 8));
+    __syncthreads();
+    prepare_loaded(P, lane);
+    return immediate_win(P, lane);
+}
+
+// the child's replies, kept while grandchildren are evaluated on the board
+struct Replies {
+    uint8_t mv[kMaxLegal][6];
+    uint32_t need[8];  // replies whose grandchild must be tested for an immediate win
+    int n;
+};
+
+// probe_win2: after root move m, does every reply keep the opponent's queen
+// surround at or above its level after m, and leave a position the root
+// player has already won or wins at once?  `active` false: the group follows
+// the other group of its wave and its result is meaningless.
+HW_INL bool probe_win2(Pos& P, Replies& Rp, const uint8_t* __restrict__ S, const uint8_t* __restrict__ m,
+                       bool active, int lane) {
+    const int l = gl(lane);
+    const int mt = m[0], mp = m[1], mf = m[2] | (m[3] << 8), mto = m[4] | (m[5] << 8);
+    load_position(P, S, lane);
+    __syncthreads();
+    if (l == 0) apply_on_board(P, S, mt, mp, mf, mto);
+    __syncthreads();
+    prepare_loaded(P, lane);
+    const int opp = P.turn & 1, me = opp ^ 1;  // the opponent replies
+    const int cs = surround_now(P, opp);
+    ListInfo L = generate_legal(P, lane);
+    // keep the list: decoded slots (a lone PASS when there is no move)
+    for (int i = l; i < L.n; i += kW) {
+        int tp = MV_PASS, from = 0, to = 0, seg;
+        if (L.total > 0) list_slot(P, L, i, tp, from, to, seg);
+        Rp.mv[i][0] = (uint8_t)(tp & 0xFF);
+        Rp.mv[i][1] = (uint8_t)(tp >> 8);
+        Rp.mv[i][2] = (uint8_t)from;
+        Rp.mv[i][3] = (uint8_t)(from >> 8);
+        Rp.mv[i][4] = (uint8_t)to;
+        Rp.mv[i][5] = (uint8_t)(to >> 8);
+    }
+    // generate_non_decreasing_surround_replies (move_gen.cuh:876-898) and the
+    // replies that already win for the root player
+    bool drop = false;
+    for (int k = 0; k < 8; k++) {
+        int i = 32 * k + l;
+        bool need = false;
+        if (i < L.n) {
+            int tp = MV_PASS, from = 0, to = 0, seg;
+            if (L.total > 0) list_slot(P, L, i, tp, from, to, seg);
+            MoveEffect e = move_effect(P, tp & 0xFF, tp >> 8, from, to);
+            if (surround_after(P, e, opp) < cs) drop = true;
+            need = result_after(P, e) != (me ? 2 : 1);
+        }
+        uint32_t nw = grp_ballot(need, lane);
+        if (l == 0) Rp.need[k] = nw;
+    }
+    if (l == 0) Rp.n = L.n;
+    bool ok = active && grp_ballot(drop, lane) == 0;
+    __syncthreads();
+    // every remaining grandchild: the root player wins at once (any order;
+    // the first failure decides)
+    int k = 0;
+    uint32_t w = Rp.need[0];
+    for (;;) {
+        while (w == 0 && k < 7) w = Rp.need[++k];
+        const bool more = ok && w != 0;
+        if (!hw_wave_any(more)) break;
+        int r = more ? 32 * k + __ffs(w) - 1 : -1;
+        if (more) w &= w - 1;
+        load_position(P, S, lane);
+        __syncthreads();
+        if (l == 0 && r >= 0) {
+            apply_on_board(P, S, mt, mp, mf, mto);
+            apply_on_board(P, S, Rp.mv[r][0], Rp.mv[r][1], Rp.mv[r][2] | (Rp.mv[r][3] << 8),
+                           Rp.mv[r][4] | (Rp.mv[r][5] << 8));
+        }
+        __syncthreads();
+        prepare_loaded(P, lane);
+        bool won = immediate_win(P, lane);
+        if (more && !won) ok = false;
+        __syncthreads();
+    }
+    return ok;
+}
+
+}  // namespace hw

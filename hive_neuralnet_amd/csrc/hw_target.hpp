@@ -14,6 +14,11 @@
 // occupancy of the inlined form for k_legal).
 #define HW_INL __device__ __attribute__((always_inline)) inline
 
+// true in every lane of the wavefront when p holds in any of its lanes
+#ifndef HW_HOST_EMU
+__device__ __forceinline__ bool hw_wave_any(bool p) { return __ballot(p) != 0; }
+#endif
+
 // four dwords loaded or stored together (16-byte access, 4-byte alignment)
 #ifdef HW_HOST_EMU
 typedef uint32_t u32x4 __attribute__((vector_size(16), aligned(4)));

@@ -88,6 +88,11 @@ _SIGS = {
     "hg_mcts_root_noise": [_c_void_p, _c_void_p, _c_void_p, _c_int, ctypes.c_float, ctypes.c_float, _c_i64,
                            _c_void_p],
     "hg_mcts_reset_trees": [_c_void_p, _c_void_p, _c_void_p, _c_i64, _c_void_p],
+    "hg_root_tactical_probe": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_i64, _c_int, _c_int, _c_int, _c_void_p,
+                               _c_void_p, _c_void_p, _c_void_p, _c_void_p],
+}
+_SIGS_I64 = {  # entry points returning a size (int64_t)
+    "hg_root_tactical_probe_workspace": [_c_i64],
 }
 
 
@@ -151,6 +156,10 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
             fn = getattr(lib, name)
             fn.argtypes = args
             fn.restype = ctypes.c_int
+        for name, args in _SIGS_I64.items():
+            fn = getattr(lib, name)
+            fn.argtypes = args
+            fn.restype = _c_i64
         _lib = lib
         return lib
 
@@ -339,6 +348,31 @@ class HiveGpuExtension:
             w[6].data_ptr(), vb, w[7].data_ptr(), w[8].data_ptr(), w[9].data_ptr(), ab, ws.data_ptr(),
             priors.data_ptr(), values.data_ptr(), child_q.data_ptr(), _stream()), "fnn_leaf_eval")
         return priors, values, child_q
+
+    def root_tactical_probe_batch(self, states, legal_moves, num_legal, priors, batch_size: int,
+                                  enable_win_in_one: bool = True, enable_check_opponent_wins: bool = True,
+                                  enable_win_in_two: bool = True):
+        """(winning [B] int64, -1 filled; allowed [B, 256] uint8; forced [B] uint8)
+        -- bindings.cpp:336-344 / game_logic.cu:1579-1616."""
+        B = int(batch_size)
+        if B <= 0:
+            return (torch.full((0,), -1, dtype=torch.int64, device="cuda"),
+                    torch.zeros((0, MAX_LEGAL_MOVES), dtype=torch.uint8, device="cuda"),
+                    torch.zeros((0,), dtype=torch.uint8, device="cuda"))
+        states = _state_rows(states, B)
+        legal_moves = _dev(legal_moves, "legal_moves", torch.uint8, (MAX_LEGAL_MOVES, SIZEOF_GPU_MOVE), B)
+        num_legal = _dev(num_legal, "num_legal", torch.int32, (), B)
+        priors = _dev(priors, "priors", torch.float32, (MAX_LEGAL_MOVES,), B)
+        winning = torch.empty((B,), dtype=torch.int64, device="cuda")
+        allowed = torch.empty((B, MAX_LEGAL_MOVES), dtype=torch.uint8, device="cuda")
+        forced = torch.empty((B,), dtype=torch.uint8, device="cuda")
+        ws = torch.empty((int(self._lib.hg_root_tactical_probe_workspace(B)),), dtype=torch.int32, device="cuda")
+        _check(self._lib.hg_root_tactical_probe(states.data_ptr(), legal_moves.data_ptr(), num_legal.data_ptr(),
+                                                priors.data_ptr(), B, int(bool(enable_win_in_one)),
+                                                int(bool(enable_check_opponent_wins)), int(bool(enable_win_in_two)),
+                                                winning.data_ptr(), allowed.data_ptr(), forced.data_ptr(),
+                                                ws.data_ptr(), _stream()), "root_tactical_probe_batch")
+        return winning, allowed, forced
 
     def queen_escape_flags_batch(self, states: torch.Tensor, batch_size: int) -> torch.Tensor:
         B = int(batch_size)

@@ -95,6 +95,7 @@ class PlyResult:
     has_actions: torch.Tensor
     simulations: int = 0
     stats: dict = field(default_factory=dict)
+    forced_random: torch.Tensor | None = None  # the root probe left no safe move: random move, no policy target
 
 
 def topk_stable(x: torch.Tensor, k: int):
@@ -417,8 +418,6 @@ class FNNMCTSOrchestrator:
     def search_ply(self, states: torch.Tensor, tree: dict, active_mask: torch.Tensor) -> PlyResult:
         """Root evaluation + Gumbel sequential halving for every active game (:589-755)."""
         cfg = self.config
-        if cfg.short_forced_win_probe:
-            raise NotImplementedError("short_forced_win_probe (root tactical probes) is not part of this engine")
         cfg.max_num_considered_actions = max(1, min(cfg.max_num_considered_actions, self._max_legal))
         B = states.shape[0]
         MAX_L = self._max_legal
@@ -429,7 +428,15 @@ class FNNMCTSOrchestrator:
         priors, _, child_q = self._eval_states(states, legal, nl, B, root_feat)
         valid_slot = self._slot_idx < n64.unsqueeze(1)
         allowed = valid_slot
-        wins = self._find_immediate_wins(states, legal, nl, B)
+        forced = torch.zeros((B,), dtype=torch.bool, device="cuda")
+        if cfg.short_forced_win_probe:  # _analyze_short_tactics, :527-545 / :611-617
+            wins, allowed_u8, forced_u8 = self.ext.root_tactical_probe_batch(
+                states, legal, nl, priors, B, cfg.probe_win_in_one, cfg.probe_check_opponent_wins,
+                cfg.probe_win_in_two)
+            allowed = allowed_u8.to(torch.bool) & valid_slot
+            forced = forced_u8.to(torch.bool) & has_actions
+        else:
+            wins = self._find_immediate_wins(states, legal, nl, B)
         has_win = wins >= 0
         if bool(has_win.any().item()):
             # the reference clears priors and child Q of EVERY game in the batch
@@ -437,7 +444,7 @@ class FNNMCTSOrchestrator:
             priors.zero_()
             priors[has_win, wins[has_win]] = 1.0
             child_q.zero_()
-        search_rows = has_actions & ~has_win
+        search_rows = has_actions & ~has_win & ~forced
         legal_logits = torch.where(allowed, priors.clamp(min=1e-20).log(), torch.full_like(priors, -1e30))
         u = torch.rand(B, MAX_L, device="cuda").clamp(1e-4, 1 - 1e-4)
         gumbel = torch.where(allowed, -torch.log(-torch.log(u)), torch.full_like(u, -1e30))
@@ -497,7 +504,11 @@ class FNNMCTSOrchestrator:
             probs[has_win] = 0.0
             probs[has_win, wins[has_win]] = 1.0
             chosen = torch.where(has_win, wins, chosen)
-        return PlyResult(chosen, legal, nl, probs, slot_visits, has_actions, sims, stats)
+        if bool(forced.any().item()):  # no safe move: a uniform random one, no policy target (:768-776)
+            rand_slots = (torch.rand((B,), device="cuda") * n64.clamp(min=1).to(torch.float32)).to(torch.int64)
+            chosen = torch.where(forced, rand_slots, chosen)
+            probs = torch.where(forced.unsqueeze(1), torch.zeros_like(probs), probs)
+        return PlyResult(chosen, legal, nl, probs, slot_visits, has_actions, sims, stats, forced)
 
     def apply_and_rebase(self, states, tree, ply: PlyResult):
         B = states.shape[0]
@@ -542,8 +553,9 @@ class FNNMCTSOrchestrator:
             n_cpu = ply.num_legal.cpu().numpy()
             st_cpu = states.cpu().numpy()
             pr_cpu = ply.policy.cpu().numpy()
+            fr_cpu = ply.forced_random.cpu().numpy() if ply.forced_random is not None else np.zeros_like(has_cpu)
             for i in np.nonzero(has_cpu)[0]:
-                histories[i].append((st_cpu[i].copy(), pr_cpu[i, : n_cpu[i]].astype(np.float32), True))
+                histories[i].append((st_cpu[i].copy(), pr_cpu[i, : n_cpu[i]].astype(np.float32), not fr_cpu[i]))
             self.apply_and_rebase(states, tree, ply)
             moves_done += ply.has_actions.to(torch.int64)
             res = self.ext.check_results_batch(states, B)

@@ -123,6 +123,23 @@ int hg_fnn_leaf_eval(const float* features, int64_t T, int64_t N, int F, const i
                      const float* action2_w, float action2_b, float* workspace, float* priors, float* root_values,
                      float* child_q, void* stream);
 
+/* root_tactical_probe_batch -- game_logic.cu:1579-1616 (root_tactical_probe_kernel
+ * :290-397; has_immediate_surround_win_for_current_player and
+ * generate_non_decreasing_surround_replies, move_gen.cuh:825-898).  For each
+ * root: winning[B] int64 = the immediate win with the highest prior (first on
+ * ties; only when the opponent's queen has 5 neighbours), else the lowest
+ * slot after which every reply loses at once (opponent queen at 4 or 5),
+ * else -1; allowed[B][256] uint8 = legal slots, minus those after which the
+ * opponent wins at once (only when the own queen has 5 neighbours);
+ * forced[B] uint8 = that screen left no slot.  num_legal is clamped to 256.
+ * workspace: hg_root_tactical_probe_workspace(B) int32 (job lists).  Four
+ * launches on `stream`, no host synchronisation. */
+int64_t hg_root_tactical_probe_workspace(int64_t B);
+int hg_root_tactical_probe(const uint8_t* states, const uint8_t* legal_moves, const int32_t* num_legal,
+                           const float* priors, int64_t B, int enable_win_in_one, int enable_check_opponent_wins,
+                           int enable_win_in_two, int64_t* winning, uint8_t* allowed, uint8_t* forced,
+                           int32_t* workspace, void* stream);
+
 /* queen_escape_flags_batch -- game_logic.cu:1538-1554.  flags[B] uint8. */
 int hg_queen_escape_flags(const uint8_t* states, int64_t B, uint8_t* flags, void* stream);
 

@@ -161,10 +161,12 @@ class SearchPlyOracle:
                      (-tr / np.maximum(vr, 1).astype(np.float32)).astype(np.float32), np.float32(0))
         return visits, q.astype(np.float32)
 
-    def run(self, t, states, active, legal, n, root_eval, uniforms, noise, wave_evals):
+    def run(self, t, states, active, legal, n, root_eval, uniforms, noise, wave_evals, forced_uniforms=None):
         """One ply.  root_eval = (priors, root values, child_q); uniforms = the
         [B, 256] Gumbel draws; noise = the [B, max_children] Dirichlet rows;
-        wave_evals = per simulation wave (priors, values, child_q).
+        wave_evals = per simulation wave (priors, values, child_q);
+        forced_uniforms = the [B] draws of the random move of games the root
+        probe leaves without a safe move (short_forced_win_probe only).
         Returns (chosen slot, policy, slot visits); t is updated in place."""
         cfg = self.cfg
         B = states.shape[0]
@@ -172,18 +174,26 @@ class SearchPlyOracle:
         valid = slot < n[:, None]
         has_actions = active & (n > 0)
         priors, _, child_q = (np.array(a, np.float32, copy=True) for a in root_eval)
-        wins = self.immediate_wins(states, legal, n)
+        allowed = valid
+        forced = np.zeros(B, bool)
+        if cfg.short_forced_win_probe:  # _analyze_short_tactics :527-545, used at :611-617
+            wins, allowed_u8, forced_u8 = self.o.batch_root_tactical_probe(
+                states, legal, n, priors, cfg.probe_win_in_one, cfg.probe_check_opponent_wins, cfg.probe_win_in_two)
+            allowed = (allowed_u8 != 0) & valid
+            forced = (forced_u8 != 0) & has_actions
+        else:
+            wins = self.immediate_wins(states, legal, n)
         has_win = wins >= 0
         if has_win.any():
             priors[:] = 0.0
             priors[has_win, wins[has_win]] = 1.0
             child_q[:] = 0.0
-        search = has_actions & ~has_win
-        legal_logits = np.where(valid, np.log(np.maximum(priors, np.float32(1e-20))), np.float32(-1e30))
+        search = has_actions & ~has_win & ~forced
+        legal_logits = np.where(allowed, np.log(np.maximum(priors, np.float32(1e-20))), np.float32(-1e30))
         legal_logits = legal_logits.astype(np.float32)
         u = np.clip(uniforms.astype(np.float32), np.float32(1e-4), np.float32(1 - 1e-4))
-        gumbel = np.where(valid, -np.log(-np.log(u)), np.float32(-1e30)).astype(np.float32)
-        cand_all = self.candidates(states, legal, n, priors, legal_logits, valid)
+        gumbel = np.where(allowed, -np.log(-np.log(u)), np.float32(-1e30)).astype(np.float32)
+        cand_all = self.candidates(states, legal, n, priors, legal_logits, allowed)
         # root expansion (:879-902) and noise (:904-925)
         rows = np.arange(B)
         fc = t["first_child"][rows, t["root_node"]]
@@ -252,4 +262,8 @@ class SearchPlyOracle:
             probs[has_win] = 0.0
             probs[has_win, wins[has_win]] = 1.0
             chosen = np.where(has_win, wins, chosen)
+        if forced.any():  # :768-776
+            rnd = (np.asarray(forced_uniforms, np.float32) * np.maximum(n, 1).astype(np.float32)).astype(np.int64)
+            chosen = np.where(forced, rnd, chosen)
+            probs[forced] = 0.0
         return chosen, probs, slot_visits

@@ -7,7 +7,7 @@
 #include <thread>
 #include <vector>
 
-#include "../../hive_neuralnet_amd/csrc/hive_phases.hpp"
+#include "../../hive_neuralnet_amd/csrc/hive_probe.hpp"
 
 using namespace hw;
 
@@ -39,6 +39,7 @@ void run_group(int threads, int64_t count, F&& body) {
     wave_emu::g_ctx = nullptr;
 }
 static Pos g_pos[kPosPerWave];
+static Replies g_rep[kPosPerWave];
 }  // namespace
 
 extern "C" {
@@ -71,5 +72,66 @@ void emu_queen_escape(const uint8_t* states, int64_t B, uint8_t* out) {
         bool e = run_queen_escape(g_pos[t / kW], states + i * kStateBytes, t);
         if (live && t % kW == 0) out[i] = e ? 1 : 0;
     });
+}
+
+// root_tactical_probe_batch: the group programs of hive_probe.hpp in the
+// order and with the bookkeeping of hive_probe.hip's four launches
+void emu_root_probe(const uint8_t* states, const uint8_t* legal, const int32_t* nl, const float* pr, int64_t B, int f1,
+                    int f2, int f3, int64_t* win, uint8_t* allowed, uint8_t* forced) {
+    std::vector<RootProbe> R(B);
+    run_group(64, (B + kPosPerWave - 1) / kPosPerWave, [&](int64_t w, int t) {
+        int64_t i = w * kPosPerWave + t / kW;
+        bool live = i < B;
+        if (!live) i = B - 1;
+        RootProbe rp = probe_root(g_pos[t / kW], states + i * kStateBytes, legal + i * 1536, nl[i], pr + i * 256,
+                                  f1 != 0, f2 != 0, f3 != 0, t);
+        if (live && t % kW == 0) R[i] = rp;
+    });
+    std::vector<int> js, jw;
+    for (int64_t r = 0; r < B; r++) {
+        for (int i = 0; i < 256; i++) allowed[r * 256 + i] = i < R[r].n;
+        win[r] = R[r].win >= 0 ? R[r].win : ((R[r].gate & kProbeWin2) ? (1 << 20) : -1);
+        if (R[r].gate & kProbeScreen)
+            for (int i = 0; i < R[r].n; i++) js.push_back((int)(r * 256 + i));
+        if (R[r].gate & kProbeWin2)
+            for (int k = 0; k < 8; k++)
+                for (uint32_t m = R[r].cand[k]; m; m &= m - 1) jw.push_back((int)(r * 256 + 32 * k + __builtin_ctz(m)));
+    }
+    int64_t ns = (int64_t)js.size(), nw = (int64_t)jw.size();
+    if (ns)
+        run_group(64, (ns + 1) / 2, [&](int64_t p, int t) {
+            int64_t j = 2 * p + t / kW;
+            bool live = j < ns;
+            int job = js[live ? j : 2 * p];
+            int64_t r = job / 256, i = job % 256;
+            bool bad = probe_screen(g_pos[t / kW], states + r * kStateBytes, legal + (r * 256 + i) * 6, t);
+            if (live && t % kW == 0) allowed[job] = bad ? 0 : 1;
+        });
+    if (nw)
+        run_group(64, (nw + 1) / 2, [&](int64_t p, int t) {
+            int64_t j = 2 * p + t / kW;
+            bool live = j < nw;
+            int job = jw[live ? j : 2 * p];
+            int64_t r = job / 256, i = job % 256;
+            bool active = live && allowed[job];
+            bool ok = probe_win2(g_pos[t / kW], g_rep[t / kW], states + r * kStateBytes, legal + (r * 256 + i) * 6,
+                                 active, t);
+            if (active && ok && t % kW == 0) {
+                int64_t cur = __atomic_load_n(&win[r], __ATOMIC_SEQ_CST);
+                while (i < cur && !__atomic_compare_exchange_n(&win[r], &cur, i, false, __ATOMIC_SEQ_CST,
+                                                               __ATOMIC_SEQ_CST)) {
+                }
+            }
+        });
+    for (int64_t r = 0; r < B; r++) {
+        if (win[r] == (1 << 20)) win[r] = -1;
+        uint8_t f = 0;
+        if (R[r].gate & kProbeScreen) {
+            bool any = false;
+            for (int i = 0; i < R[r].n; i++) any |= allowed[r * 256 + i] != 0;
+            f = any ? 0 : 1;
+        }
+        forced[r] = f;
+    }
 }
 }

@@ -87,6 +87,15 @@ inline uint64_t __ballot(int pred) {
     wave_emu::group_sync();
     return m;
 }
+// wave-wide "any": a rendezvous of the whole (one-wave) workgroup
+inline bool hw_wave_any(bool p) {
+    wave_emu::g_ctx->slot[wave_emu::g_tid] = p ? 1 : 0;
+    wave_emu::wg_sync();
+    bool any = false;
+    for (int i = 0; i < 64; i++) any |= wave_emu::g_ctx->slot[i] != 0;
+    wave_emu::wg_sync();
+    return any;
+}
 inline uint32_t __builtin_amdgcn_alignbyte(uint32_t hi, uint32_t lo, uint32_t s) {
     return (uint32_t)(((((uint64_t)hi) << 32) | lo) >> (8 * (s & 3)));
 }

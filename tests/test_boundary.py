@@ -12,7 +12,7 @@ LIB = os.path.join(ROOT, "hive_neuralnet_amd", "libhive_gpu.so")
 
 def _declared():
     text = open(HEADER).read()
-    return sorted(set(re.findall(r"^int (hg_\w+)\(", text, flags=re.M)))
+    return sorted(set(re.findall(r"^(?:int|int64_t) (hg_\w+)\(", text, flags=re.M)))
 
 
 def test_header_declares_entry_points():
@@ -32,7 +32,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_python_binding_matches_header():
     from hive_neuralnet_amd import hive_gpu
-    assert sorted(hive_gpu._SIGS) == _declared()
+    assert sorted(list(hive_gpu._SIGS) + list(hive_gpu._SIGS_I64)) == _declared()
 
 
 def test_reference_surface_names():
@@ -41,7 +41,8 @@ def test_reference_surface_names():
     for name in ["initialize_tables", "create_initial_states", "generate_legal_moves_batch",
                  "apply_moves_batch", "check_results_batch", "extract_fnn_features_batch",
                  "generate_legal_moves_and_fnn_features_batch", "fnn_successor_features_batch",
-                 "legal_moves_to_actions_batch", "compute_centroids_batch", "queen_escape_flags_batch"]:
+                 "legal_moves_to_actions_batch", "compute_centroids_batch", "queen_escape_flags_batch",
+                 "root_tactical_probe_batch"]:
         assert callable(getattr(HiveGpuExtension, name)), name
 
 

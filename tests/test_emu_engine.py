@@ -59,3 +59,25 @@ def test_emulated_successors_queen_escape(emu, name):
     q = np.zeros(64, np.uint8)
     emu.emu_queen_escape(_p(st), ctypes.c_int64(64), _p(q))
     assert np.array_equal(q, g["queen_escape"][:64])
+
+
+def test_emulated_root_tactical_probe(emu):
+    """hive_probe.hpp's group programs, orchestrated as hive_probe.hip's
+    launches, against the reference's probe vectors: four positions of every
+    outcome kind with all stages enabled (the emulator runs a move generation
+    in ~10 ms, so the full fixture is left to the GPU test)."""
+    g = load_golden("probe")
+    kinds = g["kinds"]
+    sel = np.concatenate([np.nonzero(kinds == k)[0][:4] for k in sorted(set(kinds.tolist()))])
+    st, lm, nl, pr = (np.ascontiguousarray(g[k][sel]) for k in ("states", "legal", "nlegal", "priors"))
+    B = len(st)
+    j = 0
+    assert tuple(g["flags"][j]) == (1, 1, 1)
+    win = np.zeros(B, np.int64)
+    allowed = np.zeros((B, 256), np.uint8)
+    forced = np.zeros(B, np.uint8)
+    emu.emu_root_probe(_p(st), _p(lm), _p(nl), _p(pr), ctypes.c_int64(B), 1, 1, 1, _p(win), _p(allowed),
+                       _p(forced))
+    assert np.array_equal(win, g["win"][j][sel]), np.nonzero(win != g["win"][j][sel])[0][:8]
+    assert np.array_equal(forced, g["forced"][j][sel])
+    assert np.array_equal(allowed, g["allowed"][j][sel])

@@ -247,8 +247,11 @@ def test_fused_leaf_evaluation_matches_torch(mask, max_ply):
     np.testing.assert_allclose(pr[live].sum(axis=1), 1.0, atol=1e-5)
 
     # the fused fp32 outputs against the network restated in float64 numpy
-    # (fnn_network.py:175-220 over the same features): 1e-5 relative, with an
-    # absolute floor of 1e-7 for outputs that round to ~0
+    # (fnn_network.py:175-220 over the same features): within 1e-5 relative,
+    # with an absolute floor of 1e-6 -- values and Q lie in [-1, 1] and priors
+    # in [0, 1], and a 64-term fp32 dot product carries ~4e-7 absolute
+    # rounding whatever its result, so outputs near 0 cannot meet a bare
+    # relative bound (torch's fp32 composition does not either)
     a2r = np.repeat(np.arange(B), n).astype(np.int64)
     mi = np.concatenate([np.arange(k) for k in n]).astype(np.int64)
     succ = ext.fnn_successor_features_batch(states, legal, torch.from_numpy(a2r).cuda(), torch.from_numpy(mi).cuda(),
@@ -274,9 +277,9 @@ def test_fused_leaf_evaluation_matches_torch(mask, max_ply):
             x = np.exp(logit[s] - logit[s].max())
             want_p[t, :n[t]] = x / x.sum()
             want_q[t, :n[t]] = cv[s]
-    np.testing.assert_allclose(_np(v1), val(er), rtol=1e-5, atol=1e-7)
-    np.testing.assert_allclose(pr, want_p, rtol=1e-5, atol=1e-7)
-    np.testing.assert_allclose(_np(q1), want_q, rtol=1e-5, atol=1e-7)
+    np.testing.assert_allclose(_np(v1), val(er), rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(pr, want_p, rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(_np(q1), want_q, rtol=1e-5, atol=1e-6)
 
 
 @pytest.mark.parametrize("M", [4096, 600], ids=["roomy", "pool-exhausted"])
