@@ -50,6 +50,7 @@ def parse_args():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-mcts", action="store_true", help="skip the C5 Gumbel self-play leg")
     ap.add_argument("--mcts-only", action="store_true", help="run only the C5 leg (its own JSON line)")
+    ap.add_argument("--no-probe", action="store_true", help="skip the root tactical probe leg")
     ap.add_argument("--mcts-games", type=int, default=512)
     ap.add_argument("--mcts-sims", type=int, default=4096)
     ap.add_argument("--mcts-plies", type=int, default=1, help="timed self-play plies")
@@ -226,6 +227,43 @@ def mcts_leg(args):
     return out
 
 
+def probe_leg(args):
+    """Root tactical probe (root_tactical_probe_batch, the trainer's default root
+    analysis) on 4,096 seeded random-play positions (plies U[0,150]), every
+    stage enabled; the oracle on the host cores beside it."""
+    import numpy as np
+    import torch
+    from hive_neuralnet_amd import hive_gpu
+    ext = hive_gpu.load_extension()
+    B = 4096
+    states, _ = hive_gpu.random_positions(B, 0, 150, SEED + 7)
+    legal, nl = ext.generate_legal_moves_batch(states, B)
+    pr = torch.from_numpy((np.random.default_rng(SEED).integers(0, 8, size=(B, 256)) / 8.0).astype(np.float32)).cuda()
+    for _ in range(2):
+        ext.root_tactical_probe_batch(states, legal, nl, pr, B)
+    torch.cuda.synchronize()
+    reps = 5
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        w, a, f = ext.root_tactical_probe_batch(states, legal, nl, pr, B)
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) / reps * 1e3
+    out = {"metric": "root tactical probes/s", "value": B / ms * 1e3, "unit": "roots/s", "ms_per_call": ms,
+           "config": {"workload": "4,096 base-game positions, plies U[0,150], all probe stages", "batch": B},
+           "immediate_or_forced_wins": int((w >= 0).sum().item()), "forced_random": int(f.sum().item())}
+    if not args.no_cpu:
+        from oracle import Oracle
+        threads = args.cpu_threads or max(1, min(16, os.cpu_count() or 1))
+        st, lm, n, p = states.cpu().numpy(), legal.cpu().numpy(), nl.cpu().numpy(), pr.cpu().numpy()
+        orc = Oracle()
+        t0 = time.perf_counter()
+        orc.batch_root_tactical_probe(st, lm, n, p, threads=threads)
+        dt = time.perf_counter() - t0
+        out["cpu_baseline"] = {"value": B / dt, "unit": "roots/s", "cores": threads, "kind": "port",
+                               "sample": f"the same {B} roots, oracle/hive_oracle.c, {threads} pthreads, one pass"}
+    return out
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
@@ -323,6 +361,8 @@ def main():
         result["gpu_over_cpu"] = value / result["cpu_baseline"]["value"]
     if not args.no_mcts:
         result["mcts"] = mcts_leg(args)
+    if not args.no_probe:
+        result["probe"] = probe_leg(args)
     print(json.dumps(result))
 
 

@@ -189,18 +189,35 @@ HW_INL int descend(const Tree& T, int64_t g0, int node, int first_iter, float c_
     return node;
 }
 
-// mcts_select_with_root_slots_kernel (mcts_tree.cuh:811-955), one wave per game
+// mcts_select_with_root_slots_kernel (mcts_tree.cuh:811-955), one wave per
+// (game, candidate).  A simulation forced into root child fc + slot touches
+// only that child's subtree (the root itself is not entered), so the
+// candidates of a game with distinct slots are independent: wave (g, c)
+// runs candidate c's simulations sim = (w*C + c)*B + g in order of w, which
+// is the game's simulation order restricted to them.  A game whose slot list
+// repeats a slot runs all its simulations in one wave, in order.
 __global__ __launch_bounds__(64) void k_select_slots(Tree T, const int8_t* __restrict__ game_active,
                                                      const int32_t* __restrict__ root_nodes,
                                                      const int32_t* __restrict__ root_slots, int C, int max_root,
                                                      float c_puct, int64_t B, int64_t total, int det, float sigma,
                                                      float q_penalty, SelectOut O) {
-    const int64_t g = blockIdx.x;
+    const int64_t g = blockIdx.x / C;
+    const int c = (int)(blockIdx.x % C);
     const int lane = threadIdx.x;
     if (g >= B) return;
+    bool dup = false;
+    for (int c1 = lane; c1 < C; c1 += 64) {
+        int s1 = root_slots[g * C + c1];
+        if (s1 < 0) continue;
+        for (int c2 = c1 + 1; c2 < C; c2++) dup |= root_slots[g * C + c2] == s1;
+    }
+    dup = __ballot(dup) != 0;
+    if (dup && c != 0) return;
     const int64_t g0 = g * T.M;
-    for (int64_t sim = g; sim < total; sim += B) {
-        int cand = (int)((sim / B) % C);
+    const int64_t rounds = total / B;  // simulations per game
+    for (int64_t k = dup ? 0 : c; k < rounds; k += dup ? 1 : C) {
+        const int64_t sim = k * B + g;
+        int cand = (int)(k % C);
         if (!game_active[g]) { empty_sim(O, sim, lane); continue; }
         int slot = root_slots[g * C + cand];
         if (slot < 0 || slot >= max_root) { empty_sim(O, sim, lane); continue; }
@@ -527,7 +544,9 @@ int hg_mcts_select_root_slots(const hg_tree* tree, const int8_t* game_active, co
     if (B <= 0 || W <= 0 || num_candidates <= 0) return 0;
     int64_t total = (int64_t)W * num_candidates * B;
     SelectOut O{leaf_idx, move_paths, path_lens, vl_paths, vl_lens};
-    hipLaunchKernelGGL(k_select_slots, dim3((unsigned)B), dim3(64), 0, (hipStream_t)stream, to_tree(tree),
+    if (B * num_candidates > (int64_t)0x7fffffff) return (int)hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_select_slots, dim3((unsigned)(B * num_candidates)), dim3(64), 0, (hipStream_t)stream,
+                       to_tree(tree),
                        game_active, root_nodes, root_slots, num_candidates, max_root_children, c_puct, B, total,
                        deterministic_non_root, non_root_sigma, q_penalty, O);
     return finish();

@@ -137,7 +137,7 @@ class GpuEngine:
             self.c(pri), self.c(results), self.c(vals), self.c(vl), self.c(vlen), B, leaf.shape[0], self.M(t), 0.0)
 
 
-def run_search(engine, roots, *, seed=1, M=4096, C=4, W=2, waves=6, c_puct=1.25, eps=0.25, mode="slots"):
+def run_search(engine, roots, *, seed=1, M=4096, C=4, W=2, waves=6, c_puct=1.25, eps=0.25, mode="slots", dup=False):
     """Root expand + noise + `waves` select/replay/legal/expand-backup rounds.
 
     Returns (final tree as numpy, list of per-wave records)."""
@@ -158,6 +158,8 @@ def run_search(engine, roots, *, seed=1, M=4096, C=4, W=2, waves=6, c_puct=1.25,
     engine.root_noise(t, noise, eps)
     order = np.argsort(-pri, axis=1, kind="stable")[:, :C]
     slots = np.where(np.arange(C)[None, :] < n[:, None], order, -1).astype(np.int32)
+    if dup:  # every third game forces two candidates into the same root child
+        slots[::3, C - 1] = slots[::3, 0]
     alive = np.zeros((B, MAX_LEGAL), np.int8)
     for i in range(B):
         alive[i, slots[i][slots[i] >= 0]] = 1

@@ -19,12 +19,15 @@ def roots(oracle):
     return st
 
 
-@pytest.mark.parametrize("mode,W,C,M", [("slots", 1, 4, 8192), ("slots", 2, 4, 8192), ("slots", 4, 2, 8192),
-                                        ("mask", 3, 4, 8192), ("slots", 2, 4, 300)],
-                         ids=["slots-w1", "slots-w2", "slots-w4", "mask-w3", "slots-pool-exhaustion"])
-def test_search_matches_oracle(roots, mode, W, C, M):
-    ot, orec = run_search(OracleEngine(), roots, W=W, C=C, M=M, mode=mode, waves=6)
-    gt, grec = run_search(GpuEngine(), roots, W=W, C=C, M=M, mode=mode, waves=6)
+@pytest.mark.parametrize("mode,W,C,M,dup", [("slots", 1, 4, 8192, False), ("slots", 2, 4, 8192, False),
+                                            ("slots", 4, 2, 8192, False), ("mask", 3, 4, 8192, False),
+                                            ("slots", 2, 4, 300, False), ("slots", 3, 16, 8192, False),
+                                            ("slots", 2, 4, 8192, True)],
+                         ids=["slots-w1", "slots-w2", "slots-w4", "mask-w3", "slots-pool-exhaustion", "slots-c16-w3",
+                              "slots-duplicate"])
+def test_search_matches_oracle(roots, mode, W, C, M, dup):
+    ot, orec = run_search(OracleEngine(), roots, W=W, C=C, M=M, mode=mode, waves=6, dup=dup)
+    gt, grec = run_search(GpuEngine(), roots, W=W, C=C, M=M, mode=mode, waves=6, dup=dup)
     assert tree_equal(ot, gt) == []
     assert np.array_equal(orec[0]["was_root"], grec[0]["was_root"])
     for a, b in zip(orec[1:], grec[1:]):
