@@ -32,7 +32,8 @@ class Shadow:
         self.sync()
         ext = orch.ext
         for name in ("mcts_expand_dense_priors_batch", "mcts_apply_root_noise", "mcts_select_with_root_slots_batch",
-                     "mcts_replay_batch", "mcts_expand_and_backprop_dense_priors_batch"):
+                     "mcts_select_with_root_mask_batch", "mcts_replay_batch",
+                     "mcts_expand_and_backprop_dense_priors_batch"):
             monkeypatch.setattr(ext, name, self._wrap(name, getattr(ext, name)), raising=False)
 
     def sync(self):
@@ -67,6 +68,15 @@ class Shadow:
         rest = list(a[22:]) + [False, 4.0, 0.0][len(a) - 22:]
         exp = self.m.select_slots(self.ot, active, roots, slots, max_root, c_puct, W, bool(rest[0]),
                                   float(rest[1]), float(rest[2]))
+        for e, g in zip(exp, out):
+            assert np.array_equal(e, _np(g))
+
+    def _mcts_select_with_root_mask_batch(self, a, out):
+        active, roots, alive = _np(a[13]), _np(a[14]), _np(a[15])
+        c_puct, W = float(a[17]), int(a[19])
+        rest = list(a[21:]) + [False, 4.0, 0.0][len(a) - 21:]
+        exp = self.m.select_mask(self.ot, active, roots, alive, c_puct, W, bool(rest[0]), float(rest[1]),
+                                 float(rest[2]))
         for e, g in zip(exp, out):
             assert np.array_equal(e, _np(g))
 
