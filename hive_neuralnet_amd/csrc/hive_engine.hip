@@ -188,6 +188,28 @@ __global__ void k_random_play_step(uint8_t* __restrict__ states, const uint8_t* 
     if (plies_done) plies_done[i] += 1;
 }
 
+// legal_mask_kernel (state_encoder.cuh:908-976): the [B][85834] float mask is
+// zero-filled (16-byte stores over the whole buffer), then 1.0 is scattered
+// at each legal slot's action index (k_legal's fused action output).
+constexpr int kActionSpace = 85834;
+
+__global__ void k_zero_f32(float* __restrict__ p, int64_t count) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t n4 = count / 4;
+    if (i < n4) reinterpret_cast<float4*>(p)[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (i < count - 4 * n4) p[4 * n4 + i] = 0.0f;
+}
+
+__global__ void k_mask_scatter(const int32_t* __restrict__ actions, const int32_t* __restrict__ num_legal, int64_t B,
+                               float* __restrict__ masks) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= B * kMaxLegal) return;
+    const int64_t b = i / kMaxLegal;
+    const int slot = (int)(i % kMaxLegal);
+    const int a = actions[i];
+    if (slot < num_legal[b] && a >= 0 && a < kActionSpace) masks[b * kActionSpace + a] = 1.0f;
+}
+
 inline int grid_for(int64_t n, int block) { return (int)((n + block - 1) / block); }
 
 inline int finish() { return (int)hipGetLastError(); }
@@ -242,6 +264,19 @@ int hg_legal_features_actions(const uint8_t* states, int64_t B, uint8_t* moves, 
     if (B <= 0) return 0;
     hipLaunchKernelGGL((k_legal<true, true, true>), dim3((unsigned)grid_for(B, kPosPerWave)), dim3(64), 0, (hipStream_t)stream, states, B,
                        moves, num_legal, features, actions);
+    return finish();
+}
+
+int hg_legal_mask(const uint8_t* states, int64_t B, uint8_t* moves, int32_t* num_legal, int32_t* actions,
+                  float* masks, void* stream) {
+    if (B <= 0) return 0;
+    hipStream_t s = (hipStream_t)stream;
+    hipLaunchKernelGGL((k_legal<true, false, true>), dim3((unsigned)grid_for(B, kPosPerWave)), dim3(64), 0, s, states, B,
+                       moves, num_legal, nullptr, actions);
+    const int64_t count = B * (int64_t)kActionSpace;
+    hipLaunchKernelGGL(k_zero_f32, dim3((unsigned)((count / 4 + 255) / 256)), dim3(256), 0, s, masks, count);
+    hipLaunchKernelGGL(k_mask_scatter, dim3((unsigned)((B * kMaxLegal + 255) / 256)), dim3(256), 0, s, actions,
+                       num_legal, B, masks);
     return finish();
 }
 

@@ -532,6 +532,243 @@ __global__ void k_reset_counts(int32_t* __restrict__ cnt, int32_t* __restrict__ 
         root_node[g] = 0;
     }
 }
+// ---------------------------------------------------------------- legacy
+// The action-space engine behind hive_gpu/gpu_native_mcts.py: PUCT from the
+// root (no root slots or mask), priors looked up in [T][85834] action rows,
+// a separate backup kernel and the [B][85834] visit policy.  Same canonical
+// order as above: one wave per game, its simulations in order.
+constexpr int kActions = 85834;
+
+// mcts_select_kernel (mcts_tree.cuh:205-296): the first child stands when no
+// score beats -1e30
+__global__ __launch_bounds__(64) void k_select_legacy(Tree T, const int8_t* __restrict__ game_active,
+                                                      const int32_t* __restrict__ root_nodes, float c_puct, int64_t B,
+                                                      int64_t total, SelectOut O) {
+    const int64_t g = blockIdx.x;
+    const int lane = threadIdx.x;
+    if (g >= B) return;
+    const int64_t g0 = g * T.M;
+    for (int64_t sim = g; sim < total; sim += B) {
+        if (!game_active[g]) { empty_sim(O, sim, lane); continue; }
+        int node = root_nodes[g];
+        int plen = 0, vlen = 0;
+        for (int it = 0; it < kDepth; it++) {
+            int64_t ni = g0 + node;
+            int cfc = T.fc[ni], cnc = T.nc[ni];
+            if (cfc < 0 || T.it[ni] || cnc == 0) break;
+            if (cnc <= 0 || cnc > 1024 || cfc >= T.M) break;
+            float bs = -INFINITY;
+            int bi = 0x7fffffff;
+            for (int c = lane; c < cnc; c += 64) {
+                int child = cfc + c;
+                if (child < 0 || child >= T.M) break;
+                float sc = puct(T, ni, g0 + child, c_puct);
+                if (sc > -1e30f && (sc > bs || (sc == bs && c < bi))) { bs = sc; bi = c; }
+            }
+            int c = wave_argmax_first(bs, bi);
+            node = cfc + (c < 0 ? 0 : c);
+            enter(T, g0, node, false, 0.0f, O, sim, plen, vlen, lane);
+        }
+        if (lane == 0) {
+            O.leaf[sim] = node;
+            O.plen[sim] = plen;
+            O.vlen[sim] = vlen;
+        }
+        __syncthreads();
+    }
+}
+
+// mcts_expand_kernel (mcts_tree.cuh:330-433) body: a child per legal move with
+// an action index (moves outside the 17x17 window are skipped), prior =
+// action row[action]; virtual_q_penalty and child_init_q are not touched
+HW_INL int expand_leaf_legacy(const Tree& T, int64_t g, int64_t sim, const LeafIn& L, int lane) {
+    const int64_t g0 = g * T.M;
+    int leaf = L.leaf[sim];
+    int64_t li = g0 + leaf;
+    const uint8_t* S = L.states + sim * kStateBytes;
+    int res = L.results[sim];
+    if (res != 0) {
+        if (lane == 0) {
+            T.it[li] = 1;
+            T.tval[li] = result_value(res, S[OFF_TURN] | (S[OFF_TURN + 1] << 8));
+        }
+        __syncthreads();
+        return 0;
+    }
+    if (T.fc[li] != -1) return 0;
+    int n = L.nlegal[sim];
+    n = n > kMaxLegal ? kMaxLegal : n;
+    if (n <= 0) return 0;
+    int base = T.cnt[g];
+    if ((int64_t)base + n > T.M) return 0;
+    int cq, cr;
+    row_centroid(S, lane, cq, cr);
+    const uint8_t* mv = L.legal + sim * (kMaxLegal * 6);
+    const float* probs = L.priors + sim * (int64_t)kActions;
+    int created = 0;
+    for (int m0 = 0; m0 < n; m0 += 64) {
+        const int m = m0 + lane;
+        int a = -1;
+        const uint8_t* x = mv + 6 * m;
+        if (m < n) a = move_action(x[0], x[1], x[2] | (x[3] << 8), x[4] | (x[5] << 8), cq, cr);
+        const uint64_t keep = __ballot(a >= 0);
+        if (a >= 0) {
+            int64_t ci = g0 + base + created + __popcll(keep & ((1ull << lane) - 1ull));
+            T.vc[ci] = 0;
+            T.tv[ci] = 0.0f;
+            T.pr[ci] = probs[a];
+            T.pa[ci] = leaf;
+            T.ai[ci] = a;
+            T.fc[ci] = -1;
+            T.nc[ci] = 0;
+            T.it[ci] = 0;
+            T.tval[ci] = 0.0f;
+            uint8_t* d = T.mb + ci * 6;
+            for (int b = 0; b < 6; b++) d[b] = x[b];
+        }
+        created += __popcll(keep);
+    }
+    if (lane == 0) {
+        T.cnt[g] = base + created;
+        T.nc[li] = created;
+        T.fc[li] = base;
+    }
+    __syncthreads();
+    return 1;
+}
+
+// value backup of one simulation (mcts_backprop_kernel :555-605): virtual
+// losses undone along its path, then +1 visit and the sign-alternating value
+// from the leaf up the parent links
+HW_INL void backup_sim(const Tree& T, int64_t g0, int64_t sim, int leaf, float v, const int32_t* __restrict__ vl_paths,
+                       const int32_t* __restrict__ vl_lens) {
+    int n = vl_lens[sim];
+    const int32_t* vp = vl_paths + sim * kDepth;
+    for (int k = 0; k < n && k < kDepth; k++) {
+        int64_t ni = g0 + vp[k];
+        T.vc[ni] -= 1;
+        T.tv[ni] += 1.0f;
+    }
+    int node = leaf;
+    for (int s = 0; s < kDepth + 1 && node >= 0; s++) {
+        int64_t ni = g0 + node;
+        T.vc[ni] += 1;
+        T.tv[ni] += v;
+        v = -v;
+        node = T.pa[ni];
+    }
+}
+
+__global__ __launch_bounds__(64) void k_expand_legacy(Tree T, LeafIn L, int64_t B, int64_t total,
+                                                      int8_t* __restrict__ was_expanded) {
+    const int64_t g = blockIdx.x;
+    const int lane = threadIdx.x;
+    if (g >= B) return;
+    for (int64_t sim = g; sim < total; sim += B) {
+        int e = 0;
+        if (L.leaf[sim] >= 0) e = expand_leaf_legacy(T, g, sim, L, lane);
+        if (lane == 0) was_expanded[sim] = (int8_t)e;
+    }
+}
+
+__global__ __launch_bounds__(64) void k_backprop_legacy(Tree T, const int32_t* __restrict__ leaf_idx,
+                                                        const float* __restrict__ nn_values,
+                                                        const int32_t* __restrict__ vl_paths,
+                                                        const int32_t* __restrict__ vl_lens,
+                                                        const int8_t* __restrict__ was_expanded, int64_t B,
+                                                        int64_t total) {
+    const int64_t g = blockIdx.x;
+    if (g >= B || threadIdx.x != 0) return;
+    const int64_t g0 = g * T.M;
+    for (int64_t sim = g; sim < total; sim += B) {
+        int leaf = leaf_idx[sim];
+        if (leaf < 0) continue;
+        int64_t li = g0 + leaf;
+        float v = T.it[li] ? T.tval[li] : (was_expanded[sim] ? nn_values[sim] : 0.0f);
+        backup_sim(T, g0, sim, leaf, v, vl_paths, vl_lens);
+    }
+}
+
+// mcts_expand_and_backprop_kernel (mcts_tree.cuh:435-553)
+__global__ __launch_bounds__(64) void k_expand_backprop_legacy(Tree T, LeafIn L, const float* __restrict__ nn_values,
+                                                               const int32_t* __restrict__ vl_paths,
+                                                               const int32_t* __restrict__ vl_lens, int64_t B,
+                                                               int64_t total) {
+    const int64_t g = blockIdx.x;
+    const int lane = threadIdx.x;
+    if (g >= B) return;
+    const int64_t g0 = g * T.M;
+    for (int64_t sim = g; sim < total; sim += B) {
+        int leaf = L.leaf[sim];
+        if (leaf < 0) continue;
+        int e = expand_leaf_legacy(T, g, sim, L, lane);
+        if (lane == 0) {
+            int64_t li = g0 + leaf;
+            backup_sim(T, g0, sim, leaf, T.it[li] ? T.tval[li] : (e ? nn_values[sim] : 0.0f), vl_paths, vl_lens);
+        }
+        __syncthreads();
+    }
+}
+
+// mcts_extract_policy_kernel (mcts_tree.cuh:607-687): the game's [85834] row
+// is written whole (zeros, then the root children's values, serially in
+// child order as the reference sums them)
+__global__ __launch_bounds__(64) void k_extract_policy(Tree T, const int32_t* __restrict__ move_numbers,
+                                                       const int32_t* __restrict__ root_nodes, float temperature,
+                                                       int temp_drop, float pruning, int64_t B,
+                                                       float* __restrict__ policies) {
+    const int64_t g = blockIdx.x;
+    const int lane = threadIdx.x;
+    if (g >= B) return;
+    float* pol = policies + g * (int64_t)kActions;
+    for (int i = lane; i < kActions; i += 64) pol[i] = 0.0f;
+    __syncthreads();
+    if (lane != 0) return;
+    const int64_t g0 = g * T.M;
+    int64_t ri = g0 + root_nodes[g];
+    int fc = T.fc[ri], nc = T.nc[ri];
+    if (fc < 0 || nc == 0) return;
+    float temp = move_numbers[g] >= temp_drop ? 0.0f : temperature;
+    if (temp <= 0.0f) {
+        int best_a = -1, best_v = -1;
+        for (int c = 0; c < nc; c++) {
+            int64_t ci = g0 + fc + c;
+            int v = T.vc[ci];
+            if (v > best_v) { best_v = v; best_a = T.ai[ci]; }
+        }
+        if (best_a >= 0 && best_a < kActions) pol[best_a] = 1.0f;
+        return;
+    }
+    float max_v = 0.0f, sum = 0.0f;
+    for (int c = 0; c < nc; c++) {
+        float v = (float)T.vc[g0 + fc + c];
+        if (v > max_v) max_v = v;
+    }
+    for (int c = 0; c < nc; c++) {
+        int64_t ci = g0 + fc + c;
+        float v = (float)T.vc[ci];
+        if (pruning > 0.0f && max_v > 0.0f && v < max_v * pruning) v = 0.0f;
+        if (temp != 1.0f) v = powf(v, 1.0f / temp);
+        int a = T.ai[ci];
+        if (a >= 0 && a < kActions) {
+            pol[a] = v;
+            sum += v;
+        }
+    }
+    if (sum > 0.0f) {
+        for (int c = 0; c < nc; c++) {
+            int a = T.ai[g0 + fc + c];
+            if (a >= 0 && a < kActions) pol[a] /= sum;
+        }
+    } else {
+        float u = 1.0f / (float)nc;
+        for (int c = 0; c < nc; c++) {
+            int a = T.ai[g0 + fc + c];
+            if (a >= 0 && a < kActions) pol[a] = u;
+        }
+    }
+}
+
 }  // namespace
 
 extern "C" {
@@ -594,6 +831,54 @@ int hg_mcts_expand_backprop_dense(const hg_tree* tree, const float* child_q_valu
     LeafIn L{leaf_idx, leaf_states, legal_moves, num_legal, priors_per_legal, child_q_values, results};
     hipLaunchKernelGGL(k_expand_backprop, dim3((unsigned)B), dim3(64), 0, (hipStream_t)stream, to_tree(tree), L,
                        nn_values, vl_paths, vl_lens, q_penalty, B, total);
+    return finish();
+}
+
+int hg_mcts_select(const hg_tree* tree, const int8_t* game_active, const int32_t* root_nodes, float c_puct, int64_t B,
+                   int W, int32_t* leaf_idx, uint8_t* move_paths, int32_t* path_lens, int32_t* vl_paths,
+                   int32_t* vl_lens, void* stream) {
+    if (B <= 0 || W <= 0) return 0;
+    SelectOut O{leaf_idx, move_paths, path_lens, vl_paths, vl_lens};
+    hipLaunchKernelGGL(k_select_legacy, dim3((unsigned)B), dim3(64), 0, (hipStream_t)stream, to_tree(tree), game_active,
+                       root_nodes, c_puct, B, (int64_t)W * B, O);
+    return finish();
+}
+
+int hg_mcts_expand(const hg_tree* tree, const int32_t* leaf_idx, const uint8_t* leaf_states, const uint8_t* legal_moves,
+                   const int32_t* num_legal, const float* action_probs, const int32_t* results, int64_t B,
+                   int64_t total, int8_t* was_expanded, void* stream) {
+    if (B <= 0 || total <= 0) return 0;
+    LeafIn L{leaf_idx, leaf_states, legal_moves, num_legal, action_probs, nullptr, results};
+    hipLaunchKernelGGL(k_expand_legacy, dim3((unsigned)B), dim3(64), 0, (hipStream_t)stream, to_tree(tree), L, B, total,
+                       was_expanded);
+    return finish();
+}
+
+int hg_mcts_backprop(const hg_tree* tree, const int32_t* leaf_idx, const float* nn_values, const int32_t* vl_paths,
+                     const int32_t* vl_lens, const int8_t* was_expanded, int64_t B, int64_t total, void* stream) {
+    if (B <= 0 || total <= 0) return 0;
+    hipLaunchKernelGGL(k_backprop_legacy, dim3((unsigned)B), dim3(64), 0, (hipStream_t)stream, to_tree(tree), leaf_idx,
+                       nn_values, vl_paths, vl_lens, was_expanded, B, total);
+    return finish();
+}
+
+int hg_mcts_expand_backprop(const hg_tree* tree, const int32_t* leaf_idx, const uint8_t* leaf_states,
+                            const uint8_t* legal_moves, const int32_t* num_legal, const float* action_probs,
+                            const int32_t* results, const float* nn_values, const int32_t* vl_paths,
+                            const int32_t* vl_lens, int64_t B, int64_t total, void* stream) {
+    if (B <= 0 || total <= 0) return 0;
+    LeafIn L{leaf_idx, leaf_states, legal_moves, num_legal, action_probs, nullptr, results};
+    hipLaunchKernelGGL(k_expand_backprop_legacy, dim3((unsigned)B), dim3(64), 0, (hipStream_t)stream, to_tree(tree), L,
+                       nn_values, vl_paths, vl_lens, B, total);
+    return finish();
+}
+
+int hg_mcts_extract_policy(const hg_tree* tree, const int32_t* move_numbers, const int32_t* root_nodes,
+                           float temperature, int temp_drop_move, float pruning_threshold, int64_t B, float* policies,
+                           void* stream) {
+    if (B <= 0) return 0;
+    hipLaunchKernelGGL(k_extract_policy, dim3((unsigned)B), dim3(64), 0, (hipStream_t)stream, to_tree(tree),
+                       move_numbers, root_nodes, temperature, temp_drop_move, pruning_threshold, B, policies);
     return finish();
 }
 

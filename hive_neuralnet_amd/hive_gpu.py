@@ -88,6 +88,16 @@ _SIGS = {
     "hg_mcts_root_noise": [_c_void_p, _c_void_p, _c_void_p, _c_int, ctypes.c_float, ctypes.c_float, _c_i64,
                            _c_void_p],
     "hg_mcts_reset_trees": [_c_void_p, _c_void_p, _c_void_p, _c_i64, _c_void_p],
+    "hg_legal_mask": [_c_void_p, _c_i64, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p],
+    "hg_mcts_select": [_c_void_p, _c_void_p, _c_void_p, ctypes.c_float, _c_i64, _c_int, _c_void_p, _c_void_p,
+                       _c_void_p, _c_void_p, _c_void_p, _c_void_p],
+    "hg_mcts_expand": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_i64, _c_i64,
+                       _c_void_p, _c_void_p],
+    "hg_mcts_backprop": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_i64, _c_i64, _c_void_p],
+    "hg_mcts_expand_backprop": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+                                _c_void_p, _c_void_p, _c_void_p, _c_i64, _c_i64, _c_void_p],
+    "hg_mcts_extract_policy": [_c_void_p, _c_void_p, _c_void_p, ctypes.c_float, _c_int, ctypes.c_float, _c_i64,
+                               _c_void_p, _c_void_p],
     "hg_root_tactical_probe": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_i64, _c_int, _c_int, _c_int, _c_void_p,
                                _c_void_p, _c_void_p, _c_void_p, _c_void_p],
 }
@@ -374,6 +384,23 @@ class HiveGpuExtension:
                                                 ws.data_ptr(), _stream()), "root_tactical_probe_batch")
         return winning, allowed, forced
 
+    def generate_legal_mask_batch(self, states: torch.Tensor, batch_size: int):
+        """(masks [B, 85834] f32, num_legal [B] i32) -- bindings.cpp:292-294."""
+        moves, n, masks = self.generate_legal_moves_and_mask_batch(states, batch_size)
+        return masks, n
+
+    def generate_legal_moves_and_mask_batch(self, states: torch.Tensor, batch_size: int):
+        """(moves [B, 256, 6] u8, num_legal [B] i32, masks [B, 85834] f32) -- bindings.cpp:296-298."""
+        B = int(batch_size)
+        states = _state_rows(states, B)
+        moves = torch.empty((B, MAX_LEGAL_MOVES, SIZEOF_GPU_MOVE), dtype=torch.uint8, device="cuda")
+        n = torch.empty((B,), dtype=torch.int32, device="cuda")
+        masks = torch.empty((B, ACTION_SPACE_SIZE), dtype=torch.float32, device="cuda")
+        acts = torch.empty((B, MAX_LEGAL_MOVES), dtype=torch.int32, device="cuda")
+        _check(self._lib.hg_legal_mask(states.data_ptr(), B, moves.data_ptr(), n.data_ptr(), acts.data_ptr(),
+                                       masks.data_ptr(), _stream()), "generate_legal_moves_and_mask_batch")
+        return moves, n, masks
+
     def queen_escape_flags_batch(self, states: torch.Tensor, batch_size: int) -> torch.Tensor:
         B = int(batch_size)
         states = _state_rows(states, B)
@@ -505,6 +532,83 @@ def _mcts_methods():
         _check(self._lib.hg_mcts_expand_backprop_dense(
             ctypes.byref(tree), *args, nn_values.data_ptr(), vl_paths.data_ptr(), vl_lengths.data_ptr(),
             float(q_penalty), B, total, _stream()), "mcts_expand_and_backprop_dense_priors_batch")
+
+    # ---- legacy action-space engine (bindings.cpp:378-389; twelve tree tensors, no child_init_q,
+    # which these kernels never touch: any [B, M] f32 array fills its slot) ----
+    def mcts_select_batch(self, vc, tv, pr, pa, vq, mb, ai, fc, nc, it, tv2, cnt, game_active, root_nodes, c_puct,
+                          B, W, max_nodes):
+        """game_logic.cu:961-993 -> (leaf_idx, move_paths, path_lens, vl_paths, vl_lens), T = W * B."""
+        B, W, M = int(B), int(W), int(max_nodes)
+        tree = _tree_struct((vc, tv, pr, pa, vq, mb, ai, fc, nc, it, tv2, cnt), tv, B, M)
+        _dev(game_active, "game_active", torch.int8, (), B)
+        _dev(root_nodes, "root_nodes", torch.int32, (), B)
+        out = _select_outputs(W * B)
+        _check(self._lib.hg_mcts_select(ctypes.byref(tree), game_active.data_ptr(), root_nodes.data_ptr(),
+                                        float(c_puct), B, W, *[o.data_ptr() for o in out], _stream()),
+               "mcts_select_batch")
+        return out
+
+    def _legacy_leaf(total, leaf_indices, leaf_states, legal_moves, num_legal, action_probs, results):
+        _dev(leaf_indices, "leaf_indices", torch.int32, (), total)
+        _state_rows(leaf_states, total)
+        _dev(legal_moves, "legal_moves", torch.uint8, (MAX_LEGAL_MOVES, SIZEOF_GPU_MOVE), total)
+        _dev(num_legal, "num_legal", torch.int32, (), total)
+        _dev(action_probs, "action_probs", torch.float32, (ACTION_SPACE_SIZE,), total)
+        _dev(results, "results", torch.int32, (), total)
+        return [leaf_indices.data_ptr(), leaf_states.data_ptr(), legal_moves.data_ptr(), num_legal.data_ptr(),
+                action_probs.data_ptr(), results.data_ptr()]
+
+    def mcts_expand_batch(self, vc, tv, pr, pa, vq, mb, ai, fc, nc, it, tv2, cnt, leaf_indices, leaf_states,
+                          legal_moves, num_legal, action_probs, results, B, total, max_nodes):
+        """game_logic.cu:1018-1045 -> was_expanded [total] int8."""
+        B, total, M = int(B), int(total), int(max_nodes)
+        tree = _tree_struct((vc, tv, pr, pa, vq, mb, ai, fc, nc, it, tv2, cnt), tv, B, M)
+        args = _legacy_leaf(total, leaf_indices, leaf_states, legal_moves, num_legal, action_probs, results)
+        was = torch.zeros((total,), dtype=torch.int8, device="cuda")
+        _check(self._lib.hg_mcts_expand(ctypes.byref(tree), *args, B, total, was.data_ptr(), _stream()),
+               "mcts_expand_batch")
+        return was
+
+    def mcts_backprop_batch(self, vc, tv, pr, pa, vq, mb, ai, fc, nc, it, tv2, cnt, leaf_indices, nn_values,
+                            vl_paths, vl_lengths, was_expanded, B, total, max_nodes):
+        """game_logic.cu:1328-1349, in place."""
+        B, total, M = int(B), int(total), int(max_nodes)
+        tree = _tree_struct((vc, tv, pr, pa, vq, mb, ai, fc, nc, it, tv2, cnt), tv, B, M)
+        _dev(leaf_indices, "leaf_indices", torch.int32, (), total)
+        _dev(nn_values, "nn_values", torch.float32, (), total)
+        _dev(vl_paths, "vl_paths", torch.int32, (MAX_TREE_DEPTH,), total)
+        _dev(vl_lengths, "vl_lengths", torch.int32, (), total)
+        _dev(was_expanded, "was_expanded", torch.int8, (), total)
+        _check(self._lib.hg_mcts_backprop(ctypes.byref(tree), leaf_indices.data_ptr(), nn_values.data_ptr(),
+                                          vl_paths.data_ptr(), vl_lengths.data_ptr(), was_expanded.data_ptr(), B,
+                                          total, _stream()), "mcts_backprop_batch")
+
+    def mcts_expand_and_backprop_batch(self, vc, tv, pr, pa, vq, mb, ai, fc, nc, it, tv2, cnt, leaf_indices,
+                                       leaf_states, legal_moves, num_legal, action_probs, results, nn_values,
+                                       vl_paths, vl_lengths, B, total, max_nodes):
+        """game_logic.cu:1053-1080, in place."""
+        B, total, M = int(B), int(total), int(max_nodes)
+        tree = _tree_struct((vc, tv, pr, pa, vq, mb, ai, fc, nc, it, tv2, cnt), tv, B, M)
+        args = _legacy_leaf(total, leaf_indices, leaf_states, legal_moves, num_legal, action_probs, results)
+        _dev(nn_values, "nn_values", torch.float32, (), total)
+        _dev(vl_paths, "vl_paths", torch.int32, (MAX_TREE_DEPTH,), total)
+        _dev(vl_lengths, "vl_lengths", torch.int32, (), total)
+        _check(self._lib.hg_mcts_expand_backprop(ctypes.byref(tree), *args, nn_values.data_ptr(),
+                                                 vl_paths.data_ptr(), vl_lengths.data_ptr(), B, total, _stream()),
+               "mcts_expand_and_backprop_batch")
+
+    def mcts_extract_policy_batch(self, vc, tv, pr, pa, vq, mb, ai, fc, nc, it, tv2, cnt, move_numbers, root_nodes,
+                                  temperature, temp_drop_move, pruning_threshold, B, max_nodes):
+        """game_logic.cu:1355-1379 -> policies [B, 85834] f32."""
+        B, M = int(B), int(max_nodes)
+        tree = _tree_struct((vc, tv, pr, pa, vq, mb, ai, fc, nc, it, tv2, cnt), tv, B, M)
+        _dev(move_numbers, "move_numbers", torch.int32, (), B)
+        _dev(root_nodes, "root_nodes", torch.int32, (), B)
+        pol = torch.empty((B, ACTION_SPACE_SIZE), dtype=torch.float32, device="cuda")
+        _check(self._lib.hg_mcts_extract_policy(ctypes.byref(tree), move_numbers.data_ptr(), root_nodes.data_ptr(),
+                                                float(temperature), int(temp_drop_move), float(pruning_threshold), B,
+                                                pol.data_ptr(), _stream()), "mcts_extract_policy_batch")
+        return pol
 
     def mcts_apply_root_noise(self, vc, tv, pr, pa, vq, mb, ai, fc, nc, it, tv2, cnt, noise, root_nodes,
                               max_children_pad, dir_eps, root_policy_temp, B, max_nodes):

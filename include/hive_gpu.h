@@ -140,6 +140,16 @@ int hg_root_tactical_probe(const uint8_t* states, const uint8_t* legal_moves, co
                            int enable_win_in_two, int64_t* winning, uint8_t* allowed, uint8_t* forced,
                            int32_t* workspace, void* stream);
 
+/* generate_legal_mask_batch / generate_legal_moves_and_mask_batch --
+ * game_logic.cu:737-806 (legal_mask_kernel, state_encoder.cuh:908-976).
+ * masks[B][85834] f32 (written whole): 1.0 at the action index of every
+ * legal slot whose cells fall in the 17x17 window around the centroid, and at
+ * PASS_ACTION_INDEX for a PASS.  moves[B][256][6], num_legal[B] as
+ * hg_generate_legal_moves; actions[B][256] int32 is scratch (the slots'
+ * action indices). */
+int hg_legal_mask(const uint8_t* states, int64_t B, uint8_t* moves, int32_t* num_legal, int32_t* actions,
+                  float* masks, void* stream);
+
 /* queen_escape_flags_batch -- game_logic.cu:1538-1554.  flags[B] uint8. */
 int hg_queen_escape_flags(const uint8_t* states, int64_t B, uint8_t* flags, void* stream);
 
@@ -182,6 +192,45 @@ typedef struct hg_tree {
     float* child_init_q;
     int64_t max_nodes;
 } hg_tree;
+
+/* ---- legacy action-space engine (hive_gpu/gpu_native_mcts.py; the twelve
+ * tree arrays only, no child_init_q).  Same canonical order as below. */
+
+/* mcts_select_batch -- game_logic.cu:961-993 (mcts_select_kernel,
+ * mcts_tree.cuh:205-296): PUCT from the root at every level, first maximum,
+ * the first child when no score beats -1e30; virtual loss on every entered
+ * node.  T = W * B, outputs as hg_mcts_select_root_slots. */
+int hg_mcts_select(const hg_tree* tree, const int8_t* game_active, const int32_t* root_nodes, float c_puct, int64_t B,
+                   int W, int32_t* leaf_idx, uint8_t* move_paths, int32_t* path_lens, int32_t* vl_paths,
+                   int32_t* vl_lens, void* stream);
+
+/* mcts_expand_batch -- game_logic.cu:1018-1045 (mcts_expand_kernel,
+ * mcts_tree.cuh:330-433): children for the legal moves that have an action
+ * index, prior = action_probs[sim][action] ([T][85834] f32); was_expanded[T]. */
+int hg_mcts_expand(const hg_tree* tree, const int32_t* leaf_idx, const uint8_t* leaf_states, const uint8_t* legal_moves,
+                   const int32_t* num_legal, const float* action_probs, const int32_t* results, int64_t B,
+                   int64_t total, int8_t* was_expanded, void* stream);
+
+/* mcts_backprop_batch -- game_logic.cu:1328-1349 (mcts_backprop_kernel,
+ * mcts_tree.cuh:555-605). */
+int hg_mcts_backprop(const hg_tree* tree, const int32_t* leaf_idx, const float* nn_values, const int32_t* vl_paths,
+                     const int32_t* vl_lens, const int8_t* was_expanded, int64_t B, int64_t total, void* stream);
+
+/* mcts_expand_and_backprop_batch -- game_logic.cu:1053-1080
+ * (mcts_expand_and_backprop_kernel, mcts_tree.cuh:435-553). */
+int hg_mcts_expand_backprop(const hg_tree* tree, const int32_t* leaf_idx, const uint8_t* leaf_states,
+                            const uint8_t* legal_moves, const int32_t* num_legal, const float* action_probs,
+                            const int32_t* results, const float* nn_values, const int32_t* vl_paths,
+                            const int32_t* vl_lens, int64_t B, int64_t total, void* stream);
+
+/* mcts_extract_policy_batch -- game_logic.cu:1355-1379
+ * (mcts_extract_policy_kernel, mcts_tree.cuh:607-687): policies[B][85834]
+ * f32, written whole: root visit counts (pruned below pruning_threshold x
+ * the maximum, raised to 1/temperature, normalised; uniform when none),
+ * one-hot on the most visited child once move_numbers[g] >= temp_drop_move. */
+int hg_mcts_extract_policy(const hg_tree* tree, const int32_t* move_numbers, const int32_t* root_nodes,
+                           float temperature, int temp_drop_move, float pruning_threshold, int64_t B, float* policies,
+                           void* stream);
 
 /* Hard tree rebase of FNNMCTSOrchestrator._reroot_tree
  * (hive_fnn/fnn_mcts_orchestrator.py:1122-1142, rebase_tree_each_move): for

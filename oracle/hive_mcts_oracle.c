@@ -290,3 +290,172 @@ void or_mcts_root_noise(const or_tree* t, const float* noise, const int32_t* roo
             }
     }
 }
+
+/* ---- legacy action-space engine (hive_gpu/gpu_native_mcts.py's kernels) ---- */
+
+/* mcts_select_kernel mcts_tree.cuh:205-296: PUCT from the root at every level;
+ * the first child stands when no score beats -1e30 */
+void or_mcts_select_legacy(const or_tree* t, const int8_t* active, const int32_t* roots, float c_puct, int64_t B,
+                           int W, int32_t* leaf, uint8_t* paths, int32_t* plen, int32_t* vl, int32_t* vlen) {
+    sel_out o = {leaf, paths, plen, vl, vlen};
+    int64_t T = (int64_t)W * B;
+    for (int64_t s = 0; s < T; s++) {
+        int64_t g = s % B;
+        if (!active[g]) { blank(&o, s); continue; }
+        int node = roots[g], pl = 0, vn = 0;
+        for (int it = 0; it < DEPTH; it++) {
+            int64_t ni = at(t, g, node);
+            int f = t->fc[ni], n = t->nc[ni];
+            if (f < 0 || t->it[ni] || n == 0 || n <= 0 || n > 1024) break;
+            int best = f;
+            float bs = -1e30f;
+            for (int c = 0; c < n; c++) {
+                int child = f + c;
+                if (child < 0 || child >= t->M) break;
+                float sc = puct(t, ni, at(t, g, child), c_puct);
+                if (sc > bs) { bs = sc; best = child; }
+            }
+            node = best;
+            take_child(t, &o, s, g, node, 0, 0.0f, &pl, &vn);
+        }
+        leaf[s] = node; plen[s] = pl; vlen[s] = vn;
+    }
+}
+
+/* mcts_expand_kernel mcts_tree.cuh:330-433 body: priors from the [ACTION_SPACE]
+ * row by action index; moves outside the 17x17 window get no child */
+static int expand_legacy_one(const or_tree* t, int64_t g, int leaf, const uint8_t* state, const uint8_t* legal, int n,
+                             const float* probs, int result) {
+    int64_t li = at(t, g, leaf);
+    if (result != 0) {
+        t->it[li] = 1;
+        t->tval[li] = result_value(result, state[3412] | (state[3413] << 8));
+        return 0;
+    }
+    if (t->fc[li] != -1 || n <= 0) return 0;
+    if (n > OR_MAX_LEGAL) n = OR_MAX_LEGAL;
+    int base = t->cnt[g];
+    if ((int64_t)base + n > t->M) return 0;
+    int ccq, ccr;
+    or_centroid(state, &ccq, &ccr);
+    int created = 0;
+    for (int m = 0; m < n; m++) {
+        int a = or_move_to_action(legal + 6 * m, ccq, ccr);
+        if (a < 0) continue;
+        int64_t ci = at(t, g, base + created);
+        t->vc[ci] = 0;
+        t->tv[ci] = 0.0f;
+        t->pr[ci] = probs[a];
+        t->pa[ci] = leaf;
+        t->ai[ci] = a;
+        t->fc[ci] = -1;
+        t->nc[ci] = 0;
+        t->it[ci] = 0;
+        t->tval[ci] = 0.0f;
+        memcpy(t->mb + ci * 6, legal + 6 * m, 6);
+        created++;
+    }
+    t->cnt[g] = base + created;
+    t->nc[li] = created;
+    t->fc[li] = base;
+    return 1;
+}
+
+enum { ACTIONS = 85834 };
+
+void or_mcts_expand_legacy(const or_tree* t, const int32_t* leaf, const uint8_t* states, const uint8_t* legal,
+                           const int32_t* nlegal, const float* probs, const int32_t* results, int64_t B, int64_t total,
+                           int8_t* was) {
+    for (int64_t s = 0; s < total; s++) {
+        was[s] = 0;
+        if (leaf[s] < 0) continue;
+        was[s] = (int8_t)expand_legacy_one(t, s % B, leaf[s], states + s * OR_STATE_BYTES,
+                                           legal + s * OR_MAX_LEGAL * 6, nlegal[s], probs + s * (int64_t)ACTIONS,
+                                           results[s]);
+    }
+}
+
+/* backprop body shared by mcts_backprop_kernel :555-605 and the fused kernel :435-553 */
+static void backup_one(const or_tree* t, int64_t g, int64_t s, int leaf, float value_if_expanded, int expanded,
+                       const int32_t* vl, const int32_t* vlen) {
+    int64_t li = at(t, g, leaf);
+    float v = t->it[li] ? t->tval[li] : (expanded ? value_if_expanded : 0.0f);
+    for (int k = 0; k < vlen[s] && k < DEPTH; k++) {
+        int64_t ni = at(t, g, vl[s * DEPTH + k]);
+        t->vc[ni] -= 1;
+        t->tv[ni] += 1.0f;
+    }
+    int node = leaf;
+    for (int k = 0; k < DEPTH + 1 && node >= 0; k++) {
+        int64_t ni = at(t, g, node);
+        t->vc[ni] += 1;
+        t->tv[ni] += v;
+        v = -v;
+        node = t->pa[ni];
+    }
+}
+
+void or_mcts_backprop_legacy(const or_tree* t, const int32_t* leaf, const float* values, const int32_t* vl,
+                             const int32_t* vlen, const int8_t* was, int64_t B, int64_t total) {
+    for (int64_t s = 0; s < total; s++)
+        if (leaf[s] >= 0) backup_one(t, s % B, s, leaf[s], values[s], was[s] != 0, vl, vlen);
+}
+
+void or_mcts_expand_backprop_legacy(const or_tree* t, const int32_t* leaf, const uint8_t* states,
+                                    const uint8_t* legal, const int32_t* nlegal, const float* probs,
+                                    const int32_t* results, const float* values, const int32_t* vl,
+                                    const int32_t* vlen, int64_t B, int64_t total) {
+    for (int64_t s = 0; s < total; s++) {
+        if (leaf[s] < 0) continue;
+        int64_t g = s % B;
+        int e = expand_legacy_one(t, g, leaf[s], states + s * OR_STATE_BYTES, legal + s * OR_MAX_LEGAL * 6,
+                                  nlegal[s], probs + s * (int64_t)ACTIONS, results[s]);
+        backup_one(t, g, s, leaf[s], values[s], e, vl, vlen);
+    }
+}
+
+/* mcts_extract_policy_kernel mcts_tree.cuh:607-687: policies [B, ACTIONS] zero-filled by the caller */
+void or_mcts_extract_policy(const or_tree* t, const int32_t* move_numbers, const int32_t* roots, float temperature,
+                            int temp_drop, float pruning, int64_t B, float* policies) {
+    for (int64_t g = 0; g < B; g++) {
+        float* pol = policies + g * (int64_t)ACTIONS;
+        int64_t ri = at(t, g, roots[g]);
+        int f = t->fc[ri], n = t->nc[ri];
+        if (f < 0 || n == 0) continue;
+        float temp = move_numbers[g] >= temp_drop ? 0.0f : temperature;
+        if (temp <= 0.0f) {
+            int best_a = -1, best_v = -1;
+            for (int c = 0; c < n; c++) {
+                int64_t ci = at(t, g, f + c);
+                if (t->vc[ci] > best_v) { best_v = t->vc[ci]; best_a = t->ai[ci]; }
+            }
+            if (best_a >= 0 && best_a < ACTIONS) pol[best_a] = 1.0f;
+            continue;
+        }
+        float max_v = 0.0f, sum = 0.0f;
+        for (int c = 0; c < n; c++) {
+            float v = (float)t->vc[at(t, g, f + c)];
+            if (v > max_v) max_v = v;
+        }
+        for (int c = 0; c < n; c++) {
+            int64_t ci = at(t, g, f + c);
+            float v = (float)t->vc[ci];
+            if (pruning > 0.0f && max_v > 0.0f && v < max_v * pruning) v = 0.0f;
+            if (temp != 1.0f) v = powf(v, 1.0f / temp);
+            int a = t->ai[ci];
+            if (a >= 0 && a < ACTIONS) { pol[a] = v; sum += v; }
+        }
+        if (sum > 0.0f) {
+            for (int c = 0; c < n; c++) {
+                int a = t->ai[at(t, g, f + c)];
+                if (a >= 0 && a < ACTIONS) pol[a] /= sum;
+            }
+        } else {
+            float u = 1.0f / (float)n;
+            for (int c = 0; c < n; c++) {
+                int a = t->ai[at(t, g, f + c)];
+                if (a >= 0 && a < ACTIONS) pol[a] = u;
+            }
+        }
+    }
+}

@@ -1115,6 +1115,20 @@ void or_batch_queen_escape(const uint8_t* states, int64_t B, uint8_t* out, int t
 /* ---- Philox4x32-10 (Salmon et al., SC'11, "Parallel random numbers: as easy
  * as 1, 2, 3"), multipliers 0xD2511F53 / 0xCD9E8D57, Weyl keys
  * 0x9E3779B9 / 0xBB67AE85. ---- */
+/* legal_mask_kernel (state_encoder.cuh:908-976): masks [B, 85834] zero-filled by the caller */
+void or_legal_mask(const uint8_t* states, const uint8_t* legal, const int32_t* nlegal, int64_t B, float* masks) {
+    for (int64_t i = 0; i < B; i++) {
+        int cq, cr;
+        centroid((const hstate*)(states + i * OR_STATE_BYTES), &cq, &cr);
+        for (int m = 0; m < nlegal[i] && m < MAXLEG; m++) {
+            hmove mv;
+            memcpy(&mv, legal + (i * MAXLEG + m) * OR_MOVE_BYTES, sizeof(mv));
+            int a = move_action(&mv, cq, cr);
+            if (a >= 0) masks[i * 85834 + a] = 1.0f;
+        }
+    }
+}
+
 typedef struct {
     const uint8_t* states;
     const uint8_t* legal;

@@ -97,6 +97,21 @@ void or_mcts_expand_backprop_dense(const or_tree* t, const float* child_q, const
                                    const int32_t* vlen, float qp, int64_t B, int64_t total);
 void or_mcts_root_noise(const or_tree* t, const float* noise, const int32_t* roots, int pad, float eps, float temp,
                         int64_t B);
+/* legacy action-space engine (mcts_tree.cuh:205-687) */
+void or_mcts_select_legacy(const or_tree* t, const int8_t* active, const int32_t* roots, float c_puct, int64_t B,
+                           int W, int32_t* leaf, uint8_t* paths, int32_t* plen, int32_t* vl, int32_t* vlen);
+void or_mcts_expand_legacy(const or_tree* t, const int32_t* leaf, const uint8_t* states, const uint8_t* legal,
+                           const int32_t* nlegal, const float* probs, const int32_t* results, int64_t B, int64_t total,
+                           int8_t* was);
+void or_mcts_backprop_legacy(const or_tree* t, const int32_t* leaf, const float* values, const int32_t* vl,
+                             const int32_t* vlen, const int8_t* was, int64_t B, int64_t total);
+void or_mcts_expand_backprop_legacy(const or_tree* t, const int32_t* leaf, const uint8_t* states,
+                                    const uint8_t* legal, const int32_t* nlegal, const float* probs,
+                                    const int32_t* results, const float* values, const int32_t* vl,
+                                    const int32_t* vlen, int64_t B, int64_t total);
+void or_mcts_extract_policy(const or_tree* t, const int32_t* move_numbers, const int32_t* roots, float temperature,
+                            int temp_drop, float pruning, int64_t B, float* policies);
+void or_legal_mask(const uint8_t* states, const uint8_t* legal, const int32_t* nlegal, int64_t B, float* masks);
 
 #ifdef __cplusplus
 }

@@ -118,3 +118,52 @@ class MctsOracle:
         self.lib.or_mcts_root_noise(ctypes.byref(tr), _p(np.ascontiguousarray(noise, np.float32)),
                                     _p(np.ascontiguousarray(root_nodes, np.int32)), ctypes.c_int(pad),
                                     ctypes.c_float(eps), ctypes.c_float(temp), ctypes.c_int64(B))
+
+    # ---- legacy action-space engine (mcts_tree.cuh:205-687) ----------------
+    def select_legacy(self, t, game_active, root_nodes, c_puct, W):
+        B = t["node_count"].shape[0]
+        out = self._outs(W * B)
+        tr = self._tree(t)
+        self.lib.or_mcts_select_legacy(
+            ctypes.byref(tr), _p(np.ascontiguousarray(game_active, np.int8)),
+            _p(np.ascontiguousarray(root_nodes, np.int32)), ctypes.c_float(c_puct), ctypes.c_int64(B), ctypes.c_int(W),
+            *[_p(o) for o in out])
+        return out
+
+    def expand_legacy(self, t, leaf, states, legal, nlegal, probs, results):
+        B = t["node_count"].shape[0]
+        total = leaf.shape[0]
+        was = np.zeros(total, np.int8)
+        tr = self._tree(t)
+        self.lib.or_mcts_expand_legacy(ctypes.byref(tr), _p(leaf), _p(states), _p(legal), _p(nlegal), _p(probs),
+                                       _p(results), ctypes.c_int64(B), ctypes.c_int64(total), _p(was))
+        return was
+
+    def backprop_legacy(self, t, leaf, values, vl, vlen, was):
+        B = t["node_count"].shape[0]
+        tr = self._tree(t)
+        self.lib.or_mcts_backprop_legacy(ctypes.byref(tr), _p(leaf), _p(values), _p(vl), _p(vlen), _p(was),
+                                         ctypes.c_int64(B), ctypes.c_int64(leaf.shape[0]))
+
+    def expand_backprop_legacy(self, t, leaf, states, legal, nlegal, probs, results, values, vl, vlen):
+        B = t["node_count"].shape[0]
+        tr = self._tree(t)
+        self.lib.or_mcts_expand_backprop_legacy(ctypes.byref(tr), _p(leaf), _p(states), _p(legal), _p(nlegal),
+                                                _p(probs), _p(results), _p(values), _p(vl), _p(vlen),
+                                                ctypes.c_int64(B), ctypes.c_int64(leaf.shape[0]))
+
+    def extract_policy(self, t, move_numbers, root_nodes, temperature, temp_drop, pruning):
+        B = t["node_count"].shape[0]
+        out = np.zeros((B, 85834), np.float32)
+        tr = self._tree(t)
+        self.lib.or_mcts_extract_policy(ctypes.byref(tr), _p(np.ascontiguousarray(move_numbers, np.int32)),
+                                        _p(np.ascontiguousarray(root_nodes, np.int32)), ctypes.c_float(temperature),
+                                        ctypes.c_int(temp_drop), ctypes.c_float(pruning), ctypes.c_int64(B), _p(out))
+        return out
+
+    def legal_mask(self, states, legal, nlegal):
+        B = states.shape[0]
+        out = np.zeros((B, 85834), np.float32)
+        self.lib.or_legal_mask(_p(np.ascontiguousarray(states)), _p(np.ascontiguousarray(legal)),
+                               _p(np.ascontiguousarray(nlegal, np.int32)), ctypes.c_int64(B), _p(out))
+        return out

@@ -67,6 +67,34 @@ class OracleEngine:
         self.m.expand_backprop_dense(t, cq, leaf, states, legal, n, pri, results, vals, vl, vlen)
 
 
+def _oracle_legacy(cls):
+    def select_legacy(self, t, active, c_puct, W):
+        return self.m.select_legacy(t, active, t["root_node"], c_puct, W)
+
+    def expand_legacy(self, t, leaf, states, legal, n, probs, results):
+        return self.m.expand_legacy(t, leaf, states, legal, n, probs, results)
+
+    def backprop_legacy(self, t, leaf, vals, vl, vlen, was):
+        self.m.backprop_legacy(t, leaf, vals, vl, vlen, was)
+
+    def expand_backprop_legacy(self, t, leaf, states, legal, n, probs, results, vals, vl, vlen):
+        self.m.expand_backprop_legacy(t, leaf, states, legal, n, probs, results, vals, vl, vlen)
+
+    def extract_policy(self, t, move_numbers, temperature, temp_drop, pruning):
+        return self.m.extract_policy(t, move_numbers, t["root_node"], temperature, temp_drop, pruning)
+
+    def legal_mask(self, states):
+        legal, n = self.legal(states)
+        return self.m.legal_mask(states, legal, n), n
+
+    for f in (select_legacy, expand_legacy, backprop_legacy, expand_backprop_legacy, extract_policy, legal_mask):
+        setattr(cls, f.__name__, f)
+    return cls
+
+
+_oracle_legacy(OracleEngine)
+
+
 class GpuEngine:
     """Same interface over hive_neuralnet_amd.hive_gpu (all device work through the C-ABI)."""
 
@@ -135,6 +163,87 @@ class GpuEngine:
         self.ext.mcts_expand_and_backprop_dense_priors_batch(
             *self.args(t), t["child_init_q"], self.c(cq), self.c(leaf), self.c(states), self.c(legal), self.c(n),
             self.c(pri), self.c(results), self.c(vals), self.c(vl), self.c(vlen), B, leaf.shape[0], self.M(t), 0.0)
+
+
+def _gpu_legacy(cls):
+    def select_legacy(self, t, active, c_puct, W):
+        B = t["node_count"].shape[0]
+        out = self.ext.mcts_select_batch(*self.args(t), self.c(active.astype(np.int8)), t["root_node"], c_puct, B, W,
+                                         self.M(t))
+        return tuple(o.cpu().numpy() for o in out)
+
+    def expand_legacy(self, t, leaf, states, legal, n, probs, results):
+        B = t["node_count"].shape[0]
+        was = self.ext.mcts_expand_batch(*self.args(t), self.c(leaf), self.c(states), self.c(legal), self.c(n),
+                                         self.c(probs), self.c(results), B, leaf.shape[0], self.M(t))
+        return was.cpu().numpy()
+
+    def backprop_legacy(self, t, leaf, vals, vl, vlen, was):
+        B = t["node_count"].shape[0]
+        self.ext.mcts_backprop_batch(*self.args(t), self.c(leaf), self.c(vals), self.c(vl), self.c(vlen), self.c(was),
+                                     B, leaf.shape[0], self.M(t))
+
+    def expand_backprop_legacy(self, t, leaf, states, legal, n, probs, results, vals, vl, vlen):
+        B = t["node_count"].shape[0]
+        self.ext.mcts_expand_and_backprop_batch(*self.args(t), self.c(leaf), self.c(states), self.c(legal),
+                                                self.c(n), self.c(probs), self.c(results), self.c(vals), self.c(vl),
+                                                self.c(vlen), B, leaf.shape[0], self.M(t))
+
+    def extract_policy(self, t, move_numbers, temperature, temp_drop, pruning):
+        B = t["node_count"].shape[0]
+        return self.ext.mcts_extract_policy_batch(*self.args(t), self.c(move_numbers.astype(np.int32)),
+                                                  t["root_node"], temperature, temp_drop, pruning, B,
+                                                  self.M(t)).cpu().numpy()
+
+    def legal_mask(self, states):
+        m, n = self.ext.generate_legal_mask_batch(self.c(states), states.shape[0])
+        return m.cpu().numpy(), n.cpu().numpy()
+
+    for f in (select_legacy, expand_legacy, backprop_legacy, expand_backprop_legacy, extract_policy, legal_mask):
+        setattr(cls, f.__name__, f)
+    return cls
+
+
+_gpu_legacy(GpuEngine)
+
+
+def action_probs(rng, total):
+    """Synthetic [total, 85834] action-space priors (every entry positive)."""
+    return np.ascontiguousarray(rng.uniform(0.01, 1.0, (total, 85834)).astype(np.float32))
+
+
+def run_search_legacy(engine, roots, *, seed=3, M=4096, W=2, waves=5, c_puct=1.25, split=False):
+    """The legacy engine's loop (hive_gpu/gpu_native_mcts.py:300-365): root
+    expansion from action-space priors, then waves of PUCT select / replay /
+    legal / expand + backup (separate expand and backup kernels when split),
+    then the policies for three temperatures.  Returns (tree, records, policies)."""
+    rng = np.random.default_rng(seed)
+    B = roots.shape[0]
+    t = engine.tree(B, M)
+    legal, n = engine.legal(roots)
+    results = roots[:, 3415].astype(np.int32)
+    active = (results == 0) & (n > 0)
+    leaf0 = np.where(active, 0, -1).astype(np.int32)
+    was = engine.expand_legacy(t, leaf0, roots, legal, n, action_probs(rng, B), results)
+    records = [{"was_root": was}]
+    for _ in range(waves):
+        leaf, paths, plen, vl, vlen = engine.select_legacy(t, active, c_puct, W)
+        leaves = engine.replay(roots, paths, plen, leaf)
+        res = leaves[:, 3415].astype(np.int32)
+        lm, ln = engine.legal(leaves)
+        probs = action_probs(rng, leaf.shape[0])
+        vals = rng.uniform(-1, 1, leaf.shape[0]).astype(np.float32)
+        rec = {"leaf": leaf, "paths": paths, "plen": plen, "vl": vl, "vlen": vlen, "leaves": leaves}
+        if split:
+            rec["was"] = engine.expand_legacy(t, leaf, leaves, lm, ln, probs, res)
+            engine.backprop_legacy(t, leaf, vals, vl, vlen, rec["was"])
+        else:
+            engine.expand_backprop_legacy(t, leaf, leaves, lm, ln, probs, res, vals, vl, vlen)
+        records.append(rec)
+    mn = np.arange(B, dtype=np.int32) % 3 * 10  # 0, 10, 20: the last group past temp_drop 15
+    policies = [engine.extract_policy(t, mn, temp, 15, prune) for temp, prune in ((1.0, 0.0), (1.0, 0.2),
+                                                                                  (0.5, 0.0))]
+    return engine.to_np(t), records, policies
 
 
 def run_search(engine, roots, *, seed=1, M=4096, C=4, W=2, waves=6, c_puct=1.25, eps=0.25, mode="slots", dup=False):

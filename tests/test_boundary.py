@@ -42,7 +42,12 @@ def test_reference_surface_names():
                  "apply_moves_batch", "check_results_batch", "extract_fnn_features_batch",
                  "generate_legal_moves_and_fnn_features_batch", "fnn_successor_features_batch",
                  "legal_moves_to_actions_batch", "compute_centroids_batch", "queen_escape_flags_batch",
-                 "root_tactical_probe_batch"]:
+                 "root_tactical_probe_batch", "generate_legal_mask_batch", "generate_legal_moves_and_mask_batch",
+                 "mcts_select_batch", "mcts_replay_batch", "mcts_expand_batch", "mcts_backprop_batch",
+                 "mcts_expand_and_backprop_batch", "mcts_extract_policy_batch", "mcts_apply_root_noise",
+                 "mcts_select_with_root_mask_batch", "mcts_select_with_root_slots_batch",
+                 "mcts_select_replay_legal_fnn_root_slots_batch", "mcts_expand_dense_priors_batch",
+                 "mcts_expand_and_backprop_dense_priors_batch"]:
         assert callable(getattr(HiveGpuExtension, name)), name
 
 

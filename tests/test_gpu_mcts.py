@@ -67,3 +67,33 @@ def test_fused_select_replay_legal_fnn(roots):
     inactive = leaf_idx.cpu().numpy() < 0
     assert (ls[inactive] == 0).all()  # skipped rows stay all-zero states
     assert torch.equal(results, leaf_states[:, 3415].to(torch.int32))
+
+
+@pytest.mark.parametrize("split", [False, True], ids=["fused", "split"])
+def test_legacy_engine_matches_oracle(roots, split):
+    """The legacy action-space entry points (select / expand / backprop /
+    expand + backprop / extract policy) against the tree oracle: trees,
+    selections, leaves, expansion flags and policies.  Policies at
+    temperature 1 are bit-exact; at temperature 0.5 they go through powf,
+    whose device and host implementations may differ in the last place."""
+    from mcts_driver import run_search_legacy
+    ot, orec, opol = run_search_legacy(OracleEngine(), roots[:24], W=2, waves=4, split=split)
+    gt, grec, gpol = run_search_legacy(GpuEngine(), roots[:24], W=2, waves=4, split=split)
+    assert tree_equal(ot, gt) == []
+    assert np.array_equal(orec[0]["was_root"], grec[0]["was_root"])
+    for a, b in zip(orec[1:], grec[1:]):
+        for k in ("leaf", "paths", "plen", "vl", "vlen", "leaves") + (("was",) if split else ()):
+            assert np.array_equal(a[k], b[k]), k
+    assert np.array_equal(opol[0].view(np.uint32), gpol[0].view(np.uint32))
+    assert np.array_equal(opol[1].view(np.uint32), gpol[1].view(np.uint32))
+    np.testing.assert_allclose(gpol[2], opol[2], rtol=2e-7, atol=0)
+
+
+def test_legal_mask_matches_oracle(roots):
+    ge, oe = GpuEngine(), OracleEngine()
+    gm, gn = ge.legal_mask(roots)
+    om, on = oe.legal_mask(roots)
+    assert np.array_equal(gn, on)
+    assert np.array_equal(gm.view(np.uint32), om.view(np.uint32))
+    moves, n, masks = ge.ext.generate_legal_moves_and_mask_batch(ge.c(roots), roots.shape[0])
+    assert np.array_equal(masks.cpu().numpy(), gm) and np.array_equal(n.cpu().numpy(), on)

@@ -136,3 +136,80 @@ def test_terminal_and_pool_exhaustion(oracle):
                             np.ones(1, np.int32), np.array([0.9], np.float32), vl, vlen)
     assert t["is_terminal"][0, leaf[0]] == 1 and t["terminal_value"][0, leaf[0]] == 1.0
     assert t["total_value"][0, leaf[0]] == 1.0
+
+
+# ---- legacy action-space engine (mcts_tree.cuh:205-687) -------------------------------------
+@pytest.mark.parametrize("split", [False, True])
+def test_legacy_search_invariants(oracle, roots, split):
+    """Visit conservation and no outstanding virtual loss after waves of the legacy
+    loop; children = the legal moves with an action index, in list order, with
+    their action-space priors; the fused and split backups agree."""
+    from mcts_driver import run_search_legacy
+    t, rec, pols = run_search_legacy(OracleEngine(), roots, W=2, waves=4, split=split)
+    _check_counts(t, rec)
+    B = roots.shape[0]
+    for g in range(B):
+        expanded = t["first_child"][g] >= 0
+        assert t["node_count"][g] == 1 + t["num_children"][g][expanded].sum()
+    t2, _, pols2 = run_search_legacy(OracleEngine(), roots, W=2, waves=4, split=not split)
+    for k in t:
+        assert np.array_equal(t[k], t2[k]), k
+    for g in range(B):
+        f = t["first_child"][g, 0]
+        if f < 0:
+            continue
+        moves, n = oracle.legal_moves(roots[g])
+        cq, cr = oracle.centroid(roots[g])
+        acts = [oracle.move_to_action(moves[i], cq, cr) for i in range(n)]
+        keep = [i for i in range(n) if acts[i] >= 0]
+        assert t["num_children"][g, 0] == len(keep)
+        assert np.array_equal(t["move_bytes"][g, f:f + len(keep)], moves[keep])
+        assert list(t["action_idx"][g, f:f + len(keep)]) == [acts[i] for i in keep]
+
+
+def test_legacy_policy_known_answers(oracle, roots):
+    """extract_policy: visit distribution at temperature 1, pruning below 20% of
+    the maximum, visits^2 at temperature 0.5, one-hot argmax past the drop move."""
+    from mcts_driver import run_search_legacy
+    t, _, (p1, pp, p05) = run_search_legacy(OracleEngine(), roots, W=2, waves=4)
+    B = roots.shape[0]
+    for g in range(B):
+        f, n = t["first_child"][g, 0], t["num_children"][g, 0]
+        if f < 0 or n == 0:
+            assert not p1[g].any()
+            continue
+        v = t["visit_count"][g, f:f + n].astype(np.float64)
+        a = t["action_idx"][g, f:f + n]
+        if g % 3 == 2:  # move number 20 >= 15: greedy
+            want = np.zeros(85834)
+            want[a[int(np.argmax(v))]] = 1.0
+            assert np.array_equal(p1[g], want) and np.array_equal(p05[g], want)
+            continue
+        np.testing.assert_allclose(p1[g][a], v / v.sum(), rtol=1e-6)
+        assert abs(p1[g].sum() - 1.0) < 1e-5
+        pv = np.where(v < v.max() * 0.2, 0.0, v)
+        np.testing.assert_allclose(pp[g][a], pv / pv.sum(), rtol=1e-6)
+        np.testing.assert_allclose(p05[g][a], v ** 2 / (v ** 2).sum(), rtol=1e-5)
+
+
+def test_legacy_select_first_child_fallback():
+    """A node whose children all score -1e30 or below descends to its first child."""
+    m = MctsOracle()
+    t = new_tree(1, 16)
+    t["first_child"][0, 0], t["num_children"][0, 0] = 1, 3
+    t["parent_idx"][0, 1:4] = 0
+    t["node_count"][0] = 4
+    t["virtual_q_penalty"][0, 1:4] = 1e31  # q - penalty far below -1e30
+    leaf, paths, plen, vl, vlen = m.select_legacy(t, np.ones(1, np.int8), np.zeros(1, np.int32), 1.25, 1)
+    assert leaf[0] == 1 and plen[0] == 1 and list(vl[0, :1]) == [1]
+
+
+def test_legal_mask_is_action_scatter(oracle, roots):
+    m = MctsOracle()
+    legal, n, _, act = oracle.batch_legal_features_actions(roots)
+    mask = m.legal_mask(roots, legal, n)
+    for g in range(roots.shape[0]):
+        want = np.zeros(85834, np.float32)
+        a = act[g, :n[g]]
+        want[a[a >= 0]] = 1.0
+        assert np.array_equal(mask[g], want)
