@@ -51,6 +51,7 @@ def parse_args():
     ap.add_argument("--no-mcts", action="store_true", help="skip the C5 Gumbel self-play leg")
     ap.add_argument("--mcts-only", action="store_true", help="run only the C5 leg (its own JSON line)")
     ap.add_argument("--no-probe", action="store_true", help="skip the root tactical probe leg")
+    ap.add_argument("--no-train", action="store_true", help="skip the training forward-batch leg")
     ap.add_argument("--mcts-games", type=int, default=512)
     ap.add_argument("--mcts-sims", type=int, default=4096)
     ap.add_argument("--mcts-plies", type=int, default=1, help="timed self-play plies")
@@ -264,6 +265,31 @@ def probe_leg(args):
     return out
 
 
+def train_leg(args):
+    """Training-time encoder path (FNNTrainer._build_forward_batch counterpart):
+    roots + every legal successor's features for a 2,048-position batch drawn
+    from C2-style positions, uncached (legal lists + features generated)."""
+    import torch
+    from hive_neuralnet_amd import hive_gpu
+    from hive_neuralnet_amd.replay import build_forward_batch
+    ext = hive_gpu.load_extension()
+    B = 2048
+    states, _ = hive_gpu.random_positions(B, 0, 120, SEED + 11)
+    for _ in range(2):
+        build_forward_batch(ext, states, B)
+    torch.cuda.synchronize()
+    reps = 10
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        _, succ, _, _ = build_forward_batch(ext, states, B)
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) / reps * 1e3
+    return {"metric": "training forward batches/s", "value": 1e3 / ms, "unit": "batches/s", "ms_per_batch": ms,
+            "positions_per_s": B / ms * 1e3, "successor_rows_per_s": succ.shape[0] / ms * 1e3,
+            "config": {"workload": "2,048 base-game positions (plies U[0,120]) + all legal successors, uncached",
+                       "batch": B, "successor_rows": int(succ.shape[0])}}
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
@@ -363,6 +389,8 @@ def main():
         result["mcts"] = mcts_leg(args)
     if not args.no_probe:
         result["probe"] = probe_leg(args)
+    if not args.no_train:
+        result["train"] = train_leg(args)
     print(json.dumps(result))
 
 

@@ -76,13 +76,14 @@ class FNNMCTSConfig:  # fnn_mcts_orchestrator.py:45-82 (same fields and defaults
 
 
 @dataclass
-class FNNTrainingExample:  # hive_fnn/fnn_replay_buffer.py record shape
+class FNNTrainingExample:  # hive_fnn/fnn_replay_buffer.py:21-30 record shape
     state_bytes: np.ndarray
     policy_target: np.ndarray
     value_target: float
     use_for_policy: bool = True
     use_for_value: bool = True
     value_weight: float = 1.0
+    surprise_weight: float = 1.0
 
 
 @dataclass
