@@ -210,6 +210,73 @@ __global__ void k_mask_scatter(const int32_t* __restrict__ actions, const int32_
     if (slot < num_legal[b] && a >= 0 && a < kActionSpace) masks[b * kActionSpace + a] = 1.0f;
 }
 
+// ---------------------------------------------------------------- successor rows
+// The successor rows of a batch of leaves without a host round trip: the row
+// count stays on the device.  k_rows_offsets: exclusive prefix of the
+// clamped legal counts (one workgroup, chunks of 1024 with a running carry)
+// and the total; k_rows_map: row -> (leaf, slot); k_successor_rows: the
+// successor features of rows < total, two per wave, the grid striding over
+// the rows (sized from the capacity, the count read on the device).
+__global__ __launch_bounds__(1024) void k_rows_offsets(const int32_t* __restrict__ nlegal, int64_t T,
+                                                        int64_t* __restrict__ offsets, int64_t* __restrict__ total) {
+    __shared__ int64_t wsum[16];
+    __shared__ int64_t carry_s;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    if (tid == 0) carry_s = 0;
+    __syncthreads();
+    for (int64_t base = 0; base < T; base += 1024) {
+        const int64_t t = base + tid;
+        int n = t < T ? nlegal[t] : 0;
+        n = n < 0 ? 0 : (n > kMaxLegal ? kMaxLegal : n);
+        int incl = wave_incl_scan(n);
+        if (lane == 63) wsum[w] = incl;
+        __syncthreads();
+        int64_t before = carry_s;
+        for (int k = 0; k < w; k++) before += wsum[k];
+        if (t < T) offsets[t] = before + incl - n;
+        __syncthreads();
+        if (tid == 1023) carry_s = before + incl;
+        __syncthreads();
+    }
+    if (tid == 0) *total = carry_s;
+}
+
+__global__ void k_rows_map(const int32_t* __restrict__ nlegal, const int64_t* __restrict__ offsets, int64_t T,
+                           int64_t* __restrict__ a2r, int64_t* __restrict__ mi) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= T * kMaxLegal) return;
+    const int64_t t = i / kMaxLegal;
+    const int k = (int)(i % kMaxLegal);
+    int n = nlegal[t];
+    n = n < 0 ? 0 : (n > kMaxLegal ? kMaxLegal : n);
+    if (k < n) {
+        a2r[offsets[t] + k] = t;
+        mi[offsets[t] + k] = k;
+    }
+}
+
+__global__ __launch_bounds__(64) void k_successor_rows(const uint8_t* __restrict__ states,
+                                                       const uint8_t* __restrict__ legal,
+                                                       const int64_t* __restrict__ a2r,
+                                                       const int64_t* __restrict__ midx,
+                                                       const int64_t* __restrict__ total, int64_t num_roots,
+                                                       float* __restrict__ feat_out) {
+    __shared__ Pos PS[kPosPerWave];
+    const int lane = threadIdx.x;
+    const int64_t N = *total;
+    for (int64_t p = blockIdx.x; kPosPerWave * p < N; p += gridDim.x) {  // uniform over the workgroup
+        const int64_t i0 = kPosPerWave * p + (lane >> 5);
+        const bool live = i0 < N;
+        const int64_t i = live ? i0 : kPosPerWave * p;
+        const int64_t root = a2r[i], mi = midx[i];
+        const bool valid = root >= 0 && root < num_roots && mi >= 0 && mi < kMaxLegal;
+        const uint8_t* S = valid ? states + root * kStateBytes : kZeroRow;
+        const uint8_t* m = valid ? legal + (root * kMaxLegal + mi) * 6 : kZeroRow;
+        run_successor(PS[lane >> 5], S, m, lane, live && valid ? feat_out + i * kFeat : nullptr);
+        __syncthreads();
+    }
+}
+
 inline int grid_for(int64_t n, int block) { return (int)((n + block - 1) / block); }
 
 inline int finish() { return (int)hipGetLastError(); }
@@ -300,6 +367,26 @@ int hg_compute_centroids(const uint8_t* states, int64_t B, int32_t* centroids, v
     if (B <= 0) return 0;
     hipLaunchKernelGGL(k_actions, dim3((unsigned)grid_for(B, kPosPerWave)), dim3(64), 0, (hipStream_t)stream, states,
                        (const uint8_t*)nullptr, (const int32_t*)nullptr, B, (int32_t*)nullptr, centroids);
+    return finish();
+}
+
+int64_t hg_successor_rows_workspace(int64_t T) { return T <= 0 ? 0 : 8 * (T + 1 + 2 * T * (int64_t)kMaxLegal); }
+
+int hg_successor_rows(const uint8_t* states, const uint8_t* legal_moves, const int32_t* num_legal, int64_t T,
+                      void* workspace, float* features, void* stream) {
+    if (T <= 0) return 0;
+    if (((uintptr_t)workspace & 7)) return (int)hipErrorInvalidValue;
+    hipStream_t s = (hipStream_t)stream;
+    int64_t* offsets = reinterpret_cast<int64_t*>(workspace);
+    int64_t* total = offsets + T;
+    int64_t* a2r = total + 1;
+    int64_t* mi = a2r + T * kMaxLegal;
+    hipLaunchKernelGGL(k_rows_offsets, dim3(1), dim3(1024), 0, s, num_legal, T, offsets, total);
+    hipLaunchKernelGGL(k_rows_map, dim3((unsigned)((T * kMaxLegal + 255) / 256)), dim3(256), 0, s, num_legal, offsets,
+                       T, a2r, mi);
+    const int64_t pairs = (T * kMaxLegal + kPosPerWave - 1) / kPosPerWave;
+    const unsigned grid = (unsigned)(pairs < 65536 ? pairs : 65536);
+    hipLaunchKernelGGL(k_successor_rows, dim3(grid), dim3(64), 0, s, states, legal_moves, a2r, mi, total, T, features);
     return finish();
 }
 

@@ -94,7 +94,7 @@ __global__ __launch_bounds__(256) void k_leaf_mlp(const float* __restrict__ X, i
                                                   const float* __restrict__ wv, float bv, const float* __restrict__ a1w,
                                                   const float* __restrict__ a1b, const float* __restrict__ a2w, float ba2,
                                                   float* __restrict__ R, float* __restrict__ value,
-                                                  float* __restrict__ logit) {
+                                                  float* __restrict__ logit, const int64_t* __restrict__ rows_dev) {
     __shared__ MlpLds L;
     // permuted weights into LDS: element i of a [step][lane][tile] array is
     // unit m = 16 tile + lane%16 and step/lane group dependent K index k
@@ -125,6 +125,7 @@ __global__ __launch_bounds__(256) void k_leaf_mlp(const float* __restrict__ X, i
     __syncthreads();
 
     const int lane = threadIdx.x & 63, g = lane >> 4;
+    if (rows_dev) rows = *rows_dev;  // row count held on the device
     const int64_t ntiles = (rows + 15) >> 4;
     for (int64_t tile = (int64_t)blockIdx.x * kBlockWaves + (threadIdx.x >> 6); tile < ntiles;
          tile += (int64_t)gridDim.x * kBlockWaves) {
@@ -322,11 +323,59 @@ int hg_fnn_leaf_eval(const float* features, int64_t T, int64_t N, int F, const i
     float* cval = logit + N;        // [N]
     hipLaunchKernelGGL(k_leaf_mlp<true>, dim3(mlp_blocks(T)), dim3(64 * kBlockWaves), 0, st, features, T, F,
                        nullptr, T, fc1_w, fc1_b, ln_w, ln_b, fc2_w, fc2_b, value_w, value_b, action1_w, action1_b,
-                       action2_w, action2_b, R, root_values, nullptr);
+                       action2_w, action2_b, R, root_values, nullptr, nullptr);
     if (N > 0)
         hipLaunchKernelGGL(k_leaf_mlp<false>, dim3(mlp_blocks(N)), dim3(64 * kBlockWaves), 0, st, features + T * F,
                            N, F, succ_leaf, T, fc1_w, fc1_b, ln_w, ln_b, fc2_w, fc2_b, value_w, value_b, action1_w,
-                           action1_b, action2_w, action2_b, R, cval, logit);
+                           action1_b, action2_w, action2_b, R, cval, logit, nullptr);
+    hipLaunchKernelGGL(k_leaf_softmax, dim3(grid_for(T, 4)), dim3(256), 0, st, logit, cval, offsets, num_legal, T,
+                       priors, child_q);
+    return (int)hipGetLastError();
+}
+
+int64_t hg_fnn_leaf_eval_lists_workspace(int64_t T, int F) {
+    if (T <= 0) return 0;
+    const int64_t cap = T * kSlots;
+    int64_t b = hg_successor_rows_workspace(T);           // offsets, total, row map
+    b = (b + 255) & ~(int64_t)255;
+    b += cap * F * (int64_t)sizeof(float);                // successor features
+    b = (b + 255) & ~(int64_t)255;
+    b += (T * kE + 2 * cap) * (int64_t)sizeof(float);     // root half of the action tower, logits, child values
+    return b;
+}
+
+int hg_fnn_leaf_eval_lists(const uint8_t* leaf_states, const uint8_t* legal_moves, const int32_t* num_legal,
+                           const float* root_features, int64_t T, int F, const float* fc1_w, const float* fc1_b,
+                           const float* ln_w, const float* ln_b, const float* fc2_w, const float* fc2_b,
+                           const float* value_w, float value_b, const float* action1_w, const float* action1_b,
+                           const float* action2_w, float action2_b, void* workspace, float* priors,
+                           float* root_values, float* child_q, void* stream) {
+    if (T < 0 || F <= 0 || F > kFMax || (F & 1)) return (int)hipErrorInvalidValue;
+    if (((uintptr_t)root_features & 7) || ((uintptr_t)workspace & 255)) return (int)hipErrorInvalidValue;
+    if (F != 122) return (int)hipErrorInvalidValue;  // the successor rows are the engine's 122 features
+    if (T == 0) return 0;
+    hipStream_t st = (hipStream_t)stream;
+    const int64_t cap = T * kSlots;
+    uint8_t* base = reinterpret_cast<uint8_t*>(workspace);
+    int64_t off = hg_successor_rows_workspace(T);
+    int64_t* offsets = reinterpret_cast<int64_t*>(base);
+    int64_t* total = offsets + T;
+    int64_t* a2r = total + 1;
+    off = (off + 255) & ~(int64_t)255;
+    float* X = reinterpret_cast<float*>(base + off);
+    off += cap * F * (int64_t)sizeof(float);
+    off = (off + 255) & ~(int64_t)255;
+    float* R = reinterpret_cast<float*>(base + off);
+    float* logit = R + T * kE;
+    float* cval = logit + cap;
+    int e = hg_successor_rows(leaf_states, legal_moves, num_legal, T, workspace, X, stream);
+    if (e) return e;
+    hipLaunchKernelGGL(k_leaf_mlp<true>, dim3(mlp_blocks(T)), dim3(64 * kBlockWaves), 0, st, root_features, T, F,
+                       nullptr, T, fc1_w, fc1_b, ln_w, ln_b, fc2_w, fc2_b, value_w, value_b, action1_w, action1_b,
+                       action2_w, action2_b, R, root_values, nullptr, nullptr);
+    hipLaunchKernelGGL(k_leaf_mlp<false>, dim3(mlp_blocks(cap)), dim3(64 * kBlockWaves), 0, st, X, cap, F, a2r, T,
+                       fc1_w, fc1_b, ln_w, ln_b, fc2_w, fc2_b, value_w, value_b, action1_w, action1_b, action2_w,
+                       action2_b, R, cval, logit, total);
     hipLaunchKernelGGL(k_leaf_softmax, dim3(grid_for(T, 4)), dim3(256), 0, st, logit, cval, offsets, num_legal, T,
                        priors, child_q);
     return (int)hipGetLastError();

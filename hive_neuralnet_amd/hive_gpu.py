@@ -98,11 +98,18 @@ _SIGS = {
                                 _c_void_p, _c_void_p, _c_void_p, _c_i64, _c_i64, _c_void_p],
     "hg_mcts_extract_policy": [_c_void_p, _c_void_p, _c_void_p, ctypes.c_float, _c_int, ctypes.c_float, _c_i64,
                                _c_void_p, _c_void_p],
+    "hg_successor_rows": [_c_void_p, _c_void_p, _c_void_p, _c_i64, _c_void_p, _c_void_p, _c_void_p],
+    "hg_fnn_leaf_eval_lists": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_i64, _c_int, _c_void_p, _c_void_p,
+                               _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, ctypes.c_float, _c_void_p,
+                               _c_void_p, _c_void_p, ctypes.c_float, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+                               _c_void_p],
     "hg_root_tactical_probe": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_i64, _c_int, _c_int, _c_int, _c_void_p,
                                _c_void_p, _c_void_p, _c_void_p, _c_void_p],
 }
 _SIGS_I64 = {  # entry points returning a size (int64_t)
     "hg_root_tactical_probe_workspace": [_c_i64],
+    "hg_successor_rows_workspace": [_c_i64],
+    "hg_fnn_leaf_eval_lists_workspace": [_c_i64, _c_int],
 }
 
 
@@ -334,20 +341,7 @@ class HiveGpuExtension:
         offsets = _dev(offsets, "offsets", torch.int64, (), T)
         num_legal = _dev(num_legal, "num_legal", torch.int32, (), T)
         succ_leaf = _dev(succ_leaf, "succ_leaf", torch.int64, (), N)
-        spec = ((net.fc1.weight, "fc1.weight", 64 * F), (net.fc1.bias, "fc1.bias", 64),
-                (net.ln1.weight, "ln1.weight", 64), (net.ln1.bias, "ln1.bias", 64),
-                (net.fc2.weight, "fc2.weight", 64 * 64), (net.fc2.bias, "fc2.bias", 64),
-                (net.value_fc.weight, "value_fc.weight", 64), (net.action_fc1.weight, "action_fc1.weight", 64 * 128),
-                (net.action_fc1.bias, "action_fc1.bias", 64), (net.action_fc2.weight, "action_fc2.weight", 64))
-        w = []
-        for t, name, n in spec:
-            if t.numel() != n:
-                raise ValueError(f"fnn_leaf_eval serves 64-wide networks: {name} has {t.numel()} values, need {n}")
-            w.append(_dev(t.detach().reshape(-1), name, torch.float32, (), n))
-        if head_biases is None:
-            head_biases = (net.value_fc.bias.detach().reshape(-1)[0].item(),
-                           net.action_fc2.bias.detach().reshape(-1)[0].item())
-        vb, ab = float(head_biases[0]), float(head_biases[1])
+        w, vb, ab = _fnn_weights(net, F, head_biases)
         ws = torch.empty((T * 64 + 2 * N,), dtype=torch.float32, device="cuda")
         priors = torch.empty((T, MAX_LEGAL_MOVES), dtype=torch.float32, device="cuda")
         child_q = torch.empty((T, MAX_LEGAL_MOVES), dtype=torch.float32, device="cuda")
@@ -358,6 +352,37 @@ class HiveGpuExtension:
             w[6].data_ptr(), vb, w[7].data_ptr(), w[8].data_ptr(), w[9].data_ptr(), ab, ws.data_ptr(),
             priors.data_ptr(), values.data_ptr(), child_q.data_ptr(), _stream()), "fnn_leaf_eval")
         return priors, values, child_q
+
+    def fnn_leaf_eval_lists(self, leaf_states, legal_moves, num_legal, root_features, T: int, net,
+                            head_biases=None, workspace: torch.Tensor | None = None):
+        """(priors [T, 256], leaf values [T], child Q [T, 256]) of the leaves
+        from their own legal lists, with no host synchronisation: successor
+        rows sized on the device (hg_fnn_leaf_eval_lists).  `workspace`: a
+        uint8 device buffer of at least workspace_bytes(T) to reuse."""
+        T = int(T)
+        F = FNN_FEAT_DIM
+        leaf_states = _state_rows(leaf_states, T)
+        legal_moves = _dev(legal_moves, "legal_moves", torch.uint8, (MAX_LEGAL_MOVES, SIZEOF_GPU_MOVE), T)
+        num_legal = _dev(num_legal, "num_legal", torch.int32, (), T)
+        root_features = _dev(root_features, "root_features", torch.float32, (F,), T)
+        w, vb, ab = _fnn_weights(net, F, head_biases)
+        need = int(self._lib.hg_fnn_leaf_eval_lists_workspace(T, F))
+        if workspace is None or workspace.numel() < need + 256:
+            workspace = torch.empty((need + 256,), dtype=torch.uint8, device="cuda")
+        ptr = (workspace.data_ptr() + 255) & ~255
+        priors = torch.empty((T, MAX_LEGAL_MOVES), dtype=torch.float32, device="cuda")
+        child_q = torch.empty((T, MAX_LEGAL_MOVES), dtype=torch.float32, device="cuda")
+        values = torch.empty((T,), dtype=torch.float32, device="cuda")
+        if T > 0:
+            _check(self._lib.hg_fnn_leaf_eval_lists(
+                leaf_states.data_ptr(), legal_moves.data_ptr(), num_legal.data_ptr(), root_features.data_ptr(), T, F,
+                w[0].data_ptr(), w[1].data_ptr(), w[2].data_ptr(), w[3].data_ptr(), w[4].data_ptr(),
+                w[5].data_ptr(), w[6].data_ptr(), vb, w[7].data_ptr(), w[8].data_ptr(), w[9].data_ptr(), ab, ptr,
+                priors.data_ptr(), values.data_ptr(), child_q.data_ptr(), _stream()), "fnn_leaf_eval_lists")
+        return priors, values, child_q
+
+    def leaf_eval_workspace_bytes(self, T: int) -> int:
+        return int(self._lib.hg_fnn_leaf_eval_lists_workspace(int(T), FNN_FEAT_DIM)) + 256
 
     def root_tactical_probe_batch(self, states, legal_moves, num_legal, priors, batch_size: int,
                                   enable_win_in_one: bool = True, enable_check_opponent_wins: bool = True,
@@ -408,6 +433,25 @@ class HiveGpuExtension:
         _check(self._lib.hg_queen_escape_flags(states.data_ptr(), B, out.data_ptr(), _stream()),
                "queen_escape_flags_batch")
         return out
+
+
+def _fnn_weights(net, F: int, head_biases=None):
+    """The ten weight tensors of a 64-wide HiveFNN as flat device float32
+    arrays, and the two head biases as host floats."""
+    spec = ((net.fc1.weight, "fc1.weight", 64 * F), (net.fc1.bias, "fc1.bias", 64),
+            (net.ln1.weight, "ln1.weight", 64), (net.ln1.bias, "ln1.bias", 64),
+            (net.fc2.weight, "fc2.weight", 64 * 64), (net.fc2.bias, "fc2.bias", 64),
+            (net.value_fc.weight, "value_fc.weight", 64), (net.action_fc1.weight, "action_fc1.weight", 64 * 128),
+            (net.action_fc1.bias, "action_fc1.bias", 64), (net.action_fc2.weight, "action_fc2.weight", 64))
+    w = []
+    for t, name, n in spec:
+        if t.numel() != n:
+            raise ValueError(f"fnn_leaf_eval serves 64-wide networks: {name} has {t.numel()} values, need {n}")
+        w.append(_dev(t.detach().reshape(-1), name, torch.float32, (), n))
+    if head_biases is None:
+        head_biases = (net.value_fc.bias.detach().reshape(-1)[0].item(),
+                       net.action_fc2.bias.detach().reshape(-1)[0].item())
+    return w, float(head_biases[0]), float(head_biases[1])
 
 
 def random_positions(batch_size: int, expansion_mask: int, max_ply: int, seed: int, lockstep: bool = False):

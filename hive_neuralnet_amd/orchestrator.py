@@ -122,6 +122,9 @@ class FNNMCTSOrchestrator:
         self.last_leaves: torch.Tensor | None = None
         # (value_fc.bias, action_fc2.bias) on the host, read once per search ply
         self._head_biases: tuple[float, float] | None = None
+        # device workspace of the sync-free leaf evaluation (successor rows at
+        # capacity 256 per leaf), kept across waves
+        self._leaf_ws: torch.Tensor | None = None
 
     def enable_counters(self) -> None:
         self.counters = {k: torch.zeros((), dtype=torch.int64, device="cuda")
@@ -176,11 +179,12 @@ class FNNMCTSOrchestrator:
     def _eval_states(self, states, legal_moves, num_legal, total, root_features=None):
         """(priors [total, 256], leaf values [total], child Q [total, 256]).
 
-        The 64-wide presets run the fused path: successor features written
-        straight into the network input, then hg_fnn_leaf_eval (the whole
-        network and the heads on matrix cores, softmax and the [T, 256]
-        scatter).  Other widths run the torch composition of the reference
-        (_eval_states_torch)."""
+        The 64-wide presets run the fused path, hg_fnn_leaf_eval_lists: the
+        successor rows sized and mapped on the device (no host
+        synchronisation per wave), their features written straight into the
+        network input, then the whole network and the heads on matrix cores,
+        softmax and the [T, 256] scatter.  Other widths run the torch
+        composition of the reference (_eval_states_torch)."""
         if not self._fused_eval_ok():
             return self._eval_states_torch(states, legal_moves, num_legal, total, root_features)
         MAX_L = self._max_legal
@@ -189,19 +193,11 @@ class FNNMCTSOrchestrator:
         if total == 0:
             empty = torch.zeros(0, MAX_L, dtype=torch.float32, device="cuda")
             return empty, empty.new_zeros((0,)), empty
-        n64 = num_legal.to(torch.int64).clamp(0, MAX_L)
-        ends = torch.cumsum(n64, 0)
-        N = int(ends[-1].item())
-        offsets = ends - n64
-        X = torch.empty((total + N, root_features.shape[1]), dtype=torch.float32, device="cuda")
-        X[:total] = root_features
-        if N > 0:
-            a2r = torch.repeat_interleave(torch.arange(total, device="cuda"), n64, output_size=N)
-            mi = torch.arange(N, device="cuda") - offsets[a2r]
-            self.ext.fnn_successor_features_batch(states, legal_moves, a2r, mi, N, out=X[total:])
-        else:
-            a2r = torch.empty((0,), dtype=torch.int64, device="cuda")
-        return self.ext.fnn_leaf_eval(X, total, offsets, num_legal, a2r, self.net, self._head_biases)
+        need = self.ext.leaf_eval_workspace_bytes(total)
+        if self._leaf_ws is None or self._leaf_ws.numel() < need:
+            self._leaf_ws = torch.empty((need,), dtype=torch.uint8, device="cuda")
+        return self.ext.fnn_leaf_eval_lists(states, legal_moves, num_legal, root_features.contiguous(), total,
+                                            self.net, self._head_biases, self._leaf_ws)
 
     def _eval_states_torch(self, states, legal_moves, num_legal, total, root_features=None):
         MAX_L = self._max_legal

@@ -150,6 +150,31 @@ int hg_root_tactical_probe(const uint8_t* states, const uint8_t* legal_moves, co
 int hg_legal_mask(const uint8_t* states, int64_t B, uint8_t* moves, int32_t* num_legal, int32_t* actions,
                   float* masks, void* stream);
 
+/* Successor rows of a batch of leaves with the row count kept on the device
+ * (no counterpart in the reference, which sizes them on the host:
+ * fnn_mcts_orchestrator.py:243-316): offsets[T] int64 = exclusive prefix of
+ * the clamped num_legal, total int64 = their sum, the row map (leaf, slot) and
+ * features[total][122] of every successor in (leaf, slot) order
+ * (fnn_successor_features_kernel semantics, game_logic.cu:182-229).  features
+ * must hold T * 256 rows; workspace hg_successor_rows_workspace(T) bytes,
+ * 8-byte aligned: offsets, total, then the map. */
+int64_t hg_successor_rows_workspace(int64_t T);
+int hg_successor_rows(const uint8_t* states, const uint8_t* legal_moves, const int32_t* num_legal, int64_t T,
+                      void* workspace, float* features, void* stream);
+
+/* hg_fnn_leaf_eval over the leaves' own legal lists, with no host
+ * synchronisation: hg_successor_rows into the workspace, then the network
+ * (F = 122; the root rows are root_features [T][122]).  Outputs as
+ * hg_fnn_leaf_eval.  workspace: hg_fnn_leaf_eval_lists_workspace(T, F) bytes,
+ * 256-byte aligned (the successor rows at capacity T * 256). */
+int64_t hg_fnn_leaf_eval_lists_workspace(int64_t T, int F);
+int hg_fnn_leaf_eval_lists(const uint8_t* leaf_states, const uint8_t* legal_moves, const int32_t* num_legal,
+                           const float* root_features, int64_t T, int F, const float* fc1_w, const float* fc1_b,
+                           const float* ln_w, const float* ln_b, const float* fc2_w, const float* fc2_b,
+                           const float* value_w, float value_b, const float* action1_w, const float* action1_b,
+                           const float* action2_w, float action2_b, void* workspace, float* priors,
+                           float* root_values, float* child_q, void* stream);
+
 /* queen_escape_flags_batch -- game_logic.cu:1538-1554.  flags[B] uint8. */
 int hg_queen_escape_flags(const uint8_t* states, int64_t B, uint8_t* flags, void* stream);
 
