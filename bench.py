@@ -57,6 +57,8 @@ def parse_args():
     ap.add_argument("--mcts-plies", type=int, default=1, help="timed self-play plies")
     ap.add_argument("--mcts-warmup", type=int, default=1, help="untimed self-play plies before timing")
     ap.add_argument("--mcts-roots", choices=("empty", "midgame"), default="empty")
+    ap.add_argument("--graphs", choices=("auto", "on", "off"), default="auto",
+                    help="C5 simulation waves from HIP graphs: auto = waves under 8,192 rows")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 256 MiB device-to-device copy 3 times (rocprof counter calibration)")
     return ap.parse_args()
@@ -172,6 +174,7 @@ def mcts_leg(args):
     cfg = FNNMCTSConfig(num_simulations=S, max_num_considered_actions=16, batch_size=G,
                         max_tree_nodes=1 + S * 256)
     orch = FNNMCTSOrchestrator(net, cfg)
+    orch.use_graphs = {"auto": None, "on": True, "off": False}[args.graphs]
     ext = orch.ext
     if args.mcts_roots == "empty":
         states = ext.create_initial_states(G, 0)

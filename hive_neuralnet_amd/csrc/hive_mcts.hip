@@ -769,9 +769,50 @@ __global__ __launch_bounds__(64) void k_extract_policy(Tree T, const int32_t* __
     }
 }
 
+// Per-wave search counters in one workgroup: stats[0] += simulations that
+// reached a leaf, [1] += their leaf legal counts, [2] += their virtual-loss
+// path lengths, [3] += rows.  A single workgroup owns stats, so the update is
+// a plain read-modify-write ordered by the stream.
+__global__ __launch_bounds__(1024) void k_wave_stats(const int32_t* __restrict__ leaf_idx,
+                                                     const int32_t* __restrict__ num_legal,
+                                                     const int32_t* __restrict__ vl_lens, int64_t total,
+                                                     int64_t* __restrict__ stats) {
+    __shared__ int64_t part[3][16];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    int64_t a = 0, b = 0, c = 0;
+    for (int64_t i = tid; i < total; i += 1024) {
+        if (leaf_idx[i] < 0) continue;
+        a += 1;
+        b += num_legal[i];
+        c += vl_lens[i];
+    }
+    for (int off = 32; off > 0; off >>= 1) {
+        a += __shfl_xor(a, off);
+        b += __shfl_xor(b, off);
+        c += __shfl_xor(c, off);
+    }
+    if (lane == 0) { part[0][w] = a; part[1][w] = b; part[2][w] = c; }
+    __syncthreads();
+    if (tid < 3) {
+        int64_t sum = 0;
+        for (int k = 0; k < 16; k++) sum += part[tid][k];
+        stats[tid] += sum;
+    } else if (tid == 3) {
+        stats[3] += total;
+    }
+}
+
 }  // namespace
 
 extern "C" {
+
+int hg_mcts_wave_stats(const int32_t* leaf_idx, const int32_t* num_legal, const int32_t* vl_lens, int64_t total,
+                       int64_t* stats, void* stream) {
+    if (total <= 0) return 0;
+    hipLaunchKernelGGL(k_wave_stats, dim3(1), dim3(1024), 0, (hipStream_t)stream, leaf_idx, num_legal, vl_lens, total,
+                       stats);
+    return finish();
+}
 
 int hg_mcts_select_root_slots(const hg_tree* tree, const int8_t* game_active, const int32_t* root_nodes,
                               const int32_t* root_slots, int num_candidates, int max_root_children, float c_puct,

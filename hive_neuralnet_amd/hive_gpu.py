@@ -88,6 +88,7 @@ _SIGS = {
     "hg_mcts_root_noise": [_c_void_p, _c_void_p, _c_void_p, _c_int, ctypes.c_float, ctypes.c_float, _c_i64,
                            _c_void_p],
     "hg_mcts_reset_trees": [_c_void_p, _c_void_p, _c_void_p, _c_i64, _c_void_p],
+    "hg_mcts_wave_stats": [_c_void_p, _c_void_p, _c_void_p, _c_i64, _c_void_p, _c_void_p],
     "hg_legal_mask": [_c_void_p, _c_i64, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p],
     "hg_mcts_select": [_c_void_p, _c_void_p, _c_void_p, ctypes.c_float, _c_i64, _c_int, _c_void_p, _c_void_p,
                        _c_void_p, _c_void_p, _c_void_p, _c_void_p],
@@ -664,6 +665,18 @@ def _mcts_methods():
         _check(self._lib.hg_mcts_root_noise(ctypes.byref(tree), noise.data_ptr(), root_nodes.data_ptr(), pad,
                                             float(dir_eps), float(root_policy_temp), B, _stream()),
                "mcts_apply_root_noise")
+
+    def mcts_wave_stats(self, leaf_indices, num_legal, vl_lengths, total, stats):
+        """Search counters of one wave (no counterpart in the reference):
+        stats int64[4] += (leaves reached, their legal counts, their virtual-loss
+        path lengths, rows), in stream order."""
+        total = int(total)
+        _dev(leaf_indices, "leaf_indices", torch.int32, (), total)
+        _dev(num_legal, "num_legal", torch.int32, (), total)
+        _dev(vl_lengths, "vl_lengths", torch.int32, (), total)
+        _dev(stats, "stats", torch.int64, (), 4)
+        _check(self._lib.hg_mcts_wave_stats(leaf_indices.data_ptr(), num_legal.data_ptr(), vl_lengths.data_ptr(),
+                                            total, stats.data_ptr(), _stream()), "mcts_wave_stats")
 
     def mcts_reset_trees(self, vc, tv, pr, pa, vq, mb, ai, fc, nc, it, tv2, cnt, child_init_q, reset, root_node,
                          B, max_nodes):

@@ -313,6 +313,14 @@ int hg_mcts_expand_backprop_dense(const hg_tree* tree, const float* child_q_valu
 int hg_mcts_root_noise(const hg_tree* tree, const float* noise, const int32_t* root_nodes, int max_children_pad,
                        float dir_eps, float root_policy_temp, int64_t B, void* stream);
 
+/* Search counters of one simulation wave (no counterpart in the reference:
+ * instrumentation for throughput accounting).  Over rows t < total with
+ * leaf_idx[t] >= 0: stats[0] += 1, stats[1] += num_legal[t], stats[2] +=
+ * vl_lens[t]; and stats[3] += total.  stats is int64[4] in device memory,
+ * updated in stream order (calls on one stream accumulate). */
+int hg_mcts_wave_stats(const int32_t* leaf_idx, const int32_t* num_legal, const int32_t* vl_lens, int64_t total,
+                       int64_t* stats, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

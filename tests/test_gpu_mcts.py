@@ -97,3 +97,24 @@ def test_legal_mask_matches_oracle(roots):
     assert np.array_equal(gm.view(np.uint32), om.view(np.uint32))
     moves, n, masks = ge.ext.generate_legal_moves_and_mask_batch(ge.c(roots), roots.shape[0])
     assert np.array_equal(masks.cpu().numpy(), gm) and np.array_equal(n.cpu().numpy(), on)
+
+
+@pytest.mark.parametrize("total", [1, 1000, 5000])
+def test_wave_stats(total):
+    """hg_mcts_wave_stats accumulates (leaves reached, their legal counts,
+    their virtual-loss lengths, rows) in stream order over several calls."""
+    import torch
+    from hive_neuralnet_amd import hive_gpu
+    ext = hive_gpu.load_extension()
+    rng = np.random.default_rng(total)
+    stats = torch.zeros((4,), dtype=torch.int64, device="cuda")
+    want = np.zeros(4, np.int64)
+    for _ in range(3):
+        leaf = rng.integers(-1, 50, size=total).astype(np.int32)
+        nl = rng.integers(0, 257, size=total).astype(np.int32)
+        vl = rng.integers(0, 64, size=total).astype(np.int32)
+        ext.mcts_wave_stats(torch.from_numpy(leaf).cuda(), torch.from_numpy(nl).cuda(), torch.from_numpy(vl).cuda(),
+                            total, stats)
+        live = leaf >= 0
+        want += (live.sum(), nl[live].sum(), vl[live].sum(), total)
+    assert np.array_equal(stats.cpu().numpy(), want)

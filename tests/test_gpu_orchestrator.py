@@ -26,6 +26,7 @@ class Shadow:
 
     def __init__(self, orch, tree, monkeypatch):
         from oracle.mcts import MctsOracle
+        orch.use_graphs = False  # every call is checked on the host as it happens
         self.m = MctsOracle()
         self.orch, self.tree = orch, tree
         self.calls = {}
@@ -216,6 +217,7 @@ def test_search_ply_matches_numpy_orchestrator(monkeypatch, sims, mask, max_ply,
     monkeypatch.setattr(orch, "_eval_states", rec_eval)
     monkeypatch.setattr(torch, "rand", rec_rand)
     monkeypatch.setattr(ext, "mcts_apply_root_noise", rec_noise, raising=False)
+    orch.use_graphs = False  # the recording reads every evaluation on the host
     t0 = {k: _np(v).copy() for k, v in tree.items()}
     st = _np(states).copy()
     active = torch.ones((B,), dtype=torch.bool, device="cuda")
@@ -315,3 +317,37 @@ def test_reset_trees_equals_full_refill(M):
     expect["root_node"][rows] = 0
     orch._reset_games(tree, reset)
     assert tree_equal({k: _np(v) for k, v in expect.items()}, {k: _np(v) for k, v in tree.items()}) == []
+
+
+@pytest.mark.parametrize("mask,max_ply,wave_parallel", [(0, 60, True), (7, 90, True), (0, 40, False)])
+def test_graph_waves_equal_eager(mask, max_ply, wave_parallel):
+    """Simulation waves replayed from captured HIP graphs against the same
+    waves run eagerly: three plies (so each graph is replayed across rounds,
+    plies and tree rebases, with eager work and host reads in between), every
+    ply's choice, policy and visits and the final trees bit-identical."""
+    import torch
+    from hive_neuralnet_amd import hive_gpu
+    outs = []
+    for graphs in (False, True):
+        B = 16
+        orch, _, tree = _setup(B, 64, 8192, mask, max_ply, 71, wave_parallel=wave_parallel)
+        orch.use_graphs = graphs
+        states, _ = hive_gpu.random_positions(B, mask, max_ply, 72)
+        torch.manual_seed(73)
+        np.random.seed(73)
+        active = torch.ones((B,), dtype=torch.bool, device="cuda")
+        rec = []
+        for _ in range(3):
+            r = orch.search_ply(states, tree, active)
+            rec.append((_np(r.chosen_slot), _np(r.policy), _np(r.slot_visits)))
+            orch.apply_and_rebase(states, tree, r)
+            active &= orch.ext.check_results_batch(states, B) == 0
+        rec.append({k: _np(v).copy() for k, v in tree.items()})
+        if graphs:
+            assert len(orch._graphs) >= 1
+        outs.append(rec)
+    for a, b in zip(outs[0][:-1], outs[1][:-1]):
+        for x, y in zip(a, b):
+            assert np.array_equal(x.view(np.uint32) if x.dtype == np.float32 else x,
+                                  y.view(np.uint32) if y.dtype == np.float32 else y)
+    assert tree_equal(outs[0][-1], outs[1][-1]) == []
