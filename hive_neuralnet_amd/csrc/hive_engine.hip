@@ -122,25 +122,42 @@ __global__ __launch_bounds__(64) void k_actions(const uint8_t* __restrict__ stat
 // a zero state and move for rows that reference no valid (root, move)
 __device__ __attribute__((aligned(16))) const uint8_t kZeroRow[kStateBytes] = {};
 
-// fnn_successor_features_kernel (game_logic.cu:182-229): one lane group per (root, move).
-__global__ __launch_bounds__(64) void k_successor_features(const uint8_t* __restrict__ states,
+// rows of successor features per lane group: consecutive rows of one root
+// share the root's load
+constexpr int kSuccRows = 8;
+constexpr int64_t kSuccGrid = 16384;  // workgroups of the successor kernels (they stride beyond)
+// register budget of the successor kernels: 5 waves per SIMD (96 VGPRs, no
+// spills; the LDS board allows 5.5); left alone the row loop takes ~109
+constexpr int kSuccWaves = 5;
+
+// Row blocks of kSuccRows rows: lane group q of the grid takes blocks q,
+// q + 2 * gridDim.x, ... one row after another, as one stream (a root's
+// board carries over a block boundary).  The loop count is uniform over the
+// workgroup: both groups run while the first group's block is in range.
+HW_INL void successor_stream(const uint8_t* __restrict__ states, const uint8_t* __restrict__ legal,
+                             const int64_t* __restrict__ a2r, const int64_t* __restrict__ midx, int64_t N,
+                             int64_t num_roots, float* __restrict__ feat_out) {
+    __shared__ Pos PS[kPosPerWave];
+    const int grp = threadIdx.x >> 5;
+    const int64_t blocks = (N + kSuccRows - 1) / kSuccRows;
+    SuccessorStream st;
+    for (int64_t r = 0;; r++) {
+        const int lane = hw_opaque(threadIdx.x);
+        const int64_t p = blockIdx.x + (r / kSuccRows) * gridDim.x;
+        if (kPosPerWave * p >= blocks) break;
+        const int64_t i = (kPosPerWave * p + grp) * kSuccRows + r % kSuccRows;
+        successor_row(PS[grp], st, states, legal, a2r, midx, i, N, num_roots, kZeroRow, lane, feat_out);
+    }
+}
+
+// fnn_successor_features_kernel (game_logic.cu:182-229): kSuccRows (root, move)
+// rows per lane group, two groups per wave, the grid striding over the rows.
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kSuccWaves))) void k_successor_features(const uint8_t* __restrict__ states,
                                                            const uint8_t* __restrict__ legal,
                                                            const int64_t* __restrict__ a2r,
                                                            const int64_t* __restrict__ midx, int64_t N,
                                                            int64_t num_roots, float* __restrict__ feat_out) {
-    __shared__ Pos PS[kPosPerWave];
-    const int lane = threadIdx.x;
-    bool live;
-    const int64_t i = item_of(N, live);
-    const int64_t root = a2r[i];
-    const int64_t mi = midx[i];
-    const bool valid = root >= 0 && root < num_roots && mi >= 0 && mi < kMaxLegal;
-    const uint8_t* S = valid ? states + root * kStateBytes : kZeroRow;
-    const uint8_t* m = valid ? legal + (root * kMaxLegal + mi) * 6 : kZeroRow;
-    float* out = live ? feat_out + i * kFeat : nullptr;
-    run_successor(PS[lane >> 5], S, m, lane, valid ? out : nullptr);
-    if (live && !valid)  // out-of-range rows: zero features
-        for (int k = gl(lane); k < kFeat; k += kW) out[k] = 0.0f;
+    successor_stream(states, legal, a2r, midx, N, num_roots, feat_out);
 }
 
 __global__ __launch_bounds__(64) void k_queen_escape(const uint8_t* __restrict__ states, int64_t B,
@@ -215,8 +232,9 @@ __global__ void k_mask_scatter(const int32_t* __restrict__ actions, const int32_
 // count stays on the device.  k_rows_offsets: exclusive prefix of the
 // clamped legal counts (one workgroup, chunks of 1024 with a running carry)
 // and the total; k_rows_map: row -> (leaf, slot); k_successor_rows: the
-// successor features of rows < total, two per wave, the grid striding over
-// the rows (sized from the capacity, the count read on the device).
+// successor features of rows < total, kSuccRows per lane group, the grid
+// striding over the rows (sized from the capacity, the count read on the
+// device).
 __global__ __launch_bounds__(1024) void k_rows_offsets(const int32_t* __restrict__ nlegal, int64_t T,
                                                         int64_t* __restrict__ offsets, int64_t* __restrict__ total) {
     __shared__ int64_t wsum[16];
@@ -255,26 +273,13 @@ __global__ void k_rows_map(const int32_t* __restrict__ nlegal, const int64_t* __
     }
 }
 
-__global__ __launch_bounds__(64) void k_successor_rows(const uint8_t* __restrict__ states,
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kSuccWaves))) void k_successor_rows(const uint8_t* __restrict__ states,
                                                        const uint8_t* __restrict__ legal,
                                                        const int64_t* __restrict__ a2r,
                                                        const int64_t* __restrict__ midx,
                                                        const int64_t* __restrict__ total, int64_t num_roots,
                                                        float* __restrict__ feat_out) {
-    __shared__ Pos PS[kPosPerWave];
-    const int lane = threadIdx.x;
-    const int64_t N = *total;
-    for (int64_t p = blockIdx.x; kPosPerWave * p < N; p += gridDim.x) {  // uniform over the workgroup
-        const int64_t i0 = kPosPerWave * p + (lane >> 5);
-        const bool live = i0 < N;
-        const int64_t i = live ? i0 : kPosPerWave * p;
-        const int64_t root = a2r[i], mi = midx[i];
-        const bool valid = root >= 0 && root < num_roots && mi >= 0 && mi < kMaxLegal;
-        const uint8_t* S = valid ? states + root * kStateBytes : kZeroRow;
-        const uint8_t* m = valid ? legal + (root * kMaxLegal + mi) * 6 : kZeroRow;
-        run_successor(PS[lane >> 5], S, m, lane, live && valid ? feat_out + i * kFeat : nullptr);
-        __syncthreads();
-    }
+    successor_stream(states, legal, a2r, midx, *total, num_roots, feat_out);
 }
 
 inline int grid_for(int64_t n, int block) { return (int)((n + block - 1) / block); }
@@ -384,8 +389,8 @@ int hg_successor_rows(const uint8_t* states, const uint8_t* legal_moves, const i
     hipLaunchKernelGGL(k_rows_offsets, dim3(1), dim3(1024), 0, s, num_legal, T, offsets, total);
     hipLaunchKernelGGL(k_rows_map, dim3((unsigned)((T * kMaxLegal + 255) / 256)), dim3(256), 0, s, num_legal, offsets,
                        T, a2r, mi);
-    const int64_t pairs = (T * kMaxLegal + kPosPerWave - 1) / kPosPerWave;
-    const unsigned grid = (unsigned)(pairs < 65536 ? pairs : 65536);
+    const int64_t pairs = (T * kMaxLegal + kSuccRows * kPosPerWave - 1) / (kSuccRows * kPosPerWave);
+    const unsigned grid = (unsigned)(pairs < kSuccGrid ? pairs : kSuccGrid);
     hipLaunchKernelGGL(k_successor_rows, dim3(grid), dim3(64), 0, s, states, legal_moves, a2r, mi, total, T, features);
     return finish();
 }
@@ -394,8 +399,9 @@ int hg_fnn_successor_features(const uint8_t* states, const uint8_t* legal_moves,
                               const int64_t* action_to_root, const int64_t* move_indices, int64_t N, float* features,
                               void* stream) {
     if (N <= 0) return 0;
-    hipLaunchKernelGGL(k_successor_features, dim3((unsigned)grid_for(N, kPosPerWave)), dim3(64), 0, (hipStream_t)stream, states,
-                       legal_moves, action_to_root, move_indices, N, num_roots, features);
+    const int64_t pairs = (N + kSuccRows * kPosPerWave - 1) / (kSuccRows * kPosPerWave);
+    hipLaunchKernelGGL(k_successor_features, dim3((unsigned)(pairs < kSuccGrid ? pairs : kSuccGrid)), dim3(64), 0,
+                       (hipStream_t)stream, states, legal_moves, action_to_root, move_indices, N, num_roots, features);
     return finish();
 }
 

@@ -800,11 +800,10 @@ HW_INL void run_extract(Pos& P, ListSets& X, const uint8_t* __restrict__ S, cons
     features_finish(P, S, feat_row, lane, kFeatList, 0u, 0, &X);
 }
 
-// fnn_successor_features_kernel (game_logic.cu:182-229) for one (root, move)
-HW_INL void run_successor(Pos& P, const uint8_t* __restrict__ S, const uint8_t* __restrict__ m, int lane,
-                          float* __restrict__ feat_row) {
-    load_position(P, S, lane);
-    __syncthreads();
+// fnn_successor_features_kernel (game_logic.cu:182-229) for one (root, move),
+// the root's row S already on the board
+HW_INL void successor_on_board(Pos& P, const uint8_t* __restrict__ S, const uint8_t* __restrict__ m, int lane,
+                               float* __restrict__ feat_row) {
     if (gl(lane) == 0) apply_on_board(P, S, m[0], m[1], m[2] | (m[3] << 8), m[4] | (m[5] << 8));
     __syncthreads();
     build_occ_list(P, lane);
@@ -820,6 +819,48 @@ HW_INL void run_successor(Pos& P, const uint8_t* __restrict__ S, const uint8_t* 
     // stacked levels under a top piece are read from the root row: a single
     // move leaves every level under a top unchanged
     features_finish(P, S, feat_row, lane, kFeatBucket, bucket, n_place);
+}
+
+HW_INL void run_successor(Pos& P, const uint8_t* __restrict__ S, const uint8_t* __restrict__ m, int lane,
+                          float* __restrict__ feat_row) {
+    load_position(P, S, lane);
+    __syncthreads();
+    successor_on_board(P, S, m, lane, feat_row);
+}
+
+// Successor features of a stream of rows taken by one lane group: rows come
+// in (root, slot) order, so consecutive rows mostly share their root; the
+// root's row is loaded when the root changes and otherwise the board is
+// restored from registers (BaseRegs).  A row at or past N produces nothing;
+// a row whose root or slot is out of range gets zero features.  zero_row: a
+// state row and move of zero bytes.
+struct SuccessorStream {
+    BaseRegs R;
+    int64_t cur = -2;  // root whose base R holds (-1: the zero row)
+};
+
+HW_INL void successor_row(Pos& P, SuccessorStream& st, const uint8_t* __restrict__ states,
+                          const uint8_t* __restrict__ legal, const int64_t* __restrict__ a2r,
+                          const int64_t* __restrict__ midx, int64_t i, int64_t N, int64_t num_roots,
+                          const uint8_t* __restrict__ zero_row, int lane, float* __restrict__ feat_out) {
+    const bool live = i < N;
+    int64_t root = live ? a2r[i] : -1;
+    const int64_t mi = live ? midx[i] : -1;
+    const bool valid = root >= 0 && root < num_roots && mi >= 0 && mi < kMaxLegal;
+    if (!valid) root = -1;
+    const uint8_t* S = valid ? states + root * kStateBytes : zero_row;
+    const uint8_t* m = valid ? legal + (root * kMaxLegal + mi) * 6 : zero_row;
+    const bool fresh = root != st.cur;
+    if (fresh) load_position(P, S, lane);
+    else restore_base(P, st.R, lane);
+    __syncthreads();
+    if (fresh) save_base(P, st.R, lane);
+    st.cur = root;
+    __syncthreads();
+    successor_on_board(P, S, m, lane, live && valid ? feat_out + i * kFeat : nullptr);
+    if (live && !valid)
+        for (int k = gl(lane); k < kFeat; k += kW) feat_out[i * kFeat + k] = 0.0f;
+    __syncthreads();
 }
 
 HW_INL bool run_queen_escape(Pos& P, const uint8_t* __restrict__ S, int lane) {

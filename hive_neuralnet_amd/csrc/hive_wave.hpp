@@ -24,6 +24,7 @@
 // with the height array, as apply keeps them.
 #pragma once
 
+#include <stddef.h>
 #include <stdint.h>
 
 #include "hw_target.hpp"
@@ -341,6 +342,49 @@ HW_INL void load_position(Pos& P, const uint8_t* __restrict__ S, int lane) {
         P.qplaced = (uint8_t)(m5 >> 16);
         P.result = (uint8_t)(m5 >> 24);
         P.stun = (uint16_t)m6;
+    }
+}
+
+// A loaded board's base fields -- everything load_position writes -- held in
+// the group's registers: lane l keeps its 16-cell chunks l and (l < 2) 32 + l,
+// the bitboard words l + 1 (l < 18) and metadata word l - 24 (24 <= l < 31;
+// queen squares, turn, stun, hands, queen-placed, result).  restore_base puts
+// them back after a move was applied on the board, so the successors of one
+// parent read its row once.  Only load_position and apply_on_board write these
+// fields; the later passes rebuild everything else of the board.
+struct BaseRegs {
+    u32x4 c0, c1;
+    uint32_t occ, wt, bt, meta;
+};
+static_assert(offsetof(Pos, queen) % 4 == 0 && offsetof(Pos, turn) == offsetof(Pos, queen) + 4 &&
+                  offsetof(Pos, stun) == offsetof(Pos, queen) + 6 && offsetof(Pos, hand) == offsetof(Pos, queen) + 8 &&
+                  offsetof(Pos, qplaced) == offsetof(Pos, queen) + 24 &&
+                  offsetof(Pos, result) == offsetof(Pos, queen) + 25 && offsetof(Pos, cell) % 16 == 0,
+              "metadata words and cell chunks");
+
+HW_INL void save_base(const Pos& P, BaseRegs& R, int lane) {  // after the barrier that follows the load
+    const int l = gl(lane);
+    const uint32_t* cell32 = reinterpret_cast<const uint32_t*>(P.cell);
+    R.c0 = *reinterpret_cast<const u32x4*>(cell32 + 4 * l);
+    u32x4 z = {0u, 0u, 0u, 0u};
+    R.c1 = l < 34 - kW ? *reinterpret_cast<const u32x4*>(cell32 + 4 * (kW + l)) : z;
+    R.occ = l < 18 ? P.occ[l + 1] : 0u;
+    R.wt = l < 18 ? P.wt[l + 1] : 0u;
+    R.bt = l < 18 ? P.bt[l + 1] : 0u;
+    R.meta = (l >= 24 && l < 31) ? reinterpret_cast<const uint32_t*>(P.queen)[l - 24] : 0u;
+}
+
+HW_INL void restore_base(Pos& P, const BaseRegs& R, int lane) {
+    const int l = gl(lane);
+    uint32_t* cell32 = reinterpret_cast<uint32_t*>(P.cell);
+    *reinterpret_cast<u32x4*>(cell32 + 4 * l) = R.c0;
+    if (l < 34 - kW) *reinterpret_cast<u32x4*>(cell32 + 4 * (kW + l)) = R.c1;
+    if (l < 18) {
+        P.occ[l + 1] = R.occ;
+        P.wt[l + 1] = R.wt;
+        P.bt[l + 1] = R.bt;
+    } else if (l >= 24 && l < 31) {
+        reinterpret_cast<uint32_t*>(P.queen)[l - 24] = R.meta;
     }
 }
 

@@ -14,6 +14,18 @@
 // occupancy of the inlined form for k_legal).
 #define HW_INL __device__ __attribute__((always_inline)) inline
 
+// v, opaque to the optimiser: values derived from it inside a loop body are
+// recomputed per iteration instead of being hoisted and kept in registers
+// across the whole body (which costs occupancy in the large programs)
+#ifdef HW_HOST_EMU
+inline int hw_opaque(int v) { return v; }
+#else
+__device__ __forceinline__ int hw_opaque(int v) {
+    asm volatile("" : "+v"(v));
+    return v;
+}
+#endif
+
 // true in every lane of the wavefront when p holds in any of its lanes
 #ifndef HW_HOST_EMU
 __device__ __forceinline__ bool hw_wave_any(bool p) { return __ballot(p) != 0; }

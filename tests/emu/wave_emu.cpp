@@ -64,6 +64,20 @@ void emu_successor(const uint8_t* states, const uint8_t* legal, const int64_t* a
                       live ? feat + i * kFeat : nullptr);
     });
 }
+// k_successor_features' row streams with blocks of 4 rows and one workgroup
+// (each group's stream runs through the blocks 2w + group), the board of a
+// run of rows with one root restored from registers
+void emu_successor_rows(const uint8_t* states, const uint8_t* legal, const int64_t* a2r, const int64_t* midx,
+                        int64_t N, int64_t num_roots, float* feat) {
+    static const uint8_t zero_row[kStateBytes] = {};
+    const int64_t blocks = (N + 3) / 4;
+    static SuccessorStream st[64];
+    for (auto& s : st) s = SuccessorStream();
+    run_group(64, (blocks + kPosPerWave - 1) / kPosPerWave * 4, [&](int64_t r, int t) {
+        int64_t q = (r / 4) * kPosPerWave + t / kW;
+        successor_row(g_pos[t / kW], st[t], states, legal, a2r, midx, q * 4 + r % 4, N, num_roots, zero_row, t, feat);
+    });
+}
 void emu_queen_escape(const uint8_t* states, int64_t B, uint8_t* out) {
     run_group(64, (B + kPosPerWave - 1) / kPosPerWave, [&](int64_t w, int t) {
         int64_t i = w * kPosPerWave + t / kW;

@@ -61,6 +61,86 @@ def test_emulated_successors_queen_escape(emu, name):
     assert np.array_equal(q, g["queen_escape"][:64])
 
 
+def test_emulated_successor_rows(emu):
+    """The blocked successor program (a root's row loaded once per run of its
+    rows, the board restored from registers between them) against the
+    reference's successor vectors, with runs that start mid-block, a root
+    that recurs after another, and out-of-range rows (zero features)."""
+    g = load_golden("c2")
+    k = 90
+    roots = np.ascontiguousarray(g["succ_root"][:k]).copy()
+    idx = np.ascontiguousarray(g["succ_idx"][:k]).copy()
+    want = g["succ_features"][:k].copy()
+    # a recurring root after a different one, and two bad rows
+    roots = np.concatenate([roots[:7], roots[40:43], roots[7:12], [-1, roots[0]], roots[12:]])
+    idx = np.concatenate([idx[:7], idx[40:43], idx[7:12], [0, 300], idx[12:]])
+    want = np.concatenate([want[:7], want[40:43], want[7:12], np.zeros((2, 122), np.float32), want[12:]])
+    st = np.ascontiguousarray(g["states"])
+    mv = np.ascontiguousarray(g["moves"])
+    n = len(roots)
+    f = np.full((n, 122), np.nan, np.float32)
+    roots, idx = roots.astype(np.int64), idx.astype(np.int64)
+    emu.emu_successor_rows(_p(st), _p(mv), _p(roots), _p(idx), ctypes.c_int64(n), ctypes.c_int64(st.shape[0]), _p(f))
+    assert np.array_equal(f.view(np.uint32), want.view(np.uint32))
+
+
+def _shift_down(st, r):
+    """The position moved r grid rows down (cells + 23 r): stacks, heights,
+    bitboards, queen squares and the stunned cell; every piece must stay on
+    the grid."""
+    d = 23 * r
+    out = st.copy()
+    lv = st[:5 * 529].reshape(5, 529)
+    out[:5 * 529] = np.concatenate([np.zeros((5, d), np.uint8), lv[:, :529 - d]], axis=1).ravel()
+    h = st[2645:2645 + 529]
+    assert not h[529 - d:].any()
+    out[2645:2645 + 529] = np.concatenate([np.zeros(d, np.uint8), h[:529 - d]])
+    for off in (3176, 3248, 3320):
+        bits = np.unpackbits(st[off:off + 72], bitorder="little")[:529]
+        nb = np.zeros(576, np.uint8)
+        nb[d:529] = bits[:529 - d]
+        out[off:off + 72] = np.packbits(nb, bitorder="little")
+    for off in (3392, 3394, 3416):
+        c = int(st[off]) | (int(st[off + 1]) << 8)
+        if c < 529:
+            c += d
+            out[off], out[off + 1] = c & 255, c >> 8
+    return out
+
+
+def test_emulated_successor_rows_grid_edge(emu, oracle):
+    """Blocked successor rows of positions moved to the bottom rows of the
+    grid, where moves write cells 506-528 (cells 512-528 are the last two
+    16-cell chunks, which lanes 0 and 1 restore), against the oracle's
+    successor features."""
+    g = load_golden("c3")
+    states = []
+    for st in g["states"][:40]:
+        h = st[2645:2645 + 529]
+        occ = np.nonzero(h)[0]
+        if len(occ) < 6:
+            continue
+        r = 22 - int(occ.max()) // 23
+        if r > 0:
+            states.append(_shift_down(st, r))
+        if len(states) == 3:
+            break
+    st = np.ascontiguousarray(np.stack(states))
+    mv, n, _, _ = oracle.batch_legal_features_actions(st)
+    to = mv[..., 4].astype(np.int64) | (mv[..., 5].astype(np.int64) << 8)
+    assert (to >= 512).any()
+    roots = np.concatenate([np.full(int(k), i, np.int64) for i, k in enumerate(n)])
+    # each root's rows ordered by destination, so that moves to one cell follow
+    # each other inside a run (a board not restored would keep the last one)
+    idx = np.concatenate([np.argsort(to[i, :int(k)], kind="stable").astype(np.int64) for i, k in enumerate(n)])
+    want = oracle.batch_successor_features(st, mv, roots, idx)
+    f = np.full((len(roots), 122), np.nan, np.float32)
+    mv = np.ascontiguousarray(mv)
+    emu.emu_successor_rows(_p(st), _p(mv), _p(roots), _p(idx), ctypes.c_int64(len(roots)),
+                           ctypes.c_int64(st.shape[0]), _p(f))
+    assert np.array_equal(f.view(np.uint32), want.view(np.uint32))
+
+
 def test_emulated_root_tactical_probe(emu):
     """hive_probe.hpp's group programs, orchestrated as hive_probe.hip's
     launches, against the reference's probe vectors: four positions of every
