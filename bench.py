@@ -33,6 +33,7 @@ sys.path.insert(0, ROOT)
 
 BYTES_PER_POSITION = 3424 + 256 * 6 + 4 + 122 * 4 + 256 * 4  # 6476
 HBM_PEAK_GBS = 8000.0
+C4_BYTES_PER_PLY = 2 * 3424  # lockstep random play, unfused model: the state read and written back
 SEED = 0x5EED
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "k_legal_c2_traffic.txt")
 
@@ -52,6 +53,11 @@ def parse_args():
     ap.add_argument("--mcts-only", action="store_true", help="run only the C5 leg (its own JSON line)")
     ap.add_argument("--no-probe", action="store_true", help="skip the root tactical probe leg")
     ap.add_argument("--no-train", action="store_true", help="skip the training forward-batch leg")
+    ap.add_argument("--no-c4", action="store_true", help="skip the C4 lockstep random-play leg")
+    ap.add_argument("--c4-games", type=int, default=16384)
+    ap.add_argument("--c4-plies", type=int, default=300)
+    ap.add_argument("--mcts-waves", choices=("schedule", "1"), default="schedule",
+                    help="C5 simulations per candidate per wave: the (2,4,8,16) schedule or 1")
     ap.add_argument("--mcts-games", type=int, default=512)
     ap.add_argument("--mcts-sims", type=int, default=4096)
     ap.add_argument("--mcts-plies", type=int, default=1, help="timed self-play plies")
@@ -172,7 +178,7 @@ def mcts_leg(args):
     G, S = args.mcts_games, args.mcts_sims
     net = seeded_large(SEED)
     cfg = FNNMCTSConfig(num_simulations=S, max_num_considered_actions=16, batch_size=G,
-                        max_tree_nodes=1 + S * 256)
+                        max_tree_nodes=1 + S * 256, wave_parallel=args.mcts_waves == "schedule")
     orch = FNNMCTSOrchestrator(net, cfg)
     orch.use_graphs = {"auto": None, "on": True, "off": False}[args.graphs]
     ext = orch.ext
@@ -211,7 +217,9 @@ def mcts_leg(args):
         "warmup_plies": args.mcts_warmup, "ms_per_ply": wall / args.mcts_plies * 1e3,
         "config": {"workload": f"C5: Gumbel-root self-play, {G} games from the "
                                f"{'empty board' if args.mcts_roots == 'empty' else 'C2-style mid-game roots'}, "
-                               f"{S} sims/move, k=16, wave schedule (2,4,8,16), FNN large random init",
+                               f"{S} sims/move, k=16, "
+                               f"{'wave schedule (2,4,8,16)' if cfg.wave_parallel else 'one simulation per candidate per wave'}, "
+                               "FNN large random init",
                    "games": G, "sims_per_move": S, "max_tree_nodes": 1 + S * 256, "seed": SEED,
                    "roots": args.mcts_roots},
         "simulations": sims, "sim_rows": c["rows"], "mean_leaf_legal": Lm, "mean_vl_len": Dm,
@@ -291,6 +299,75 @@ def train_leg(args):
             "positions_per_s": B / ms * 1e3, "successor_rows_per_s": succ.shape[0] / ms * 1e3,
             "config": {"workload": "2,048 base-game positions (plies U[0,120]) + all legal successors, uncached",
                        "batch": B, "successor_rows": int(succ.shape[0])}}
+
+
+def fnv1a64_rows(states_np):
+    """FNV-1a-64 of each state row, padding bytes 3174-3175 and 3420-3423
+    masked to zero (they carry no state)."""
+    import numpy as np
+    x = states_np.copy()
+    x[:, 3174:3176] = 0
+    x[:, 3420:3424] = 0
+    h = np.full(x.shape[0], 0xCBF29CE484222325, dtype=np.uint64)
+    prime = np.uint64(0x100000001B3)
+    with np.errstate(over="ignore"):
+        for j in range(x.shape[1]):
+            h ^= x[:, j].astype(np.uint64)
+            h *= prime
+    return h
+
+
+def fnv1a64_of(hashes):
+    """FNV-1a-64 over the little-endian bytes of a hash list."""
+    import numpy as np
+    return int(fnv1a64_rows(hashes.astype("<u8").view(np.uint8).reshape(1, -1))[0])
+
+
+def c4_leg(args):
+    """C4: 16,384 lockstep random games from the empty board, up to 300 plies,
+    Philox (seed, game, ply) move choice; every ply one legal-move generation
+    over all games and one move step (finished games stay put)."""
+    import numpy as np
+    import torch
+    from hive_neuralnet_amd import hive_gpu
+    G, P = args.c4_games, args.c4_plies
+    hive_gpu.random_positions(256, 0, 8, SEED + 3, lockstep=True)  # warm
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    states, plies = hive_gpu.random_positions(G, 0, P, SEED + 3, lockstep=True)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    done = int(plies.sum().item())
+    finals = states.cpu().numpy()
+    hashes = fnv1a64_rows(finals)
+    results = finals[:, 3415]
+    out = {"metric": "lockstep random-play plies/s", "value": done / wall, "unit": "plies/s", "ms": wall * 1e3,
+           "config": {"workload": f"C4: {G} lockstep games, base game, up to {P} plies, Philox (seed, game, ply)",
+                      "games": G, "max_plies": P, "seed": SEED + 3},
+           "plies_played": done, "games_decided": int((results != 0).sum()),
+           "roofline": {"bound": "hbm", "achieved": done * C4_BYTES_PER_PLY / wall / 1e9, "peak": HBM_PEAK_GBS,
+                        "unit": "GB/s", "frac": done * C4_BYTES_PER_PLY / wall / 1e9 / HBM_PEAK_GBS, "traffic": None,
+                        "bytes_per_ply": C4_BYTES_PER_PLY, "model": "unfused: state read + write-back per ply"},
+           "final_state_hash": f"{fnv1a64_of(hashes):016x}"}
+    if not args.no_cpu:
+        from oracle import Oracle
+        threads = args.cpu_threads or max(1, min(16, os.cpu_count() or 1))
+        orc = Oracle()
+        k = min(G, 64)
+        t1 = time.perf_counter()
+        orc.lockstep_selfplay(k, 0, P, SEED + 3, threads=threads)
+        one = (time.perf_counter() - t1) / k
+        k = int(max(64, min(G, args.cpu_seconds / max(one * threads, 1e-9))))  # ~cpu_seconds of thread time
+        t1 = time.perf_counter()
+        cst, cpl = orc.lockstep_selfplay(k, 0, P, SEED + 3, threads=threads)
+        cw = time.perf_counter() - t1
+        out["cpu_baseline"] = {
+            "value": int(cpl.sum()) / cw, "unit": "plies/s", "cores": threads, "kind": "port",
+            "sample": f"the first {k} of the {G} games replayed by oracle/hive_oracle.c ({threads} pthreads)",
+            "final_states_match": bool(np.array_equal(fnv1a64_rows(cst), hashes[:k])
+                                       and np.array_equal(cpl, plies[:k].cpu().numpy())),
+        }
+    return out
 
 
 def main():
@@ -394,6 +471,8 @@ def main():
         result["probe"] = probe_leg(args)
     if not args.no_train:
         result["train"] = train_leg(args)
+    if not args.no_c4:
+        result["c4"] = c4_leg(args)
     print(json.dumps(result))
 
 
