@@ -362,10 +362,14 @@ struct LeafIn {
 // :971-1062 body); returns 1 when this simulation created the children.
 HW_INL int expand_leaf(const Tree& T, int64_t g, int64_t sim, const LeafIn& L, int lane) {
     const int64_t g0 = g * T.M;
-    int leaf = L.leaf[sim];
-    int64_t li = g0 + leaf;
+    const int leaf = L.leaf[sim];
+    const int64_t li = g0 + leaf;
     const uint8_t* S = L.states + sim * kStateBytes;
-    int res = L.results[sim];
+    // every value the decision needs, loaded together (one memory round trip)
+    const int res = L.results[sim];
+    const int fc = T.fc[li];
+    const int n = L.nlegal[sim];
+    const int base = T.cnt[g];
     if (res != 0) {
         if (lane == 0) {
             T.it[li] = 1;
@@ -374,10 +378,8 @@ HW_INL int expand_leaf(const Tree& T, int64_t g, int64_t sim, const LeafIn& L, i
         __syncthreads();
         return 0;
     }
-    if (T.fc[li] != -1) return 0;
-    int n = L.nlegal[sim];
+    if (fc != -1) return 0;
     if (n <= 0) return 0;
-    int base = T.cnt[g];
     if ((int64_t)base + n > T.M) return 0;  // pool exhausted: leaf stays unexpanded
     int cq, cr;
     row_centroid(S, lane, cq, cr);
@@ -431,16 +433,47 @@ __global__ __launch_bounds__(64) void k_expand_backprop(Tree T, LeafIn L, const 
     if (g >= B) return;
     const int64_t g0 = g * T.M;
     for (int64_t sim = g; sim < total; sim += B) {
-        int leaf = L.leaf[sim];
+        const int leaf = L.leaf[sim];
         if (leaf < 0) continue;
-        int e = expand_leaf(T, g, sim, L, lane);
-        if (lane == 0) {
-            int64_t li = g0 + leaf;
-            float v = T.it[li] ? T.tval[li] : (e ? nn_values[sim] : 0.0f);
-            int n = vl_lens[sim];
-            const int32_t* vp = vl_paths + sim * kDepth;
-            for (int k = 0; k < n && k < kDepth; k++) {
-                int64_t ni = g0 + vp[k];
+        int n = vl_lens[sim];
+        n = n < 0 ? 0 : (n > kDepth ? kDepth : n);
+        const int32_t* vp = vl_paths + sim * kDepth;
+        const int last = n > 0 ? vp[n - 1] : leaf;
+        const int e = expand_leaf(T, g, sim, L, lane);
+        const int64_t li = g0 + leaf;
+        const float v = T.it[li] ? T.tval[li] : (e ? nn_values[sim] : 0.0f);
+        if (last == leaf) {
+            // The selection entered vp[0..n) below the root, each node a child
+            // of the one before, so the backup chain leaf -> root is that path
+            // reversed, then the root.  Each node takes the virtual-loss undo
+            // then the value, as the serial walk below does; the nodes are
+            // distinct, so lanes take them side by side.
+            for (int k = lane; k < n; k += 64) {
+                const int64_t ni = g0 + vp[k];
+                const float sv = ((n - 1 - k) & 1) ? -v : v;
+                if (q_penalty > 0.0f) {
+                    T.vq[ni] += -q_penalty;
+                    T.vc[ni] += 1;
+                    T.tv[ni] += sv;
+                } else {  // visits -1 then +1; value +1.0 then the backed-up value
+                    const float t = T.tv[ni] + 1.0f;
+                    T.tv[ni] = t + sv;
+                }
+            }
+            if (lane == 0) {  // the root, and any node above it
+                int node = n > 0 ? T.pa[g0 + vp[0]] : leaf;
+                float w = (n & 1) ? -v : v;
+                for (int s = n; s < kDepth + 1 && node >= 0; s++) {
+                    const int64_t ni = g0 + node;
+                    T.vc[ni] += 1;
+                    T.tv[ni] += w;
+                    w = -w;
+                    node = T.pa[ni];
+                }
+            }
+        } else if (lane == 0) {  // not a selection path: the reference's serial walk
+            for (int k = 0; k < n; k++) {
+                const int64_t ni = g0 + vp[k];
                 if (q_penalty > 0.0f) {
                     T.vq[ni] += -q_penalty;
                 } else {
@@ -448,12 +481,13 @@ __global__ __launch_bounds__(64) void k_expand_backprop(Tree T, LeafIn L, const 
                     T.tv[ni] += 1.0f;
                 }
             }
+            float w = v;
             int node = leaf;
             for (int s = 0; s < kDepth + 1 && node >= 0; s++) {
-                int64_t ni = g0 + node;
+                const int64_t ni = g0 + node;
                 T.vc[ni] += 1;
-                T.tv[ni] += v;
-                v = -v;
+                T.tv[ni] += w;
+                w = -w;
                 node = T.pa[ni];
             }
         }

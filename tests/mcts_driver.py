@@ -52,19 +52,19 @@ class OracleEngine:
     def root_noise(self, t, noise, eps):
         self.m.root_noise(t, noise, t["root_node"], eps)
 
-    def select_slots(self, t, active, slots, max_root, c_puct, W):
-        return self.m.select_slots(t, active, t["root_node"], slots, max_root, c_puct, W)
+    def select_slots(self, t, active, slots, max_root, c_puct, W, det=False, sigma=4.0, qp=0.0):
+        return self.m.select_slots(t, active, t["root_node"], slots, max_root, c_puct, W, det, sigma, qp)
 
-    def select_mask(self, t, active, alive, c_puct, W):
-        return self.m.select_mask(t, active, t["root_node"], alive, c_puct, W)
+    def select_mask(self, t, active, alive, c_puct, W, det=False, sigma=4.0, qp=0.0):
+        return self.m.select_mask(t, active, t["root_node"], alive, c_puct, W, det, sigma, qp)
 
     def replay(self, roots, paths, plen, leaf):
         leaves = np.zeros((leaf.shape[0], 3424), np.uint8)
         self.m.replay(roots, leaves, paths, plen, leaf)
         return leaves
 
-    def expand_backprop(self, t, cq, leaf, states, legal, n, pri, results, vals, vl, vlen):
-        self.m.expand_backprop_dense(t, cq, leaf, states, legal, n, pri, results, vals, vl, vlen)
+    def expand_backprop(self, t, cq, leaf, states, legal, n, pri, results, vals, vl, vlen, qp=0.0):
+        self.m.expand_backprop_dense(t, cq, leaf, states, legal, n, pri, results, vals, vl, vlen, qp)
 
 
 def _oracle_legacy(cls):
@@ -137,18 +137,18 @@ class GpuEngine:
         self.ext.mcts_apply_root_noise(*self.args(t), self.c(noise.astype(np.float32)), t["root_node"],
                                        noise.shape[1], eps, 1.0, B, self.M(t))
 
-    def select_slots(self, t, active, slots, max_root, c_puct, W):
+    def select_slots(self, t, active, slots, max_root, c_puct, W, det=False, sigma=4.0, qp=0.0):
         B, C = slots.shape
         out = self.ext.mcts_select_with_root_slots_batch(
             *self.args(t), t["child_init_q"], self.c(active.astype(np.int8)), t["root_node"],
-            self.c(slots.astype(np.int32)), C, max_root, c_puct, B, W, self.M(t))
+            self.c(slots.astype(np.int32)), C, max_root, c_puct, B, W, self.M(t), det, sigma, qp)
         return tuple(o.cpu().numpy() for o in out)
 
-    def select_mask(self, t, active, alive, c_puct, W):
+    def select_mask(self, t, active, alive, c_puct, W, det=False, sigma=4.0, qp=0.0):
         B, max_root = alive.shape
         out = self.ext.mcts_select_with_root_mask_batch(
             *self.args(t), t["child_init_q"], self.c(active.astype(np.int8)), t["root_node"],
-            self.c(alive.astype(np.int8)), max_root, c_puct, B, W, self.M(t))
+            self.c(alive.astype(np.int8)), max_root, c_puct, B, W, self.M(t), det, sigma, qp)
         return tuple(o.cpu().numpy() for o in out)
 
     def replay(self, roots, paths, plen, leaf):
@@ -158,11 +158,11 @@ class GpuEngine:
                                    roots.shape[0], total)
         return leaves.cpu().numpy()
 
-    def expand_backprop(self, t, cq, leaf, states, legal, n, pri, results, vals, vl, vlen):
+    def expand_backprop(self, t, cq, leaf, states, legal, n, pri, results, vals, vl, vlen, qp=0.0):
         B = t["node_count"].shape[0]
         self.ext.mcts_expand_and_backprop_dense_priors_batch(
             *self.args(t), t["child_init_q"], self.c(cq), self.c(leaf), self.c(states), self.c(legal), self.c(n),
-            self.c(pri), self.c(results), self.c(vals), self.c(vl), self.c(vlen), B, leaf.shape[0], self.M(t), 0.0)
+            self.c(pri), self.c(results), self.c(vals), self.c(vl), self.c(vlen), B, leaf.shape[0], self.M(t), qp)
 
 
 def _gpu_legacy(cls):
@@ -246,8 +246,11 @@ def run_search_legacy(engine, roots, *, seed=3, M=4096, W=2, waves=5, c_puct=1.2
     return engine.to_np(t), records, policies
 
 
-def run_search(engine, roots, *, seed=1, M=4096, C=4, W=2, waves=6, c_puct=1.25, eps=0.25, mode="slots", dup=False):
-    """Root expand + noise + `waves` select/replay/legal/expand-backup rounds.
+def run_search(engine, roots, *, seed=1, M=4096, C=4, W=2, waves=6, c_puct=1.25, eps=0.25, mode="slots", dup=False,
+               det=False, sigma=4.0, qp=0.0):
+    """Root expand + noise + `waves` select/replay/legal/expand-backup rounds
+    (det: completed-Q descent below the root with q penalty qp, as the
+    orchestrator's deterministic_non_root mode).
 
     Returns (final tree as numpy, list of per-wave records)."""
     rng = np.random.default_rng(seed)
@@ -275,16 +278,16 @@ def run_search(engine, roots, *, seed=1, M=4096, C=4, W=2, waves=6, c_puct=1.25,
     records = [{"was_root": was, "post_visits": engine.to_np(t)["visit_count"].copy(), "start": start_visits}]
     for _ in range(waves):
         if mode == "slots":
-            leaf, paths, plen, vl, vlen = engine.select_slots(t, active, slots, MAX_LEGAL, c_puct, W)
+            leaf, paths, plen, vl, vlen = engine.select_slots(t, active, slots, MAX_LEGAL, c_puct, W, det, sigma, qp)
         else:
-            leaf, paths, plen, vl, vlen = engine.select_mask(t, active, alive, c_puct, W)
+            leaf, paths, plen, vl, vlen = engine.select_mask(t, active, alive, c_puct, W, det, sigma, qp)
         leaves = engine.replay(roots, paths, plen, leaf)
         res = leaves[:, 3415].astype(np.int32)
         lm, ln = engine.legal(leaves)
         p2, v2, q2 = synthetic_eval(rng, ln, leaf.shape[0])
         mid = engine.to_np(t)
         mid_visits, mid_total = mid["visit_count"].copy(), mid["total_value"].copy()
-        engine.expand_backprop(t, q2, leaf, leaves, lm, ln, p2, res, v2, vl, vlen)
+        engine.expand_backprop(t, q2, leaf, leaves, lm, ln, p2, res, v2, vl, vlen, qp)
         post_visits = engine.to_np(t)["visit_count"].copy()
         records.append({"leaf": leaf, "paths": paths, "plen": plen, "vl": vl, "vlen": vlen, "leaves": leaves,
                         "mid_visits": mid_visits, "mid_total": mid_total, "post_visits": post_visits})

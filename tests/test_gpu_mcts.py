@@ -36,6 +36,21 @@ def test_search_matches_oracle(roots, mode, W, C, M, dup):
         assert np.array_equal(a["mid_total"].view(np.uint32), b["mid_total"].view(np.uint32))
 
 
+@pytest.mark.parametrize("mode,W,qp", [("slots", 2, 0.25), ("slots", 1, 0.0), ("mask", 3, 0.25)],
+                         ids=["slots-w2-penalty", "slots-w1", "mask-w3-penalty"])
+def test_search_completed_q_matches_oracle(roots, mode, W, qp):
+    """deterministic_non_root: completed-Q descent below the root, the q
+    penalty as virtual loss (W > 1) and its undo in the backup."""
+    kw = dict(W=W, C=4, M=8192, mode=mode, waves=6, det=True, sigma=4.0, qp=qp)
+    ot, orec = run_search(OracleEngine(), roots, **kw)
+    gt, grec = run_search(GpuEngine(), roots, **kw)
+    assert tree_equal(ot, gt) == []
+    for a, b in zip(orec[1:], grec[1:]):
+        for k in ("leaf", "paths", "plen", "vl", "vlen", "leaves", "mid_visits"):
+            assert np.array_equal(a[k], b[k]), k
+        assert np.array_equal(a["mid_total"].view(np.uint32), b["mid_total"].view(np.uint32))
+
+
 def test_fused_select_replay_legal_fnn(roots):
     import torch
     eng = GpuEngine()
