@@ -156,38 +156,128 @@ __device__ __forceinline__ void enter(const Tree& T, int64_t g0, int node, bool 
     __syncthreads();  // later reads of this game's statistics see the update
 }
 
-// PUCT descent below `node` (mcts_tree.cuh:895-950 / 729-795 below the root).
-HW_INL int descend(const Tree& T, int64_t g0, int node, int first_iter, float c_puct, bool det, float sigma,
-                       float q_penalty, const SelectOut& O, int64_t sim, int& plen, int& vlen, int lane) {
-    for (int it = first_iter; it < kDepth; it++) {
+// What the descent reads of a child, loaded in one round trip by the lane
+// that scores it: statistics for PUCT and the virtual loss, the child's own
+// children (the next level) and its move bytes (the path record).
+struct ChildRec {
+    int vc;
+    float tv, vq, pr;
+    int fc, nc;
+    int it;
+    uint16_t mb0, mb1, mb2;
+};
+
+__device__ __forceinline__ ChildRec load_rec(const Tree& T, int64_t ci) {
+    ChildRec r;
+    r.vc = T.vc[ci];
+    r.tv = T.tv[ci];
+    r.vq = T.vq[ci];
+    r.pr = T.pr[ci];
+    r.fc = T.fc[ci];
+    r.nc = T.nc[ci];
+    r.it = T.it[ci];
+    const uint16_t* m = reinterpret_cast<const uint16_t*>(T.mb + ci * 6);
+    r.mb0 = m[0];
+    r.mb1 = m[1];
+    r.mb2 = m[2];
+    return r;
+}
+
+__device__ __forceinline__ ChildRec shfl_rec(const ChildRec& r, int src) {
+    ChildRec o;
+    o.vc = __shfl(r.vc, src, 64);
+    o.tv = __shfl(r.tv, src, 64);
+    o.vq = __shfl(r.vq, src, 64);
+    o.pr = __shfl(r.pr, src, 64);
+    o.fc = __shfl(r.fc, src, 64);
+    o.nc = __shfl(r.nc, src, 64);
+    o.it = __shfl(r.it, src, 64);
+    o.mb0 = (uint16_t)__shfl((int)r.mb0, src, 64);
+    o.mb1 = (uint16_t)__shfl((int)r.mb1, src, 64);
+    o.mb2 = (uint16_t)__shfl((int)r.mb2, src, 64);
+    return o;
+}
+
+// puct_score (mcts_tree.cuh:55-67) of a loaded child, parent visits pvc
+__device__ __forceinline__ float puct_rec(const ChildRec& r, int pvc, float c_puct) {
+    int n = r.vc;
+    float q = n > 0 ? (-r.tv / (float)n) : 0.0f;
+    q -= r.vq;
+    float explore = c_puct * r.pr * sqrtf((float)pvc) / (1.0f + (float)n);
+    return q + explore;
+}
+
+// Enter `node` (record r, as loaded) below the root: virtual loss or q
+// penalty written from the loaded values (no other wave touches this node
+// during the kernel, and this simulation reads it again only as the parent,
+// whose visit count the caller carries in a register), path records.
+__device__ __forceinline__ void enter_rec(const Tree& T, int64_t g0, int node, const ChildRec& r, bool det,
+                                          float q_penalty, const SelectOut& O, int64_t sim, int& plen, int& vlen,
+                                          int lane) {
+    if (lane == 0) {
         int64_t ni = g0 + node;
-        int cfc = T.fc[ni];
-        int cnc = T.nc[ni];
-        if (cfc < 0 || T.it[ni] || cnc == 0) break;
+        T.vc[ni] = r.vc + 1;
+        if (det) T.vq[ni] = r.vq + q_penalty;
+        else T.tv[ni] = r.tv + -1.0f;
+        if (vlen < kDepth) O.vl[sim * kDepth + vlen] = node;
+        if (plen < kDepth) {
+            uint16_t* dst = reinterpret_cast<uint16_t*>(O.paths + (sim * kDepth + plen) * 6);
+            dst[0] = r.mb0;
+            dst[1] = r.mb1;
+            dst[2] = r.mb2;
+        }
+    }
+    vlen = vlen < kDepth ? vlen + 1 : vlen;
+    plen = plen < kDepth ? plen + 1 : plen;
+}
+
+// PUCT descent below `node` (mcts_tree.cuh:895-950 / 729-795 below the root):
+// r is the record of `node`, pvc its visit count as this simulation left it.
+// One round trip of loads per level: each lane loads its children's records,
+// the winner's record is broadcast and carries the next level.
+HW_INL int descend_rec(const Tree& T, int64_t g0, int node, ChildRec r, int pvc, int first_iter, float c_puct,
+                       bool det, float sigma, float q_penalty, const SelectOut& O, int64_t sim, int& plen, int& vlen,
+                       int lane) {
+    for (int it = first_iter; it < kDepth; it++) {
+        const int cfc = r.fc, cnc = r.nc;
+        if (cfc < 0 || r.it || cnc == 0) break;
         if (cnc <= 0 || cnc > 1024) break;
         int best;
+        ChildRec win;
         if (det) {
             int b = 0;
             if (lane == 0) b = completed_q_child(T, g0, cfc, cnc, sigma);
             best = __shfl(b, 0, 64);
+            if (best < 0) break;
+            win = load_rec(T, g0 + best);
         } else {
             float bs = -INFINITY;
             int bi = 0x7fffffff;
+            ChildRec mine = r;
             for (int c = lane; c < cnc; c += 64) {
                 int child = cfc + c;
                 if (child < 0 || child >= T.M) break;
-                float sc = puct(T, ni, g0 + child, c_puct);
-                if (sc > -1e30f && (sc > bs || (sc == bs && c < bi))) { bs = sc; bi = c; }
+                ChildRec cr = load_rec(T, g0 + child);
+                float sc = puct_rec(cr, pvc, c_puct);
+                if (sc > -1e30f && (sc > bs || (sc == bs && c < bi))) {
+                    bs = sc;
+                    bi = c;
+                    mine = cr;
+                }
             }
             int c = wave_argmax_first(bs, bi);
-            best = c < 0 ? -1 : cfc + c;
+            if (c < 0) break;
+            best = cfc + c;
+            win = shfl_rec(mine, c & 63);
         }
-        if (best < 0) break;
         node = best;
-        enter(T, g0, node, det, q_penalty, O, sim, plen, vlen, lane);
+        enter_rec(T, g0, node, win, det, q_penalty, O, sim, plen, vlen, lane);
+        pvc = win.vc + 1;
+        r = win;
     }
     return node;
 }
+
 
 // mcts_select_with_root_slots_kernel (mcts_tree.cuh:811-955), one wave per
 // (game, candidate).  A simulation forced into root child fc + slot touches
@@ -215,36 +305,44 @@ __global__ __launch_bounds__(64) void k_select_slots(Tree T, const int8_t* __res
     if (dup && c != 0) return;
     const int64_t g0 = g * T.M;
     const int64_t rounds = total / B;  // simulations per game
+    // the game's root and slots do not change during the kernel
+    const bool active = game_active[g] != 0;
+    const int root = root_nodes[g];
+    const int64_t ri = g0 + root;
+    const int rfc = T.fc[ri], rnc = T.nc[ri];
+    const bool rterm = T.it[ri] != 0;
+    const int lane_slot = lane < C ? root_slots[g * C + lane] : -1;
     for (int64_t k = dup ? 0 : c; k < rounds; k += dup ? 1 : C) {
         const int64_t sim = k * B + g;
         int cand = (int)(k % C);
-        if (!game_active[g]) { empty_sim(O, sim, lane); continue; }
-        int slot = root_slots[g * C + cand];
+        if (!active) { empty_sim(O, sim, lane); continue; }
+        int slot = C <= 64 ? __shfl(lane_slot, cand, 64) : root_slots[g * C + cand];
         if (slot < 0 || slot >= max_root) { empty_sim(O, sim, lane); continue; }
-        int root = root_nodes[g];
-        int64_t ri = g0 + root;
-        int fc = T.fc[ri], nc = T.nc[ri];
-        if (fc < 0 || T.it[ri] || nc <= 0 || slot >= nc) { empty_sim(O, sim, lane); continue; }
-        int node = fc + slot;
+        if (rfc < 0 || rterm || rnc <= 0 || slot >= rnc) { empty_sim(O, sim, lane); continue; }
+        int node = rfc + slot;
         if (node < 0 || node >= T.M) { empty_sim(O, sim, lane); continue; }
         int plen = 0, vlen = 0;
+        const ChildRec r = load_rec(T, g0 + node);
+        int pvc = r.vc;
         if (!det) {
-            enter(T, g0, node, false, 0.0f, O, sim, plen, vlen, lane);
+            enter_rec(T, g0, node, r, false, 0.0f, O, sim, plen, vlen, lane);
+            pvc = r.vc + 1;
         } else {  // the root child gets no penalty in this mode, only the path record
             if (lane == 0) {
-                const uint8_t* src = T.mb + (g0 + node) * 6;
-                uint8_t* dst = O.paths + sim * kDepth * 6;
-                for (int b = 0; b < 6; b++) dst[b] = src[b];
+                uint16_t* dst = reinterpret_cast<uint16_t*>(O.paths + sim * kDepth * 6);
+                dst[0] = r.mb0;
+                dst[1] = r.mb1;
+                dst[2] = r.mb2;
             }
             plen = 1;
         }
-        node = descend(T, g0, node, 1, c_puct, det, sigma, q_penalty, O, sim, plen, vlen, lane);
+        node = descend_rec(T, g0, node, r, pvc, 1, c_puct, det, sigma, q_penalty, O, sim, plen, vlen, lane);
         if (lane == 0) {
             O.leaf[sim] = node;
             O.plen[sim] = plen;
             O.vlen[sim] = vlen;
         }
-        __syncthreads();
+        __syncthreads();  // the next simulation reads this one's statistics
     }
 }
 
@@ -264,29 +362,40 @@ __global__ __launch_bounds__(64) void k_select_mask(Tree T, const int8_t* __rest
         int node = root;
         int plen = 0, vlen = 0;
         int64_t ri = g0 + root;
-        int fc = T.fc[ri], nc = T.nc[ri];
-        bool go = !(fc < 0 || T.it[ri] || nc == 0) && !(nc <= 0 || nc > 1024);
+        ChildRec rr = load_rec(T, ri);  // the root's record (its children, visits)
+        const int fc = rr.fc, nc = rr.nc;
+        bool go = !(fc < 0 || rr.it || nc == 0) && !(nc <= 0 || nc > 1024);
         int first_iter = 0;
+        int pvc = rr.vc;
         if (go) {  // root level: PUCT over alive children
             float bs = -INFINITY;
             int bi = 0x7fffffff;
+            ChildRec mine = rr;
             for (int c = lane; c < nc; c += 64) {
                 int child = fc + c;
                 if (child < 0 || child >= T.M) break;
                 if (c >= max_root || !alive[g * max_root + c]) continue;
-                float sc = puct(T, ri, g0 + child, c_puct);
-                if (sc > -1e30f && (sc > bs || (sc == bs && c < bi))) { bs = sc; bi = c; }
+                ChildRec cr = load_rec(T, g0 + child);
+                float sc = puct_rec(cr, pvc, c_puct);
+                if (sc > -1e30f && (sc > bs || (sc == bs && c < bi))) {
+                    bs = sc;
+                    bi = c;
+                    mine = cr;
+                }
             }
             int c = wave_argmax_first(bs, bi);
             if (c >= 0) {
                 node = fc + c;
-                enter(T, g0, node, false, 0.0f, O, sim, plen, vlen, lane);
+                rr = shfl_rec(mine, c & 63);
+                enter_rec(T, g0, node, rr, false, 0.0f, O, sim, plen, vlen, lane);
+                pvc = rr.vc + 1;
                 first_iter = 1;
             } else {
                 go = false;
             }
         }
-        if (go) node = descend(T, g0, node, first_iter, c_puct, det, sigma, q_penalty, O, sim, plen, vlen, lane);
+        if (go) node = descend_rec(T, g0, node, rr, pvc, first_iter, c_puct, det, sigma, q_penalty, O, sim, plen,
+                                   vlen, lane);
         if (lane == 0) {
             O.leaf[sim] = node;
             O.plen[sim] = plen;
