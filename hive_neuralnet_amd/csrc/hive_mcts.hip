@@ -532,7 +532,31 @@ __global__ __launch_bounds__(64) void k_expand(Tree T, LeafIn L, int64_t B, int6
     }
 }
 
-// mcts_expand_and_backprop_dense_priors_kernel (mcts_tree.cuh:1068-1187)
+// centroid of the occupied cells from the 18 bitboard words held by lanes
+// 0-17 (compute_centroid, state_encoder.cuh:889-906); wave-uniform result
+HW_INL void words_centroid(uint32_t w, int lane, int& cq, int& cr) {
+    int q = 0, r = 0, n = 0;
+    while (w) {
+        int c = lane * 32 + __ffs(w) - 1;
+        w &= w - 1;
+        int row = c / kGrid;
+        q += c - row * kGrid - kHalf;
+        r += row - kHalf;
+        n++;
+    }
+    int sq = wave_sum(q), sr = wave_sum(r), sn = wave_sum(n);
+    cq = sn ? round_half_even_div(sq, sn) : 0;
+    cr = sn ? round_half_even_div(sr, sn) : 0;
+}
+
+// mcts_expand_and_backprop_dense_priors_kernel (mcts_tree.cuh:1068-1187).
+// One wave per game, simulations in order.  A simulation's loads come in
+// three rounds: its inputs (leaf, result, legal count, path, value, the
+// leaf's bitboards, legal list, priors and child values), then the tree
+// state they index (the leaf's children and terminal fields, the path nodes'
+// statistics, the root above the path), then the root's statistics.
+// Expansion and backup are stores; one fence per simulation makes them
+// visible to the next.
 __global__ __launch_bounds__(64) void k_expand_backprop(Tree T, LeafIn L, const float* __restrict__ nn_values,
                                                         const int32_t* __restrict__ vl_paths,
                                                         const int32_t* __restrict__ vl_lens, float q_penalty,
@@ -541,38 +565,151 @@ __global__ __launch_bounds__(64) void k_expand_backprop(Tree T, LeafIn L, const 
     const int lane = threadIdx.x;
     if (g >= B) return;
     const int64_t g0 = g * T.M;
+    int cnt = T.cnt[g];  // the game's node counter: only this wave changes it during the kernel
     for (int64_t sim = g; sim < total; sim += B) {
         const int leaf = L.leaf[sim];
         if (leaf < 0) continue;
+        // round 1: the simulation's inputs (this kernel never writes them)
+        const int res = L.results[sim];
+        const int nl = L.nlegal[sim];
         int n = vl_lens[sim];
         n = n < 0 ? 0 : (n > kDepth ? kDepth : n);
+        const float nn = nn_values[sim];
         const int32_t* vp = vl_paths + sim * kDepth;
-        const int last = n > 0 ? vp[n - 1] : leaf;
-        const int e = expand_leaf(T, g, sim, L, lane);
+        const int p0 = vp[lane], p1 = vp[64 + lane];  // a path row holds kDepth = 128 entries
+        const uint8_t* S = L.states + sim * kStateBytes;
+        const int turn = S[OFF_TURN] | (S[OFF_TURN + 1] << 8);
+        const uint32_t occw = lane < 18 ? reinterpret_cast<const uint32_t*>(S + OFF_OCC)[lane] : 0u;
+        const uint8_t* mv = L.legal + sim * (kMaxLegal * 6);
+        const float* pri = L.priors + sim * kMaxLegal;
+        const float* cqv = L.childq + sim * kMaxLegal;
+        uint16_t x0[4], x1[4], x2[4];
+        float xp[4], xq[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int m = lane + 64 * j;
+            x0[j] = x1[j] = x2[j] = 0;
+            xp[j] = xq[j] = 0.0f;
+            if (m < nl) {
+                const uint16_t* x = reinterpret_cast<const uint16_t*>(mv + 6 * m);
+                x0[j] = x[0];
+                x1[j] = x[1];
+                x2[j] = x[2];
+                xp[j] = pri[m];
+                xq[j] = cqv[m];
+            }
+        }
+        // round 2: the tree state they index
         const int64_t li = g0 + leaf;
-        const float v = T.it[li] ? T.tval[li] : (e ? nn_values[sim] : 0.0f);
-        if (last == leaf) {
-            // The selection entered vp[0..n) below the root, each node a child
-            // of the one before, so the backup chain leaf -> root is that path
-            // reversed, then the root.  Each node takes the virtual-loss undo
-            // then the value, as the serial walk below does; the nodes are
-            // distinct, so lanes take them side by side.
-            for (int k = lane; k < n; k += 64) {
-                const int64_t ni = g0 + vp[k];
-                const float sv = ((n - 1 - k) & 1) ? -v : v;
+        const int fc = T.fc[li];
+        const int lit = T.it[li];
+        const float ltv = T.tval[li];
+        const int last = n > 0 ? __shfl(n - 1 < 64 ? p0 : p1, (n - 1) & 63, 64) : leaf;
+        // The selection entered vp[0..n) below the root, each node a child of
+        // the one before, so the backup chain leaf -> root is that path
+        // reversed, then the root; the expansion below writes none of them.
+        const bool chain = last == leaf;
+        int vc0 = 0, vc1 = 0;
+        float tv0 = 0.0f, tv1 = 0.0f, vq0 = 0.0f, vq1 = 0.0f;
+        if (chain) {
+            if (lane < n) {
+                const int64_t ni = g0 + p0;
+                tv0 = T.tv[ni];
+                vc0 = T.vc[ni];
+                vq0 = T.vq[ni];
+            }
+            if (lane + 64 < n) {
+                const int64_t ni = g0 + p1;
+                tv1 = T.tv[ni];
+                vc1 = T.vc[ni];
+                vq1 = T.vq[ni];
+            }
+        }
+        const int top = (chain && n > 0) ? T.pa[g0 + __shfl(p0, 0, 64)] : leaf;  // the root above the path
+        // expansion (mcts_expand_dense_priors_kernel :971-1062 body)
+        int e = 0;
+        float rv = 0.0f;
+        if (res != 0) {
+            rv = result_value(res, turn);
+            if (lane == 0) {
+                T.it[li] = 1;
+                T.tval[li] = rv;
+            }
+        } else if (fc == -1 && nl > 0 && (int64_t)cnt + nl <= T.M) {
+            int cq, cr;
+            words_centroid(occw, lane, cq, cr);
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int m = lane + 64 * j;
+                if (m >= nl) break;
+                const int64_t ci = g0 + cnt + m;
+                T.vc[ci] = 0;
+                T.tv[ci] = 0.0f;
+                T.pr[ci] = xp[j];
+                T.pa[ci] = leaf;
+                T.ai[ci] = move_action(x0[j] & 0xFF, x0[j] >> 8, x1[j], x2[j], cq, cr);
+                T.fc[ci] = -1;
+                T.nc[ci] = 0;
+                T.it[ci] = 0;
+                T.tval[ci] = 0.0f;
+                T.ciq[ci] = xq[j];
+                uint16_t* d = reinterpret_cast<uint16_t*>(T.mb + ci * 6);
+                d[0] = x0[j];
+                d[1] = x1[j];
+                d[2] = x2[j];
+            }
+            for (int m = lane + 256; m < nl; m += 64) {  // lists beyond 256 entries (never produced here)
+                const uint8_t* x = mv + 6 * m;
+                const int64_t ci = g0 + cnt + m;
+                T.vc[ci] = 0;
+                T.tv[ci] = 0.0f;
+                T.pr[ci] = pri[m];
+                T.pa[ci] = leaf;
+                T.ai[ci] = move_action(x[0], x[1], x[2] | (x[3] << 8), x[4] | (x[5] << 8), cq, cr);
+                T.fc[ci] = -1;
+                T.nc[ci] = 0;
+                T.it[ci] = 0;
+                T.tval[ci] = 0.0f;
+                T.ciq[ci] = cqv[m];
+                uint8_t* d = T.mb + ci * 6;
+                for (int b = 0; b < 6; b++) d[b] = x[b];
+            }
+            if (lane == 0) {
+                T.cnt[g] = cnt + nl;
+                T.nc[li] = nl;
+                T.fc[li] = cnt;
+            }
+            cnt += nl;
+            e = 1;
+        }
+        const float v = res != 0 ? rv : (lit ? ltv : (e ? nn : 0.0f));
+        if (chain) {  // each path node: virtual-loss undo, then the value; lanes side by side
+            if (lane < n) {
+                const int64_t ni = g0 + p0;
+                const float sv = ((n - 1 - lane) & 1) ? -v : v;
                 if (q_penalty > 0.0f) {
-                    T.vq[ni] += -q_penalty;
-                    T.vc[ni] += 1;
-                    T.tv[ni] += sv;
+                    T.vq[ni] = vq0 + -q_penalty;
+                    T.vc[ni] = vc0 + 1;
+                    T.tv[ni] = tv0 + sv;
                 } else {  // visits -1 then +1; value +1.0 then the backed-up value
-                    const float t = T.tv[ni] + 1.0f;
-                    T.tv[ni] = t + sv;
+                    T.tv[ni] = (tv0 + 1.0f) + sv;
                 }
             }
-            if (lane == 0) {  // the root, and any node above it
-                int node = n > 0 ? T.pa[g0 + vp[0]] : leaf;
+            if (lane + 64 < n) {
+                const int64_t ni = g0 + p1;
+                const float sv = ((n - 1 - (lane + 64)) & 1) ? -v : v;
+                if (q_penalty > 0.0f) {
+                    T.vq[ni] = vq1 + -q_penalty;
+                    T.vc[ni] = vc1 + 1;
+                    T.tv[ni] = tv1 + sv;
+                } else {
+                    T.tv[ni] = (tv1 + 1.0f) + sv;
+                }
+            }
+            if (lane == 0) {  // round 3: the root, and any node above it
+                int node = top;
                 float w = (n & 1) ? -v : v;
-                for (int s = n; s < kDepth + 1 && node >= 0; s++) {
+                for (int s2 = n; s2 < kDepth + 1 && node >= 0; s2++) {
                     const int64_t ni = g0 + node;
                     T.vc[ni] += 1;
                     T.tv[ni] += w;
@@ -592,7 +729,7 @@ __global__ __launch_bounds__(64) void k_expand_backprop(Tree T, LeafIn L, const 
             }
             float w = v;
             int node = leaf;
-            for (int s = 0; s < kDepth + 1 && node >= 0; s++) {
+            for (int s2 = 0; s2 < kDepth + 1 && node >= 0; s2++) {
                 const int64_t ni = g0 + node;
                 T.vc[ni] += 1;
                 T.tv[ni] += w;
@@ -600,7 +737,7 @@ __global__ __launch_bounds__(64) void k_expand_backprop(Tree T, LeafIn L, const 
                 node = T.pa[ni];
             }
         }
-        __syncthreads();
+        __syncthreads();  // the next simulation reads this one's stores
     }
 }
 
