@@ -230,30 +230,43 @@ __global__ void k_mask_scatter(const int32_t* __restrict__ actions, const int32_
 // ---------------------------------------------------------------- successor rows
 // The successor rows of a batch of leaves without a host round trip: the row
 // count stays on the device.  k_rows_offsets: exclusive prefix of the
-// clamped legal counts (one workgroup, chunks of 1024 with a running carry)
+// clamped legal counts (one workgroup, chunks of 4,096 with a running carry)
 // and the total; k_rows_map: row -> (leaf, slot); k_successor_rows: the
 // successor features of rows < total, kSuccRows per lane group, the grid
 // striding over the rows (sized from the capacity, the count read on the
 // device).
 __global__ __launch_bounds__(1024) void k_rows_offsets(const int32_t* __restrict__ nlegal, int64_t T,
                                                         int64_t* __restrict__ offsets, int64_t* __restrict__ total) {
-    __shared__ int64_t wsum[16];
+    // chunks of 4,096 counts, four consecutive counts per thread, with a
+    // running carry between chunks
+    __shared__ int wsum[16];
     __shared__ int64_t carry_s;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     if (tid == 0) carry_s = 0;
     __syncthreads();
-    for (int64_t base = 0; base < T; base += 1024) {
-        const int64_t t = base + tid;
-        int n = t < T ? nlegal[t] : 0;
-        n = n < 0 ? 0 : (n > kMaxLegal ? kMaxLegal : n);
-        int incl = wave_incl_scan(n);
+    for (int64_t base = 0; base < T; base += 4096) {
+        int v[4];
+        int sum = 0;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int64_t t = base + 4 * tid + j;
+            int n = t < T ? nlegal[t] : 0;
+            v[j] = n < 0 ? 0 : (n > kMaxLegal ? kMaxLegal : n);
+            sum += v[j];
+        }
+        const int incl = wave_incl_scan(sum);  // at most 64 * 4 * 256 per wave
         if (lane == 63) wsum[w] = incl;
         __syncthreads();
-        int64_t before = carry_s;
-        for (int k = 0; k < w; k++) before += wsum[k];
-        if (t < T) offsets[t] = before + incl - n;
+        int64_t run = carry_s + incl - sum;
+        for (int k = 0; k < w; k++) run += wsum[k];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int64_t t = base + 4 * tid + j;
+            if (t < T) offsets[t] = run;
+            run += v[j];
+        }
         __syncthreads();
-        if (tid == 1023) carry_s = before + incl;
+        if (tid == 1023) carry_s = run;
         __syncthreads();
     }
     if (tid == 0) *total = carry_s;

@@ -124,12 +124,28 @@ struct SelectOut {
     int32_t* vlen;
 };
 
+// Zeros past the recorded entries of a simulation's path rows (move bytes
+// from plen, node ids from vlen), so the dense selects write whole rows and
+// their callers need not clear the outputs.
+__device__ __forceinline__ void zero_tails(const SelectOut& O, int64_t sim, int plen, int vlen, int lane) {
+    uint16_t* pw = reinterpret_cast<uint16_t*>(O.paths + sim * kDepth * 6);
+    for (int k = 3 * plen + lane; k < 3 * kDepth; k += 64) pw[k] = 0;
+    int32_t* vw = O.vl + sim * kDepth;
+    for (int k = vlen + lane; k < kDepth; k += 64) vw[k] = 0;
+}
+
 __device__ __forceinline__ void empty_sim(const SelectOut& O, int64_t sim, int lane) {
     if (lane == 0) {
         O.leaf[sim] = -1;
         O.plen[sim] = 0;
         O.vlen[sim] = 0;
     }
+}
+
+// an empty simulation of a dense select: whole rows
+__device__ __forceinline__ void empty_sim_rows(const SelectOut& O, int64_t sim, int lane) {
+    empty_sim(O, sim, lane);
+    zero_tails(O, sim, 0, 0, lane);
 }
 
 // Enter `node` below the root (virtual loss or q penalty, path records).
@@ -315,12 +331,12 @@ __global__ __launch_bounds__(64) void k_select_slots(Tree T, const int8_t* __res
     for (int64_t k = dup ? 0 : c; k < rounds; k += dup ? 1 : C) {
         const int64_t sim = k * B + g;
         int cand = (int)(k % C);
-        if (!active) { empty_sim(O, sim, lane); continue; }
+        if (!active) { empty_sim_rows(O, sim, lane); continue; }
         int slot = C <= 64 ? __shfl(lane_slot, cand, 64) : root_slots[g * C + cand];
-        if (slot < 0 || slot >= max_root) { empty_sim(O, sim, lane); continue; }
-        if (rfc < 0 || rterm || rnc <= 0 || slot >= rnc) { empty_sim(O, sim, lane); continue; }
+        if (slot < 0 || slot >= max_root) { empty_sim_rows(O, sim, lane); continue; }
+        if (rfc < 0 || rterm || rnc <= 0 || slot >= rnc) { empty_sim_rows(O, sim, lane); continue; }
         int node = rfc + slot;
-        if (node < 0 || node >= T.M) { empty_sim(O, sim, lane); continue; }
+        if (node < 0 || node >= T.M) { empty_sim_rows(O, sim, lane); continue; }
         int plen = 0, vlen = 0;
         const ChildRec r = load_rec(T, g0 + node);
         int pvc = r.vc;
@@ -342,6 +358,7 @@ __global__ __launch_bounds__(64) void k_select_slots(Tree T, const int8_t* __res
             O.plen[sim] = plen;
             O.vlen[sim] = vlen;
         }
+        zero_tails(O, sim, plen, vlen, lane);
         __syncthreads();  // the next simulation reads this one's statistics
     }
 }
@@ -357,7 +374,7 @@ __global__ __launch_bounds__(64) void k_select_mask(Tree T, const int8_t* __rest
     if (g >= B) return;
     const int64_t g0 = g * T.M;
     for (int64_t sim = g; sim < total; sim += B) {
-        if (!game_active[g]) { empty_sim(O, sim, lane); continue; }
+        if (!game_active[g]) { empty_sim_rows(O, sim, lane); continue; }
         int root = root_nodes[g];
         int node = root;
         int plen = 0, vlen = 0;
@@ -401,6 +418,7 @@ __global__ __launch_bounds__(64) void k_select_mask(Tree T, const int8_t* __rest
             O.plen[sim] = plen;
             O.vlen[sim] = vlen;
         }
+        zero_tails(O, sim, plen, vlen, lane);
         __syncthreads();
     }
 }
@@ -410,11 +428,19 @@ __global__ __launch_bounds__(64) void k_select_mask(Tree T, const int8_t* __rest
 __global__ __launch_bounds__(64) void k_replay(const uint8_t* __restrict__ roots, int64_t B,
                                                uint8_t* __restrict__ leaves, const uint8_t* __restrict__ paths,
                                                const int32_t* __restrict__ plen, const int32_t* __restrict__ leaf_idx,
-                                               int64_t total) {
+                                               int64_t total, int zero_idle) {
     __shared__ uint4 row[kStateBytes / 16];
     const int64_t sim = blockIdx.x;
     const int lane = threadIdx.x;
-    if (sim >= total || leaf_idx[sim] < 0) return;
+    if (sim >= total) return;
+    if (leaf_idx[sim] < 0) {
+        if (zero_idle) {
+            uint4* dst = reinterpret_cast<uint4*>(leaves + sim * kStateBytes);
+            const uint4 z = make_uint4(0u, 0u, 0u, 0u);
+            for (int i = lane; i < kStateBytes / 16; i += 64) dst[i] = z;
+        }
+        return;
+    }
     const uint4* src = reinterpret_cast<const uint4*>(roots + (sim % B) * kStateBytes);
     for (int i = lane; i < kStateBytes / 16; i += 64) row[i] = src[i];
     __syncthreads();
@@ -1128,7 +1154,15 @@ int hg_mcts_replay(const uint8_t* root_states, int64_t B, uint8_t* leaf_states, 
                    const int32_t* path_lens, const int32_t* leaf_idx, int64_t total, void* stream) {
     if (B <= 0 || total <= 0) return 0;
     hipLaunchKernelGGL(k_replay, dim3((unsigned)total), dim3(64), 0, (hipStream_t)stream, root_states, B,
-                       leaf_states, move_paths, path_lens, leaf_idx, total);
+                       leaf_states, move_paths, path_lens, leaf_idx, total, 0);
+    return finish();
+}
+
+int hg_mcts_replay_fill(const uint8_t* root_states, int64_t B, uint8_t* leaf_states, const uint8_t* move_paths,
+                        const int32_t* path_lens, const int32_t* leaf_idx, int64_t total, void* stream) {
+    if (B <= 0 || total <= 0) return 0;
+    hipLaunchKernelGGL(k_replay, dim3((unsigned)total), dim3(64), 0, (hipStream_t)stream, root_states, B,
+                       leaf_states, move_paths, path_lens, leaf_idx, total, 1);
     return finish();
 }
 

@@ -80,6 +80,7 @@ _SIGS = {
                                  _c_int, ctypes.c_float, ctypes.c_float, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                                  _c_void_p, _c_void_p],
     "hg_mcts_replay": [_c_void_p, _c_i64, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_i64, _c_void_p],
+    "hg_mcts_replay_fill": [_c_void_p, _c_i64, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_i64, _c_void_p],
     "hg_mcts_expand_dense": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                              _c_i64, _c_i64, _c_void_p, _c_void_p],
     "hg_mcts_expand_backprop_dense": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
@@ -148,12 +149,14 @@ def _tree_struct(tensors, child_init_q, B: int, max_nodes: int) -> HgTree:
     return HgTree(vc, tv, pr, pa, vq, mb, ai, fc, nc, it, tv2, cnt, child_init_q.data_ptr(), int(max_nodes))
 
 
-def _select_outputs(T: int):
-    leaf = torch.zeros((T,), dtype=torch.int32, device="cuda")
-    paths = torch.zeros((T, MAX_TREE_DEPTH, SIZEOF_GPU_MOVE), dtype=torch.uint8, device="cuda")
-    plen = torch.zeros((T,), dtype=torch.int32, device="cuda")
-    vl = torch.zeros((T, MAX_TREE_DEPTH), dtype=torch.int32, device="cuda")
-    vlen = torch.zeros((T,), dtype=torch.int32, device="cuda")
+def _select_outputs(T: int, whole_rows: bool = False):
+    """Select outputs; zero-filled unless the kernel writes whole rows."""
+    new = torch.empty if whole_rows else torch.zeros
+    leaf = new((T,), dtype=torch.int32, device="cuda")
+    paths = new((T, MAX_TREE_DEPTH, SIZEOF_GPU_MOVE), dtype=torch.uint8, device="cuda")
+    plen = new((T,), dtype=torch.int32, device="cuda")
+    vl = new((T, MAX_TREE_DEPTH), dtype=torch.int32, device="cuda")
+    vlen = new((T,), dtype=torch.int32, device="cuda")
     return leaf, paths, plen, vl, vlen
 
 _lib = None
@@ -487,7 +490,7 @@ def _mcts_methods():
         _dev(root_nodes, "root_nodes", torch.int32, (), B)
         _dev(alive_mask, "alive_mask", torch.int8, (int(max_root_children),), B)
         T = W * B
-        out = _select_outputs(T)
+        out = _select_outputs(T, whole_rows=True)
         _check(self._lib.hg_mcts_select_root_mask(
             ctypes.byref(tree), game_active.data_ptr(), root_nodes.data_ptr(), alive_mask.data_ptr(),
             int(max_root_children), float(c_puct), B, W, 1 if deterministic_non_root else 0, float(non_root_sigma),
@@ -504,7 +507,7 @@ def _mcts_methods():
         _dev(root_nodes, "root_nodes", torch.int32, (), B)
         _dev(root_slots, "root_slots", torch.int32, (C,), B)
         T = W * C * B
-        out = _select_outputs(T)
+        out = _select_outputs(T, whole_rows=True)
         _check(self._lib.hg_mcts_select_root_slots(
             ctypes.byref(tree), game_active.data_ptr(), root_nodes.data_ptr(), root_slots.data_ptr(), C,
             int(max_root_children), float(c_puct), B, W, 1 if deterministic_non_root else 0, float(non_root_sigma),
@@ -522,6 +525,20 @@ def _mcts_methods():
                                         path_lengths.data_ptr(), leaf_indices.data_ptr(), total, _stream()),
                "mcts_replay_batch")
 
+    def mcts_replay_fill_batch(self, root_states, leaf_states, move_paths, path_lengths, leaf_indices, B, total):
+        """mcts_replay_batch into an uninitialised buffer: rows of idle
+        simulations (leaf index < 0) are written as zero rows, as the fused
+        prefix's zero-filled leaf states (game_logic.cu:1183-1254)."""
+        B, total = int(B), int(total)
+        _state_rows(root_states, B)
+        _state_rows(leaf_states, total)
+        _dev(move_paths, "move_paths", torch.uint8, (MAX_TREE_DEPTH, SIZEOF_GPU_MOVE), total)
+        _dev(path_lengths, "path_lengths", torch.int32, (), total)
+        _dev(leaf_indices, "leaf_indices", torch.int32, (), total)
+        _check(self._lib.hg_mcts_replay_fill(root_states.data_ptr(), B, leaf_states.data_ptr(), move_paths.data_ptr(),
+                                             path_lengths.data_ptr(), leaf_indices.data_ptr(), total, _stream()),
+               "mcts_replay_fill_batch")
+
     def mcts_select_replay_legal_fnn_root_slots_batch(self, vc, tv, pr, pa, vq, mb, ai, fc, nc, it, tv2, cnt,
                                                       child_init_q, root_states, game_active, root_nodes, root_slots,
                                                       num_candidates, max_root_children, c_puct, B, W, max_nodes,
@@ -533,8 +550,9 @@ def _mcts_methods():
             num_candidates, max_root_children, c_puct, B, W, max_nodes, deterministic_non_root, non_root_sigma,
             q_penalty)
         T = leaf_idx.shape[0]
-        leaf_states = torch.zeros((T, root_states.shape[1]), dtype=torch.uint8, device="cuda")
-        self.mcts_replay_batch(root_states, leaf_states, paths, plen, leaf_idx, B, T)
+        # replayed in full: rows of idle simulations are written as zero rows
+        leaf_states = torch.empty((T, root_states.shape[1]), dtype=torch.uint8, device="cuda")
+        self.mcts_replay_fill_batch(root_states, leaf_states, paths, plen, leaf_idx, B, T)
         results = self.check_results_batch(leaf_states, T)
         moves, n, feat = self.generate_legal_moves_and_fnn_features_batch(leaf_states, T)
         return leaf_idx, leaf_states, moves, n, feat, results, vl, vlen

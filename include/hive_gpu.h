@@ -270,7 +270,8 @@ int hg_mcts_reset_trees(const hg_tree* tree, const int8_t* reset, int32_t* root_
 /* mcts_select_with_root_slots_batch -- game_logic.cu:1134-1175
  * (mcts_select_with_root_slots_kernel, mcts_tree.cuh:811-955).
  * T = W * num_candidates * B simulations, sim = (w*C + c)*B + game.
- * Outputs (caller zero-fills move_paths/vl_paths): leaf_idx[T], move_paths[T][128][6],
+ * Outputs, whole rows written (entries past path_lens / vl_lens are zero, as the
+ * reference's zero-filled outputs): leaf_idx[T], move_paths[T][128][6],
  * path_lens[T], vl_paths[T][128], vl_lens[T]. */
 int hg_mcts_select_root_slots(const hg_tree* tree, const int8_t* game_active, const int32_t* root_nodes,
                               const int32_t* root_slots, int num_candidates, int max_root_children, float c_puct,
@@ -291,6 +292,13 @@ int hg_mcts_select_root_mask(const hg_tree* tree, const int8_t* game_active, con
  * leaf_idx < 0 are left untouched. */
 int hg_mcts_replay(const uint8_t* root_states, int64_t B, uint8_t* leaf_states, const uint8_t* move_paths,
                    const int32_t* path_lens, const int32_t* leaf_idx, int64_t total, void* stream);
+
+/* The replay step of mcts_select_replay_legal_fnn_root_slots_batch
+ * (game_logic.cu:1183-1254), which replays into a zero-filled buffer: as
+ * hg_mcts_replay, and rows with leaf_idx < 0 are written as zero rows, so
+ * leaf_states may start uninitialised. */
+int hg_mcts_replay_fill(const uint8_t* root_states, int64_t B, uint8_t* leaf_states, const uint8_t* move_paths,
+                        const int32_t* path_lens, const int32_t* leaf_idx, int64_t total, void* stream);
 
 /* mcts_expand_dense_priors_batch -- game_logic.cu:1259-1288
  * (mcts_expand_dense_priors_kernel, mcts_tree.cuh:971-1062).  was_expanded[total] int8. */

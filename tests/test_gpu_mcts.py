@@ -8,7 +8,7 @@ selection output and leaf state must be bit-identical.
 import numpy as np
 import pytest
 
-from mcts_driver import GpuEngine, OracleEngine, run_search, tree_equal
+from mcts_driver import GpuEngine, OracleEngine, run_search, synthetic_eval, tree_equal
 
 pytestmark = pytest.mark.gpu
 
@@ -133,3 +133,28 @@ def test_wave_stats(total):
         live = leaf >= 0
         want += (live.sum(), nl[live].sum(), vl[live].sum(), total)
     assert np.array_equal(stats.cpu().numpy(), want)
+
+
+def test_replay_fill_writes_idle_rows(roots):
+    """hg_mcts_replay_fill over a buffer of stale bytes: replayed rows as
+    hg_mcts_replay, rows of idle simulations (leaf index < 0) all zero."""
+    import torch
+    ge, oe = GpuEngine(), OracleEngine()
+    B = roots.shape[0]
+    T = 3 * B
+    rng = np.random.default_rng(5)
+    t = oe.tree(B, 4096)
+    legal, n = oe.legal(roots)
+    pri, _, cq = synthetic_eval(rng, n, B)
+    res = roots[:, 3415].astype(np.int32)
+    act = (res == 0) & (n > 0)
+    oe.expand_dense(t, cq, np.where(act, 0, -1).astype(np.int32), roots, legal, n, pri, res)
+    slots = np.where(n[:, None] > np.arange(3)[None, :], np.arange(3)[None, :], -1).astype(np.int32)
+    idle = act.copy()
+    idle[::4] = False  # every fourth game idle: its simulations are empty
+    leaf, paths, plen, _, _ = oe.select_slots(t, idle, slots, 256, 1.25, 1)
+    assert (leaf < 0).any() and (leaf >= 0).any()
+    want = oe.replay(roots, paths, plen, leaf)
+    buf = torch.full((T, 3424), 0xAB, dtype=torch.uint8, device="cuda")
+    ge.ext.mcts_replay_fill_batch(ge.c(roots), buf, ge.c(paths), ge.c(plen), ge.c(leaf), B, T)
+    assert np.array_equal(buf.cpu().numpy(), want)

@@ -33,7 +33,7 @@ class Shadow:
         self.sync()
         ext = orch.ext
         for name in ("mcts_expand_dense_priors_batch", "mcts_apply_root_noise", "mcts_select_with_root_slots_batch",
-                     "mcts_select_with_root_mask_batch", "mcts_replay_batch",
+                     "mcts_select_with_root_mask_batch", "mcts_replay_batch", "mcts_replay_fill_batch",
                      "mcts_expand_and_backprop_dense_priors_batch"):
             monkeypatch.setattr(ext, name, self._wrap(name, getattr(ext, name)), raising=False)
 
@@ -87,6 +87,9 @@ class Shadow:
         self.m.replay(roots, exp, paths, plen, leaf)
         assert np.array_equal(exp, leaves)
 
+    def _mcts_replay_fill_batch(self, a, out):  # the buffer started uninitialised: idle rows must be zero
+        self._mcts_replay_batch(a, out)
+
     def _mcts_expand_and_backprop_dense_priors_batch(self, a, out):
         cq, leaf, st, lm, nl, pri, res, vals, vl, vlen = [_np(x) for x in a[13:23]]
         self.m.expand_backprop_dense(self.ot, cq, leaf, st, lm, nl, pri, res, vals, vl, vlen, float(a[26]))
@@ -119,7 +122,7 @@ def test_search_ply_tree_calls_match_oracle(monkeypatch, sims, M, mask, max_ply,
     active = torch.ones((B,), dtype=torch.bool, device="cuda")
     r = orch.search_ply(states, tree, active)
     assert sh.calls.get("mcts_expand_and_backprop_dense_priors_batch", 0) > 0
-    assert sh.calls.get("mcts_replay_batch", 0) == sh.calls["mcts_select_with_root_slots_batch"]
+    assert sh.calls.get("mcts_replay_fill_batch", 0) == sh.calls["mcts_select_with_root_slots_batch"]
     sh.check_tree("end of ply")
     # the chosen slot is a legal move and the policy is a distribution over legal slots
     n = _np(r.num_legal)

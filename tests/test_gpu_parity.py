@@ -171,3 +171,36 @@ def test_edge_cases(ext, oracle):
     mv = torch.zeros((2, 256, 6), dtype=torch.uint8, device="cuda")
     f = ext.extract_fnn_features_batch(st, mv, torch.tensor([-3, 999], dtype=torch.int32, device="cuda"), 2)
     assert f.shape == (2, 122)
+
+
+@pytest.mark.parametrize("T,zero_every", [(1, 0), (777, 0), (5000, 3)], ids=["one", "odd", "chunked-scan"])
+def test_successor_rows_device_sized(ext, oracle, T, zero_every):
+    """hg_successor_rows: offsets, total, row map and the successor features of
+    every legal move, sized on the device, against the oracle.  T = 5,000
+    leaves takes several legal counts per scan thread; every third leaf's
+    count is forced to 0 (an idle row) there."""
+    import ctypes
+    st, _ = oracle.generate_positions(T, 7, 140, 0xABCD + T)
+    moves, n, _, _ = oracle.batch_legal_features_actions(st, want_features=False, want_actions=False)
+    n = n.astype(np.int32)
+    if zero_every:
+        n[::zero_every] = 0
+    lib = ext._lib
+    ws = torch.zeros((int(lib.hg_successor_rows_workspace(T)),), dtype=torch.uint8, device="cuda")
+    feat = torch.full((T * 256, 122), float("nan"), dtype=torch.float32, device="cuda")
+    s, m, nn = _cuda(st), _cuda(moves), _cuda(n)
+    err = lib.hg_successor_rows(s.data_ptr(), m.data_ptr(), nn.data_ptr(), T, ws.data_ptr(), feat.data_ptr(),
+                                torch.cuda.current_stream().cuda_stream)
+    assert err == 0
+    torch.cuda.synchronize()
+    w = ws.view(torch.int64).cpu().numpy()
+    offs, total = w[:T], int(w[T])
+    want_offs = np.concatenate([[0], np.cumsum(n)[:-1]]).astype(np.int64)
+    assert total == int(n.sum()) and np.array_equal(offs, want_offs)
+    a2r, mi = w[T + 1: T + 1 + total], w[T + 1 + T * 256: T + 1 + T * 256 + total]
+    want_a2r = np.repeat(np.arange(T), n).astype(np.int64)
+    want_mi = np.concatenate([np.arange(k) for k in n]).astype(np.int64)
+    assert np.array_equal(a2r, want_a2r) and np.array_equal(mi, want_mi)
+    want = oracle.batch_successor_features(st, moves, want_a2r, want_mi)
+    got = feat[:total].cpu().numpy()
+    assert np.array_equal(_bits(got), _bits(want))
