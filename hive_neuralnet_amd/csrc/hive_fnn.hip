@@ -51,8 +51,11 @@ namespace {
 constexpr int kE = 64;       // hidden / embedding / action-tower width served here
 constexpr int kFMax = 128;   // feature rows up to 128 wide (Hive FNN: 122)
 constexpr int kSlots = 256;  // legal-slot rows of priors / child Q
-constexpr int kBlockWaves = 4;
-constexpr int kMaxBlocks = 512;  // 2 resident blocks (67 KB LDS each) on each of 256 CUs
+// 8 waves share one LDS copy of the weights: 2 resident blocks (67 KB LDS
+// each) per CU give 4 waves per SIMD to overlap the element-wise work and
+// loads with the matrix cores
+constexpr int kBlockWaves = 8;
+constexpr int kMaxBlocks = 512;  // 2 resident blocks on each of 256 CUs
 
 typedef float f4 __attribute__((ext_vector_type(4)));
 
@@ -86,7 +89,7 @@ __device__ __forceinline__ f4 vec4(const MlpLds& L, int which, int t, int g) {
 // !kRoot: row -> leaf = succ_leaf[row]; value[rows] <- tanh(wv . e + bv),
 //         logit[rows] <- wa2 . sigmoid(Ws e + R[leaf]) + ba2.
 template <bool kRoot>
-__global__ __launch_bounds__(256) void k_leaf_mlp(const float* __restrict__ X, int64_t rows, int F,
+__global__ __launch_bounds__(64 * kBlockWaves) void k_leaf_mlp(const float* __restrict__ X, int64_t rows, int F,
                                                   const int64_t* __restrict__ succ_leaf, int64_t T,
                                                   const float* __restrict__ w1, const float* __restrict__ b1,
                                                   const float* __restrict__ lnw, const float* __restrict__ lnb,
