@@ -336,12 +336,23 @@ class FNNMCTSOrchestrator:
         act = active.cpu().numpy()
         max_nc = int(nc.max()) if nc.size and nc.max() > 0 else 1
         noise = np.zeros((B, max_nc), dtype=np.float32)
-        for i in range(B):
-            n = int(nc[i])
-            if n == 0 or not act[i]:
-                continue
-            alpha = max(0.03, min(cfg.dirichlet_alpha, 10.0 / n))
-            noise[i, :n] = np.random.dirichlet([alpha] * n)
+        # Dirichlet(alpha_g, ..., alpha_g) for every active game at once: independent
+        # Gamma(alpha_g) draws normalised per game (the same law as one
+        # np.random.dirichlet call per game); a game whose draws all underflow
+        # to 0 takes np.random.dirichlet itself
+        games = np.nonzero((nc > 0) & act)[0]
+        if games.size:
+            n = nc[games].astype(np.int64)
+            alpha = np.maximum(0.03, np.minimum(cfg.dirichlet_alpha, 10.0 / n))
+            draws = np.random.standard_gamma(np.repeat(alpha, n))
+            starts = np.concatenate([[0], np.cumsum(n)[:-1]])
+            sums = np.add.reduceat(draws, starts)
+            cols = np.arange(int(n.sum())) - np.repeat(starts, n)
+            rows = np.repeat(games, n)
+            ok = np.repeat(sums > 0, n)
+            noise[rows[ok], cols[ok]] = (draws / np.repeat(np.where(sums > 0, sums, 1.0), n))[ok]
+            for k in np.nonzero(sums <= 0)[0]:
+                noise[games[k], : n[k]] = np.random.dirichlet([alpha[k]] * int(n[k]))
         self.ext.mcts_apply_root_noise(*self._tree_args(tree), torch.from_numpy(noise).cuda(), tree["root_node"],
                                        max_nc, cfg.dirichlet_epsilon, 1.0, B, self._max_nodes)
 

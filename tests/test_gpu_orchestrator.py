@@ -354,3 +354,39 @@ def test_graph_waves_equal_eager(mask, max_ply, wave_parallel):
             assert np.array_equal(x.view(np.uint32) if x.dtype == np.float32 else x,
                                   y.view(np.uint32) if y.dtype == np.float32 else y)
     assert tree_equal(outs[0][-1], outs[1][-1]) == []
+
+
+def test_root_dirichlet_noise_rows(monkeypatch):
+    """_apply_root_dirichlet: one Dirichlet draw per active game over its root
+    children (rows sum to 1 on exactly the first num_children entries),
+    nothing for idle games; the mean over games of each row's first entry
+    is 1/n, as Dirichlet(alpha, ..., alpha) gives."""
+    import torch
+    B = 64
+    orch, states, tree = _setup(B, 16, 4096, 0, 30, 5)
+    ext = orch.ext
+    legal, nl, feat = ext.generate_legal_moves_and_fnn_features_batch(states, B)
+    orch._head_biases = (float(orch.net.value_fc.bias.item()), float(orch.net.action_fc2.bias.item()))
+    priors, _, cq = orch._eval_states(states, legal, nl, B, feat)
+    act = torch.ones((B,), dtype=torch.bool, device="cuda")
+    act[::5] = False
+    orch._expand_root_if_needed(tree, states, legal, nl, priors, cq, act.to(torch.int8), B)
+    got = []
+    monkeypatch.setattr(ext, "mcts_apply_root_noise", lambda *a: got.append(_np(a[12]).copy()), raising=False)
+    np.random.seed(3)
+    draws = []
+    for _ in range(200):
+        orch._apply_root_dirichlet(tree, B, act)
+        draws.append(got[-1])
+    nc = _np(tree["num_children"][torch.arange(B, device="cuda"), tree["root_node"]])
+    a = _np(act)
+    for d in draws:
+        for i in range(B):
+            n = int(nc[i])
+            if not a[i] or n == 0:
+                assert not d[i].any()
+            else:
+                assert abs(float(d[i, :n].sum()) - 1.0) < 1e-5 and not d[i, n:].any() and (d[i, :n] >= 0).all()
+    first = np.array([d[:, 0] for d in draws])  # [draws, B]
+    for i in np.nonzero(a & (nc > 1))[0]:
+        assert abs(first[:, i].mean() - 1.0 / nc[i]) < 0.12
