@@ -11,6 +11,16 @@ The network is not run here: its outputs for the root and for every
 simulation wave, the uniform draws of the Gumbel noise and the Dirichlet
 noise are inputs (recorded from the GPU run), in call order.  Top-k ties go
 to the lowest slot, as in the GPU counterpart.
+
+Pinning (tests/test_oracle_orchestrator.py): policy_target against the
+closed form of its temperature search, _stable_topk's tie order,
+immediate_wins against the reference's win detector (golden probe vectors)
+and _surround against the C oracle's count.  The reference has no test of
+its orchestrator, so the rest -- the reserve / fill ranking of `candidates`
+and the sequential-halving composition of `run` -- is parity unpinned: it is
+checked only against the independent torch restatement and invariants
+(legal chosen slot, policy a distribution over legal slots, root visits =
+completed simulations).
 """
 from __future__ import annotations
 
