@@ -1075,22 +1075,22 @@ __global__ __launch_bounds__(64) void k_extract_policy(Tree T, const int32_t* __
     }
 }
 
-// Per-wave search counters in one workgroup: stats[0] += simulations that
-// reached a leaf, [1] += their leaf legal counts, [2] += their virtual-loss
-// path lengths, [3] += rows.  A single workgroup owns stats, so the update is
-// a plain read-modify-write ordered by the stream.
+// Per-wave search counters: stats[0] += simulations that reached a leaf,
+// [1] += their leaf legal counts, [2] += their virtual-loss path lengths,
+// [3] += rows.  Each workgroup sums 1,024 rows and adds its partial sums
+// with device atomics (integer sums: the order does not matter).
 __global__ __launch_bounds__(1024) void k_wave_stats(const int32_t* __restrict__ leaf_idx,
                                                      const int32_t* __restrict__ num_legal,
                                                      const int32_t* __restrict__ vl_lens, int64_t total,
-                                                     int64_t* __restrict__ stats) {
-    __shared__ int64_t part[3][16];
+                                                     unsigned long long* __restrict__ stats) {
+    __shared__ unsigned long long part[3][16];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    int64_t a = 0, b = 0, c = 0;
-    for (int64_t i = tid; i < total; i += 1024) {
-        if (leaf_idx[i] < 0) continue;
-        a += 1;
-        b += num_legal[i];
-        c += vl_lens[i];
+    const int64_t i = (int64_t)blockIdx.x * 1024 + tid;
+    unsigned long long a = 0, b = 0, c = 0;
+    if (i < total && leaf_idx[i] >= 0) {
+        a = 1;
+        b = (unsigned long long)(long long)num_legal[i];
+        c = (unsigned long long)(long long)vl_lens[i];
     }
     for (int off = 32; off > 0; off >>= 1) {
         a += __shfl_xor(a, off);
@@ -1100,11 +1100,11 @@ __global__ __launch_bounds__(1024) void k_wave_stats(const int32_t* __restrict__
     if (lane == 0) { part[0][w] = a; part[1][w] = b; part[2][w] = c; }
     __syncthreads();
     if (tid < 3) {
-        int64_t sum = 0;
+        unsigned long long sum = 0;
         for (int k = 0; k < 16; k++) sum += part[tid][k];
-        stats[tid] += sum;
-    } else if (tid == 3) {
-        stats[3] += total;
+        atomicAdd(&stats[tid], sum);
+    } else if (tid == 3 && blockIdx.x == 0) {
+        atomicAdd(&stats[3], (unsigned long long)total);
     }
 }
 
@@ -1115,8 +1115,8 @@ extern "C" {
 int hg_mcts_wave_stats(const int32_t* leaf_idx, const int32_t* num_legal, const int32_t* vl_lens, int64_t total,
                        int64_t* stats, void* stream) {
     if (total <= 0) return 0;
-    hipLaunchKernelGGL(k_wave_stats, dim3(1), dim3(1024), 0, (hipStream_t)stream, leaf_idx, num_legal, vl_lens, total,
-                       stats);
+    hipLaunchKernelGGL(k_wave_stats, dim3((unsigned)((total + 1023) / 1024)), dim3(1024), 0, (hipStream_t)stream,
+                       leaf_idx, num_legal, vl_lens, total, reinterpret_cast<unsigned long long*>(stats));
     return finish();
 }
 
