@@ -353,13 +353,15 @@ __global__ __launch_bounds__(64) void k_select_slots(Tree T, const int8_t* __res
             plen = 1;
         }
         node = descend_rec(T, g0, node, r, pvc, 1, c_puct, det, sigma, q_penalty, O, sim, plen, vlen, lane);
+        __syncthreads();  // the next simulation reads this one's statistics
+        // the simulation's outputs go after the fence: nothing in this kernel
+        // reads them, so their stores complete while the next one descends
         if (lane == 0) {
             O.leaf[sim] = node;
             O.plen[sim] = plen;
             O.vlen[sim] = vlen;
         }
         zero_tails(O, sim, plen, vlen, lane);
-        __syncthreads();  // the next simulation reads this one's statistics
     }
 }
 
@@ -413,13 +415,13 @@ __global__ __launch_bounds__(64) void k_select_mask(Tree T, const int8_t* __rest
         }
         if (go) node = descend_rec(T, g0, node, rr, pvc, first_iter, c_puct, det, sigma, q_penalty, O, sim, plen,
                                    vlen, lane);
+        __syncthreads();  // the next simulation reads this one's statistics; outputs after the fence
         if (lane == 0) {
             O.leaf[sim] = node;
             O.plen[sim] = plen;
             O.vlen[sim] = vlen;
         }
         zero_tails(O, sim, plen, vlen, lane);
-        __syncthreads();
     }
 }
 
