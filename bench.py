@@ -467,6 +467,9 @@ def main():
         result["gpu_over_cpu"] = value / result["cpu_baseline"]["value"]
     if not args.no_mcts:
         result["mcts"] = mcts_leg(args)
+        if args.mcts_waves == "schedule":  # the second C5 schedule: one simulation per candidate per wave
+            w1 = argparse.Namespace(**{**vars(args), "mcts_waves": "1", "no_cpu": True})
+            result["mcts_w1"] = mcts_leg(w1)
     if not args.no_probe:
         result["probe"] = probe_leg(args)
     if not args.no_train:
