@@ -56,6 +56,8 @@ def parse_args():
     ap.add_argument("--no-c4", action="store_true", help="skip the C4 lockstep random-play leg")
     ap.add_argument("--c4-games", type=int, default=16384)
     ap.add_argument("--c4-plies", type=int, default=300)
+    ap.add_argument("--game-parts", type=int, default=None,
+                    help="C5 game ranges whose waves run on their own streams (default: 2 from 256 games)")
     ap.add_argument("--mcts-waves", choices=("schedule", "1"), default="schedule",
                     help="C5 simulations per candidate per wave: the (2,4,8,16) schedule or 1")
     ap.add_argument("--mcts-games", type=int, default=512)
@@ -181,6 +183,7 @@ def mcts_leg(args):
                         max_tree_nodes=1 + S * 256, wave_parallel=args.mcts_waves == "schedule")
     orch = FNNMCTSOrchestrator(net, cfg)
     orch.use_graphs = {"auto": None, "on": True, "off": False}[args.graphs]
+    orch.game_parts = args.game_parts
     ext = orch.ext
     if args.mcts_roots == "empty":
         states = ext.create_initial_states(G, 0)

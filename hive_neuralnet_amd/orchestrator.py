@@ -134,6 +134,14 @@ class FNNMCTSOrchestrator:
         self.graph_rows = 8192
         self.max_graphs = 64
         self._graphs: dict = {}
+        # simulation waves of disjoint game ranges on their own streams, so that
+        # one range's latency-bound tree walks overlap another's leaf evaluation
+        # (games are independent: results are identical to one range); None =
+        # two ranges from split_min_games games up, 1 = off
+        self.game_parts: int | None = None
+        self.split_min_games = 256
+        self._part_streams: list = []
+        self._part_ws: dict = {}
 
     def enable_counters(self) -> None:
         self._stats = torch.zeros((4,), dtype=torch.int64, device="cuda")
@@ -185,7 +193,7 @@ class FNNMCTSOrchestrator:
         c = self.net.config
         return c.hidden_dim == 64 and c.embed_dim == 64 and c.action_hidden == 64
 
-    def _eval_states(self, states, legal_moves, num_legal, total, root_features=None):
+    def _eval_states(self, states, legal_moves, num_legal, total, root_features=None, workspace=None):
         """(priors [total, 256], leaf values [total], child Q [total, 256]).
 
         The 64-wide presets run the fused path, hg_fnn_leaf_eval_lists: the
@@ -202,11 +210,13 @@ class FNNMCTSOrchestrator:
         if total == 0:
             empty = torch.zeros(0, MAX_L, dtype=torch.float32, device="cuda")
             return empty, empty.new_zeros((0,)), empty
-        need = self.ext.leaf_eval_workspace_bytes(total)
-        if self._leaf_ws is None or self._leaf_ws.numel() < need:
-            self._leaf_ws = torch.empty((need,), dtype=torch.uint8, device="cuda")
+        if workspace is None:
+            need = self.ext.leaf_eval_workspace_bytes(total)
+            if self._leaf_ws is None or self._leaf_ws.numel() < need:
+                self._leaf_ws = torch.empty((need,), dtype=torch.uint8, device="cuda")
+            workspace = self._leaf_ws
         return self.ext.fnn_leaf_eval_lists(states, legal_moves, num_legal, root_features.contiguous(), total,
-                                            self.net, self._head_biases, self._leaf_ws)
+                                            self.net, self._head_biases, workspace)
 
     def _eval_states_torch(self, states, legal_moves, num_legal, total, root_features=None):
         MAX_L = self._max_legal
@@ -361,6 +371,9 @@ class FNNMCTSOrchestrator:
         C = int(root_slots.shape[1])
         W = max(1, int(wave_size))
         q_penalty = float(cfg.virtual_q_penalty) if cfg.deterministic_non_root and W > 1 else 0.0
+        parts = self.game_parts if self.game_parts is not None else (2 if B >= self.split_min_games else 1)
+        if parts > 1 and B >= parts:
+            return self._run_split(tree, root_states, game_active, root_slots, B, C, per_slot, W, q_penalty, parts)
         sims = 0
         for wave in range(math.ceil(per_slot / W)):
             w = min(W, per_slot - wave * W)
@@ -379,7 +392,53 @@ class FNNMCTSOrchestrator:
             sims += total
         return sims
 
-    def _wave(self, tree, root_states, game_active, root_slots, C, B, w, q_penalty):
+    def _run_split(self, tree, root_states, game_active, root_slots, B, C, per_slot, W, q_penalty, parts):
+        """The waves of _run_simulations_for_root_slots over `parts` contiguous
+        game ranges, each range's waves in order on its own stream (default
+        priority), the ranges' launches interleaved wave by wave.  Every tree
+        array is per game ([B, ...] rows), so a range is a set of row views;
+        the ranges share nothing but the device-atomic wave counters."""
+        bounds = [(B * p) // parts for p in range(parts + 1)]
+        while len(self._part_streams) < parts:
+            self._part_streams.append(torch.cuda.Stream())
+        main = torch.cuda.current_stream()
+        ready = torch.cuda.Event()
+        ready.record(main)
+        ranges = []
+        for p in range(parts):
+            lo, hi = bounds[p], bounds[p + 1]
+            s = self._part_streams[p]
+            s.wait_event(ready)
+            ranges.append((p, {k: v[lo:hi] for k, v in tree.items()}, root_states[lo:hi], game_active[lo:hi],
+                           root_slots[lo:hi], hi - lo, s))
+        sims = 0
+        waves = math.ceil(per_slot / W)
+        last = []
+        for wave in range(waves):
+            w = min(W, per_slot - wave * W)
+            for p, tv, rs, ga, sl, nb, s in ranges:
+                with torch.cuda.stream(s):
+                    total = w * C * nb
+                    need = self.ext.leaf_eval_workspace_bytes(total)
+                    ws = self._part_ws.get(p)
+                    if ws is None or ws.numel() < need:
+                        ws = torch.empty((need,), dtype=torch.uint8, device="cuda")
+                        self._part_ws[p] = ws
+                    leaf_idx, leaf_states, nl, vlen = self._wave(tv, rs, ga, sl, C, nb, w, q_penalty, ws)
+                    if self.counters is not None:
+                        self.ext.mcts_wave_stats(leaf_idx, nl, vlen, total, self._stats)
+                    if self.keep_last_leaves and wave == waves - 1:
+                        last.append(leaf_states[leaf_idx >= 0])
+            sims += w * C * B
+        for r in ranges:
+            done = torch.cuda.Event()
+            done.record(r[-1])
+            main.wait_event(done)
+        if last:
+            self.last_leaves = torch.cat(last)
+        return sims
+
+    def _wave(self, tree, root_states, game_active, root_slots, C, B, w, q_penalty, workspace=None):
         """One wave of w simulations per root candidate (:982-1055): select ->
         replay -> legal + features -> leaf evaluation -> expansion + backup.
         No host synchronisation.  Returns (leaf_idx, leaf_states, num_legal, vl_lens)."""
@@ -390,7 +449,7 @@ class FNNMCTSOrchestrator:
                 *self._tree_args(tree), tree["child_init_q"], root_states, game_active, tree["root_node"],
                 root_slots, C, self._max_legal, cfg.c_puct, B, w, self._max_nodes, cfg.deterministic_non_root,
                 cfg.non_root_sigma, q_penalty)
-        priors, vals, child_q = self._eval_states(leaf_states, legal, nl, total, feat)
+        priors, vals, child_q = self._eval_states(leaf_states, legal, nl, total, feat, workspace)
         self.ext.mcts_expand_and_backprop_dense_priors_batch(
             *self._tree_args(tree), tree["child_init_q"], child_q, leaf_idx, leaf_states, legal, nl, priors,
             results, vals, vl, vlen, B, total, self._max_nodes, q_penalty)
@@ -416,10 +475,9 @@ class FNNMCTSOrchestrator:
             # the graph's own leaf-evaluation workspace, allocated outside capture and
             # kept alive with the graph
             ws = torch.empty((self.ext.leaf_eval_workspace_bytes(w * C * B),), dtype=torch.uint8, device="cuda")
-            self._leaf_ws = ws
             graph = torch.cuda.CUDAGraph()
             with torch.cuda.graph(graph):
-                outs = self._wave(tree, static["roots"], static["active"], static["slots"], C, B, w, q_penalty)
+                outs = self._wave(tree, static["roots"], static["active"], static["slots"], C, B, w, q_penalty, ws)
             entry = (graph, static, outs, ws)
             self._graphs[key] = entry
             # capture records the launches without running them: the replay below runs this wave

@@ -390,3 +390,39 @@ def test_root_dirichlet_noise_rows(monkeypatch):
     first = np.array([d[:, 0] for d in draws])  # [draws, B]
     for i in np.nonzero(a & (nc > 1))[0]:
         assert abs(first[:, i].mean() - 1.0 / nc[i]) < 0.12
+
+
+@pytest.mark.parametrize("mask,max_ply,parts", [(0, 60, 2), (7, 90, 3)])
+def test_game_ranges_on_streams_equal_one_range(mask, max_ply, parts):
+    """Simulation waves of disjoint game ranges on their own streams
+    (game_parts) against one range on the current stream: three plies with
+    rebases, every ply's choice, policy and visits, the wave counters and the
+    final trees identical."""
+    import torch
+    from hive_neuralnet_amd import hive_gpu
+    outs = []
+    for gp in (1, parts):
+        B = 18
+        orch, _, tree = _setup(B, 64, 8192, mask, max_ply, 81)
+        orch.game_parts = gp
+        orch.use_graphs = False
+        orch.enable_counters()
+        states, _ = hive_gpu.random_positions(B, mask, max_ply, 82)
+        torch.manual_seed(83)
+        np.random.seed(83)
+        active = torch.ones((B,), dtype=torch.bool, device="cuda")
+        rec = []
+        for _ in range(3):
+            r = orch.search_ply(states, tree, active)
+            rec.append((_np(r.chosen_slot), _np(r.policy), _np(r.slot_visits)))
+            orch.apply_and_rebase(states, tree, r)
+            active &= orch.ext.check_results_batch(states, B) == 0
+        rec.append(_np(orch._stats).copy())
+        rec.append({k: _np(v).copy() for k, v in tree.items()})
+        outs.append(rec)
+    for a, b in zip(outs[0][:3], outs[1][:3]):
+        for x, y in zip(a, b):
+            assert np.array_equal(x.view(np.uint32) if x.dtype == np.float32 else x,
+                                  y.view(np.uint32) if y.dtype == np.float32 else y)
+    assert np.array_equal(outs[0][3], outs[1][3])
+    assert tree_equal(outs[0][4], outs[1][4]) == []
