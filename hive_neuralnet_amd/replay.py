@@ -58,15 +58,17 @@ def build_forward_batch(ext, state_bytes: torch.Tensor, batch_size: int, num_act
     else:
         legal_moves, num_legal, root_features = ext.generate_legal_moves_and_fnn_features_batch(state_bytes, batch_size)
         num_actions = num_legal.to(torch.int64)
-    max_legal = legal_moves.shape[1]
-    slot = torch.arange(max_legal, device=state_bytes.device, dtype=torch.int64).unsqueeze(0)
-    valid = slot < num_actions.unsqueeze(1)
-    action_to_root = torch.arange(batch_size, device=state_bytes.device, dtype=torch.int64).unsqueeze(1) \
-        .expand_as(valid)[valid]
-    move_indices = slot.expand_as(valid)[valid]
-    total = int(action_to_root.shape[0])
+    dev = state_bytes.device
+    # rows in (root, slot) order: one host read of the row count, the row map
+    # built on the device
+    counts = num_actions.clamp(0, legal_moves.shape[1])
+    total = int(counts.sum().item())
     if total == 0:
-        return root_features, root_features[:0], action_to_root, num_actions
+        return root_features, root_features[:0], torch.zeros((0,), dtype=torch.int64, device=dev), num_actions
+    roots = torch.arange(batch_size, device=dev, dtype=torch.int64)
+    action_to_root = torch.repeat_interleave(roots, counts, output_size=total)
+    starts = torch.cumsum(counts, 0) - counts
+    move_indices = torch.arange(total, device=dev, dtype=torch.int64) - starts[action_to_root]
     succ = ext.fnn_successor_features_batch(state_bytes, legal_moves, action_to_root, move_indices, total)
     return root_features, succ, action_to_root, num_actions
 
