@@ -127,19 +127,23 @@ class FNNMCTSOrchestrator:
         self._leaf_ws: torch.Tensor | None = None
         # simulation waves replayed from captured HIP graphs (one per wave shape):
         # True, False, or None = only waves of fewer than graph_rows rows, where
-        # launch overhead is a large part of a wave (at 16 games x 1,024 sims a
-        # ply runs 14% faster from graphs; at 512 games x 4,096 sims eager
-        # launches are 1.5% faster, the graph's input copies outweighing it)
+        # launch overhead is a large part of a wave (at 16 games x 1,024 sims,
+        # 512-row waves, a ply runs 14% faster from graphs; with 2,048-row waves
+        # it is even, and from 4,096 rows eager launches are faster, the graph's
+        # input copies outweighing it)
         self.use_graphs: bool | None = None
-        self.graph_rows = 8192
+        self.graph_rows = 2048
         self.max_graphs = 64
         self._graphs: dict = {}
         # simulation waves of disjoint game ranges on their own streams, so that
         # one range's latency-bound tree walks overlap another's leaf evaluation
         # (games are independent: results are identical to one range); None =
-        # two ranges from split_min_games games up, 1 = off
+        # two ranges from split_min_games games and split_min_rows rows per
+        # range and wave up (smaller waves are bound by host launches, which
+        # ranges multiply), 1 = off
         self.game_parts: int | None = None
         self.split_min_games = 256
+        self.split_min_rows = 8192
         self._part_streams: list = []
         self._part_ws: dict = {}
 
@@ -371,7 +375,10 @@ class FNNMCTSOrchestrator:
         C = int(root_slots.shape[1])
         W = max(1, int(wave_size))
         q_penalty = float(cfg.virtual_q_penalty) if cfg.deterministic_non_root and W > 1 else 0.0
-        parts = self.game_parts if self.game_parts is not None else (2 if B >= self.split_min_games else 1)
+        if self.game_parts is not None:
+            parts = self.game_parts
+        else:
+            parts = 2 if B >= self.split_min_games and W * C * B >= 2 * self.split_min_rows else 1
         if parts > 1 and B >= parts:
             return self._run_split(tree, root_states, game_active, root_slots, B, C, per_slot, W, q_penalty, parts)
         sims = 0
