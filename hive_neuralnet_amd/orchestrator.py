@@ -464,21 +464,23 @@ class FNNMCTSOrchestrator:
 
     def _graph_wave(self, tree, root_states, game_active, root_slots, C, B, w, q_penalty):
         """_wave replayed from a captured HIP graph.  A graph is kept per wave
-        shape and tree; its inputs (root states, active games, root slots) are
-        copied into the graph's own buffers before each replay, and the network
-        enters through its parameter addresses and head biases, which are part
-        of the key.  The graph holds only kernel launches (the extension fills
+        shape, tree and root-state tensor; the active games and root slots are
+        copied into the graph's own buffers before each replay, the root states
+        and the network enter by address (parameter addresses and head biases
+        are part of the key).  The graph holds only kernel launches (the extension fills
         and zeroes with kernels, never memset nodes)."""
         cfg = self.config
         net_key = tuple(p.data_ptr() for p in self.net.parameters()) + tuple(self._head_biases or ())
         tree_key = tuple(v.data_ptr() for v in tree.values())
         key = (tree_key, B, C, w, float(q_penalty), bool(cfg.deterministic_non_root), float(cfg.c_puct),
-               float(cfg.non_root_sigma), tuple(root_states.shape), net_key)
+               float(cfg.non_root_sigma), root_states.data_ptr(), tuple(root_states.shape), net_key)
         entry = self._graphs.get(key)
         if entry is None:
             if len(self._graphs) >= self.max_graphs:  # oldest first
                 self._graphs.pop(next(iter(self._graphs)))
-            static = {"roots": root_states.clone(), "active": game_active.clone(), "slots": root_slots.clone()}
+            # the root states enter by address (part of the key: a ply's states
+            # do not move); the per-round inputs are copied into the graph's buffers
+            static = {"roots": root_states, "active": game_active.clone(), "slots": root_slots.clone()}
             # the graph's own leaf-evaluation workspace, allocated outside capture and
             # kept alive with the graph
             ws = torch.empty((self.ext.leaf_eval_workspace_bytes(w * C * B),), dtype=torch.uint8, device="cuda")
@@ -489,7 +491,6 @@ class FNNMCTSOrchestrator:
             self._graphs[key] = entry
             # capture records the launches without running them: the replay below runs this wave
         graph, static, outs, _ = entry
-        static["roots"].copy_(root_states)
         static["active"].copy_(game_active)
         static["slots"].copy_(root_slots)
         graph.replay()
