@@ -719,6 +719,32 @@ for _name, _fn in _mcts_methods().items():
 _extension = None
 
 
+# Entry points of the reference module outside this engine's path (bindings.cpp:254-476):
+# GNN / transformer token encoders, mobility labels, the PRS classifier, the
+# endgame hit mask, the experimental fused self-play kernel and the
+# move-generation profiling hooks.  They are present so a caller gets a clear
+# error instead of an AttributeError.
+_OUT_OF_SCOPE = (
+    "compute_mobility_batch", "debug_tactical_state_batch", "encode_states_batch", "endgame_hit_mask_batch",
+    "fnn_selfplay_batch", "generate_legal_moves_and_hybrid_root_features_batch", "get_movegen_profile",
+    "hybrid_gnn_encode_batch", "hybrid_gnn_encode_with_moves_batch", "hybrid_transformer_encode_with_moves_batch",
+    "hybrid_transformer_move_features_batch", "prs_v2_classify_batch", "reset_movegen_profile",
+)
+
+
+def _out_of_scope(name):
+    def fn(self, *args, **kwargs):
+        raise NotImplementedError(
+            f"{name} is not provided by the MI355X engine: it serves the GNN/transformer, PRS, mobility-label "
+            "or profiling lines of the reference, outside the move-generation / FNN / MCTS path built here")
+    fn.__name__ = name
+    return fn
+
+
+for _name in _OUT_OF_SCOPE:
+    setattr(HiveGpuExtension, _name, _out_of_scope(_name))
+
+
 def load_extension() -> HiveGpuExtension:
     """Idempotent: load libhive_gpu.so, initialise tables, return the extension."""
     global _extension

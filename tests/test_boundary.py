@@ -59,3 +59,21 @@ def test_no_fallback_without_device(monkeypatch):
     monkeypatch.setattr(hive_gpu, "_extension", None)
     with pytest.raises(RuntimeError):
         hive_gpu.load_extension()
+
+
+def test_reference_surface_complete():
+    """Every entry point of the reference module (bindings.cpp) exists on the
+    extension object; those outside this engine's path raise
+    NotImplementedError with a message."""
+    import pytest
+    from hive_neuralnet_amd import hive_gpu
+    names = ["initialize_tables", "create_initial_states", "apply_moves_batch", "check_results_batch",
+             "generate_legal_moves_batch", "generate_legal_moves_and_fnn_features_batch",
+             "fnn_successor_features_batch", "legal_moves_to_actions_batch", "compute_centroids_batch",
+             "mcts_select_with_root_slots_batch", "mcts_expand_and_backprop_dense_priors_batch",
+             "root_tactical_probe_batch", "queen_escape_flags_batch"] + list(hive_gpu._OUT_OF_SCOPE)
+    for n in names:
+        assert callable(getattr(hive_gpu.HiveGpuExtension, n, None)), n
+    ext = hive_gpu.HiveGpuExtension.__new__(hive_gpu.HiveGpuExtension)
+    with pytest.raises(NotImplementedError, match="not provided"):
+        ext.encode_states_batch(None, 1)
