@@ -579,7 +579,7 @@ HW_INL void words_centroid(uint32_t w, int lane, int& cq, int& cr) {
 
 // mcts_expand_and_backprop_dense_priors_kernel (mcts_tree.cuh:1068-1187).
 // One wave per game, simulations in order.  A simulation's loads come in
-// three rounds: its inputs (leaf, result, legal count, path, value, the
+// three dependent batches: its inputs (leaf, result, legal count, path, value, the
 // leaf's bitboards, legal list, priors and child values), then the tree
 // state they index (the leaf's children and terminal fields, the path nodes'
 // statistics, the root above the path), then the root's statistics.
@@ -597,7 +597,7 @@ __global__ __launch_bounds__(64) void k_expand_backprop(Tree T, LeafIn L, const 
     for (int64_t sim = g; sim < total; sim += B) {
         const int leaf = L.leaf[sim];
         if (leaf < 0) continue;
-        // round 1: the simulation's inputs (this kernel never writes them)
+        // first loads: the simulation's inputs (this kernel never writes them)
         const int res = L.results[sim];
         const int nl = L.nlegal[sim];
         int n = vl_lens[sim];
@@ -627,7 +627,7 @@ __global__ __launch_bounds__(64) void k_expand_backprop(Tree T, LeafIn L, const 
                 xq[j] = cqv[m];
             }
         }
-        // round 2: the tree state they index
+        // second loads: the tree state they index
         const int64_t li = g0 + leaf;
         const int fc = T.fc[li];
         const int lit = T.it[li];
@@ -734,7 +734,7 @@ __global__ __launch_bounds__(64) void k_expand_backprop(Tree T, LeafIn L, const 
                     T.tv[ni] = (tv1 + 1.0f) + sv;
                 }
             }
-            if (lane == 0) {  // round 3: the root, and any node above it
+            if (lane == 0) {  // third loads: the root, and any node above it
                 int node = top;
                 float w = (n & 1) ? -v : v;
                 for (int s2 = n; s2 < kDepth + 1 && node >= 0; s2++) {

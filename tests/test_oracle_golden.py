@@ -2,7 +2,7 @@
 
 Fixtures: tests/golden/golden_c{1,2,3,4}.npz, produced by
 tests/golden/make_golden.py from the reference's hive_gpu/csrc/cpu_native.cpp
-compiled in the survey container.  Every comparison is bit-exact (features
+compiled for the host (oracle/Makefile, target ref).  Every comparison is bit-exact (features
 are compared as raw float32 bit patterns).
 """
 import numpy as np
