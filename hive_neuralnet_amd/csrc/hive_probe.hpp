@@ -232,6 +232,10 @@ HW_INL bool probe_win2(Pos& P, Replies& Rp, const uint8_t* __restrict__ S, const
     __syncthreads();
     if (l == 0) apply_on_board(P, S, mt, mp, mf, mto);
     __syncthreads();
+    // the child's base fields, put back before each reply instead of
+    // reloading the root and applying m again
+    BaseRegs child;
+    save_base(P, child, lane);
     prepare_loaded(P, lane);
     const int opp = P.turn & 1, me = opp ^ 1;  // the opponent replies
     const int cs = surround_now(P, opp);
@@ -276,13 +280,11 @@ HW_INL bool probe_win2(Pos& P, Replies& Rp, const uint8_t* __restrict__ S, const
         if (!hw_wave_any(more)) break;
         int r = more ? 32 * k + __ffs(w) - 1 : -1;
         if (more) w &= w - 1;
-        load_position(P, S, lane);
+        restore_base(P, child, lane);
         __syncthreads();
-        if (l == 0 && r >= 0) {
-            apply_on_board(P, S, mt, mp, mf, mto);
+        if (l == 0 && r >= 0)
             apply_on_board(P, S, Rp.mv[r][0], Rp.mv[r][1], Rp.mv[r][2] | (Rp.mv[r][3] << 8),
                            Rp.mv[r][4] | (Rp.mv[r][5] << 8));
-        }
         __syncthreads();
         prepare_loaded(P, lane);
         bool won = immediate_win(P, lane);
