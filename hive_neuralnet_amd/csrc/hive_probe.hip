@@ -1,5 +1,5 @@
 // hive_probe.hip -- root_tactical_probe_batch (game_logic.cu:1579-1616 over
-// root_tactical_probe_kernel :290-397) as four launches on the caller's
+// root_tactical_probe_kernel :290-397) as six launches on the caller's
 // stream, no host synchronisation:
 //
 //   k_probe_roots   one lane group per root (hive_probe.hpp probe_root):
@@ -9,9 +9,12 @@
 //                   stages appended to the workspace's job lists;
 //   k_probe_screen  one lane group per screen job: allowed[r][i] = 0 when
 //                   the opponent wins at once after move i;
-//   k_probe_win2    one lane group per two-move candidate still allowed:
-//                   the lowest passing slot of each root by atomic min
-//                   (winning[] holds kUndecided meanwhile);
+//   k_probe_win2    one lane group per (two-move candidate, part) still
+//                   allowed: the part's grandchildren, fail[candidate] = 1
+//                   when one is not won;
+//   k_probe_win2_commit  per candidate no part failed: the lowest passing
+//                   slot of each root by atomic min (winning[] holds
+//                   kUndecided meanwhile);
 //   k_probe_finish  per root: kUndecided -> -1, forced = the screen ran and
 //                   left no move allowed.
 //
@@ -41,7 +44,7 @@ __global__ __launch_bounds__(64) void k_probe_roots(const uint8_t* __restrict__ 
                                                     int win2, int64_t* __restrict__ winning,
                                                     uint8_t* __restrict__ allowed, uint8_t* __restrict__ gate_out,
                                                     int32_t* __restrict__ counters, int32_t* __restrict__ jobs_screen,
-                                                    int32_t* __restrict__ jobs_win2) {
+                                                    int32_t* __restrict__ jobs_win2, int32_t* __restrict__ fail_win2) {
     __shared__ Pos PS[kPosPerWave];
     const int lane = threadIdx.x, l = gl(lane);
     const int64_t r0 = (int64_t)blockIdx.x * kPosPerWave + (lane >> 5);
@@ -70,7 +73,10 @@ __global__ __launch_bounds__(64) void k_probe_roots(const uint8_t* __restrict__ 
         if (l == 0) {
             int j = base;
             for (int k = 0; k < 8; k++)
-                for (uint32_t w = R.cand[k]; w; w &= w - 1) jobs_win2[j++] = (int32_t)(r * kMaxLegal + 32 * k + __ffs(w) - 1);
+                for (uint32_t w = R.cand[k]; w; w &= w - 1) {
+                    fail_win2[j] = 0;
+                    jobs_win2[j++] = (int32_t)(r * kMaxLegal + 32 * k + __ffs(w) - 1);
+                }
         }
     }
 }
@@ -98,22 +104,35 @@ __global__ __launch_bounds__(64) void k_probe_win2(const uint8_t* __restrict__ s
                                                    const int32_t* __restrict__ counters,
                                                    const int32_t* __restrict__ jobs,
                                                    const uint8_t* __restrict__ allowed,
-                                                   int64_t* __restrict__ winning) {
+                                                   int32_t* __restrict__ fail) {
     __shared__ Pos PS[kPosPerWave];
     __shared__ Replies RS[kPosPerWave];
     const int lane = threadIdx.x;
-    const int64_t count = counters[1];
-    for (int64_t p = blockIdx.x; 2 * p < count; p += gridDim.x) {
-        const int64_t j0 = 2 * p + (lane >> 5);
-        const bool live = j0 < count;
-        const int job = jobs[live ? j0 : 2 * p];
+    const int64_t items = (int64_t)counters[1] * kWin2Parts;  // (candidate, part)
+    for (int64_t p = blockIdx.x; 2 * p < items; p += gridDim.x) {
+        const int64_t q0 = 2 * p + (lane >> 5);
+        const bool live = q0 < items;
+        const int64_t q = live ? q0 : 2 * p;
+        const int64_t j = q / kWin2Parts;
+        const int job = jobs[j];
         const int64_t r = job / kMaxLegal, i = job % kMaxLegal;
         const bool active = live && allowed[job] != 0;
         bool ok = probe_win2(PS[lane >> 5], RS[lane >> 5], states + r * kStateBytes,
-                             legal + (r * kMaxLegal + i) * 6, active, lane);
-        if (active && ok && gl(lane) == 0)
-            atomicMin(reinterpret_cast<unsigned long long*>(winning + r), (unsigned long long)i);
+                             legal + (r * kMaxLegal + i) * 6, active, (int)(q % kWin2Parts), lane);
+        if (active && !ok && gl(lane) == 0) fail[j] = 1;
         __syncthreads();
+    }
+}
+
+// a candidate no part failed wins: the lowest such slot of each root
+__global__ void k_probe_win2_commit(const int32_t* __restrict__ counters, const int32_t* __restrict__ jobs,
+                                    const uint8_t* __restrict__ allowed, const int32_t* __restrict__ fail,
+                                    int64_t* __restrict__ winning) {
+    const int64_t count = counters[1];
+    for (int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; j < count; j += (int64_t)gridDim.x * blockDim.x) {
+        const int job = jobs[j];
+        if (allowed[job] != 0 && fail[j] == 0)
+            atomicMin(reinterpret_cast<unsigned long long*>(winning + job / kMaxLegal), (unsigned long long)(job % kMaxLegal));
     }
 }
 
@@ -138,7 +157,7 @@ __global__ void k_probe_finish(const int32_t* __restrict__ num_legal, int64_t B,
 
 extern "C" {
 
-int64_t hg_root_tactical_probe_workspace(int64_t B) { return B <= 0 ? 0 : 2 + 2 * B * kMaxLegal; }
+int64_t hg_root_tactical_probe_workspace(int64_t B) { return B <= 0 ? 0 : 2 + 3 * B * kMaxLegal; }
 
 int hg_root_tactical_probe(const uint8_t* states, const uint8_t* legal_moves, const int32_t* num_legal,
                            const float* priors, int64_t B, int enable_win_in_one, int enable_check_opponent_wins,
@@ -150,15 +169,19 @@ int hg_root_tactical_probe(const uint8_t* states, const uint8_t* legal_moves, co
     int32_t* counters = workspace;
     int32_t* jobs_screen = workspace + 2;
     int32_t* jobs_win2 = jobs_screen + B * kMaxLegal;
+    int32_t* fail_win2 = jobs_win2 + B * kMaxLegal;
     hipLaunchKernelGGL(k_probe_reset, dim3(1), dim3(64), 0, s, counters);
     hipLaunchKernelGGL(k_probe_roots, dim3((unsigned)((B + kPosPerWave - 1) / kPosPerWave)), dim3(64), 0, s, states,
                        legal_moves, num_legal, priors, B, enable_win_in_one, enable_check_opponent_wins,
-                       enable_win_in_two, winning, allowed, forced, counters, jobs_screen, jobs_win2);
+                       enable_win_in_two, winning, allowed, forced, counters, jobs_screen, jobs_win2, fail_win2);
     const int64_t pairs = (B * kMaxLegal + 1) / 2;
     const unsigned grid = (unsigned)(pairs < kJobGrid ? pairs : kJobGrid);
     hipLaunchKernelGGL(k_probe_screen, dim3(grid), dim3(64), 0, s, states, legal_moves, counters, jobs_screen, allowed);
-    hipLaunchKernelGGL(k_probe_win2, dim3(grid), dim3(64), 0, s, states, legal_moves, counters, jobs_win2, allowed,
-                       winning);
+    const int64_t items = (B * kMaxLegal * kWin2Parts + 1) / 2;
+    hipLaunchKernelGGL(k_probe_win2, dim3((unsigned)(items < kJobGrid ? items : kJobGrid)), dim3(64), 0, s, states,
+                       legal_moves, counters, jobs_win2, allowed, fail_win2);
+    hipLaunchKernelGGL(k_probe_win2_commit, dim3((unsigned)((B + 255) / 256)), dim3(256), 0, s, counters, jobs_win2,
+                       allowed, fail_win2, winning);
     hipLaunchKernelGGL(k_probe_finish, dim3((unsigned)((B + 255) / 256)), dim3(256), 0, s, num_legal, B, winning,
                        allowed, forced);
     return (int)hipGetLastError();

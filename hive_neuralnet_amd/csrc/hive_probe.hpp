@@ -220,12 +220,19 @@ struct Replies {
     int n;
 };
 
+// The grandchildren of one candidate are split over kWin2Parts programs (part
+// p tests the replies whose slot is p modulo kWin2Parts), so a candidate with
+// many replies is not one long serial walk; the candidate passes when no part
+// fails.  kWin2Parts divides 32.
+constexpr int kWin2Parts = 8;
+
 // probe_win2: after root move m, does every reply keep the opponent's queen
-// surround at or above its level after m, and leave a position the root
-// player has already won or wins at once?  `active` false: the group follows
-// the other group of its wave and its result is meaningless.
+// surround at or above its level after m, and does every reply of this part
+// leave a position the root player has already won or wins at once?  `active`
+// false: the group follows the other group of its wave and its result is
+// meaningless.
 HW_INL bool probe_win2(Pos& P, Replies& Rp, const uint8_t* __restrict__ S, const uint8_t* __restrict__ m,
-                       bool active, int lane) {
+                       bool active, int part, int lane) {
     const int l = gl(lane);
     const int mt = m[0], mp = m[1], mf = m[2] | (m[3] << 8), mto = m[4] | (m[5] << 8);
     load_position(P, S, lane);
@@ -254,6 +261,8 @@ HW_INL bool probe_win2(Pos& P, Replies& Rp, const uint8_t* __restrict__ S, const
     // generate_non_decreasing_surround_replies (move_gen.cuh:876-898) and the
     // replies that already win for the root player
     bool drop = false;
+    uint32_t pm = 0;  // the slots of this part within each 32-slot word
+    for (int b = part; b < 32; b += kWin2Parts) pm |= 1u << b;
     for (int k = 0; k < 8; k++) {
         int i = 32 * k + l;
         bool need = false;
@@ -264,7 +273,7 @@ HW_INL bool probe_win2(Pos& P, Replies& Rp, const uint8_t* __restrict__ S, const
             if (surround_after(P, e, opp) < cs) drop = true;
             need = result_after(P, e) != (me ? 2 : 1);
         }
-        uint32_t nw = grp_ballot(need, lane);
+        uint32_t nw = grp_ballot(need, lane) & pm;
         if (l == 0) Rp.need[k] = nw;
     }
     if (l == 0) Rp.n = L.n;

@@ -89,7 +89,7 @@ void emu_queen_escape(const uint8_t* states, int64_t B, uint8_t* out) {
 }
 
 // root_tactical_probe_batch: the group programs of hive_probe.hpp in the
-// order and with the bookkeeping of hive_probe.hip's four launches
+// order and with the bookkeeping of hive_probe.hip's launches
 void emu_root_probe(const uint8_t* states, const uint8_t* legal, const int32_t* nl, const float* pr, int64_t B, int f1,
                     int f2, int f3, int64_t* win, uint8_t* allowed, uint8_t* forced) {
     std::vector<RootProbe> R(B);
@@ -121,22 +121,25 @@ void emu_root_probe(const uint8_t* states, const uint8_t* legal, const int32_t* 
             bool bad = probe_screen(g_pos[t / kW], states + r * kStateBytes, legal + (r * 256 + i) * 6, t);
             if (live && t % kW == 0) allowed[job] = bad ? 0 : 1;
         });
+    std::vector<int> fail(nw, 0);
+    const int64_t items = nw * kWin2Parts;
     if (nw)
-        run_group(64, (nw + 1) / 2, [&](int64_t p, int t) {
-            int64_t j = 2 * p + t / kW;
-            bool live = j < nw;
-            int job = jw[live ? j : 2 * p];
+        run_group(64, (items + 1) / 2, [&](int64_t p, int t) {
+            int64_t q = 2 * p + t / kW;
+            bool live = q < items;
+            if (!live) q = 2 * p;
+            int64_t j = q / kWin2Parts;
+            int job = jw[j];
             int64_t r = job / 256, i = job % 256;
             bool active = live && allowed[job];
             bool ok = probe_win2(g_pos[t / kW], g_rep[t / kW], states + r * kStateBytes, legal + (r * 256 + i) * 6,
-                                 active, t);
-            if (active && ok && t % kW == 0) {
-                int64_t cur = __atomic_load_n(&win[r], __ATOMIC_SEQ_CST);
-                while (i < cur && !__atomic_compare_exchange_n(&win[r], &cur, i, false, __ATOMIC_SEQ_CST,
-                                                               __ATOMIC_SEQ_CST)) {
-                }
-            }
+                                 active, (int)(q % kWin2Parts), t);
+            if (active && !ok && t % kW == 0) __atomic_store_n(&fail[j], 1, __ATOMIC_SEQ_CST);
         });
+    for (int64_t j = 0; j < nw; j++) {
+        int64_t r = jw[j] / 256, i = jw[j] % 256;
+        if (allowed[jw[j]] && !fail[j] && i < win[r]) win[r] = i;
+    }
     for (int64_t r = 0; r < B; r++) {
         if (win[r] == (1 << 20)) win[r] = -1;
         uint8_t f = 0;
