@@ -14,9 +14,9 @@ algorithmic bytes per position = state 3424 + moves 1536 + n 4 + features
 time measured with HIP events on the launch stream.
 
 cpu_baseline: this repository's C restatement of the reference algorithm
-(oracle/, "port", the same work: moves + features + action indices) on the
-host cores; when oracle/_ref/libhive_ref.so (the reference's own CPU build)
-is present, its legal-moves + features rate is reported beside it.
+(oracle/, "port", the same work: moves + features + action indices) on
+every host CPU granted to the job, with nproc, the affinity mask, the cgroup
+quota and the CPU model.  The reference's own CPU build never runs here.
 """
 from __future__ import annotations
 
@@ -46,7 +46,7 @@ def parse_args():
     ap.add_argument("--batch", type=int, default=65536)
     ap.add_argument("--max-ply", type=int, default=120)
     ap.add_argument("--mask", type=int, default=0)
-    ap.add_argument("--cpu-threads", type=int, default=0, help="0 = min(16, cores)")
+    ap.add_argument("--cpu-threads", type=int, default=0, help="0 = every CPU granted to the job")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="target CPU-thread seconds for the baseline")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-mcts", action="store_true", help="skip the C5 Gumbel self-play leg")
@@ -80,41 +80,60 @@ def traffic_per_launch():
     return float(m.group(1)) if m else None
 
 
+def host_cpus():
+    """The host CPUs this process may use: os.cpu_count() (nproc of the
+    machine), the affinity mask, the cgroup CPU quota, and the thread count
+    the CPU baselines use -- every CPU granted to the job (the smaller of the
+    affinity mask and the quota).  With the full model name."""
+    nproc = os.cpu_count() or 1
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except AttributeError:
+        affinity = nproc
+    quota = None
+    try:
+        q, period = open("/sys/fs/cgroup/cpu.max").read().split()[:2]
+        if q != "max":
+            quota = float(q) / float(period)
+    except (OSError, ValueError):
+        pass
+    threads = affinity if quota is None else max(1, min(affinity, int(quota + 0.5)))
+    model = "unknown"
+    try:
+        model = next(l.split(":", 1)[1].strip() for l in open("/proc/cpuinfo") if l.startswith("model name"))
+    except (OSError, StopIteration):
+        pass
+    return {"nproc": nproc, "affinity": affinity, "cgroup_quota": quota, "threads": threads, "cpu_model": model}
+
+
+def baseline_threads(args):
+    return args.cpu_threads or host_cpus()["threads"]
+
+
 def cpu_baseline(states_np, threads, target_s):
-    from oracle import Oracle, Reference
+    """The oracle's moves + features + action indices over the workload on
+    `threads` pthreads, median of 5 passes; one thread over a slice beside it."""
+    from oracle import Oracle
     orc = Oracle()
     B = states_np.shape[0]
     orc.batch_legal_features_actions(states_np[: min(B, 4096)], threads=threads)  # warm
-    t0 = time.perf_counter()
-    orc.batch_legal_features_actions(states_np, threads=threads)
-    one = time.perf_counter() - t0
-    reps = max(3, min(50, int(target_s / max(one * threads, 1e-6))))
     rates = []
-    for _ in range(reps):
+    for _ in range(5):
         t0 = time.perf_counter()
         orc.batch_legal_features_actions(states_np, threads=threads)
         rates.append(B / (time.perf_counter() - t0))
-    out = {
+    one = states_np[: min(B, 8192)]
+    t0 = time.perf_counter()
+    orc.batch_legal_features_actions(one, threads=1)
+    per_core = one.shape[0] / (time.perf_counter() - t0)
+    cpus = host_cpus()
+    return {
         "value": statistics.median(rates), "unit": "positions/s", "cores": threads, "kind": "port",
-        "sample": f"the full {B}-position workload, {reps} passes, median; oracle/hive_oracle.c "
-                  f"(moves + features + action indices), {threads} pthreads",
+        "sample": f"the full {B}-position workload, 5 passes, median; oracle/hive_oracle.c "
+                  f"(moves + features + action indices), {threads} pthreads = every CPU granted to this job",
+        "per_core_value": per_core, "per_core_sample": f"the first {one.shape[0]} positions on one thread",
+        "nproc_linear_estimate": per_core * cpus["nproc"], **cpus,
     }
-    ref = Reference.load()
-    if ref is not None:
-        ref.batch_legal_features(states_np[: min(B, 4096)], threads=threads)
-        rr = []
-        for _ in range(max(3, reps // 2)):
-            t0 = time.perf_counter()
-            ref.batch_legal_features(states_np, threads=threads)
-            rr.append(B / (time.perf_counter() - t0))
-        out["reference_value"] = statistics.median(rr)
-        out["reference_sample"] = ("reference hive_gpu/csrc headers compiled for the host (oracle/_ref), "
-                                   f"legal moves + features only, {threads} threads, same positions")
-    try:
-        out["cpu_model"] = next(l.split(":", 1)[1].strip() for l in open("/proc/cpuinfo") if l.startswith("model name"))
-    except Exception:
-        pass
-    return out
 
 
 def mcts_cpu_baseline(net, leaves_np, threads, target_s):
@@ -236,8 +255,7 @@ def mcts_leg(args):
         cfg.num_simulations = min(S, 256)
         orch.search_ply(states, tree, active)
         leaves = orch.last_leaves.cpu().numpy()
-        threads = args.cpu_threads or max(1, min(16, os.cpu_count() or 1))
-        out["cpu_baseline"] = mcts_cpu_baseline(net, leaves, threads, args.cpu_seconds)
+        out["cpu_baseline"] = mcts_cpu_baseline(net, leaves, baseline_threads(args), args.cpu_seconds)
         out["gpu_over_cpu"] = value / out["cpu_baseline"]["value"]
     return out
 
@@ -268,7 +286,7 @@ def probe_leg(args):
            "immediate_or_forced_wins": int((w >= 0).sum().item()), "forced_random": int(f.sum().item())}
     if not args.no_cpu:
         from oracle import Oracle
-        threads = args.cpu_threads or max(1, min(16, os.cpu_count() or 1))
+        threads = baseline_threads(args)
         st, lm, n, p = states.cpu().numpy(), legal.cpu().numpy(), nl.cpu().numpy(), pr.cpu().numpy()
         orc = Oracle()
         t0 = time.perf_counter()
@@ -354,7 +372,7 @@ def c4_leg(args):
            "final_state_hash": f"{fnv1a64_of(hashes):016x}"}
     if not args.no_cpu:
         from oracle import Oracle
-        threads = args.cpu_threads or max(1, min(16, os.cpu_count() or 1))
+        threads = baseline_threads(args)
         orc = Oracle()
         k = min(G, 64)
         t1 = time.perf_counter()
@@ -472,7 +490,7 @@ def main():
         "api_unfused_positions_per_s": unfused,
     }
     if not args.no_cpu:
-        threads = args.cpu_threads or max(1, min(16, os.cpu_count() or 1))
+        threads = baseline_threads(args)
         result["cpu_baseline"] = cpu_baseline(states.cpu().numpy(), threads, args.cpu_seconds)
         result["gpu_over_cpu"] = value / result["cpu_baseline"]["value"]
     if not args.no_mcts:

@@ -13,6 +13,7 @@ GPU, the calls raise.
 from __future__ import annotations
 
 import ctypes
+import math
 import os
 import threading
 
@@ -195,14 +196,19 @@ def _check(err: int, what: str) -> None:
 
 
 def _dev(t: torch.Tensor, name: str, dtype: torch.dtype, inner: tuple, rows: int) -> torch.Tensor:
-    """Validate a device tensor: dtype, trailing shape, >= rows rows, contiguous."""
+    """Validate a device tensor: dtype, trailing shape, >= rows rows, contiguous.
+
+    A tensor whose trailing shape differs is accepted only when it is flat
+    (1-D) and contiguous, as a view of rows of `inner` (never a copy: an
+    output buffer the kernel writes must be the caller's memory)."""
     if not isinstance(t, torch.Tensor) or t.device.type != "cuda":
         raise ValueError(f"{name} must be a GPU tensor")
     if t.dtype != dtype:
         raise ValueError(f"{name} must be {dtype}, got {t.dtype}")
     if inner and tuple(t.shape[-len(inner):]) != tuple(inner):
-        if t.numel() != 0 and t.numel() % max(1, int(torch.tensor(inner).prod())) == 0:
-            t = t.reshape(-1, *inner)
+        size = math.prod(inner)
+        if t.dim() == 1 and t.is_contiguous() and t.numel() % size == 0:
+            t = t.view(-1, *inner)
         else:
             raise ValueError(f"{name} must have trailing shape {inner}, got {tuple(t.shape)}")
     lead = t.shape[0] if t.dim() > len(inner) else 1

@@ -204,3 +204,28 @@ def test_successor_rows_device_sized(ext, oracle, T, zero_every):
     want = oracle.batch_successor_features(st, moves, want_a2r, want_mi)
     got = feat[:total].cpu().numpy()
     assert np.array_equal(_bits(got), _bits(want))
+
+
+def test_mismatched_shapes_rejected(ext):
+    """A tensor whose trailing shape differs from the entry point's layout is
+    rejected unless it is a flat contiguous buffer, which is taken as a view
+    (so an output buffer is never silently replaced by a copy)."""
+    st = ext.create_initial_states(4)
+    with pytest.raises(ValueError, match="trailing shape"):
+        ext.generate_legal_moves_batch(st.view(4, 214, 16), 4)
+    with pytest.raises(ValueError, match="trailing shape"):
+        ext.generate_legal_moves_batch(st.view(8, 1712), 4)
+    flat = st.reshape(-1)
+    m1, n1 = ext.generate_legal_moves_batch(flat, 4)
+    m2, n2 = ext.generate_legal_moves_batch(st, 4)
+    assert torch.equal(m1, m2) and torch.equal(n1, n2)
+    # a flat out= buffer is written in place
+    legal, nl = m2, n2
+    a2r = torch.zeros((int(nl[0].item()),), dtype=torch.int64, device="cuda")
+    mi = torch.arange(a2r.shape[0], dtype=torch.int64, device="cuda")
+    want = ext.fnn_successor_features_batch(st, legal, a2r, mi, a2r.shape[0])
+    out = torch.full((a2r.shape[0] * 122,), float("nan"), dtype=torch.float32, device="cuda")
+    ext.fnn_successor_features_batch(st, legal, a2r, mi, a2r.shape[0], out=out)
+    assert torch.equal(out.view(-1, 122), want)
+    with pytest.raises(ValueError, match="trailing shape"):
+        ext.fnn_successor_features_batch(st, legal, a2r, mi, a2r.shape[0], out=out.view(-1, 61))
