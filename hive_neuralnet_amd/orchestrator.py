@@ -298,6 +298,15 @@ class FNNMCTSOrchestrator:
             g = torch.where(valid, -torch.log(-torch.log(u)), torch.full_like(u, -1e30))
             return topk_stable(g + legal_logits, k)[1].to(torch.int32)
         qual = self._queen_surround_qualifying_mask(states, legal_moves, num_legal, total)
+        return self._candidate_row(qual, valid, priors, k, reserve)
+
+    def _candidate_row(self, qual, valid, priors, k, reserve):
+        """The root candidate row (fnn_mcts_orchestrator.py:411-444): `reserve`
+        columns of qualifying slots by prior (-1 padded), then `k` columns of the
+        other legal slots by prior, the concatenation cut to k columns.  The fill
+        ranks every slot (chosen and illegal ones at -1e30), so past the other
+        legal slots it continues with the reserve slots, lowest slot first."""
+        total, max_legal = priors.shape
         reserve_scores = torch.where(qual, priors, torch.full_like(priors, -1e30))
         reserve_per_game = qual.sum(dim=1).clamp(max=reserve)
         _, reserve_order = topk_stable(reserve_scores, reserve)
@@ -589,32 +598,11 @@ class FNNMCTSOrchestrator:
             cand = topk_slots.to(torch.int32)
             cvalid = torch.gather(valid_slot, 1, cand.long().clamp(min=0)) & (cand >= 0)
             cand = torch.where(cvalid, cand, torch.full_like(cand, -1))
-            per_round = max(1, cfg.num_simulations // _GUMBEL_ROUNDS)
-            for r in range(_GUMBEL_ROUNDS):
-                cvalid = cand >= 0
-                C = int(cand.shape[1])
-                wave = _GUMBEL_WAVE_SCHEDULE[min(r, len(_GUMBEL_WAVE_SCHEDULE) - 1)] if cfg.wave_parallel else 1
-                sims += self._run_simulations_for_root_slots(tree, states, game_active, cand, B,
-                                                             max(1, per_round // C), wave)
-                if C <= 1:
-                    continue
-                keep_n = (cvalid.sum(dim=1) // 2).clamp(min=1)
-                max_keep = C // 2
-                visits, q = self._root_child_stats(tree, B, cand)
-                sigma = (cfg.c_visit + visits.max()) * cfg.c_scale
-                score = (torch.gather(gumbel + legal_logits, 1, cand.long().clamp(min=0)) + sigma * q).float()
-                score = torch.where(cvalid, score, torch.full_like(score, -1e30))
-                _, keep_pos = topk_stable(score, max_keep)
-                keep_ok = torch.arange(max_keep, device="cuda").unsqueeze(0) < keep_n.unsqueeze(1)
-                cand = torch.where(keep_ok, torch.gather(cand, 1, keep_pos), torch.full_like(keep_pos, -1,
-                                                                                            dtype=torch.int32))
-            cvalid = cand >= 0
-            visits, q = self._root_child_stats(tree, B, cand)
-            sigma = (cfg.c_visit + visits.max()) * cfg.c_scale
-            final = (torch.gather(gumbel + legal_logits, 1, cand.long().clamp(min=0)) + sigma * q).float()
-            final = torch.where(cvalid, final, torch.full_like(final, -1e30))
-            pos = torch.argmax(final, dim=1)
-            chosen = torch.gather(cand, 1, pos.unsqueeze(1)).squeeze(1).clamp(min=0).to(torch.long)
+            chosen, sims = self._sequential_halving(
+                cand, gumbel + legal_logits,
+                lambda c, per_slot, wave: self._run_simulations_for_root_slots(tree, states, game_active, c, B,
+                                                                               per_slot, wave),
+                lambda c: self._root_child_stats(tree, B, c))
             slot_visits, slot_q = self._root_child_stats(tree, B, self._slot_idx.expand(B, -1))
             visited = (slot_visits > 0) & valid_slot
             max_n = slot_visits.float().max(dim=1, keepdim=True).values
@@ -637,6 +625,48 @@ class FNNMCTSOrchestrator:
             chosen = torch.where(forced, rand_slots, chosen)
             probs = torch.where(forced.unsqueeze(1), torch.zeros_like(probs), probs)
         return PlyResult(chosen, legal, nl, probs, slot_visits, has_actions, sims, stats, forced)
+
+    def _sequential_halving(self, cand, base, run_round, child_stats):
+        """Gumbel sequential halving (fnn_mcts_orchestrator.py:650-731).
+
+        cand [B, C] int32 root slots (-1 = none); base [B, 256] = Gumbel noise +
+        legal logits.  Round r (of 4) calls run_round(cand, per_slot, wave): per_slot
+        = max(1, (simulations // 4) // C) simulations per candidate column, in waves
+        of `wave` per column ((2, 4, 8, 16)[r], or 1 without wave_parallel); unless
+        C = 1 it then keeps, in C // 2 columns, the top max(1, valid // 2)
+        candidates by base[slot] + sigma * q, where (visits, q) = child_stats(cand)
+        and sigma = (c_visit + the largest visit count of any candidate in the
+        batch) * c_scale.  The final choice is the argmax of the same score over
+        the survivors.  Returns (chosen slot [B] int64, simulations run)."""
+        cfg = self.config
+        B = cand.shape[0]
+        sims = 0
+        per_round = max(1, cfg.num_simulations // _GUMBEL_ROUNDS)
+        for r in range(_GUMBEL_ROUNDS):
+            cvalid = cand >= 0
+            C = int(cand.shape[1])
+            wave = _GUMBEL_WAVE_SCHEDULE[min(r, len(_GUMBEL_WAVE_SCHEDULE) - 1)] if cfg.wave_parallel else 1
+            sims += run_round(cand, max(1, per_round // C), wave)
+            if C <= 1:
+                continue
+            keep_n = (cvalid.sum(dim=1) // 2).clamp(min=1)
+            max_keep = C // 2
+            visits, q = child_stats(cand)
+            sigma = (cfg.c_visit + visits.max()) * cfg.c_scale
+            score = (torch.gather(base, 1, cand.long().clamp(min=0)) + sigma * q).float()
+            score = torch.where(cvalid, score, torch.full_like(score, -1e30))
+            _, keep_pos = topk_stable(score, max_keep)
+            keep_ok = torch.arange(max_keep, device="cuda").unsqueeze(0) < keep_n.unsqueeze(1)
+            cand = torch.where(keep_ok, torch.gather(cand, 1, keep_pos), torch.full_like(keep_pos, -1,
+                                                                                        dtype=torch.int32))
+        cvalid = cand >= 0
+        visits, q = child_stats(cand)
+        sigma = (cfg.c_visit + visits.max()) * cfg.c_scale
+        final = (torch.gather(base, 1, cand.long().clamp(min=0)) + sigma * q).float()
+        final = torch.where(cvalid, final, torch.full_like(final, -1e30))
+        pos = torch.argmax(final, dim=1)
+        chosen = torch.gather(cand, 1, pos.unsqueeze(1)).squeeze(1).clamp(min=0).to(torch.long)
+        return chosen, sims
 
     def apply_and_rebase(self, states, tree, ply: PlyResult):
         B = states.shape[0]

@@ -14,13 +14,15 @@ to the lowest slot, as in the GPU counterpart.
 
 Pinning (tests/test_oracle_orchestrator.py): policy_target against the
 closed form of its temperature search, _stable_topk's tie order,
-immediate_wins against the reference's win detector (golden probe vectors)
-and _surround against the C oracle's count.  The reference has no test of
-its orchestrator, so the rest -- the reserve / fill ranking of `candidates`
-and the sequential-halving composition of `run` -- is parity unpinned: it is
-checked only against the independent torch restatement and invariants
-(legal chosen slot, policy a distribution over legal slots, root visits =
-completed simulations).
+immediate_wins against the reference's win detector (golden probe vectors),
+_surround against the C oracle's count, `candidate_row` and `qualifying` on
+hand-built positions whose qualifying moves and candidate rows were worked
+out by hand (tests/orchestrator_cases.py), and `sequential_halving` on
+injected candidates, scores and Q whose survivors per round, per-round
+simulation counts, wave widths and final choices were worked out in float64
+and which each plausible misreading of the rule fails.  The composition in
+`run` (root analysis -> candidates -> halving -> policy target) is checked
+against the independent torch restatement on recorded GPU plies.
 """
 from __future__ import annotations
 
@@ -99,6 +101,60 @@ def policy_target(cfg, sampled, valid):
     return soft(final), final[:, 0]
 
 
+def candidate_row(qual, valid, priors, k, reserve):
+    """_root_candidate_slots (fnn_mcts_orchestrator.py:411-444) from the
+    qualifying mask: `reserve` columns of qualifying slots by prior (-1
+    padded), then k columns of the other legal slots by prior, cut to k."""
+    B = priors.shape[0]
+    rscore = np.where(qual, priors, np.float32(-1e30)).astype(np.float32)
+    per_game = np.minimum(qual.sum(axis=1), reserve)
+    rorder = _stable_topk(rscore, reserve)
+    rvalid = np.arange(reserve)[None, :] < per_game[:, None]
+    rcand = np.where(rvalid, rorder, -1).astype(np.int32)
+    chosen = np.zeros((B, MAX_LEGAL), bool)
+    for g in range(B):
+        chosen[g, rorder[g][rvalid[g]]] = True
+    fscore = np.where(valid & ~chosen, priors, np.float32(-1e30)).astype(np.float32)
+    forder = _stable_topk(fscore, k)
+    fkeep = np.maximum(k - per_game, 0)
+    fvalid = np.arange(k)[None, :] < fkeep[:, None]
+    fcand = np.where(fvalid, forder, -1).astype(np.int32)
+    return np.concatenate([rcand, fcand], axis=1)[:, :k]
+
+
+def sequential_halving(cfg, cand, base, run_round, child_stats):
+    """The four halving rounds and the final choice (fnn_mcts_orchestrator.py:650-731).
+    cand [B, C] int32 (-1 = none); base [B, 256] float32 Gumbel + legal logits;
+    run_round(cand, per_slot, W) runs the simulations of a round; child_stats(cand)
+    -> (visits, q) of the candidates' root children.  Returns the chosen slots."""
+    B = cand.shape[0]
+    rows = np.arange(B)
+    per_round = max(1, cfg.num_simulations // ROUNDS)
+    for r in range(ROUNDS):
+        cvalid = cand >= 0
+        C = cand.shape[1]
+        W = WAVES[min(r, len(WAVES) - 1)] if cfg.wave_parallel else 1
+        run_round(cand, max(1, per_round // C), W)
+        if C <= 1:
+            continue
+        keep_n = np.maximum(cvalid.sum(axis=1) // 2, 1)
+        max_keep = C // 2
+        visits, q = child_stats(cand)
+        sigma = np.float32((cfg.c_visit + visits.max()) * cfg.c_scale)
+        b = np.take_along_axis(base, np.maximum(cand, 0).astype(np.int64), axis=1)
+        score = np.where(cvalid, (b + sigma * q).astype(np.float32), np.float32(-1e30))
+        keep_pos = _stable_topk(score, max_keep)
+        ok = np.arange(max_keep)[None, :] < keep_n[:, None]
+        cand = np.where(ok, np.take_along_axis(cand, keep_pos, axis=1), -1).astype(np.int32)
+    cvalid = cand >= 0
+    visits, q = child_stats(cand)
+    sigma = np.float32((cfg.c_visit + visits.max()) * cfg.c_scale)
+    b = np.take_along_axis(base, np.maximum(cand, 0).astype(np.int64), axis=1)
+    final = np.where(cvalid, (b + sigma * q).astype(np.float32), np.float32(-1e30))
+    pos = np.argmax(final, axis=1)
+    return np.maximum(cand[rows, pos], 0).astype(np.int64)
+
+
 class SearchPlyOracle:
     def __init__(self, cfg, mcts: MctsOracle | None = None):
         self.cfg = cfg
@@ -139,20 +195,7 @@ class SearchPlyOracle:
         if reserve <= 0:
             raise NotImplementedError("reserve_slots <= 0 draws a second Gumbel sample")
         qual = self.qualifying(states, legal, n)
-        rscore = np.where(qual, priors, np.float32(-1e30)).astype(np.float32)
-        per_game = np.minimum(qual.sum(axis=1), reserve)
-        rorder = _stable_topk(rscore, reserve)
-        rvalid = np.arange(reserve)[None, :] < per_game[:, None]
-        rcand = np.where(rvalid, rorder, -1).astype(np.int32)
-        chosen = np.zeros((B, MAX_LEGAL), bool)
-        for g in range(B):
-            chosen[g, rorder[g][rvalid[g]]] = True
-        fscore = np.where(valid & ~chosen, priors, np.float32(-1e30)).astype(np.float32)
-        forder = _stable_topk(fscore, k)
-        fkeep = np.maximum(k - per_game, 0)
-        fvalid = np.arange(k)[None, :] < fkeep[:, None]
-        fcand = np.where(fvalid, forder, -1).astype(np.int32)
-        return np.concatenate([rcand, fcand], axis=1)[:, :k]
+        return candidate_row(qual, valid, priors, k, reserve)
 
     # ---- search --------------------------------------------------------
     def root_stats(self, t, slots):  # _gather_root_candidate_stats :1072-1096
@@ -222,13 +265,9 @@ class SearchPlyOracle:
             cand = cand_all.astype(np.int32)
             cvalid = np.take_along_axis(valid, np.maximum(cand, 0), axis=1) & (cand >= 0)
             cand = np.where(cvalid, cand, -1).astype(np.int32)
-            per_round = max(1, cfg.num_simulations // ROUNDS)
             active8 = search.astype(np.int8)
-            for r in range(ROUNDS):
-                cvalid = cand >= 0
-                C = cand.shape[1]
-                W = WAVES[min(r, len(WAVES) - 1)] if cfg.wave_parallel else 1
-                per_slot = max(1, per_round // C)
+
+            def run_round(cand, per_slot, W):
                 for w in range(math.ceil(per_slot / W)):
                     ww = min(W, per_slot - w * W)
                     leaf, paths, plen, vl, vlen = self.m.select_slots(
@@ -242,24 +281,10 @@ class SearchPlyOracle:
                     self.m.expand_backprop_dense(t, np.ascontiguousarray(q2, np.float32), leaf, leaves, lm, ln,
                                                  np.ascontiguousarray(p2, np.float32), res,
                                                  np.ascontiguousarray(v2, np.float32), vl, vlen)
-                if C <= 1:
-                    continue
-                keep_n = np.maximum(cvalid.sum(axis=1) // 2, 1)
-                max_keep = C // 2
-                visits, q = self.root_stats(t, cand)
-                sigma = np.float32((cfg.c_visit + visits.max()) * cfg.c_scale)
-                base = np.take_along_axis(gumbel + legal_logits, np.maximum(cand, 0).astype(np.int64), axis=1)
-                score = np.where(cvalid, (base + sigma * q).astype(np.float32), np.float32(-1e30))
-                keep_pos = _stable_topk(score, max_keep)
-                ok = np.arange(max_keep)[None, :] < keep_n[:, None]
-                cand = np.where(ok, np.take_along_axis(cand, keep_pos, axis=1), -1).astype(np.int32)
-            cvalid = cand >= 0
-            visits, q = self.root_stats(t, cand)
-            sigma = np.float32((cfg.c_visit + visits.max()) * cfg.c_scale)
-            base = np.take_along_axis(gumbel + legal_logits, np.maximum(cand, 0).astype(np.int64), axis=1)
-            final = np.where(cvalid, (base + sigma * q).astype(np.float32), np.float32(-1e30))
-            pos = np.argmax(final, axis=1)
-            chosen = np.maximum(cand[rows, pos], 0).astype(np.int64)
+                return per_slot * cand.shape[1] * B
+
+            chosen = sequential_halving(cfg, cand, (gumbel + legal_logits).astype(np.float32), run_round,
+                                        lambda c: self.root_stats(t, c))
             slot_visits, slot_q = self.root_stats(t, np.broadcast_to(slot, (B, MAX_LEGAL)))
             visited = (slot_visits > 0) & valid
             max_n = slot_visits.astype(np.float32).max(axis=1, keepdims=True)

@@ -303,3 +303,49 @@ def tree_equal(a, b):
         if not np.array_equal(x, y):
             bad.append(k)
     return bad
+
+
+# Completed-Q descent known answers (deterministic_completed_q_child,
+# mcts_tree.cuh:77-143).  Each case: the children of the forced root child
+# as (N, W, prior, child_init_q, virtual_q_penalty), the forced child's own
+# N, and the child the rule picks.  The choice was computed by hand in float64
+# (pi0 = softmax_c(log max(prior, 1e-20) + 4 q_c), q = -W/N, or child_init_q
+# when N = 0, minus the virtual-Q penalty; score = pi0 - N / (1 + sum N)):
+#   case 0 scores  0.049245  0.019896  0.082595  0.014931 -> child 2 (margin 0.033)
+#   case 1 scores  0.389749 -0.429166  0.150528           -> child 0
+#   case 2 scores -0.108718  0.348829 -0.115111           -> child 1
+# Each plausible misreading picks another child: +W/N (case 0 -> 0, case 1 -> 1,
+# case 2 -> 2); 0 or -child_init_q for unvisited children (case 0 -> 0);
+# no penalty or +penalty (case 0 -> 3, case 2 -> 0); no log prior (case 0 -> 3);
+# the parent's N in the denominator (case 0 -> 3); N / sum N (case 0 -> 0);
+# pi0 + N/(1 + sum N) (case 0 -> 3); sigma 1 instead of 4 (case 0 -> 0, case 1 -> 2).
+COMPLETED_Q_CASES = [
+    ([(0, 0.0, 0.4, -0.82, 0.0), (0, 0.0, 0.1, -0.7, 0.0), (2, -0.62, 0.1, 0.0, 0.25), (3, -2.36, 0.05, 0.0, 0.5)],
+     65, 2),
+    ([(4, -2.0, 0.3, 0.0, 0.0), (4, 2.0, 0.3, 0.0, 0.0), (0, 0.0, 0.4, 0.0, 0.0)], 8, 0),
+    ([(3, -1.5, 0.4, 0.0, 0.35), (3, -1.2, 0.4, 0.0, 0.0), (1, 0.5, 0.2, 0.0, 0.0)], 7, 1),
+]
+
+
+def completed_q_trees(M=16):
+    """One game per case: root 0 -> forced child 1 -> children 2.. (unexpanded).
+    Returns (tree, expected leaf node per game)."""
+    B = len(COMPLETED_Q_CASES)
+    t = new_tree(B, M)
+    want = []
+    for g, (kids, parent_n, pick) in enumerate(COMPLETED_Q_CASES):
+        t["first_child"][g, 0], t["num_children"][g, 0] = 1, 1
+        t["parent_idx"][g, 1] = 0
+        t["prior"][g, 1] = 1.0
+        t["visit_count"][g, 0] = t["visit_count"][g, 1] = parent_n
+        t["first_child"][g, 1], t["num_children"][g, 1] = 2, len(kids)
+        for i, (n, w, p, ciq, vq) in enumerate(kids):
+            u = 2 + i
+            t["visit_count"][g, u], t["total_value"][g, u], t["prior"][g, u] = n, w, p
+            t["child_init_q"][g, u], t["virtual_q_penalty"][g, u] = ciq, vq
+            t["parent_idx"][g, u] = 1
+            t["move_bytes"][g, u] = [2, 0, 0, 0, 0, 0]
+        t["move_bytes"][g, 1] = [2, 0, 0, 0, 0, 0]
+        t["node_count"][g] = 2 + len(kids)
+        want.append(2 + pick)
+    return t, np.array(want, np.int32)

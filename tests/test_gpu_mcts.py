@@ -158,3 +158,31 @@ def test_replay_fill_writes_idle_rows(roots):
     buf = torch.full((T, 3424), 0xAB, dtype=torch.uint8, device="cuda")
     ge.ext.mcts_replay_fill_batch(ge.c(roots), buf, ge.c(paths), ge.c(plen), ge.c(leaf), B, T)
     assert np.array_equal(buf.cpu().numpy(), want)
+
+
+@pytest.mark.parametrize("mode", ["slots", "mask"])
+def test_completed_q_descent_known_answers(mode):
+    """The deterministic_non_root descent on the GPU against hand-computed
+    float64 choices (tests/mcts_driver.py COMPLETED_Q_CASES, mcts_tree.cuh:77-143)."""
+    import torch
+    from mcts_driver import COMPLETED_Q_CASES, completed_q_trees
+    eng = GpuEngine()
+    t0, want = completed_q_trees()
+    t = {k: eng.c(v) for k, v in t0.items()}
+    B = want.shape[0]
+    active = torch.ones((B,), dtype=torch.int8, device="cuda")
+    if mode == "slots":
+        out = eng.ext.mcts_select_with_root_slots_batch(
+            *eng.args(t), t["child_init_q"], active, t["root_node"], torch.zeros((B, 1), dtype=torch.int32,
+                                                                               device="cuda"),
+            1, 256, 1.25, B, 1, eng.M(t), True, 4.0, 0.0)
+    else:
+        out = eng.ext.mcts_select_with_root_mask_batch(
+            *eng.args(t), t["child_init_q"], active, t["root_node"], torch.ones((B, 1), dtype=torch.int8,
+                                                                              device="cuda"),
+            1, 1.25, B, 1, eng.M(t), True, 4.0, 0.0)
+    leaf, paths, plen, vl, vlen = [o.cpu().numpy() for o in out]
+    assert np.array_equal(leaf, want)
+    vc = t["visit_count"].cpu().numpy()
+    assert np.array_equal(vc[np.arange(B), want], [c[0][w - 2][0] + 1 for c, w in zip(COMPLETED_Q_CASES, want)])
+    assert (plen == 2).all() and np.array_equal(vl[np.arange(B), vlen - 1], want)

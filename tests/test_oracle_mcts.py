@@ -213,3 +213,27 @@ def test_legal_mask_is_action_scatter(oracle, roots):
         a = act[g, :n[g]]
         want[a[a >= 0]] = 1.0
         assert np.array_equal(mask[g], want)
+
+
+@pytest.mark.parametrize("mode", ["slots", "mask"])
+def test_completed_q_descent_known_answers(oracle, mode):
+    """deterministic_non_root descent (mcts_tree.cuh:77-143) on hand-built
+    trees whose choice was computed by hand in float64 (tests/mcts_driver.py
+    COMPLETED_Q_CASES: each plausible misreading of the rule picks another child)."""
+    from mcts_driver import COMPLETED_Q_CASES, completed_q_trees
+    t, want = completed_q_trees()
+    B = want.shape[0]
+    m = MctsOracle(oracle)
+    if mode == "slots":
+        leaf, paths, plen, vl, vlen = m.select_slots(t, np.ones(B, np.int8), np.zeros(B, np.int32),
+                                                     np.zeros((B, 1), np.int32), 256, 1.25, 1, True, 4.0, 0.0)
+    else:
+        leaf, paths, plen, vl, vlen = m.select_mask(t, np.ones(B, np.int8), np.zeros(B, np.int32),
+                                                    np.ones((B, 1), np.int8), 1.25, 1, True, 4.0, 0.0)
+    assert np.array_equal(leaf, want)
+    # the chosen child takes N + 1; a forced root child (slots) takes no virtual
+    # loss in this mode (mcts_tree.cuh:879-885), one chosen by the mask does
+    assert (plen == 2).all() and np.array_equal(vl[np.arange(B), vlen - 1], want)
+    assert (vlen == (1 if mode == "slots" else 2)).all()
+    assert np.array_equal(t["visit_count"][np.arange(B), want], [c[0][w - 2][0] + 1 for c, w in
+                                                                 zip(COMPLETED_Q_CASES, want)])

@@ -99,3 +99,51 @@ def test_surround_counts_match_c_oracle(oracle):
         for s in st:
             for colour in (0, 1):
                 assert _surround(s, colour) == oracle.surround_count(s, colour)
+
+
+@pytest.mark.parametrize("name", ["k16-schedule", "k16-w1", "k64-schedule"])
+def test_sequential_halving_known_answers(name):
+    """oracle.orchestrator.sequential_halving against the hand-worked cases
+    of tests/orchestrator_cases.py: the rows of every round, per_slot, the
+    wave width and the final choice."""
+    from orchestrator_cases import HALVING_CASES, HalvingStub, halving_base
+    from oracle.orchestrator import sequential_halving
+    over, rows, calls, chosen = HALVING_CASES[name]
+    cand = np.array(rows, np.int32)
+    stub = HalvingStub()
+    got = sequential_halving(_cfg(**over), cand, halving_base(cand.shape[0]), stub.run_round, stub.child_stats)
+    assert stub.calls == calls
+    assert got.tolist() == chosen
+
+
+@pytest.mark.parametrize("case", [0, 1])
+def test_reserve_candidates_known_answers(oracle, case):
+    """The queen-surround reserve rule (fnn_mcts_orchestrator.py:339-444) on
+    hand-built positions: which moves qualify, with and without the
+    immobile-queen filter, and the candidate row they give with the
+    tests/orchestrator_cases.py priors."""
+    from orchestrator_cases import RESERVE_CASES, priors_formula
+    from oracle.orchestrator import SearchPlyOracle, candidate_row
+    build, n, want = RESERVE_CASES[case]
+    s = build()[None]
+    legal, nl = oracle.legal_moves(s[0])
+    assert nl == n
+    for immobile, (qual_slots, row) in want.items():
+        ref = SearchPlyOracle(_cfg(queen_surround_reserve_immobile_only=immobile))
+        qual = ref.qualifying(s, legal[None], np.array([n]))
+        assert np.nonzero(qual[0])[0].tolist() == qual_slots
+        valid = (np.arange(256) < n)[None]
+        assert candidate_row(qual, valid, priors_formula(n)[None], 16, 6)[0].tolist() == row
+
+
+def test_candidate_row_short_list():
+    """Fewer legal moves than fill columns: the fill continues with the
+    reserve slot (lowest slot first among the -1e30 entries), then illegal slots."""
+    from orchestrator_cases import CANDIDATE_SHORT as c
+    from oracle.orchestrator import candidate_row
+    priors = np.zeros((1, 256), np.float32)
+    priors[0, :c["n"]] = c["priors"]
+    qual = np.zeros((1, 256), bool)
+    qual[0, c["qual"]] = True
+    valid = (np.arange(256) < c["n"])[None]
+    assert candidate_row(qual, valid, priors, 16, 6)[0].tolist() == c["row"]
