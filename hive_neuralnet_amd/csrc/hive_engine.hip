@@ -306,7 +306,9 @@ extern "C" {
 
 int hg_abi_version(void) { return HG_ABI_VERSION; }
 
-int hg_initialize_tables(void) { return 0; }
+// The geometry is closed-form (no tables to upload); set-up looks up the current
+// device's scratch array of the no-allocation probe entry point.
+int hg_initialize_tables(void) { return hg_probe_scratch_init(); }
 
 int hg_create_initial_states(uint8_t* states, int64_t B, int expansion_mask, void* stream) {
     if (B <= 0) return 0;

@@ -23,6 +23,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <mutex>
+
 #include "../../include/hive_gpu.h"
 #include "hive_probe.hpp"
 
@@ -153,9 +155,43 @@ __global__ void k_probe_finish(const int32_t* __restrict__ num_legal, int64_t B,
     forced[r] = f;
 }
 
+// Scratch of the no-allocation entry point: the probe's two job counters, job
+// lists and failure flags for up to HG_PROBE_NOALLOC_MAX_ROOTS roots
+// (12.6 MB), one copy per GPU, held until the process ends.  Host code never
+// uses the symbol itself (on the host it names a stand-in, not device
+// memory): it uses the per-device address hipGetSymbolAddress returns.
+constexpr int64_t kScratchInts = 2 + 3 * (int64_t)HG_PROBE_NOALLOC_MAX_ROOTS * kMaxLegal;
+__device__ __align__(256) int32_t scratch[kScratchInts];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+int32_t* g_scratch[kMaxDevices] = {};
+
+// The current device's scratch address, looked up once per device.
+int scratch_of_current_device(int32_t** out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return (int)e;
+    if (dev < 0 || dev >= kMaxDevices) return (int)hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch[dev] == nullptr) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return (int)e;
+        g_scratch[dev] = static_cast<int32_t*>(p);
+    }
+    *out = g_scratch[dev];
+    return 0;
+}
+
 }  // namespace
 
 extern "C" {
+
+int hg_probe_scratch_init(void) {
+    int32_t* p = nullptr;
+    return scratch_of_current_device(&p);
+}
 
 int64_t hg_root_tactical_probe_workspace(int64_t B) { return B <= 0 ? 0 : 2 + 3 * B * kMaxLegal; }
 
@@ -185,6 +221,19 @@ int hg_root_tactical_probe(const uint8_t* states, const uint8_t* legal_moves, co
     hipLaunchKernelGGL(k_probe_finish, dim3((unsigned)((B + 255) / 256)), dim3(256), 0, s, num_legal, B, winning,
                        allowed, forced);
     return (int)hipGetLastError();
+}
+
+int hg_root_tactical_probe_noalloc(const uint8_t* states, const uint8_t* legal_moves, const int32_t* num_legal,
+                                   const float* priors, int64_t B, int enable_win_in_one,
+                                   int enable_check_opponent_wins, int enable_win_in_two, int64_t* winning,
+                                   uint8_t* allowed, uint8_t* forced, void* stream) {
+    if (B <= 0) return 0;
+    if (B > HG_PROBE_NOALLOC_MAX_ROOTS) return (int)hipErrorInvalidValue;
+    int32_t* ws = nullptr;
+    const int err = scratch_of_current_device(&ws);
+    if (err != 0) return err;
+    return hg_root_tactical_probe(states, legal_moves, num_legal, priors, B, enable_win_in_one,
+                                  enable_check_opponent_wins, enable_win_in_two, winning, allowed, forced, ws, stream);
 }
 
 }  // extern "C"

@@ -43,6 +43,7 @@ MOVEMENT_OFFSET = 2312
 DEFAULT_MAX_TREE_NODES = 65536
 MAX_TREE_DEPTH = 128
 FNN_FEAT_DIM = 122
+PROBE_NOALLOC_MAX_ROOTS = 4096  # include/hive_gpu.h HG_PROBE_NOALLOC_MAX_ROOTS
 MAX_ENC_NODES = 48
 MAX_ENC_EDGES = 200
 NODE_FEAT_DIM = 25
@@ -108,6 +109,9 @@ _SIGS = {
                                _c_void_p],
     "hg_root_tactical_probe": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_i64, _c_int, _c_int, _c_int, _c_void_p,
                                _c_void_p, _c_void_p, _c_void_p, _c_void_p],
+    "hg_probe_scratch_init": [],
+    "hg_root_tactical_probe_noalloc": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_i64, _c_int, _c_int, _c_int,
+                                       _c_void_p, _c_void_p, _c_void_p, _c_void_p],
 }
 _SIGS_I64 = {  # entry points returning a size (int64_t)
     "hg_root_tactical_probe_workspace": [_c_i64],
@@ -417,6 +421,37 @@ class HiveGpuExtension:
                                                 int(bool(enable_check_opponent_wins)), int(bool(enable_win_in_two)),
                                                 winning.data_ptr(), allowed.data_ptr(), forced.data_ptr(),
                                                 ws.data_ptr(), _stream()), "root_tactical_probe_batch")
+        return winning, allowed, forced
+
+    def root_tactical_probe_batch_noalloc(self, states, legal_moves, num_legal, priors, batch_size: int,
+                                          enable_win_in_one: bool = True, enable_check_opponent_wins: bool = True,
+                                          enable_win_in_two: bool = True, out=None):
+        """root_tactical_probe_batch without a device allocation in the call
+        (extension; hg_root_tactical_probe_noalloc): the job lists live in the
+        library's per-GPU scratch array, for at most PROBE_NOALLOC_MAX_ROOTS
+        roots.  `out` = (winning [B] int64, allowed [B, 256] uint8, forced [B]
+        uint8) buffers to write; when None they are allocated here.  Calls
+        that overlap on one GPU share the scratch and race."""
+        B = int(batch_size)
+        if B > PROBE_NOALLOC_MAX_ROOTS:
+            raise ValueError(f"root_tactical_probe_batch_noalloc: {B} roots, at most {PROBE_NOALLOC_MAX_ROOTS}")
+        if out is None:
+            out = (torch.empty((max(B, 0),), dtype=torch.int64, device="cuda"),
+                   torch.empty((max(B, 0), MAX_LEGAL_MOVES), dtype=torch.uint8, device="cuda"),
+                   torch.empty((max(B, 0),), dtype=torch.uint8, device="cuda"))
+        winning = _dev(out[0], "winning", torch.int64, (), B)
+        allowed = _dev(out[1], "allowed", torch.uint8, (MAX_LEGAL_MOVES,), B)
+        forced = _dev(out[2], "forced", torch.uint8, (), B)
+        if B <= 0:
+            return winning, allowed, forced
+        states = _state_rows(states, B)
+        legal_moves = _dev(legal_moves, "legal_moves", torch.uint8, (MAX_LEGAL_MOVES, SIZEOF_GPU_MOVE), B)
+        num_legal = _dev(num_legal, "num_legal", torch.int32, (), B)
+        priors = _dev(priors, "priors", torch.float32, (MAX_LEGAL_MOVES,), B)
+        _check(self._lib.hg_root_tactical_probe_noalloc(
+            states.data_ptr(), legal_moves.data_ptr(), num_legal.data_ptr(), priors.data_ptr(), B,
+            int(bool(enable_win_in_one)), int(bool(enable_check_opponent_wins)), int(bool(enable_win_in_two)),
+            winning.data_ptr(), allowed.data_ptr(), forced.data_ptr(), _stream()), "root_tactical_probe_batch_noalloc")
         return winning, allowed, forced
 
     def generate_legal_mask_batch(self, states: torch.Tensor, batch_size: int):

@@ -141,6 +141,23 @@ int hg_root_tactical_probe(const uint8_t* states, const uint8_t* legal_moves, co
                            int enable_win_in_two, int64_t* winning, uint8_t* allowed, uint8_t* forced,
                            int32_t* workspace, void* stream);
 
+/* hg_root_tactical_probe with no workspace argument and no allocation.  No
+ * counterpart in the reference: it is for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  The job lists live in a static device array of this
+ * library, one per GPU, sized for at most HG_PROBE_NOALLOC_MAX_ROOTS roots
+ * (12.6 MB); B above that returns hipErrorInvalidValue and launches nothing.
+ * Every call on one GPU shares that GPU's array: calls that overlap on one
+ * GPU (other streams, other threads) race and must be serialised by the
+ * caller.  Outputs as hg_root_tactical_probe.  hg_probe_scratch_init looks up
+ * the current device's array once (the first call on a device does it too). */
+#define HG_PROBE_NOALLOC_MAX_ROOTS 4096
+int hg_probe_scratch_init(void);
+int hg_root_tactical_probe_noalloc(const uint8_t* states, const uint8_t* legal_moves, const int32_t* num_legal,
+                                   const float* priors, int64_t B, int enable_win_in_one,
+                                   int enable_check_opponent_wins, int enable_win_in_two, int64_t* winning,
+                                   uint8_t* allowed, uint8_t* forced, void* stream);
+
 /* generate_legal_mask_batch / generate_legal_moves_and_mask_batch --
  * game_logic.cu:737-806 (legal_mask_kernel, state_encoder.cuh:908-976).
  * masks[B][85834] f32 (written whole): 1.0 at the action index of every
