@@ -577,14 +577,204 @@ HW_INL void words_centroid(uint32_t w, int lane, int& cq, int& cr) {
     cr = sn ? round_half_even_div(sr, sn) : 0;
 }
 
-// mcts_expand_and_backprop_dense_priors_kernel (mcts_tree.cuh:1068-1187).
-// One wave per game, simulations in order.  A simulation's loads come in
-// three dependent batches: its inputs (leaf, result, legal count, path, value, the
-// leaf's bitboards, legal list, priors and child values), then the tree
-// state they index (the leaf's children and terminal fields, the path nodes'
-// statistics, the root above the path), then the root's statistics.
-// Expansion and backup are stores; one fence per simulation makes them
-// visible to the next.
+// One simulation of mcts_expand_and_backprop_dense_priors_kernel
+// (mcts_tree.cuh:1068-1187), run by the whole wave.  A simulation's loads come
+// in three dependent batches: its inputs (leaf, result, legal count, path,
+// value, the leaf's bitboards, legal list, priors and child values), then the
+// tree state they index (the leaf's children and terminal fields, the path
+// nodes' statistics, the root above the path), then the root's statistics.
+// Expansion and backup are stores; the caller's fence between simulations
+// makes them visible to the next.
+//
+// kPlanned = false: the game's simulations in order on one wave; `cnt` is the
+//   game's running node counter and the backup walks up to the root.
+// kPlanned = true: one root child's simulations (k_eb_apply): the expansion
+//   decision and node base come from k_eb_plan (`planned` >= 0: expand at that
+//   node id), the node counter and the root belong to the plan, so the walk
+//   above the path stops below the root; only selection paths get here.
+template <bool kPlanned>
+HW_INL void eb_sim(const Tree& T, const LeafIn& L, const float* __restrict__ nn_values,
+                   const int32_t* __restrict__ vl_paths, const int32_t* __restrict__ vl_lens, float q_penalty,
+                   int64_t g, int64_t sim, int lane, int& cnt, int planned) {
+    const int64_t g0 = g * T.M;
+    const int leaf = L.leaf[sim];
+    // first loads: the simulation's inputs (this kernel never writes them)
+    const int res = L.results[sim];
+    const int nl = L.nlegal[sim];
+    int n = vl_lens[sim];
+    n = n < 0 ? 0 : (n > kDepth ? kDepth : n);
+    const float nn = nn_values[sim];
+    const int32_t* vp = vl_paths + sim * kDepth;
+    const int p0 = vp[lane], p1 = vp[64 + lane];  // a path row holds kDepth = 128 entries
+    const uint8_t* S = L.states + sim * kStateBytes;
+    const int turn = S[OFF_TURN] | (S[OFF_TURN + 1] << 8);
+    const uint32_t occw = lane < 18 ? reinterpret_cast<const uint32_t*>(S + OFF_OCC)[lane] : 0u;
+    const uint8_t* mv = L.legal + sim * (kMaxLegal * 6);
+    const float* pri = L.priors + sim * kMaxLegal;
+    const float* cqv = L.childq + sim * kMaxLegal;
+    uint16_t x0[4], x1[4], x2[4];
+    float xp[4], xq[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int m = lane + 64 * j;
+        x0[j] = x1[j] = x2[j] = 0;
+        xp[j] = xq[j] = 0.0f;
+        if (m < nl) {
+            const uint16_t* x = reinterpret_cast<const uint16_t*>(mv + 6 * m);
+            x0[j] = x[0];
+            x1[j] = x[1];
+            x2[j] = x[2];
+            xp[j] = pri[m];
+            xq[j] = cqv[m];
+        }
+    }
+    // second loads: the tree state they index
+    const int64_t li = g0 + leaf;
+    const int fc = T.fc[li];
+    const int lit = T.it[li];
+    const float ltv = T.tval[li];
+    const int last = n > 0 ? __shfl(n - 1 < 64 ? p0 : p1, (n - 1) & 63, 64) : leaf;
+    // The selection entered vp[0..n) below the root, each node a child of
+    // the one before, so the backup chain leaf -> root is that path
+    // reversed, then the root; the expansion below writes none of them.
+    const bool chain = last == leaf;
+    int vc0 = 0, vc1 = 0;
+    float tv0 = 0.0f, tv1 = 0.0f, vq0 = 0.0f, vq1 = 0.0f;
+    if (chain) {
+        if (lane < n) {
+            const int64_t ni = g0 + p0;
+            tv0 = T.tv[ni];
+            vc0 = T.vc[ni];
+            vq0 = T.vq[ni];
+        }
+        if (lane + 64 < n) {
+            const int64_t ni = g0 + p1;
+            tv1 = T.tv[ni];
+            vc1 = T.vc[ni];
+            vq1 = T.vq[ni];
+        }
+    }
+    const int top = (chain && n > 0) ? T.pa[g0 + __shfl(p0, 0, 64)] : leaf;  // the node above the path
+    // expansion (mcts_expand_dense_priors_kernel :971-1062 body)
+    int e = 0;
+    float rv = 0.0f;
+    const bool grow = kPlanned ? (res == 0 && planned >= 0)
+                               : (res == 0 && fc == -1 && nl > 0 && (int64_t)cnt + nl <= T.M);
+    const int base = kPlanned ? planned : cnt;
+    if (res != 0) {
+        rv = result_value(res, turn);
+        if (lane == 0) {
+            T.it[li] = 1;
+            T.tval[li] = rv;
+        }
+    } else if (grow) {
+        int cq, cr;
+        words_centroid(occw, lane, cq, cr);
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int m = lane + 64 * j;
+            if (m >= nl) break;
+            const int64_t ci = g0 + base + m;
+            T.vc[ci] = 0;
+            T.tv[ci] = 0.0f;
+            T.pr[ci] = xp[j];
+            T.pa[ci] = leaf;
+            T.ai[ci] = move_action(x0[j] & 0xFF, x0[j] >> 8, x1[j], x2[j], cq, cr);
+            T.fc[ci] = -1;
+            T.nc[ci] = 0;
+            T.it[ci] = 0;
+            T.tval[ci] = 0.0f;
+            T.ciq[ci] = xq[j];
+            uint16_t* d = reinterpret_cast<uint16_t*>(T.mb + ci * 6);
+            d[0] = x0[j];
+            d[1] = x1[j];
+            d[2] = x2[j];
+        }
+        for (int m = lane + 256; m < nl; m += 64) {  // lists beyond 256 entries (never produced here)
+            const uint8_t* x = mv + 6 * m;
+            const int64_t ci = g0 + base + m;
+            T.vc[ci] = 0;
+            T.tv[ci] = 0.0f;
+            T.pr[ci] = pri[m];
+            T.pa[ci] = leaf;
+            T.ai[ci] = move_action(x[0], x[1], x[2] | (x[3] << 8), x[4] | (x[5] << 8), cq, cr);
+            T.fc[ci] = -1;
+            T.nc[ci] = 0;
+            T.it[ci] = 0;
+            T.tval[ci] = 0.0f;
+            T.ciq[ci] = cqv[m];
+            uint8_t* d = T.mb + ci * 6;
+            for (int b = 0; b < 6; b++) d[b] = x[b];
+        }
+        if (lane == 0) {
+            if (!kPlanned) T.cnt[g] = base + nl;
+            T.nc[li] = nl;
+            T.fc[li] = base;
+        }
+        if (!kPlanned) cnt += nl;
+        e = 1;
+    }
+    const float v = res != 0 ? rv : (lit ? ltv : (e ? nn : 0.0f));
+    if (chain) {  // each path node: virtual-loss undo, then the value; lanes side by side
+        if (lane < n) {
+            const int64_t ni = g0 + p0;
+            const float sv = ((n - 1 - lane) & 1) ? -v : v;
+            if (q_penalty > 0.0f) {
+                T.vq[ni] = vq0 + -q_penalty;
+                T.vc[ni] = vc0 + 1;
+                T.tv[ni] = tv0 + sv;
+            } else {  // visits -1 then +1; value +1.0 then the backed-up value
+                T.tv[ni] = (tv0 + 1.0f) + sv;
+            }
+        }
+        if (lane + 64 < n) {
+            const int64_t ni = g0 + p1;
+            const float sv = ((n - 1 - (lane + 64)) & 1) ? -v : v;
+            if (q_penalty > 0.0f) {
+                T.vq[ni] = vq1 + -q_penalty;
+                T.vc[ni] = vc1 + 1;
+                T.tv[ni] = tv1 + sv;
+            } else {
+                T.tv[ni] = (tv1 + 1.0f) + sv;
+            }
+        }
+        if (lane == 0) {  // third loads: the nodes above the path (below the root when planned)
+            int node = top;
+            float w = (n & 1) ? -v : v;
+            for (int s2 = n; s2 < kDepth + 1 && node >= 0; s2++) {
+                const int64_t ni = g0 + node;
+                const int up = T.pa[ni];
+                if (kPlanned && up < 0) break;  // the root: k_eb_plan's
+                T.vc[ni] += 1;
+                T.tv[ni] += w;
+                w = -w;
+                node = up;
+            }
+        }
+    } else if (!kPlanned && lane == 0) {  // not a selection path: the reference's serial walk
+        for (int k = 0; k < n; k++) {
+            const int64_t ni = g0 + vp[k];
+            if (q_penalty > 0.0f) {
+                T.vq[ni] += -q_penalty;
+            } else {
+                T.vc[ni] -= 1;
+                T.tv[ni] += 1.0f;
+            }
+        }
+        float w = v;
+        int node = leaf;
+        for (int s2 = 0; s2 < kDepth + 1 && node >= 0; s2++) {
+            const int64_t ni = g0 + node;
+            T.vc[ni] += 1;
+            T.tv[ni] += w;
+            w = -w;
+            node = T.pa[ni];
+        }
+    }
+}
+
+// mcts_expand_and_backprop_dense_priors_kernel (mcts_tree.cuh:1068-1187):
+// one wave per game, the game's simulations in order.
 __global__ __launch_bounds__(64) void k_expand_backprop(Tree T, LeafIn L, const float* __restrict__ nn_values,
                                                         const int32_t* __restrict__ vl_paths,
                                                         const int32_t* __restrict__ vl_lens, float q_penalty,
@@ -592,180 +782,178 @@ __global__ __launch_bounds__(64) void k_expand_backprop(Tree T, LeafIn L, const 
     const int64_t g = blockIdx.x;
     const int lane = threadIdx.x;
     if (g >= B) return;
-    const int64_t g0 = g * T.M;
     int cnt = T.cnt[g];  // the game's node counter: only this wave changes it during the kernel
     for (int64_t sim = g; sim < total; sim += B) {
-        const int leaf = L.leaf[sim];
-        if (leaf < 0) continue;
-        // first loads: the simulation's inputs (this kernel never writes them)
-        const int res = L.results[sim];
-        const int nl = L.nlegal[sim];
-        int n = vl_lens[sim];
-        n = n < 0 ? 0 : (n > kDepth ? kDepth : n);
-        const float nn = nn_values[sim];
-        const int32_t* vp = vl_paths + sim * kDepth;
-        const int p0 = vp[lane], p1 = vp[64 + lane];  // a path row holds kDepth = 128 entries
-        const uint8_t* S = L.states + sim * kStateBytes;
-        const int turn = S[OFF_TURN] | (S[OFF_TURN + 1] << 8);
-        const uint32_t occw = lane < 18 ? reinterpret_cast<const uint32_t*>(S + OFF_OCC)[lane] : 0u;
-        const uint8_t* mv = L.legal + sim * (kMaxLegal * 6);
-        const float* pri = L.priors + sim * kMaxLegal;
-        const float* cqv = L.childq + sim * kMaxLegal;
-        uint16_t x0[4], x1[4], x2[4];
-        float xp[4], xq[4];
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int m = lane + 64 * j;
-            x0[j] = x1[j] = x2[j] = 0;
-            xp[j] = xq[j] = 0.0f;
-            if (m < nl) {
-                const uint16_t* x = reinterpret_cast<const uint16_t*>(mv + 6 * m);
-                x0[j] = x[0];
-                x1[j] = x[1];
-                x2[j] = x[2];
-                xp[j] = pri[m];
-                xq[j] = cqv[m];
-            }
-        }
-        // second loads: the tree state they index
-        const int64_t li = g0 + leaf;
-        const int fc = T.fc[li];
-        const int lit = T.it[li];
-        const float ltv = T.tval[li];
-        const int last = n > 0 ? __shfl(n - 1 < 64 ? p0 : p1, (n - 1) & 63, 64) : leaf;
-        // The selection entered vp[0..n) below the root, each node a child of
-        // the one before, so the backup chain leaf -> root is that path
-        // reversed, then the root; the expansion below writes none of them.
-        const bool chain = last == leaf;
-        int vc0 = 0, vc1 = 0;
-        float tv0 = 0.0f, tv1 = 0.0f, vq0 = 0.0f, vq1 = 0.0f;
-        if (chain) {
-            if (lane < n) {
-                const int64_t ni = g0 + p0;
-                tv0 = T.tv[ni];
-                vc0 = T.vc[ni];
-                vq0 = T.vq[ni];
-            }
-            if (lane + 64 < n) {
-                const int64_t ni = g0 + p1;
-                tv1 = T.tv[ni];
-                vc1 = T.vc[ni];
-                vq1 = T.vq[ni];
-            }
-        }
-        const int top = (chain && n > 0) ? T.pa[g0 + __shfl(p0, 0, 64)] : leaf;  // the root above the path
-        // expansion (mcts_expand_dense_priors_kernel :971-1062 body)
-        int e = 0;
-        float rv = 0.0f;
-        if (res != 0) {
-            rv = result_value(res, turn);
-            if (lane == 0) {
-                T.it[li] = 1;
-                T.tval[li] = rv;
-            }
-        } else if (fc == -1 && nl > 0 && (int64_t)cnt + nl <= T.M) {
-            int cq, cr;
-            words_centroid(occw, lane, cq, cr);
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const int m = lane + 64 * j;
-                if (m >= nl) break;
-                const int64_t ci = g0 + cnt + m;
-                T.vc[ci] = 0;
-                T.tv[ci] = 0.0f;
-                T.pr[ci] = xp[j];
-                T.pa[ci] = leaf;
-                T.ai[ci] = move_action(x0[j] & 0xFF, x0[j] >> 8, x1[j], x2[j], cq, cr);
-                T.fc[ci] = -1;
-                T.nc[ci] = 0;
-                T.it[ci] = 0;
-                T.tval[ci] = 0.0f;
-                T.ciq[ci] = xq[j];
-                uint16_t* d = reinterpret_cast<uint16_t*>(T.mb + ci * 6);
-                d[0] = x0[j];
-                d[1] = x1[j];
-                d[2] = x2[j];
-            }
-            for (int m = lane + 256; m < nl; m += 64) {  // lists beyond 256 entries (never produced here)
-                const uint8_t* x = mv + 6 * m;
-                const int64_t ci = g0 + cnt + m;
-                T.vc[ci] = 0;
-                T.tv[ci] = 0.0f;
-                T.pr[ci] = pri[m];
-                T.pa[ci] = leaf;
-                T.ai[ci] = move_action(x[0], x[1], x[2] | (x[3] << 8), x[4] | (x[5] << 8), cq, cr);
-                T.fc[ci] = -1;
-                T.nc[ci] = 0;
-                T.it[ci] = 0;
-                T.tval[ci] = 0.0f;
-                T.ciq[ci] = cqv[m];
-                uint8_t* d = T.mb + ci * 6;
-                for (int b = 0; b < 6; b++) d[b] = x[b];
-            }
-            if (lane == 0) {
-                T.cnt[g] = cnt + nl;
-                T.nc[li] = nl;
-                T.fc[li] = cnt;
-            }
-            cnt += nl;
-            e = 1;
-        }
-        const float v = res != 0 ? rv : (lit ? ltv : (e ? nn : 0.0f));
-        if (chain) {  // each path node: virtual-loss undo, then the value; lanes side by side
-            if (lane < n) {
-                const int64_t ni = g0 + p0;
-                const float sv = ((n - 1 - lane) & 1) ? -v : v;
-                if (q_penalty > 0.0f) {
-                    T.vq[ni] = vq0 + -q_penalty;
-                    T.vc[ni] = vc0 + 1;
-                    T.tv[ni] = tv0 + sv;
-                } else {  // visits -1 then +1; value +1.0 then the backed-up value
-                    T.tv[ni] = (tv0 + 1.0f) + sv;
-                }
-            }
-            if (lane + 64 < n) {
-                const int64_t ni = g0 + p1;
-                const float sv = ((n - 1 - (lane + 64)) & 1) ? -v : v;
-                if (q_penalty > 0.0f) {
-                    T.vq[ni] = vq1 + -q_penalty;
-                    T.vc[ni] = vc1 + 1;
-                    T.tv[ni] = tv1 + sv;
-                } else {
-                    T.tv[ni] = (tv1 + 1.0f) + sv;
-                }
-            }
-            if (lane == 0) {  // third loads: the root, and any node above it
-                int node = top;
-                float w = (n & 1) ? -v : v;
-                for (int s2 = n; s2 < kDepth + 1 && node >= 0; s2++) {
-                    const int64_t ni = g0 + node;
-                    T.vc[ni] += 1;
-                    T.tv[ni] += w;
-                    w = -w;
-                    node = T.pa[ni];
-                }
-            }
-        } else if (lane == 0) {  // not a selection path: the reference's serial walk
-            for (int k = 0; k < n; k++) {
-                const int64_t ni = g0 + vp[k];
-                if (q_penalty > 0.0f) {
-                    T.vq[ni] += -q_penalty;
-                } else {
-                    T.vc[ni] -= 1;
-                    T.tv[ni] += 1.0f;
-                }
-            }
-            float w = v;
-            int node = leaf;
-            for (int s2 = 0; s2 < kDepth + 1 && node >= 0; s2++) {
-                const int64_t ni = g0 + node;
-                T.vc[ni] += 1;
-                T.tv[ni] += w;
-                w = -w;
-                node = T.pa[ni];
-            }
-        }
+        if (L.leaf[sim] < 0) continue;
+        eb_sim<false>(T, L, nn_values, vl_paths, vl_lens, q_penalty, g, sim, lane, cnt, -1);
         __syncthreads();  // the next simulation reads this one's stores
+    }
+}
+
+// The same kernel over root children.  Below the root, a simulation touches
+// only the subtree of the root child it entered: its path, its leaf and the
+// leaf's new children.  So the simulations of different root children are
+// independent except for two things k_eb_plan settles first, in simulation
+// order: node ids (an exclusive prefix sum of the expansion sizes) and the
+// root's statistics.  Then k_eb_apply runs one wave per (game, root child),
+// that child's simulations in order, with the same float operations in the
+// same order per node as the one-wave kernel.  Games where this does not
+// hold -- the node pool could run short, a path that is not a selection path,
+// a leaf at the root -- are flagged, and the first k_eb_apply wave of such a
+// game runs all its simulations in order instead.
+struct EbWork {
+    int32_t* base;        // [total] node id of the simulation's first new child, -1 = none
+    int32_t* group;       // [total] root-child group of the simulation, -1 = idle
+    int32_t* ngroups;     // [B]
+    int32_t* sequential;  // [B] 1 = the game runs in the one-wave order
+};
+constexpr int kPlanMax = 64;  // simulations per game one planning wave takes (one per lane)
+
+__global__ __launch_bounds__(64) void k_eb_plan(Tree T, LeafIn L, const float* __restrict__ nn_values,
+                                                const int32_t* __restrict__ vl_paths,
+                                                const int32_t* __restrict__ vl_lens, int64_t B, int64_t total,
+                                                EbWork Wk) {
+    const int64_t g = blockIdx.x;
+    const int lane = threadIdx.x;
+    if (g >= B) return;
+    const int K = (int)(total / B);  // the host launches this only for total = K * B, K <= kPlanMax
+    const int64_t g0 = g * T.M;
+    const int64_t sim = (int64_t)lane * B + g;
+    const int cnt0 = T.cnt[g];
+    int leaf = -1;
+    if (lane < K) leaf = L.leaf[sim];
+    const bool live = leaf >= 0;
+    int res = 0, nl = 0, n = 0, fc0 = -1, lit = 0, turn = 0, top = -1, x = -1, head = -1;
+    float ltv = 0.0f, nn = 0.0f;
+    if (live) {  // loads in three dependent rounds: the simulation's inputs, then the path's ends, then above
+        const int32_t* vp = vl_paths + sim * kDepth;
+        const int v0 = vp[0];
+        res = L.results[sim];
+        nl = L.nlegal[sim];
+        n = vl_lens[sim];
+        nn = nn_values[sim];
+        const uint8_t* S = L.states + sim * kStateBytes;
+        turn = S[OFF_TURN] | (S[OFF_TURN + 1] << 8);
+        fc0 = T.fc[g0 + leaf];
+        lit = T.it[g0 + leaf];
+        ltv = T.tval[g0 + leaf];
+        n = n < 0 ? 0 : (n > kDepth ? kDepth : n);
+        head = n > 0 ? v0 : leaf;
+        x = n > 0 ? vp[n - 1] : leaf;  // must be the leaf: a selection path
+        top = n > 0 ? T.pa[g0 + head] : leaf;
+    }
+    bool bad = live && x != leaf;
+    // the walk above the path: top, its parent, ... up to the root (parent -1)
+    int root = -1, steps = 0, key = head;
+    if (live && !bad) {
+        int node = top, below = head, up = top >= 0 ? T.pa[g0 + top] : -1;
+        while (node >= 0 && up >= 0 && steps < kDepth + 1) {
+            below = node;
+            node = up;
+            up = T.pa[g0 + node];
+            steps++;
+        }
+        root = node;
+        key = below;  // the root child the simulation went through
+        if (node < 0 || up >= 0 || key == root) bad = true;  // no root within reach, or the leaf is the root
+    }
+    // expansion sizes: the first simulation reaching an unexpanded leaf expands it
+    bool first = live;
+    for (int k = 0; k < K; k++) {  // k is wave-uniform: lane values by readlane (no LDS round trip)
+        const int lk = __builtin_amdgcn_readlane(leaf, k);
+        if (k < lane && lk == leaf) first = false;
+    }
+    const int sz = (live && res == 0 && fc0 == -1 && nl > 0 && first) ? nl : 0;
+    const int pre = wave_excl_scan(sz, lane);
+    const int tot = wave_sum(sz);
+    const bool seq = __ballot(bad) != 0ull || (int64_t)cnt0 + tot > T.M;
+    // root-child groups in order of first appearance
+    int firstk = lane;
+    const uint64_t livem = __ballot(live);
+    for (int k = K - 1; k >= 0; k--) {
+        const int kk = __builtin_amdgcn_readlane(key, k);
+        if (k < lane && ((livem >> k) & 1ull) && kk == key) firstk = k;
+    }
+    const bool opens = live && firstk == lane;
+    const uint64_t om = __ballot(opens);
+    const int gid_own = __popcll(om & ((1ull << lane) - 1ull));
+    const int gid = __shfl(gid_own, firstk, 64);
+    if (lane < K) {
+        Wk.base[sim] = (!seq && sz > 0) ? cnt0 + pre : -1;
+        Wk.group[sim] = (!seq && live) ? gid : -1;
+    }
+    if (lane == 0) {
+        Wk.ngroups[g] = seq ? 0 : __popcll(om);
+        Wk.sequential[g] = seq ? 1 : 0;
+        if (!seq) T.cnt[g] = cnt0 + tot;
+    }
+    if (seq) return;
+    // the root's statistics, in simulation order: +1 visit and the value with the
+    // sign it has at the root (alternating per level from the leaf)
+    const float v = res != 0 ? result_value(res, turn) : (lit ? ltv : (sz > 0 ? nn : 0.0f));
+    const float wtop = (n & 1) ? -v : v;
+    const float wroot = (steps & 1) ? -wtop : wtop;
+    const bool hits = live && n + steps < kDepth + 1;  // the walk's bound (as k_expand_backprop)
+    // (the loop runs on the whole wave, so the shuffles read active lanes; lane 0
+    // holds the accumulators and does the memory accesses)
+    int cur = -1, vcn = 0;
+    float tvn = 0.0f;
+    const uint64_t hitm = __ballot(hits);
+    for (int k = 0; k < K; k++) {
+        if (!((hitm >> k) & 1ull)) continue;
+        const int r = __builtin_amdgcn_readlane(root, k);
+        const float w = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wroot), k));
+        if (r != cur) {
+            if (cur >= 0 && lane == 0) {
+                T.vc[g0 + cur] = vcn;
+                T.tv[g0 + cur] = tvn;
+            }
+            cur = r;
+            if (lane == 0) {
+                vcn = T.vc[g0 + r];
+                tvn = T.tv[g0 + r];
+            }
+        }
+        vcn += 1;
+        tvn += w;
+    }
+    if (cur >= 0 && lane == 0) {
+        T.vc[g0 + cur] = vcn;
+        T.tv[g0 + cur] = tvn;
+    }
+}
+
+// One wave per (game, root-child group): blockIdx.x = g + B * j.
+__global__ __launch_bounds__(64) void k_eb_apply(Tree T, LeafIn L, const float* __restrict__ nn_values,
+                                                 const int32_t* __restrict__ vl_paths,
+                                                 const int32_t* __restrict__ vl_lens, float q_penalty, int64_t B,
+                                                 int64_t total, EbWork Wk) {
+    const int64_t g = blockIdx.x % B;
+    const int j = (int)(blockIdx.x / B);
+    const int lane = threadIdx.x;
+    if (Wk.sequential[g]) {  // a game the plan left to the one-wave order: its first wave runs it
+        if (j != 0) return;
+        int cnt = T.cnt[g];
+        for (int64_t sim = g; sim < total; sim += B) {
+            if (L.leaf[sim] < 0) continue;
+            eb_sim<false>(T, L, nn_values, vl_paths, vl_lens, q_penalty, g, sim, lane, cnt, -1);
+            __syncthreads();
+        }
+        return;
+    }
+    if (j >= Wk.ngroups[g]) return;
+    const int K = (int)(total / B);
+    const int64_t mine = lane < K ? (int64_t)lane * B + g : 0;
+    const uint64_t todo = __ballot(lane < K && Wk.group[mine] == j);
+    const int plan = lane < K ? Wk.base[mine] : -1;
+    uint64_t m = todo;
+    int unused = 0;
+    while (m) {
+        const int k = __ffsll((unsigned long long)m) - 1;
+        m &= m - 1;
+        eb_sim<true>(T, L, nn_values, vl_paths, vl_lens, q_penalty, g, (int64_t)k * B + g, lane, unused,
+                     __shfl(plan, k, 64));
+        __syncthreads();  // the next simulation of this root child reads this one's stores
     }
 }
 
@@ -1188,6 +1376,33 @@ int hg_mcts_expand_backprop_dense(const hg_tree* tree, const float* child_q_valu
     LeafIn L{leaf_idx, leaf_states, legal_moves, num_legal, priors_per_legal, child_q_values, results};
     hipLaunchKernelGGL(k_expand_backprop, dim3((unsigned)B), dim3(64), 0, (hipStream_t)stream, to_tree(tree), L,
                        nn_values, vl_paths, vl_lens, q_penalty, B, total);
+    return finish();
+}
+
+int64_t hg_mcts_expand_backprop_dense_workspace(int64_t B, int64_t total) {
+    return B <= 0 || total <= 0 ? 0 : 4 * (2 * total + 2 * B);
+}
+
+int hg_mcts_expand_backprop_dense_ws(const hg_tree* tree, const float* child_q_values, const int32_t* leaf_idx,
+                                     const uint8_t* leaf_states, const uint8_t* legal_moves,
+                                     const int32_t* num_legal, const float* priors_per_legal, const int32_t* results,
+                                     const float* nn_values, const int32_t* vl_paths, const int32_t* vl_lens,
+                                     float q_penalty, int64_t B, int64_t total, void* workspace, void* stream) {
+    if (B <= 0 || total <= 0) return 0;
+    const int64_t K = total / B;
+    if (total % B != 0 || K > kPlanMax || B * K > (int64_t)INT32_MAX)  // outside the planner's shape
+        return hg_mcts_expand_backprop_dense(tree, child_q_values, leaf_idx, leaf_states, legal_moves, num_legal,
+                                             priors_per_legal, results, nn_values, vl_paths, vl_lens, q_penalty, B,
+                                             total, stream);
+    LeafIn L{leaf_idx, leaf_states, legal_moves, num_legal, priors_per_legal, child_q_values, results};
+    int32_t* w = static_cast<int32_t*>(workspace);
+    EbWork Wk{w, w + total, w + 2 * total, w + 2 * total + B};
+    hipStream_t s = (hipStream_t)stream;
+    const Tree T = to_tree(tree);
+    hipLaunchKernelGGL(k_eb_plan, dim3((unsigned)B), dim3(64), 0, s, T, L, nn_values, vl_paths, vl_lens, B, total,
+                       Wk);
+    hipLaunchKernelGGL(k_eb_apply, dim3((unsigned)(B * K)), dim3(64), 0, s, T, L, nn_values, vl_paths, vl_lens,
+                       q_penalty, B, total, Wk);
     return finish();
 }
 

@@ -88,6 +88,9 @@ _SIGS = {
     "hg_mcts_expand_backprop_dense": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                                       _c_void_p, _c_void_p, _c_void_p, _c_void_p, ctypes.c_float, _c_i64, _c_i64,
                                       _c_void_p],
+    "hg_mcts_expand_backprop_dense_ws": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+                                         _c_void_p, _c_void_p, _c_void_p, _c_void_p, ctypes.c_float, _c_i64, _c_i64,
+                                         _c_void_p, _c_void_p],
     "hg_mcts_root_noise": [_c_void_p, _c_void_p, _c_void_p, _c_int, ctypes.c_float, ctypes.c_float, _c_i64,
                            _c_void_p],
     "hg_mcts_reset_trees": [_c_void_p, _c_void_p, _c_void_p, _c_i64, _c_void_p],
@@ -117,6 +120,7 @@ _SIGS_I64 = {  # entry points returning a size (int64_t)
     "hg_root_tactical_probe_workspace": [_c_i64],
     "hg_successor_rows_workspace": [_c_i64],
     "hg_fnn_leaf_eval_lists_workspace": [_c_i64, _c_int],
+    "hg_mcts_expand_backprop_dense_workspace": [_c_i64, _c_i64],
 }
 
 
@@ -633,9 +637,12 @@ def _mcts_methods():
         _dev(nn_values, "nn_values", torch.float32, (), total)
         _dev(vl_paths, "vl_paths", torch.int32, (MAX_TREE_DEPTH,), total)
         _dev(vl_lengths, "vl_lengths", torch.int32, (), total)
-        _check(self._lib.hg_mcts_expand_backprop_dense(
+        # the root children's simulations in parallel (hg_mcts_expand_backprop_dense_ws): same tree
+        ws = torch.empty((max(1, int(self._lib.hg_mcts_expand_backprop_dense_workspace(B, total))) // 4,),
+                         dtype=torch.int32, device="cuda")
+        _check(self._lib.hg_mcts_expand_backprop_dense_ws(
             ctypes.byref(tree), *args, nn_values.data_ptr(), vl_paths.data_ptr(), vl_lengths.data_ptr(),
-            float(q_penalty), B, total, _stream()), "mcts_expand_and_backprop_dense_priors_batch")
+            float(q_penalty), B, total, ws.data_ptr(), _stream()), "mcts_expand_and_backprop_dense_priors_batch")
 
     # ---- legacy action-space engine (bindings.cpp:378-389; twelve tree tensors, no child_init_q,
     # which these kernels never touch: any [B, M] f32 array fills its slot) ----

@@ -333,6 +333,20 @@ int hg_mcts_expand_backprop_dense(const hg_tree* tree, const float* child_q_valu
                                   const int32_t* vl_paths, const int32_t* vl_lens, float q_penalty, int64_t B,
                                   int64_t total, void* stream);
 
+/* hg_mcts_expand_backprop_dense with a workspace of
+ * hg_mcts_expand_backprop_dense_workspace(B, total) bytes (4-byte aligned):
+ * the same tree, the simulations of different root children applied in
+ * parallel (a planning launch settles node ids and the root's statistics in
+ * simulation order, then one wave per root child).  Identical results; the
+ * one-wave-per-game order is kept for games whose node pool could run short
+ * or whose paths are not selection paths. */
+int64_t hg_mcts_expand_backprop_dense_workspace(int64_t B, int64_t total);
+int hg_mcts_expand_backprop_dense_ws(const hg_tree* tree, const float* child_q_values, const int32_t* leaf_idx,
+                                     const uint8_t* leaf_states, const uint8_t* legal_moves,
+                                     const int32_t* num_legal, const float* priors_per_legal, const int32_t* results,
+                                     const float* nn_values, const int32_t* vl_paths, const int32_t* vl_lens,
+                                     float q_penalty, int64_t B, int64_t total, void* workspace, void* stream);
+
 /* mcts_apply_root_noise -- game_logic.cu:1384-1402 (mcts_root_noise_kernel,
  * mcts_tree.cuh:1192-1234).  noise[B][max_children_pad]; children beyond the
  * pad are left unchanged (the reference reads past the row there). */

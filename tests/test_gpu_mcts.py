@@ -186,3 +186,43 @@ def test_completed_q_descent_known_answers(mode):
     vc = t["visit_count"].cpu().numpy()
     assert np.array_equal(vc[np.arange(B), want], [c[0][w - 2][0] + 1 for c, w in zip(COMPLETED_Q_CASES, want)])
     assert (plen == 2).all() and np.array_equal(vl[np.arange(B), vlen - 1], want)
+
+
+class _OneWavePerGame(GpuEngine):
+    """GpuEngine whose expansion + backup calls the original one-wave-per-game
+    entry (hg_mcts_expand_backprop_dense) through the C-ABI."""
+
+    def expand_backprop(self, t, cq, leaf, states, legal, n, pri, results, vals, vl, vlen, qp=0.0):
+        import ctypes
+        import torch
+        from hive_neuralnet_amd.hive_gpu import _tree_struct
+        B, M = t["node_count"].shape[0], self.M(t)
+        tree = _tree_struct(self.args(t), t["child_init_q"], B, M)
+        ins = [self.c(x) for x in (cq, leaf, states, legal, n, pri, results, vals, vl, vlen)]
+        err = self.ext._lib.hg_mcts_expand_backprop_dense(ctypes.byref(tree), *[x.data_ptr() for x in ins],
+                                                          float(qp), B, leaf.shape[0],
+                                                          torch.cuda.current_stream().cuda_stream)
+        assert err == 0
+        torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("mode,W,C,M,dup,det,qp", [
+    ("slots", 2, 16, 8192, False, False, 0.0), ("slots", 4, 4, 8192, True, False, 0.0),
+    ("slots", 3, 4, 700, False, False, 0.0), ("slots", 2, 4, 8192, False, True, 0.25),
+    ("slots", 1, 4, 8192, False, True, 0.0), ("mask", 3, 4, 8192, False, False, 0.0)],
+    ids=["c16-w2", "duplicate-w4", "pool-short", "completed-q-w2", "completed-q-w1", "mask-w3"])
+def test_parallel_expand_backprop_equals_one_wave(roots, mode, W, C, M, dup, det, qp):
+    """hg_mcts_expand_backprop_dense_ws (root children in parallel after a
+    planning launch; the Python binding's path) against the original entry:
+    identical trees and selections after every wave, including duplicate
+    candidate slots (one root child, two columns), a node pool that runs short
+    (those games take the one-wave order), completed-Q descent with and
+    without the q penalty, and root-mask selection."""
+    kw = dict(W=W, C=C, M=M, mode=mode, waves=6, dup=dup, det=det, sigma=4.0, qp=qp)
+    a_t, a_rec = run_search(GpuEngine(), roots, **kw)
+    b_t, b_rec = run_search(_OneWavePerGame(), roots, **kw)
+    assert tree_equal(a_t, b_t) == []
+    for a, b in zip(a_rec[1:], b_rec[1:]):
+        for k in ("leaf", "paths", "plen", "vl", "vlen", "mid_visits"):
+            assert np.array_equal(a[k], b[k]), k
+        assert np.array_equal(a["mid_total"].view(np.uint32), b["mid_total"].view(np.uint32))
