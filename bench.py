@@ -35,7 +35,6 @@ BYTES_PER_POSITION = 3424 + 256 * 6 + 4 + 122 * 4 + 256 * 4  # 6476
 HBM_PEAK_GBS = 8000.0
 C4_BYTES_PER_PLY = 2 * 3424  # lockstep random play, unfused model: the state read and written back
 SEED = 0x5EED
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "k_legal_c2_traffic.txt")
 
 
 def parse_args():
@@ -54,6 +53,7 @@ def parse_args():
     ap.add_argument("--no-probe", action="store_true", help="skip the root tactical probe leg")
     ap.add_argument("--no-train", action="store_true", help="skip the training forward-batch leg")
     ap.add_argument("--no-c4", action="store_true", help="skip the C4 lockstep random-play leg")
+    ap.add_argument("--no-c3", action="store_true", help="skip the C3 expansion-piece positions leg")
     ap.add_argument("--c4-games", type=int, default=16384)
     ap.add_argument("--c4-plies", type=int, default=300)
     ap.add_argument("--game-parts", type=int, default=None,
@@ -62,7 +62,7 @@ def parse_args():
                     help="C5 simulations per candidate per wave: the (2,4,8,16) schedule or 1")
     ap.add_argument("--mcts-games", type=int, default=512)
     ap.add_argument("--mcts-sims", type=int, default=4096)
-    ap.add_argument("--mcts-plies", type=int, default=1, help="timed self-play plies")
+    ap.add_argument("--mcts-plies", type=int, default=3, help="timed self-play plies")
     ap.add_argument("--mcts-warmup", type=int, default=1, help="untimed self-play plies before timing")
     ap.add_argument("--mcts-roots", choices=("empty", "midgame"), default="empty")
     ap.add_argument("--graphs", choices=("auto", "on", "off"), default="auto",
@@ -72,11 +72,13 @@ def parse_args():
     return ap.parse_args()
 
 
-def traffic_per_launch():
-    """HBM bytes per launch from the committed rocprofv3 --pmc summary, else None."""
-    if not os.path.exists(TRAFFIC_FILE):
+def traffic_per_launch(config="C2"):
+    """HBM bytes per launch of k_legal at a configuration, from the committed
+    rocprofv3 --pmc summary (profiles/k_legal_<config>_traffic.txt), else None."""
+    path = os.path.join(ROOT, "profiles", f"k_legal_{(config or '').lower()}_traffic.txt")
+    if not config or not os.path.exists(path):
         return None
-    m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", open(TRAFFIC_FILE).read())
+    m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", open(path).read())
     return float(m.group(1)) if m else None
 
 
@@ -133,6 +135,29 @@ def cpu_baseline(states_np, threads, target_s):
                   f"(moves + features + action indices), {threads} pthreads = every CPU granted to this job",
         "per_core_value": per_core, "per_core_sample": f"the first {one.shape[0]} positions on one thread",
         "nproc_linear_estimate": per_core * cpus["nproc"], **cpus,
+    }
+
+
+def cpu_player_baseline(net, roots_np, sims, threads):
+    """The reference's CPU search player (FNNNativeCPUPlayer, fnn_native_cpu_player.py:126-266)
+    restated in oracle/hive_cpu_player.c: per game a serial Gumbel search of `sims`
+    simulations, each leaf evaluated with full-list successor features and the fp32
+    network; one game per thread on `threads` of the timed ply's roots."""
+    import numpy as np
+    from oracle import Oracle
+    orc = Oracle()
+    W = {k: v.detach().float().cpu().numpy() for k, v in net.state_dict().items()}
+    live = roots_np[roots_np[:, 3415] == 0]
+    sample = live[:threads]
+    t0 = time.perf_counter()
+    _, done = orc.cpu_player_search(sample, W, sims, 16, threads=threads)
+    wall = time.perf_counter() - t0
+    return {
+        "value": float(done.sum()) / wall, "unit": "sims/s", "cores": threads, "kind": "port",
+        "sample": f"{sample.shape[0]} of the first timed ply's roots, one game per thread, {sims} simulations "
+                  "each: FNNNativeCPUPlayer's serial Gumbel search (full-list successor features, fp32 network) "
+                  f"restated in oracle/hive_cpu_player.c; {int(done.sum())} simulations in {wall:.2f} s",
+        **host_cpus(),
     }
 
 
@@ -220,6 +245,7 @@ def mcts_leg(args):
 
     for _ in range(args.mcts_warmup):
         ply()
+    timed_roots = states.clone()  # the first timed ply's roots (the CPU player searches the same positions)
     orch.enable_counters()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -250,13 +276,15 @@ def mcts_leg(args):
                      "bytes_per_sim": b_sim, "formula": "5976 + 535*L + 16*D"},
     }
     if not args.no_cpu:
+        threads = baseline_threads(args)
+        out["cpu_baseline"] = cpu_player_baseline(net, timed_roots.cpu().numpy(), S, threads)
+        out["gpu_over_cpu"] = value / out["cpu_baseline"]["value"]
         orch.keep_last_leaves = True
         orch.counters = None
         cfg.num_simulations = min(S, 256)
         orch.search_ply(states, tree, active)
         leaves = orch.last_leaves.cpu().numpy()
-        out["cpu_baseline"] = mcts_cpu_baseline(net, leaves, baseline_threads(args), args.cpu_seconds)
-        out["gpu_over_cpu"] = value / out["cpu_baseline"]["value"]
+        out["cpu_leaf_eval_bound"] = mcts_cpu_baseline(net, leaves, threads, args.cpu_seconds)
     return out
 
 
@@ -391,32 +419,17 @@ def c4_leg(args):
     return out
 
 
-def main():
-    args = parse_args()
-    if args.gpus != 1:
-        print(f"bench.py measures one GPU only (got --gpus {args.gpus}): positions and games are "
-              "independent, so N GPUs shard the batch with no collectives; run with --gpus 1.", file=sys.stderr)
-        sys.exit(2)
+def positions_leg(args, B, mask, max_ply):
+    """One configuration of batched move generation + features + action indices
+    (hg_legal_features_actions, kernel k_legal<true,true,true>) over B seeded
+    random-play positions resident in HBM: positions/s over `steps` launches back
+    to back, the kernel's mean time from HIP events, its HBM roofline, and the
+    oracle on the host CPUs beside it."""
     import torch
-
-    if args.copy_calibration:
-        a = torch.ones(64 * 1024 * 1024, dtype=torch.float32, device="cuda")
-        b = torch.empty_like(a)
-        for _ in range(3):
-            b.copy_(a)
-        torch.cuda.synchronize()
-        print(json.dumps({"copy_bytes": a.numel() * 4, "copies": 3}))
-        return
-
-    if args.mcts_only:
-        print(json.dumps(mcts_leg(args)))
-        return
-
     from hive_neuralnet_amd import hive_gpu
 
     ext = hive_gpu.load_extension()
-    B = args.batch
-    states, plies = hive_gpu.random_positions(B, args.mask, args.max_ply, SEED)
+    states, plies = hive_gpu.random_positions(B, mask, max_ply, SEED)
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
 
@@ -459,42 +472,77 @@ def main():
 
     value = B * args.steps / wall
     achieved_gbs = BYTES_PER_POSITION * B / mean_kernel_s / 1e9
-    traffic = traffic_per_launch()
-    result = {
-        "metric": "positions/sec (move-gen+encode) at 65,536 batch; MCTS sims/sec at 512 games",
-        "value": value,
-        "unit": "positions/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": wall / args.steps * 1e3,
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "int32",
-        "data": "synthetic (seeded Philox random-play positions generated on the GPU)",
+    name = {(65536, 0, 120): "C2", (65536, 7, 150): "C3"}.get((B, mask, max_ply))
+    out = {
+        "value": value, "unit": "positions/s", "ms_per_step": wall / args.steps * 1e3,
         "config": {
-            "workload": "C2: fused legal moves + FNN features + action indices over 65,536 base-game positions "
-                        "(plies U[0,120])" if (B == 65536 and args.mask == 0 and args.max_ply == 120) else
-                        f"batch {B}, expansion mask {args.mask}, plies U[0,{args.max_ply}]",
-            "batch": B, "expansion_mask": args.mask, "max_ply": args.max_ply, "seed": SEED,
+            "workload": (f"{name}: fused legal moves + FNN features + action indices over {B:,} "
+                         f"{'base-game' if mask == 0 else 'expansion-piece (mosquito, ladybug, pillbug)'} "
+                         f"positions (plies U[0,{max_ply}])") if name else
+                        f"batch {B}, expansion mask {mask}, plies U[0,{max_ply}]",
+            "batch": B, "expansion_mask": mask, "max_ply": max_ply, "seed": SEED,
             "mean_legal_moves": n_mean, "mean_plies": float(plies.float().mean().item()),
             "entry_point": "hg_legal_features_actions",
         },
         "roofline": {
             "bound": "hbm", "achieved": achieved_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": achieved_gbs / HBM_PEAK_GBS, "traffic": traffic,
+            "frac": achieved_gbs / HBM_PEAK_GBS, "traffic": traffic_per_launch(name),
             "kernel": "k_legal<true,true,true>", "mean_kernel_ms": mean_kernel_s * 1e3,
             "bytes_per_position": BYTES_PER_POSITION,
         },
         "api_unfused_positions_per_s": unfused,
     }
     if not args.no_cpu:
-        threads = baseline_threads(args)
-        result["cpu_baseline"] = cpu_baseline(states.cpu().numpy(), threads, args.cpu_seconds)
-        result["gpu_over_cpu"] = value / result["cpu_baseline"]["value"]
+        out["cpu_baseline"] = cpu_baseline(states.cpu().numpy(), baseline_threads(args), args.cpu_seconds)
+        out["gpu_over_cpu"] = value / out["cpu_baseline"]["value"]
+    return out
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}): positions and games are "
+              "independent, so N GPUs shard the batch with no collectives; run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    if args.copy_calibration:
+        a = torch.ones(64 * 1024 * 1024, dtype=torch.float32, device="cuda")
+        b = torch.empty_like(a)
+        for _ in range(3):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes": a.numel() * 4, "copies": 3}))
+        return
+
+    if args.mcts_only:
+        print(json.dumps(mcts_leg(args)))
+        return
+
+    result = positions_leg(args, args.batch, args.mask, args.max_ply)
+    result = {
+        "metric": "positions/sec (move-gen+encode) at 65,536 batch; MCTS sims/sec at 512 games",
+        "value": result.pop("value"),
+        "unit": "positions/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": result.pop("ms_per_step"),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int32",
+        "data": "synthetic (seeded Philox random-play positions generated on the GPU)",
+        **result,
+    }
+    if not args.no_c3:  # configs[2]: the expansion-piece variant, same kernel and bytes per position
+        c3 = positions_leg(args, 65536, 7, 150)
+        c3["metric"] = "positions/sec (move-gen+encode), expansion pieces"
+        result["c3"] = c3
     if not args.no_mcts:
         result["mcts"] = mcts_leg(args)
+        mid = argparse.Namespace(**{**vars(args), "mcts_roots": "midgame", "no_cpu": args.no_cpu})
+        result["mcts_midgame"] = mcts_leg(mid)
         if args.mcts_waves == "schedule":  # the second C5 schedule: one simulation per candidate per wave
             w1 = argparse.Namespace(**{**vars(args), "mcts_waves": "1", "no_cpu": True})
             result["mcts_w1"] = mcts_leg(w1)

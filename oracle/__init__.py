@@ -222,6 +222,33 @@ class Oracle(_Engine):
                                               threads or default_threads())
         return win, allowed, forced
 
+    def cpu_player_search(self, states, weights: dict, num_sims: int, considered: int = 16, c_puct: float = 1.25,
+                          c_visit: float = 50.0, c_scale: float = 1.0, threads: int | None = None):
+        """FNNNativeCPUPlayer's serial Gumbel search on every state (one game per
+        thread, hive_cpu_player.c); weights = the `large` network's state dict as
+        float32 numpy arrays.  Returns (chosen slot [G] int32, simulations [G] int64)."""
+        states = np.ascontiguousarray(states, dtype=np.uint8)
+        G = states.shape[0]
+        W = {k: np.ascontiguousarray(v, dtype=np.float32) for k, v in weights.items()}
+        fp = ctypes.POINTER(ctypes.c_float)
+
+        class _W(ctypes.Structure):
+            _fields_ = [("fc1_w", fp), ("fc1_b", fp), ("ln_w", fp), ("ln_b", fp), ("fc2_w", fp), ("fc2_b", fp),
+                        ("value_w", fp), ("value_b", ctypes.c_float), ("a1_w", fp), ("a1_b", fp), ("a2_w", fp),
+                        ("a2_b", ctypes.c_float)]
+
+        p = lambda k: W[k].ctypes.data_as(fp)  # noqa: E731
+        w = _W(p("fc1.weight"), p("fc1.bias"), p("ln1.weight"), p("ln1.bias"), p("fc2.weight"), p("fc2.bias"),
+               p("value_fc.weight"), float(W["value_fc.bias"].reshape(-1)[0]), p("action_fc1.weight"),
+               p("action_fc1.bias"), p("action_fc2.weight"), float(W["action_fc2.bias"].reshape(-1)[0]))
+        chosen = np.zeros(G, np.int32)
+        sims = np.zeros(G, np.int64)
+        self.lib.or_cpu_player_search(_ptr(states, _u8p), ctypes.c_int64(G), ctypes.byref(w), int(num_sims),
+                                      int(considered), ctypes.c_float(c_puct), ctypes.c_float(c_visit),
+                                      ctypes.c_float(c_scale), _ptr(chosen, _i32p), _ptr(sims, _i64p),
+                                      int(threads or default_threads()))
+        return chosen, sims
+
     def surround_count(self, state, colour: int) -> int:
         s = np.ascontiguousarray(state, dtype=np.uint8)
         return int(self.lib.or_surround_count(_ptr(s, _u8p), int(colour)))

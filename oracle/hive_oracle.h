@@ -113,6 +113,18 @@ void or_mcts_extract_policy(const or_tree* t, const int32_t* move_numbers, const
                             int temp_drop, float pruning, int64_t B, float* policies);
 void or_legal_mask(const uint8_t* states, const uint8_t* legal, const int32_t* nlegal, int64_t B, float* masks);
 
+/* CPU search player (hive_cpu_player.c): FNNNativeCPUPlayer's serial Gumbel
+ * search (hive_fnn/fnn_native_cpu_player.py:126-266), one game per thread.
+ * Weights of the `large` network in torch's layout (Linear weight [out, in]). */
+typedef struct {
+    const float *fc1_w, *fc1_b, *ln_w, *ln_b, *fc2_w, *fc2_b, *value_w;
+    float value_b;
+    const float *a1_w, *a1_b, *a2_w;
+    float a2_b;
+} or_fnn_weights;
+void or_cpu_player_search(const uint8_t* states, int64_t G, const or_fnn_weights* w, int num_sims, int considered,
+                          float c_puct, float c_visit, float c_scale, int32_t* chosen, int64_t* sims, int threads);
+
 #ifdef __cplusplus
 }
 #endif
