@@ -432,23 +432,22 @@ template <bool WithMoves, bool WithAct, bool WithFeat>
 HW_INL void emit_list(Pos& P, const ListInfo& L, int lane, uint8_t* __restrict__ moves_row,
                       int32_t* __restrict__ act_row, int cq, int cr) {
     const int me = P.turn & 1;
+    const int l = gl(lane);
     uint16_t* row16 = reinterpret_cast<uint16_t*>(moves_row);
-    for (int i = gl(lane); i < kMaxLegal; i += kW) {
+    for (int i = l; i < L.n; i += kW) {
         int tp = 0, from = 0, to = 0;
-        if (i < L.n) {
-            if (L.total == 0) {
-                tp = MV_PASS;
-            } else {
-                int seg;
-                list_slot(P, L, i, tp, from, to, seg);
-                if (WithFeat && seg > 0) {
-                    bool thr = seg > L.n_pieces;
-                    int pt = tp >> 8;
-                    if ((thr || i == P.seg_base[seg]) && from < kCells && pt >= 1 && pt <= 8) {
-                        int owner = thr ? (P.tp(from) >> 4) & 1 : me;
-                        int r = occ_rank(P, from);  // sources of generated moves are occupied
-                        if (r < 32) atomicOr(&P.u1.from_d[(pt - 1) * 2 + owner], 1u << r);
-                    }
+        if (L.total == 0) {
+            tp = MV_PASS;
+        } else {
+            int seg;
+            list_slot(P, L, i, tp, from, to, seg);
+            if (WithFeat && seg > 0) {
+                bool thr = seg > L.n_pieces;
+                int pt = tp >> 8;
+                if ((thr || i == P.seg_base[seg]) && from < kCells && pt >= 1 && pt <= 8) {
+                    int owner = thr ? (P.tp(from) >> 4) & 1 : me;
+                    int r = occ_rank(P, from);  // sources of generated moves are occupied
+                    if (r < 32) atomicOr(&P.u1.from_d[(pt - 1) * 2 + owner], 1u << r);
                 }
             }
         }
@@ -457,10 +456,23 @@ HW_INL void emit_list(Pos& P, const ListInfo& L, int lane, uint8_t* __restrict__
             row16[3 * i + 1] = (uint16_t)from;
             row16[3 * i + 2] = (uint16_t)to;
         }
-        if (WithAct) act_row[i] = i < L.n ? move_action(tp & 0xFF, tp >> 8, from, to, cq, cr) : -1;
+        if (WithAct) act_row[i] = move_action(tp & 0xFF, tp >> 8, from, to, cq, cr);
+    }
+    // the rest of the rows: zero moves and -1 action indices, in 16-byte stores
+    // (rows are 16-byte aligned: 1,536 and 1,024 bytes per position)
+    if (WithMoves) {
+        const int h0 = 3 * L.n, c0 = (h0 + 7) >> 3;  // first padding half-word, first whole 16-byte chunk
+        if (l < 8 * c0 - h0) row16[h0 + l] = 0;
+        const u32x4 z = {0u, 0u, 0u, 0u};
+        for (int k = c0 + l; k < kMaxLegal * 6 / 16; k += kW) reinterpret_cast<u32x4*>(moves_row)[k] = z;
+    }
+    if (WithAct) {
+        const int c0 = (L.n + 3) >> 2;
+        if (l < 4 * c0 - L.n) act_row[L.n + l] = -1;
+        const u32x4 m1 = {~0u, ~0u, ~0u, ~0u};
+        for (int k = c0 + l; k < kMaxLegal / 4; k += kW) reinterpret_cast<u32x4*>(act_row)[k] = m1;
     }
 }
-
 
 // ---------------------------------------------------------------- summaries
 // Existence predicates: "the generator for this piece type is non-empty"

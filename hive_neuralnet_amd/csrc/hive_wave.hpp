@@ -435,17 +435,16 @@ HW_INL void build_cell_masks(Pos& P, int lane) {
     int rlo = r0 > 0 ? r0 - 1 : 0, rhi = r1 < kGrid - 1 ? r1 + 1 : kGrid - 1;
     int clo = c0 > 0 ? c0 - 1 : 0, chi = c1 < kGrid - 1 ? c1 + 1 : kGrid - 1;
     int bw = chi - clo + 1, n = bw * (rhi - rlo + 1);
+    const uint32_t inv = (65536u + (uint32_t)bw - 1u) / (uint32_t)bw;  // k / bw = (k * inv) >> 16 for k < 1024
     for (int k = l; k < n; k += kW) {
-        int rr = k / bw;
+        int rr = (int)(((uint32_t)k * inv) >> 16);
         int row = rlo + rr, col = clo + (k - rr * bw);
         int c = row * kGrid + col;
-        uint32_t gm = 0;
-        if (col < 22) gm |= 1u;
-        if (col < 22 && row > 0) gm |= 2u;
-        if (row > 0) gm |= 4u;
-        if (col > 0) gm |= 8u;
-        if (col > 0 && row < 22) gm |= 16u;
-        if (row < 22) gm |= 32u;
+        uint32_t gm = 63u;  // on-grid neighbour directions: E NE | NW | W SW | SE
+        if (col == kGrid - 1) gm &= ~3u;
+        if (col == 0) gm &= ~24u;
+        if (row == 0) gm &= ~6u;
+        if (row == kGrid - 1) gm &= ~48u;
         uint32_t nm = nbr_bits_raw(P.occ, c) & gm;
         P.sm[c] = (uint8_t)(gm & ~nm & (rotl6(nm) ^ rotr6(nm)));
         if (pb_get(P.occ, c)) {
