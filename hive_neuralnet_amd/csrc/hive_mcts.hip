@@ -465,7 +465,7 @@ HW_INL void row_centroid(const uint8_t* __restrict__ S, int lane, int& cq, int& 
         while (w) {
             int c = lane * 32 + __ffs(w) - 1;
             w &= w - 1;
-            int row = c / kGrid;
+            int row = row_of(c);
             q += c - row * kGrid - kHalf;
             r += row - kHalf;
             n++;
@@ -567,7 +567,7 @@ HW_INL void words_centroid(uint32_t w, int lane, int& cq, int& cr) {
     while (w) {
         int c = lane * 32 + __ffs(w) - 1;
         w &= w - 1;
-        int row = c / kGrid;
+        int row = row_of(c);
         q += c - row * kGrid - kHalf;
         r += row - kHalf;
         n++;

@@ -348,14 +348,28 @@ HW_INL void features_finish(Pos& P, const uint8_t* __restrict__ S, float* __rest
         F.cnt[100] = n_place;
     }
     __syncthreads();
+    // write-out: lane l takes features l, 32 + l, 64 + l and 96 + l, so each
+    // of the four stores has only the cases of its own range
+    static_assert(kW == 32 && kFeat == 122, "feature ranges per lane");
+    if (!out) return;
     constexpr float kPer[8] = {1.f, 3.f, 3.f, 2.f, 2.f, 1.f, 1.f, 1.f};
-    for (int i = l; i < kFeat; i += kW) {
+    if (l < 16) {
+        out[l] = (float)F.cnt[l];
+    } else {
+        int t = (l - 16) >> 1, c = (l - 16) & 1;
+        out[l] = (float)P.hand[c][t] / kPer[t];
+    }
+    if (l < 16) {
+        out[32 + l] = (float)F.cnt[32 + l];
+    } else {
+        int k = l - 16;
+        out[32 + l] = F.dcnt[k] > 0 ? (float)F.dsum[k] / (float)F.dcnt[k] / 10.0f : 0.0f;
+    }
+    out[64 + l] = (float)F.cnt[64 + l];
+    if (l < kFeat - 96) {
+        int i = 96 + l;
         float v;
-        if (i < 16) v = (float)F.cnt[i];
-        else if (i < 32) { int t = (i - 16) >> 1, c = (i - 16) & 1; v = (float)P.hand[c][t] / kPer[t]; }
-        else if (i < 48) v = (float)F.cnt[i];
-        else if (i < 64) { int k = i - 48; v = F.dcnt[k] > 0 ? (float)F.dsum[k] / (float)F.dcnt[k] / 10.0f : 0.0f; }
-        else if (i < 98) v = (float)F.cnt[i];
+        if (i < 98) v = (float)F.cnt[i];
         else if (i < 100) v = F.covered[i - 98] ? 1.0f : 0.0f;
         else if (i < 102) v = (i - 100) == me ? (float)F.cnt[100] / 10.0f : 0.0f;
         else if (i == 102) { int left = 200 - (int)P.turn; v = (float)(left < 0 ? 0 : left) / 200.0f; }
@@ -366,7 +380,7 @@ HW_INL void features_finish(Pos& P, const uint8_t* __restrict__ S, float* __rest
             int qc = (i - 110) / 6, b = (i - 110) % 6;
             v = (F.ring[qc] == b + 1) ? 1.0f : 0.0f;
         }
-        if (out) out[i] = v;
+        out[i] = v;
     }
 }
 
@@ -387,7 +401,7 @@ HW_INL void centroid(const Pos& P, int lane, int& cq, int& cr) {
     int q = 0, r = 0;
     if (l < P.n_occ) {
         int c = P.occ_cells[l];
-        int row = c / kGrid;
+        int row = row_of(c);
         q = c - row * kGrid - kHalf;
         r = row - kHalf;
     }
@@ -397,7 +411,7 @@ HW_INL void centroid(const Pos& P, int lane, int& cq, int& cr) {
 }
 
 __device__ __forceinline__ int window17(int cell, int cq, int cr) {
-    int row = cell / kGrid;
+    int row = row_of(cell);
     int ec = (cell - row * kGrid - kHalf) - cq + 8, er = (row - kHalf) - cr + 8;
     return (ec < 0 || ec >= 17 || er < 0 || er >= 17) ? -1 : er * 17 + ec;
 }

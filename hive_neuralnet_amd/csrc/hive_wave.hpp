@@ -71,9 +71,13 @@ constexpr uint64_t kOfs = (24ull) | (1ull << 6) | (0ull << 12) | (22ull << 18) |
 __device__ __forceinline__ int win_ofs(int d) { return (int)((kOfs >> (6 * d)) & 63); }
 __device__ __forceinline__ int step(int c, int d) { return c + win_ofs(d) - 23; }
 
+// grid row of a cell: c / 23 for 0 <= c < 4096 (one multiply and a shift;
+// (c * 2850) >> 16 equals c / 23 over that whole range)
+__device__ __forceinline__ int row_of(int c) { return (int)(((uint32_t)c * 2850u) >> 16); }
+
 // directions whose neighbour is on the 23x23 grid
 __device__ __forceinline__ uint32_t grid6(int c) {
-    int r = c / kGrid, col = c - r * kGrid;
+    int r = row_of(c), col = c - r * kGrid;
     uint32_t m = 0;
     if (col < 22) m |= 1u;
     if (col < 22 && r > 0) m |= 2u;
@@ -126,7 +130,7 @@ __device__ __forceinline__ uint32_t dir_bit_to(int c, int g, uint32_t gm) {
 }
 
 __device__ __forceinline__ int hexdist(int a, int b) {  // fnn_features.cuh:44-61
-    int ra = a / kGrid, rb = b / kGrid;
+    int ra = row_of(a), rb = row_of(b);
     int dq = (b - rb * kGrid) - (a - ra * kGrid), dr = rb - ra, ds = -(dq + dr);
     int m = abs(dq);
     m = max(m, abs(dr));
@@ -241,19 +245,17 @@ __device__ __forceinline__ uint32_t grp_or(uint32_t v) {
 
 // ---------------------------------------------------------------- state load
 // Four cells' bytes (height in bits 5-7, clamped to 7; top piece in bits 0-4
-// when the stack is non-empty) from their heights and level-0 bytes; bit k of
-// *stacked is set for cell c0 + k when its top is above level 0.
-__device__ __forceinline__ uint32_t pack_cells4(uint32_t hts, uint32_t lv0, int c0, uint32_t& stacked) {
-    uint32_t packed = 0;
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-        int hh = (int)((hts >> (8 * k)) & 0xFFu);
-        if (c0 + k >= kCells) hh = 0;
-        int h7 = hh > 7 ? 7 : hh;
-        if (hh > 1) stacked |= 1u << k;
-        packed |= (uint32_t)((h7 << 5) | (h7 ? (int)((lv0 >> (8 * k)) & 31u) : 0)) << (8 * k);
-    }
-    return packed;
+// when the stack is non-empty) from their heights and level-0 bytes, four
+// bytes at a time (no byte carries into its neighbour: every per-byte sum
+// stays below 256); bit k of *stacked is set for byte k when its top is above
+// level 0.  Cells past the board must come with height 0.
+__device__ __forceinline__ uint32_t pack_cells4(uint32_t hts, uint32_t lv0, uint32_t& stacked) {
+    const uint32_t big = ((((hts & 0xF8F8F8F8u) >> 3) + 0x1F1F1F1Fu) >> 5) & 0x01010101u;  // height >= 8
+    const uint32_t h7 = (hts & 0x07070707u) | (big * 7u);                               // min(height, 7)
+    const uint32_t nz = ((h7 + 0x7F7F7F7Fu) >> 7) & 0x01010101u;                        // height >= 1
+    const uint32_t up = ((h7 + 0x7E7E7E7Eu) >> 7) & 0x01010101u;                        // height >= 2
+    stacked = ((up * 0x00204081u) >> 21) & 15u;  // byte k's flag (bit 8k) lands on bit 21 + k
+    return (h7 << 5) | (lv0 & 0x1F1F1F1Fu & (nz * 0xFFu));
 }
 
 // Heights, top bytes, bitboards and metadata of the state row S into P.
@@ -294,22 +296,26 @@ HW_INL void load_position(Pos& P, const uint8_t* __restrict__ S, int lane) {
     uint32_t st_a = 0, st_b = 0;
     {
         u32x4 o;
-        uint32_t s;
-        s = 0; o[0] = pack_cells4(__builtin_amdgcn_alignbyte(ht_a[1], ht_a[0], 1), lv_a[0], 16 * l + 0, s); st_a |= s;
-        s = 0; o[1] = pack_cells4(__builtin_amdgcn_alignbyte(ht_a[2], ht_a[1], 1), lv_a[1], 16 * l + 4, s); st_a |= s << 4;
-        s = 0; o[2] = pack_cells4(__builtin_amdgcn_alignbyte(ht_a[3], ht_a[2], 1), lv_a[2], 16 * l + 8, s); st_a |= s << 8;
-        s = 0; o[3] = pack_cells4(__builtin_amdgcn_alignbyte(ht_a4, ht_a[3], 1), lv_a[3], 16 * l + 12, s); st_a |= s << 12;
+        uint32_t s0, s1, s2, s3;
+        o[0] = pack_cells4(__builtin_amdgcn_alignbyte(ht_a[1], ht_a[0], 1), lv_a[0], s0);
+        o[1] = pack_cells4(__builtin_amdgcn_alignbyte(ht_a[2], ht_a[1], 1), lv_a[1], s1);
+        o[2] = pack_cells4(__builtin_amdgcn_alignbyte(ht_a[3], ht_a[2], 1), lv_a[2], s2);
+        o[3] = pack_cells4(__builtin_amdgcn_alignbyte(ht_a4, ht_a[3], 1), lv_a[3], s3);
+        st_a = s0 | (s1 << 4) | (s2 << 8) | (s3 << 12);
         *reinterpret_cast<u32x4*>(cell32 + 4 * l) = o;
     }
-    if (two) {
+    if (two) {  // chunks 32 (cells 512-527) and 33 (528-543: only cell 528 is on the board)
+        const uint32_t keep = k1 == 33 ? 0xFFu : 0xFFFFFFFFu;
         u32x4 o;
-        uint32_t s;
-        s = 0; o[0] = pack_cells4(__builtin_amdgcn_alignbyte(ht_b[1], ht_b[0], 1), lv_b[0], 16 * k1 + 0, s); st_b |= s;
-        s = 0; o[1] = pack_cells4(__builtin_amdgcn_alignbyte(ht_b[2], ht_b[1], 1), lv_b[1], 16 * k1 + 4, s); st_b |= s << 4;
-        s = 0; o[2] = pack_cells4(__builtin_amdgcn_alignbyte(ht_b[3], ht_b[2], 1), lv_b[2], 16 * k1 + 8, s); st_b |= s << 8;
-        s = 0; o[3] = pack_cells4(__builtin_amdgcn_alignbyte(ht_b4, ht_b[3], 1), lv_b[3], 16 * k1 + 12, s); st_b |= s << 12;
+        uint32_t s0, s1, s2, s3;
+        o[0] = pack_cells4(__builtin_amdgcn_alignbyte(ht_b[1], ht_b[0], 1) & keep, lv_b[0], s0);
+        o[1] = pack_cells4(k1 == 33 ? 0u : __builtin_amdgcn_alignbyte(ht_b[2], ht_b[1], 1), lv_b[1], s1);
+        o[2] = pack_cells4(k1 == 33 ? 0u : __builtin_amdgcn_alignbyte(ht_b[3], ht_b[2], 1), lv_b[2], s2);
+        o[3] = pack_cells4(k1 == 33 ? 0u : __builtin_amdgcn_alignbyte(ht_b4, ht_b[3], 1), lv_b[3], s3);
+        st_b = s0 | (s1 << 4) | (s2 << 8) | (s3 << 12);
         *reinterpret_cast<u32x4*>(cell32 + 4 * k1) = o;
     }
+    static_assert(kCells == 16 * 33 + 1, "the last chunk holds one board cell");
     // stacked tops: level min(h, 5) - 1 of the cell (h is the clamped height)
     uint32_t st = st_a | (st_b << 16);
     while (st) {
@@ -592,25 +598,77 @@ HW_INL int gen_hopper(const Pos& P, int c, uint16_t* out) {
 // the exit back to the parent leads to a visited cell and is skipped.
 constexpr int kDirShift = 10;
 constexpr int kCellMask = (1 << kDirShift) - 1;
+
+// Byte d of the 8-byte table {hi:lo} (one v_perm_b32; selector 0x0c = zero byte).
+__device__ __forceinline__ uint32_t dir_byte(uint32_t hi, uint32_t lo, int d) {
+    return __builtin_amdgcn_perm(hi, lo, 0x0c0c0c00u | (uint32_t)d);
+}
+// cell offset + 23 of direction d (24 1 0 22 45 46) and the opposite
+// direction's bit 1 << ((d + 3) % 6) (8 16 32 1 2 4)
+constexpr uint32_t kOfsLo = 24u | (1u << 8) | (0u << 16) | (22u << 24), kOfsHi = 45u | (46u << 8);
+constexpr uint32_t kOppLo = 8u | (16u << 8) | (32u << 16) | (1u << 24), kOppHi = 2u | (4u << 8);
+
+// Slide exits of x, an empty neighbour of the lifted origin c in direction
+// d of c, from its exits s with c occupied.  Only the exits b - 1, b, b + 1
+// around b = d + 3 (the direction x -> c) change:
+//   * exit b leads into c; its flanks are c's neighbours d + 1 and d + 5:
+//     open iff exactly one of them is occupied (bit d of ox);
+//   * exits b + 1 and b - 1 lead to c's neighbours d + 5 and d + 1; their
+//     flank c turns empty, so an on-grid empty target is now open iff the
+//     far flank is occupied, i.e. iff the exit was closed: ey / ez carry
+//     "target on-grid and empty" at bit d.
+__device__ __forceinline__ uint32_t lifted_exits(uint32_t s, int d, uint32_t ox, uint32_t ey, uint32_t ez) {
+    const int b = d >= 3 ? d - 3 : d + 3;
+    const int bh = b == 5 ? 0 : b + 1, bl = b == 0 ? 5 : b - 1;
+    uint32_t r = s & ~((1u << b) | (1u << bh) | (1u << bl));
+    r |= ((ox >> d) & 1u) << b;
+    r |= ((ey >> d) & ~(s >> bh) & 1u) << bh;
+    r |= ((ez >> d) & ~(s >> bl) & 1u) << bl;
+    return r;
+}
+
+// Queue entries are cell | (bit of the direction back to the parent) <<
+// kDirShift: that exit leads to a visited cell and is skipped.  A dequeued
+// cell within one row of c is tested for adjacency to c (window position
+// w = cur - c + 23 on the ring); its direction d from c is read from w:
+// the row r = (w + 1) / 23 and w + 1 - 20 r in {5 2 1 3 6 7} for d = 0..5.
 HW_INL int gen_ant(const Pos& P, int c, uint16_t* out, int cap, uint32_t* seen) {
     set_clear(seen);
     set_insert(seen, c);
+    const uint32_t oc = nbo(P, c), ec = grid6(c) & ~oc;
+    const uint32_t ox = rotr6(oc) ^ rotl6(oc), ey = rotl6(ec), ez = rotr6(ec);
     int head = 0, tail = 0;
     int cur = c;
     uint32_t back = 0;
     for (;;) {
-        uint32_t m = slide_mask(P, cur, c) & ~back;
-        while (m && tail < cap) {
-            int d = __ffs(m) - 1;
-            m &= m - 1;
-            int dest = step(cur, d);
-            if (set_insert(seen, dest)) out[tail++] = (uint16_t)(dest | (d << kDirShift));
+        uint32_t m = P.sm[cur];
+        const uint32_t w = (uint32_t)(cur - c + 23);
+        if (w < 47u && ((kRingWin >> w) & 1ull)) {
+            const uint32_t w1 = w + 1u, r = (w1 * 2850u) >> 16;
+            const int d = (int)((0x54003120u >> (4u * (w1 - 20u * r))) & 15u);
+            m = lifted_exits(m, d, ox, ey, ez);
+        }
+        m &= ~back;
+        const int base = cur - 23;
+        if (tail + 6 <= cap) {  // room for every exit
+            while (m) {
+                int d = __ffs(m) - 1;
+                m &= m - 1;
+                int dest = base + (int)dir_byte(kOfsHi, kOfsLo, d);
+                if (set_insert(seen, dest)) out[tail++] = (uint16_t)(dest | (dir_byte(kOppHi, kOppLo, d) << kDirShift));
+            }
+        } else {
+            while (m && tail < cap) {
+                int d = __ffs(m) - 1;
+                m &= m - 1;
+                int dest = base + (int)dir_byte(kOfsHi, kOfsLo, d);
+                if (set_insert(seen, dest)) out[tail++] = (uint16_t)(dest | (dir_byte(kOppHi, kOppLo, d) << kDirShift));
+            }
         }
         if (head >= tail || tail >= cap) break;
-        int e = out[head++];
-        cur = e & kCellMask;
-        int d = e >> kDirShift;
-        back = 1u << (d >= 3 ? d - 3 : d + 3);
+        const uint32_t e = out[head++];
+        cur = (int)(e & kCellMask);
+        back = e >> kDirShift;
     }
     return tail;
 }

@@ -101,6 +101,18 @@ inline uint32_t __builtin_amdgcn_alignbyte(uint32_t hi, uint32_t lo, uint32_t s)
 }
 // DPP lane moves used by the engine's prefix sums: row_shr:1..15, row_bcast:15,
 // row_bcast:31 (GFX9 semantics).  Every lane of the wave calls it.
+// v_perm_b32: byte k of the result is selected by byte k of sel from the
+// 8 bytes {hi:lo} (0-7), or 0x00 for selector 0x0c (the only other value used)
+inline uint32_t __builtin_amdgcn_perm(uint32_t hi, uint32_t lo, uint32_t sel) {
+    uint64_t v = ((uint64_t)hi << 32) | lo;
+    uint32_t r = 0;
+    for (int k = 0; k < 4; k++) {
+        uint32_t b = (sel >> (8 * k)) & 0xFF;
+        if (b < 8) r |= (uint32_t)((v >> (8 * b)) & 0xFF) << (8 * k);
+        else if (b != 0x0c) abort();
+    }
+    return r;
+}
 inline int __builtin_amdgcn_update_dpp(int old, int src, int ctrl, int row_mask, int bank_mask, bool bound_ctrl) {
     int l = wave_emu::lane(), row = l >> 4, r = l & 15, bank = r >> 2;
     bool enabled = ((row_mask >> row) & 1) && ((bank_mask >> bank) & 1);
