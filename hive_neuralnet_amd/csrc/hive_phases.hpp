@@ -124,7 +124,7 @@ HW_INL ListInfo generate_legal(Pos& P, int lane) {
         int m = 0;
         switch (t) {
             case PT_Q: case PT_P: m = gen_step(P, c, out); break;
-            case PT_A: m = gen_ant(P, c, out, 64, s0); break;
+            case PT_A: m = gen_ant(P, c, out, kAntCap, s0); break;
             case PT_G: m = gen_hopper(P, c, out); break;
             case PT_S: m = gen_spider(P, c, out, s0); break;
             case PT_B: m = gen_beetle(P, c, out); break;
@@ -133,7 +133,7 @@ HW_INL ListInfo generate_legal(Pos& P, int lane) {
             default: break;
         }
         P.piece_off[l] = (uint16_t)off;
-        P.piece_cnt[l] = (uint16_t)m;
+        P.piece_cnt[l] = (uint8_t)m;
     } else if (l >= kMaxPieces && l - kMaxPieces < n_actors) {
         int j = l - kMaxPieces;
         P.throw_cnt[j] = (uint16_t)gen_throws(P, P.actor_cell[j], P.throw_from[j], P.throw_to[j], P.throw_pt[j]);
@@ -227,7 +227,7 @@ enum { kFeatList = 0, kFeatGen = 1, kFeatBucket = 2 };
 // caller-supplied list's cell sets) ...
 HW_INL void sources_clear(Pos& P, int lane, ListSets* X = nullptr) {
     const int l = gl(lane);
-    if (l < 16) P.u1.from_d[l] = 0;
+    if (l < 16) P.u1.e.from_d[l] = 0;
     if (X) {
         for (int i = l; i < 16 * 18; i += kW) (&X->from_bb[0][0])[i] = 0;
         if (l < 18) X->place_bb[l] = 0;
@@ -289,7 +289,7 @@ HW_INL void features_finish(Pos& P, const uint8_t* __restrict__ S, float* __rest
             int q = P.queen[qc];
             if (q != 0xFFFF && q < kCells && dir_bit_to(q, c, grid6(q))) atomicAdd(&F.ring[qc], 1);
         }
-        if (pt && h == 1 && pb_get(P.ap, c)) atomicAdd(&F.cnt[80 + tc], 1);
+        if (pt && pb_get(P.pin, c)) atomicAdd(&F.cnt[80 + tc], 1);  // articulation point, one piece high
         if (pt != PT_Q && h >= 2) {
             for (int lv = 0; lv < h - 1 && lv < 5; lv++) {
                 int b = S[lv * kCells + c];
@@ -343,7 +343,7 @@ HW_INL void features_finish(Pos& P, const uint8_t* __restrict__ S, float* __rest
             F.cnt[100] = s;
         }
     } else if (l < 16) {
-        F.cnt[64 + l] = __popc(P.u1.from_d[l]);
+        F.cnt[64 + l] = __popc(P.u1.e.from_d[l]);
     } else if (l == 16) {
         F.cnt[100] = n_place;
     }
@@ -439,19 +439,44 @@ HW_INL void list_actions(const uint8_t* __restrict__ M, int n, int cq, int cr, i
     }
 }
 
+// Placement cells in ascending order (the first kPlist) into u1.e.plist, for
+// emit_list; lane w < 18 takes board word w.  After generation (u1 no longer
+// holds visited sets), before the barrier that precedes emit_list.
+HW_INL void place_list(Pos& P, int lane) {
+    const int l = gl(lane);
+    if (l < 18) {
+        uint32_t pw = P.plc[l + 1];
+        int k = P.plc_pre[l];
+        while (pw && k < kPlist) {
+            P.u1.e.plist[k++] = (uint16_t)(32 * l + __ffs(pw) - 1);
+            pw &= pw - 1;
+        }
+    }
+}
+
 // Writes the generated list: moves (zero padded), action indices (-1
 // padded), and the MOVE-source sets of the features (one bit per piece
-// segment that is inside the cut, one per throw entry).
+// segment that is inside the cut, one per throw entry).  Placement slot i
+// is cell i / ntypes of the placement list with the (i % ntypes)-th
+// placeable type (the quotient by a multiply: (i * ceil(65536 / ntypes))
+// >> 16 is exact for i < 256, ntypes <= 8); later slots are decoded by
+// list_slot.
 template <bool WithMoves, bool WithAct, bool WithFeat>
 HW_INL void emit_list(Pos& P, const ListInfo& L, int lane, uint8_t* __restrict__ moves_row,
                       int32_t* __restrict__ act_row, int cq, int cr) {
     const int me = P.turn & 1;
     const int l = gl(lane);
     uint16_t* row16 = reinterpret_cast<uint16_t*>(moves_row);
+    const uint32_t nt = (uint32_t)(L.ntypes > 0 ? L.ntypes : 1);
+    const uint32_t inv = (65536u + nt - 1u) / nt;
     for (int i = l; i < L.n; i += kW) {
         int tp = 0, from = 0, to = 0;
         if (L.total == 0) {
             tp = MV_PASS;
+        } else if (i < L.n_place && i < kPlist) {  // cell rank <= i
+            const int r = (int)(((uint32_t)i * inv) >> 16);
+            to = P.u1.e.plist[r];
+            tp = MV_PLACE | ((select_bit(L.emit_types, i - r * (int)nt) + 1) << 8);
         } else {
             int seg;
             list_slot(P, L, i, tp, from, to, seg);
@@ -461,7 +486,7 @@ HW_INL void emit_list(Pos& P, const ListInfo& L, int lane, uint8_t* __restrict__
                 if ((thr || i == P.seg_base[seg]) && from < kCells && pt >= 1 && pt <= 8) {
                     int owner = thr ? (P.tp(from) >> 4) & 1 : me;
                     int r = occ_rank(P, from);  // sources of generated moves are occupied
-                    if (r < 32) atomicOr(&P.u1.from_d[(pt - 1) * 2 + owner], 1u << r);
+                    if (r < 32) atomicOr(&P.u1.e.from_d[(pt - 1) * 2 + owner], 1u << r);
                 }
             }
         }
@@ -508,18 +533,19 @@ HW_INL bool has_hopper(const Pos& P, int c) {
 }
 
 HW_INL bool has_spider(const Pos& P, int c) {
-    uint32_t m1 = slide_mask(P, c, c);
+    const Lift lf = lift_of(P, c);
+    uint32_t m1 = P.sm[c];
     while (m1) {
         int d1 = __ffs(m1) - 1;
         m1 &= m1 - 1;
         int p1 = step(c, d1);
-        uint32_t m2 = slide_mask(P, p1, c);
+        uint32_t m2 = exits_next_to(P, p1, d1, lf);
         while (m2) {
             int d2 = __ffs(m2) - 1;
             m2 &= m2 - 1;
             int p2 = step(p1, d2);
             if (p2 == c) continue;
-            uint32_t m3 = slide_mask(P, p2, c);
+            uint32_t m3 = exits_lifted(P, p2, lf);
             while (m3) {
                 int d3 = __ffs(m3) - 1;
                 m3 &= m3 - 1;
@@ -799,6 +825,7 @@ HW_INL void run_legal(Pos& P, const uint8_t* __restrict__ S, int lane, uint8_t* 
                       int32_t* __restrict__ n_slot, float* __restrict__ feat_row, int32_t* __restrict__ act_row) {
     prepare(P, S, lane);
     ListInfo L = generate_legal(P, lane);
+    place_list(P, lane);
     if (WithFeat) sources_clear(P, lane);
     int cq = 0, cr = 0;
     if (WithAct) centroid(P, lane, cq, cr);

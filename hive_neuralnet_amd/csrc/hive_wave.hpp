@@ -40,18 +40,22 @@ constexpr int kFeat = 122;
 constexpr int kPW = 20;  // padded words per bitboard
 constexpr int kMaxPieces = 16;
 // Destination pool entries for one side's pieces at type_capacity() each:
-// 3 ants x 64 + mosquito 128 + 2 spiders x 32 + ladybug 32 + 8 others x 6.
+// 3 ants x 60 + mosquito 96 + 2 spiders x 32 + ladybug 32 + 8 others x 6.
 // Capacities are bounds for states built by init/apply: a connected hive of
 // n cells has at most 2n + 4 empty neighbour cells (each cell added next to
 // the hive removes one and adds at most three), every ant destination is
-// one of them with n <= 27 (the ant lifted), so an ant has < 64; a
-// mosquito's union adds at most its 6 neighbours.
-constexpr int kPool = 464;
+// one of them with n <= 27 (the ant lifted), so an ant has <= 58; a
+// mosquito's union (<= 58 empty cells + 6 neighbours to climb on) plus the
+// sub-list being merged (<= 32) fits in 96.
+constexpr int kAntCap = 60;
+constexpr int kMosqRoom = 96;
+constexpr int kPool = 3 * kAntCap + kMosqRoom + 2 * 32 + 32 + 8 * 6;
 constexpr int kActors = 2;  // throw actors of one colour: its pillbug and its mosquito
 // throws of one actor: targets are occupied and drops empty neighbours of
 // the actor, so targets x drops <= 3 x 3
-constexpr int kThrowCap = 12;
+constexpr int kThrowCap = 9;
 constexpr int kSets = 8;  // visited / dedup sets: 3 ants, 2 spiders, 1 ladybug, 1 mosquito (2)
+constexpr int kPlist = 240;  // placement cells kept for emission (a board has <= 60)
 constexpr int kSegs = 1 + kMaxPieces + kActors + 1;  // placements, pieces, actors, end
 constexpr int kW = 32;               // lanes per position
 constexpr int kPosPerWave = 64 / kW;  // positions per wavefront
@@ -138,9 +142,10 @@ __device__ __forceinline__ int hexdist(int a, int b) {  // fnn_features.cuh:44-6
 }
 
 struct alignas(16) Pos {
-    uint32_t occ[kPW], wt[kPW], bt[kPW], ap[kPW], pin[kPW], plc[kPW];
+    // pin: articulation points whose stack is one piece high
+    uint32_t occ[kPW], wt[kPW], bt[kPW], pin[kPW], plc[kPW];
     uint8_t cell[544];  // top piece byte (type | colour << 4) in bits 0-4, stack height in bits 5-7
-    uint8_t sm[544];  // ground-slide exits of each cell with nothing lifted
+    uint8_t sm[532];  // ground-slide exits of each board cell with nothing lifted
     uint16_t occ_pre[20];  // occupied cells in board words before word w
     uint16_t plc_pre[20];  // placement cells in board words before word w
     int16_t seg_base[kSegs];  // legal-list segment starts (placements, pieces, actors, end)
@@ -156,18 +161,22 @@ struct alignas(16) Pos {
     uint16_t piece_cell[kMaxPieces];
     uint8_t piece_type[kMaxPieces];
     uint16_t piece_off[kMaxPieces];
-    uint16_t piece_cnt[kMaxPieces];
+    uint8_t piece_cnt[kMaxPieces];
     uint16_t actor_cell[kActors];
     uint16_t throw_cnt[kActors];
     uint16_t throw_from[kActors][kThrowCap];
     uint16_t throw_to[kActors][kThrowCap];
     uint8_t throw_pt[kActors][kThrowCap];
     // articulation: dense adjacency; generation: visited sets; emission and
-    // features: the generated list's MOVE sources per (type, owner), by rank
+    // features: the generated list's MOVE sources per (type, owner), by rank,
+    // and the placement cells in ascending order (the first kPlist)
     union {
         uint32_t adj[32];
-        uint32_t sets[kSets][18];
-        uint32_t from_d[16];
+        uint32_t sets[kSets][17];
+        struct {
+            uint32_t from_d[16];
+            uint16_t plist[kPlist];
+        } e;
     } u1;
     // generation and emission: destinations; features (after emission): counters
     union {
@@ -472,7 +481,7 @@ HW_INL void articulation(Pos& P, int lane) {
     const int l = gl(lane);
     int total = P.n_occ;
     int N = total < 28 ? total : 28;
-    if (l < 20) { P.ap[l] = 0; P.pin[l] = 0; }
+    if (l < 20) P.pin[l] = 0;
     if (l < N) {
         int c = P.occ_cells[l];
         uint32_t nm = nbr_bits(P.occ, c);
@@ -512,7 +521,6 @@ HW_INL void articulation(Pos& P, int lane) {
     bool is_ap = v >= 0 && ((c0 >> v) & 1u) && reach != (c0 & ~vbit);
     if (is_ap) {
         int c = P.occ_cells[v];
-        atomicOr(&P.ap[(c >> 5) + 1], 1u << (c & 31));
         if (P.hgt(c) == 1) atomicOr(&P.pin[(c >> 5) + 1], 1u << (c & 31));
     }
 }
@@ -547,9 +555,9 @@ __device__ __forceinline__ bool gate_high(uint32_t nh, int d, int lvl) {
 }
 
 // lane-private set helpers over an 18-word bitboard
-__device__ __forceinline__ void set_clear(uint32_t* s) {
+__device__ __forceinline__ void set_clear(uint32_t* s) {  // 17 words: cells < 544
 #pragma unroll
-    for (int i = 0; i < 18; i++) s[i] = 0;
+    for (int i = 0; i < 17; i++) s[i] = 0;
 }
 __device__ __forceinline__ bool set_insert(uint32_t* s, int c) {  // true if newly inserted
     uint32_t bit = 1u << (c & 31);
@@ -627,28 +635,46 @@ __device__ __forceinline__ uint32_t lifted_exits(uint32_t s, int d, uint32_t ox,
     return r;
 }
 
-// Queue entries are cell | (bit of the direction back to the parent) <<
-// kDirShift: that exit leads to a visited cell and is skipped.  A dequeued
-// cell within one row of c is tested for adjacency to c (window position
-// w = cur - c + 23 on the ring); its direction d from c is read from w:
+// A piece at c about to move: c's occupied / empty on-grid neighbour masks
+// rotated so that bit d carries what lifted_exits needs for c's neighbour d.
+struct Lift {
+    int c;
+    uint32_t ox, ey, ez;
+};
+HW_INL Lift lift_of(const Pos& P, int c) {
+    const uint32_t oc = nbo(P, c), ec = grid6(c) & ~oc;
+    return Lift{c, rotr6(oc) ^ rotl6(oc), rotl6(ec), rotr6(ec)};
+}
+// exits of the empty cell x = step(lf.c, d) with the piece at lf.c lifted
+__device__ __forceinline__ uint32_t exits_next_to(const Pos& P, int x, int d, const Lift& lf) {
+    return lifted_exits(P.sm[x], d, lf.ox, lf.ey, lf.ez);
+}
+// exits of an empty cell x with the piece at lf.c lifted (slide_mask(P, x,
+// lf.c)): x is tested for adjacency to lf.c by its window position
+// w = x - lf.c + 23 on the ring; its direction d from lf.c is read from w:
 // the row r = (w + 1) / 23 and w + 1 - 20 r in {5 2 1 3 6 7} for d = 0..5.
+__device__ __forceinline__ uint32_t exits_lifted(const Pos& P, int x, const Lift& lf) {
+    uint32_t m = P.sm[x];
+    const uint32_t w = (uint32_t)(x - lf.c + 23);
+    if (w < 47u && ((kRingWin >> w) & 1ull)) {
+        const uint32_t w1 = w + 1u, r = (w1 * 2850u) >> 16;
+        const int d = (int)((0x54003120u >> (4u * (w1 - 20u * r))) & 15u);
+        m = lifted_exits(m, d, lf.ox, lf.ey, lf.ez);
+    }
+    return m;
+}
+
+// Queue entries are cell | (bit of the direction back to the parent) <<
+// kDirShift: that exit leads to a visited cell and is skipped.
 HW_INL int gen_ant(const Pos& P, int c, uint16_t* out, int cap, uint32_t* seen) {
     set_clear(seen);
     set_insert(seen, c);
-    const uint32_t oc = nbo(P, c), ec = grid6(c) & ~oc;
-    const uint32_t ox = rotr6(oc) ^ rotl6(oc), ey = rotl6(ec), ez = rotr6(ec);
+    const Lift lf = lift_of(P, c);
     int head = 0, tail = 0;
     int cur = c;
     uint32_t back = 0;
     for (;;) {
-        uint32_t m = P.sm[cur];
-        const uint32_t w = (uint32_t)(cur - c + 23);
-        if (w < 47u && ((kRingWin >> w) & 1ull)) {
-            const uint32_t w1 = w + 1u, r = (w1 * 2850u) >> 16;
-            const int d = (int)((0x54003120u >> (4u * (w1 - 20u * r))) & 15u);
-            m = lifted_exits(m, d, ox, ey, ez);
-        }
-        m &= ~back;
+        uint32_t m = exits_lifted(P, cur, lf) & ~back;
         const int base = cur - 23;
         if (tail + 6 <= cap) {  // room for every exit
             while (m) {
@@ -677,18 +703,19 @@ HW_INL int gen_ant(const Pos& P, int c, uint16_t* out, int cap, uint32_t* seen) 
 HW_INL int gen_spider(const Pos& P, int c, uint16_t* out, uint32_t* got) {
     set_clear(got);
     int n = 0;
-    uint32_t m1 = slide_mask(P, c, c);
+    const Lift lf = lift_of(P, c);
+    uint32_t m1 = P.sm[c];
     while (m1) {
         int d1 = __ffs(m1) - 1;
         m1 &= m1 - 1;
         int p1 = step(c, d1);
-        uint32_t m2 = slide_mask(P, p1, c);
+        uint32_t m2 = exits_next_to(P, p1, d1, lf);
         while (m2) {
             int d2 = __ffs(m2) - 1;
             m2 &= m2 - 1;
             int p2 = step(p1, d2);
             if (p2 == c) continue;
-            uint32_t m3 = slide_mask(P, p2, c);
+            uint32_t m3 = exits_lifted(P, p2, lf);
             while (m3) {
                 int d3 = __ffs(m3) - 1;
                 m3 &= m3 - 1;
@@ -757,9 +784,12 @@ HW_INL int gen_ladybug(const Pos& P, int c, uint16_t* out, uint32_t* got) {
 
 // gen_mosquito_moves :907-1008: beetle when stacked; otherwise the union, in
 // order Q/P, A, G, S, B, L, of the abilities of adjacent non-mosquito top
-// pieces, first occurrence kept, at most 128.  Each sub-list is generated
-// into the free tail of out[] and merged in place (merge write index never
-// passes the read index).  Needs 6 + 128 slots of room.
+// pieces, first occurrence kept (the reference caps it at 128; it has at
+// most 64 entries).  Each sub-list is generated into the free tail of out[]
+// and merged in place (merge write index never passes the read index);
+// kMosqRoom slots hold the union so far (<= 64) and a sub-list (<= 32), and
+// a union past 64 entries (no state built by init/apply has one) stops the
+// merging before a sub-list could run past the room.
 HW_INL int gen_mosquito(const Pos& P, int c, uint16_t* out, uint32_t* tmpset, uint32_t* unionset) {
     if (P.hgt(c) > 1) return gen_beetle(P, c, out);
     uint32_t gm = grid6(c);
@@ -773,12 +803,12 @@ HW_INL int gen_mosquito(const Pos& P, int c, uint16_t* out, uint32_t* tmpset, ui
     (void)gm;
     set_clear(unionset);
     int n = 0;
-    for (int k = 0; k < 6; k++) {
+    for (int k = 0; k < 6 && n <= kMosqRoom - 32; k++) {
         uint16_t* tail = out + n;
         int m = 0;
         switch (k) {
             case 0: if (has & ((1u << PT_Q) | (1u << PT_P))) m = gen_step(P, c, tail); break;
-            case 1: if (has & (1u << PT_A)) m = gen_ant(P, c, tail, 128 - n, tmpset); break;
+            case 1: if (has & (1u << PT_A)) m = gen_ant(P, c, tail, kMosqRoom - n, tmpset); break;
             case 2: if (has & (1u << PT_G)) m = gen_hopper(P, c, tail); break;
             case 3: if (has & (1u << PT_S)) m = gen_spider(P, c, tail, tmpset); break;
             case 4: if (has & (1u << PT_B)) m = gen_beetle(P, c, tail); break;
@@ -787,7 +817,7 @@ HW_INL int gen_mosquito(const Pos& P, int c, uint16_t* out, uint32_t* tmpset, ui
         int w = n;
         for (int i = 0; i < m; i++) {
             int x = tail[i] & kCellMask;
-            if (set_insert(unionset, x) && w < 128) out[w++] = (uint16_t)x;
+            if (set_insert(unionset, x) && w < kMosqRoom) out[w++] = (uint16_t)x;
         }
         n = w;
     }
@@ -838,7 +868,7 @@ __device__ __forceinline__ bool touches_top_pillbug(const Pos& P, int c) {
 }
 
 __device__ __forceinline__ int type_capacity(int t) {
-    return t == PT_A ? 64 : t == PT_M ? 128 : (t == PT_S || t == PT_L) ? 32 : 6;
+    return t == PT_A ? kAntCap : t == PT_M ? kMosqRoom : (t == PT_S || t == PT_L) ? 32 : 6;
 }
 __device__ __forceinline__ int type_sets(int t) {
     return t == PT_M ? 2 : (t == PT_A || t == PT_S || t == PT_L) ? 1 : 0;
