@@ -433,42 +433,62 @@ HW_INL uint32_t nbo(const Pos& P, int c) {
     return r < 32 ? (uint32_t)P.nbd[r] : nbr_bits(P.occ, c);
 }
 
+// On-grid neighbour directions of every board cell, one byte per cell (the
+// grid6 bits), four cells per word; cells past the board have none.
+struct GridBytes {
+    uint32_t w[133];
+};
+constexpr GridBytes make_grid_bytes() {
+    GridBytes g{};
+    for (int c = 0; c < kCells; c++) {
+        int r = c / kGrid, col = c % kGrid;
+        uint32_t m = (col < 22 ? 1u : 0u) | (col < 22 && r > 0 ? 2u : 0u) | (r > 0 ? 4u : 0u) |
+                     (col > 0 ? 8u : 0u) | (col > 0 && r < 22 ? 16u : 0u) | (r < 22 ? 32u : 0u);
+        g.w[c >> 2] |= m << (8 * (c & 3));
+    }
+    return g;
+}
+static __constant__ GridBytes kGridBytes = make_grid_bytes();
+
+// bits 0-3 of x to bits 0, 8, 16, 24 (x * 0x204081 puts bit k at 7k + 8k' for
+// its four copies; bit k's copy at 8k is the only one on a byte's bit 0)
+__device__ __forceinline__ uint32_t spread4(uint32_t x) { return (x * 0x00204081u) & 0x01010101u; }
+
 // Ground-slide direction masks of the current occupancy (P.occ with zero
-// pads) for the cells of the hive's bounding box grown by one row and
-// column (every hex neighbour of an occupied cell lies in it; readers only
-// look at occupied cells and their neighbours, other entries are left
-// unwritten), and the occupied-neighbour masks of the occupied cells (nbd,
-// by rank; needs occ_pre).
+// pads) for the board rows of the hive grown by one row each way (every hex
+// neighbour of an occupied cell lies in them; readers only look at occupied
+// cells and their neighbours), and the occupied-neighbour masks of the
+// occupied cells (nbd, by rank).  A lane takes four cells c..c+3 (one word of
+// sm): their neighbours in direction d are bits k + OFS(d) of the occupancy
+// window starting at cell c - 23, spread to one byte per cell; the exit rule
+// gm & ~n & (rotl6(n) ^ rotr6(n)) then runs on the four bytes at once.
 HW_INL void build_cell_masks(Pos& P, int lane) {
     const int l = gl(lane);
+    if (l < P.n_occ) P.nbd[l] = (uint8_t)nbr_bits(P.occ, P.occ_cells[l]);
     uint32_t rowbits = l < kGrid ? (word_field(P.occ, kGrid * l) & 0x7FFFFFu) : 0u;
     uint32_t rows = grp_ballot(rowbits != 0, lane);
-    uint32_t cols = grp_or(rowbits);
     if (rows == 0) return;
     int r0 = __ffs(rows) - 1, r1 = 31 - __clz(rows);
-    int c0 = __ffs(cols) - 1, c1 = 31 - __clz(cols);
     int rlo = r0 > 0 ? r0 - 1 : 0, rhi = r1 < kGrid - 1 ? r1 + 1 : kGrid - 1;
-    int clo = c0 > 0 ? c0 - 1 : 0, chi = c1 < kGrid - 1 ? c1 + 1 : kGrid - 1;
-    int bw = chi - clo + 1, n = bw * (rhi - rlo + 1);
-    const uint32_t inv = (65536u + (uint32_t)bw - 1u) / (uint32_t)bw;  // k / bw = (k * inv) >> 16 for k < 1024
-    for (int k = l; k < n; k += kW) {
-        int rr = (int)(((uint32_t)k * inv) >> 16);
-        int row = rlo + rr, col = clo + (k - rr * bw);
-        int c = row * kGrid + col;
-        uint32_t gm = 63u;  // on-grid neighbour directions: E NE | NW | W SW | SE
-        if (col == kGrid - 1) gm &= ~3u;
-        if (col == 0) gm &= ~24u;
-        if (row == 0) gm &= ~6u;
-        if (row == kGrid - 1) gm &= ~48u;
-        uint32_t nm = nbr_bits_raw(P.occ, c) & gm;
-        P.sm[c] = (uint8_t)(gm & ~nm & (rotl6(nm) ^ rotr6(nm)));
-        if (pb_get(P.occ, c)) {
-            int r = occ_rank(P, c);
-            if (r < 32) P.nbd[r] = (uint8_t)nm;
-        }
+    const int g0 = (kGrid * rlo) >> 2, g1 = (kGrid * rhi + kGrid - 1) >> 2;
+    uint32_t* sm4 = reinterpret_cast<uint32_t*>(P.sm);
+    for (int g = g0 + l; g <= g1; g += kW) {
+        const int lo = 4 * g - 23;
+        const int wi = (lo >> 5) + 1, sh = lo & 31;
+        uint64_t win = ((uint64_t)P.occ[wi] | ((uint64_t)P.occ[wi + 1] << 32)) >> sh;
+        if (sh) win |= (uint64_t)P.occ[wi + 2] << (64 - sh);
+        const uint32_t wl = (uint32_t)win, wh = (uint32_t)(win >> 32);
+        uint32_t n = spread4((wl >> 24) & 15u) | (spread4((wl >> 1) & 15u) << 1) | (spread4(wl & 15u) << 2) |
+                     (spread4((wl >> 22) & 15u) << 3) | (spread4((wh >> 13) & 15u) << 4) |
+                     (spread4((wh >> 14) & 15u) << 5);
+        const uint32_t gm = kGridBytes.w[g];
+        n &= gm;
+        const uint32_t rl = ((n << 1) & 0x3E3E3E3Eu) | ((n >> 5) & 0x01010101u);
+        const uint32_t rr = ((n >> 1) & 0x1F1F1F1Fu) | ((n << 5) & 0x20202020u);
+        sm4[g] = gm & ~n & (rl ^ rr);
     }
 }
-
+static_assert(sizeof(((Pos*)nullptr)->sm) >= 4 * 133, "sm holds whole words up to cell 531");
 
 // Articulation points (articulation.cuh:34-168).  The reference runs one DFS
 // from the lowest occupied cell, so its result is the articulation set of
