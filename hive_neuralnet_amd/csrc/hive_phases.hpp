@@ -518,16 +518,11 @@ HW_INL void emit_list(Pos& P, const ListInfo& L, int lane, uint8_t* __restrict__
 // (the reference's has_*_move helpers, move_gen.cuh:214-1049).
 HW_INL bool has_hopper(const Pos& P, int c) {
     uint32_t m = nbo(P, c);
+    const int r0 = row_of(c), q0 = c - r0 * kGrid;
     while (m) {
         int d = __ffs(m) - 1;
         m &= m - 1;
-        int p = step(c, d);
-        bool on = true;
-        while (on && pb_get(P.occ, p)) {
-            if ((grid6(p) >> d) & 1u) p = step(p, d);
-            else on = false;
-        }
-        if (on) return true;
+        if (hop_dest(P, c, r0, q0, d) >= 0) return true;
     }
     return false;
 }
@@ -535,22 +530,20 @@ HW_INL bool has_hopper(const Pos& P, int c) {
 HW_INL bool has_spider(const Pos& P, int c) {
     const Lift lf = lift_of(P, c);
     uint32_t m1 = P.sm[c];
-    while (m1) {
+    while (m1) {  // as gen_spider: steps back masked out
         int d1 = __ffs(m1) - 1;
         m1 &= m1 - 1;
-        int p1 = step(c, d1);
-        uint32_t m2 = exits_next_to(P, p1, d1, lf);
+        int p1 = c - 23 + (int)dir_byte(kOfsHi, kOfsLo, d1);
+        uint32_t m2 = exits_next_to(P, p1, d1, lf) & ~dir_byte(kOppHi, kOppLo, d1);
         while (m2) {
             int d2 = __ffs(m2) - 1;
             m2 &= m2 - 1;
-            int p2 = step(p1, d2);
-            if (p2 == c) continue;
-            uint32_t m3 = exits_lifted(P, p2, lf);
+            int p2 = p1 - 23 + (int)dir_byte(kOfsHi, kOfsLo, d2);
+            uint32_t m3 = exits_lifted(P, p2, lf) & ~dir_byte(kOppHi, kOppLo, d2);
             while (m3) {
                 int d3 = __ffs(m3) - 1;
                 m3 &= m3 - 1;
-                int p3 = step(p2, d3);
-                if (p3 != c && p3 != p1) return true;
+                if (p2 - 23 + (int)dir_byte(kOfsHi, kOfsLo, d3) != c) return true;
             }
         }
     }

@@ -600,33 +600,6 @@ HW_INL int gen_step(const Pos& P, int c, uint16_t* out) {
     return n;
 }
 
-// gen_grasshopper_moves :228-245
-HW_INL int gen_hopper(const Pos& P, int c, uint16_t* out) {
-    int n = 0;
-    uint32_t gm = grid6(c);
-    uint32_t m = nbo(P, c);
-    for (int d = 0; d < 6; d++) {
-        if (!((m >> d) & 1u)) continue;
-        int p = step(c, d);
-        bool on = true;
-        while (on && pb_get(P.occ, p)) {
-            if ((grid6(p) >> d) & 1u) p = step(p, d);
-            else on = false;
-        }
-        if (on) out[n++] = (uint16_t)p;
-    }
-    (void)gm;
-    return n;
-}
-
-// FIFO breadth-first ant search (gen_ant_moves_with_perimeter :267-313,
-// emit_ant_moves_with_perimeter :348-388): seeds in direction order, each
-// dequeued cell expanded in direction order, ant lifted from c.  An entry
-// is the cell | arrival direction << kDirShift (readers mask with kCellMask):
-// the exit back to the parent leads to a visited cell and is skipped.
-constexpr int kDirShift = 10;
-constexpr int kCellMask = (1 << kDirShift) - 1;
-
 // Byte d of the 8-byte table {hi:lo} (one v_perm_b32; selector 0x0c = zero byte).
 __device__ __forceinline__ uint32_t dir_byte(uint32_t hi, uint32_t lo, int d) {
     return __builtin_amdgcn_perm(hi, lo, 0x0c0c0c00u | (uint32_t)d);
@@ -635,6 +608,44 @@ __device__ __forceinline__ uint32_t dir_byte(uint32_t hi, uint32_t lo, int d) {
 // direction's bit 1 << ((d + 3) % 6) (8 16 32 1 2 4)
 constexpr uint32_t kOfsLo = 24u | (1u << 8) | (0u << 16) | (22u << 24), kOfsHi = 45u | (46u << 8);
 constexpr uint32_t kOppLo = 8u | (16u << 8) | (32u << 16) | (1u << 24), kOppHi = 2u | (4u << 8);
+
+// gen_grasshopper_moves :228-245: over each occupied neighbour (directions
+// in order), along the line to the first empty cell; no move when the line
+// leaves the grid.  Row and column are stepped along (row / column deltas
+// of direction d: nibble d of kDRow / kDCol, plus one).
+constexpr uint32_t kDRow = 0x221001u, kDCol = 0x100122u;
+// landing cell of a jump from c (row r0, column q0) over its occupied
+// neighbour in direction d, or -1 when the line leaves the grid
+HW_INL int hop_dest(const Pos& P, int c, int r0, int q0, int d) {
+    const int dc = (int)dir_byte(kOfsHi, kOfsLo, d) - 23;
+    const int dr = (int)((kDRow >> (4 * d)) & 15u) - 1, dq = (int)((kDCol >> (4 * d)) & 15u) - 1;
+    int p = c + dc, r = r0 + dr, q = q0 + dq;  // occupied
+    while (pb_get(P.occ, p)) {
+        r += dr;
+        q += dq;
+        if ((unsigned)r >= (unsigned)kGrid || (unsigned)q >= (unsigned)kGrid) return -1;
+        p += dc;
+    }
+    return p;
+}
+HW_INL int gen_hopper(const Pos& P, int c, uint16_t* out) {
+    int n = 0;
+    uint32_t m = nbo(P, c);
+    const int r0 = row_of(c), q0 = c - r0 * kGrid;
+    while (m) {
+        const int d = __ffs(m) - 1;
+        m &= m - 1;
+        const int p = hop_dest(P, c, r0, q0, d);
+        if (p >= 0) out[n++] = (uint16_t)p;
+    }
+    return n;
+}
+
+// FIFO breadth-first ant search (gen_ant_moves_with_perimeter :267-313,
+// emit_ant_moves_with_perimeter :348-388): seeds in direction order, each
+// dequeued cell expanded in direction order, ant lifted from c.
+constexpr int kDirShift = 10;
+constexpr int kCellMask = (1 << kDirShift) - 1;
 
 // Slide exits of x, an empty neighbour of the lifted origin c in direction
 // d of c, from its exits s with c occupied.  Only the exits b - 1, b, b + 1
@@ -725,22 +736,23 @@ HW_INL int gen_spider(const Pos& P, int c, uint16_t* out, uint32_t* got) {
     int n = 0;
     const Lift lf = lift_of(P, c);
     uint32_t m1 = P.sm[c];
+    // the step back (p2 == c, p3 == p1) is the exit opposite the arrival
+    // direction: masked out instead of taken and skipped
     while (m1) {
         int d1 = __ffs(m1) - 1;
         m1 &= m1 - 1;
-        int p1 = step(c, d1);
-        uint32_t m2 = exits_next_to(P, p1, d1, lf);
+        int p1 = c - 23 + (int)dir_byte(kOfsHi, kOfsLo, d1);
+        uint32_t m2 = exits_next_to(P, p1, d1, lf) & ~dir_byte(kOppHi, kOppLo, d1);
         while (m2) {
             int d2 = __ffs(m2) - 1;
             m2 &= m2 - 1;
-            int p2 = step(p1, d2);
-            if (p2 == c) continue;
-            uint32_t m3 = exits_lifted(P, p2, lf);
+            int p2 = p1 - 23 + (int)dir_byte(kOfsHi, kOfsLo, d2);
+            uint32_t m3 = exits_lifted(P, p2, lf) & ~dir_byte(kOppHi, kOppLo, d2);
             while (m3) {
                 int d3 = __ffs(m3) - 1;
                 m3 &= m3 - 1;
-                int p3 = step(p2, d3);
-                if (p3 == c || p3 == p1) continue;
+                int p3 = p2 - 23 + (int)dir_byte(kOfsHi, kOfsLo, d3);
+                if (p3 == c) continue;
                 if (n < 32 && set_insert(got, p3)) out[n++] = (uint16_t)p3;
             }
         }
