@@ -142,19 +142,20 @@ def cpu_player_baseline(net, roots_np, sims, threads):
     """The reference's CPU search player (FNNNativeCPUPlayer, fnn_native_cpu_player.py:126-266)
     restated in oracle/hive_cpu_player.c: per game a serial Gumbel search of `sims`
     simulations, each leaf evaluated with full-list successor features and the fp32
-    network; one game per thread on `threads` of the timed ply's roots."""
+    network; one game per thread at a time, three games per thread from the timed
+    ply's roots (about 20 thread-seconds from the empty board)."""
     import numpy as np
     from oracle import Oracle
     orc = Oracle()
     W = {k: v.detach().float().cpu().numpy() for k, v in net.state_dict().items()}
     live = roots_np[roots_np[:, 3415] == 0]
-    sample = live[:threads]
+    sample = live[:3 * threads]
     t0 = time.perf_counter()
     _, done = orc.cpu_player_search(sample, W, sims, 16, threads=threads)
     wall = time.perf_counter() - t0
     return {
         "value": float(done.sum()) / wall, "unit": "sims/s", "cores": threads, "kind": "port",
-        "sample": f"{sample.shape[0]} of the first timed ply's roots, one game per thread, {sims} simulations "
+        "sample": f"{sample.shape[0]} of the first timed ply's roots, one game per thread at a time, {sims} simulations "
                   "each: FNNNativeCPUPlayer's serial Gumbel search (full-list successor features, fp32 network) "
                   f"restated in oracle/hive_cpu_player.c; {int(done.sum())} simulations in {wall:.2f} s",
         **host_cpus(),

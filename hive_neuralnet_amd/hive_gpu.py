@@ -638,7 +638,7 @@ def _mcts_methods():
         _dev(vl_paths, "vl_paths", torch.int32, (MAX_TREE_DEPTH,), total)
         _dev(vl_lengths, "vl_lengths", torch.int32, (), total)
         # the root children's simulations in parallel (hg_mcts_expand_backprop_dense_ws): same tree
-        ws = torch.empty((max(1, int(self._lib.hg_mcts_expand_backprop_dense_workspace(B, total))) // 4,),
+        ws = torch.empty((max(1, (int(self._lib.hg_mcts_expand_backprop_dense_workspace(B, total)) + 3) // 4),),
                          dtype=torch.int32, device="cuda")
         _check(self._lib.hg_mcts_expand_backprop_dense_ws(
             ctypes.byref(tree), *args, nn_values.data_ptr(), vl_paths.data_ptr(), vl_lengths.data_ptr(),
