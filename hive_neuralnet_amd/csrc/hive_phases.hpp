@@ -278,17 +278,23 @@ HW_INL void features_finish(Pos& P, const uint8_t* __restrict__ S, float* __rest
         if (pt) atomicAdd(&F.cnt[tc], 1);
         uint32_t nm = P.nbd[l];
         if (nm == 0) atomicAdd(&F.cnt[96 + col], 1);
-        uint32_t gm = grid6(c);
-        int oq = P.queen[col ^ 1];
+        // hex distances to both queens (hexdist, fnn_features.cuh:44-61) from c's row and column;
+        // a queen on the board is c's neighbour exactly when the distance is 1
+        const int rc = row_of(c), cc = c - rc * kGrid;
+        auto dist_to = [&](int q) {
+            const int rq = row_of(q), dq = (q - rq * kGrid) - cc, dr = rq - rc, ds = -(dq + dr);
+            return max(max(abs(dq), abs(dr)), abs(ds));
+        };
+        const int q0 = P.queen[0], q1 = P.queen[1];
+        const int d0 = q0 != 0xFFFF ? dist_to(q0) : 0, d1 = q1 != 0xFFFF ? dist_to(q1) : 0;
+        const int oq = col ? q0 : q1, dopp = col ? d0 : d1;  // the opponent's queen, queen[col ^ 1]
         if (oq != 0xFFFF && pt) {
-            if (dir_bit_to(c, oq, gm)) atomicAdd(&F.cnt[32 + tc], 1);
-            atomicAdd(&F.dsum[(pt - 1) * 2 + col], hexdist(c, oq));
+            if (oq < kCells && dopp == 1) atomicAdd(&F.cnt[32 + tc], 1);
+            atomicAdd(&F.dsum[(pt - 1) * 2 + col], dopp);
             atomicAdd(&F.dcnt[(pt - 1) * 2 + col], 1);
         }
-        for (int qc = 0; qc < 2; qc++) {
-            int q = P.queen[qc];
-            if (q != 0xFFFF && q < kCells && dir_bit_to(q, c, grid6(q))) atomicAdd(&F.ring[qc], 1);
-        }
+        if (q0 != 0xFFFF && q0 < kCells && d0 == 1) atomicAdd(&F.ring[0], 1);
+        if (q1 != 0xFFFF && q1 < kCells && d1 == 1) atomicAdd(&F.ring[1], 1);
         if (pt && pb_get(P.pin, c)) atomicAdd(&F.cnt[80 + tc], 1);  // articulation point, one piece high
         if (pt != PT_Q && h >= 2) {
             for (int lv = 0; lv < h - 1 && lv < 5; lv++) {

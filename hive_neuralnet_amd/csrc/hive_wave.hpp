@@ -133,14 +133,6 @@ __device__ __forceinline__ uint32_t dir_bit_to(int c, int g, uint32_t gm) {
     return b & gm;
 }
 
-__device__ __forceinline__ int hexdist(int a, int b) {  // fnn_features.cuh:44-61
-    int ra = row_of(a), rb = row_of(b);
-    int dq = (b - rb * kGrid) - (a - ra * kGrid), dr = rb - ra, ds = -(dq + dr);
-    int m = abs(dq);
-    m = max(m, abs(dr));
-    return max(m, abs(ds));
-}
-
 struct alignas(16) Pos {
     // pin: articulation points whose stack is one piece high
     uint32_t occ[kPW], wt[kPW], bt[kPW], pin[kPW], plc[kPW];
