@@ -422,7 +422,8 @@ def c4_leg(args):
 
 def positions_leg(args, B, mask, max_ply):
     """One configuration of batched move generation + features + action indices
-    (hg_legal_features_actions, kernel k_legal<true,true,true>) over B seeded
+    (hg_legal_features_actions_ordered: k_zero_i32, k_order_buckets, then
+    k_legal<true,true,true,true>) over B seeded
     random-play positions resident in HBM: positions/s over `steps` launches back
     to back, the kernel's mean time from HIP events, its HBM roofline, and the
     oracle on the host CPUs beside it."""
@@ -483,12 +484,13 @@ def positions_leg(args, B, mask, max_ply):
                         f"batch {B}, expansion mask {mask}, plies U[0,{max_ply}]",
             "batch": B, "expansion_mask": mask, "max_ply": max_ply, "seed": SEED,
             "mean_legal_moves": n_mean, "mean_plies": float(plies.float().mean().item()),
-            "entry_point": "hg_legal_features_actions",
+            "entry_point": "hg_legal_features_actions_ordered",
         },
         "roofline": {
             "bound": "hbm", "achieved": achieved_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": achieved_gbs / HBM_PEAK_GBS, "traffic": traffic_per_launch(name),
-            "kernel": "k_legal<true,true,true>", "mean_kernel_ms": mean_kernel_s * 1e3,
+            "kernel": "k_legal<true,true,true,true> (after k_zero_i32 + k_order_buckets: the turn order)",
+            "mean_kernel_ms": mean_kernel_s * 1e3,
             "bytes_per_position": BYTES_PER_POSITION,
         },
         "api_unfused_positions_per_s": unfused,

@@ -59,15 +59,66 @@ __device__ __forceinline__ int64_t item_of(int64_t n, bool& live) {
     return live ? i : n - 1;
 }
 
+// Processing order by turn.  A position's work grows with the pieces on the
+// board, which follow the turn; a wave pays for the longer of its two
+// positions' searches, and the launch ends with its longest waves.  So a
+// launch can take its positions in buckets of 4 turns, latest turns first:
+// k_order_buckets appends each position's index to the list of its bucket
+// (lists[b * B ...], counts[b]; counts zeroed before), and k_legal<..,
+// true> maps its item s to the s-th index of the concatenated lists.
+// Outputs are written at each position's own row, so the order changes no
+// result.
+constexpr int kOrderBuckets = 32, kOrderShift = 2;  // buckets of 4 turns, turn >= 124 in the last
+__global__ void k_zero_i32(int32_t* __restrict__ p, int64_t count) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < count) p[i] = 0;
+}
+__global__ __launch_bounds__(256) void k_order_buckets(const uint8_t* __restrict__ states, int64_t B,
+                                                       int32_t* __restrict__ counts, int32_t* __restrict__ lists) {
+    __shared__ int cnt[kOrderBuckets], base[kOrderBuckets];
+    if (threadIdx.x < kOrderBuckets) cnt[threadIdx.x] = 0;
+    __syncthreads();
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    int b = -1, r = 0;
+    if (i < B) {
+        const int turn = *reinterpret_cast<const uint16_t*>(states + i * kStateBytes + OFF_TURN);
+        b = min(turn >> kOrderShift, kOrderBuckets - 1);
+        r = atomicAdd(&cnt[b], 1);
+    }
+    __syncthreads();
+    if (threadIdx.x < kOrderBuckets)
+        base[threadIdx.x] = cnt[threadIdx.x] ? atomicAdd(&counts[threadIdx.x], cnt[threadIdx.x]) : 0;
+    __syncthreads();
+    if (b >= 0) lists[(int64_t)b * B + base[b] + r] = (int32_t)i;
+}
+
+// item s of the ordered launch (buckets from the latest turns down): lane
+// k < 32 of the group holds the count of bucket 31 - k and its exclusive
+// prefix; the item's bucket is the last one whose prefix is <= s
+__device__ __forceinline__ int64_t ordered_item(int64_t s, const int32_t* __restrict__ counts,
+                                                const int32_t* __restrict__ lists, int64_t B, int lane) {
+    static_assert(kOrderBuckets == kW, "one bucket per lane of the group");
+    const int k = gl(lane);
+    const int c = counts[kOrderBuckets - 1 - k];
+    const int excl = grp_excl_scan(c);
+    const uint32_t le = grp_ballot(excl <= s, lane);
+    const int j = 31 - __clz(le);  // prefixes are non-decreasing: the highest lane with excl <= s
+    const int start = grp_shfl(excl, j, lane);
+    return lists[(int64_t)(kOrderBuckets - 1 - j) * B + (s - start)];
+}
+
 // 6 waves per SIMD: the register cap (80 VGPRs, a few bytes of spill) pays
 // for itself, the kernel is bound by issue and latency, not by registers
-template <bool WithMoves, bool WithFeat, bool WithAct>
+template <bool WithMoves, bool WithFeat, bool WithAct, bool Ordered = false>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(6))) void k_legal(const uint8_t* __restrict__ states, int64_t B,
                                               uint8_t* __restrict__ moves_out, int32_t* __restrict__ n_out,
-                                              float* __restrict__ feat_out, int32_t* __restrict__ act_out) {
+                                              float* __restrict__ feat_out, int32_t* __restrict__ act_out,
+                                              const int32_t* __restrict__ counts = nullptr,
+                                              const int32_t* __restrict__ lists = nullptr) {
     __shared__ Pos PS[kPosPerWave];
     bool live;
-    const int64_t pos = item_of(B, live);
+    int64_t pos = item_of(B, live);
+    if (Ordered) pos = ordered_item(pos, counts, lists, B, threadIdx.x);
     run_legal<WithMoves, WithFeat, WithAct>(PS[threadIdx.x >> 5], states + pos * kStateBytes, threadIdx.x,
                                             live ? moves_out + pos * (kMaxLegal * 6) : nullptr,
                                             live ? n_out + pos : nullptr,
@@ -351,6 +402,24 @@ int hg_legal_features_actions(const uint8_t* states, int64_t B, uint8_t* moves, 
     if (B <= 0) return 0;
     hipLaunchKernelGGL((k_legal<true, true, true>), dim3((unsigned)grid_for(B, kPosPerWave)), dim3(64), 0, (hipStream_t)stream, states, B,
                        moves, num_legal, features, actions);
+    return finish();
+}
+
+int64_t hg_legal_features_actions_ordered_workspace(int64_t B) {
+    return B <= 0 ? 0 : (int64_t)sizeof(int32_t) * (kOrderBuckets + kOrderBuckets * B);
+}
+
+int hg_legal_features_actions_ordered(const uint8_t* states, int64_t B, uint8_t* moves, int32_t* num_legal,
+                                      float* features, int32_t* actions, void* workspace, void* stream) {
+    if (B <= 0) return 0;
+    if (!workspace) return (int)hipErrorInvalidValue;
+    hipStream_t s = (hipStream_t)stream;
+    int32_t* counts = reinterpret_cast<int32_t*>(workspace);
+    int32_t* lists = counts + kOrderBuckets;
+    hipLaunchKernelGGL(k_zero_i32, dim3(1), dim3(64), 0, s, counts, (int64_t)kOrderBuckets);
+    hipLaunchKernelGGL(k_order_buckets, dim3((unsigned)grid_for(B, 256)), dim3(256), 0, s, states, B, counts, lists);
+    hipLaunchKernelGGL((k_legal<true, true, true, true>), dim3((unsigned)grid_for(B, kPosPerWave)), dim3(64), 0, s,
+                       states, B, moves, num_legal, features, actions, counts, lists);
     return finish();
 }
 

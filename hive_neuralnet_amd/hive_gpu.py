@@ -63,6 +63,8 @@ _SIGS = {
     "hg_generate_legal_moves": [_c_void_p, _c_i64, _c_void_p, _c_void_p, _c_void_p],
     "hg_generate_legal_moves_and_fnn_features": [_c_void_p, _c_i64, _c_void_p, _c_void_p, _c_void_p, _c_void_p],
     "hg_legal_features_actions": [_c_void_p, _c_i64, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p],
+    "hg_legal_features_actions_ordered": [_c_void_p, _c_i64, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+                                          _c_void_p],
     "hg_extract_fnn_features": [_c_void_p, _c_void_p, _c_void_p, _c_i64, _c_void_p, _c_void_p],
     "hg_legal_moves_to_actions": [_c_void_p, _c_void_p, _c_void_p, _c_i64, _c_void_p, _c_void_p],
     "hg_compute_centroids": [_c_void_p, _c_i64, _c_void_p, _c_void_p],
@@ -121,6 +123,7 @@ _SIGS_I64 = {  # entry points returning a size (int64_t)
     "hg_successor_rows_workspace": [_c_i64],
     "hg_fnn_leaf_eval_lists_workspace": [_c_i64, _c_int],
     "hg_mcts_expand_backprop_dense_workspace": [_c_i64, _c_i64],
+    "hg_legal_features_actions_ordered_workspace": [_c_i64],
 }
 
 
@@ -285,17 +288,29 @@ class HiveGpuExtension:
             "generate_legal_moves_and_fnn_features_batch")
         return moves, n, feat
 
-    def generate_legal_moves_features_actions_batch(self, states: torch.Tensor, batch_size: int):
-        """Fused: (moves, num_legal, features, action_indices) in one pass."""
+    def generate_legal_moves_features_actions_batch(self, states: torch.Tensor, batch_size: int,
+                                                    ordered: bool = True):
+        """Fused: (moves, num_legal, features, action_indices) in one pass.  With
+        `ordered` (default) the positions are taken in buckets of turns, latest
+        first (hg_legal_features_actions_ordered; an int32 workspace is
+        allocated per call): the same outputs, a shorter launch on batches of
+        mixed game stages."""
         B = int(batch_size)
         states = _state_rows(states, B)
         moves = torch.empty((B, MAX_LEGAL_MOVES, SIZEOF_GPU_MOVE), dtype=torch.uint8, device="cuda")
         n = torch.empty((B,), dtype=torch.int32, device="cuda")
         feat = torch.empty((B, FNN_FEAT_DIM), dtype=torch.float32, device="cuda")
         act = torch.empty((B, MAX_LEGAL_MOVES), dtype=torch.int32, device="cuda")
-        _check(self._lib.hg_legal_features_actions(
-            states.data_ptr(), B, moves.data_ptr(), n.data_ptr(), feat.data_ptr(), act.data_ptr(), _stream()),
-            "generate_legal_moves_features_actions_batch")
+        if ordered and B > 0:
+            ws = torch.empty((int(self._lib.hg_legal_features_actions_ordered_workspace(B)) // 4,),
+                             dtype=torch.int32, device="cuda")
+            _check(self._lib.hg_legal_features_actions_ordered(
+                states.data_ptr(), B, moves.data_ptr(), n.data_ptr(), feat.data_ptr(), act.data_ptr(),
+                ws.data_ptr(), _stream()), "generate_legal_moves_features_actions_batch")
+        else:
+            _check(self._lib.hg_legal_features_actions(
+                states.data_ptr(), B, moves.data_ptr(), n.data_ptr(), feat.data_ptr(), act.data_ptr(), _stream()),
+                "generate_legal_moves_features_actions_batch")
         return moves, n, feat, act
 
     def extract_fnn_features_batch(self, states, legal_moves, num_legal, batch_size: int) -> torch.Tensor:

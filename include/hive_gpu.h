@@ -70,6 +70,16 @@ int hg_generate_legal_moves_and_fnn_features(const uint8_t* states, int64_t B, u
 int hg_legal_features_actions(const uint8_t* states, int64_t B, uint8_t* moves, int32_t* num_legal,
                               float* features, int32_t* actions, void* stream);
 
+/* hg_legal_features_actions taking the positions in buckets of 4 turns,
+ * latest first (a wave's cost is its longer position; the launch ends with
+ * its longest waves): identical outputs.  workspace:
+ * hg_legal_features_actions_ordered_workspace(B) bytes, 4-byte aligned
+ * (bucket counts, then one index list per bucket).  No reference
+ * counterpart (same outputs as the entry above). */
+int64_t hg_legal_features_actions_ordered_workspace(int64_t B);
+int hg_legal_features_actions_ordered(const uint8_t* states, int64_t B, uint8_t* moves, int32_t* num_legal,
+                                      float* features, int32_t* actions, void* workspace, void* stream);
+
 /* extract_fnn_features_batch -- game_logic.cu:1409-1431.
  * features for caller-supplied lists (num_legal clamped to [0, 256]). */
 int hg_extract_fnn_features(const uint8_t* states, const uint8_t* moves, const int32_t* num_legal, int64_t B,

@@ -68,12 +68,13 @@ def test_golden_moves_features(ext, name):
     assert feat3.shape == (B, 122)
 
 
+@pytest.mark.parametrize("ordered", [True, False], ids=["turn-order", "index-order"])
 @pytest.mark.parametrize("B", [1, 2, 3, 5, 7, 130])
-def test_small_batches(ext, B):
+def test_small_batches(ext, B, ordered):
     """Small and odd batch sizes, fused entry point against the golden lists."""
     g = load_golden("c3")
     st = _cuda(g["states"][1:B + 1])
-    moves, n, feat, act = ext.generate_legal_moves_features_actions_batch(st, B)
+    moves, n, feat, act = ext.generate_legal_moves_features_actions_batch(st, B, ordered=ordered)
     assert np.array_equal(n.cpu().numpy(), g["n"][1:B + 1])
     assert np.array_equal(moves.cpu().numpy(), g["moves"][1:B + 1])
     assert np.array_equal(_bits(feat.cpu().numpy()), _bits(g["features"][1:B + 1]))
@@ -116,6 +117,10 @@ def test_full_size_parity(ext, oracle, cfg):
     assert np.array_equal(act.cpu().numpy(), oa)
     act2 = ext.legal_moves_to_actions_batch(st, moves, n, B)
     assert np.array_equal(act2.cpu().numpy(), oa)
+    # the launch in index order (hg_legal_features_actions) writes the same bytes
+    plain = ext.generate_legal_moves_features_actions_batch(st, B, ordered=False)
+    for a, b in zip((moves, n, feat, act), plain):
+        assert torch.equal(a, b)
     cen = ext.compute_centroids_batch(st, B).cpu().numpy()
     for i in range(0, B, 997):
         assert tuple(cen[i]) == oracle.centroid(states[i])
