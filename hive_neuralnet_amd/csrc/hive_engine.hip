@@ -64,19 +64,19 @@ __device__ __forceinline__ int64_t item_of(int64_t n, bool& live) {
 // positions' searches, and the launch ends with its longest waves.  So a
 // launch can take its positions in buckets of 4 turns, latest turns first:
 // k_order_buckets appends each position's index to the list of its bucket
-// (lists[b * B ...], counts[b]; counts zeroed before), and k_legal<..,
-// true> maps its item s to the s-th index of the concatenated lists.
-// Outputs are written at each position's own row, so the order changes no
-// result.
+// (lists[b * B ...], counts[b]), and k_legal<.., true> maps its item s to
+// the s-th index of the concatenated lists.  Outputs are written at each
+// position's own row, so the order changes no result.  The workspace holds
+// two count arrays used in turn: a call counts into the one that is zero
+// and clears the other (the previous call's, whose readers have finished
+// on the same stream), so no launch is spent clearing.
 constexpr int kOrderBuckets = 32, kOrderShift = 2;  // buckets of 4 turns, turn >= 124 in the last
-__global__ void k_zero_i32(int32_t* __restrict__ p, int64_t count) {
-    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < count) p[i] = 0;
-}
 __global__ __launch_bounds__(256) void k_order_buckets(const uint8_t* __restrict__ states, int64_t B,
-                                                       int32_t* __restrict__ counts, int32_t* __restrict__ lists) {
+                                                       int32_t* __restrict__ counts, int32_t* __restrict__ clear,
+                                                       int32_t* __restrict__ lists) {
     __shared__ int cnt[kOrderBuckets], base[kOrderBuckets];
     if (threadIdx.x < kOrderBuckets) cnt[threadIdx.x] = 0;
+    if (blockIdx.x == 0 && threadIdx.x < kOrderBuckets) clear[threadIdx.x] = 0;
     __syncthreads();
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
     int b = -1, r = 0;
@@ -89,7 +89,7 @@ __global__ __launch_bounds__(256) void k_order_buckets(const uint8_t* __restrict
     if (threadIdx.x < kOrderBuckets)
         base[threadIdx.x] = cnt[threadIdx.x] ? atomicAdd(&counts[threadIdx.x], cnt[threadIdx.x]) : 0;
     __syncthreads();
-    if (b >= 0) lists[(int64_t)b * B + base[b] + r] = (int32_t)i;
+    if (b >= 0 && base[b] + r < B) lists[(int64_t)b * B + base[b] + r] = (int32_t)i;
 }
 
 // item s of the ordered launch (buckets from the latest turns down): lane
@@ -104,7 +104,8 @@ __device__ __forceinline__ int64_t ordered_item(int64_t s, const int32_t* __rest
     const uint32_t le = grp_ballot(excl <= s, lane);
     const int j = 31 - __clz(le);  // prefixes are non-decreasing: the highest lane with excl <= s
     const int start = grp_shfl(excl, j, lane);
-    return lists[(int64_t)(kOrderBuckets - 1 - j) * B + (s - start)];
+    const int64_t off = s - start;  // in [0, B) for counts that sum to B
+    return lists[(int64_t)(kOrderBuckets - 1 - j) * B + (off < 0 ? 0 : (off < B ? off : B - 1))];
 }
 
 // 6 waves per SIMD: the register cap (80 VGPRs, a few bytes of spill) pays
@@ -118,7 +119,10 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(6))) void k_
     __shared__ Pos PS[kPosPerWave];
     bool live;
     int64_t pos = item_of(B, live);
-    if (Ordered) pos = ordered_item(pos, counts, lists, B, threadIdx.x);
+    if (Ordered) {  // kept inside the batch even for a workspace used against its contract
+        pos = ordered_item(pos, counts, lists, B, threadIdx.x);
+        pos = pos < 0 ? 0 : (pos >= B ? B - 1 : pos);
+    }
     run_legal<WithMoves, WithFeat, WithAct>(PS[threadIdx.x >> 5], states + pos * kStateBytes, threadIdx.x,
                                             live ? moves_out + pos * (kMaxLegal * 6) : nullptr,
                                             live ? n_out + pos : nullptr,
@@ -406,18 +410,20 @@ int hg_legal_features_actions(const uint8_t* states, int64_t B, uint8_t* moves, 
 }
 
 int64_t hg_legal_features_actions_ordered_workspace(int64_t B) {
-    return B <= 0 ? 0 : (int64_t)sizeof(int32_t) * (kOrderBuckets + kOrderBuckets * B);
+    return B <= 0 ? 0 : (int64_t)sizeof(int32_t) * (2 * kOrderBuckets + kOrderBuckets * B);
 }
 
 int hg_legal_features_actions_ordered(const uint8_t* states, int64_t B, uint8_t* moves, int32_t* num_legal,
-                                      float* features, int32_t* actions, void* workspace, void* stream) {
+                                      float* features, int32_t* actions, void* workspace, int parity,
+                                      void* stream) {
     if (B <= 0) return 0;
-    if (!workspace) return (int)hipErrorInvalidValue;
+    if (!workspace || (parity & ~1)) return (int)hipErrorInvalidValue;
     hipStream_t s = (hipStream_t)stream;
-    int32_t* counts = reinterpret_cast<int32_t*>(workspace);
-    int32_t* lists = counts + kOrderBuckets;
-    hipLaunchKernelGGL(k_zero_i32, dim3(1), dim3(64), 0, s, counts, (int64_t)kOrderBuckets);
-    hipLaunchKernelGGL(k_order_buckets, dim3((unsigned)grid_for(B, 256)), dim3(256), 0, s, states, B, counts, lists);
+    int32_t* counts = reinterpret_cast<int32_t*>(workspace) + parity * kOrderBuckets;
+    int32_t* clear = reinterpret_cast<int32_t*>(workspace) + (parity ^ 1) * kOrderBuckets;
+    int32_t* lists = reinterpret_cast<int32_t*>(workspace) + 2 * kOrderBuckets;
+    hipLaunchKernelGGL(k_order_buckets, dim3((unsigned)grid_for(B, 256)), dim3(256), 0, s, states, B, counts, clear,
+                       lists);
     hipLaunchKernelGGL((k_legal<true, true, true, true>), dim3((unsigned)grid_for(B, kPosPerWave)), dim3(64), 0, s,
                        states, B, moves, num_legal, features, actions, counts, lists);
     return finish();

@@ -180,11 +180,14 @@ __device__ __forceinline__ int select_bit(uint32_t x, int r) {
 
 // Slot i (i < L.n, L.total > 0) of the generated list as (type | pt << 8, from, to).
 HW_INL void list_slot(const Pos& P, const ListInfo& L, int i, int& tp, int& from, int& to, int& seg) {
-    int lo = 0, hi = L.nseg - 1;  // last segment starting at or before i
-    while (lo < hi) {
-        int mid = (lo + hi + 1) >> 1;
-        if (P.seg_base[mid] <= i) lo = mid;
-        else hi = mid - 1;
+    // last segment starting at or before i: five fixed halving steps over
+    // the non-decreasing starts (nseg <= 19 < 32)
+    static_assert(kSegs <= 32, "five steps cover the segments");
+    int lo = 0;
+#pragma unroll
+    for (int step = 16; step > 0; step >>= 1) {
+        const int mid = lo + step;
+        if (mid < L.nseg && P.seg_base[mid] <= i) lo = mid;
     }
     seg = lo;
     int k = i - P.seg_base[lo];

@@ -64,7 +64,7 @@ _SIGS = {
     "hg_generate_legal_moves_and_fnn_features": [_c_void_p, _c_i64, _c_void_p, _c_void_p, _c_void_p, _c_void_p],
     "hg_legal_features_actions": [_c_void_p, _c_i64, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p],
     "hg_legal_features_actions_ordered": [_c_void_p, _c_i64, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
-                                          _c_void_p],
+                                          _c_int, _c_void_p],
     "hg_extract_fnn_features": [_c_void_p, _c_void_p, _c_void_p, _c_i64, _c_void_p, _c_void_p],
     "hg_legal_moves_to_actions": [_c_void_p, _c_void_p, _c_void_p, _c_i64, _c_void_p, _c_void_p],
     "hg_compute_centroids": [_c_void_p, _c_i64, _c_void_p, _c_void_p],
@@ -239,6 +239,10 @@ class HiveGpuExtension:
 
     def __init__(self, lib: ctypes.CDLL):
         self._lib = lib
+        # turn-ordered legal lists: per (device, stream) a zero-filled workspace
+        # kept across calls and the parity of its next call
+        self._order_ws = {}
+        self._order_lock = threading.Lock()
         for k, v in globals().items():
             if k.isupper() and isinstance(v, int):
                 setattr(self, k, v)
@@ -302,11 +306,20 @@ class HiveGpuExtension:
         feat = torch.empty((B, FNN_FEAT_DIM), dtype=torch.float32, device="cuda")
         act = torch.empty((B, MAX_LEGAL_MOVES), dtype=torch.int32, device="cuda")
         if ordered and B > 0:
-            ws = torch.empty((int(self._lib.hg_legal_features_actions_ordered_workspace(B)) // 4,),
-                             dtype=torch.int32, device="cuda")
+            stream = _stream()
+            key = (torch.cuda.current_device(), stream)
+            need = int(self._lib.hg_legal_features_actions_ordered_workspace(B)) // 4
+            with self._order_lock:
+                ws, parity = self._order_ws.get(key, (None, 0))
+                if ws is None or ws.numel() < need:
+                    ws, parity = torch.zeros((need,), dtype=torch.int32, device="cuda"), 0
+                # dropped while the call is in flight, so a failed call leaves no half-used workspace
+                self._order_ws.pop(key, None)
             _check(self._lib.hg_legal_features_actions_ordered(
                 states.data_ptr(), B, moves.data_ptr(), n.data_ptr(), feat.data_ptr(), act.data_ptr(),
-                ws.data_ptr(), _stream()), "generate_legal_moves_features_actions_batch")
+                ws.data_ptr(), parity, stream), "generate_legal_moves_features_actions_batch")
+            with self._order_lock:
+                self._order_ws[key] = (ws, parity ^ 1)
         else:
             _check(self._lib.hg_legal_features_actions(
                 states.data_ptr(), B, moves.data_ptr(), n.data_ptr(), feat.data_ptr(), act.data_ptr(), _stream()),

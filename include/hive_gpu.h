@@ -73,12 +73,16 @@ int hg_legal_features_actions(const uint8_t* states, int64_t B, uint8_t* moves, 
 /* hg_legal_features_actions taking the positions in buckets of 4 turns,
  * latest first (a wave's cost is its longer position; the launch ends with
  * its longest waves): identical outputs.  workspace:
- * hg_legal_features_actions_ordered_workspace(B) bytes, 4-byte aligned
- * (bucket counts, then one index list per bucket).  No reference
- * counterpart (same outputs as the entry above). */
+ * hg_legal_features_actions_ordered_workspace(B) bytes, 4-byte aligned: two
+ * arrays of 32 bucket counts, then one index list per bucket.  A call needs
+ * counts[parity] zero, uses it and clears counts[parity ^ 1]: zero-fill a new
+ * workspace once, then alternate parity (0, 1, 0, ...) on calls that use it
+ * on one stream.  No reference counterpart (same outputs as the entry
+ * above). */
 int64_t hg_legal_features_actions_ordered_workspace(int64_t B);
 int hg_legal_features_actions_ordered(const uint8_t* states, int64_t B, uint8_t* moves, int32_t* num_legal,
-                                      float* features, int32_t* actions, void* workspace, void* stream);
+                                      float* features, int32_t* actions, void* workspace, int parity,
+                                      void* stream);
 
 /* extract_fnn_features_batch -- game_logic.cu:1409-1431.
  * features for caller-supplied lists (num_legal clamped to [0, 256]). */

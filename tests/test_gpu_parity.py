@@ -82,6 +82,39 @@ def test_small_batches(ext, B, ordered):
     assert torch.equal(act, act2)
 
 
+def test_turn_order_workspace_reuse(ext, oracle):
+    """hg_legal_features_actions_ordered on one zero-filled workspace across
+    calls of alternating parity (each call counts into one array and clears
+    the other), with batches that shrink and grow: every call matches the
+    index-order launch; a parity other than 0 / 1 is refused."""
+    import ctypes
+    lib = ext._lib
+    states, _ = _oracle_positions(oracle, 4096, 7, 150, seed=0xACE)
+    st = _cuda(states)
+    ws = torch.zeros((int(lib.hg_legal_features_actions_ordered_workspace(4096)) // 4,), dtype=torch.int32,
+                     device="cuda")
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    for k, B in enumerate((4096, 1000, 4096, 3, 2048)):
+        moves = torch.empty((B, 256, 6), dtype=torch.uint8, device="cuda")
+        n = torch.empty((B,), dtype=torch.int32, device="cuda")
+        feat = torch.empty((B, 122), dtype=torch.float32, device="cuda")
+        act = torch.empty((B, 256), dtype=torch.int32, device="cuda")
+        rc = lib.hg_legal_features_actions_ordered(st.data_ptr(), B, moves.data_ptr(), n.data_ptr(), feat.data_ptr(),
+                                                   act.data_ptr(), ws.data_ptr(), k & 1, stream)
+        assert rc == 0
+        plain = ext.generate_legal_moves_features_actions_batch(st[:B], B, ordered=False)
+        for a, b in zip((moves, n, feat, act), plain):
+            assert torch.equal(a, b), (k, B)
+    assert lib.hg_legal_features_actions_ordered(st.data_ptr(), 3, moves.data_ptr(), n.data_ptr(), feat.data_ptr(),
+                                                 act.data_ptr(), ws.data_ptr(), 2, stream) != 0
+    # the Python entry keeps its own workspace per (device, stream) across calls
+    for B in (4096, 17, 4096):
+        out = ext.generate_legal_moves_features_actions_batch(st[:B], B)
+        plain = ext.generate_legal_moves_features_actions_batch(st[:B], B, ordered=False)
+        for a, b in zip(out, plain):
+            assert torch.equal(a, b), B
+
+
 @pytest.mark.parametrize("name", ["c1", "c2", "c3"])
 def test_golden_successors_queen_escape_apply(ext, name):
     g = load_golden(name)
