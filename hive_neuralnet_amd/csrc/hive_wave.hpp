@@ -496,7 +496,7 @@ HW_INL void articulation(Pos& P, int lane) {
     if (l < 20) P.pin[l] = 0;
     if (l < N) {
         int c = P.occ_cells[l];
-        uint32_t nm = nbr_bits(P.occ, c);
+        uint32_t nm = P.nbd[l];  // occupied on-grid neighbours, written by this lane in build_cell_masks
         uint32_t a = 0;
         while (nm) {
             int d = __ffs(nm) - 1;
@@ -519,12 +519,16 @@ HW_INL void articulation(Pos& P, int lane) {
     }
     uint32_t reach = 0;
     if (l < N || l == kW - 1) {
+        // the flood's result is a set: frontier vertices are taken two at a
+        // time (the second read repeats the first when only one is left)
         reach = start;
         uint32_t frontier = start;
         while (frontier) {
-            int i = __ffs(frontier) - 1;
+            const int i1 = __ffs(frontier) - 1;
             frontier &= frontier - 1;
-            uint32_t nb = P.u1.adj[i] & ~reach & ~vbit;
+            const int i2 = frontier ? __ffs(frontier) - 1 : i1;
+            frontier &= frontier - 1;
+            const uint32_t nb = (P.u1.adj[i1] | P.u1.adj[i2]) & ~reach & ~vbit;
             reach |= nb;
             frontier |= nb;
         }
