@@ -697,33 +697,37 @@ HW_INL int gen_ant(const Pos& P, int c, uint16_t* out, int cap, uint32_t* seen) 
     set_clear(seen);
     set_insert(seen, c);
     const Lift lf = lift_of(P, c);
-    int head = 0, tail = 0;
+    // queue by pointers: q = next free entry, h = next entry to expand
+    uint16_t* q = out;
+    const uint16_t* h = out;
+    uint16_t* const end = out + cap;
+    uint16_t* const roomy = out + (cap - 6);  // q <= roomy: every exit of a cell fits
     int cur = c;
     uint32_t back = 0;
     for (;;) {
         uint32_t m = exits_lifted(P, cur, lf) & ~back;
         const int base = cur - 23;
-        if (tail + 6 <= cap) {  // room for every exit
+        if (q <= roomy) {
             while (m) {
-                int d = __ffs(m) - 1;
+                const int d = __ffs(m) - 1;
                 m &= m - 1;
-                int dest = base + (int)dir_byte(kOfsHi, kOfsLo, d);
-                if (set_insert(seen, dest)) out[tail++] = (uint16_t)(dest | (dir_byte(kOppHi, kOppLo, d) << kDirShift));
+                const int dest = base + (int)dir_byte(kOfsHi, kOfsLo, d);
+                if (set_insert(seen, dest)) *q++ = (uint16_t)(dest | (dir_byte(kOppHi, kOppLo, d) << kDirShift));
             }
         } else {
-            while (m && tail < cap) {
-                int d = __ffs(m) - 1;
+            while (m && q < end) {
+                const int d = __ffs(m) - 1;
                 m &= m - 1;
-                int dest = base + (int)dir_byte(kOfsHi, kOfsLo, d);
-                if (set_insert(seen, dest)) out[tail++] = (uint16_t)(dest | (dir_byte(kOppHi, kOppLo, d) << kDirShift));
+                const int dest = base + (int)dir_byte(kOfsHi, kOfsLo, d);
+                if (set_insert(seen, dest)) *q++ = (uint16_t)(dest | (dir_byte(kOppHi, kOppLo, d) << kDirShift));
             }
         }
-        if (head >= tail || tail >= cap) break;
-        const uint32_t e = out[head++];
+        if (h >= q || q >= end) break;
+        const uint32_t e = *h++;
         cur = (int)(e & kCellMask);
         back = e >> kDirShift;
     }
-    return tail;
+    return (int)(q - out);
 }
 
 // gen_spider_moves :397-431 (first occurrence over d1,d2,d3; at most 32)
