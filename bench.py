@@ -66,7 +66,9 @@ def parse_args():
     ap.add_argument("--mcts-warmup", type=int, default=1, help="untimed self-play plies before timing")
     ap.add_argument("--mcts-roots", choices=("empty", "midgame"), default="empty")
     ap.add_argument("--graphs", choices=("auto", "on", "off"), default="auto",
-                    help="C5 simulation waves from HIP graphs: auto = waves under 8,192 rows")
+                    help="C5 simulation waves from HIP graphs: auto = waves under 2,048 rows")
+    ap.add_argument("--native-waves", choices=("on", "off"), default="on",
+                    help="C5 simulation waves as one library call each (on) or through the step entry points")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 256 MiB device-to-device copy 3 times (rocprof counter calibration)")
     return ap.parse_args()
@@ -229,6 +231,7 @@ def mcts_leg(args):
     orch = FNNMCTSOrchestrator(net, cfg)
     orch.use_graphs = {"auto": None, "on": True, "off": False}[args.graphs]
     orch.game_parts = args.game_parts
+    orch.native_waves = args.native_waves == "on"
     ext = orch.ext
     if args.mcts_roots == "empty":
         states = ext.create_initial_states(G, 0)

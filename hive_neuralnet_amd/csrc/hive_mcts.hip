@@ -426,11 +426,13 @@ __global__ __launch_bounds__(64) void k_select_mask(Tree T, const int8_t* __rest
 }
 
 // mcts_replay_kernel (mcts_tree.cuh:298-320): leaf = root + path moves.  One
-// wave per simulation; the row is assembled in LDS and written once.
+// wave per simulation; the row is assembled in LDS and written once.  With
+// `results`, also the leaf's stored result byte (the check_results_kernel
+// pass of game_logic.cu:1239-1241 over the replayed rows; 0 for a zero row).
 __global__ __launch_bounds__(64) void k_replay(const uint8_t* __restrict__ roots, int64_t B,
                                                uint8_t* __restrict__ leaves, const uint8_t* __restrict__ paths,
                                                const int32_t* __restrict__ plen, const int32_t* __restrict__ leaf_idx,
-                                               int64_t total, int zero_idle) {
+                                               int64_t total, int zero_idle, int32_t* __restrict__ results) {
     __shared__ uint4 row[kStateBytes / 16];
     const int64_t sim = blockIdx.x;
     const int lane = threadIdx.x;
@@ -440,6 +442,7 @@ __global__ __launch_bounds__(64) void k_replay(const uint8_t* __restrict__ roots
             uint4* dst = reinterpret_cast<uint4*>(leaves + sim * kStateBytes);
             const uint4 z = make_uint4(0u, 0u, 0u, 0u);
             for (int i = lane; i < kStateBytes / 16; i += 64) dst[i] = z;
+            if (results && lane == 0) results[sim] = 0;
         }
         return;
     }
@@ -455,6 +458,7 @@ __global__ __launch_bounds__(64) void k_replay(const uint8_t* __restrict__ roots
     __syncthreads();
     uint4* dst = reinterpret_cast<uint4*>(leaves + sim * kStateBytes);
     for (int i = lane; i < kStateBytes / 16; i += 64) dst[i] = row[i];
+    if (results && lane == 0) results[sim] = reinterpret_cast<const uint8_t*>(row)[OFF_RESULT];
 }
 
 // centroid of a state row (compute_centroid, state_encoder.cuh:889-906)
@@ -1344,7 +1348,7 @@ int hg_mcts_replay(const uint8_t* root_states, int64_t B, uint8_t* leaf_states, 
                    const int32_t* path_lens, const int32_t* leaf_idx, int64_t total, void* stream) {
     if (B <= 0 || total <= 0) return 0;
     hipLaunchKernelGGL(k_replay, dim3((unsigned)total), dim3(64), 0, (hipStream_t)stream, root_states, B,
-                       leaf_states, move_paths, path_lens, leaf_idx, total, 0);
+                       leaf_states, move_paths, path_lens, leaf_idx, total, 0, nullptr);
     return finish();
 }
 
@@ -1352,7 +1356,7 @@ int hg_mcts_replay_fill(const uint8_t* root_states, int64_t B, uint8_t* leaf_sta
                         const int32_t* path_lens, const int32_t* leaf_idx, int64_t total, void* stream) {
     if (B <= 0 || total <= 0) return 0;
     hipLaunchKernelGGL(k_replay, dim3((unsigned)total), dim3(64), 0, (hipStream_t)stream, root_states, B,
-                       leaf_states, move_paths, path_lens, leaf_idx, total, 1);
+                       leaf_states, move_paths, path_lens, leaf_idx, total, 1, nullptr);
     return finish();
 }
 
@@ -1460,6 +1464,40 @@ int hg_mcts_root_noise(const hg_tree* tree, const float* noise, const int32_t* r
     hipLaunchKernelGGL(k_root_noise, dim3((unsigned)((B + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
                        to_tree(tree), noise, root_nodes, max_children_pad, dir_eps, root_policy_temp, B);
     return finish();
+}
+
+int hg_mcts_wave_root_slots(const hg_tree* tree, const uint8_t* root_states, const int8_t* game_active,
+                            const int32_t* root_nodes, const int32_t* root_slots, int num_candidates,
+                            int max_root_children, float c_puct, int64_t B, int W, int deterministic_non_root,
+                            float non_root_sigma, float q_penalty, const hg_fnn_net* net,
+                            const hg_wave_buffers* buf, void* stream) {
+    if (B <= 0 || W <= 0 || num_candidates <= 0) return 0;
+    if (!tree || !net || !buf || net->F != 122) return (int)hipErrorInvalidValue;
+    const int64_t T = (int64_t)W * num_candidates * B;
+    if (T > buf->capacity || T > (int64_t)INT32_MAX) return (int)hipErrorInvalidValue;
+    hipStream_t s = (hipStream_t)stream;
+    int e = hg_mcts_select_root_slots(tree, game_active, root_nodes, root_slots, num_candidates, max_root_children,
+                                      c_puct, B, W, deterministic_non_root, non_root_sigma, q_penalty, buf->leaf_idx,
+                                      buf->move_paths, buf->path_lens, buf->vl_paths, buf->vl_lens, stream);
+    if (e) return e;
+    // replay into the leaf rows (idle simulations: zero rows) with each leaf's result
+    hipLaunchKernelGGL(k_replay, dim3((unsigned)T), dim3(64), 0, s, root_states, B, buf->leaf_states,
+                       buf->move_paths, buf->path_lens, buf->leaf_idx, T, 1, buf->results);
+    if ((e = finish())) return e;
+    if ((e = hg_generate_legal_moves_and_fnn_features(buf->leaf_states, T, buf->legal_moves, buf->num_legal,
+                                                      buf->features, stream)))
+        return e;
+    if ((e = hg_fnn_leaf_eval_lists(buf->leaf_states, buf->legal_moves, buf->num_legal, buf->features, T, net->F,
+                                    net->fc1_w, net->fc1_b, net->ln_w, net->ln_b, net->fc2_w, net->fc2_b,
+                                    net->value_w, net->value_b, net->action1_w, net->action1_b, net->action2_w,
+                                    net->action2_b, buf->leaf_workspace, buf->priors, buf->values, buf->child_q,
+                                    stream)))
+        return e;
+    if (buf->stats && (e = hg_mcts_wave_stats(buf->leaf_idx, buf->num_legal, buf->vl_lens, T, buf->stats, stream)))
+        return e;
+    return hg_mcts_expand_backprop_dense_ws(tree, buf->child_q, buf->leaf_idx, buf->leaf_states, buf->legal_moves,
+                                            buf->num_legal, buf->priors, buf->results, buf->values, buf->vl_paths,
+                                            buf->vl_lens, q_penalty, B, T, buf->tree_workspace, stream);
 }
 
 int hg_mcts_reset_trees(const hg_tree* tree, const int8_t* reset, int32_t* root_node, int64_t B, void* stream) {

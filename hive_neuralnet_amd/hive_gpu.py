@@ -97,6 +97,9 @@ _SIGS = {
                            _c_void_p],
     "hg_mcts_reset_trees": [_c_void_p, _c_void_p, _c_void_p, _c_i64, _c_void_p],
     "hg_mcts_wave_stats": [_c_void_p, _c_void_p, _c_void_p, _c_i64, _c_void_p, _c_void_p],
+    "hg_mcts_wave_root_slots": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, ctypes.c_float,
+                                _c_i64, _c_int, _c_int, ctypes.c_float, ctypes.c_float, _c_void_p, _c_void_p,
+                                _c_void_p],
     "hg_legal_mask": [_c_void_p, _c_i64, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p],
     "hg_mcts_select": [_c_void_p, _c_void_p, _c_void_p, ctypes.c_float, _c_i64, _c_int, _c_void_p, _c_void_p,
                        _c_void_p, _c_void_p, _c_void_p, _c_void_p],
@@ -134,6 +137,23 @@ class HgTree(ctypes.Structure):
         "visit_count", "total_value", "prior", "parent_idx", "virtual_q_penalty", "move_bytes", "action_idx",
         "first_child", "num_children", "is_terminal", "terminal_value", "node_count", "child_init_q")] + [
         ("max_nodes", ctypes.c_int64)]
+
+
+class HgFnnNet(ctypes.Structure):
+    """C layout of `hg_fnn_net` (include/hive_gpu.h)."""
+
+    _fields_ = [(name, ctypes.c_void_p) for name in (
+        "fc1_w", "fc1_b", "ln_w", "ln_b", "fc2_w", "fc2_b", "value_w", "action1_w", "action1_b", "action2_w")] + [
+        ("value_b", ctypes.c_float), ("action2_b", ctypes.c_float), ("F", ctypes.c_int32)]
+
+
+class HgWaveBuffers(ctypes.Structure):
+    """C layout of `hg_wave_buffers` (include/hive_gpu.h)."""
+
+    _fields_ = [(name, ctypes.c_void_p) for name in (
+        "leaf_idx", "move_paths", "path_lens", "vl_paths", "vl_lens", "leaf_states", "results", "legal_moves",
+        "num_legal", "features", "priors", "values", "child_q", "leaf_workspace", "tree_workspace", "stats")] + [
+        ("capacity", ctypes.c_int64)]
 
 
 _TREE_SPEC = [  # the 12 tree tensors in the reference's argument order (game_logic.cu:933-953)
@@ -427,6 +447,14 @@ class HiveGpuExtension:
                 priors.data_ptr(), values.data_ptr(), child_q.data_ptr(), _stream()), "fnn_leaf_eval_lists")
         return priors, values, child_q
 
+    def prepare_wave_root_slots(self, vc, tv, pr, pa, vq, mb, ai, fc, nc, it, tv2, cnt, child_init_q, B: int,
+                                max_nodes: int, net, head_biases=None, capacity: int | None = None) -> "WavePlan":
+        """A WavePlan: simulation waves of the Gumbel root search over this
+        tree and network (hg_mcts_wave_root_slots), for up to `capacity`
+        simulations per wave (default 16 * B)."""
+        return WavePlan(self._lib, (vc, tv, pr, pa, vq, mb, ai, fc, nc, it, tv2, cnt), child_init_q, B, max_nodes,
+                        net, head_biases, capacity if capacity is not None else 16 * int(B))
+
     def leaf_eval_workspace_bytes(self, T: int) -> int:
         return int(self._lib.hg_fnn_leaf_eval_lists_workspace(int(T), FNN_FEAT_DIM)) + 256
 
@@ -529,6 +557,89 @@ def _fnn_weights(net, F: int, head_biases=None):
         head_biases = (net.value_fc.bias.detach().reshape(-1)[0].item(),
                        net.action_fc2.bias.detach().reshape(-1)[0].item())
     return w, float(head_biases[0]), float(head_biases[1])
+
+
+class WavePlan:
+    """hg_mcts_wave_root_slots with its fixed arguments prepared once.
+
+    The tree (12 arrays + child_init_q) and the 64-wide network are validated
+    and packed here, and the per-simulation buffers are allocated for
+    `capacity` simulations; each run() then costs one library call.  The
+    tensors stay referenced by the plan, so their addresses stay valid;
+    the network enters by address (weights updated in place are seen, a
+    re-created network needs a new plan).  run() returns views of the
+    plan's buffers, which the next run() overwrites in stream order."""
+
+    def __init__(self, lib, tree_tensors, child_init_q, B: int, max_nodes: int, net, head_biases, capacity: int):
+        B, M, cap = int(B), int(max_nodes), int(capacity)
+        if B <= 0 or cap <= 0:
+            raise ValueError("WavePlan: B and capacity must be positive")
+        self._lib = lib
+        self.B, self.max_nodes, self.capacity = B, M, cap
+        self._keep = (tuple(tree_tensors), child_init_q)
+        self._tree = _tree_struct(tuple(tree_tensors), child_init_q, B, M)
+        self.set_net(net, head_biases)
+
+        def buf(shape, dtype):
+            return torch.empty(shape, dtype=dtype, device="cuda")
+
+        self.leaf_idx = buf((cap,), torch.int32)
+        self.move_paths = buf((cap, MAX_TREE_DEPTH, SIZEOF_GPU_MOVE), torch.uint8)
+        self.path_lens = buf((cap,), torch.int32)
+        self.vl_paths = buf((cap, MAX_TREE_DEPTH), torch.int32)
+        self.vl_lens = buf((cap,), torch.int32)
+        self.leaf_states = buf((cap, SIZEOF_HIVE_STATE), torch.uint8)
+        self.results = buf((cap,), torch.int32)
+        self.legal_moves = buf((cap, MAX_LEGAL_MOVES, SIZEOF_GPU_MOVE), torch.uint8)
+        self.num_legal = buf((cap,), torch.int32)
+        self.features = buf((cap, FNN_FEAT_DIM), torch.float32)
+        self.priors = buf((cap, MAX_LEGAL_MOVES), torch.float32)
+        self.values = buf((cap,), torch.float32)
+        self.child_q = buf((cap, MAX_LEGAL_MOVES), torch.float32)
+        # both workspaces grow with the simulation count: sized at capacity they
+        # serve every smaller wave
+        self._leaf_ws = buf((int(lib.hg_fnn_leaf_eval_lists_workspace(cap, FNN_FEAT_DIM)) + 256,), torch.uint8)
+        self._tree_ws = buf((max(1, (int(lib.hg_mcts_expand_backprop_dense_workspace(B, cap)) + 3) // 4),),
+                            torch.int32)
+        ptrs = [t.data_ptr() for t in (self.leaf_idx, self.move_paths, self.path_lens, self.vl_paths, self.vl_lens,
+                                       self.leaf_states, self.results, self.legal_moves, self.num_legal,
+                                       self.features, self.priors, self.values, self.child_q)]
+        self._bufs = HgWaveBuffers(*ptrs, (self._leaf_ws.data_ptr() + 255) & ~255, self._tree_ws.data_ptr(), None,
+                                   cap)
+
+    def tree_base(self) -> int:
+        """Address of the plan's visit_count array (its first game's row)."""
+        return self._keep[0][0].data_ptr()
+
+    def set_net(self, net, head_biases=None) -> None:
+        """Point later waves at `net` (validated and packed as in __init__)."""
+        w, vb, ab = _fnn_weights(net, FNN_FEAT_DIM, head_biases)
+        self._weights = w
+        self._net = HgFnnNet(*[t.data_ptr() for t in w], vb, ab, FNN_FEAT_DIM)
+
+    def run(self, root_states, game_active, root_nodes, root_slots, num_candidates: int, max_root_children: int,
+            c_puct: float, W: int, deterministic_non_root: bool = False, non_root_sigma: float = 4.0,
+            q_penalty: float = 0.0, stats: torch.Tensor | None = None):
+        """One wave of W simulations per root candidate; returns (leaf_idx,
+        leaf_states, num_legal, vl_lens) of its T = W * C * B simulations.
+        `stats`: hg_mcts_wave_stats' int64[4] counters to accumulate into."""
+        B, C, W = self.B, int(num_candidates), int(W)
+        T = W * C * B
+        if T > self.capacity:
+            raise ValueError(f"WavePlan: {T} simulations, capacity {self.capacity}")
+        _state_rows(root_states, B)
+        _dev(game_active, "game_active", torch.int8, (), B)
+        _dev(root_nodes, "root_nodes", torch.int32, (), B)
+        _dev(root_slots, "root_slots", torch.int32, (C,), B)
+        if stats is not None:
+            _dev(stats, "stats", torch.int64, (), 4)
+        self._bufs.stats = stats.data_ptr() if stats is not None else None
+        _check(self._lib.hg_mcts_wave_root_slots(
+            ctypes.byref(self._tree), root_states.data_ptr(), game_active.data_ptr(), root_nodes.data_ptr(),
+            root_slots.data_ptr(), C, int(max_root_children), float(c_puct), B, W,
+            1 if deterministic_non_root else 0, float(non_root_sigma), float(q_penalty), ctypes.byref(self._net),
+            ctypes.byref(self._bufs), _stream()), "mcts_wave_root_slots")
+        return self.leaf_idx[:T], self.leaf_states[:T], self.num_legal[:T], self.vl_lens[:T]
 
 
 def random_positions(batch_size: int, expansion_mask: int, max_ply: int, seed: int, lockstep: bool = False):

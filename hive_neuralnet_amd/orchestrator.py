@@ -146,6 +146,12 @@ class FNNMCTSOrchestrator:
         self.split_min_rows = 8192
         self._part_streams: list = []
         self._part_ws: dict = {}
+        # simulation waves as one library call each (hg_mcts_wave_root_slots:
+        # the tree, network and per-simulation buffers prepared once per buffer
+        # set) wherever the fused leaf evaluation serves the network; False =
+        # the step entry points one by one, in the reference's call sequence
+        self.native_waves = True
+        self._wave_plans: dict = {}
 
     def enable_counters(self) -> None:
         self._stats = torch.zeros((4,), dtype=torch.int64, device="cuda")
@@ -398,11 +404,11 @@ class FNNMCTSOrchestrator:
             if graphs:
                 leaf_idx, leaf_states, nl, vlen = self._graph_wave(tree, root_states, game_active, root_slots, C, B,
                                                                   w, q_penalty)
+                if self.counters is not None:
+                    self.ext.mcts_wave_stats(leaf_idx, nl, vlen, total, self._stats)
             else:
                 leaf_idx, leaf_states, nl, vlen = self._wave(tree, root_states, game_active, root_slots, C, B, w,
                                                              q_penalty)
-            if self.counters is not None:
-                self.ext.mcts_wave_stats(leaf_idx, nl, vlen, total, self._stats)
             if self.keep_last_leaves:
                 self.last_leaves = leaf_states[leaf_idx >= 0]
             sims += total
@@ -435,14 +441,16 @@ class FNNMCTSOrchestrator:
             for p, tv, rs, ga, sl, nb, s in ranges:
                 with torch.cuda.stream(s):
                     total = w * C * nb
-                    need = self.ext.leaf_eval_workspace_bytes(total)
-                    ws = self._part_ws.get(p)
-                    if ws is None or ws.numel() < need:
-                        ws = torch.empty((need,), dtype=torch.uint8, device="cuda")
-                        self._part_ws[p] = ws
-                    leaf_idx, leaf_states, nl, vlen = self._wave(tv, rs, ga, sl, C, nb, w, q_penalty, ws)
-                    if self.counters is not None:
-                        self.ext.mcts_wave_stats(leaf_idx, nl, vlen, total, self._stats)
+                    if self._native_waves_ok():
+                        leaf_idx, leaf_states, nl, vlen = self._wave(
+                            tv, rs, ga, sl, C, nb, w, q_penalty, plan=self._wave_plan(("part", p), tv, nb, total))
+                    else:
+                        need = self.ext.leaf_eval_workspace_bytes(total)
+                        ws = self._part_ws.get(p)
+                        if ws is None or ws.numel() < need:
+                            ws = torch.empty((need,), dtype=torch.uint8, device="cuda")
+                            self._part_ws[p] = ws
+                        leaf_idx, leaf_states, nl, vlen = self._wave(tv, rs, ga, sl, C, nb, w, q_penalty, ws)
                     if self.keep_last_leaves and wave == waves - 1:
                         last.append(leaf_states[leaf_idx >= 0])
             sims += w * C * B
@@ -454,12 +462,43 @@ class FNNMCTSOrchestrator:
             self.last_leaves = torch.cat(last)
         return sims
 
-    def _wave(self, tree, root_states, game_active, root_slots, C, B, w, q_penalty, workspace=None):
+    def _native_waves_ok(self) -> bool:
+        return self.native_waves and self._fused_eval_ok()
+
+    def _wave_plan(self, slot, tree, B, total):
+        """The WavePlan of buffer set `slot`: re-made for another tree or B or
+        when a wave outgrows its buffers, re-pointed when the network (its
+        parameter addresses or head biases) changes."""
+        key = (tuple(v.data_ptr() for v in tree.values()), B)
+        net_key = tuple(p.data_ptr() for p in self.net.parameters()) + tuple(self._head_biases or ())
+        entry = self._wave_plans.get(slot)
+        if entry is None or entry[0] != key or entry[1].capacity < total:
+            self._wave_plans.pop(slot, None)  # release the old buffers first
+            plan = self.ext.prepare_wave_root_slots(*self._tree_args(tree), tree["child_init_q"], B, self._max_nodes,
+                                                    self.net, self._head_biases, capacity=total)
+            entry = [key, plan, net_key]
+            self._wave_plans[slot] = entry
+        elif entry[2] != net_key:
+            entry[1].set_net(self.net, self._head_biases)
+            entry[2] = net_key
+        return entry[1]
+
+    def _wave(self, tree, root_states, game_active, root_slots, C, B, w, q_penalty, workspace=None, plan=None,
+              stats=True):
         """One wave of w simulations per root candidate (:982-1055): select ->
-        replay -> legal + features -> leaf evaluation -> expansion + backup.
-        No host synchronisation.  Returns (leaf_idx, leaf_states, num_legal, vl_lens)."""
+        replay -> legal + features -> leaf evaluation -> expansion + backup,
+        and the search counters when enabled and `stats`.  No host
+        synchronisation.  Native waves (one library call) run on `plan`, or
+        on the single-range buffer set.  Returns (leaf_idx, leaf_states,
+        num_legal, vl_lens)."""
         cfg = self.config
         total = w * C * B
+        counters = self._stats if (stats and self.counters is not None) else None
+        if self._native_waves_ok():
+            if plan is None:
+                plan = self._wave_plan("main", tree, B, total)
+            return plan.run(root_states, game_active, tree["root_node"], root_slots, C, self._max_legal, cfg.c_puct,
+                            w, cfg.deterministic_non_root, cfg.non_root_sigma, q_penalty, stats=counters)
         (leaf_idx, leaf_states, legal, nl, feat, results, vl, vlen) = \
             self.ext.mcts_select_replay_legal_fnn_root_slots_batch(
                 *self._tree_args(tree), tree["child_init_q"], root_states, game_active, tree["root_node"],
@@ -469,6 +508,8 @@ class FNNMCTSOrchestrator:
         self.ext.mcts_expand_and_backprop_dense_priors_batch(
             *self._tree_args(tree), tree["child_init_q"], child_q, leaf_idx, leaf_states, legal, nl, priors,
             results, vals, vl, vlen, B, total, self._max_nodes, q_penalty)
+        if counters is not None:
+            self.ext.mcts_wave_stats(leaf_idx, nl, vlen, total, counters)
         return leaf_idx, leaf_states, nl, vlen
 
     def _graph_wave(self, tree, root_states, game_active, root_slots, C, B, w, q_penalty):
@@ -490,12 +531,21 @@ class FNNMCTSOrchestrator:
             # the root states enter by address (part of the key: a ply's states
             # do not move); the per-round inputs are copied into the graph's buffers
             static = {"roots": root_states, "active": game_active.clone(), "slots": root_slots.clone()}
-            # the graph's own leaf-evaluation workspace, allocated outside capture and
-            # kept alive with the graph
-            ws = torch.empty((self.ext.leaf_eval_workspace_bytes(w * C * B),), dtype=torch.uint8, device="cuda")
+            # the graph's own buffers (a wave plan, or the leaf-evaluation workspace
+            # of the step entry points), allocated outside capture and kept alive
+            # with the graph; its counters are added after each replay
+            if self._native_waves_ok():
+                ws = self.ext.prepare_wave_root_slots(*self._tree_args(tree), tree["child_init_q"], B,
+                                                      self._max_nodes, self.net, self._head_biases,
+                                                      capacity=w * C * B)
+                wave = dict(plan=ws)
+            else:
+                ws = torch.empty((self.ext.leaf_eval_workspace_bytes(w * C * B),), dtype=torch.uint8, device="cuda")
+                wave = dict(workspace=ws)
             graph = torch.cuda.CUDAGraph()
             with torch.cuda.graph(graph):
-                outs = self._wave(tree, static["roots"], static["active"], static["slots"], C, B, w, q_penalty, ws)
+                outs = self._wave(tree, static["roots"], static["active"], static["slots"], C, B, w, q_penalty,
+                                  stats=False, **wave)
             entry = (graph, static, outs, ws)
             self._graphs[key] = entry
             # capture records the launches without running them: the replay below runs this wave

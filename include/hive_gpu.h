@@ -375,6 +375,58 @@ int hg_mcts_root_noise(const hg_tree* tree, const float* noise, const int32_t* r
 int hg_mcts_wave_stats(const int32_t* leaf_idx, const int32_t* num_legal, const int32_t* vl_lens, int64_t total,
                        int64_t* stats, void* stream);
 
+/* ---- one simulation wave of the Gumbel root search, launched natively ----
+ * The body of the reference's per-wave loop (fnn_mcts_orchestrator.py:982-1055:
+ * mcts_select_replay_legal_fnn_root_slots_batch, the FNN leaf evaluation,
+ * mcts_expand_and_backprop_dense_priors_batch) as one host call: select over
+ * the root slots -> replay (rows of idle simulations zero) and the leaves'
+ * results -> legal lists + features -> hg_fnn_leaf_eval_lists -> expansion +
+ * backup (hg_mcts_expand_backprop_dense_ws), launched in that order on
+ * `stream` with no host synchronisation and no allocation.  No single
+ * reference entry point: it saves the host the per-call argument handling of
+ * six entry points per wave.  Results are those of the six calls. */
+typedef struct hg_fnn_net {   /* a 64-wide HiveFNN (fnn_network.py:97-140), F = 122 */
+    const float* fc1_w;       /* [64][F] */
+    const float* fc1_b;       /* [64] */
+    const float* ln_w;        /* [64] */
+    const float* ln_b;        /* [64] */
+    const float* fc2_w;       /* [64][64] */
+    const float* fc2_b;       /* [64] */
+    const float* value_w;     /* [64] */
+    const float* action1_w;   /* [64][128] */
+    const float* action1_b;   /* [64] */
+    const float* action2_w;   /* [64] */
+    float value_b;
+    float action2_b;
+    int32_t F;
+} hg_fnn_net;
+
+typedef struct hg_wave_buffers {  /* rows for T = W * num_candidates * B simulations (or more) */
+    int32_t* leaf_idx;       /* [T] */
+    uint8_t* move_paths;     /* [T][128][6] */
+    int32_t* path_lens;      /* [T] */
+    int32_t* vl_paths;       /* [T][128] */
+    int32_t* vl_lens;        /* [T] */
+    uint8_t* leaf_states;    /* [T][3424] */
+    int32_t* results;        /* [T] */
+    uint8_t* legal_moves;    /* [T][256][6] */
+    int32_t* num_legal;      /* [T] */
+    float* features;         /* [T][122], 8-byte aligned */
+    float* priors;           /* [T][256] */
+    float* values;           /* [T] */
+    float* child_q;          /* [T][256] */
+    void* leaf_workspace;    /* hg_fnn_leaf_eval_lists_workspace(T, 122) bytes, 256-byte aligned */
+    void* tree_workspace;    /* hg_mcts_expand_backprop_dense_workspace(B, T) bytes, 4-byte aligned */
+    int64_t* stats;          /* NULL, or hg_mcts_wave_stats' int64[4], accumulated */
+    int64_t capacity;        /* rows each [T] array above holds */
+} hg_wave_buffers;
+
+int hg_mcts_wave_root_slots(const hg_tree* tree, const uint8_t* root_states, const int8_t* game_active,
+                            const int32_t* root_nodes, const int32_t* root_slots, int num_candidates,
+                            int max_root_children, float c_puct, int64_t B, int W, int deterministic_non_root,
+                            float non_root_sigma, float q_penalty, const hg_fnn_net* net,
+                            const hg_wave_buffers* buffers, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -349,3 +349,20 @@ def completed_q_trees(M=16):
         t["node_count"][g] = 2 + len(kids)
         want.append(2 + pick)
     return t, np.array(want, np.int32)
+
+
+def record_wave_evaluations(monkeypatch, evals):
+    """Append each native simulation wave's (priors, values, child Q) to
+    `evals` (numpy copies), as a recorded _eval_states call would: the
+    orchestrator's waves run as one library call (WavePlan.run) whose
+    evaluation outputs stay in the plan's buffers."""
+    from hive_neuralnet_amd import hive_gpu
+    real_run = hive_gpu.WavePlan.run
+
+    def run(plan, *a, **k):
+        out = real_run(plan, *a, **k)
+        T = int(a[7]) * int(a[4]) * plan.B
+        evals.append(tuple(x[:T].detach().cpu().numpy().copy() for x in (plan.priors, plan.values, plan.child_q)))
+        return out
+    monkeypatch.setattr(hive_gpu.WavePlan, "run", run)
+

@@ -35,6 +35,35 @@ def test_python_binding_matches_header():
     assert sorted(list(hive_gpu._SIGS) + list(hive_gpu._SIGS_I64)) == _declared()
 
 
+def test_struct_layouts_match_header(tmp_path):
+    """The ctypes mirrors of the header's structs (hg_tree, hg_fnn_net,
+    hg_wave_buffers) have the C compiler's field offsets and sizes: the
+    header compiled by gcc prints offsetof / sizeof of every field."""
+    import shutil
+    import subprocess
+    from hive_neuralnet_amd import hive_gpu
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        pytest.skip("gcc not available")
+    mirrors = {"hg_tree": hive_gpu.HgTree, "hg_fnn_net": hive_gpu.HgFnnNet, "hg_wave_buffers": hive_gpu.HgWaveBuffers}
+    lines = []
+    for cname, cls in mirrors.items():
+        lines.append(f'printf("{cname} %zu\\n", sizeof({cname}));')
+        for f, _ in cls._fields_:
+            lines.append(f'printf("{cname}.{f} %zu\\n", offsetof({cname}, {f}));')
+    src = tmp_path / "layout.c"
+    src.write_text('#include <stddef.h>\n#include <stdio.h>\n#include "hive_gpu.h"\nint main(void) {\n'
+                   + "\n".join(lines) + "\nreturn 0;\n}\n")
+    exe = tmp_path / "layout"
+    subprocess.run([gcc, "-std=c99", "-I", os.path.join(ROOT, "include"), str(src), "-o", str(exe)], check=True)
+    got = dict(line.split() for line in subprocess.run([str(exe)], check=True, capture_output=True,
+                                                         text=True).stdout.splitlines())
+    for cname, cls in mirrors.items():
+        assert int(got[cname]) == ctypes.sizeof(cls), cname
+        for f, _ in cls._fields_:
+            assert int(got[f"{cname}.{f}"]) == getattr(cls, f).offset, f"{cname}.{f}"
+
+
 def test_reference_surface_names():
     """Every entry point the reference's hive_fnn callers use exists (bindings.cpp:254-476)."""
     from hive_neuralnet_amd.hive_gpu import HiveGpuExtension

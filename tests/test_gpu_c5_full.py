@@ -60,6 +60,19 @@ class SliceShadow:
         for name in ("mcts_expand_dense_priors_batch", "mcts_apply_root_noise", "mcts_select_with_root_slots_batch",
                      "mcts_replay_fill_batch", "mcts_expand_and_backprop_dense_priors_batch"):
             monkeypatch.setattr(ext, name, self._wrap(name, getattr(ext, name)), raising=False)
+        # native waves (one library call each): the same three steps checked
+        # from the wave's buffers
+        from hive_neuralnet_amd import hive_gpu
+        real_run = hive_gpu.WavePlan.run
+
+        def run(plan, *a, **k):
+            out = real_run(plan, *a, **k)
+            self._wave_run(plan, a)
+            for name in ("mcts_select_with_root_slots_batch", "mcts_replay_fill_batch",
+                         "mcts_expand_and_backprop_dense_priors_batch"):
+                self.calls[name] = self.calls.get(name, 0) + 1
+            return out
+        monkeypatch.setattr(hive_gpu.WavePlan, "run", run)
 
     def sync(self):
         idx = self.torch.tensor(self.games, device="cuda")
@@ -154,6 +167,35 @@ class SliceShadow:
             assert np.array_equal(st[:, 3415].astype(np.int32), res), "leaf results differ"
             self.m.expand_backprop_dense(self._sub(js), cq, leaf, st, om, on, pri, res, vals, vl, vlen,
                                          float(a[26]))
+
+
+    def _wave_run(self, plan, a):
+        roots, active, rnodes, slots = a[:4]
+        C, max_root, c_puct, W = int(a[4]), int(a[5]), float(a[6]), int(a[7])
+        det, sigma, qp = bool(a[8]), float(a[9]), float(a[10])
+        B = plan.B
+        T = W * C * B
+        first = (plan.tree_base() - self.base) // (4 * self.M)
+        for js, local in self._blocks(first, B):
+            g = self.torch.tensor(local, device="cuda")
+            r = self._rows(T, B, local)
+            sub = self._sub(js)
+            exp = self.m.select_slots(sub, _np(active[g]), _np(rnodes[g]), np.ascontiguousarray(_np(slots[g])),
+                                      max_root, c_puct, W, det, sigma, qp)
+            b = {k: np.ascontiguousarray(_np(getattr(plan, k)[:T][r])) for k in (
+                "leaf_idx", "move_paths", "path_lens", "vl_paths", "vl_lens", "leaf_states", "results",
+                "legal_moves", "num_legal", "priors", "values", "child_q")}
+            for e, k in zip(exp, ("leaf_idx", "move_paths", "path_lens", "vl_paths", "vl_lens")):
+                assert np.array_equal(e, b[k]), f"native wave: select output {k} differs"
+            st = np.zeros((len(r), 3424), np.uint8)
+            self.m.replay(np.ascontiguousarray(_np(roots[g])), st, b["move_paths"], b["path_lens"], b["leaf_idx"])
+            assert np.array_equal(st, b["leaf_states"]), "native wave: replayed leaf states differ"
+            om, on, _, _ = self.m.o.batch_legal_features_actions(st, want_features=False, want_actions=False)
+            assert np.array_equal(om, b["legal_moves"]) and np.array_equal(on, b["num_legal"]), \
+                "native wave: leaf legal lists differ"
+            assert np.array_equal(st[:, 3415].astype(np.int32), b["results"]), "native wave: leaf results differ"
+            self.m.expand_backprop_dense(sub, b["child_q"], b["leaf_idx"], st, om, on, b["priors"], b["results"],
+                                         b["values"], b["vl_paths"], b["vl_lens"], qp)
 
 
 def expected_sims(n_legal, n_reserve):

@@ -12,7 +12,7 @@ check covers the orchestrator's tree traffic exactly.
 import numpy as np
 import pytest
 
-from mcts_driver import tree_equal
+from mcts_driver import record_wave_evaluations, tree_equal
 
 pytestmark = pytest.mark.gpu
 
@@ -36,6 +36,20 @@ class Shadow:
                      "mcts_select_with_root_mask_batch", "mcts_replay_batch", "mcts_replay_fill_batch",
                      "mcts_expand_and_backprop_dense_priors_batch"):
             monkeypatch.setattr(ext, name, self._wrap(name, getattr(ext, name)), raising=False)
+        # native waves (one library call each): the same select, replay and
+        # expansion + backup applied to the mirror from the wave's buffers
+        from hive_neuralnet_amd import hive_gpu
+        real_run = hive_gpu.WavePlan.run
+
+        def run(plan, *a, **k):
+            out = real_run(plan, *a, **k)
+            self._wave_run(plan, a)
+            for name in ("mcts_select_with_root_slots_batch", "mcts_replay_fill_batch",
+                         "mcts_expand_and_backprop_dense_priors_batch"):
+                self.calls[name] = self.calls.get(name, 0) + 1
+            self.check_tree("native wave")
+            return out
+        monkeypatch.setattr(hive_gpu.WavePlan, "run", run)
 
     def sync(self):
         self.ot = {k: _np(v).copy() for k, v in self.tree.items()}
@@ -93,6 +107,24 @@ class Shadow:
     def _mcts_expand_and_backprop_dense_priors_batch(self, a, out):
         cq, leaf, st, lm, nl, pri, res, vals, vl, vlen = [_np(x) for x in a[13:23]]
         self.m.expand_backprop_dense(self.ot, cq, leaf, st, lm, nl, pri, res, vals, vl, vlen, float(a[26]))
+
+    def _wave_run(self, plan, a):
+        roots, active, rnodes, slots = [_np(x) for x in a[:4]]
+        C, max_root, c_puct, W = int(a[4]), int(a[5]), float(a[6]), int(a[7])
+        det, sigma, qp = bool(a[8]), float(a[9]), float(a[10])
+        T = W * C * plan.B
+        b = {k: _np(getattr(plan, k)[:T]) for k in (
+            "leaf_idx", "move_paths", "path_lens", "vl_paths", "vl_lens", "leaf_states", "results", "legal_moves",
+            "num_legal", "priors", "values", "child_q")}
+        exp = self.m.select_slots(self.ot, active, rnodes, slots, max_root, c_puct, W, det, sigma, qp)
+        for e, k in zip(exp, ("leaf_idx", "move_paths", "path_lens", "vl_paths", "vl_lens")):
+            assert np.array_equal(e, b[k]), f"native wave: select output {k} differs"
+        leaves = np.zeros_like(b["leaf_states"])
+        self.m.replay(roots, leaves, b["move_paths"], b["path_lens"], b["leaf_idx"])
+        assert np.array_equal(leaves, b["leaf_states"]), "native wave: replayed leaf states differ"
+        assert np.array_equal(leaves[:, 3415].astype(np.int32), b["results"]), "native wave: leaf results differ"
+        self.m.expand_backprop_dense(self.ot, b["child_q"], b["leaf_idx"], leaves, b["legal_moves"], b["num_legal"],
+                                     b["priors"], b["results"], b["values"], b["vl_paths"], b["vl_lens"], qp)
 
 
 def _setup(B, sims, M, mask, max_ply, seed, **kw):
@@ -220,6 +252,7 @@ def test_search_ply_matches_numpy_orchestrator(monkeypatch, sims, mask, max_ply,
     monkeypatch.setattr(orch, "_eval_states", rec_eval)
     monkeypatch.setattr(torch, "rand", rec_rand)
     monkeypatch.setattr(ext, "mcts_apply_root_noise", rec_noise, raising=False)
+    record_wave_evaluations(monkeypatch, evals)
     orch.use_graphs = False  # the recording reads every evaluation on the host
     t0 = {k: _np(v).copy() for k, v in tree.items()}
     st = _np(states).copy()
@@ -435,6 +468,67 @@ def test_game_ranges_on_streams_equal_one_range(mask, max_ply, parts):
                                   y.view(np.uint32) if y.dtype == np.float32 else y)
     assert np.array_equal(outs[0][3], outs[1][3])
     assert tree_equal(outs[0][4], outs[1][4]) == []
+
+
+@pytest.mark.parametrize("mask,max_ply,M,parts,kw", [
+    (0, 60, 8192, 1, {}),
+    (7, 90, 8192, 1, {"wave_parallel": False}),
+    (7, 90, 8192, 2, {}),
+    (0, 30, 600, 1, {}),                        # node pool runs out mid-search
+], ids=["schedule", "w1", "two-ranges", "pool-exhaustion"])
+def test_native_waves_equal_step_waves(mask, max_ply, M, parts, kw):
+    """Simulation waves as one library call (hg_mcts_wave_root_slots through
+    WavePlan) against the same waves through the step entry points (select,
+    replay, results, legal + features, leaf evaluation, expansion + backup):
+    three plies with rebases, every ply's choice, policy and visits, the wave
+    counters and the final trees bit-identical."""
+    import torch
+    from hive_neuralnet_amd import hive_gpu
+    outs = []
+    for native in (False, True):
+        B = 18
+        orch, _, tree = _setup(B, 64, M, mask, max_ply, 91, **kw)
+        orch.native_waves = native
+        orch.game_parts = parts
+        orch.use_graphs = False
+        orch.enable_counters()
+        states, _ = hive_gpu.random_positions(B, mask, max_ply, 92)
+        torch.manual_seed(93)
+        np.random.seed(93)
+        active = torch.ones((B,), dtype=torch.bool, device="cuda")
+        rec = []
+        for _ in range(3):
+            r = orch.search_ply(states, tree, active)
+            rec.append((_np(r.chosen_slot), _np(r.policy), _np(r.slot_visits)))
+            orch.apply_and_rebase(states, tree, r)
+            active &= orch.ext.check_results_batch(states, B) == 0
+        assert bool(orch._wave_plans) == native
+        rec.append(_np(orch._stats).copy())
+        rec.append({k: _np(v).copy() for k, v in tree.items()})
+        outs.append(rec)
+    for a, b in zip(outs[0][:3], outs[1][:3]):
+        for x, y in zip(a, b):
+            assert np.array_equal(x.view(np.uint32) if x.dtype == np.float32 else x,
+                                  y.view(np.uint32) if y.dtype == np.float32 else y)
+    assert np.array_equal(outs[0][3], outs[1][3])
+    assert tree_equal(outs[0][4], outs[1][4]) == []
+
+
+def test_wave_plan_rejects_oversized_wave():
+    """A wave of more simulations than the plan's buffers hold is refused
+    before any launch; a smaller one runs."""
+    import torch
+    B = 4
+    orch, states, tree = _setup(B, 16, 2048, 0, 20, 7)
+    orch._head_biases = (float(orch.net.value_fc.bias.item()), float(orch.net.action_fc2.bias.item()))
+    plan = orch.ext.prepare_wave_root_slots(*orch._tree_args(tree), tree["child_init_q"], B, 2048, orch.net,
+                                            orch._head_biases, capacity=2 * B)
+    active = torch.zeros((B,), dtype=torch.int8, device="cuda")
+    slots = torch.full((B, 2), -1, dtype=torch.int32, device="cuda")
+    with pytest.raises(ValueError, match="capacity"):
+        plan.run(states, active, tree["root_node"], slots, 2, 256, 1.25, 2)
+    leaf, _, _, _ = plan.run(states, active, tree["root_node"], slots, 2, 256, 1.25, 1)
+    assert (_np(leaf) == -1).all()  # no active game: every simulation idle
 
 
 def _bare_orch(**over):

@@ -244,6 +244,41 @@ def test_successor_rows_device_sized(ext, oracle, T, zero_every):
     assert np.array_equal(_bits(got), _bits(want))
 
 
+def test_successor_rows_large_batch(ext, oracle):
+    """hg_successor_rows past the one-launch planner's batch limit (32,768
+    leaves: there the offsets take one scan workgroup and the row map its own
+    launch): 33,000 leaves, 1,000 positions tiled with every seventh count
+    forced to 0.  Offsets, total and map in full; the features of the rows of
+    the first and the last 300 leaves against the oracle."""
+    T, P = 33000, 1000
+    st1, _ = oracle.generate_positions(P, 7, 140, 0x5A5A)
+    mv1, n1, _, _ = oracle.batch_legal_features_actions(st1, want_features=False, want_actions=False)
+    st, moves = np.tile(st1, (T // P, 1)), np.tile(mv1, (T // P, 1, 1))
+    n = np.tile(n1.astype(np.int32), T // P)
+    n[::7] = 0
+    lib = ext._lib
+    ws = torch.zeros((int(lib.hg_successor_rows_workspace(T)),), dtype=torch.uint8, device="cuda")
+    feat = torch.full((int(n.sum()), 122), float("nan"), dtype=torch.float32, device="cuda")
+    s, m, nn = _cuda(st), _cuda(moves), _cuda(n)
+    err = lib.hg_successor_rows(s.data_ptr(), m.data_ptr(), nn.data_ptr(), T, ws.data_ptr(), feat.data_ptr(),
+                                torch.cuda.current_stream().cuda_stream)
+    assert err == 0
+    torch.cuda.synchronize()
+    w = ws.view(torch.int64).cpu().numpy()
+    offs, total = w[:T], int(w[T])
+    want_offs = np.concatenate([[0], np.cumsum(n)[:-1]]).astype(np.int64)
+    assert total == int(n.sum()) and np.array_equal(offs, want_offs)
+    a2r, mi = w[T + 1: T + 1 + total], w[T + 1 + T * 256: T + 1 + T * 256 + total]
+    want_a2r = np.repeat(np.arange(T), n).astype(np.int64)
+    want_mi = np.concatenate([np.arange(k) for k in n]).astype(np.int64)
+    assert np.array_equal(a2r, want_a2r) and np.array_equal(mi, want_mi)
+    got = feat.cpu().numpy()
+    for lo, hi in ((0, 300), (T - 300, T)):
+        r0, r1 = int(want_offs[lo]), int(want_offs[hi - 1] + n[hi - 1])
+        want = oracle.batch_successor_features(st, moves, want_a2r[r0:r1], want_mi[r0:r1])
+        assert np.array_equal(_bits(got[r0:r1]), _bits(want))
+
+
 def test_mismatched_shapes_rejected(ext):
     """A tensor whose trailing shape differs from the entry point's layout is
     rejected unless it is a flat contiguous buffer, which is taken as a view

@@ -120,6 +120,8 @@ def test_orchestrator_probe_matches_numpy(monkeypatch):
         return real_noise(*a)
 
     monkeypatch.setattr(orch, "_eval_states", rec_eval)
+    from mcts_driver import record_wave_evaluations
+    record_wave_evaluations(monkeypatch, evals)
     monkeypatch.setattr(torch, "rand", rec_rand)
     monkeypatch.setattr(ext, "mcts_apply_root_noise", rec_noise, raising=False)
     t0 = {k: _np(v).copy() for k, v in tree.items()}
