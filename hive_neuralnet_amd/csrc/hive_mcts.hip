@@ -1302,6 +1302,92 @@ __global__ __launch_bounds__(1024) void k_wave_stats(const int32_t* __restrict__
     }
 }
 
+// ---------------------------------------------------------------- Gumbel halving
+// One decision of sequential halving (fnn_mcts_orchestrator.py:650-731: the
+// torch work between rounds, and the final choice).  A candidate column of
+// game g holds a root slot (-1 = none); its statistics are those of the root
+// child in that slot (_gather_root_candidate_stats: N, and Q = -W / max(N, 1)
+// when N > min_visits; both 0 for a slot outside the root's children).  With
+// m the batch's largest candidate visit count, sigma = (c_visit + m) *
+// c_scale and the column's score is base[g][slot] + sigma * Q (-1e30 for an
+// empty column).  keep > 0: the columns ranked by score (descending, ties to
+// the lower column), the first keep of them written to cand_out[g][0..keep),
+// the first max(1, valid / 2) as their slots and the rest as -1; keep = 0:
+// chosen[g] = max(slot of the first highest column, 0).  Each workgroup finds
+// m itself (every candidate, from L2), then ranks the columns of its games,
+// one game per segment of Cp lanes (Cp = C rounded up to a power of two, at
+// most 64), by shuffles.
+constexpr int kHalvThreads = 1024;
+struct RootStat {
+    int v;
+    float q;
+};
+__device__ __forceinline__ RootStat root_slot_stat(const Tree& T, const int32_t* __restrict__ root_nodes,
+                                                   int64_t g, int slot, int min_visits) {
+    RootStat r{0, 0.0f};
+    if (slot < 0) return r;
+    const int64_t g0 = g * T.M;
+    const int root = root_nodes[g];
+    const int fc = T.fc[g0 + root], nc = T.nc[g0 + root];
+    if (fc < 0 || slot >= nc) return r;
+    int64_t idx = (int64_t)fc + slot;
+    idx = idx < T.M ? idx : T.M - 1;
+    const int v = T.vc[g0 + idx];
+    r.v = v;
+    if (v > min_visits) r.q = -T.tv[g0 + idx] / (float)(v > 1 ? v : 1);
+    return r;
+}
+
+__global__ __launch_bounds__(kHalvThreads) void k_gumbel_halving(Tree T, const int32_t* __restrict__ root_nodes,
+                                                                 const int32_t* __restrict__ cand, int C, int Cp,
+                                                                 const float* __restrict__ base, float c_visit,
+                                                                 float c_scale, int min_visits, int keep, int64_t B,
+                                                                 int32_t* __restrict__ cand_out,
+                                                                 int64_t* __restrict__ chosen) {
+    __shared__ int wmax[kHalvThreads / 64];
+    const int tid = threadIdx.x, lane = tid & 63;
+    // the batch's largest candidate visit count (0 when none)
+    int mx = 0;
+    const int64_t n = B * C;
+#pragma unroll 4
+    for (int64_t i = tid; i < n; i += kHalvThreads) mx = max(mx, root_slot_stat(T, root_nodes, i / C, cand[i],
+                                                                                  min_visits).v);
+    for (int o = 32; o > 0; o >>= 1) mx = max(mx, __shfl_xor(mx, o, 64));
+    if (lane == 0) wmax[tid >> 6] = mx;
+    __syncthreads();
+    mx = 0;
+#pragma unroll
+    for (int k = 0; k < kHalvThreads / 64; k++) mx = max(mx, wmax[k]);
+    const float sigma = (c_visit + (float)mx) * c_scale;
+    // this workgroup's games: one per Cp-lane segment
+    const int c = tid & (Cp - 1), seg0 = lane & ~(Cp - 1);
+    const int64_t g = (int64_t)blockIdx.x * (kHalvThreads / Cp) + tid / Cp;
+    const bool real = g < B && c < C;
+    int slot = -1;
+    float score = -1e30f;
+    if (real) {
+        slot = cand[g * C + c];
+        if (slot >= 0) {
+            const RootStat st = root_slot_stat(T, root_nodes, g, slot, min_visits);
+            score = base[g * kMaxLegal + (slot < kMaxLegal ? slot : kMaxLegal - 1)] + sigma * st.q;
+        }
+    }
+    int rank = 0;
+    for (int j = 0; j < Cp; j++) {  // uniform trip count: every lane takes part in the shuffles
+        const float sj = __shfl(score, seg0 + j, 64);
+        if (j < C && (sj > score || (sj == score && j < c))) rank++;
+    }
+    const uint64_t segmask = Cp == 64 ? ~0ull : (((1ull << Cp) - 1ull) << seg0);
+    const int nvalid = __popcll(__ballot(real && slot >= 0) & segmask);
+    if (!real) return;
+    if (keep > 0) {
+        const int keep_n = nvalid / 2 > 1 ? nvalid / 2 : 1;
+        if (rank < keep) cand_out[g * keep + rank] = rank < keep_n ? slot : -1;
+    } else if (rank == 0) {
+        chosen[g] = slot < 0 ? 0 : slot;
+    }
+}
+
 }  // namespace
 
 extern "C" {
@@ -1498,6 +1584,21 @@ int hg_mcts_wave_root_slots(const hg_tree* tree, const uint8_t* root_states, con
     return hg_mcts_expand_backprop_dense_ws(tree, buf->child_q, buf->leaf_idx, buf->leaf_states, buf->legal_moves,
                                             buf->num_legal, buf->priors, buf->results, buf->values, buf->vl_paths,
                                             buf->vl_lens, q_penalty, B, T, buf->tree_workspace, stream);
+}
+
+int hg_gumbel_halving(const hg_tree* tree, const int32_t* root_nodes, const int32_t* candidates, int C,
+                      const float* base, float c_visit, float c_scale, int root_q_min_visits, int keep, int64_t B,
+                      int32_t* cand_out, int64_t* chosen, void* stream) {
+    if (B <= 0) return 0;
+    if (!tree || C < 1 || C > 64 || keep < 0 || keep > C) return (int)hipErrorInvalidValue;
+    if ((keep > 0 && !cand_out) || (keep == 0 && !chosen)) return (int)hipErrorInvalidValue;
+    int Cp = 1;
+    while (Cp < C) Cp <<= 1;
+    const int64_t per = kHalvThreads / Cp;
+    hipLaunchKernelGGL(k_gumbel_halving, dim3((unsigned)((B + per - 1) / per)), dim3(kHalvThreads), 0,
+                       (hipStream_t)stream, to_tree(tree), root_nodes, candidates, C, Cp, base, c_visit, c_scale,
+                       root_q_min_visits, keep, B, cand_out, chosen);
+    return finish();
 }
 
 int hg_mcts_reset_trees(const hg_tree* tree, const int8_t* reset, int32_t* root_node, int64_t B, void* stream) {

@@ -97,6 +97,8 @@ _SIGS = {
                            _c_void_p],
     "hg_mcts_reset_trees": [_c_void_p, _c_void_p, _c_void_p, _c_i64, _c_void_p],
     "hg_mcts_wave_stats": [_c_void_p, _c_void_p, _c_void_p, _c_i64, _c_void_p, _c_void_p],
+    "hg_gumbel_halving": [_c_void_p, _c_void_p, _c_void_p, _c_int, _c_void_p, ctypes.c_float, ctypes.c_float, _c_int,
+                          _c_int, _c_i64, _c_void_p, _c_void_p, _c_void_p],
     "hg_mcts_wave_root_slots": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, ctypes.c_float,
                                 _c_i64, _c_int, _c_int, ctypes.c_float, ctypes.c_float, _c_void_p, _c_void_p,
                                 _c_void_p],
@@ -446,6 +448,38 @@ class HiveGpuExtension:
                 w[5].data_ptr(), w[6].data_ptr(), vb, w[7].data_ptr(), w[8].data_ptr(), w[9].data_ptr(), ab, ptr,
                 priors.data_ptr(), values.data_ptr(), child_q.data_ptr(), _stream()), "fnn_leaf_eval_lists")
         return priors, values, child_q
+
+    def tree_struct(self, vc, tv, pr, pa, vq, mb, ai, fc, nc, it, tv2, cnt, child_init_q, B: int,
+                    max_nodes: int) -> HgTree:
+        """The 12 tree tensors + child_init_q validated and packed once (an
+        `hg_tree` to pass by reference to the entry points that take one)."""
+        return _tree_struct((vc, tv, pr, pa, vq, mb, ai, fc, nc, it, tv2, cnt), child_init_q, int(B), int(max_nodes))
+
+    def gumbel_halving(self, tree: HgTree, root_nodes, candidates, base, c_visit: float, c_scale: float,
+                       root_q_min_visits: int, final: bool = False):
+        """One sequential-halving decision (hg_gumbel_halving) over a packed
+        tree: the next round's candidates [B, C // 2] int32, or with `final`
+        the chosen slot [B] int64.  candidates [B, C] int32 (C <= 64), base
+        [B, 256] f32 (Gumbel + legal logits)."""
+        if candidates.dim() != 2:
+            raise ValueError("candidates must be [B, C]")
+        B, C = int(candidates.shape[0]), int(candidates.shape[1])
+        _dev(candidates, "candidates", torch.int32, (C,), B)
+        _dev(root_nodes, "root_nodes", torch.int32, (), B)
+        _dev(base, "base", torch.float32, (MAX_LEGAL_MOVES,), B)
+        keep = 0 if final else C // 2
+        if final:
+            out = torch.empty((B,), dtype=torch.int64, device="cuda")
+            args = (None, out.data_ptr())
+        else:
+            out = torch.empty((B, keep), dtype=torch.int32, device="cuda")
+            args = (out.data_ptr(), None)
+        if keep == 0 and not final:
+            return out
+        _check(self._lib.hg_gumbel_halving(ctypes.byref(tree), root_nodes.data_ptr(), candidates.data_ptr(), C,
+                                           base.data_ptr(), float(c_visit), float(c_scale), int(root_q_min_visits),
+                                           keep, B, *args, _stream()), "gumbel_halving")
+        return out
 
     def prepare_wave_root_slots(self, vc, tv, pr, pa, vq, mb, ai, fc, nc, it, tv2, cnt, child_init_q, B: int,
                                 max_nodes: int, net, head_biases=None, capacity: int | None = None) -> "WavePlan":

@@ -152,6 +152,11 @@ class FNNMCTSOrchestrator:
         # the step entry points one by one, in the reference's call sequence
         self.native_waves = True
         self._wave_plans: dict = {}
+        # sequential-halving decisions (candidate statistics, sigma, scores,
+        # survivors) as one kernel each (hg_gumbel_halving) for up to 64
+        # considered actions; False = the torch ops
+        self.native_halving = True
+        self._packed: tuple | None = None
 
     def enable_counters(self) -> None:
         self._stats = torch.zeros((4,), dtype=torch.int64, device="cuda")
@@ -462,6 +467,14 @@ class FNNMCTSOrchestrator:
             self.last_leaves = torch.cat(last)
         return sims
 
+    def _packed_tree(self, tree, B):
+        """The tree's arrays packed as an `hg_tree` (kept while they stay put)."""
+        key = (tuple(v.data_ptr() for v in tree.values()), B)
+        if self._packed is None or self._packed[0] != key:
+            self._packed = (key, self.ext.tree_struct(*self._tree_args(tree), tree["child_init_q"], B,
+                                                      self._max_nodes))
+        return self._packed[1]
+
     def _native_waves_ok(self) -> bool:
         return self.native_waves and self._fused_eval_ok()
 
@@ -648,11 +661,17 @@ class FNNMCTSOrchestrator:
             cand = topk_slots.to(torch.int32)
             cvalid = torch.gather(valid_slot, 1, cand.long().clamp(min=0)) & (cand >= 0)
             cand = torch.where(cvalid, cand, torch.full_like(cand, -1))
+            base = gumbel + legal_logits
+            decide = None
+            if self.native_halving and cand.shape[1] <= 64:
+                hg_tree = self._packed_tree(tree, B)
+                decide = lambda c, final: self.ext.gumbel_halving(  # noqa: E731
+                    hg_tree, tree["root_node"], c, base, cfg.c_visit, cfg.c_scale, int(cfg.root_q_min_visits), final)
             chosen, sims = self._sequential_halving(
-                cand, gumbel + legal_logits,
+                cand, base,
                 lambda c, per_slot, wave: self._run_simulations_for_root_slots(tree, states, game_active, c, B,
                                                                                per_slot, wave),
-                lambda c: self._root_child_stats(tree, B, c))
+                lambda c: self._root_child_stats(tree, B, c), decide)
             slot_visits, slot_q = self._root_child_stats(tree, B, self._slot_idx.expand(B, -1))
             visited = (slot_visits > 0) & valid_slot
             max_n = slot_visits.float().max(dim=1, keepdim=True).values
@@ -676,7 +695,7 @@ class FNNMCTSOrchestrator:
             probs = torch.where(forced.unsqueeze(1), torch.zeros_like(probs), probs)
         return PlyResult(chosen, legal, nl, probs, slot_visits, has_actions, sims, stats, forced)
 
-    def _sequential_halving(self, cand, base, run_round, child_stats):
+    def _sequential_halving(self, cand, base, run_round, child_stats, decide=None):
         """Gumbel sequential halving (fnn_mcts_orchestrator.py:650-731).
 
         cand [B, C] int32 root slots (-1 = none); base [B, 256] = Gumbel noise +
@@ -687,7 +706,10 @@ class FNNMCTSOrchestrator:
         candidates by base[slot] + sigma * q, where (visits, q) = child_stats(cand)
         and sigma = (c_visit + the largest visit count of any candidate in the
         batch) * c_scale.  The final choice is the argmax of the same score over
-        the survivors.  Returns (chosen slot [B] int64, simulations run)."""
+        the survivors.  `decide(cand, final)`, when given, makes each of these
+        decisions in one call (hg_gumbel_halving) instead of the torch ops:
+        the next round's candidates, or with `final` the chosen slot.
+        Returns (chosen slot [B] int64, simulations run)."""
         cfg = self.config
         B = cand.shape[0]
         sims = 0
@@ -699,6 +721,9 @@ class FNNMCTSOrchestrator:
             sims += run_round(cand, max(1, per_round // C), wave)
             if C <= 1:
                 continue
+            if decide is not None:
+                cand = decide(cand, False)
+                continue
             keep_n = (cvalid.sum(dim=1) // 2).clamp(min=1)
             max_keep = C // 2
             visits, q = child_stats(cand)
@@ -709,6 +734,8 @@ class FNNMCTSOrchestrator:
             keep_ok = torch.arange(max_keep, device="cuda").unsqueeze(0) < keep_n.unsqueeze(1)
             cand = torch.where(keep_ok, torch.gather(cand, 1, keep_pos), torch.full_like(keep_pos, -1,
                                                                                         dtype=torch.int32))
+        if decide is not None:
+            return decide(cand, True), sims
         cvalid = cand >= 0
         visits, q = child_stats(cand)
         sigma = (cfg.c_visit + visits.max()) * cfg.c_scale

@@ -375,6 +375,24 @@ int hg_mcts_root_noise(const hg_tree* tree, const float* noise, const int32_t* r
 int hg_mcts_wave_stats(const int32_t* leaf_idx, const int32_t* num_legal, const int32_t* vl_lens, int64_t total,
                        int64_t* stats, void* stream);
 
+/* One decision of the Gumbel root search's sequential halving
+ * (fnn_mcts_orchestrator.py:650-731: the statistics of the candidates' root
+ * children, the batch-global sigma, the scores and the survivors; no single
+ * reference entry point -- the reference runs these as torch ops between
+ * rounds).  candidates[B][C] root slots (-1 = none), 1 <= C <= 64; base[B][256]
+ * the Gumbel draw + legal logit of every slot.  A column's visits N and Q
+ * (-W / max(N, 1) when N > root_q_min_visits, else 0) are those of the root
+ * child in its slot (0, 0 outside the root's children); sigma = (c_visit + the
+ * largest candidate N of the batch) * c_scale; score = base[g][slot] + sigma *
+ * Q, -1e30 for an empty column.  keep > 0 (= C / 2 between rounds): the
+ * columns in descending score order (ties to the lower column), the first
+ * keep written to cand_out[B][keep] -- the first max(1, nonempty / 2) as
+ * their slots, the rest -1.  keep = 0 (the final choice): chosen[g] = the
+ * slot of the first highest column, 0 when it is empty. */
+int hg_gumbel_halving(const hg_tree* tree, const int32_t* root_nodes, const int32_t* candidates, int C,
+                      const float* base, float c_visit, float c_scale, int root_q_min_visits, int keep, int64_t B,
+                      int32_t* cand_out, int64_t* chosen, void* stream);
+
 /* ---- one simulation wave of the Gumbel root search, launched natively ----
  * The body of the reference's per-wave loop (fnn_mcts_orchestrator.py:982-1055:
  * mcts_select_replay_legal_fnn_root_slots_batch, the FNN leaf evaluation,

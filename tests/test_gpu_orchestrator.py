@@ -559,6 +559,81 @@ def test_sequential_halving_known_answers(name):
     assert sims == sum(ps * len(r[0]) * len(r) for r, ps, _ in calls)
 
 
+@pytest.mark.parametrize("name", ["k16-schedule", "k16-w1", "k64-schedule"])
+def test_halving_kernel_known_answers(name):
+    """The same hand-worked halving cases through hg_gumbel_halving: each
+    round's statistics are written into a tree (root 0, its 256 children at
+    nodes 1-256: N = the stub's visits, W = -Q * N), and every decision --
+    survivors and the final choice -- is the kernel's."""
+    import torch
+    from orchestrator_cases import HALVING_CASES, HalvingStub, halving_base, q_of
+    over, rows, calls, chosen = HALVING_CASES[name]
+    orch = _bare_orch(**over)
+    B = len(rows)
+    tree = orch._alloc_tree(B)
+    tree["first_child"][:, 0] = 1
+    tree["num_children"][:, 0] = 256
+    stub = HalvingStub()
+    hg_tree = orch.ext.tree_struct(*orch._tree_args(tree), tree["child_init_q"], B, tree["visit_count"].shape[1])
+    base = torch.from_numpy(halving_base(B)).cuda()
+
+    def run_round(c, ps, w):
+        n = stub.run_round(c.cpu().numpy(), ps, w)
+        r = len(stub.calls) - 1
+        vc = np.zeros((B, 256), np.int32)
+        tv = np.zeros((B, 256), np.float32)
+        for (g, slot), v in stub.visits.items():
+            vc[g, slot] = v
+            tv[g, slot] = np.float32(-np.float32(q_of(r, g, slot)) * np.float32(v))
+        tree["visit_count"][:, 1:257] = torch.from_numpy(vc).cuda()
+        tree["total_value"][:, 1:257] = torch.from_numpy(tv).cuda()
+        return n
+
+    def decide(c, final):
+        return orch.ext.gumbel_halving(hg_tree, tree["root_node"], c.contiguous(), base, orch.config.c_visit,
+                                       orch.config.c_scale, 0, final)
+
+    cand = torch.tensor(rows, dtype=torch.int32, device="cuda")
+    got, sims = orch._sequential_halving(cand, base, run_round, None, decide)
+    assert stub.calls == calls
+    assert got.cpu().tolist() == chosen
+
+
+@pytest.mark.parametrize("k,kw", [
+    (16, {}), (16, {"wave_parallel": False}), (5, {}), (64, {"root_q_min_visits": 3}), (3, {"c_scale": 0.1}),
+], ids=["k16", "k16-w1", "k5", "k64-minvisits", "k3-scale"])
+def test_native_halving_equals_torch(k, kw):
+    """Sequential halving decided by hg_gumbel_halving against the torch ops
+    on the same searches: three plies with rebases, every ply's choice,
+    policy and visits and the final trees bit-identical."""
+    import torch
+    from hive_neuralnet_amd import hive_gpu
+    outs = []
+    for native in (False, True):
+        B = 24
+        orch, _, tree = _setup(B, 128, 1 << 14, 7, 70, 101, max_num_considered_actions=k, **kw)
+        orch.native_halving = native
+        orch.use_graphs = False
+        states, _ = hive_gpu.random_positions(B, 7, 70, 102)
+        torch.manual_seed(103)
+        np.random.seed(103)
+        active = torch.ones((B,), dtype=torch.bool, device="cuda")
+        rec = []
+        for _ in range(3):
+            r = orch.search_ply(states, tree, active)
+            rec.append((_np(r.chosen_slot), _np(r.policy), _np(r.slot_visits)))
+            orch.apply_and_rebase(states, tree, r)
+            active &= orch.ext.check_results_batch(states, B) == 0
+        assert (orch._packed is not None) == native
+        rec.append({kk: _np(v).copy() for kk, v in tree.items()})
+        outs.append(rec)
+    for a, b in zip(outs[0][:3], outs[1][:3]):
+        for x, y in zip(a, b):
+            assert np.array_equal(x.view(np.uint32) if x.dtype == np.float32 else x,
+                                  y.view(np.uint32) if y.dtype == np.float32 else y)
+    assert tree_equal(outs[0][3], outs[1][3]) == []
+
+
 @pytest.mark.parametrize("case", [0, 1])
 def test_reserve_candidates_known_answers(case):
     """The reserve rule on the hand-built positions of tests/orchestrator_cases.py:
