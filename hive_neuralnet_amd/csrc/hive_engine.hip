@@ -94,18 +94,22 @@ __global__ __launch_bounds__(256) void k_order_buckets(const uint8_t* __restrict
 
 // item s of the ordered launch (buckets from the latest turns down): lane
 // k < 32 of the group holds the count of bucket 31 - k and its exclusive
-// prefix; the item's bucket is the last one whose prefix is <= s
-__device__ __forceinline__ int64_t ordered_item(int64_t s, const int32_t* __restrict__ counts,
-                                                const int32_t* __restrict__ lists, int64_t B, int lane) {
+// prefix; the item's bucket is the last one whose prefix is <= s.  32-bit
+// index math (the entry point takes B < 2^31); the result is kept inside
+// the batch even for a workspace used against its contract.
+__device__ __forceinline__ uint32_t ordered_item(int s, const int32_t* __restrict__ counts,
+                                                 const int32_t* __restrict__ lists, int B, int lane) {
     static_assert(kOrderBuckets == kW, "one bucket per lane of the group");
     const int k = gl(lane);
     const int c = counts[kOrderBuckets - 1 - k];
     const int excl = grp_excl_scan(c);
-    const uint32_t le = grp_ballot(excl <= s, lane);
+    const uint32_t le = grp_ballot(excl <= s, lane);  // lane 0's prefix is 0 <= s
     const int j = 31 - __clz(le);  // prefixes are non-decreasing: the highest lane with excl <= s
     const int start = grp_shfl(excl, j, lane);
-    const int64_t off = s - start;  // in [0, B) for counts that sum to B
-    return lists[(int64_t)(kOrderBuckets - 1 - j) * B + (off < 0 ? 0 : (off < B ? off : B - 1))];
+    const uint32_t last = (uint32_t)(B - 1);
+    const uint32_t off = min((uint32_t)max(s - start, 0), last);
+    const uint32_t p = (uint32_t)lists[(size_t)(uint32_t)(kOrderBuckets - 1 - j) * (uint32_t)B + off];
+    return min(p, last);
 }
 
 // 6 waves per SIMD: the register cap (80 VGPRs, a few bytes of spill) pays
@@ -119,10 +123,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(6))) void k_
     __shared__ Pos PS[kPosPerWave];
     bool live;
     int64_t pos = item_of(B, live);
-    if (Ordered) {  // kept inside the batch even for a workspace used against its contract
-        pos = ordered_item(pos, counts, lists, B, threadIdx.x);
-        pos = pos < 0 ? 0 : (pos >= B ? B - 1 : pos);
-    }
+    if (Ordered) pos = ordered_item((int)pos, counts, lists, (int)B, threadIdx.x);
     run_legal<WithMoves, WithFeat, WithAct>(PS[threadIdx.x >> 5], states + pos * kStateBytes, threadIdx.x,
                                             live ? moves_out + pos * (kMaxLegal * 6) : nullptr,
                                             live ? n_out + pos : nullptr,
@@ -459,7 +460,7 @@ int hg_legal_features_actions_ordered(const uint8_t* states, int64_t B, uint8_t*
                                       float* features, int32_t* actions, void* workspace, int parity,
                                       void* stream) {
     if (B <= 0) return 0;
-    if (!workspace || (parity & ~1)) return (int)hipErrorInvalidValue;
+    if (!workspace || (parity & ~1) || B > INT32_MAX) return (int)hipErrorInvalidValue;
     hipStream_t s = (hipStream_t)stream;
     int32_t* counts = reinterpret_cast<int32_t*>(workspace) + parity * kOrderBuckets;
     int32_t* clear = reinterpret_cast<int32_t*>(workspace) + (parity ^ 1) * kOrderBuckets;

@@ -39,11 +39,8 @@ HW_INL ListInfo generate_legal(Pos& P, int lane) {
     const int ptn = P.turn >> 1;
     const bool queen_down = (P.qplaced >> me) & 1;
     const bool queen_now = (ptn == 3) && !queen_down;
-    uint32_t placeable = 0;
-    for (int p = 0; p < 8; p++) {
-        bool ok = queen_now ? (p == 0 && P.hand[me][0] > 0) : (P.hand[me][p] > 0);
-        if (ok && go) placeable |= 1u << p;
-    }
+    const uint32_t held = hand_mask(P, me);
+    const uint32_t placeable = go ? (queen_now ? (held & 1u) : held) : 0u;
     uint32_t emit_types = placeable & ~(ptn == 0 ? 1u : 0u);
     int ntypes = __popc(emit_types);
 
@@ -68,40 +65,37 @@ HW_INL ListInfo generate_legal(Pos& P, int lane) {
     }
     int n_place = npos * ntypes;
 
-    // -- movable pieces: own top cells, not stunned, not pinned (cell order)
+    // -- movable pieces (own top cells, not stunned, not pinned) and throw
+    // actors, both in cell order: one lane per occupied cell (the list is
+    // ascending), ranks by ballot.  The thrower is not checked for stun or
+    // pin (move_gen.cuh:1304-1345).
     int n_pieces = 0, n_actors = 0;
     if (go && queen_down) {
-        uint32_t mw = 0;
-        if (l < 18) {
-            const uint32_t* mine = me ? P.bt : P.wt;
-            mw = mine[l + 1] & ~P.pin[l + 1];
-            if (P.stun != 0xFFFF && (P.stun >> 5) == l) mw &= ~(1u << (P.stun & 31));
-        }
-        int k = grp_excl_scan(__popc(mw));
-        n_pieces = min(grp_sum(__popc(mw), lane), kMaxPieces);
-        while (mw && k < kMaxPieces) {
-            int b = __ffs(mw) - 1;
-            mw &= mw - 1;
-            int c = l * 32 + b;
-            P.piece_cell[k] = (uint16_t)c;
-            P.piece_type[k] = P.tp(c) & 15;
-            k++;
-        }
-        // throw actors among occupied cells (cell order); the thrower is not
-        // checked for stun or pin (move_gen.cuh:1304-1345)
-        bool actor = false;
+        bool movable = false, actor = false;
+        int c = 0, tb = 0;
         if (l < P.n_occ) {
-            int c = P.occ_cells[l];
-            int tb = P.tp(c);
-            int t = tb & 15;
+            c = P.occ_cells[l];
+            tb = P.tp(c);
+            const int t = tb & 15;
+            movable = pb_get(me ? P.bt : P.wt, c) && !pb_get(P.pin, c) && c != (int)P.stun;
             if (((tb >> 4) & 1) == me)
                 actor = (t == PT_P) || (t == PT_M && P.hgt(c) == 1 && touches_top_pillbug(P, c));
         }
-        uint32_t am = grp_ballot(actor, lane);
+        const uint32_t below = (1u << l) - 1u;
+        const uint32_t pm = grp_ballot(movable, lane);
+        n_pieces = min(__popc(pm), kMaxPieces);
+        if (movable) {
+            const int k = __popc(pm & below);
+            if (k < kMaxPieces) {
+                P.piece_cell[k] = (uint16_t)c;
+                P.piece_type[k] = (uint8_t)(tb & 15);
+            }
+        }
+        const uint32_t am = grp_ballot(actor, lane);
         n_actors = min(__popc(am), kActors);
         if (actor) {
-            int r = __popc(am & ((1u << l) - 1u));
-            if (r < kActors) P.actor_cell[r] = P.occ_cells[l];
+            const int r = __popc(am & below);
+            if (r < kActors) P.actor_cell[r] = (uint16_t)c;
         }
     }
     __syncthreads();
@@ -404,6 +398,20 @@ __device__ __forceinline__ int round_half_even_div(int sum, int n) {
     return (q & 1) == 0 ? q : away;
 }
 
+// The same for |sum| <= 4096 and 1 <= n <= 64 (the occupied-cell list: |sum|
+// <= 32 * 11, n <= 32) without an integer division.
+// rcp_n is 1 / n to within 1 ulp, so f = sum * rcp_n is within 2^-10 of
+// x = sum / n.  Unless x is a half-integer it is at least 1 / (2n) >= 2^-7
+// from one, so rounding f to the nearest integer gives round(x); q is then
+// exact and d = 2 sum - 2 q n = 2n (x - q) tells an exact tie (|d| == n),
+// which goes to the even one of q and q + sign(d).
+__device__ __forceinline__ int round_half_even_div(int sum, int n, float rcp_n) {
+    const int q = (int)__builtin_rintf((float)sum * rcp_n);
+    const int d = 2 * (sum - q * n);
+    if (d == n || d == -n) return (q & 1) ? q + (d > 0 ? 1 : -1) : q;
+    return q;
+}
+
 // compute_centroid (state_encoder.cuh:889-906) over the occupied-cell list
 HW_INL void centroid(const Pos& P, int lane, int& cq, int& cr) {
     const int l = gl(lane);
@@ -415,8 +423,9 @@ HW_INL void centroid(const Pos& P, int lane, int& cq, int& cr) {
         r = row - kHalf;
     }
     int sq = grp_sum(q, lane), sr = grp_sum(r, lane), n = P.n_occ;
-    cq = n ? round_half_even_div(sq, n) : 0;
-    cr = n ? round_half_even_div(sr, n) : 0;
+    const float rcp_n = __builtin_amdgcn_rcpf((float)(n ? n : 1));
+    cq = n ? round_half_even_div(sq, n, rcp_n) : 0;
+    cr = n ? round_half_even_div(sr, n, rcp_n) : 0;
 }
 
 __device__ __forceinline__ int window17(int cell, int cq, int cr) {
@@ -672,12 +681,8 @@ HW_INL uint32_t compact_summary(Pos& P, int lane, int* n_place) {
     const int ptn = P.turn >> 1;
     const bool queen_down = (P.qplaced >> me) & 1;
     const bool queen_now = (ptn == 3) && !queen_down;
-    bool any = false;
-    for (int p = 0; p < 8; p++) {
-        bool ok = queen_now ? (p == 0 && P.hand[me][0] > 0) : (P.hand[me][p] > 0);
-        if (ptn == 0 && p == 0) ok = false;
-        any = any || ok;
-    }
+    const uint32_t held = hand_mask(P, me);
+    const bool any = ((queen_now ? (held & 1u) : held) & ~(ptn == 0 ? 1u : 0u)) != 0;
     const int l = gl(lane);
     uint32_t pw = 0;
     if (any && l < 18) {

@@ -189,6 +189,21 @@ struct alignas(16) Pos {
     }
 };
 
+static_assert(offsetof(Pos, hand) % 4 == 0, "hand rows are read as two dwords each");
+
+// Bit p set when colour col holds pieces of type p + 1 in hand.  Four hand
+// bytes at a time: bit 7 of (b & 0x7F) + 0x7F, or'ed with b, is set iff b is
+// non-zero (no carry leaves a byte); the bits 7, 15, 23, 31 are gathered to
+// bits 28..31 by one multiply (the partial products land on distinct bits).
+__device__ __forceinline__ uint32_t hand_mask(const Pos& P, int col) {
+    const uint32_t* h = reinterpret_cast<const uint32_t*>(P.hand[col]);
+    auto nz4 = [](uint32_t x) {
+        const uint32_t t = ((((x & 0x7F7F7F7Fu) + 0x7F7F7F7Fu) | x) & 0x80808080u) >> 7;
+        return (t * 0x10204080u) >> 28;
+    };
+    return nz4(h[0]) | (nz4(h[1]) << 4);
+}
+
 // MOVE sources per (type, owner) and PLACE destinations of a caller-supplied
 // list, as bitboards over all cells (the list may name any cell)
 struct ListSets {
