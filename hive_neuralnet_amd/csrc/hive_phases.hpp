@@ -474,21 +474,42 @@ HW_INL void place_list(Pos& P, int lane) {
 
 // Writes the generated list: moves (zero padded), action indices (-1
 // padded), and the MOVE-source sets of the features (one bit per piece
-// segment that is inside the cut, one per throw entry).  Placement slot i
-// is cell i / ntypes of the placement list with the (i % ntypes)-th
-// placeable type (the quotient by a multiply: (i * ceil(65536 / ntypes))
-// >> 16 is exact for i < 256, ntypes <= 8); later slots are decoded by
-// list_slot.
+// segment that is inside the cut, one per throw entry), the latter one lane
+// per segment before the slots.  Placement slot i is cell i / ntypes of the
+// placement list with the (i % ntypes)-th placeable type (the quotient by a
+// multiply: (i * ceil(65536 / ntypes)) >> 16 is exact for i < 256, ntypes
+// <= 8); later slots are decoded by list_slot.  A piece's action window
+// index comes from P.piece_win (set after the centroid, behind a barrier).
 template <bool WithMoves, bool WithAct, bool WithFeat>
 HW_INL void emit_list(Pos& P, const ListInfo& L, int lane, uint8_t* __restrict__ moves_row,
                       int32_t* __restrict__ act_row, int cq, int cr) {
     const int me = P.turn & 1;
     const int l = gl(lane);
+    if (WithFeat && L.total > 0) {
+        const int s = l + 1;  // segment s: piece s - 1, or throw actor s - 1 - n_pieces
+        if (s <= L.n_pieces) {
+            const int j = s - 1;
+            const int c = P.piece_cell[j], pt = P.piece_type[j];
+            if (P.piece_cnt[j] > 0 && P.seg_base[s] < L.n && c < kCells && pt >= 1 && pt <= 8) {
+                const int r = occ_rank(P, c);  // sources of generated moves are occupied
+                if (r < 32) atomicOr(&P.u1.e.from_d[(pt - 1) * 2 + me], 1u << r);
+            }
+        } else if (s < L.nseg) {
+            const int j = s - 1 - L.n_pieces, base = P.seg_base[s];
+            for (int k = 0; k < (int)P.throw_cnt[j] && base + k < L.n; k++) {
+                const int c = P.throw_from[j][k], pt = P.throw_pt[j][k];
+                if (c < kCells && pt >= 1 && pt <= 8) {
+                    const int r = occ_rank(P, c);
+                    if (r < 32) atomicOr(&P.u1.e.from_d[(pt - 1) * 2 + ((P.tp(c) >> 4) & 1)], 1u << r);
+                }
+            }
+        }
+    }
     uint16_t* row16 = reinterpret_cast<uint16_t*>(moves_row);
     const uint32_t nt = (uint32_t)(L.ntypes > 0 ? L.ntypes : 1);
     const uint32_t inv = (65536u + nt - 1u) / nt;
     for (int i = l; i < L.n; i += kW) {
-        int tp = 0, from = 0, to = 0;
+        int tp = 0, from = 0, to = 0, wfrom = 0;  // wfrom: window index of a MOVE's source
         if (L.total == 0) {
             tp = MV_PASS;
         } else if (i < L.n_place && i < kPlist) {  // cell rank <= i
@@ -498,14 +519,9 @@ HW_INL void emit_list(Pos& P, const ListInfo& L, int lane, uint8_t* __restrict__
         } else {
             int seg;
             list_slot(P, L, i, tp, from, to, seg);
-            if (WithFeat && seg > 0) {
-                bool thr = seg > L.n_pieces;
-                int pt = tp >> 8;
-                if ((thr || i == P.seg_base[seg]) && from < kCells && pt >= 1 && pt <= 8) {
-                    int owner = thr ? (P.tp(from) >> 4) & 1 : me;
-                    int r = occ_rank(P, from);  // sources of generated moves are occupied
-                    if (r < 32) atomicOr(&P.u1.e.from_d[(pt - 1) * 2 + owner], 1u << r);
-                }
+            if (WithAct) {
+                if (seg > L.n_pieces) wfrom = window17(from, cq, cr);  // throws
+                else if (seg > 0) wfrom = P.piece_win[seg - 1];
             }
         }
         if (WithMoves) {
@@ -513,7 +529,16 @@ HW_INL void emit_list(Pos& P, const ListInfo& L, int lane, uint8_t* __restrict__
             row16[3 * i + 1] = (uint16_t)from;
             row16[3 * i + 2] = (uint16_t)to;
         }
-        if (WithAct) act_row[i] = move_action(tp & 0xFF, tp >> 8, from, to, cq, cr);
+        if (WithAct) {  // gpu_move_to_action (mcts_tree.cuh:146-179) with the source's window given
+            const int type = tp & 0xFF;
+            int a = 85833;
+            if (type != MV_PASS) {
+                const int b = window17(to, cq, cr);
+                if (type == MV_PLACE) a = b < 0 ? -1 : ((tp >> 8) - 1) * 289 + b;
+                else a = (wfrom < 0 || b < 0) ? -1 : 2312 + wfrom * 289 + b;
+            }
+            act_row[i] = a;
+        }
     }
     // the rest of the rows: zero moves and -1 action indices, in 16-byte stores
     // (rows are 16-byte aligned: 1,536 and 1,024 bytes per position)
@@ -835,7 +860,10 @@ HW_INL void run_legal(Pos& P, const uint8_t* __restrict__ S, int lane, uint8_t* 
     place_list(P, lane);
     if (WithFeat) sources_clear(P, lane);
     int cq = 0, cr = 0;
-    if (WithAct) centroid(P, lane, cq, cr);
+    if (WithAct) {
+        centroid(P, lane, cq, cr);
+        if (gl(lane) < L.n_pieces) P.piece_win[gl(lane)] = (int16_t)window17(P.piece_cell[gl(lane)], cq, cr);
+    }
     __syncthreads();
     if (moves_row) emit_list<WithMoves, WithAct, WithFeat>(P, L, lane, moves_row, act_row, cq, cr);
     if (gl(lane) == 0 && n_slot) *n_slot = L.n;

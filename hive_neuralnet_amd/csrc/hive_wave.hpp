@@ -57,6 +57,7 @@ constexpr int kThrowCap = 9;
 constexpr int kSets = 8;  // visited / dedup sets: 3 ants, 2 spiders, 1 ladybug, 1 mosquito (2)
 constexpr int kPlist = 240;  // placement cells kept for emission (a board has <= 60)
 constexpr int kSegs = 1 + kMaxPieces + kActors + 1;  // placements, pieces, actors, end
+constexpr int kArtN = 28;  // vertices (occupied cells in cell order) the articulation test covers
 constexpr int kW = 32;               // lanes per position
 constexpr int kPosPerWave = 64 / kW;  // positions per wavefront
 
@@ -97,21 +98,25 @@ __device__ __forceinline__ uint32_t rotr6(uint32_t n) { return ((n >> 1) | (n <<
 
 __device__ __forceinline__ int pb_get(const uint32_t* pb, int c) { return (int)((pb[(c >> 5) + 1] >> (c & 31)) & 1u); }
 
-// 6-bit mask of directions d whose neighbour is on-grid and set in pb.
-// Bits c-23 .. c+40 are gathered into one 64-bit window; direction d sits at
-// window bit win_ofs(d).
-__device__ __forceinline__ uint32_t nbr_bits_raw(const uint32_t* pb, int c) {
-    int lo = c - 23;
+// 64 board bits starting at bit lo (>= -32) of a padded bitboard
+__device__ __forceinline__ uint64_t bit_window(const uint32_t* pb, int lo) {
     int wi = (lo >> 5) + 1;
     int sh = lo & 31;
     uint64_t w01 = (uint64_t)pb[wi] | ((uint64_t)pb[wi + 1] << 32);
     uint64_t win = w01 >> sh;
     if (sh) win |= (uint64_t)pb[wi + 2] << (64 - sh);
-    uint32_t m = (uint32_t)((win >> 24) & 1u) | (uint32_t)(((win >> 1) & 1u) << 1) |
-                 (uint32_t)((win & 1u) << 2) | (uint32_t)(((win >> 22) & 1u) << 3) |
-                 (uint32_t)(((win >> 45) & 1u) << 4) | (uint32_t)(((win >> 46) & 1u) << 5);
-    return m;
+    return win;
 }
+// the six direction bits of a window that starts at cell c - 23
+__device__ __forceinline__ uint32_t ring_bits(uint64_t win) {
+    return (uint32_t)((win >> 24) & 1u) | (uint32_t)(((win >> 1) & 1u) << 1) |
+           (uint32_t)((win & 1u) << 2) | (uint32_t)(((win >> 22) & 1u) << 3) |
+           (uint32_t)(((win >> 45) & 1u) << 4) | (uint32_t)(((win >> 46) & 1u) << 5);
+}
+// 6-bit mask of directions d whose neighbour is on-grid and set in pb.
+// Bits c-23 .. c+40 are gathered into one 64-bit window; direction d sits at
+// window bit win_ofs(d).
+__device__ __forceinline__ uint32_t nbr_bits_raw(const uint32_t* pb, int c) { return ring_bits(bit_window(pb, c - 23)); }
 __device__ __forceinline__ uint32_t nbr_bits(const uint32_t* pb, int c) { return nbr_bits_raw(pb, c) & grid6(c); }
 
 // 32 board bits starting at bit_off (>= -32) of a padded bitboard
@@ -154,6 +159,7 @@ struct alignas(16) Pos {
     uint8_t piece_type[kMaxPieces];
     uint16_t piece_off[kMaxPieces];
     uint8_t piece_cnt[kMaxPieces];
+    int16_t piece_win[kMaxPieces];  // action-window index of each piece cell (emission)
     uint16_t actor_cell[kActors];
     uint16_t throw_cnt[kActors];
     uint16_t throw_from[kActors][kThrowCap];
@@ -275,25 +281,26 @@ __device__ __forceinline__ uint32_t pack_cells4(uint32_t hts, uint32_t lv0, uint
 }
 
 // Heights, top bytes, bitboards and metadata of the state row S into P.
-// Lane l of the group takes the 16-cell chunks l and (l < 2) 32 + l: the
-// chunk's level-0 bytes (one 16-byte load) and its heights, which start at
-// the odd offset 2645 (a 16-byte and a 4-byte load, realigned in registers).
-// Every load of the position is issued before the first is used, so the
-// whole row costs one memory round trip; the top byte of a stack (height > 1)
-// is a second, rare, dependent load.
+// Lane l of the group takes the 16-cell chunk l (cells 16l .. 16l + 15): its
+// level-0 bytes (one 16-byte load) and its heights, which start at the odd
+// offset 2645 (a 16-byte and a 4-byte load, realigned in registers); lanes
+// 0-4 also take the four cells 512 + 4l .. 515 + 4l (cells 529-531 are past
+// the board: their height bytes are masked off).  Every load of the position
+// is issued before the first is used, so the whole row costs one memory
+// round trip; the top byte of a stack (height > 1) is a second, rare,
+// dependent load.
 HW_INL void load_position(Pos& P, const uint8_t* __restrict__ S, int lane) {
     const int l = gl(lane);
-    const bool two = l < 34 - kW;  // lanes 0, 1 also take chunks 32, 33
-    const int k1 = kW + l;
+    static_assert(kCells == 16 * kW + 17 && kW == 32, "32 chunks of 16 cells, then 17 cells in five words");
+    const bool tail = l < 5;
     u32x4 lv_a = *reinterpret_cast<const u32x4*>(S + 16 * l);
     u32x4 ht_a = *reinterpret_cast<const u32x4*>(S + (OFF_HEIGHT - 1) + 16 * l);
     uint32_t ht_a4 = *reinterpret_cast<const uint32_t*>(S + (OFF_HEIGHT - 1) + 16 * l + 16);
-    u32x4 lv_b = {0u, 0u, 0u, 0u}, ht_b = {0u, 0u, 0u, 0u};
-    uint32_t ht_b4 = 0;
-    if (two) {
-        lv_b = *reinterpret_cast<const u32x4*>(S + 16 * k1);
-        ht_b = *reinterpret_cast<const u32x4*>(S + (OFF_HEIGHT - 1) + 16 * k1);
-        ht_b4 = *reinterpret_cast<const uint32_t*>(S + (OFF_HEIGHT - 1) + 16 * k1 + 16);
+    uint32_t lv_t = 0, ht_t0 = 0, ht_t1 = 0;
+    if (tail) {
+        lv_t = *reinterpret_cast<const uint32_t*>(S + 512 + 4 * l);
+        ht_t0 = *reinterpret_cast<const uint32_t*>(S + (OFF_HEIGHT - 1) + 512 + 4 * l);
+        ht_t1 = *reinterpret_cast<const uint32_t*>(S + (OFF_HEIGHT - 1) + 516 + 4 * l);
     }
     const uint32_t* W = reinterpret_cast<const uint32_t*>(S + OFF_OCC);  // 8-byte aligned
     uint32_t occ_w = 0, wt_w = 0, bt_w = 0;
@@ -309,7 +316,7 @@ HW_INL void load_position(Pos& P, const uint8_t* __restrict__ S, int lane) {
     }
 
     uint32_t* cell32 = reinterpret_cast<uint32_t*>(P.cell);
-    uint32_t st_a = 0, st_b = 0;
+    uint32_t st_a = 0, st_t = 0;
     {
         u32x4 o;
         uint32_t s0, s1, s2, s3;
@@ -320,24 +327,18 @@ HW_INL void load_position(Pos& P, const uint8_t* __restrict__ S, int lane) {
         st_a = s0 | (s1 << 4) | (s2 << 8) | (s3 << 12);
         *reinterpret_cast<u32x4*>(cell32 + 4 * l) = o;
     }
-    if (two) {  // chunks 32 (cells 512-527) and 33 (528-543: only cell 528 is on the board)
-        const uint32_t keep = k1 == 33 ? 0xFFu : 0xFFFFFFFFu;
-        u32x4 o;
-        uint32_t s0, s1, s2, s3;
-        o[0] = pack_cells4(__builtin_amdgcn_alignbyte(ht_b[1], ht_b[0], 1) & keep, lv_b[0], s0);
-        o[1] = pack_cells4(k1 == 33 ? 0u : __builtin_amdgcn_alignbyte(ht_b[2], ht_b[1], 1), lv_b[1], s1);
-        o[2] = pack_cells4(k1 == 33 ? 0u : __builtin_amdgcn_alignbyte(ht_b[3], ht_b[2], 1), lv_b[2], s2);
-        o[3] = pack_cells4(k1 == 33 ? 0u : __builtin_amdgcn_alignbyte(ht_b4, ht_b[3], 1), lv_b[3], s3);
-        st_b = s0 | (s1 << 4) | (s2 << 8) | (s3 << 12);
-        *reinterpret_cast<u32x4*>(cell32 + 4 * k1) = o;
+    if (tail) {  // board word 128 + l; word 132 holds cell 528 only
+        const uint32_t keep = l == 4 ? 0xFFu : 0xFFFFFFFFu;
+        cell32[128 + l] = pack_cells4(__builtin_amdgcn_alignbyte(ht_t1, ht_t0, 1) & keep, lv_t, st_t);
+    } else if (l < 8) {
+        cell32[128 + l] = 0u;  // words 133-135: cells 532-543, past the board
     }
-    static_assert(kCells == 16 * 33 + 1, "the last chunk holds one board cell");
     // stacked tops: level min(h, 5) - 1 of the cell (h is the clamped height)
-    uint32_t st = st_a | (st_b << 16);
+    uint32_t st = st_a | (st_t << 16);
     while (st) {
         int b = __ffs(st) - 1;
         st &= st - 1;
-        int c = b < 16 ? 16 * l + b : 16 * k1 + (b - 16);
+        int c = b < 16 ? 16 * l + b : 512 + 4 * l + (b - 16);
         int h = P.cell[c] >> 5;
         int t = S[((h > 5 ? 5 : h) - 1) * kCells + c];
         P.cell[c] = (uint8_t)((h << 5) | (t & 31));
@@ -354,12 +355,11 @@ HW_INL void load_position(Pos& P, const uint8_t* __restrict__ S, int lane) {
     } else if (l == 24) {
         P.queen[0] = (uint16_t)m0;
         P.queen[1] = (uint16_t)(m0 >> 16);
-        for (int k = 0; k < 4; k++) {
-            P.hand[0][k] = (uint8_t)(m1 >> (8 * k));
-            P.hand[0][4 + k] = (uint8_t)(m2 >> (8 * k));
-            P.hand[1][k] = (uint8_t)(m3 >> (8 * k));
-            P.hand[1][4 + k] = (uint8_t)(m4 >> (8 * k));
-        }
+        uint32_t* hand32 = reinterpret_cast<uint32_t*>(P.hand);  // the 16 hand bytes, as in the row
+        hand32[0] = m1;
+        hand32[1] = m2;
+        hand32[2] = m3;
+        hand32[3] = m4;
         P.turn = (uint16_t)m5;  // turn u16, queen_placed u8, result u8
         P.qplaced = (uint8_t)(m5 >> 16);
         P.result = (uint8_t)(m5 >> 24);
@@ -464,14 +464,35 @@ __device__ __forceinline__ uint32_t spread4(uint32_t x) { return (x * 0x00204081
 // Ground-slide direction masks of the current occupancy (P.occ with zero
 // pads) for the board rows of the hive grown by one row each way (every hex
 // neighbour of an occupied cell lies in them; readers only look at occupied
-// cells and their neighbours), and the occupied-neighbour masks of the
-// occupied cells (nbd, by rank).  A lane takes four cells c..c+3 (one word of
+// cells and their neighbours), the occupied-neighbour masks of the occupied
+// cells (nbd, by rank) and the articulation test's adjacency rows (u1.adj).  A lane takes four cells c..c+3 (one word of
 // sm): their neighbours in direction d are bits k + OFS(d) of the occupancy
 // window starting at cell c - 23, spread to one byte per cell; the exit rule
 // gm & ~n & (rotl6(n) ^ rotr6(n)) then runs on the four bytes at once.
 HW_INL void build_cell_masks(Pos& P, int lane) {
     const int l = gl(lane);
-    if (l < P.n_occ) P.nbd[l] = (uint8_t)nbr_bits(P.occ, P.occ_cells[l]);
+    if (l < P.n_occ) {
+        const int c = P.occ_cells[l];
+        const uint64_t win = bit_window(P.occ, c - 23);  // bit k: cell c - 23 + k
+        const uint32_t nm = ring_bits(win) & grid6(c);
+        P.nbd[l] = (uint8_t)nm;
+        // the articulation flood's dense adjacency row of vertex l (ranks
+        // below kArtN): a neighbour's rank is l plus or minus the occupied
+        // cells between it and c, counted in the same window
+        const int N = min(P.n_occ, kArtN);
+        if (l < N) {
+            const uint32_t lo = (uint32_t)win, hi = (uint32_t)(win >> 24);
+            const int up = __popc(lo & 0x7FFFFEu);    // cells c-22 .. c-1
+            const int dn = __popc(hi & 0x1FFFFFu);    // cells c+1 .. c+21
+            const int rk[6] = {l + 1, l - up, l - up - (int)(lo & 1u), l - 1, l + 1 + dn,
+                               l + 1 + dn + (int)((hi >> 21) & 1u)};  // E NE NW W SW SE
+            uint32_t a = 0;
+#pragma unroll
+            for (int d = 0; d < 6; d++)
+                if (((nm >> d) & 1u) && rk[d] < N) a |= 1u << rk[d];
+            P.u1.adj[l] = a;
+        }
+    }
     uint32_t rowbits = l < kGrid ? (word_field(P.occ, kGrid * l) & 0x7FFFFFu) : 0u;
     uint32_t rows = grp_ballot(rowbits != 0, lane);
     if (rows == 0) return;
@@ -507,21 +528,9 @@ static_assert(sizeof(((Pos*)nullptr)->sm) >= 4 * 133, "sm holds whole words up t
 HW_INL void articulation(Pos& P, int lane) {
     const int l = gl(lane);
     int total = P.n_occ;
-    int N = total < 28 ? total : 28;
+    int N = total < kArtN ? total : kArtN;
     if (l < 20) P.pin[l] = 0;
-    if (l < N) {
-        int c = P.occ_cells[l];
-        uint32_t nm = P.nbd[l];  // occupied on-grid neighbours, written by this lane in build_cell_masks
-        uint32_t a = 0;
-        while (nm) {
-            int d = __ffs(nm) - 1;
-            nm &= nm - 1;
-            int j = occ_rank(P, step(c, d));
-            if (j < N) a |= 1u << j;
-        }
-        P.u1.adj[l] = a;
-    }
-    __syncthreads();
+    __syncthreads();  // the adjacency rows written by build_cell_masks
     if (total <= 2) return;
     int v = l < N ? l : -1;
     uint32_t vbit = v >= 0 ? (1u << v) : 0u;
