@@ -29,11 +29,12 @@ struct ListInfo {
     int n_pieces;   // piece segments
     int nseg;       // segments before the end marker
     uint32_t emit_types;
+    uint32_t type_list;  // the emitted placeable types, ascending, one per nibble
 };
 
 HW_INL ListInfo generate_legal(Pos& P, int lane) {
     const int l = gl(lane);
-    ListInfo L{0, 0, 0, 0, 0, 0, 0, 0u};
+    ListInfo L{0, 0, 0, 0, 0, 0, 0, 0u, 0u};
     const bool go = P.result == 0;  // barriers below are reached by both positions of the wave
     const int me = P.turn & 1;
     const int ptn = P.turn >> 1;
@@ -142,7 +143,8 @@ HW_INL ListInfo generate_legal(Pos& P, int lane) {
     int base = grp_excl_scan(cnt);
     int total = grp_sum(cnt, lane);
     int nseg = 1 + n_pieces + n_actors;
-    if (l <= nseg) P.seg_base[l] = (int16_t)min(base, 32767);
+    static_assert(kSegs <= kW, "one lane per segment start");
+    P.seg_base[l] = (int16_t)(l <= nseg ? min(base, 32767) : 32767);
     __syncthreads();
     if (!go) return L;
     L.total = total;
@@ -153,6 +155,7 @@ HW_INL ListInfo generate_legal(Pos& P, int lane) {
     L.n_pieces = n_pieces;
     L.nseg = nseg;
     L.emit_types = emit_types;
+    for (uint32_t m = emit_types, k = 0; m; m &= m - 1, k += 4) L.type_list |= (uint32_t)__ffs(m) << k;
     return L;
 }
 
@@ -175,13 +178,14 @@ __device__ __forceinline__ int select_bit(uint32_t x, int r) {
 // Slot i (i < L.n, L.total > 0) of the generated list as (type | pt << 8, from, to).
 HW_INL void list_slot(const Pos& P, const ListInfo& L, int i, int& tp, int& from, int& to, int& seg) {
     // last segment starting at or before i: five fixed halving steps over
-    // the non-decreasing starts (nseg <= 19 < 32)
+    // the non-decreasing starts (nseg <= 19 < 32; the end marker and the
+    // entries past it hold starts beyond every slot)
     static_assert(kSegs <= 32, "five steps cover the segments");
     int lo = 0;
 #pragma unroll
     for (int step = 16; step > 0; step >>= 1) {
         const int mid = lo + step;
-        if (mid < L.nseg && P.seg_base[mid] <= i) lo = mid;
+        if (P.seg_base[mid] <= i) lo = mid;
     }
     seg = lo;
     int k = i - P.seg_base[lo];
@@ -196,7 +200,7 @@ HW_INL void list_slot(const Pos& P, const ListInfo& L, int i, int& tp, int& from
         }
         to = wl * 32 + select_bit(P.plc[wl + 1], r - P.plc_pre[wl]);
         from = 0;
-        tp = MV_PLACE | ((select_bit(L.emit_types, ti) + 1) << 8);
+        tp = MV_PLACE | (((L.type_list >> (4 * ti)) & 15u) << 8);
     } else if (lo <= L.n_pieces) {
         int j = lo - 1;
         from = P.piece_cell[j];
@@ -515,7 +519,7 @@ HW_INL void emit_list(Pos& P, const ListInfo& L, int lane, uint8_t* __restrict__
         } else if (i < L.n_place && i < kPlist) {  // cell rank <= i
             const int r = (int)(((uint32_t)i * inv) >> 16);
             to = P.u1.e.plist[r];
-            tp = MV_PLACE | ((select_bit(L.emit_types, i - r * (int)nt) + 1) << 8);
+            tp = MV_PLACE | (((L.type_list >> (4 * (i - r * (int)nt))) & 15u) << 8);
         } else {
             int seg;
             list_slot(P, L, i, tp, from, to, seg);

@@ -145,7 +145,7 @@ struct alignas(16) Pos {
     uint8_t sm[532];  // ground-slide exits of each board cell with nothing lifted
     uint16_t occ_pre[20];  // occupied cells in board words before word w
     uint16_t plc_pre[20];  // placement cells in board words before word w
-    int16_t seg_base[kSegs];  // legal-list segment starts (placements, pieces, actors, end)
+    int16_t seg_base[32];  // legal-list segment starts (placements, pieces, actors, end); 32767 past the end
     uint16_t queen[2];
     uint16_t turn, stun;
     uint8_t hand[2][8];
