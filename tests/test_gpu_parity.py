@@ -191,6 +191,21 @@ def test_lockstep_selfplay_golden():
     assert np.array_equal(st.cpu().numpy(), g["finals"])
 
 
+def test_c4_full_lockstep(oracle):
+    """C4 at its configuration: all 16,384 lockstep games of the base game
+    from the empty board, up to 300 plies (Philox (seed, game, ply) move
+    choice); every final state byte and every game's ply count equal the
+    oracle's replay of the same games."""
+    from hive_neuralnet_amd.hive_gpu import random_positions
+    G, P, seed = 16384, 300, 0x5EED + 3
+    st, plies = random_positions(G, 0, P, seed, lockstep=True)
+    ost, oplies = oracle.lockstep_selfplay(G, 0, P, seed)
+    assert np.array_equal(plies.cpu().numpy(), oplies)
+    assert np.array_equal(st.cpu().numpy(), ost)
+    decided = int((ost[:, 3415] != 0).sum())
+    assert 0 < decided < G  # the run covers finished and unfinished games
+
+
 def test_edge_cases(ext, oracle):
     e = ext.create_initial_states(0)
     m, n = ext.generate_legal_moves_batch(e, 0)
