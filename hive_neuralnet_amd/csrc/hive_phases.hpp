@@ -30,11 +30,38 @@ struct ListInfo {
     int nseg;       // segments before the end marker
     uint32_t emit_types;
     uint32_t type_list;  // the emitted placeable types, ascending, one per nibble
+    int ub_total;        // gated lists: a bound on the whole list's length (the full list: total)
 };
 
-HW_INL ListInfo generate_legal(Pos& P, int lane) {
+// Which pieces generate_legal runs.  The full list runs every piece.  A gate
+// with kTargeted set may skip a piece (its segment is then empty) and may
+// stop the ant searches once they reach cell `stop`; generate_legal then
+// reports in ub_total a bound on the length of the whole list, with each
+// skipped or stopped piece counted at the most destinations it can have.
+struct FullList {
+    static constexpr bool kTargeted = false;
+    int stop = -1;
+    HW_INL bool run(const Pos&, int, int) const { return true; }
+};
+
+// The most destinations a piece of type t can have on a board whose hive has
+// e empty neighbour cells: sliding searches end on such cells (an ant or a
+// spider can end on no other; the origin is never one), the others have
+// their generators' bounds.
+__device__ __forceinline__ int dest_bound(int t, int e) {
+    switch (t) {
+        case PT_A: return min(e, kAntCap);
+        case PT_S: return min(e, 32);
+        case PT_L: return 32;
+        case PT_M: return 64;
+        default: return 6;
+    }
+}
+
+template <class Gate = FullList>
+HW_INL ListInfo generate_legal(Pos& P, int lane, const Gate& G = Gate()) {
     const int l = gl(lane);
-    ListInfo L{0, 0, 0, 0, 0, 0, 0, 0u, 0u};
+    ListInfo L{0, 0, 0, 0, 0, 0, 0, 0u, 0u, 0};
     const bool go = P.result == 0;  // barriers below are reached by both positions of the wave
     const int me = P.turn & 1;
     const int ptn = P.turn >> 1;
@@ -107,6 +134,13 @@ HW_INL ListInfo generate_legal(Pos& P, int lane) {
     int off = grp_excl_scan(cap);
     int nsets = l < n_pieces ? type_sets(P.piece_type[l]) : 0;
     int set0 = grp_excl_scan(nsets);
+    // gated lists: the empty cells next to the hive bound the sliding searches
+    int empties = 0;
+    if (Gate::kTargeted) {
+        const uint32_t ew = l < 18 ? nbr_union_word(P.occ, l) & ~P.occ[l + 1] : 0u;
+        empties = grp_sum(__popc(ew), lane);
+    }
+    int ub = 0;  // this lane's piece or throw actor, counted toward ub_total
     if (l < n_pieces && (off + cap > kPool || set0 + nsets > kSets)) {  // impossible piece counts
         P.piece_off[l] = 0;
         P.piece_cnt[l] = 0;
@@ -117,22 +151,29 @@ HW_INL ListInfo generate_legal(Pos& P, int lane) {
         uint32_t* s0 = P.u1.sets[set0 < kSets ? set0 : 0];
         uint32_t* s1 = P.u1.sets[set0 + 1 < kSets ? set0 + 1 : 0];
         int m = 0;
-        switch (t) {
-            case PT_Q: case PT_P: m = gen_step(P, c, out); break;
-            case PT_A: m = gen_ant(P, c, out, kAntCap, s0); break;
-            case PT_G: m = gen_hopper(P, c, out); break;
-            case PT_S: m = gen_spider(P, c, out, s0); break;
-            case PT_B: m = gen_beetle(P, c, out); break;
-            case PT_M: m = gen_mosquito(P, c, out, s0, s1); break;
-            case PT_L: m = gen_ladybug(P, c, out, s0); break;
-            default: break;
+        bool stopped = false;
+        const bool run = G.run(P, c, t);
+        if (run) {
+            switch (t) {
+                case PT_Q: case PT_P: m = gen_step(P, c, out); break;
+                case PT_A: m = gen_ant<Gate::kTargeted>(P, c, out, kAntCap, s0, G.stop, &stopped); break;
+                case PT_G: m = gen_hopper(P, c, out); break;
+                case PT_S: m = gen_spider(P, c, out, s0); break;
+                case PT_B: m = gen_beetle(P, c, out); break;
+                case PT_M: m = gen_mosquito<Gate::kTargeted>(P, c, out, s0, s1, G.stop, &stopped); break;
+                case PT_L: m = gen_ladybug(P, c, out, s0); break;
+                default: break;
+            }
         }
         P.piece_off[l] = (uint16_t)off;
         P.piece_cnt[l] = (uint8_t)m;
+        ub = (run && !stopped) ? m : dest_bound(t, empties);
     } else if (l >= kMaxPieces && l - kMaxPieces < n_actors) {
         int j = l - kMaxPieces;
         P.throw_cnt[j] = (uint16_t)gen_throws(P, P.actor_cell[j], P.throw_from[j], P.throw_to[j], P.throw_pt[j]);
+        ub = P.throw_cnt[j];
     }
+    if (Gate::kTargeted) L.ub_total = n_place + grp_sum(ub, lane);
     __syncthreads();
 
     // -- segment starts: lane 0 placements, lanes 1..n_pieces pieces, then actors, then the end
@@ -148,6 +189,7 @@ HW_INL ListInfo generate_legal(Pos& P, int lane) {
     __syncthreads();
     if (!go) return L;
     L.total = total;
+    if (!Gate::kTargeted) L.ub_total = total;
     L.n = total == 0 ? 1 : (total < kMaxLegal ? total : kMaxLegal);  // PASS = all-zero from/to, type 2
     L.n_place = n_place;
     L.npos = npos;

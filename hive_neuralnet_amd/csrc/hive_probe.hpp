@@ -101,15 +101,42 @@ HW_INL int lone_empty_cell(const Pos& P, int target) {
     return step(q, __ffs(e) - 1);
 }
 
-// has_immediate_surround_win_for_current_player (move_gen.cuh:853-874) on a
-// prepared board: some legal move to the lone empty neighbour of the
-// opponent's queen wins.  Uniform within the group.
-HW_INL bool immediate_win(Pos& P, int lane) {
+// hex distance between two cells of the 23x23 grid
+__device__ __forceinline__ int hex_distance(int a, int b) {
+    const int ra = row_of(a), rb = row_of(b);
+    const int dq = (b - rb * kGrid) - (a - ra * kGrid), dr = rb - ra, ds = -(dq + dr);
+    return max(max(abs(dq), abs(dr)), abs(ds));
+}
+
+// The pieces whose move to cell `stop` could win for the mover: the move's
+// result (the opponent queen's sixth neighbour filled, the mover's own queen
+// not surrounded with it) decides before any search, and the pieces that
+// cannot get there in their own way are left out: one-step movers (queen,
+// pillbug, beetle, a stacked mosquito) further than one cell, spiders and
+// ladybugs further than three, and the sliding movers (queen, pillbug, ant,
+// spider: their last step is a ground slide) when `stop` has no open side
+// with the piece lifted -- a slide into a cell is a slide out of it, so its
+// lifted slide exits (the exits of an empty cell) must not be empty.  Ant
+// searches stop on reaching the cell.
+struct WinGate {
+    static constexpr bool kTargeted = true;
+    int stop;
+    int win;  // the mover's winning result (1 or 2); 0: run nothing
+    HW_INL bool run(const Pos& P, int c, int t) const {
+        if (stop < 0 || win == 0) return false;
+        const int d = hex_distance(c, stop);
+        if ((t == PT_Q || t == PT_P || t == PT_B || (t == PT_M && P.hgt(c) > 1)) && d != 1) return false;
+        if ((t == PT_S || t == PT_L) && d > 3) return false;
+        if ((t == PT_Q || t == PT_P || t == PT_A || t == PT_S) && exits_lifted(P, stop, lift_of(P, c)) == 0)
+            return false;
+        return result_after(P, move_effect(P, MV_MOVE, t, c, stop)) == win;
+    }
+};
+
+// Moves of the (possibly gated) list L to `cell` that win for the mover: any
+// slot before the cut; uniform within the group.
+HW_INL bool wins_into(const Pos& P, const ListInfo& L, int cell, int lane) {
     const int me = P.turn & 1;
-    const int cell = lone_empty_cell(P, me ^ 1);
-    const bool any = hw_wave_any(cell >= 0);
-    if (!any) return false;  // neither group needs the list
-    ListInfo L = generate_legal(P, lane);
     bool hit = false;
     if (cell >= 0 && L.total > 0) {
         for (int i = gl(lane); i < L.n; i += kW) {
@@ -121,6 +148,35 @@ HW_INL bool immediate_win(Pos& P, int lane) {
         }
     }
     return grp_ballot(hit, lane) != 0;
+}
+
+// has_immediate_surround_win_for_current_player (move_gen.cuh:853-874) on a
+// prepared board: some legal move to the lone empty neighbour of the
+// opponent's queen wins, among the first 256 of the list.  Uniform within
+// the group.  First a gated list (WinGate): only the pieces whose move to the
+// cell would win are searched, the ant searches stop on the cell.  A gated
+// list without such a move decides (no piece of the whole list has one); a
+// gated list with one decides when the whole list is known to fit in 256
+// slots (ub_total), else the full list is generated and scanned as the
+// reference does.
+template <bool kGated = true>
+HW_INL bool immediate_win(Pos& P, int lane) {
+    const int me = P.turn & 1;
+    const int cell = lone_empty_cell(P, me ^ 1);
+    const bool any = hw_wave_any(cell >= 0);
+    if (!any) return false;  // neither group needs a list
+    if (!kGated) return wins_into(P, generate_legal(P, lane), cell, lane);
+    const WinGate gate{cell, cell >= 0 ? (me ? 2 : 1) : 0};
+    const ListInfo L = generate_legal(P, lane, gate);
+    bool hit = wins_into(P, L, cell, lane);
+    const bool sure = !hit || L.ub_total <= kMaxLegal;
+    if (hw_wave_any(!sure)) {  // a winning move that could lie past the cut
+        __syncthreads();
+        const ListInfo F = generate_legal(P, lane);
+        const bool full = wins_into(P, F, cell, lane);
+        if (!sure) hit = full;
+    }
+    return hit;
 }
 
 // board prepared for move generation (load_position done, moves applied)
@@ -210,7 +266,7 @@ HW_INL bool probe_screen(Pos& P, const uint8_t* __restrict__ S, const uint8_t* _
     if (gl(lane) == 0) apply_on_board(P, S, m[0], m[1], m[2] | (m[3] << 8), m[4] | (m[5] << 8));
     __syncthreads();
     prepare_loaded(P, lane);
-    return immediate_win(P, lane);
+    return immediate_win<false>(P, lane);
 }
 
 // the child's replies, kept while grandchildren are evaluated on the board
@@ -224,7 +280,7 @@ struct Replies {
 // p tests the replies whose slot is p modulo kWin2Parts), so a candidate with
 // many replies is not one long serial walk; the candidate passes when no part
 // fails.  kWin2Parts divides 32.
-constexpr int kWin2Parts = 8;
+constexpr int kWin2Parts = 16;
 
 // probe_win2: after root move m, does every reply keep the opponent's queen
 // surround at or above its level after m, and does every reply of this part

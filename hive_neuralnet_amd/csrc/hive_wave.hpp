@@ -716,8 +716,12 @@ __device__ __forceinline__ uint32_t exits_lifted(const Pos& P, int x, const Lift
 }
 
 // Queue entries are cell | (bit of the direction back to the parent) <<
-// kDirShift: that exit leads to a visited cell and is skipped.
-HW_INL int gen_ant(const Pos& P, int c, uint16_t* out, int cap, uint32_t* seen) {
+// kDirShift: that exit leads to a visited cell and is skipped.  kStop: the
+// search ends as soon as cell `stop` is discovered (*stopped set), leaving a
+// prefix of the list that ends with it.
+template <bool kStop = false>
+HW_INL int gen_ant(const Pos& P, int c, uint16_t* out, int cap, uint32_t* seen, int stop = -1,
+                   bool* stopped = nullptr) {
     set_clear(seen);
     set_insert(seen, c);
     const Lift lf = lift_of(P, c);
@@ -736,14 +740,26 @@ HW_INL int gen_ant(const Pos& P, int c, uint16_t* out, int cap, uint32_t* seen) 
                 const int d = __ffs(m) - 1;
                 m &= m - 1;
                 const int dest = base + (int)dir_byte(kOfsHi, kOfsLo, d);
-                if (set_insert(seen, dest)) *q++ = (uint16_t)(dest | (dir_byte(kOppHi, kOppLo, d) << kDirShift));
+                if (set_insert(seen, dest)) {
+                    *q++ = (uint16_t)(dest | (dir_byte(kOppHi, kOppLo, d) << kDirShift));
+                    if (kStop && dest == stop) {
+                        *stopped = true;
+                        return (int)(q - out);
+                    }
+                }
             }
         } else {
             while (m && q < end) {
                 const int d = __ffs(m) - 1;
                 m &= m - 1;
                 const int dest = base + (int)dir_byte(kOfsHi, kOfsLo, d);
-                if (set_insert(seen, dest)) *q++ = (uint16_t)(dest | (dir_byte(kOppHi, kOppLo, d) << kDirShift));
+                if (set_insert(seen, dest)) {
+                    *q++ = (uint16_t)(dest | (dir_byte(kOppHi, kOppLo, d) << kDirShift));
+                    if (kStop && dest == stop) {
+                        *stopped = true;
+                        return (int)(q - out);
+                    }
+                }
             }
         }
         if (h >= q || q >= end) break;
@@ -846,7 +862,9 @@ HW_INL int gen_ladybug(const Pos& P, int c, uint16_t* out, uint32_t* got) {
 // kMosqRoom slots hold the union so far (<= 64) and a sub-list (<= 32), and
 // a union past 64 entries (no state built by init/apply has one) stops the
 // merging before a sub-list could run past the room.
-HW_INL int gen_mosquito(const Pos& P, int c, uint16_t* out, uint32_t* tmpset, uint32_t* unionset) {
+template <bool kStop = false>
+HW_INL int gen_mosquito(const Pos& P, int c, uint16_t* out, uint32_t* tmpset, uint32_t* unionset, int stop = -1,
+                        bool* stopped = nullptr) {
     if (P.hgt(c) > 1) return gen_beetle(P, c, out);
     uint32_t gm = grid6(c);
     uint32_t om = nbo(P, c);
@@ -864,7 +882,7 @@ HW_INL int gen_mosquito(const Pos& P, int c, uint16_t* out, uint32_t* tmpset, ui
         int m = 0;
         switch (k) {
             case 0: if (has & ((1u << PT_Q) | (1u << PT_P))) m = gen_step(P, c, tail); break;
-            case 1: if (has & (1u << PT_A)) m = gen_ant(P, c, tail, kMosqRoom - n, tmpset); break;
+            case 1: if (has & (1u << PT_A)) m = gen_ant<kStop>(P, c, tail, kMosqRoom - n, tmpset, stop, stopped); break;
             case 2: if (has & (1u << PT_G)) m = gen_hopper(P, c, tail); break;
             case 3: if (has & (1u << PT_S)) m = gen_spider(P, c, tail, tmpset); break;
             case 4: if (has & (1u << PT_B)) m = gen_beetle(P, c, tail); break;
