@@ -88,6 +88,54 @@ void emu_queen_escape(const uint8_t* states, int64_t B, uint8_t* out) {
     });
 }
 
+// The gated list of the immediate-win test against the whole list, per
+// position: out[i] = {target cell, ub_total, whole-list total, gated hit,
+// whole-list hit (the first 256 slots)}.  The target is the lone empty
+// neighbour of the opponent's queen, else its first empty neighbour (a cell
+// no move wins into: the gate still runs its bound), else -1.
+void emu_gated_win(const uint8_t* states, int64_t B, int32_t* out) {
+    run_group(64, (B + kPosPerWave - 1) / kPosPerWave, [&](int64_t w, int t) {
+        int64_t i = w * kPosPerWave + t / kW;
+        bool live = i < B;
+        if (!live) i = B - 1;
+        Pos& P = g_pos[t / kW];
+        prepare(P, states + i * kStateBytes, t);
+        const int me = P.turn & 1, opp = me ^ 1;
+        int cell = lone_empty_cell(P, opp);
+        if (cell < 0 && ((P.qplaced >> opp) & 1) && P.queen[opp] < kCells) {
+            const int q = P.queen[opp];
+            const uint32_t e = grid6(q) & ~nbr_bits_raw(P.occ, q);
+            if (e) cell = step(q, __ffs(e) - 1);
+        }
+        const WinGate gate{cell, cell >= 0 ? (me ? 2 : 1) : 0};
+        const ListInfo L = generate_legal(P, t, gate);
+        const bool hg = wins_into(P, L, cell, t);
+        __syncthreads();
+        const ListInfo F = generate_legal(P, t);
+        const bool hf = wins_into(P, F, cell, t);
+        if (live && t % kW == 0) {
+            int32_t* o = out + 5 * i;
+            o[0] = cell;
+            o[1] = L.ub_total;
+            o[2] = F.total;
+            o[3] = hg ? 1 : 0;
+            o[4] = hf ? 1 : 0;
+        }
+    });
+}
+
+// has_immediate_surround_win_for_current_player as the probe runs it (immediate_win)
+void emu_immediate_win(const uint8_t* states, int64_t B, uint8_t* out) {
+    run_group(64, (B + kPosPerWave - 1) / kPosPerWave, [&](int64_t w, int t) {
+        int64_t i = w * kPosPerWave + t / kW;
+        bool live = i < B;
+        if (!live) i = B - 1;
+        prepare(g_pos[t / kW], states + i * kStateBytes, t);
+        const bool win = immediate_win(g_pos[t / kW], t);
+        if (live && t % kW == 0) out[i] = win ? 1 : 0;
+    });
+}
+
 // root_tactical_probe_batch: the group programs of hive_probe.hpp in the
 // order and with the bookkeeping of hive_probe.hip's launches
 void emu_root_probe(const uint8_t* states, const uint8_t* legal, const int32_t* nl, const float* pr, int64_t B, int f1,

@@ -161,3 +161,59 @@ def test_emulated_root_tactical_probe(emu):
     assert np.array_equal(win, g["win"][j][sel]), np.nonzero(win != g["win"][j][sel])[0][:8]
     assert np.array_equal(forced, g["forced"][j][sel])
     assert np.array_equal(allowed, g["allowed"][j][sel])
+
+
+def oracle_lone(oracle, s):
+    """lone_empty_neighbor_of_queen (move_gen.cuh:833-851) for the opponent of
+    the side to move, from the state bytes: its queen's on-grid neighbours
+    hold five pieces and one empty cell, that cell; else -1."""
+    del oracle
+    turn = int(s[3412]) | (int(s[3413]) << 8)
+    opp = (turn & 1) ^ 1
+    if not (int(s[3414]) >> opp) & 1:
+        return -1
+    q = int(s[3392 + 2 * opp]) | (int(s[3393 + 2 * opp]) << 8)
+    if q >= 529:
+        return -1
+    r, c = divmod(q, 23)
+    nbrs = [(r + dr) * 23 + (c + dc) for dr, dc in ((0, 1), (-1, 1), (-1, 0), (0, -1), (1, -1), (1, 0))
+            if 0 <= r + dr < 23 and 0 <= c + dc < 23]
+    occ = [x for x in nbrs if s[2645 + x] > 0]
+    empty = [x for x in nbrs if s[2645 + x] == 0]
+    return empty[0] if len(occ) == 5 and len(empty) == 1 else -1
+
+
+@pytest.mark.parametrize("mask,max_ply,seed", [(0, 150, 61), (7, 150, 62)])
+def test_emulated_gated_immediate_win(emu, oracle, mask, max_ply, seed):
+    """The probe's gated immediate-win list (WinGate) against the whole list
+    on random-play positions and their children, with the target the lone
+    empty neighbour of the opponent's queen (else another empty neighbour):
+    ub_total bounds the whole list's length, a gated list without a winning
+    move into the target means the whole list has none in its first 256
+    slots, and a gated hit decides whenever ub_total <= 256."""
+    st, _ = oracle.generate_positions(96, mask, max_ply, seed)
+    moves, n, _, _ = oracle.batch_legal_features_actions(st)
+    # children: every position's first legal moves applied, for more queens at five neighbours
+    kids = []
+    for i in range(len(st)):
+        for k in range(min(int(n[i]), 3)):
+            kids.append(oracle.apply_move(st[i], moves[i, k]))
+    st = np.concatenate([st, np.stack(kids)])
+    B = len(st)
+    out = np.zeros((B, 5), np.int32)
+    emu.emu_gated_win(_p(st), ctypes.c_int64(B), _p(out))
+    cell, ub, total, hg, hf = out.T
+    has = cell >= 0
+    assert has.sum() > B // 2
+    assert (ub[has] >= total[has]).all(), np.nonzero(has & (ub < total))[0][:8]
+    assert not (hf.astype(bool) & ~hg.astype(bool)).any()  # a gated miss is a whole-list miss
+    sure = hg.astype(bool) & (ub <= 256)
+    assert np.array_equal(hg[sure], hf[sure])
+    assert hf.sum() > 0  # the set holds immediate wins
+    # the probe's own test (gated list, the whole list when the cut could matter)
+    # against the whole list where the target is the queen's lone empty neighbour
+    win = np.zeros(B, np.uint8)
+    emu.emu_immediate_win(_p(st), ctypes.c_int64(B), _p(win))
+    lone = has & (np.array([oracle_lone(oracle, s) for s in st]) == cell)
+    assert np.array_equal(win[lone], hf[lone])
+    assert not win[~lone].any()
