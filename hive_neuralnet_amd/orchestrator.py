@@ -105,6 +105,20 @@ def topk_stable(x: torch.Tensor, k: int):
     return vals[:, :k], idx[:, :k]
 
 
+# The streams of the game ranges, one set per device for the whole process:
+# HIP maps streams onto a few hardware queues (4 by default), so streams made
+# afresh by every orchestrator would end up sharing queues with each other and
+# with the default stream, and the ranges would no longer overlap.
+_RANGE_STREAMS: dict = {}
+
+
+def _range_streams(parts: int) -> list:
+    pool = _RANGE_STREAMS.setdefault(torch.cuda.current_device(), [])
+    while len(pool) < parts:
+        pool.append(torch.cuda.Stream())
+    return pool
+
+
 class FNNMCTSOrchestrator:
     def __init__(self, net: HiveFNN, config: FNNMCTSConfig | None = None) -> None:
         self.ext = hive_gpu.load_extension()
@@ -144,7 +158,7 @@ class FNNMCTSOrchestrator:
         self.game_parts: int | None = None
         self.split_min_games = 256
         self.split_min_rows = 8192
-        self._part_streams: list = []
+        self.max_game_parts = 1  # the most game ranges a simulation phase has used
         self._part_ws: dict = {}
         # simulation waves as one library call each (hg_mcts_wave_root_slots:
         # the tree, network and per-simulation buffers prepared once per buffer
@@ -400,6 +414,7 @@ class FNNMCTSOrchestrator:
         else:
             parts = 2 if B >= self.split_min_games and W * C * B >= 2 * self.split_min_rows else 1
         if parts > 1 and B >= parts:
+            self.max_game_parts = max(self.max_game_parts, parts)
             return self._run_split(tree, root_states, game_active, root_slots, B, C, per_slot, W, q_penalty, parts)
         sims = 0
         for wave in range(math.ceil(per_slot / W)):
@@ -426,15 +441,14 @@ class FNNMCTSOrchestrator:
         array is per game ([B, ...] rows), so a range is a set of row views;
         the ranges share nothing but the device-atomic wave counters."""
         bounds = [(B * p) // parts for p in range(parts + 1)]
-        while len(self._part_streams) < parts:
-            self._part_streams.append(torch.cuda.Stream())
+        streams = _range_streams(parts)
         main = torch.cuda.current_stream()
         ready = torch.cuda.Event()
         ready.record(main)
         ranges = []
         for p in range(parts):
             lo, hi = bounds[p], bounds[p + 1]
-            s = self._part_streams[p]
+            s = streams[p]
             s.wait_event(ready)
             ranges.append((p, {k: v[lo:hi] for k, v in tree.items()}, root_states[lo:hi], game_active[lo:hi],
                            root_slots[lo:hi], hi - lo, s))

@@ -330,14 +330,14 @@ def _run(monkeypatch, wave_parallel, roots, plies=1, mask=0):
 
 def test_c5_schedule_midgame_roots_two_ranges(monkeypatch):
     orch, sh = _run(monkeypatch, True, "midgame")
-    assert len(orch._part_streams) == 2  # the default split ran: two game ranges on two streams
+    assert orch.max_game_parts == 2  # the default split ran: two game ranges on two streams
     # 4 rounds x 32 waves, each wave shadowed in both ranges
     assert sh.calls["mcts_select_with_root_slots_batch"] == 2 * 128
 
 
 def test_c5_one_simulation_per_wave_midgame_roots(monkeypatch):
     orch, sh = _run(monkeypatch, False, "midgame")
-    assert len(orch._part_streams) == 0  # 8,192-row waves stay on one range
+    assert orch.max_game_parts == 1  # 8,192-row waves stay on one range
     assert sh.calls["mcts_select_with_root_slots_batch"] == 64 + 128 + 256 + 512
 
 
