@@ -305,6 +305,18 @@ HW_INL void list_sources(Pos& P, const uint8_t* __restrict__ M, int n, int lane,
     }
 }
 
+// x / d rounded as IEEE division rounds it, for the features' divisors:
+// q = x * rd with rd = 1 / d rounded to float, then one residual step
+// q + fma(-q, d, x) * rd.  It gives the correctly rounded quotient for every
+// integer x in [0, 2^24) with d in {3, 10, 100, 200}, and for (s / n) / 10
+// with n <= 3, s < 4096 (both checked exhaustively against host division
+// under the wave emulator); with d = 1 or 2 every step is exact.  A quarter of
+// the instructions of the full division sequence.
+__device__ __forceinline__ float div_exact(float x, float d, float rd) {
+    const float q = x * rd;
+    return __builtin_fmaf(__builtin_fmaf(-q, d, x), rd, q);
+}
+
 // Needs sources_clear / counters_clear and the legal-move sets (modes kFeatList / kFeatGen)
 // complete, behind a barrier.
 HW_INL void features_finish(Pos& P, const uint8_t* __restrict__ S, float* __restrict__ out, int lane, int mode,
@@ -402,17 +414,20 @@ HW_INL void features_finish(Pos& P, const uint8_t* __restrict__ S, float* __rest
     static_assert(kW == 32 && kFeat == 122, "feature ranges per lane");
     if (!out) return;
     constexpr float kPer[8] = {1.f, 3.f, 3.f, 2.f, 2.f, 1.f, 1.f, 1.f};
+    constexpr float kRcpPer[8] = {1.f, 1.f / 3.f, 1.f / 3.f, 0.5f, 0.5f, 1.f, 1.f, 1.f};
     if (l < 16) {
         out[l] = (float)F.cnt[l];
     } else {
         int t = (l - 16) >> 1, c = (l - 16) & 1;
-        out[l] = (float)P.hand[c][t] / kPer[t];
+        out[l] = div_exact((float)P.hand[c][t], kPer[t], kRcpPer[t]);
     }
     if (l < 16) {
         out[32 + l] = (float)F.cnt[32 + l];
     } else {
-        int k = l - 16;
-        out[32 + l] = F.dcnt[k] > 0 ? (float)F.dsum[k] / (float)F.dcnt[k] / 10.0f : 0.0f;
+        // dcnt is a piece count of one type and colour, 1..3 when positive
+        int k = l - 16, n = F.dcnt[k];
+        const float rn = n == 3 ? 1.f / 3.f : n == 2 ? 0.5f : 1.f;
+        out[32 + l] = n > 0 ? div_exact(div_exact((float)F.dsum[k], (float)n, rn), 10.0f, 0.1f) : 0.0f;
     }
     out[64 + l] = (float)F.cnt[64 + l];
     if (l < kFeat - 96) {
@@ -420,9 +435,9 @@ HW_INL void features_finish(Pos& P, const uint8_t* __restrict__ S, float* __rest
         float v;
         if (i < 98) v = (float)F.cnt[i];
         else if (i < 100) v = F.covered[i - 98] ? 1.0f : 0.0f;
-        else if (i < 102) v = (i - 100) == me ? (float)F.cnt[100] / 10.0f : 0.0f;
-        else if (i == 102) { int left = 200 - (int)P.turn; v = (float)(left < 0 ? 0 : left) / 200.0f; }
-        else if (i == 103) { float t = (float)P.turn / 100.0f; v = t < 1.0f ? t : 1.0f; }
+        else if (i < 102) v = (i - 100) == me ? div_exact((float)F.cnt[100], 10.0f, 0.1f) : 0.0f;
+        else if (i == 102) { int left = 200 - (int)P.turn; v = div_exact((float)(left < 0 ? 0 : left), 200.0f, 0.005f); }
+        else if (i == 103) { float t = div_exact((float)P.turn, 100.0f, 0.01f); v = t < 1.0f ? t : 1.0f; }
         else if (i < 106) v = F.capable[i - 104] ? 1.0f : 0.0f;
         else if (i < 110) v = (float)F.cnt[i];
         else {

@@ -715,6 +715,43 @@ __device__ __forceinline__ uint32_t exits_lifted(const Pos& P, int x, const Lift
     return m;
 }
 
+// exits_lifted for the ant search, as a lookup: the lifted exits of the
+// origin's six neighbour cells are computed once per search and kept in 8
+// bytes {hi:lo} by ring slot.  The window position w = x - c + 23 of c's
+// neighbour in direction d is one of 24 1 0 22 45 46 (d = 0..5), and
+// ((w * 19) >> 4) & 7 sends these to the distinct slots 4 1 0 2 5 6; x is a
+// neighbour of c exactly when byte slot(w) of kRingW is w (slots 3 and 7 hold
+// 0, whose own slot is 0, so no w matches them).
+constexpr uint32_t kRingW[6] = {24, 1, 0, 22, 45, 46};
+constexpr uint32_t ring_slot_of(uint32_t w) { return ((w * 19u) >> 4) & 7u; }
+constexpr uint32_t kRingWLo = 0u | (1u << 8) | (22u << 16), kRingWHi = 24u | (45u << 8) | (46u << 16);
+static_assert(ring_slot_of(24) == 4 && ring_slot_of(1) == 1 && ring_slot_of(0) == 0 && ring_slot_of(22) == 2 &&
+                  ring_slot_of(45) == 5 && ring_slot_of(46) == 6,
+              "ring slots: byte s of {kRingWHi:kRingWLo} is the window position of slot s");
+__device__ __forceinline__ uint32_t ring_slot(uint32_t w) { return (__umul24(w, 19u) >> 4) & 7u; }
+struct RingLift {
+    int base;        // c - 23
+    uint32_t lo, hi;  // lifted exits by ring slot
+};
+HW_INL RingLift ring_lift(const Pos& P, int c) {
+    const Lift lf = lift_of(P, c);
+    uint32_t t[2] = {0u, 0u};
+#pragma unroll
+    for (int d = 0; d < 6; d++) {
+        const int x = c - 23 + (int)kRingW[d];
+        const uint32_t e = (unsigned)x < (unsigned)kCells ? lifted_exits(P.sm[x], d, lf.ox, lf.ey, lf.ez) : 0u;
+        const uint32_t s = ring_slot_of(kRingW[d]);
+        t[s >> 2] |= e << (8 * (s & 3));
+    }
+    return RingLift{c - 23, t[0], t[1]};
+}
+// exits_lifted(P, x, lift_of(P, c)) for any cell x
+__device__ __forceinline__ uint32_t exits_ring(const Pos& P, int x, const RingLift& rl) {
+    const uint32_t w = (uint32_t)(x - rl.base), s = ring_slot(w);
+    const uint32_t m = P.sm[x], lifted = __builtin_amdgcn_perm(rl.hi, rl.lo, 0x0c0c0c00u | s);
+    return __builtin_amdgcn_perm(kRingWHi, kRingWLo, 0x0c0c0c00u | s) == w ? lifted : m;
+}
+
 // Queue entries are cell | (bit of the direction back to the parent) <<
 // kDirShift: that exit leads to a visited cell and is skipped.  kStop: the
 // search ends as soon as cell `stop` is discovered (*stopped set), leaving a
@@ -724,7 +761,7 @@ HW_INL int gen_ant(const Pos& P, int c, uint16_t* out, int cap, uint32_t* seen, 
                    bool* stopped = nullptr) {
     set_clear(seen);
     set_insert(seen, c);
-    const Lift lf = lift_of(P, c);
+    const RingLift rl = ring_lift(P, c);
     // queue by pointers: q = next free entry, h = next entry to expand
     uint16_t* q = out;
     const uint16_t* h = out;
@@ -733,7 +770,7 @@ HW_INL int gen_ant(const Pos& P, int c, uint16_t* out, int cap, uint32_t* seen, 
     int cur = c;
     uint32_t back = 0;
     for (;;) {
-        uint32_t m = exits_lifted(P, cur, lf) & ~back;
+        uint32_t m = exits_ring(P, cur, rl) & ~back;
         const int base = cur - 23;
         if (q <= roomy) {
             while (m) {

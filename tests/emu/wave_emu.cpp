@@ -1,3 +1,4 @@
+#include <atomic>
 // wave_emu.cpp -- runs the engine's per-position programs (hive_phases.hpp)
 // on the host, one emulated 64-lane wave per call.  TEST INFRASTRUCTURE ONLY:
 // used by tests/test_emu_engine.py to check the device logic on the CPU and
@@ -122,6 +123,52 @@ void emu_gated_win(const uint8_t* states, int64_t B, int32_t* out) {
             o[4] = hf ? 1 : 0;
         }
     });
+}
+
+// The ant search's lifted-exit lookup against exits_lifted: every occupied
+// cell c as the origin, every cell x of the grid; returns the mismatches.
+int64_t emu_ring_exits_mismatches(const uint8_t* states, int64_t B) {
+    std::atomic<int64_t> bad{0};
+    run_group(64, (B + kPosPerWave - 1) / kPosPerWave, [&](int64_t w, int t) {
+        int64_t i = w * kPosPerWave + t / kW;
+        if (i >= B) i = B - 1;
+        Pos& P = g_pos[t / kW];
+        prepare(P, states + i * kStateBytes, t);
+        for (int c = 0; c < kCells; c++) {
+            if (!pb_get(P.occ, c)) continue;
+            const Lift lf = lift_of(P, c);
+            const RingLift rl = ring_lift(P, c);
+            for (int x = t % kW; x < kCells; x += kW)
+                if (exits_ring(P, x, rl) != exits_lifted(P, x, lf)) bad++;
+        }
+        __syncthreads();
+    });
+    return bad.load();
+}
+
+// div_exact against host IEEE division: the number of integers x in [lo, hi)
+// where div_exact(x, d, rd) differs from x / d
+int64_t emu_div_exact_mismatches(int64_t lo, int64_t hi, float d, float rd) {
+    int64_t bad = 0;
+    for (int64_t x = lo; x < hi; x++) {
+        const volatile float want = (float)x / d;
+        if (div_exact((float)x, d, rd) != want) bad++;
+    }
+    return bad;
+}
+
+// the same for the distance mean (s / n) / 10 of features_finish, n in 1..3, s in [0, smax)
+int64_t emu_div_mean_mismatches(int64_t smax) {
+    int64_t bad = 0;
+    for (int n = 1; n <= 3; n++) {
+        const float rn = n == 3 ? 1.f / 3.f : n == 2 ? 0.5f : 1.f;
+        for (int64_t s = 0; s < smax; s++) {
+            const volatile float m = (float)s / (float)n;
+            const volatile float want = m / 10.0f;
+            if (div_exact(div_exact((float)s, (float)n, rn), 10.0f, 0.1f) != want) bad++;
+        }
+    }
+    return bad;
 }
 
 // has_immediate_surround_win_for_current_player as the probe runs it (immediate_win)

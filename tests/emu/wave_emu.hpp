@@ -96,6 +96,7 @@ inline bool hw_wave_any(bool p) {
     wave_emu::wg_sync();
     return any;
 }
+inline uint32_t __umul24(uint32_t a, uint32_t b) { return (a & 0xFFFFFFu) * (b & 0xFFFFFFu); }
 inline uint32_t __builtin_amdgcn_alignbyte(uint32_t hi, uint32_t lo, uint32_t s) {
     return (uint32_t)(((((uint64_t)hi) << 32) | lo) >> (8 * (s & 3)));
 }

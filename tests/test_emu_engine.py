@@ -217,3 +217,35 @@ def test_emulated_gated_immediate_win(emu, oracle, mask, max_ply, seed):
     lone = has & (np.array([oracle_lone(oracle, s) for s in st]) == cell)
     assert np.array_equal(win[lone], hf[lone])
     assert not win[~lone].any()
+
+
+@pytest.mark.parametrize("d", [3.0, 10.0, 100.0, 200.0])
+def test_div_exact_matches_ieee_division(emu, d):
+    """features_finish divides by 3 (hand counts), 10, 100 and 200 with
+    div_exact (a reciprocal product and one residual step): every integer
+    numerator below 2^24 gives the quotient IEEE division gives."""
+    emu.emu_div_exact_mismatches.restype = ctypes.c_int64
+    rd = np.float32(1.0) / np.float32(d)
+    assert float(rd) == float(np.float32(1.0 / d))  # the literal the kernel uses
+    bad = emu.emu_div_exact_mismatches(ctypes.c_int64(0), ctypes.c_int64(1 << 24),
+                                       ctypes.c_float(d), ctypes.c_float(rd))
+    assert bad == 0
+
+
+def test_div_exact_distance_mean(emu):
+    """The distance-mean feature (s / n) / 10 for piece counts n = 1..3 and
+    every distance sum s below 4096, as two div_exact steps, equals the two
+    IEEE divisions."""
+    emu.emu_div_mean_mismatches.restype = ctypes.c_int64
+    assert emu.emu_div_mean_mismatches(ctypes.c_int64(4096)) == 0
+
+
+@pytest.mark.parametrize("name", ["c2", "c3"])
+def test_ant_lifted_exit_lookup(emu, name):
+    """The ant search reads the lifted exits of its origin's six neighbours
+    from an 8-byte table by a hashed ring slot; for every occupied origin and
+    every cell of the grid it equals the direct patch (exits_lifted)."""
+    g = load_golden(name)
+    st = np.ascontiguousarray(g["states"][:24])
+    emu.emu_ring_exits_mismatches.restype = ctypes.c_int64
+    assert emu.emu_ring_exits_mismatches(_p(st), ctypes.c_int64(len(st))) == 0
