@@ -1,5 +1,5 @@
 // hive_probe.hip -- root_tactical_probe_batch (game_logic.cu:1579-1616 over
-// root_tactical_probe_kernel :290-397) as six launches on the caller's
+// root_tactical_probe_kernel :290-397) as seven launches on the caller's
 // stream, no host synchronisation:
 //
 //   k_probe_roots   one lane group per root (hive_probe.hpp probe_root):
@@ -9,10 +9,15 @@
 //                   stages appended to the workspace's job lists;
 //   k_probe_screen  one lane group per screen job: allowed[r][i] = 0 when
 //                   the opponent wins at once after move i;
-//   k_probe_win2    one lane group per (two-move candidate, part) still
-//                   allowed: the part's grandchildren, fail[candidate] = 1
-//                   when one is not won;
-//   k_probe_win2_commit  per candidate no part failed: the lowest passing
+//   k_probe_drop    one lane group per two-move candidate still allowed:
+//                   fail[candidate] = 1 when a reply lowers the opponent
+//                   queen's surround, else the candidate is appended to the
+//                   survivors' list (kept where the screen's job list was,
+//                   which k_probe_screen has finished reading);
+//   k_probe_win2    one lane group per (surviving candidate, part): the
+//                   part's grandchildren, fail[candidate] = 1 when one is
+//                   not won;
+//   k_probe_win2_commit  per candidate no stage failed: the lowest passing
 //                   slot of each root by atomic min (winning[] holds
 //                   kUndecided meanwhile);
 //   k_probe_finish  per root: kUndecided -> -1, forced = the screen ran and
@@ -35,8 +40,11 @@ namespace {
 constexpr int64_t kUndecided = 1 << 20;  // above every slot; replaced by -1 at the end
 constexpr int kJobGrid = 4096;           // workgroups of the job kernels (two jobs each per pass)
 
+// counters[0]: screen jobs, [1]: two-move candidates, [2]: candidates past
+// k_probe_drop, [3]: unused (keeps the job lists 16-byte aligned)
+constexpr int kCounters = 4;
 __global__ void k_probe_reset(int32_t* __restrict__ counters) {
-    if (threadIdx.x < 2) counters[threadIdx.x] = 0;
+    if (threadIdx.x < kCounters) counters[threadIdx.x] = 0;
 }
 
 __global__ __launch_bounds__(64) void k_probe_roots(const uint8_t* __restrict__ states,
@@ -101,21 +109,46 @@ __global__ __launch_bounds__(64) void k_probe_screen(const uint8_t* __restrict__
     }
 }
 
+__global__ __launch_bounds__(64) void k_probe_drop(const uint8_t* __restrict__ states,
+                                                   const uint8_t* __restrict__ legal,
+                                                   int32_t* __restrict__ counters,
+                                                   const int32_t* __restrict__ jobs,
+                                                   const uint8_t* __restrict__ allowed,
+                                                   int32_t* __restrict__ fail, int32_t* __restrict__ survivors) {
+    __shared__ Pos PS[kPosPerWave];
+    const int lane = threadIdx.x;
+    const int64_t count = counters[1];
+    for (int64_t p = blockIdx.x; 2 * p < count; p += gridDim.x) {  // uniform over the workgroup
+        const int64_t j0 = 2 * p + (lane >> 5);
+        const bool live = j0 < count;
+        const int64_t j = live ? j0 : 2 * p;
+        const int job = jobs[j];
+        const int64_t r = job / kMaxLegal, i = job % kMaxLegal;
+        const bool drop = probe_drop(PS[lane >> 5], states + r * kStateBytes, legal + (r * kMaxLegal + i) * 6, lane);
+        if (live && gl(lane) == 0 && allowed[job] != 0) {
+            if (drop) fail[j] = 1;
+            else survivors[atomicAdd(&counters[2], 1)] = (int32_t)j;
+        }
+        __syncthreads();
+    }
+}
+
 __global__ __launch_bounds__(64) void k_probe_win2(const uint8_t* __restrict__ states,
                                                    const uint8_t* __restrict__ legal,
                                                    const int32_t* __restrict__ counters,
                                                    const int32_t* __restrict__ jobs,
+                                                   const int32_t* __restrict__ survivors,
                                                    const uint8_t* __restrict__ allowed,
                                                    int32_t* __restrict__ fail) {
     __shared__ Pos PS[kPosPerWave];
     __shared__ Replies RS[kPosPerWave];
     const int lane = threadIdx.x;
-    const int64_t items = (int64_t)counters[1] * kWin2Parts;  // (candidate, part)
+    const int64_t items = (int64_t)counters[2] * kWin2Parts;  // (surviving candidate, part)
     for (int64_t p = blockIdx.x; 2 * p < items; p += gridDim.x) {
         const int64_t q0 = 2 * p + (lane >> 5);
         const bool live = q0 < items;
         const int64_t q = live ? q0 : 2 * p;
-        const int64_t j = q / kWin2Parts;
+        const int64_t j = survivors[q / kWin2Parts];
         const int job = jobs[j];
         const int64_t r = job / kMaxLegal, i = job % kMaxLegal;
         const bool active = live && allowed[job] != 0;
@@ -160,7 +193,7 @@ __global__ void k_probe_finish(const int32_t* __restrict__ num_legal, int64_t B,
 // (12.6 MB), one copy per GPU, held until the process ends.  Host code never
 // uses the symbol itself (on the host it names a stand-in, not device
 // memory): it uses the per-device address hipGetSymbolAddress returns.
-constexpr int64_t kScratchInts = 2 + 3 * (int64_t)HG_PROBE_NOALLOC_MAX_ROOTS * kMaxLegal;
+constexpr int64_t kScratchInts = kCounters + 3 * (int64_t)HG_PROBE_NOALLOC_MAX_ROOTS * kMaxLegal;
 __device__ __align__(256) int32_t scratch[kScratchInts];
 
 constexpr int kMaxDevices = 64;
@@ -193,7 +226,7 @@ int hg_probe_scratch_init(void) {
     return scratch_of_current_device(&p);
 }
 
-int64_t hg_root_tactical_probe_workspace(int64_t B) { return B <= 0 ? 0 : 2 + 3 * B * kMaxLegal; }
+int64_t hg_root_tactical_probe_workspace(int64_t B) { return B <= 0 ? 0 : kCounters + 3 * B * kMaxLegal; }
 
 int hg_root_tactical_probe(const uint8_t* states, const uint8_t* legal_moves, const int32_t* num_legal,
                            const float* priors, int64_t B, int enable_win_in_one, int enable_check_opponent_wins,
@@ -203,7 +236,8 @@ int hg_root_tactical_probe(const uint8_t* states, const uint8_t* legal_moves, co
     if (B > (int64_t)(INT32_MAX / kMaxLegal)) return (int)hipErrorInvalidValue;
     hipStream_t s = (hipStream_t)stream;
     int32_t* counters = workspace;
-    int32_t* jobs_screen = workspace + 2;
+    int32_t* jobs_screen = workspace + kCounters;
+    int32_t* survivors = jobs_screen;  // the screen's list is read before k_probe_drop runs
     int32_t* jobs_win2 = jobs_screen + B * kMaxLegal;
     int32_t* fail_win2 = jobs_win2 + B * kMaxLegal;
     hipLaunchKernelGGL(k_probe_reset, dim3(1), dim3(64), 0, s, counters);
@@ -213,9 +247,11 @@ int hg_root_tactical_probe(const uint8_t* states, const uint8_t* legal_moves, co
     const int64_t pairs = (B * kMaxLegal + 1) / 2;
     const unsigned grid = (unsigned)(pairs < kJobGrid ? pairs : kJobGrid);
     hipLaunchKernelGGL(k_probe_screen, dim3(grid), dim3(64), 0, s, states, legal_moves, counters, jobs_screen, allowed);
+    hipLaunchKernelGGL(k_probe_drop, dim3(grid), dim3(64), 0, s, states, legal_moves, counters, jobs_win2, allowed,
+                       fail_win2, survivors);
     const int64_t items = (B * kMaxLegal * kWin2Parts + 1) / 2;
     hipLaunchKernelGGL(k_probe_win2, dim3((unsigned)(items < kJobGrid ? items : kJobGrid)), dim3(64), 0, s, states,
-                       legal_moves, counters, jobs_win2, allowed, fail_win2);
+                       legal_moves, counters, jobs_win2, survivors, allowed, fail_win2);
     hipLaunchKernelGGL(k_probe_win2_commit, dim3((unsigned)((B + 255) / 256)), dim3(256), 0, s, counters, jobs_win2,
                        allowed, fail_win2, winning);
     hipLaunchKernelGGL(k_probe_finish, dim3((unsigned)((B + 255) / 256)), dim3(256), 0, s, num_legal, B, winning,

@@ -16,10 +16,12 @@
 //                 the later stages and the two-move candidates;
 //   probe_screen  one (root, move): the child, then
 //                 has_immediate_surround_win_for_current_player on it;
-//   probe_win2    one (root, candidate move): the child's replies, the
-//                 non-decreasing-surround test over all of them, then the
-//                 immediate-win test of every grandchild the reply does not
-//                 already win.
+//   probe_drop    one (root, candidate move): the child's replies and the
+//                 non-decreasing-surround test over all of them (most
+//                 candidates fail here, with no grandchild to test);
+//   probe_win2    one (candidate that passed probe_drop, part): the child's
+//                 replies again, then the immediate-win test of every
+//                 grandchild of the part that the reply does not already win.
 //
 // Every program reaches the same barriers in both groups of a wave: a group
 // without work runs on the data it has and its caller writes nothing.
@@ -276,64 +278,91 @@ struct Replies {
     int n;
 };
 
+// A candidate's child board, its replies' list and the opponent queen's
+// surround on the child (the replies are the opponent's moves).
+struct ChildList {
+    ListInfo L;
+    int opp, cs;
+};
+HW_INL ChildList child_replies(Pos& P, const uint8_t* __restrict__ S, const uint8_t* __restrict__ m, int lane,
+                               BaseRegs* child = nullptr) {
+    load_position(P, S, lane);
+    __syncthreads();
+    if (gl(lane) == 0) apply_on_board(P, S, m[0], m[1], m[2] | (m[3] << 8), m[4] | (m[5] << 8));
+    __syncthreads();
+    if (child) save_base(P, *child, lane);
+    prepare_loaded(P, lane);
+    ChildList C;
+    C.opp = P.turn & 1;
+    C.cs = surround_now(P, C.opp);
+    C.L = generate_legal(P, lane);
+    return C;
+}
+
+// slot i of the replies' list (a lone PASS when the list is empty)
+HW_INL MoveEffect reply_effect(const Pos& P, const ListInfo& L, int i) {
+    int tp = MV_PASS, from = 0, to = 0, seg;
+    if (L.total > 0) list_slot(P, L, i, tp, from, to, seg);
+    return move_effect(P, tp & 0xFF, tp >> 8, from, to);
+}
+
+// probe_drop: after root move m, does some reply lower the opponent queen's
+// surround below its level after m (generate_non_decreasing_surround_replies,
+// move_gen.cuh:876-898, finds a reply it leaves out)?  Such a candidate is no
+// forced win whatever the grandchildren hold.  A child that is a finished
+// game (m won) has no replies and drops nothing.  Uniform within the group.
+HW_INL bool probe_drop(Pos& P, const uint8_t* __restrict__ S, const uint8_t* __restrict__ m, int lane) {
+    const ChildList C = child_replies(P, S, m, lane);
+    bool drop = false;
+    for (int i = gl(lane); i < C.L.n; i += kW)
+        if (surround_after(P, reply_effect(P, C.L, i), C.opp) < C.cs) drop = true;
+    return grp_ballot(drop, lane) != 0;
+}
+
 // The grandchildren of one candidate are split over kWin2Parts programs (part
 // p tests the replies whose slot is p modulo kWin2Parts), so a candidate with
 // many replies is not one long serial walk; the candidate passes when no part
-// fails.  kWin2Parts divides 32.
-constexpr int kWin2Parts = 16;
+// fails.
+constexpr int kWin2Parts = 64;
+static_assert(kWin2Parts > 0 && kWin2Parts <= kMaxLegal && (kWin2Parts & (kWin2Parts - 1)) == 0,
+              "parts: a power of two, at most one slot each");
 
-// probe_win2: after root move m, does every reply keep the opponent's queen
-// surround at or above its level after m, and does every reply of this part
-// leave a position the root player has already won or wins at once?  `active`
-// false: the group follows the other group of its wave and its result is
-// meaningless.
+// probe_win2, for a candidate that passed probe_drop (no reply lowers the
+// opponent queen's surround): does every reply of this part leave a position
+// the root player has already won or wins at once?  `active` false: the
+// group follows the other group of its wave and its result is meaningless.
 HW_INL bool probe_win2(Pos& P, Replies& Rp, const uint8_t* __restrict__ S, const uint8_t* __restrict__ m,
                        bool active, int part, int lane) {
     const int l = gl(lane);
-    const int mt = m[0], mp = m[1], mf = m[2] | (m[3] << 8), mto = m[4] | (m[5] << 8);
-    load_position(P, S, lane);
-    __syncthreads();
-    if (l == 0) apply_on_board(P, S, mt, mp, mf, mto);
-    __syncthreads();
     // the child's base fields, put back before each reply instead of
     // reloading the root and applying m again
     BaseRegs child;
-    save_base(P, child, lane);
-    prepare_loaded(P, lane);
-    const int opp = P.turn & 1, me = opp ^ 1;  // the opponent replies
-    const int cs = surround_now(P, opp);
-    ListInfo L = generate_legal(P, lane);
-    // keep the list: decoded slots (a lone PASS when there is no move)
-    for (int i = l; i < L.n; i += kW) {
-        int tp = MV_PASS, from = 0, to = 0, seg;
-        if (L.total > 0) list_slot(P, L, i, tp, from, to, seg);
-        Rp.mv[i][0] = (uint8_t)(tp & 0xFF);
-        Rp.mv[i][1] = (uint8_t)(tp >> 8);
-        Rp.mv[i][2] = (uint8_t)from;
-        Rp.mv[i][3] = (uint8_t)(from >> 8);
-        Rp.mv[i][4] = (uint8_t)to;
-        Rp.mv[i][5] = (uint8_t)(to >> 8);
-    }
-    // generate_non_decreasing_surround_replies (move_gen.cuh:876-898) and the
-    // replies that already win for the root player
-    bool drop = false;
-    uint32_t pm = 0;  // the slots of this part within each 32-slot word
-    for (int b = part; b < 32; b += kWin2Parts) pm |= 1u << b;
+    const ChildList C = child_replies(P, S, m, lane, &child);
+    const ListInfo& L = C.L;
+    const int me = C.opp ^ 1;
+    // the replies of this part that do not already win for the root player,
+    // decoded (a lone PASS when the list is empty) and kept by slot
     for (int k = 0; k < 8; k++) {
-        int i = 32 * k + l;
+        const int i = 32 * k + l;
         bool need = false;
-        if (i < L.n) {
+        if (i < L.n && (i & (kWin2Parts - 1)) == part) {
             int tp = MV_PASS, from = 0, to = 0, seg;
             if (L.total > 0) list_slot(P, L, i, tp, from, to, seg);
-            MoveEffect e = move_effect(P, tp & 0xFF, tp >> 8, from, to);
-            if (surround_after(P, e, opp) < cs) drop = true;
-            need = result_after(P, e) != (me ? 2 : 1);
+            need = result_after(P, move_effect(P, tp & 0xFF, tp >> 8, from, to)) != (me ? 2 : 1);
+            if (need) {
+                Rp.mv[i][0] = (uint8_t)(tp & 0xFF);
+                Rp.mv[i][1] = (uint8_t)(tp >> 8);
+                Rp.mv[i][2] = (uint8_t)from;
+                Rp.mv[i][3] = (uint8_t)(from >> 8);
+                Rp.mv[i][4] = (uint8_t)to;
+                Rp.mv[i][5] = (uint8_t)(to >> 8);
+            }
         }
-        uint32_t nw = grp_ballot(need, lane) & pm;
+        const uint32_t nw = grp_ballot(need, lane);
         if (l == 0) Rp.need[k] = nw;
     }
     if (l == 0) Rp.n = L.n;
-    bool ok = active && grp_ballot(drop, lane) == 0;
+    bool ok = active;
     __syncthreads();
     // every remaining grandchild: the root player wins at once (any order;
     // the first failure decides)

@@ -147,7 +147,7 @@ int hg_fnn_leaf_eval(const float* features, int64_t T, int64_t N, int F, const i
  * opponent wins at once (only when the own queen has 5 neighbours);
  * forced[B] uint8 = that screen left no slot.  num_legal is clamped to 256.
  * workspace: hg_root_tactical_probe_workspace(B) int32 (job lists and the
- * two-move candidates' failure flags).  Six launches on `stream`, no host
+ * two-move candidates' failure flags).  Seven launches on `stream`, no host
  * synchronisation. */
 int64_t hg_root_tactical_probe_workspace(int64_t B);
 int hg_root_tactical_probe(const uint8_t* states, const uint8_t* legal_moves, const int32_t* num_legal,

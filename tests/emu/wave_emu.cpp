@@ -1,3 +1,4 @@
+#include <mutex>
 #include <atomic>
 // wave_emu.cpp -- runs the engine's per-position programs (hive_phases.hpp)
 // on the host, one emulated 64-lane wave per call.  TEST INFRASTRUCTURE ONLY:
@@ -216,14 +217,28 @@ void emu_root_probe(const uint8_t* states, const uint8_t* legal, const int32_t* 
             bool bad = probe_screen(g_pos[t / kW], states + r * kStateBytes, legal + (r * 256 + i) * 6, t);
             if (live && t % kW == 0) allowed[job] = bad ? 0 : 1;
         });
-    std::vector<int> fail(nw, 0);
-    const int64_t items = nw * kWin2Parts;
+    std::vector<int> fail(nw, 0), surv;
+    std::mutex surv_mu;
     if (nw)
+        run_group(64, (nw + 1) / 2, [&](int64_t p, int t) {
+            int64_t j = 2 * p + t / kW;
+            bool live = j < nw;
+            if (!live) j = 2 * p;
+            int job = jw[j];
+            int64_t r = job / 256, i = job % 256;
+            bool drop = probe_drop(g_pos[t / kW], states + r * kStateBytes, legal + (r * 256 + i) * 6, t);
+            if (live && t % kW == 0 && allowed[job]) {
+                if (drop) __atomic_store_n(&fail[j], 1, __ATOMIC_SEQ_CST);
+                else { std::lock_guard<std::mutex> g(surv_mu); surv.push_back((int)j); }
+            }
+        });
+    const int64_t items = (int64_t)surv.size() * kWin2Parts;
+    if (items)
         run_group(64, (items + 1) / 2, [&](int64_t p, int t) {
             int64_t q = 2 * p + t / kW;
             bool live = q < items;
             if (!live) q = 2 * p;
-            int64_t j = q / kWin2Parts;
+            int64_t j = surv[q / kWin2Parts];
             int job = jw[j];
             int64_t r = job / 256, i = job % 256;
             bool active = live && allowed[job];

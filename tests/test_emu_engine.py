@@ -141,22 +141,25 @@ def test_emulated_successor_rows_grid_edge(emu, oracle):
     assert np.array_equal(f.view(np.uint32), want.view(np.uint32))
 
 
-def test_emulated_root_tactical_probe(emu):
+@pytest.mark.parametrize("flags", [(1, 1, 1), (0, 0, 1)])
+def test_emulated_root_tactical_probe(emu, flags):
     """hive_probe.hpp's group programs, orchestrated as hive_probe.hip's
     launches, against the reference's probe vectors: four positions of every
-    outcome kind with all stages enabled (the emulator runs a move generation
-    in ~10 ms, so the full fixture is left to the GPU test)."""
+    outcome kind, all stages enabled and the two-move search alone (with the
+    immediate-win scan off, a root's own winning move is a two-move candidate
+    whose child is a finished game with no replies: it passes).  The emulator
+    runs a move generation in ~10 ms, so the full fixture is left to the GPU
+    test."""
     g = load_golden("probe")
     kinds = g["kinds"]
     sel = np.concatenate([np.nonzero(kinds == k)[0][:4] for k in sorted(set(kinds.tolist()))])
     st, lm, nl, pr = (np.ascontiguousarray(g[k][sel]) for k in ("states", "legal", "nlegal", "priors"))
     B = len(st)
-    j = 0
-    assert tuple(g["flags"][j]) == (1, 1, 1)
+    j = [tuple(int(x) for x in f) for f in g["flags"]].index(flags)
     win = np.zeros(B, np.int64)
     allowed = np.zeros((B, 256), np.uint8)
     forced = np.zeros(B, np.uint8)
-    emu.emu_root_probe(_p(st), _p(lm), _p(nl), _p(pr), ctypes.c_int64(B), 1, 1, 1, _p(win), _p(allowed),
+    emu.emu_root_probe(_p(st), _p(lm), _p(nl), _p(pr), ctypes.c_int64(B), *flags, _p(win), _p(allowed),
                        _p(forced))
     assert np.array_equal(win, g["win"][j][sel]), np.nonzero(win != g["win"][j][sel])[0][:8]
     assert np.array_equal(forced, g["forced"][j][sel])
