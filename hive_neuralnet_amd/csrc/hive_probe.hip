@@ -1,5 +1,5 @@
 // hive_probe.hip -- root_tactical_probe_batch (game_logic.cu:1579-1616 over
-// root_tactical_probe_kernel :290-397) as seven launches on the caller's
+// root_tactical_probe_kernel :290-397) as eight launches on the caller's
 // stream, no host synchronisation:
 //
 //   k_probe_roots   one lane group per root (hive_probe.hpp probe_root):
@@ -11,10 +11,15 @@
 //                   the opponent wins at once after move i;
 //   k_probe_drop    one lane group per two-move candidate still allowed:
 //                   fail[candidate] = 1 when a reply lowers the opponent
-//                   queen's surround, else the candidate is appended to the
-//                   survivors' list (kept where the screen's job list was,
-//                   which k_probe_screen has finished reading);
-//   k_probe_win2    one lane group per (surviving candidate, part): the
+//                   queen's surround, else the candidate's grandchildren
+//                   (its replies that do not already win for the root
+//                   player) go to the grandchild list; a candidate whose
+//                   grandchildren do not fit is appended to the overflow
+//                   list (kept where the screen's job list was, which
+//                   k_probe_screen has finished reading);
+//   k_probe_grand   one lane group per listed grandchild: fail[candidate] =
+//                   1 when the root player does not win at once;
+//   k_probe_win2    one lane group per (overflow candidate, part): the
 //                   part's grandchildren, fail[candidate] = 1 when one is
 //                   not won;
 //   k_probe_win2_commit  per candidate no stage failed: the lowest passing
@@ -40,9 +45,13 @@ namespace {
 constexpr int64_t kUndecided = 1 << 20;  // above every slot; replaced by -1 at the end
 constexpr int kJobGrid = 4096;           // workgroups of the job kernels (two jobs each per pass)
 
-// counters[0]: screen jobs, [1]: two-move candidates, [2]: candidates past
-// k_probe_drop, [3]: unused (keeps the job lists 16-byte aligned)
-constexpr int kCounters = 4;
+// counters[0]: screen jobs, [1]: two-move candidates, [2]: overflow
+// candidates, [4..5]: grandchild-list reservations, 64-bit (may pass the
+// capacity); [3], [6], [7] unused (the lists start 32 bytes in)
+constexpr int kCounters = 8;
+__device__ __forceinline__ unsigned long long* reservations(int32_t* counters) {
+    return reinterpret_cast<unsigned long long*>(counters + 4);
+}
 __global__ void k_probe_reset(int32_t* __restrict__ counters) {
     if (threadIdx.x < kCounters) counters[threadIdx.x] = 0;
 }
@@ -114,7 +123,8 @@ __global__ __launch_bounds__(64) void k_probe_drop(const uint8_t* __restrict__ s
                                                    int32_t* __restrict__ counters,
                                                    const int32_t* __restrict__ jobs,
                                                    const uint8_t* __restrict__ allowed,
-                                                   int32_t* __restrict__ fail, int32_t* __restrict__ survivors) {
+                                                   int32_t* __restrict__ fail, int32_t* __restrict__ overflow,
+                                                   int32_t* __restrict__ gc, int64_t cap) {
     __shared__ Pos PS[kPosPerWave];
     const int lane = threadIdx.x;
     const int64_t count = counters[1];
@@ -124,11 +134,40 @@ __global__ __launch_bounds__(64) void k_probe_drop(const uint8_t* __restrict__ s
         const int64_t j = live ? j0 : 2 * p;
         const int job = jobs[j];
         const int64_t r = job / kMaxLegal, i = job % kMaxLegal;
-        const bool drop = probe_drop(PS[lane >> 5], states + r * kStateBytes, legal + (r * kMaxLegal + i) * 6, lane);
-        if (live && gl(lane) == 0 && allowed[job] != 0) {
-            if (drop) fail[j] = 1;
-            else survivors[atomicAdd(&counters[2], 1)] = (int32_t)j;
+        const bool active = live && allowed[job] != 0;
+        const int res = probe_drop_list(PS[lane >> 5], states + r * kStateBytes, legal + (r * kMaxLegal + i) * 6,
+                                        active, (int32_t)j, reservations(counters), gc, cap, lane);
+        if (active && gl(lane) == 0) {
+            if (res == kDropped) fail[j] = 1;
+            else if (res == kOverflow) overflow[atomicAdd(&counters[2], 1)] = (int32_t)j;
         }
+        __syncthreads();
+    }
+}
+
+__global__ __launch_bounds__(64) void k_probe_grand(const uint8_t* __restrict__ states,
+                                                    const uint8_t* __restrict__ legal,
+                                                    int32_t* __restrict__ counters,
+                                                    const int32_t* __restrict__ jobs,
+                                                    const int32_t* __restrict__ gc, int64_t cap,
+                                                    int32_t* __restrict__ fail) {
+    __shared__ Pos PS[kPosPerWave];
+    const int lane = threadIdx.x;
+    const int64_t reserved = (int64_t)*reservations(counters);
+    const int64_t count = reserved < cap ? reserved : cap;
+    for (int64_t p = blockIdx.x; 2 * p < count; p += gridDim.x) {  // uniform over the workgroup
+        const int64_t g0 = 2 * p + (lane >> 5);
+        const bool live = g0 < count;
+        const int64_t g = live ? g0 : 2 * p;
+        const int32_t j = gc[2 * g];
+        // a sentinel entry (-1) or a candidate another grandchild has already failed
+        const bool active = live && j >= 0 && fail[j] == 0;
+        if (!hw_wave_any(active)) continue;  // uniform: one wave per workgroup
+        const int job = jobs[j >= 0 ? j : 0];  // jobs[0] exists whenever an entry does
+        const int64_t r = job / kMaxLegal, i = job % kMaxLegal;
+        const bool won = probe_grand(PS[lane >> 5], states + r * kStateBytes, legal + (r * kMaxLegal + i) * 6,
+                                     (uint32_t)gc[2 * g + 1], lane);
+        if (active && !won && gl(lane) == 0) fail[j] = 1;
         __syncthreads();
     }
 }
@@ -137,18 +176,18 @@ __global__ __launch_bounds__(64) void k_probe_win2(const uint8_t* __restrict__ s
                                                    const uint8_t* __restrict__ legal,
                                                    const int32_t* __restrict__ counters,
                                                    const int32_t* __restrict__ jobs,
-                                                   const int32_t* __restrict__ survivors,
+                                                   const int32_t* __restrict__ overflow,
                                                    const uint8_t* __restrict__ allowed,
                                                    int32_t* __restrict__ fail) {
     __shared__ Pos PS[kPosPerWave];
     __shared__ Replies RS[kPosPerWave];
     const int lane = threadIdx.x;
-    const int64_t items = (int64_t)counters[2] * kWin2Parts;  // (surviving candidate, part)
+    const int64_t items = (int64_t)counters[2] * kWin2Parts;  // (overflow candidate, part)
     for (int64_t p = blockIdx.x; 2 * p < items; p += gridDim.x) {
         const int64_t q0 = 2 * p + (lane >> 5);
         const bool live = q0 < items;
         const int64_t q = live ? q0 : 2 * p;
-        const int64_t j = survivors[q / kWin2Parts];
+        const int64_t j = overflow[q / kWin2Parts];
         const int job = jobs[j];
         const int64_t r = job / kMaxLegal, i = job % kMaxLegal;
         const bool active = live && allowed[job] != 0;
@@ -188,12 +227,15 @@ __global__ void k_probe_finish(const int32_t* __restrict__ num_legal, int64_t B,
     forced[r] = f;
 }
 
-// Scratch of the no-allocation entry point: the probe's two job counters, job
-// lists and failure flags for up to HG_PROBE_NOALLOC_MAX_ROOTS roots
-// (12.6 MB), one copy per GPU, held until the process ends.  Host code never
+// Scratch of the no-allocation entry point: the probe's job counters, job
+// lists, failure flags and grandchild list for up to HG_PROBE_NOALLOC_MAX_ROOTS
+// roots (21.0 MB), one copy per GPU, held until the process ends.  Host code never
 // uses the symbol itself (on the host it names a stand-in, not device
 // memory): it uses the per-device address hipGetSymbolAddress returns.
-constexpr int64_t kScratchInts = kCounters + 3 * (int64_t)HG_PROBE_NOALLOC_MAX_ROOTS * kMaxLegal;
+// counters, then three lists of B * 256 int32 (screen jobs, two-move
+// candidates, their failure flags) and the grandchild list of B * 256 pairs
+constexpr int64_t kListInts = 5;
+constexpr int64_t kScratchInts = kCounters + kListInts * (int64_t)HG_PROBE_NOALLOC_MAX_ROOTS * kMaxLegal;
 __device__ __align__(256) int32_t scratch[kScratchInts];
 
 constexpr int kMaxDevices = 64;
@@ -226,7 +268,7 @@ int hg_probe_scratch_init(void) {
     return scratch_of_current_device(&p);
 }
 
-int64_t hg_root_tactical_probe_workspace(int64_t B) { return B <= 0 ? 0 : kCounters + 3 * B * kMaxLegal; }
+int64_t hg_root_tactical_probe_workspace(int64_t B) { return B <= 0 ? 0 : kCounters + kListInts * B * kMaxLegal; }
 
 int hg_root_tactical_probe(const uint8_t* states, const uint8_t* legal_moves, const int32_t* num_legal,
                            const float* priors, int64_t B, int enable_win_in_one, int enable_check_opponent_wins,
@@ -237,9 +279,11 @@ int hg_root_tactical_probe(const uint8_t* states, const uint8_t* legal_moves, co
     hipStream_t s = (hipStream_t)stream;
     int32_t* counters = workspace;
     int32_t* jobs_screen = workspace + kCounters;
-    int32_t* survivors = jobs_screen;  // the screen's list is read before k_probe_drop runs
+    int32_t* overflow = jobs_screen;  // the screen's list is read before k_probe_drop runs
     int32_t* jobs_win2 = jobs_screen + B * kMaxLegal;
     int32_t* fail_win2 = jobs_win2 + B * kMaxLegal;
+    int32_t* gc = fail_win2 + B * kMaxLegal;  // (candidate, packed reply) pairs
+    const int64_t cap = B * kMaxLegal;
     hipLaunchKernelGGL(k_probe_reset, dim3(1), dim3(64), 0, s, counters);
     hipLaunchKernelGGL(k_probe_roots, dim3((unsigned)((B + kPosPerWave - 1) / kPosPerWave)), dim3(64), 0, s, states,
                        legal_moves, num_legal, priors, B, enable_win_in_one, enable_check_opponent_wins,
@@ -248,10 +292,12 @@ int hg_root_tactical_probe(const uint8_t* states, const uint8_t* legal_moves, co
     const unsigned grid = (unsigned)(pairs < kJobGrid ? pairs : kJobGrid);
     hipLaunchKernelGGL(k_probe_screen, dim3(grid), dim3(64), 0, s, states, legal_moves, counters, jobs_screen, allowed);
     hipLaunchKernelGGL(k_probe_drop, dim3(grid), dim3(64), 0, s, states, legal_moves, counters, jobs_win2, allowed,
-                       fail_win2, survivors);
+                       fail_win2, overflow, gc, cap);
+    hipLaunchKernelGGL(k_probe_grand, dim3(grid), dim3(64), 0, s, states, legal_moves, counters, jobs_win2, gc, cap,
+                       fail_win2);
     const int64_t items = (B * kMaxLegal * kWin2Parts + 1) / 2;
     hipLaunchKernelGGL(k_probe_win2, dim3((unsigned)(items < kJobGrid ? items : kJobGrid)), dim3(64), 0, s, states,
-                       legal_moves, counters, jobs_win2, survivors, allowed, fail_win2);
+                       legal_moves, counters, jobs_win2, overflow, allowed, fail_win2);
     hipLaunchKernelGGL(k_probe_win2_commit, dim3((unsigned)((B + 255) / 256)), dim3(256), 0, s, counters, jobs_win2,
                        allowed, fail_win2, winning);
     hipLaunchKernelGGL(k_probe_finish, dim3((unsigned)((B + 255) / 256)), dim3(256), 0, s, num_legal, B, winning,

@@ -16,12 +16,16 @@
 //                 the later stages and the two-move candidates;
 //   probe_screen  one (root, move): the child, then
 //                 has_immediate_surround_win_for_current_player on it;
-//   probe_drop    one (root, candidate move): the child's replies and the
-//                 non-decreasing-surround test over all of them (most
-//                 candidates fail here, with no grandchild to test);
-//   probe_win2    one (candidate that passed probe_drop, part): the child's
-//                 replies again, then the immediate-win test of every
-//                 grandchild of the part that the reply does not already win.
+//   probe_drop_list  one (root, candidate move): the child's replies and
+//                 the non-decreasing-surround test over all of them (most
+//                 candidates fail here, with no grandchild to test); a
+//                 surviving candidate lists its grandchildren (the replies
+//                 that do not already win for the root player);
+//   probe_grand   one listed grandchild: the root player's immediate win;
+//   probe_win2    one (surviving candidate whose grandchildren did not fit
+//                 the list, part): the child's replies again, then the
+//                 immediate-win test of every grandchild of the part that the
+//                 reply does not already win.
 //
 // Every program reaches the same barriers in both groups of a wave: a group
 // without work runs on the data it has and its caller writes nothing.
@@ -306,17 +310,90 @@ HW_INL MoveEffect reply_effect(const Pos& P, const ListInfo& L, int i) {
     return move_effect(P, tp & 0xFF, tp >> 8, from, to);
 }
 
+// A reply packed for the grandchild list: move type (2 bits), piece type
+// (4), from (10), to (10).  Listed moves have both cells below kCells
+// (placements and PASS carry from = 0), so the packing is lossless.
+static_assert(kCells <= 1024 && MV_PASS < 4, "reply fields in 26 bits");
+__device__ __forceinline__ uint32_t pack_reply(int tp, int from, int to) {
+    return ((uint32_t)tp & 3u) | (((uint32_t)tp >> 8) & 15u) << 2 | (uint32_t)from << 6 | (uint32_t)to << 16;
+}
+
 // probe_drop: after root move m, does some reply lower the opponent queen's
 // surround below its level after m (generate_non_decreasing_surround_replies,
 // move_gen.cuh:876-898, finds a reply it leaves out)?  Such a candidate is no
-// forced win whatever the grandchildren hold.  A child that is a finished
-// game (m won) has no replies and drops nothing.  Uniform within the group.
-HW_INL bool probe_drop(Pos& P, const uint8_t* __restrict__ S, const uint8_t* __restrict__ m, int lane) {
+// forced win whatever the grandchildren hold: kDropped.  Otherwise every
+// reply that does not already win for the root player leaves a grandchild
+// to test; an `active` group reserves that many entries of the grandchild
+// list (gc: pairs of int32, the candidate's index `cand` and the packed
+// reply; *count counts reservations in 64 bits, cap entries fit) and writes them:
+// kListed.  A reservation that does not fit writes the sentinel -1 into the
+// entries of its range below cap and returns kOverflow (the caller tests
+// that candidate's grandchildren by the part programs).  A child that is a
+// finished game (m won) has no replies and lists nothing.  Uniform within
+// the group.
+enum { kDropped = 0, kListed = 1, kOverflow = 2 };
+HW_INL int probe_drop_list(Pos& P, const uint8_t* __restrict__ S, const uint8_t* __restrict__ m, bool active,
+                           int32_t cand, unsigned long long* __restrict__ count, int32_t* __restrict__ gc,
+                           int64_t cap, int lane) {
+    const int l = gl(lane);
     const ChildList C = child_replies(P, S, m, lane);
+    const int win = (C.opp ^ 1) ? 2 : 1;
     bool drop = false;
-    for (int i = gl(lane); i < C.L.n; i += kW)
-        if (surround_after(P, reply_effect(P, C.L, i), C.opp) < C.cs) drop = true;
-    return grp_ballot(drop, lane) != 0;
+    uint32_t need[8];
+    int n_need = 0;
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        const int i = 32 * k + l;
+        bool nd = false;
+        if (i < C.L.n) {
+            const MoveEffect e = reply_effect(P, C.L, i);
+            if (surround_after(P, e, C.opp) < C.cs) drop = true;
+            nd = result_after(P, e) != win;
+        }
+        need[k] = grp_ballot(nd, lane);
+        n_need += __popc(need[k]);
+    }
+    if (grp_ballot(drop, lane) != 0) return kDropped;
+    const int want = active ? n_need : 0;
+    int64_t base = 0;
+    if (l == 0 && want > 0) base = (int64_t)atomicAdd(count, (unsigned long long)want);
+    base = grp_shfl(base, 0, lane);
+    const bool fits = base + want <= cap;
+    int rank = 0;
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        if (want > 0 && ((need[k] >> l) & 1u)) {
+            const int64_t e = base + rank + __popc(need[k] & ((1u << l) - 1u));
+            if (fits) {
+                int tp = MV_PASS, from = 0, to = 0, seg;
+                if (C.L.total > 0) list_slot(P, C.L, 32 * k + l, tp, from, to, seg);
+                gc[2 * e] = cand;
+                gc[2 * e + 1] = (int32_t)pack_reply(tp, from, to);
+            } else if (e < cap) {
+                gc[2 * e] = -1;
+            }
+        }
+        rank += __popc(need[k]);
+    }
+    return fits ? kListed : kOverflow;
+}
+
+// probe_grand: one grandchild of the two-move search -- the root row S,
+// root move m, then the packed reply -- does the root player win at once?
+// (The piece a move reveals is read from S: the levels under a top are
+// unchanged by two moves, since a reply can only lift what m put on top.)
+HW_INL bool probe_grand(Pos& P, const uint8_t* __restrict__ S, const uint8_t* __restrict__ m, uint32_t reply,
+                        int lane) {
+    load_position(P, S, lane);
+    __syncthreads();
+    if (gl(lane) == 0) {
+        apply_on_board(P, S, m[0], m[1], m[2] | (m[3] << 8), m[4] | (m[5] << 8));
+        apply_on_board(P, S, (int)(reply & 3u), (int)((reply >> 2) & 15u), (int)((reply >> 6) & 1023u),
+                       (int)((reply >> 16) & 1023u));
+    }
+    __syncthreads();
+    prepare_loaded(P, lane);
+    return immediate_win(P, lane);
 }
 
 // The grandchildren of one candidate are split over kWin2Parts programs (part
@@ -327,7 +404,7 @@ constexpr int kWin2Parts = 64;
 static_assert(kWin2Parts > 0 && kWin2Parts <= kMaxLegal && (kWin2Parts & (kWin2Parts - 1)) == 0,
               "parts: a power of two, at most one slot each");
 
-// probe_win2, for a candidate that passed probe_drop (no reply lowers the
+// probe_win2, for a candidate that passed probe_drop_list (no reply lowers the
 // opponent queen's surround): does every reply of this part leave a position
 // the root player has already won or wins at once?  `active` false: the
 // group follows the other group of its wave and its result is meaningless.

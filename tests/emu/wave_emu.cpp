@@ -185,9 +185,13 @@ void emu_immediate_win(const uint8_t* states, int64_t B, uint8_t* out) {
 }
 
 // root_tactical_probe_batch: the group programs of hive_probe.hpp in the
-// order and with the bookkeeping of hive_probe.hip's launches
-void emu_root_probe(const uint8_t* states, const uint8_t* legal, const int32_t* nl, const float* pr, int64_t B, int f1,
-                    int f2, int f3, int64_t* win, uint8_t* allowed, uint8_t* forced) {
+// order and with the bookkeeping of hive_probe.hip's launches.  cap: entries
+// of the grandchild list (<= 0: B * 256, as the library sizes it; a small
+// cap sends surviving candidates to the part programs).  Returns the number
+// of candidates the part programs tested.
+int64_t emu_root_probe(const uint8_t* states, const uint8_t* legal, const int32_t* nl, const float* pr, int64_t B, int f1,
+                    int f2, int f3, int64_t* win, uint8_t* allowed, uint8_t* forced, int64_t cap) {
+    if (cap <= 0) cap = B * 256;
     std::vector<RootProbe> R(B);
     run_group(64, (B + kPosPerWave - 1) / kPosPerWave, [&](int64_t w, int t) {
         int64_t i = w * kPosPerWave + t / kW;
@@ -217,8 +221,10 @@ void emu_root_probe(const uint8_t* states, const uint8_t* legal, const int32_t* 
             bool bad = probe_screen(g_pos[t / kW], states + r * kStateBytes, legal + (r * 256 + i) * 6, t);
             if (live && t % kW == 0) allowed[job] = bad ? 0 : 1;
         });
-    std::vector<int> fail(nw, 0), surv;
-    std::mutex surv_mu;
+    std::vector<int> fail(nw, 0), over;
+    std::vector<int32_t> gc(2 * cap, 0);
+    unsigned long long reserved = 0;
+    std::mutex over_mu;
     if (nw)
         run_group(64, (nw + 1) / 2, [&](int64_t p, int t) {
             int64_t j = 2 * p + t / kW;
@@ -226,19 +232,36 @@ void emu_root_probe(const uint8_t* states, const uint8_t* legal, const int32_t* 
             if (!live) j = 2 * p;
             int job = jw[j];
             int64_t r = job / 256, i = job % 256;
-            bool drop = probe_drop(g_pos[t / kW], states + r * kStateBytes, legal + (r * 256 + i) * 6, t);
-            if (live && t % kW == 0 && allowed[job]) {
-                if (drop) __atomic_store_n(&fail[j], 1, __ATOMIC_SEQ_CST);
-                else { std::lock_guard<std::mutex> g(surv_mu); surv.push_back((int)j); }
+            const bool active = live && allowed[job];
+            int res = probe_drop_list(g_pos[t / kW], states + r * kStateBytes, legal + (r * 256 + i) * 6, active,
+                                      (int32_t)j, &reserved, gc.data(), cap, t);
+            if (active && t % kW == 0) {
+                if (res == kDropped) __atomic_store_n(&fail[j], 1, __ATOMIC_SEQ_CST);
+                else if (res == kOverflow) { std::lock_guard<std::mutex> g(over_mu); over.push_back((int)j); }
             }
         });
-    const int64_t items = (int64_t)surv.size() * kWin2Parts;
+    const int64_t ng = (int64_t)reserved < cap ? (int64_t)reserved : cap;
+    if (ng)
+        run_group(64, (ng + 1) / 2, [&](int64_t p, int t) {
+            int64_t g = 2 * p + t / kW;
+            bool live = g < ng;
+            if (!live) g = 2 * p;
+            const int32_t j = gc[2 * g];
+            const bool active = live && j >= 0 && __atomic_load_n(&fail[j], __ATOMIC_SEQ_CST) == 0;
+            if (!hw_wave_any(active)) return;
+            int job = jw[j >= 0 ? j : 0];
+            int64_t r = job / 256, i = job % 256;
+            bool won = probe_grand(g_pos[t / kW], states + r * kStateBytes, legal + (r * 256 + i) * 6,
+                                   (uint32_t)gc[2 * g + 1], t);
+            if (active && !won && t % kW == 0) __atomic_store_n(&fail[j], 1, __ATOMIC_SEQ_CST);
+        });
+    const int64_t items = (int64_t)over.size() * kWin2Parts;
     if (items)
         run_group(64, (items + 1) / 2, [&](int64_t p, int t) {
             int64_t q = 2 * p + t / kW;
             bool live = q < items;
             if (!live) q = 2 * p;
-            int64_t j = surv[q / kWin2Parts];
+            int64_t j = over[q / kWin2Parts];
             int job = jw[j];
             int64_t r = job / 256, i = job % 256;
             bool active = live && allowed[job];
@@ -260,5 +283,6 @@ void emu_root_probe(const uint8_t* states, const uint8_t* legal, const int32_t* 
         }
         forced[r] = f;
     }
+    return (int64_t)over.size();
 }
 }

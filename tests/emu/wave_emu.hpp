@@ -138,6 +138,9 @@ inline int __builtin_amdgcn_readlane(int v, int l) { return wave_emu::exchange(v
 // v_rcp_f32 is within 1 ulp of 1 / x; the correctly rounded quotient is one such value
 inline float __builtin_amdgcn_rcpf(float x) { return 1.0f / x; }
 inline int atomicAdd(int* p, int v) { return __atomic_fetch_add(p, v, __ATOMIC_SEQ_CST); }
+inline unsigned long long atomicAdd(unsigned long long* p, unsigned long long v) {
+    return __atomic_fetch_add(p, v, __ATOMIC_SEQ_CST);
+}
 inline uint32_t atomicOr(uint32_t* p, uint32_t v) { return __atomic_fetch_or(p, v, __ATOMIC_SEQ_CST); }
 inline int __popc(uint32_t x) { return __builtin_popcount(x); }
 inline int __popcll(uint64_t x) { return __builtin_popcountll(x); }

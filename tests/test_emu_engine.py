@@ -141,15 +141,17 @@ def test_emulated_successor_rows_grid_edge(emu, oracle):
     assert np.array_equal(f.view(np.uint32), want.view(np.uint32))
 
 
-@pytest.mark.parametrize("flags", [(1, 1, 1), (0, 0, 1)])
-def test_emulated_root_tactical_probe(emu, flags):
+@pytest.mark.parametrize("flags,cap", [((1, 1, 1), 0), ((0, 0, 1), 0), ((1, 1, 1), 3)])
+def test_emulated_root_tactical_probe(emu, flags, cap):
     """hive_probe.hpp's group programs, orchestrated as hive_probe.hip's
     launches, against the reference's probe vectors: four positions of every
     outcome kind, all stages enabled and the two-move search alone (with the
     immediate-win scan off, a root's own winning move is a two-move candidate
-    whose child is a finished game with no replies: it passes).  The emulator
-    runs a move generation in ~10 ms, so the full fixture is left to the GPU
-    test."""
+    whose child is a finished game with no replies: it passes).  cap 3: a
+    grandchild list of three entries, so nearly every surviving candidate
+    overflows it and is tested by the part programs instead (the library
+    sizes the list at 256 entries per root).  The emulator runs a move
+    generation in ~10 ms, so the full fixture is left to the GPU test."""
     g = load_golden("probe")
     kinds = g["kinds"]
     sel = np.concatenate([np.nonzero(kinds == k)[0][:4] for k in sorted(set(kinds.tolist()))])
@@ -159,8 +161,10 @@ def test_emulated_root_tactical_probe(emu, flags):
     win = np.zeros(B, np.int64)
     allowed = np.zeros((B, 256), np.uint8)
     forced = np.zeros(B, np.uint8)
-    emu.emu_root_probe(_p(st), _p(lm), _p(nl), _p(pr), ctypes.c_int64(B), *flags, _p(win), _p(allowed),
-                       _p(forced))
+    emu.emu_root_probe.restype = ctypes.c_int64
+    n_parts = emu.emu_root_probe(_p(st), _p(lm), _p(nl), _p(pr), ctypes.c_int64(B), *flags, _p(win), _p(allowed),
+                                 _p(forced), ctypes.c_int64(cap))
+    assert (n_parts > 0) == (cap > 0), n_parts  # the part programs ran exactly when the list was cut short
     assert np.array_equal(win, g["win"][j][sel]), np.nonzero(win != g["win"][j][sel])[0][:8]
     assert np.array_equal(forced, g["forced"][j][sel])
     assert np.array_equal(allowed, g["allowed"][j][sel])

@@ -35,6 +35,27 @@ def test_probe_golden_vectors():
         assert np.array_equal(a, g["allowed"][j]), tuple(flags)
 
 
+def test_probe_single_roots_part_programs():
+    """Every two-move root of the reference vectors ('w2' and 'forced'), each
+    probed alone (a batch of one), under all four flag combinations.  The
+    grandchild list then holds 256 entries, fewer than many of these roots'
+    surviving candidates need (roots 209, 215, 219, 230, 244 and 258 among
+    them, by the wave emulator), so those candidates are tested by the part
+    programs (k_probe_win2) instead, the path large batches rarely take."""
+    from hive_neuralnet_amd import hive_gpu
+    ext = hive_gpu.load_extension()
+    g = load_golden("probe")
+    roots = np.nonzero(np.isin(g["kinds"], ["w2", "forced"]))[0]
+    assert {209, 215, 219, 230, 244, 258} <= set(roots.tolist())
+    for j, flags in enumerate(g["flags"]):
+        for r in roots:
+            sl = slice(int(r), int(r) + 1)
+            w, a, f = _run(ext, g["states"][sl], g["legal"][sl], g["nlegal"][sl], g["priors"][sl], flags)
+            assert w[0] == g["win"][j][r], (tuple(flags), int(r))
+            assert f[0] == g["forced"][j][r], (tuple(flags), int(r))
+            assert np.array_equal(a[0], g["allowed"][j][r]), (tuple(flags), int(r))
+
+
 @pytest.mark.parametrize("mask,max_ply,seed", [(0, 150, 41), (7, 150, 42), (0, 300, 43)])
 def test_probe_matches_oracle(oracle, mask, max_ply, seed):
     """4,096 GPU-generated positions per case (about one in six has a gate open),
