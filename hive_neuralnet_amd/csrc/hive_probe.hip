@@ -1,5 +1,5 @@
 // hive_probe.hip -- root_tactical_probe_batch (game_logic.cu:1579-1616 over
-// root_tactical_probe_kernel :290-397) as eight launches on the caller's
+// root_tactical_probe_kernel :290-397) as six launches on the caller's
 // stream, no host synchronisation:
 //
 //   k_probe_roots   one lane group per root (hive_probe.hpp probe_root):
@@ -7,29 +7,28 @@
 //                   the screen and two-move stages (kept in forced[] until
 //                   k_probe_finish), and the (root, move) jobs of both
 //                   stages appended to the workspace's job lists;
-//   k_probe_screen  one lane group per screen job: allowed[r][i] = 0 when
-//                   the opponent wins at once after move i;
-//   k_probe_drop    one lane group per two-move candidate still allowed:
+//   k_probe_jobs    one lane group per screen job: allowed[r][i] = 0 when
+//                   the opponent wins at once after move i; and, in the same
+//                   launch, one lane group per two-move candidate:
 //                   fail[candidate] = 1 when a reply lowers the opponent
 //                   queen's surround, else the candidate's grandchildren
 //                   (its replies that do not already win for the root
 //                   player) go to the grandchild list; a candidate whose
 //                   grandchildren do not fit is appended to the overflow
-//                   list (kept where the screen's job list was, which
-//                   k_probe_screen has finished reading);
-//   k_probe_grand   one lane group per listed grandchild: fail[candidate] =
-//                   1 when the root player does not win at once;
-//   k_probe_win2    one lane group per (overflow candidate, part): the
-//                   part's grandchildren, fail[candidate] = 1 when one is
-//                   not won;
+//                   list;
+//   k_probe_grand   one lane group per listed grandchild of an allowed
+//                   candidate: fail[candidate] = 1 when the root player does
+//                   not win at once; and, in the same launch, one lane group
+//                   per (overflow candidate, part): the part's
+//                   grandchildren, fail[candidate] = 1 when one is not won;
 //   k_probe_win2_commit  per candidate no stage failed: the lowest passing
 //                   slot of each root by atomic min (winning[] holds
 //                   kUndecided meanwhile);
 //   k_probe_finish  per root: kUndecided -> -1, forced = the screen ran and
 //                   left no move allowed.
 //
-// The job kernels stride over their list with a grid sized from the batch;
-// the list length is read on the device.
+// The job kernels stride over their lists with a grid sized from the batch;
+// the list lengths are read on the device.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -100,105 +99,101 @@ __global__ __launch_bounds__(64) void k_probe_roots(const uint8_t* __restrict__ 
     }
 }
 
-__global__ __launch_bounds__(64) void k_probe_screen(const uint8_t* __restrict__ states,
-                                                     const uint8_t* __restrict__ legal,
-                                                     const int32_t* __restrict__ counters,
-                                                     const int32_t* __restrict__ jobs, uint8_t* __restrict__ allowed) {
-    __shared__ Pos PS[kPosPerWave];
-    const int lane = threadIdx.x;
-    const int64_t count = counters[0];
-    for (int64_t p = blockIdx.x; 2 * p < count; p += gridDim.x) {  // uniform over the workgroup
-        const int64_t j0 = 2 * p + (lane >> 5);
-        const bool live = j0 < count;
-        const int job = jobs[live ? j0 : 2 * p];
-        const int64_t r = job / kMaxLegal, i = job % kMaxLegal;
-        bool bad = probe_screen(PS[lane >> 5], states + r * kStateBytes, legal + (r * kMaxLegal + i) * 6, lane);
-        if (live && gl(lane) == 0) allowed[job] = bad ? 0 : 1;
-        __syncthreads();
-    }
-}
-
-__global__ __launch_bounds__(64) void k_probe_drop(const uint8_t* __restrict__ states,
+// The screen jobs and the two-move candidates' drop stage in one launch:
+// the two are independent (the drop stage lists the grandchildren of every
+// candidate, and the later stages skip the candidates the screen
+// disallows).  Waves [0, w_screen) take pairs of screen jobs, the rest pairs
+// of candidates; the branch is uniform per wave.
+__global__ __launch_bounds__(64) void k_probe_jobs(const uint8_t* __restrict__ states,
                                                    const uint8_t* __restrict__ legal,
                                                    int32_t* __restrict__ counters,
-                                                   const int32_t* __restrict__ jobs,
-                                                   const uint8_t* __restrict__ allowed,
-                                                   int32_t* __restrict__ fail, int32_t* __restrict__ overflow,
-                                                   int32_t* __restrict__ gc, int64_t cap) {
+                                                   const int32_t* __restrict__ jobs_screen,
+                                                   const int32_t* __restrict__ jobs_win2,
+                                                   uint8_t* __restrict__ allowed, int32_t* __restrict__ fail,
+                                                   int32_t* __restrict__ overflow, int32_t* __restrict__ gc,
+                                                   int64_t cap) {
     __shared__ Pos PS[kPosPerWave];
     const int lane = threadIdx.x;
-    const int64_t count = counters[1];
-    for (int64_t p = blockIdx.x; 2 * p < count; p += gridDim.x) {  // uniform over the workgroup
-        const int64_t j0 = 2 * p + (lane >> 5);
-        const bool live = j0 < count;
-        const int64_t j = live ? j0 : 2 * p;
-        const int job = jobs[j];
-        const int64_t r = job / kMaxLegal, i = job % kMaxLegal;
-        const bool active = live && allowed[job] != 0;
-        const int res = probe_drop_list(PS[lane >> 5], states + r * kStateBytes, legal + (r * kMaxLegal + i) * 6,
-                                        active, (int32_t)j, reservations(counters), gc, cap, lane);
-        if (active && gl(lane) == 0) {
-            if (res == kDropped) fail[j] = 1;
-            else if (res == kOverflow) overflow[atomicAdd(&counters[2], 1)] = (int32_t)j;
+    const int64_t n_screen = counters[0], n_cand = counters[1];
+    const int64_t w_screen = (n_screen + 1) / 2, w_total = w_screen + (n_cand + 1) / 2;
+    for (int64_t p = blockIdx.x; p < w_total; p += gridDim.x) {  // uniform over the workgroup
+        if (p < w_screen) {
+            const int64_t j0 = 2 * p + (lane >> 5);
+            const bool live = j0 < n_screen;
+            const int job = jobs_screen[live ? j0 : 2 * p];
+            const int64_t r = job / kMaxLegal, i = job % kMaxLegal;
+            const bool bad =
+                probe_screen(PS[lane >> 5], states + r * kStateBytes, legal + (r * kMaxLegal + i) * 6, lane);
+            if (live && gl(lane) == 0) allowed[job] = bad ? 0 : 1;
+        } else {
+            const int64_t q = p - w_screen;
+            const int64_t j0 = 2 * q + (lane >> 5);
+            const bool live = j0 < n_cand;
+            const int64_t j = live ? j0 : 2 * q;
+            const int job = jobs_win2[j];
+            const int64_t r = job / kMaxLegal, i = job % kMaxLegal;
+            const int res = probe_drop_list(PS[lane >> 5], states + r * kStateBytes,
+                                            legal + (r * kMaxLegal + i) * 6, live, (int32_t)j,
+                                            reservations(counters), gc, cap, lane);
+            if (live && gl(lane) == 0) {
+                if (res == kDropped) fail[j] = 1;
+                else if (res == kOverflow) overflow[atomicAdd(&counters[2], 1)] = (int32_t)j;
+            }
         }
         __syncthreads();
     }
 }
 
+// The listed grandchildren and the overflow candidates' part programs in one
+// launch: waves [0, w_grand) take pairs of grandchild entries, the rest pairs
+// of (overflow candidate, part); the branch is uniform per wave.  A
+// candidate the screen disallowed, or one already failed, is skipped.
 __global__ __launch_bounds__(64) void k_probe_grand(const uint8_t* __restrict__ states,
                                                     const uint8_t* __restrict__ legal,
                                                     int32_t* __restrict__ counters,
                                                     const int32_t* __restrict__ jobs,
+                                                    const uint8_t* __restrict__ allowed,
                                                     const int32_t* __restrict__ gc, int64_t cap,
+                                                    const int32_t* __restrict__ overflow,
                                                     int32_t* __restrict__ fail) {
-    __shared__ Pos PS[kPosPerWave];
-    const int lane = threadIdx.x;
-    const int64_t reserved = (int64_t)*reservations(counters);
-    const int64_t count = reserved < cap ? reserved : cap;
-    for (int64_t p = blockIdx.x; 2 * p < count; p += gridDim.x) {  // uniform over the workgroup
-        const int64_t g0 = 2 * p + (lane >> 5);
-        const bool live = g0 < count;
-        const int64_t g = live ? g0 : 2 * p;
-        const int32_t j = gc[2 * g];
-        // a sentinel entry (-1) or a candidate another grandchild has already failed
-        const bool active = live && j >= 0 && fail[j] == 0;
-        if (!hw_wave_any(active)) continue;  // uniform: one wave per workgroup
-        const int job = jobs[j >= 0 ? j : 0];  // jobs[0] exists whenever an entry does
-        const int64_t r = job / kMaxLegal, i = job % kMaxLegal;
-        const bool won = probe_grand(PS[lane >> 5], states + r * kStateBytes, legal + (r * kMaxLegal + i) * 6,
-                                     (uint32_t)gc[2 * g + 1], lane);
-        if (active && !won && gl(lane) == 0) fail[j] = 1;
-        __syncthreads();
-    }
-}
-
-__global__ __launch_bounds__(64) void k_probe_win2(const uint8_t* __restrict__ states,
-                                                   const uint8_t* __restrict__ legal,
-                                                   const int32_t* __restrict__ counters,
-                                                   const int32_t* __restrict__ jobs,
-                                                   const int32_t* __restrict__ overflow,
-                                                   const uint8_t* __restrict__ allowed,
-                                                   int32_t* __restrict__ fail) {
     __shared__ Pos PS[kPosPerWave];
     __shared__ Replies RS[kPosPerWave];
     const int lane = threadIdx.x;
-    const int64_t items = (int64_t)counters[2] * kWin2Parts;  // (overflow candidate, part)
-    for (int64_t p = blockIdx.x; 2 * p < items; p += gridDim.x) {
-        const int64_t q0 = 2 * p + (lane >> 5);
-        const bool live = q0 < items;
-        const int64_t q = live ? q0 : 2 * p;
-        const int64_t j = overflow[q / kWin2Parts];
-        const int job = jobs[j];
-        const int64_t r = job / kMaxLegal, i = job % kMaxLegal;
-        const bool active = live && allowed[job] != 0;
-        bool ok = probe_win2(PS[lane >> 5], RS[lane >> 5], states + r * kStateBytes,
-                             legal + (r * kMaxLegal + i) * 6, active, (int)(q % kWin2Parts), lane);
-        if (active && !ok && gl(lane) == 0) fail[j] = 1;
+    const int64_t reserved = (int64_t)*reservations(counters);
+    const int64_t n_grand = reserved < cap ? reserved : cap;
+    const int64_t n_parts = (int64_t)counters[2] * kWin2Parts;  // (overflow candidate, part)
+    const int64_t w_grand = (n_grand + 1) / 2, w_total = w_grand + (n_parts + 1) / 2;
+    for (int64_t p = blockIdx.x; p < w_total; p += gridDim.x) {  // uniform over the workgroup
+        if (p < w_grand) {
+            const int64_t g0 = 2 * p + (lane >> 5);
+            const bool live = g0 < n_grand;
+            const int64_t g = live ? g0 : 2 * p;
+            const int32_t j = gc[2 * g];
+            const int job = jobs[j >= 0 ? j : 0];  // jobs[0] exists whenever an entry does
+            // a sentinel entry (-1), a disallowed candidate or one already failed
+            const bool active = live && j >= 0 && allowed[job] != 0 && fail[j] == 0;
+            if (!hw_wave_any(active)) continue;  // uniform: one wave per workgroup
+            const int64_t r = job / kMaxLegal, i = job % kMaxLegal;
+            const bool won = probe_grand(PS[lane >> 5], states + r * kStateBytes,
+                                         legal + (r * kMaxLegal + i) * 6, (uint32_t)gc[2 * g + 1], lane);
+            if (active && !won && gl(lane) == 0) fail[j] = 1;
+        } else {
+            const int64_t q0 = 2 * (p - w_grand) + (lane >> 5);
+            const bool live = q0 < n_parts;
+            const int64_t q = live ? q0 : 2 * (p - w_grand);
+            const int64_t j = overflow[q / kWin2Parts];
+            const int job = jobs[j];
+            const int64_t r = job / kMaxLegal, i = job % kMaxLegal;
+            const bool active = live && allowed[job] != 0;
+            const bool ok = probe_win2(PS[lane >> 5], RS[lane >> 5], states + r * kStateBytes,
+                                       legal + (r * kMaxLegal + i) * 6, active, (int)(q % kWin2Parts), lane);
+            if (active && !ok && gl(lane) == 0) fail[j] = 1;
+        }
         __syncthreads();
     }
 }
 
-// a candidate no part failed wins: the lowest such slot of each root
+// a candidate no stage failed wins: the lowest such slot of each root
 __global__ void k_probe_win2_commit(const int32_t* __restrict__ counters, const int32_t* __restrict__ jobs,
                                     const uint8_t* __restrict__ allowed, const int32_t* __restrict__ fail,
                                     int64_t* __restrict__ winning) {
@@ -229,12 +224,13 @@ __global__ void k_probe_finish(const int32_t* __restrict__ num_legal, int64_t B,
 
 // Scratch of the no-allocation entry point: the probe's job counters, job
 // lists, failure flags and grandchild list for up to HG_PROBE_NOALLOC_MAX_ROOTS
-// roots (21.0 MB), one copy per GPU, held until the process ends.  Host code never
+// roots (25.2 MB), one copy per GPU, held until the process ends.  Host code never
 // uses the symbol itself (on the host it names a stand-in, not device
 // memory): it uses the per-device address hipGetSymbolAddress returns.
-// counters, then three lists of B * 256 int32 (screen jobs, two-move
-// candidates, their failure flags) and the grandchild list of B * 256 pairs
-constexpr int64_t kListInts = 5;
+// counters, then four lists of B * 256 int32 (screen jobs, two-move
+// candidates, their failure flags, overflow candidates) and the grandchild
+// list of B * 256 pairs
+constexpr int64_t kListInts = 6;
 constexpr int64_t kScratchInts = kCounters + kListInts * (int64_t)HG_PROBE_NOALLOC_MAX_ROOTS * kMaxLegal;
 __device__ __align__(256) int32_t scratch[kScratchInts];
 
@@ -279,25 +275,21 @@ int hg_root_tactical_probe(const uint8_t* states, const uint8_t* legal_moves, co
     hipStream_t s = (hipStream_t)stream;
     int32_t* counters = workspace;
     int32_t* jobs_screen = workspace + kCounters;
-    int32_t* overflow = jobs_screen;  // the screen's list is read before k_probe_drop runs
     int32_t* jobs_win2 = jobs_screen + B * kMaxLegal;
     int32_t* fail_win2 = jobs_win2 + B * kMaxLegal;
-    int32_t* gc = fail_win2 + B * kMaxLegal;  // (candidate, packed reply) pairs
+    int32_t* overflow = fail_win2 + B * kMaxLegal;
+    int32_t* gc = overflow + B * kMaxLegal;  // (candidate, packed reply) pairs
     const int64_t cap = B * kMaxLegal;
     hipLaunchKernelGGL(k_probe_reset, dim3(1), dim3(64), 0, s, counters);
     hipLaunchKernelGGL(k_probe_roots, dim3((unsigned)((B + kPosPerWave - 1) / kPosPerWave)), dim3(64), 0, s, states,
                        legal_moves, num_legal, priors, B, enable_win_in_one, enable_check_opponent_wins,
                        enable_win_in_two, winning, allowed, forced, counters, jobs_screen, jobs_win2, fail_win2);
-    const int64_t pairs = (B * kMaxLegal + 1) / 2;
+    const int64_t pairs = B * kMaxLegal;  // screen jobs and candidates: at most B * 256 each
     const unsigned grid = (unsigned)(pairs < kJobGrid ? pairs : kJobGrid);
-    hipLaunchKernelGGL(k_probe_screen, dim3(grid), dim3(64), 0, s, states, legal_moves, counters, jobs_screen, allowed);
-    hipLaunchKernelGGL(k_probe_drop, dim3(grid), dim3(64), 0, s, states, legal_moves, counters, jobs_win2, allowed,
-                       fail_win2, overflow, gc, cap);
-    hipLaunchKernelGGL(k_probe_grand, dim3(grid), dim3(64), 0, s, states, legal_moves, counters, jobs_win2, gc, cap,
-                       fail_win2);
-    const int64_t items = (B * kMaxLegal * kWin2Parts + 1) / 2;
-    hipLaunchKernelGGL(k_probe_win2, dim3((unsigned)(items < kJobGrid ? items : kJobGrid)), dim3(64), 0, s, states,
-                       legal_moves, counters, jobs_win2, overflow, allowed, fail_win2);
+    hipLaunchKernelGGL(k_probe_jobs, dim3(grid), dim3(64), 0, s, states, legal_moves, counters, jobs_screen,
+                       jobs_win2, allowed, fail_win2, overflow, gc, cap);
+    hipLaunchKernelGGL(k_probe_grand, dim3((unsigned)kJobGrid), dim3(64), 0, s, states, legal_moves, counters,
+                       jobs_win2, allowed, gc, cap, overflow, fail_win2);
     hipLaunchKernelGGL(k_probe_win2_commit, dim3((unsigned)((B + 255) / 256)), dim3(256), 0, s, counters, jobs_win2,
                        allowed, fail_win2, winning);
     hipLaunchKernelGGL(k_probe_finish, dim3((unsigned)((B + 255) / 256)), dim3(256), 0, s, num_legal, B, winning,

@@ -148,7 +148,7 @@ int hg_fnn_leaf_eval(const float* features, int64_t T, int64_t N, int F, const i
  * forced[B] uint8 = that screen left no slot.  num_legal is clamped to 256.
  * workspace: hg_root_tactical_probe_workspace(B) int32, 8-byte aligned (job
  * counters, job lists, the two-move candidates' failure flags and their
- * grandchildren's list).  Eight launches on `stream`, no host
+ * grandchildren's list).  Six launches on `stream`, no host
  * synchronisation. */
 int64_t hg_root_tactical_probe_workspace(int64_t B);
 int hg_root_tactical_probe(const uint8_t* states, const uint8_t* legal_moves, const int32_t* num_legal,
@@ -161,7 +161,7 @@ int hg_root_tactical_probe(const uint8_t* states, const uint8_t* legal_moves, co
  * memory (code under HIP graph capture, tight serving loops, harnesses that
  * forbid hipMalloc).  The job lists live in a static device array of this
  * library, one per GPU, sized for at most HG_PROBE_NOALLOC_MAX_ROOTS roots
- * (21.0 MB); B above that returns hipErrorInvalidValue and launches nothing.
+ * (25.2 MB); B above that returns hipErrorInvalidValue and launches nothing.
  * Every call on one GPU shares that GPU's array: calls that overlap on one
  * GPU (other streams, other threads) race and must be serialised by the
  * caller.  Outputs as hg_root_tactical_probe.  hg_probe_scratch_init looks up

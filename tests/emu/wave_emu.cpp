@@ -232,10 +232,10 @@ int64_t emu_root_probe(const uint8_t* states, const uint8_t* legal, const int32_
             if (!live) j = 2 * p;
             int job = jw[j];
             int64_t r = job / 256, i = job % 256;
-            const bool active = live && allowed[job];
-            int res = probe_drop_list(g_pos[t / kW], states + r * kStateBytes, legal + (r * 256 + i) * 6, active,
+            // independent of the screen (one launch in the library): every candidate
+            int res = probe_drop_list(g_pos[t / kW], states + r * kStateBytes, legal + (r * 256 + i) * 6, live,
                                       (int32_t)j, &reserved, gc.data(), cap, t);
-            if (active && t % kW == 0) {
+            if (live && t % kW == 0) {
                 if (res == kDropped) __atomic_store_n(&fail[j], 1, __ATOMIC_SEQ_CST);
                 else if (res == kOverflow) { std::lock_guard<std::mutex> g(over_mu); over.push_back((int)j); }
             }
@@ -247,9 +247,9 @@ int64_t emu_root_probe(const uint8_t* states, const uint8_t* legal, const int32_
             bool live = g < ng;
             if (!live) g = 2 * p;
             const int32_t j = gc[2 * g];
-            const bool active = live && j >= 0 && __atomic_load_n(&fail[j], __ATOMIC_SEQ_CST) == 0;
-            if (!hw_wave_any(active)) return;
             int job = jw[j >= 0 ? j : 0];
+            const bool active = live && j >= 0 && allowed[job] && __atomic_load_n(&fail[j], __ATOMIC_SEQ_CST) == 0;
+            if (!hw_wave_any(active)) return;
             int64_t r = job / 256, i = job % 256;
             bool won = probe_grand(g_pos[t / kW], states + r * kStateBytes, legal + (r * 256 + i) * 6,
                                    (uint32_t)gc[2 * g + 1], t);
