@@ -272,6 +272,8 @@ int hg_root_tactical_probe(const uint8_t* states, const uint8_t* legal_moves, co
                            int32_t* workspace, void* stream) {
     if (B <= 0) return 0;
     if (B > (int64_t)(INT32_MAX / kMaxLegal)) return (int)hipErrorInvalidValue;
+    // the grandchild-list counter is a 64-bit atomic at counters + 4
+    if (!workspace || (reinterpret_cast<uintptr_t>(workspace) & 7u)) return (int)hipErrorInvalidValue;
     hipStream_t s = (hipStream_t)stream;
     int32_t* counters = workspace;
     int32_t* jobs_screen = workspace + kCounters;

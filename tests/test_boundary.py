@@ -106,3 +106,20 @@ def test_reference_surface_complete():
     ext = hive_gpu.HiveGpuExtension.__new__(hive_gpu.HiveGpuExtension)
     with pytest.raises(NotImplementedError, match="not provided"):
         ext.encode_states_batch(None, 1)
+
+
+@pytest.mark.skipif(not os.path.exists(LIB), reason="libhive_gpu.so not built (run python -m hive_neuralnet_amd.build)")
+def test_probe_rejects_misaligned_workspace():
+    """hg_root_tactical_probe keeps a 64-bit atomic counter in its workspace:
+    a workspace that is not 8-byte aligned, or missing, is refused with
+    hipErrorInvalidValue (1) on the host, before any launch (so this runs
+    without a GPU: no device memory is touched)."""
+    lib = ctypes.CDLL(LIB)
+    f = lib.hg_root_tactical_probe
+    f.restype = ctypes.c_int
+    f.argtypes = [ctypes.c_void_p] * 4 + [ctypes.c_int64] + [ctypes.c_int] * 3 + [ctypes.c_void_p] * 5
+    buf = (ctypes.c_int32 * 64)()
+    base = ctypes.addressof(buf)
+    aligned = (base + 7) & ~7
+    for ws in (aligned + 4, aligned + 2, 0):
+        assert f(aligned, aligned, aligned, aligned, 1, 1, 1, 1, aligned, aligned, aligned, ws or None, None) == 1
