@@ -10,8 +10,10 @@ C-ABI entry point hg_legal_features_actions.  Prints one JSON line.
 
 Roofline: the dominant (only) kernel is k_legal<moves,features,actions>;
 algorithmic bytes per position = state 3424 + moves 1536 + n 4 + features
-488 + actions 1024 = 6476 B.  `achieved` = 6476 B x batch / mean kernel
-time measured with HIP events on the launch stream.
+488 + actions 1024 = 6476 B.  `achieved` = 6476 B x batch / the step's GPU
+time: one HIP event pair on the launch stream around K back-to-back calls of
+the C-ABI entry (outputs allocated once), / K, median of 5 groups; beside it
+the committed rocprof average of k_legal and the host cost per public call.
 
 cpu_baseline: this repository's C restatement of the reference algorithm
 (oracle/, "port", the same work: moves + features + action indices) on
@@ -84,6 +86,58 @@ def traffic_per_launch(config="C2"):
         return None
     m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", open(path).read())
     return float(m.group(1)) if m else None
+
+
+def rocprof_kernel_us(config):
+    """Average k_legal<true,true,true,true> duration (us) in the committed
+    rocprofv3 --kernel-trace --stats summary for `config`, else None."""
+    path = os.path.join(ROOT, "profiles", f"k_legal_{(config or '').lower()}_kernel_stats.md")
+    if not config or not os.path.exists(path):
+        return None
+    m = re.search(r"^\| k_legal<true, true, true, true>[^|]*\|\s*\d+\s*\|\s*([0-9.]+)", open(path).read(), re.M)
+    return float(m.group(1)) if m else None
+
+
+def step_gpu_time(ext, states, B, K, groups=5):
+    """Seconds of GPU time per fused turn-ordered step: per group, one HIP event
+    pair on the launch stream around K back-to-back hg_legal_features_actions_ordered
+    calls through the C-ABI with outputs and workspace allocated once (the host
+    enqueues far faster than the kernels run, so the stream never idles between
+    them), divided by K; the median of `groups` groups."""
+    import torch
+
+    lib = ext._lib
+    moves = torch.empty((B, 256, 6), dtype=torch.uint8, device="cuda")
+    n = torch.empty((B,), dtype=torch.int32, device="cuda")
+    feat = torch.empty((B, 122), dtype=torch.float32, device="cuda")
+    act = torch.empty((B, 256), dtype=torch.int32, device="cuda")
+    ws = torch.zeros((int(lib.hg_legal_features_actions_ordered_workspace(B)) // 4,), dtype=torch.int32,
+                     device="cuda")
+    stream = torch.cuda.current_stream()
+    sp = stream.cuda_stream
+    args = (states.data_ptr(), B, moves.data_ptr(), n.data_ptr(), feat.data_ptr(), act.data_ptr(), ws.data_ptr())
+    parity = 0
+
+    def call():
+        nonlocal parity
+        err = lib.hg_legal_features_actions_ordered(*args, parity, sp)
+        if err:
+            raise RuntimeError(f"hg_legal_features_actions_ordered failed: {err}")
+        parity ^= 1
+
+    for _ in range(3):
+        call()
+    torch.cuda.synchronize()
+    per = []
+    for _ in range(groups):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for _ in range(K):
+            call()
+        b.record(stream)
+        torch.cuda.synchronize()
+        per.append(a.elapsed_time(b) / 1e3 / K)
+    return statistics.median(per)
 
 
 def host_cpus():
@@ -452,18 +506,15 @@ def positions_leg(args, B, mask, max_ply):
         out = step()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    # the kernel's own duration: K more launches, each bracketed by HIP events on
-    # its stream (kept out of the timed region, where the event records would
-    # add their own gaps between launches)
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
-    for k in range(args.steps):
-        starts[k].record(stream)
-        step()
-        ends[k].record(stream)
+    # host cost of one call of the public entry point: K enqueues with no wait
+    # between them (the GPU runs behind; the loop ends when the last call returns)
     torch.cuda.synchronize()
-    kernel_ms = [s.elapsed_time(e) for s, e in zip(starts, ends)]
-    mean_kernel_s = statistics.mean(kernel_ms) / 1e3
+    t1 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    host_ms_per_call = (time.perf_counter() - t1) / args.steps * 1e3
+    torch.cuda.synchronize()
+    step_gpu_s = step_gpu_time(ext, states, B, args.steps)
     moves, n, feat, act = out
     n_mean = float(n.float().mean().item())
 
@@ -478,10 +529,15 @@ def positions_leg(args, B, mask, max_ply):
     unfused = B * reps / (time.perf_counter() - t1)
 
     value = B * args.steps / wall
-    achieved_gbs = BYTES_PER_POSITION * B / mean_kernel_s / 1e9
+    achieved_gbs = BYTES_PER_POSITION * B / step_gpu_s / 1e9
     name = {(65536, 0, 120): "C2", (65536, 7, 150): "C3"}.get((B, mask, max_ply))
+    ms_per_step = wall / args.steps * 1e3
+    if step_gpu_s * 1e3 > ms_per_step * 1.001:
+        print(f"bench: the step's GPU time {step_gpu_s * 1e3:.4f} ms exceeds the timed region's "
+              f"{ms_per_step:.4f} ms per step", file=sys.stderr)
+    rocprof_us = rocprof_kernel_us(name)
     out = {
-        "value": value, "unit": "positions/s", "ms_per_step": wall / args.steps * 1e3,
+        "value": value, "unit": "positions/s", "ms_per_step": ms_per_step,
         "config": {
             "workload": (f"{name}: fused legal moves + FNN features + action indices over {B:,} "
                          f"{'base-game' if mask == 0 else 'expansion-piece (mosquito, ladybug, pillbug)'} "
@@ -495,7 +551,15 @@ def positions_leg(args, B, mask, max_ply):
             "bound": "hbm", "achieved": achieved_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": achieved_gbs / HBM_PEAK_GBS, "traffic": traffic_per_launch(name),
             "kernel": "k_legal<true,true,true,true> (after k_order_buckets: the turn order)",
-            "mean_kernel_ms": mean_kernel_s * 1e3,
+            "step_gpu_ms": step_gpu_s * 1e3,
+            "step_gpu_ms_is": ("GPU time of one step (k_order_buckets + k_legal and the gap between them): "
+                               "one HIP event pair on the launch stream around K back-to-back calls of the "
+                               "C-ABI entry with preallocated outputs, / K; median of 5 such groups"),
+            "step_gpu_within_ms_per_step": step_gpu_s * 1e3 <= ms_per_step * 1.001,
+            "rocprof_k_legal_avg_us": rocprof_us,
+            "frac_from_rocprof_avg": (BYTES_PER_POSITION * B / (rocprof_us * 1e-6) / 1e9 / HBM_PEAK_GBS
+                                      if rocprof_us else None),
+            "host_ms_per_call": host_ms_per_call,
             "bytes_per_position": BYTES_PER_POSITION,
         },
         "api_unfused_positions_per_s": unfused,

@@ -641,24 +641,38 @@ HW_INL void eb_sim(const Tree& T, const LeafIn& L, const float* __restrict__ nn_
     // The selection entered vp[0..n) below the root, each node a child of
     // the one before, so the backup chain leaf -> root is that path
     // reversed, then the root; the expansion below writes none of them.
-    const bool chain = last == leaf;
-    int vc0 = 0, vc1 = 0;
+    // A path that ends at the leaf but is not such a chain (an entry outside
+    // the pool, or one whose parent is not the entry before it) takes the
+    // reference's serial walk instead: the parent links load beside the
+    // statistics, and lane 0's is the node above the path.
+    const bool in0 = lane < n && p0 >= 0 && p0 < T.M;
+    const bool in1 = lane + 64 < n && p1 >= 0 && p1 < T.M;
+    const bool maybe = last == leaf && __ballot((lane < n && !in0) || (lane + 64 < n && !in1)) == 0ull;
+    int vc0 = 0, vc1 = 0, pa0 = -1, pa1 = -1;
     float tv0 = 0.0f, tv1 = 0.0f, vq0 = 0.0f, vq1 = 0.0f;
-    if (chain) {
-        if (lane < n) {
+    if (maybe) {
+        if (in0) {
             const int64_t ni = g0 + p0;
             tv0 = T.tv[ni];
             vc0 = T.vc[ni];
             vq0 = T.vq[ni];
+            pa0 = T.pa[ni];
         }
-        if (lane + 64 < n) {
+        if (in1) {
             const int64_t ni = g0 + p1;
             tv1 = T.tv[ni];
             vc1 = T.vc[ni];
             vq1 = T.vq[ni];
+            pa1 = T.pa[ni];
         }
     }
-    const int top = (chain && n > 0) ? T.pa[g0 + __shfl(p0, 0, 64)] : leaf;  // the node above the path
+    const int prev0 = __shfl(p0, (lane + 63) & 63, 64);  // vp[lane - 1] (lane > 0)
+    const int p0_63 = __shfl(p0, 63, 64);
+    const int p1_up = __shfl(p1, (lane + 63) & 63, 64);
+    const int prev1 = lane == 0 ? p0_63 : p1_up;  // vp[lane + 63]
+    const bool broken = (in0 && lane > 0 && pa0 != prev0) || (in1 && pa1 != prev1);
+    const bool chain = maybe && __ballot(broken) == 0ull;
+    const int top = (chain && n > 0) ? __shfl(pa0, 0, 64) : leaf;  // the node above the path
     // expansion (mcts_expand_dense_priors_kernel :971-1062 body)
     int e = 0;
     float rv = 0.0f;
@@ -829,9 +843,13 @@ __global__ __launch_bounds__(64) void k_eb_plan(Tree T, LeafIn L, const float* _
     const bool live = leaf >= 0;
     int res = 0, nl = 0, n = 0, fc0 = -1, lit = 0, turn = 0, top = -1, x = -1, head = -1;
     float ltv = 0.0f, nn = 0.0f;
-    if (live) {  // loads in three dependent rounds: the simulation's inputs, then the path's ends, then above
+    bool chain = true;
+    if (live) {  // loads in dependent rounds: the simulation's inputs (with the path's first 8
+                 // entries), then the path nodes' parents, then the walk above the path
         const int32_t* vp = vl_paths + sim * kDepth;
-        const int v0 = vp[0];
+        int pv[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) pv[k] = vp[k];  // a path row holds kDepth = 128 entries
         res = L.results[sim];
         nl = L.nlegal[sim];
         n = vl_lens[sim];
@@ -842,11 +860,35 @@ __global__ __launch_bounds__(64) void k_eb_plan(Tree T, LeafIn L, const float* _
         lit = T.it[g0 + leaf];
         ltv = T.tval[g0 + leaf];
         n = n < 0 ? 0 : (n > kDepth ? kDepth : n);
-        head = n > 0 ? v0 : leaf;
-        x = n > 0 ? vp[n - 1] : leaf;  // must be the leaf: a selection path
-        top = n > 0 ? T.pa[g0 + head] : leaf;
+        // a selection path: every entry in the pool, each the child of the entry
+        // before, the last one the leaf (eb_sim's chain test, which k_eb_apply relies on)
+        head = n > 0 ? pv[0] : leaf;
+        top = leaf;
+        x = leaf;
+        int prev = -1;
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            if (k < n) {
+                const int e = pv[k];
+                if (e < 0 || e >= T.M) {
+                    chain = false;
+                } else {
+                    const int up = T.pa[g0 + e];
+                    if (k == 0) top = up;
+                    else if (up != prev) chain = false;
+                }
+                prev = e;
+                x = e;
+            }
+        }
+        for (int k = 8; k < n && chain; k++) {  // longer paths, entry by entry
+            const int e = vp[k];
+            if (e < 0 || e >= T.M || T.pa[g0 + e] != prev) chain = false;
+            prev = e;
+            x = e;
+        }
     }
-    bool bad = live && x != leaf;
+    bool bad = live && (!chain || x != leaf);
     // the walk above the path: top, its parent, ... up to the root (parent -1)
     int root = -1, steps = 0, key = head;
     if (live && !bad) {

@@ -318,16 +318,18 @@ class HiveGpuExtension:
                                                     ordered: bool = True):
         """Fused: (moves, num_legal, features, action_indices) in one pass.  With
         `ordered` (default) the positions are taken in buckets of turns, latest
-        first (hg_legal_features_actions_ordered; an int32 workspace is
-        allocated per call): the same outputs, a shorter launch on batches of
-        mixed game stages."""
+        first (hg_legal_features_actions_ordered): the same outputs, a shorter
+        launch on batches of mixed game stages.  Its int32 workspace is kept per
+        (device, stream) and its two count arrays are used in turn, so a call
+        made while the stream is being captured into a HIP graph (whose replays
+        would all repeat the captured turn) takes the index order instead."""
         B = int(batch_size)
         states = _state_rows(states, B)
         moves = torch.empty((B, MAX_LEGAL_MOVES, SIZEOF_GPU_MOVE), dtype=torch.uint8, device="cuda")
         n = torch.empty((B,), dtype=torch.int32, device="cuda")
         feat = torch.empty((B, FNN_FEAT_DIM), dtype=torch.float32, device="cuda")
         act = torch.empty((B, MAX_LEGAL_MOVES), dtype=torch.int32, device="cuda")
-        if ordered and B > 0:
+        if ordered and B > 0 and not torch.cuda.is_current_stream_capturing():
             stream = _stream()
             key = (torch.cuda.current_device(), stream)
             need = int(self._lib.hg_legal_features_actions_ordered_workspace(B)) // 4

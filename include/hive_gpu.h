@@ -77,8 +77,10 @@ int hg_legal_features_actions(const uint8_t* states, int64_t B, uint8_t* moves, 
  * arrays of 32 bucket counts, then one index list per bucket.  A call needs
  * counts[parity] zero, uses it and clears counts[parity ^ 1]: zero-fill a new
  * workspace once, then alternate parity (0, 1, 0, ...) on calls that use it
- * on one stream.  No reference counterpart (same outputs as the entry
- * above). */
+ * on one stream.  A HIP graph replays the parity it captured and would count
+ * into arrays that nothing clears: capture hg_legal_features_actions instead
+ * (the Python mirror does so while its stream is capturing).  No reference
+ * counterpart (same outputs as the entry above). */
 int64_t hg_legal_features_actions_ordered_workspace(int64_t B);
 int hg_legal_features_actions_ordered(const uint8_t* states, int64_t B, uint8_t* moves, int32_t* num_legal,
                                       float* features, int32_t* actions, void* workspace, int parity,
@@ -354,7 +356,9 @@ int hg_mcts_expand_backprop_dense(const hg_tree* tree, const float* child_q_valu
  * parallel (a planning launch settles node ids and the root's statistics in
  * simulation order, then one wave per root child).  Identical results; the
  * one-wave-per-game order is kept for games whose node pool could run short
- * or whose paths are not selection paths. */
+ * or with a path that is not a selection path (each entry a node of the pool
+ * whose parent is the entry before it, the last entry the leaf).  Path
+ * entries are node ids below max_nodes, as in the reference. */
 int64_t hg_mcts_expand_backprop_dense_workspace(int64_t B, int64_t total);
 int hg_mcts_expand_backprop_dense_ws(const hg_tree* tree, const float* child_q_values, const int32_t* leaf_idx,
                                      const uint8_t* leaf_states, const uint8_t* legal_moves,

@@ -49,8 +49,8 @@ class OracleEngine:
     def expand_dense(self, t, cq, leaf, states, legal, n, pri, results):
         return self.m.expand_dense(t, cq, leaf, states, legal, n, pri, results)
 
-    def root_noise(self, t, noise, eps):
-        self.m.root_noise(t, noise, t["root_node"], eps)
+    def root_noise(self, t, noise, eps, temp=1.0):
+        self.m.root_noise(t, noise, t["root_node"], eps, temp)
 
     def select_slots(self, t, active, slots, max_root, c_puct, W, det=False, sigma=4.0, qp=0.0):
         return self.m.select_slots(t, active, t["root_node"], slots, max_root, c_puct, W, det, sigma, qp)
@@ -132,10 +132,10 @@ class GpuEngine:
             self.c(pri), self.c(results), B, leaf.shape[0], self.M(t))
         return was.cpu().numpy()
 
-    def root_noise(self, t, noise, eps):
+    def root_noise(self, t, noise, eps, temp=1.0):
         B = t["node_count"].shape[0]
         self.ext.mcts_apply_root_noise(*self.args(t), self.c(noise.astype(np.float32)), t["root_node"],
-                                       noise.shape[1], eps, 1.0, B, self.M(t))
+                                       noise.shape[1], eps, temp, B, self.M(t))
 
     def select_slots(self, t, active, slots, max_root, c_puct, W, det=False, sigma=4.0, qp=0.0):
         B, C = slots.shape
@@ -366,3 +366,170 @@ def record_wave_evaluations(monkeypatch, evals):
         return out
     monkeypatch.setattr(hive_gpu.WavePlan, "run", run)
 
+
+
+# Root noise known answers (mcts_root_noise_kernel, mcts_tree.cuh:1192-1234).
+# For the current root's children c = 0..n-1: when T > 1, p_c <- p_c^(1/T) / sum_c p_c^(1/T);
+# then, when eps > 0, p_c <- (1 - eps) p_c + eps noise[c] for c < pad (the reference reads
+# noise[c] past the row when n > pad; here those children keep their tempered prior).
+# The priors are squares of dyadic fractions (1/2, 1/4, 3/4, 3/8 squared), so at T = 2 the
+# root and the sum are exact: sqrt p = (0.5, 0.25, 0.75, 0.375), sum 1.875.  Expected
+# values below are worked out in float64 from that closed form, not from the kernel's
+# operation sequence.  Misreadings each move some prior by >= 0.01: eps on the wrong term
+# (eps p + (1 - eps) n), the mix before the temperature, p^T instead of p^(1/T), no
+# renormalisation, tempering at T <= 1, mixing children past pad.
+NOISE_PRIORS = (0.25, 0.0625, 0.5625, 0.140625)
+NOISE_ROW = (0.1, 0.2, 0.3, 0.4)
+# (eps, T, pad)
+NOISE_CASES = [(0.0, 1.0, 4), (0.25, 1.0, 4), (0.25, 0.5, 4), (0.0, 2.0, 4), (0.25, 2.0, 4), (0.25, 2.0, 2)]
+
+
+def noise_expected(eps, temp, pad):
+    """The root's four new priors in float64 (the closed form above)."""
+    p = np.array(NOISE_PRIORS, np.float64)
+    if temp > 1.0:
+        r = p ** (1.0 / temp)
+        p = r / r.sum()
+    z = np.array(NOISE_ROW, np.float32).astype(np.float64)
+    if eps > 0.0:
+        k = min(pad, len(p))
+        p[:k] = (1.0 - eps) * p[:k] + eps * z[:k]
+    return p
+
+
+def noise_trees(pad, M=16):
+    """Four games.  g0: root 0, children 1..4.  g1: current root node 5 with children
+    9..12 (node 0 also has children 1..4, which must stay untouched).  g2: root not
+    expanded (first_child -1) with stray priors at 1..4.  g3: root with first_child 1
+    and no children.  Returns (tree, noise [4, pad], the node ids whose priors move)."""
+    t = new_tree(4, M)
+    for g in range(4):
+        t["prior"][g, 1:5] = NOISE_PRIORS
+        t["parent_idx"][g, 1:5] = 0
+    t["first_child"][0, 0], t["num_children"][0, 0] = 1, 4
+    t["first_child"][1, 0], t["num_children"][1, 0] = 1, 4
+    t["root_node"][1] = 5
+    t["first_child"][1, 5], t["num_children"][1, 5] = 9, 4
+    t["prior"][1, 9:13] = NOISE_PRIORS
+    t["parent_idx"][1, 9:13] = 5
+    t["first_child"][3, 0], t["num_children"][3, 0] = 1, 0
+    for g in range(4):
+        t["node_count"][g] = 13
+    noise = np.tile(np.array(NOISE_ROW, np.float32)[:pad], (4, 1))
+    return t, np.ascontiguousarray(noise), {0: np.arange(1, 5), 1: np.arange(9, 13)}
+
+
+def check_noise_case(engine, eps, temp, pad, ulps):
+    """Run one root-noise call on the four games and check every prior: the two
+    expanded roots' children against the float64 closed form within `ulps` units
+    in the last place of float32, every other prior unchanged bit for bit."""
+    t0, noise, moved = noise_trees(pad)
+    t = engine.tree(4, 16)
+    if isinstance(t["prior"], np.ndarray):
+        for k in t:
+            t[k][...] = t0[k]
+    else:
+        for k in t:
+            t[k].copy_(engine.torch.from_numpy(t0[k]))
+    engine.root_noise(t, noise, eps, temp)
+    got = engine.to_np(t)
+    want = noise_expected(eps, temp, pad)
+    keep = np.ones_like(t0["prior"], bool)
+    for g, nodes in moved.items():
+        keep[g, nodes] = False
+        p = got["prior"][g, nodes]
+        err = np.abs(p.astype(np.float64) - want) / np.spacing(np.abs(want).astype(np.float32)).astype(np.float64)
+        assert (err <= ulps).all(), (eps, temp, pad, g, p, want, err)
+    assert np.array_equal(got["prior"][keep].view(np.uint32), t0["prior"][keep].view(np.uint32))
+    for k in TREE_KEYS:
+        if k != "prior":
+            assert np.array_equal(got[k], t0[k]), k
+    return got
+
+
+# Virtual-Q penalty known answers (deterministic_non_root with q_penalty > 0:
+# select mcts_tree.cuh:770-777,929-934; backup undo :1164-1172).  Tree: root 0 (N 1)
+# -> child 1 (N 1) -> unexpanded grandchildren 2 (prior 0.8) and 3 (prior 0.2), child Q 0.
+# Completed-Q scores (pi0 = softmax(log p + 4 q), q = -W/N or child_init_q, minus the
+# penalty; score = pi0 - N / (1 + sum N)), worked in float64:
+#   simulation 0: A 0.8, B 0.2 -> node 2; it takes N + 1 and, with q_penalty 0.25, vq + 0.25.
+#   simulation 1, q_penalty 0.25: q_A = 0 - 0.25, pi0_A = e^(ln .8 - 1) / (e^(ln .8 - 1) + .2)
+#     = 0.59537, score_A = 0.59537 - 1/2 = 0.09537 < score_B = 0.40463 -> node 3.
+#   simulation 1, q_penalty 0: score_A = 0.8 - 1/2 = 0.3 > 0.2 -> node 2 again.
+# In root-slot mode the forced root child takes no virtual visit; each chosen
+# grandchild takes N + 1 and vq + penalty.  The backup with q_penalty > 0 takes the
+# penalty off every virtual-loss node (vq back to 0) but leaves the selection's N + 1 in
+# place, then adds N + 1 and W + v up the path with alternating sign.  With values
+# v0 = 0.5 (sim 0, expands node 2) and v1 = -0.25 (sim 1, expands node 3):
+#   node 2: N 2, W 0.5;  node 3: N 2, W -0.25;  node 1: N 3, W -(0.5) - (-0.25) = -0.25;
+#   node 0: N 3, W 0.5 + (-0.25) = 0.25;  every vq 0.
+# Root-mask mode, one simulation, q_penalty 0.25: the root child chosen by PUCT takes
+# N + 1 and W - 1 (the ordinary virtual loss) while the grandchild takes N + 1, vq + 0.25;
+# the backup takes 0.25 off both, so the root child ends at vq = -0.25 with its W - 1 and
+# N + 1 kept: node 1: N 1 + 1 + 1 = 3, W -1 - 0.5 = -1.5, vq -0.25; node 2: N 2, W 0.5,
+# vq 0; node 0: N 2, W 0.5.
+def q_penalty_tree():
+    t = new_tree(1, 32)
+    t["visit_count"][0, :2] = 1
+    t["first_child"][0, 0], t["num_children"][0, 0] = 1, 1
+    t["first_child"][0, 1], t["num_children"][0, 1] = 2, 2
+    t["parent_idx"][0, 1], t["parent_idx"][0, 2:4] = 0, 1
+    t["prior"][0, 1:4] = (1.0, 0.8, 0.2)
+    t["move_bytes"][0, 1:4] = [2, 0, 0, 0, 0, 0]
+    t["node_count"][0] = 4
+    return t
+
+
+def check_q_penalty_case(engine, init_state, mode):
+    """Select (two simulations in root-slot mode, one in root-mask mode) then expand + backup
+    on q_penalty_tree() with q_penalty 0.25, checked against the known answers above; and
+    the penalty's effect on the second simulation's choice (q_penalty 0 picks node 2)."""
+    def fresh():
+        t0 = q_penalty_tree()
+        t = engine.tree(1, 32)
+        for k in t:
+            if isinstance(t[k], np.ndarray):
+                t[k][...] = t0[k]
+            else:
+                t[k].copy_(engine.torch.from_numpy(t0[k]))
+        return t
+    one = np.ones(1, np.int8)
+    if mode == "slots":
+        slots = np.zeros((1, 1), np.int32)
+        t = fresh()
+        leaf = engine.select_slots(t, one, slots, 256, 1.25, 2, True, 4.0, 0.0)[0]
+        assert list(leaf) == [2, 2]
+        t = fresh()
+        leaf, paths, plen, vl, vlen = engine.select_slots(t, one, slots, 256, 1.25, 2, True, 4.0, 0.25)
+        assert list(leaf) == [2, 3] and list(plen) == [2, 2] and list(vlen) == [1, 1]
+        assert list(vl[:, 0]) == [2, 3]
+        mid = engine.to_np(t)
+        assert list(mid["visit_count"][0, :4]) == [1, 1, 1, 1]
+        assert list(mid["virtual_q_penalty"][0, :4]) == [0.0, 0.0, 0.25, 0.25]
+        assert not mid["total_value"][0].any()
+        vals = np.array([0.5, -0.25], np.float32)
+        want_n, want_w, want_vq = [3, 3, 2, 2], [0.25, -0.25, 0.5, -0.25], [0.0] * 4
+    else:
+        alive = np.zeros((1, 256), np.int8)
+        alive[0, 0] = 1
+        t = fresh()
+        leaf, paths, plen, vl, vlen = engine.select_mask(t, one, alive, 1.25, 1, True, 4.0, 0.25)
+        assert list(leaf) == [2] and plen[0] == 2 and vlen[0] == 2 and list(vl[0, :2]) == [1, 2]
+        mid = engine.to_np(t)
+        assert list(mid["visit_count"][0, :4]) == [1, 2, 1, 0]
+        assert list(mid["total_value"][0, :4]) == [0.0, -1.0, 0.0, 0.0]
+        assert list(mid["virtual_q_penalty"][0, :4]) == [0.0, 0.0, 0.25, 0.0]
+        vals = np.array([0.5], np.float32)
+        want_n, want_w, want_vq = [2, 3, 2, 0], [0.5, -1.5, 0.5, 0.0], [0.0, -0.25, 0.0, 0.0]
+    T = leaf.shape[0]
+    leaves = np.repeat(init_state[None], T, axis=0)
+    legal, n = engine.legal(leaves)
+    pri = np.zeros((T, 256), np.float32)
+    pri[:, :4] = 0.25
+    z = np.zeros((T, 256), np.float32)
+    engine.expand_backprop(t, z, leaf, leaves, legal, n, pri, np.zeros(T, np.int32), vals, vl, vlen, 0.25)
+    got = engine.to_np(t)
+    assert list(got["visit_count"][0, :4]) == want_n
+    assert list(got["total_value"][0, :4]) == want_w
+    assert list(got["virtual_q_penalty"][0, :4]) == want_vq
+    assert got["node_count"][0] == 4 + 4 * T

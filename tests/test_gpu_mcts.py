@@ -226,3 +226,91 @@ def test_parallel_expand_backprop_equals_one_wave(roots, mode, W, C, M, dup, det
         for k in ("leaf", "paths", "plen", "vl", "vlen", "mid_visits"):
             assert np.array_equal(a[k], b[k]), k
         assert np.array_equal(a["mid_total"].view(np.uint32), b["mid_total"].view(np.uint32))
+
+
+@pytest.mark.parametrize("eps,temp,pad", __import__("mcts_driver").NOISE_CASES)
+def test_root_noise_known_answers(eps, temp, pad):
+    """k_root_noise against the float64 closed form (tests/mcts_driver.py NOISE_CASES),
+    within 2 float32 ulp (as the oracle); untouched priors and arrays bit for bit."""
+    from mcts_driver import check_noise_case
+    check_noise_case(GpuEngine(), eps, temp, pad, ulps=2.0)
+
+
+def test_root_noise_temperature_matches_oracle(roots):
+    """root_policy_temp 2 with eps 0.25 on 48 expanded roots of seeded priors and
+    Dirichlet noise, GPU against the oracle.  The tempered path goes through powf:
+    the host's is correctly rounded, the device's is accurate to about 1 ulp, so a
+    tempered term may differ in the last place; the renormalising sum over up to
+    ~100 children adds those differences up and the quotient carries both.  Priors
+    agree within 8 float32 ulp (measured: about 28% of the 3,625 priors differ, by
+    at most 4 ulp); every other tree array bit for bit.  The closed-form known
+    answers (test_root_noise_known_answers, exact roots) hold to 2 ulp on both."""
+    B = roots.shape[0]
+    res = {}
+    for name, eng in (("gpu", GpuEngine()), ("oracle", OracleEngine())):
+        r = np.random.default_rng(11)
+        t = eng.tree(B, 4096)
+        legal, n = eng.legal(roots)
+        pri, _, cq = synthetic_eval(r, n, B)
+        results = roots[:, 3415].astype(np.int32)
+        leaf0 = np.where((results == 0) & (n > 0), 0, -1).astype(np.int32)
+        eng.expand_dense(t, cq, leaf0, roots, legal, n, pri, results)
+        pad = int(np.maximum(n, 1).max())
+        noise = np.zeros((B, pad), np.float32)
+        for i in range(B):
+            noise[i, : n[i]] = r.dirichlet([0.3] * max(1, n[i]))[: n[i]]
+        eng.root_noise(t, noise, 0.25, 2.0)
+        res[name] = eng.to_np(t)
+    g, o = res["gpu"], res["oracle"]
+    assert tree_equal(o, g) in ([], ["prior"])
+    ulps = np.abs(g["prior"].astype(np.float64) - o["prior"]) / np.spacing(np.abs(o["prior"])).astype(np.float64)
+    print(f"root noise at T=2: {int((ulps > 0).sum())} of {int(o['num_children'][:, 0].sum())} priors differ, "
+          f"max {ulps.max():.2f} ulp")
+    assert ulps.max() <= 8.0
+    assert (o["prior"][:, 0] == 0).all()  # the roots' own priors are never touched
+
+
+@pytest.mark.parametrize("mode", ["slots", "mask"])
+def test_q_penalty_known_answers(oracle, mode):
+    """The hand-worked q_penalty case (tests/mcts_driver.py) through the GPU selects and
+    expansion + backup: same choices, visit counts, values and penalties as worked out."""
+    from mcts_driver import check_q_penalty_case
+    check_q_penalty_case(GpuEngine(), oracle.init_state(0), mode)
+
+
+def test_expand_backprop_paths_not_chains(roots):
+    """Virtual-loss paths that end at the leaf but are not selection chains (a middle
+    entry swapped for a node of another subtree) take the reference's serial walk --
+    the virtual-loss undo over the listed entries, the backup up the leaf's parents --
+    in both GPU entry points: identical to the oracle, and the planned entry leaves
+    those games to the one-wave order (no two waves write one subtree)."""
+    import torch
+    oe = OracleEngine()
+    t, _ = run_search(oe, roots, W=2, C=4, M=8192, waves=5)
+    B = roots.shape[0]
+    slots = np.tile(np.arange(4, dtype=np.int32), (B, 1))
+    slots[t["num_children"][:, 0][:, None] <= np.arange(4)[None, :]] = -1
+    active = (t["num_children"][:, 0] > 0).astype(np.int8)
+    leaf, paths, plen, vl, vlen = oe.select_slots(t, active, slots, 256, 1.25, 2)
+    deep = np.nonzero(vlen >= 3)[0]
+    assert len(deep) >= 8
+    rng = np.random.default_rng(9)
+    for s in deep[::2]:  # every other deep path: its second entry becomes another node of the game
+        g = s % B
+        other = int(rng.integers(1, t["node_count"][g]))
+        while other in vl[s, : vlen[s]]:
+            other = int(rng.integers(1, t["node_count"][g]))
+        vl[s, 1] = other
+    leaves = oe.replay(roots, paths, plen, leaf)
+    lm, ln = oe.legal(leaves)
+    p2, v2, q2 = synthetic_eval(rng, ln, leaf.shape[0])
+    res = leaves[:, 3415].astype(np.int32)
+    outs = []
+    for eng in (GpuEngine(), _OneWavePerGame()):
+        gt = {k: eng.c(v.copy()) for k, v in t.items()}
+        eng.expand_backprop(gt, q2, leaf, leaves, lm, ln, p2, res, v2, vl, vlen)
+        torch.cuda.synchronize()
+        outs.append(eng.to_np(gt))
+    oe.expand_backprop(t, q2, leaf, leaves, lm, ln, p2, res, v2, vl, vlen)
+    assert tree_equal(t, outs[0]) == []
+    assert tree_equal(t, outs[1]) == []

@@ -51,7 +51,7 @@ def test_initial_states(ext, oracle):
 
 
 @pytest.mark.parametrize("name", ["c1", "c2", "c3"])
-def test_golden_moves_features(ext, name):
+def test_golden_moves_features(ext, oracle, name):
     g = load_golden(name)
     B = len(g["states"])
     st = _cuda(g["states"])
@@ -65,7 +65,9 @@ def test_golden_moves_features(ext, name):
     assert np.array_equal(_bits(feat2.cpu().numpy()), _bits(g["features"]))
     # compact successor lists of the golden moves, via extract on the oracle's compact lists
     feat3 = ext.extract_fnn_features_batch(st, _cuda(g["compact"]), _cuda(g["ncompact"]), B)
-    assert feat3.shape == (B, 122)
+    want3 = np.stack([oracle.fnn_features(g["states"][i], g["compact"][i], int(g["ncompact"][i]))
+                      for i in range(B)])
+    assert np.array_equal(_bits(feat3.cpu().numpy()), _bits(want3))
 
 
 @pytest.mark.parametrize("ordered", [True, False], ids=["turn-order", "index-order"])
@@ -223,7 +225,10 @@ def test_edge_cases(ext, oracle):
     st = _cuda(g["finals"][:2])
     mv = torch.zeros((2, 256, 6), dtype=torch.uint8, device="cuda")
     f = ext.extract_fnn_features_batch(st, mv, torch.tensor([-3, 999], dtype=torch.int32, device="cuda"), 2)
-    assert f.shape == (2, 122)
+    fin = g["finals"][:2]
+    zeros = np.zeros((256, 6), np.uint8)
+    want = np.stack([oracle.fnn_features(fin[0], zeros, 0), oracle.fnn_features(fin[1], zeros, 256)])
+    assert np.array_equal(_bits(f.cpu().numpy()), _bits(want))
 
 
 @pytest.mark.parametrize("T,zero_every", [(1, 0), (777, 0), (5000, 3)], ids=["one", "odd", "chunked-scan"])

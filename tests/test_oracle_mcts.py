@@ -237,3 +237,47 @@ def test_completed_q_descent_known_answers(oracle, mode):
     assert (vlen == (1 if mode == "slots" else 2)).all()
     assert np.array_equal(t["visit_count"][np.arange(B), want], [c[0][w - 2][0] + 1 for c, w in
                                                                  zip(COMPLETED_Q_CASES, want)])
+
+
+@pytest.mark.parametrize("eps,temp,pad", __import__("mcts_driver").NOISE_CASES)
+def test_root_noise_known_answers(eps, temp, pad):
+    """or_mcts_root_noise (mcts_tree.cuh:1192-1234) against the float64 closed form
+    of tests/mcts_driver.py (NOISE_CASES).  Tolerance 2 float32 ulp: at T = 2 the
+    roots and their sum are exact, then one division and the two roundings of the
+    mix; with eps = 0 and T <= 1 the priors must come back bit for bit."""
+    from mcts_driver import OracleEngine, check_noise_case
+    got = check_noise_case(OracleEngine(), eps, temp, pad, ulps=2.0)
+    if eps == 0.0 and temp <= 1.0:
+        assert np.array_equal(got["prior"][0, 1:5], np.array(__import__("mcts_driver").NOISE_PRIORS, np.float32))
+
+
+def test_root_noise_cases_discriminate():
+    """Each misreading the closed form rules out moves a prior by far more than 2 ulp
+    (the tolerance above), so the known answers pin the order and the terms."""
+    from mcts_driver import NOISE_PRIORS, NOISE_ROW, noise_expected
+    p = np.array(NOISE_PRIORS)
+    z = np.array(NOISE_ROW, np.float32).astype(np.float64)
+    r = np.sqrt(p) / np.sqrt(p).sum()
+    right = noise_expected(0.25, 2.0, 4)
+    wrong = {
+        "eps on the prior": 0.25 * r + 0.75 * z,
+        "mix before temperature": np.sqrt(0.75 * p + 0.25 * z) / np.sqrt(0.75 * p + 0.25 * z).sum(),
+        "p^T": 0.75 * (p ** 2 / (p ** 2).sum()) + 0.25 * z,
+        "no renormalisation": 0.75 * np.sqrt(p) + 0.25 * z,
+    }
+    for name, w in wrong.items():
+        assert np.abs(w - right).max() > 1e-3, name
+    assert np.abs(noise_expected(0.25, 0.5, 4) - noise_expected(0.25, 1.0, 4)).max() == 0.0
+    assert np.abs(noise_expected(0.25, 2.0, 2)[2:] - r[2:]).max() == 0.0
+
+
+@pytest.mark.parametrize("mode", ["slots", "mask"])
+def test_q_penalty_known_answers(oracle, mode):
+    """deterministic_non_root with q_penalty 0.25 (mcts_tree.cuh:770-777,929-934 in the
+    selects, :1164-1172 in the backup) on the hand-worked tree of tests/mcts_driver.py:
+    the penalty turns the second simulation away from node 2, selection leaves N + 1 and
+    vq + 0.25 on the nodes it entered, the backup takes the penalty off again and keeps
+    the selection's N + 1 (in root-mask mode the root child's ordinary virtual loss stays
+    and its vq ends at -0.25)."""
+    from mcts_driver import OracleEngine, check_q_penalty_case
+    check_q_penalty_case(OracleEngine(), oracle.init_state(0), mode)
