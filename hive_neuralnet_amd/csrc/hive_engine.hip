@@ -186,23 +186,30 @@ constexpr int64_t kSuccGrid = 16384;  // workgroups of the successor kernels (th
 // spills; the LDS board allows 5.5); left alone the row loop takes ~109
 constexpr int kSuccWaves = 5;
 
-// Row blocks of kSuccRows rows: lane group q of the grid takes blocks q,
+// Row blocks of R rows: lane group q of the grid takes blocks q,
 // q + 2 * gridDim.x, ... one row after another, as one stream (a root's
-// board carries over a block boundary).  The loop count is uniform over the
+// board carries over a block boundary).  R = kSuccRows when every lane group
+// of the grid has that many rows to do, fewer when the rows are few (down to
+// one row per group: the count is known only on the device, and a short
+// batch is bound by the latency of each group's rows in series, not by the
+// board loads that longer runs share).  The loop count is uniform over the
 // workgroup: both groups run while the first group's block is in range.
 HW_INL void successor_stream(const uint8_t* __restrict__ states, const uint8_t* __restrict__ legal,
                              const int64_t* __restrict__ a2r, const int64_t* __restrict__ midx, int64_t N,
                              int64_t num_roots, float* __restrict__ feat_out) {
     __shared__ Pos PS[kPosPerWave];
     const int grp = threadIdx.x >> 5;
-    const int64_t blocks = (N + kSuccRows - 1) / kSuccRows;
+    const int64_t groups = (int64_t)kPosPerWave * gridDim.x;
+    const int64_t per = (N + groups - 1) / groups;
+    const int R = per < 1 ? 1 : (per > kSuccRows ? kSuccRows : (int)per);
+    const int64_t blocks = (N + R - 1) / R;
     SuccessorStream st;
-    for (int64_t r = 0;; r++) {
-        const int lane = hw_opaque(threadIdx.x);
-        const int64_t p = blockIdx.x + (r / kSuccRows) * gridDim.x;
-        if (kPosPerWave * p >= blocks) break;
-        const int64_t i = (kPosPerWave * p + grp) * kSuccRows + r % kSuccRows;
-        successor_row(PS[grp], st, states, legal, a2r, midx, i, N, num_roots, kZeroRow, lane, feat_out);
+    for (int64_t p = blockIdx.x; kPosPerWave * p < blocks; p += gridDim.x) {
+        for (int k = 0; k < R; k++) {
+            const int lane = hw_opaque(threadIdx.x);
+            const int64_t i = (kPosPerWave * p + grp) * R + k;
+            successor_row(PS[grp], st, states, legal, a2r, midx, i, N, num_roots, kZeroRow, lane, feat_out);
+        }
     }
 }
 

@@ -68,6 +68,57 @@ struct MlpLds {
 };
 enum { kB1, kLnW, kLnB, kB2, kWv, kWa2, kBa1 };
 
+// The network laid out once per evaluation in the order the MLP kernels keep
+// in LDS (k_pack_net), so that each of their blocks fills LDS with straight
+// 16-byte copies instead of gathering and permuting the weights itself.
+struct PackedNet {
+    f4 w1[32][64];
+    f4 w2[16][64];
+    f4 w3[2][16][64];  // action_fc1: root half, successor half
+    float vec[7][kE];
+};
+
+// element i of a [step][lane][tile] array: unit m = 16 tile + lane % 16 and the
+// step / lane group dependent K index (fc1: 32 g + s; the 64-wide layers:
+// 16 (s / 4) + 4 g + s % 4)
+__device__ __forceinline__ void perm_index(int i, bool first, int& m, int& k) {
+    const int t = i & 3, l = (i >> 2) & 63, s = i >> 8;
+    m = 16 * t + (l & 15);
+    k = first ? 32 * (l >> 4) + s : 16 * (s >> 2) + 4 * (l >> 4) + (s & 3);
+}
+
+__global__ __launch_bounds__(256) void k_pack_net(const float* __restrict__ w1, int F, const float* __restrict__ b1,
+                                                  const float* __restrict__ lnw, const float* __restrict__ lnb,
+                                                  const float* __restrict__ w2, const float* __restrict__ b2,
+                                                  const float* __restrict__ wv, const float* __restrict__ a1w,
+                                                  const float* __restrict__ a1b, const float* __restrict__ a2w,
+                                                  PackedNet* __restrict__ out) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;  // one float of the packed layout
+    constexpr int n1 = 32 * 64 * 4, n2 = 16 * 64 * 4;
+    int m, k;
+    if (i < n1) {
+        perm_index(i, true, m, k);
+        reinterpret_cast<float*>(&out->w1[0][0])[i] = k < F ? w1[m * F + k] : 0.0f;
+    } else if (i < n1 + n2) {
+        perm_index(i - n1, false, m, k);
+        reinterpret_cast<float*>(&out->w2[0][0])[i - n1] = w2[m * kE + k];
+    } else if (i < n1 + 3 * n2) {
+        const int j = i - n1 - n2, half = j / n2;
+        perm_index(j - half * n2, false, m, k);
+        reinterpret_cast<float*>(&out->w3[0][0][0])[j] = a1w[m * 2 * kE + half * kE + k];
+    } else if (i < n1 + 3 * n2 + kE) {
+        const int u = i - n1 - 3 * n2;
+        out->vec[kB1][u] = b1[u];
+        out->vec[kLnW][u] = lnw[u];
+        out->vec[kLnB][u] = lnb[u];
+        out->vec[kB2][u] = b2[u];
+        out->vec[kWv][u] = wv[u];
+        out->vec[kWa2][u] = a2w[u];
+        out->vec[kBa1][u] = a1b[u];
+    }
+}
+constexpr int kPackThreads = 32 * 64 * 4 + 3 * 16 * 64 * 4 + kE;
+
 // sigmoid from the hardware exp2 and reciprocal (v_exp_f32, v_rcp_f32):
 // ~1e-6 relative against the correctly rounded form, inside the 1e-5
 // tolerance the network's outputs are held to, at a fraction of expf's and
@@ -104,40 +155,53 @@ __global__ __launch_bounds__(64 * kBlockWaves) void k_leaf_mlp(const float* __re
                                                   const float* __restrict__ wv, float bv, const float* __restrict__ a1w,
                                                   const float* __restrict__ a1b, const float* __restrict__ a2w, float ba2,
                                                   float* __restrict__ R, float* __restrict__ value,
-                                                  float* __restrict__ logit, const int64_t* __restrict__ rows_dev) {
+                                                  float* __restrict__ logit, const int64_t* __restrict__ rows_dev,
+                                                  const PackedNet* __restrict__ pk) {
     __shared__ MlpLds L;
-    // permuted weights into LDS: element i of a [step][lane][tile] array is
-    // unit m = 16 tile + lane%16 and step/lane group dependent K index k
-    float* l1 = reinterpret_cast<float*>(&L.w1[0][0]);
-    for (int i = threadIdx.x; i < 32 * 64 * 4; i += blockDim.x) {
-        const int t = i & 3, l = (i >> 2) & 63, s = i >> 8;
-        const int m = 16 * t + (l & 15), k = 32 * (l >> 4) + s;
-        l1[i] = k < F ? w1[m * F + k] : 0.0f;
-    }
-    float* l2 = reinterpret_cast<float*>(&L.w2[0][0]);
-    float* l3 = reinterpret_cast<float*>(&L.w3[0][0]);
-    for (int i = threadIdx.x; i < 16 * 64 * 4; i += blockDim.x) {
-        const int t = i & 3, l = (i >> 2) & 63, s = i >> 8;
-        const int m = 16 * t + (l & 15), k = 16 * (s >> 2) + 4 * (l >> 4) + (s & 3);
-        l2[i] = w2[m * kE + k];
-        l3[i] = a1w[m * 2 * kE + (kRoot ? 0 : kE) + k];
-    }
-    if (threadIdx.x < kE) {
-        const int u = threadIdx.x;
-        L.vec[kB1][u] = b1[u];
-        L.vec[kLnW][u] = lnw[u];
-        L.vec[kLnB][u] = lnb[u];
-        L.vec[kB2][u] = b2[u];
-        L.vec[kWv][u] = wv[u];
-        L.vec[kWa2][u] = a2w[u];
-        L.vec[kBa1][u] = a1b[u];
+    if (rows_dev) rows = *rows_dev;  // row count held on the device
+    const int64_t ntiles = (rows + 15) >> 4;
+    // 16-row tiles dealt over the blocks first (tile = block + grid * (wave +
+    // kBlockWaves * round)): a short batch spreads over all CUs, and a block
+    // with no tile leaves before filling LDS
+    if ((int64_t)blockIdx.x >= ntiles) return;
+    if (pk) {  // the packed layout: straight 16-byte copies
+        f4* dst = &L.w1[0][0];
+        const f4* src = &pk->w1[0][0];
+        for (int i = threadIdx.x; i < 48 * 64; i += blockDim.x) dst[i] = src[i];  // w1, w2
+        const f4* s3 = &pk->w3[kRoot ? 0 : 1][0][0];
+        f4* d3 = &L.w3[0][0];
+        for (int i = threadIdx.x; i < 16 * 64; i += blockDim.x) d3[i] = s3[i];
+        if (threadIdx.x < 7 * kE / 4)
+            reinterpret_cast<f4*>(&L.vec[0][0])[threadIdx.x] = reinterpret_cast<const f4*>(&pk->vec[0][0])[threadIdx.x];
+    } else {  // permuted weights gathered into LDS (perm_index)
+        int m, k;
+        float* l1 = reinterpret_cast<float*>(&L.w1[0][0]);
+        for (int i = threadIdx.x; i < 32 * 64 * 4; i += blockDim.x) {
+            perm_index(i, true, m, k);
+            l1[i] = k < F ? w1[m * F + k] : 0.0f;
+        }
+        float* l2 = reinterpret_cast<float*>(&L.w2[0][0]);
+        float* l3 = reinterpret_cast<float*>(&L.w3[0][0]);
+        for (int i = threadIdx.x; i < 16 * 64 * 4; i += blockDim.x) {
+            perm_index(i, false, m, k);
+            l2[i] = w2[m * kE + k];
+            l3[i] = a1w[m * 2 * kE + (kRoot ? 0 : kE) + k];
+        }
+        if (threadIdx.x < kE) {
+            const int u = threadIdx.x;
+            L.vec[kB1][u] = b1[u];
+            L.vec[kLnW][u] = lnw[u];
+            L.vec[kLnB][u] = lnb[u];
+            L.vec[kB2][u] = b2[u];
+            L.vec[kWv][u] = wv[u];
+            L.vec[kWa2][u] = a2w[u];
+            L.vec[kBa1][u] = a1b[u];
+        }
     }
     __syncthreads();
 
     const int lane = threadIdx.x & 63, g = lane >> 4;
-    if (rows_dev) rows = *rows_dev;  // row count held on the device
-    const int64_t ntiles = (rows + 15) >> 4;
-    for (int64_t tile = (int64_t)blockIdx.x * kBlockWaves + (threadIdx.x >> 6); tile < ntiles;
+    for (int64_t tile = (int64_t)blockIdx.x + (int64_t)gridDim.x * (threadIdx.x >> 6); tile < ntiles;
          tile += (int64_t)gridDim.x * kBlockWaves) {
         // the weights are re-read from LDS in every tile: hoisted out of the
         // loop they would take ~400 registers and leave one wave per SIMD
@@ -309,8 +373,10 @@ __global__ __launch_bounds__(256) void k_leaf_softmax(const float* __restrict__ 
 }
 
 inline int grid_for(int64_t n, int per) { return (int)((n + per - 1) / per); }
+// one block per 16-row tile up to kMaxBlocks (the kernels deal tiles over the
+// blocks first, so a short batch runs one tile per CU)
 inline int mlp_blocks(int64_t rows) {
-    const int64_t b = ((rows + 15) / 16 + kBlockWaves - 1) / kBlockWaves;
+    const int64_t b = (rows + 15) / 16;
     return (int)(b < kMaxBlocks ? b : kMaxBlocks);
 }
 
@@ -333,11 +399,11 @@ int hg_fnn_leaf_eval(const float* features, int64_t T, int64_t N, int F, const i
     float* cval = logit + N;        // [N]
     hipLaunchKernelGGL(k_leaf_mlp<true>, dim3(mlp_blocks(T)), dim3(64 * kBlockWaves), 0, st, features, T, F,
                        nullptr, T, fc1_w, fc1_b, ln_w, ln_b, fc2_w, fc2_b, value_w, value_b, action1_w, action1_b,
-                       action2_w, action2_b, R, root_values, nullptr, nullptr);
+                       action2_w, action2_b, R, root_values, nullptr, nullptr, nullptr);
     if (N > 0)
         hipLaunchKernelGGL(k_leaf_mlp<false>, dim3(mlp_blocks(N)), dim3(64 * kBlockWaves), 0, st, features + T * F,
                            N, F, succ_leaf, T, fc1_w, fc1_b, ln_w, ln_b, fc2_w, fc2_b, value_w, value_b, action1_w,
-                           action1_b, action2_w, action2_b, R, cval, logit, nullptr);
+                           action1_b, action2_w, action2_b, R, cval, logit, nullptr, nullptr);
     hipLaunchKernelGGL(k_leaf_softmax, dim3(grid_for(T, 4)), dim3(256), 0, st, logit, cval, offsets, num_legal, T,
                        priors, child_q);
     return (int)hipGetLastError();
@@ -351,6 +417,8 @@ int64_t hg_fnn_leaf_eval_lists_workspace(int64_t T, int F) {
     b += cap * F * (int64_t)sizeof(float);                // successor features
     b = (b + 255) & ~(int64_t)255;
     b += (T * kE + 2 * cap) * (int64_t)sizeof(float);     // root half of the action tower, logits, child values
+    b = (b + 255) & ~(int64_t)255;
+    b += (int64_t)sizeof(PackedNet);                      // the network in the kernels' LDS order
     return b;
 }
 
@@ -378,14 +446,19 @@ int hg_fnn_leaf_eval_lists(const uint8_t* leaf_states, const uint8_t* legal_move
     float* R = reinterpret_cast<float*>(base + off);
     float* logit = R + T * kE;
     float* cval = logit + cap;
+    off += (T * kE + 2 * cap) * (int64_t)sizeof(float);
+    off = (off + 255) & ~(int64_t)255;
+    PackedNet* pk = reinterpret_cast<PackedNet*>(base + off);
+    hipLaunchKernelGGL(k_pack_net, dim3(grid_for(kPackThreads, 256)), dim3(256), 0, st, fc1_w, F, fc1_b, ln_w, ln_b,
+                       fc2_w, fc2_b, value_w, action1_w, action1_b, action2_w, pk);
     int e = hg_successor_rows(leaf_states, legal_moves, num_legal, T, workspace, X, stream);
     if (e) return e;
     hipLaunchKernelGGL(k_leaf_mlp<true>, dim3(mlp_blocks(T)), dim3(64 * kBlockWaves), 0, st, root_features, T, F,
                        nullptr, T, fc1_w, fc1_b, ln_w, ln_b, fc2_w, fc2_b, value_w, value_b, action1_w, action1_b,
-                       action2_w, action2_b, R, root_values, nullptr, nullptr);
+                       action2_w, action2_b, R, root_values, nullptr, nullptr, pk);
     hipLaunchKernelGGL(k_leaf_mlp<false>, dim3(mlp_blocks(cap)), dim3(64 * kBlockWaves), 0, st, X, cap, F, a2r, T,
                        fc1_w, fc1_b, ln_w, ln_b, fc2_w, fc2_b, value_w, value_b, action1_w, action1_b, action2_w,
-                       action2_b, R, cval, logit, total);
+                       action2_b, R, cval, logit, total, pk);
     hipLaunchKernelGGL(k_leaf_softmax, dim3(grid_for(T, 4)), dim3(256), 0, st, logit, cval, offsets, num_legal, T,
                        priors, child_q);
     return (int)hipGetLastError();
