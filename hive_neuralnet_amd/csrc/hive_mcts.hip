@@ -295,6 +295,150 @@ HW_INL int descend_rec(const Tree& T, int64_t g0, int node, ChildRec r, int pvc,
 }
 
 
+// The simulations of one (game, candidate) wave in PUCT mode with the
+// candidate's root child and that child's children held in registers for the
+// whole wave: every simulation enters the same root child and scores the same
+// children, so their records are loaded once, scored and updated in
+// registers (the same float operations in the same order as through memory:
+// no other wave touches this subtree during the kernel), and written back
+// once after the wave's last simulation.  Levels below go through memory as
+// before.  Children: up to kKidRegs per lane (64 kKidRegs in all).
+constexpr int kKidRegs = 4;
+// a child record in eight registers (terminal flag and move bytes packed)
+struct KidRec {
+    int vc;
+    float tv, vq, pr;
+    int fc, nc;
+    uint32_t mb01, mb2it;
+};
+__device__ __forceinline__ KidRec pack_kid(const ChildRec& r) {
+    return KidRec{r.vc, r.tv, r.vq, r.pr, r.fc, r.nc, (uint32_t)r.mb0 | ((uint32_t)r.mb1 << 16),
+                  (uint32_t)r.mb2 | ((uint32_t)(r.it != 0) << 16)};
+}
+__device__ __forceinline__ ChildRec unpack_kid(const KidRec& k) {
+    ChildRec r;
+    r.vc = k.vc;
+    r.tv = k.tv;
+    r.vq = k.vq;
+    r.pr = k.pr;
+    r.fc = k.fc;
+    r.nc = k.nc;
+    r.it = (int)(k.mb2it >> 16);
+    r.mb0 = (uint16_t)k.mb01;
+    r.mb1 = (uint16_t)(k.mb01 >> 16);
+    r.mb2 = (uint16_t)k.mb2it;
+    return r;
+}
+__device__ __forceinline__ float puct_kid(const KidRec& r, int pvc, float c_puct) {
+    int n = r.vc;
+    float q = n > 0 ? (-r.tv / (float)n) : 0.0f;
+    q -= r.vq;
+    float explore = c_puct * r.pr * sqrtf((float)pvc) / (1.0f + (float)n);
+    return q + explore;
+}
+__device__ __forceinline__ KidRec shfl_kid(const KidRec& r, int src) {
+    return KidRec{__shfl(r.vc, src, 64), __shfl(r.tv, src, 64), __shfl(r.vq, src, 64), __shfl(r.pr, src, 64),
+                  __shfl(r.fc, src, 64), __shfl(r.nc, src, 64), (uint32_t)__shfl((int)r.mb01, src, 64),
+                  (uint32_t)__shfl((int)r.mb2it, src, 64)};
+}
+HW_INL void select_slot_cached(const Tree& T, int64_t g0, int node1, ChildRec r1, int64_t g, int64_t B, int c,
+                               int C, int64_t rounds, float c_puct, const SelectOut& O, int lane) {
+    const int fc1 = r1.fc, nc1 = r1.nc;
+    const bool grown = !(fc1 < 0 || r1.it || nc1 == 0) && !(nc1 <= 0 || nc1 > 1024);
+    // the children that descend_rec would score: stop at the first one outside the pool
+    int nk = 0;
+    if (grown) nk = (int64_t)fc1 + nc1 <= T.M ? nc1 : (fc1 < T.M ? (int)(T.M - fc1) : 0);
+    KidRec kid[kKidRegs];
+    uint32_t dirty = 0;
+#pragma unroll
+    for (int j = 0; j < kKidRegs; j++) {
+        const int k = lane + 64 * j;
+        kid[j] = pack_kid(k < nk ? load_rec(T, g0 + fc1 + k) : r1);
+    }
+    for (int64_t kk = c; kk < rounds; kk += C) {
+        const int64_t sim = kk * B + g;
+        int plen = 0, vlen = 0;
+        // level 1: the root child (virtual loss in registers, path records in memory)
+        if (lane == 0) {
+            O.vl[sim * kDepth] = node1;
+            uint16_t* dst = reinterpret_cast<uint16_t*>(O.paths + sim * kDepth * 6);
+            dst[0] = r1.mb0;
+            dst[1] = r1.mb1;
+            dst[2] = r1.mb2;
+        }
+        plen = vlen = 1;
+        const int pvc = r1.vc + 1;
+        r1.vc = pvc;
+        r1.tv = r1.tv + -1.0f;
+        int node = node1;
+        if (grown && nk > 0) {
+            // level 2: PUCT over the children in registers, first maximum
+            float bs = -INFINITY;
+            int bi = 0x7fffffff;
+            int bj = 0;
+#pragma unroll
+            for (int j = 0; j < kKidRegs; j++) {
+                const int k = lane + 64 * j;
+                if (k < nk) {
+                    const float sc = puct_kid(kid[j], pvc, c_puct);
+                    if (sc > -1e30f && (sc > bs || (sc == bs && k < bi))) {
+                        bs = sc;
+                        bi = k;
+                        bj = j;
+                    }
+                }
+            }
+            const int k2 = wave_argmax_first(bs, bi);
+            if (k2 >= 0) {
+                KidRec mine = kid[0];
+#pragma unroll
+                for (int j = 1; j < kKidRegs; j++)
+                    if (bj == j) mine = kid[j];
+                const ChildRec win = unpack_kid(shfl_kid(mine, k2 & 63));
+                node = fc1 + k2;
+                if (lane == (k2 & 63)) {
+#pragma unroll
+                    for (int j = 0; j < kKidRegs; j++)
+                        if (j == (k2 >> 6)) {
+                            kid[j].vc = win.vc + 1;
+                            kid[j].tv = win.tv + -1.0f;
+                            dirty |= 1u << j;
+                        }
+                }
+                if (lane == 0) {
+                    O.vl[sim * kDepth + 1] = node;
+                    uint16_t* dst = reinterpret_cast<uint16_t*>(O.paths + (sim * kDepth + 1) * 6);
+                    dst[0] = win.mb0;
+                    dst[1] = win.mb1;
+                    dst[2] = win.mb2;
+                }
+                plen = vlen = 2;
+                node = descend_rec(T, g0, node, win, win.vc + 1, 2, c_puct, false, 0.0f, 0.0f, O, sim, plen, vlen,
+                                   lane);
+            }
+        }
+        __syncthreads();  // the next simulation reads this one's statistics below level 2
+        if (lane == 0) {
+            O.leaf[sim] = node;
+            O.plen[sim] = plen;
+            O.vlen[sim] = vlen;
+        }
+        zero_tails(O, sim, plen, vlen, lane);
+    }
+    // write back the statistics held in registers
+    if (lane == 0) {
+        T.vc[g0 + node1] = r1.vc;
+        T.tv[g0 + node1] = r1.tv;
+    }
+#pragma unroll
+    for (int j = 0; j < kKidRegs; j++)
+        if ((dirty >> j) & 1u) {
+            const int64_t ci = g0 + fc1 + lane + 64 * j;
+            T.vc[ci] = kid[j].vc;
+            T.tv[ci] = kid[j].tv;
+        }
+}
+
 // mcts_select_with_root_slots_kernel (mcts_tree.cuh:811-955), one wave per
 // (game, candidate).  A simulation forced into root child fc + slot touches
 // only that child's subtree (the root itself is not entered), so the
@@ -311,11 +455,19 @@ __global__ __launch_bounds__(64) void k_select_slots(Tree T, const int8_t* __res
     const int c = (int)(blockIdx.x % C);
     const int lane = threadIdx.x;
     if (g >= B) return;
+    const int lane_slot = lane < C ? root_slots[g * C + lane] : -1;
     bool dup = false;
-    for (int c1 = lane; c1 < C; c1 += 64) {
-        int s1 = root_slots[g * C + c1];
-        if (s1 < 0) continue;
-        for (int c2 = c1 + 1; c2 < C; c2++) dup |= root_slots[g * C + c2] == s1;
+    if (C <= 64) {  // the slots are in lanes: compare them by shuffles
+        for (int c2 = 1; c2 < C; c2++) {
+            const int s2 = __shfl(lane_slot, c2, 64);
+            dup |= lane < c2 && lane_slot >= 0 && lane_slot == s2;
+        }
+    } else {
+        for (int c1 = lane; c1 < C; c1 += 64) {
+            int s1 = root_slots[g * C + c1];
+            if (s1 < 0) continue;
+            for (int c2 = c1 + 1; c2 < C; c2++) dup |= root_slots[g * C + c2] == s1;
+        }
     }
     dup = __ballot(dup) != 0;
     if (dup && c != 0) return;
@@ -327,7 +479,18 @@ __global__ __launch_bounds__(64) void k_select_slots(Tree T, const int8_t* __res
     const int64_t ri = g0 + root;
     const int rfc = T.fc[ri], rnc = T.nc[ri];
     const bool rterm = T.it[ri] != 0;
-    const int lane_slot = lane < C ? root_slots[g * C + lane] : -1;
+    if (!det && !dup && active) {  // one root child for the whole wave: its level in registers
+        const int slot = C <= 64 ? __shfl(lane_slot, c, 64) : root_slots[g * C + c];
+        const int node1 = rfc + slot;
+        if (slot >= 0 && slot < max_root && !(rfc < 0 || rterm || rnc <= 0 || slot >= rnc) && node1 >= 0 &&
+            node1 < T.M) {
+            const ChildRec r1 = load_rec(T, g0 + node1);
+            if (r1.nc <= 64 * kKidRegs) {
+                select_slot_cached(T, g0, node1, r1, g, B, c, C, rounds, c_puct, O, lane);
+                return;
+            }
+        }
+    }
     for (int64_t k = dup ? 0 : c; k < rounds; k += dup ? 1 : C) {
         const int64_t sim = k * B + g;
         int cand = (int)(k % C);
