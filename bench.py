@@ -54,6 +54,7 @@ def parse_args():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-mcts", action="store_true", help="skip the C5 Gumbel self-play leg")
     ap.add_argument("--mcts-only", action="store_true", help="run only the C5 leg (its own JSON line)")
+    ap.add_argument("--c4-only", action="store_true", help="run only the C4 leg (its own JSON line)")
     ap.add_argument("--no-probe", action="store_true", help="skip the root tactical probe leg")
     ap.add_argument("--no-train", action="store_true", help="skip the training forward-batch leg")
     ap.add_argument("--no-c4", action="store_true", help="skip the C4 lockstep random-play leg")
@@ -76,6 +77,15 @@ def parse_args():
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 256 MiB device-to-device copy 3 times (rocprof counter calibration)")
     return ap.parse_args()
+
+
+def profile_figure(name, key):
+    """A `key: value` figure from a committed profiles/ summary, else None."""
+    path = os.path.join(ROOT, "profiles", name)
+    if not os.path.exists(path):
+        return None
+    m = re.search(rf"^{key}:\s*([0-9.eE+]+)", open(path).read(), re.M)
+    return float(m.group(1)) if m else None
 
 
 def traffic_per_launch(config="C2"):
@@ -332,7 +342,11 @@ def mcts_leg(args):
                    "roots": args.mcts_roots},
         "simulations": sims, "sim_rows": c["rows"], "mean_leaf_legal": Lm, "mean_vl_len": Dm,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": None,
+                     "frac": achieved / HBM_PEAK_GBS,
+                     "traffic": (profile_figure("mcts_c5_traffic.txt", "traffic_bytes_per_sim")
+                                 if args.mcts_roots == "empty" and cfg.wave_parallel else None),
+                     "traffic_is": "HBM bytes per simulation over the schedule's waves from the empty board, "
+                                   "rocprofv3 FETCH_SIZE + WRITE_SIZE (profiles/mcts_c5_traffic.txt)",
                      "bytes_per_sim": b_sim, "formula": "5976 + 535*L + 16*D"},
     }
     if not args.no_cpu:
@@ -455,7 +469,10 @@ def c4_leg(args):
                       "games": G, "max_plies": P, "seed": SEED + 3},
            "plies_played": done, "games_decided": int((results != 0).sum()),
            "roofline": {"bound": "hbm", "achieved": done * C4_BYTES_PER_PLY / wall / 1e9, "peak": HBM_PEAK_GBS,
-                        "unit": "GB/s", "frac": done * C4_BYTES_PER_PLY / wall / 1e9 / HBM_PEAK_GBS, "traffic": None,
+                        "unit": "GB/s", "frac": done * C4_BYTES_PER_PLY / wall / 1e9 / HBM_PEAK_GBS,
+                        "traffic": profile_figure("c4_traffic.txt", "traffic_bytes_per_ply"),
+                        "traffic_is": "HBM bytes per played ply, from rocprofv3 FETCH_SIZE + WRITE_SIZE "
+                                      "(profiles/c4_traffic.txt)",
                         "bytes_per_ply": C4_BYTES_PER_PLY, "model": "unfused: state read + write-back per ply"},
            "final_state_hash": f"{fnv1a64_of(hashes):016x}"}
     if not args.no_cpu:
@@ -589,6 +606,9 @@ def main():
 
     if args.mcts_only:
         print(json.dumps(mcts_leg(args)))
+        return
+    if args.c4_only:
+        print(json.dumps(c4_leg(args)))
         return
 
     result = positions_leg(args, args.batch, args.mask, args.max_ply)
