@@ -72,6 +72,8 @@ def parse_args():
     ap.add_argument("--mcts-roots", choices=("empty", "midgame"), default="empty")
     ap.add_argument("--graphs", choices=("auto", "on", "off"), default="auto",
                     help="C5 simulation waves from HIP graphs: auto = waves under 2,048 rows")
+    ap.add_argument("--ply-graphs", choices=("auto", "on", "off"), default="auto",
+                    help="C5 search phase of a ply from one HIP graph: auto = when every round runs on one range")
     ap.add_argument("--native-waves", choices=("on", "off"), default="on",
                     help="C5 simulation waves as one library call each (on) or through the step entry points")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -296,6 +298,7 @@ def mcts_leg(args):
                         max_tree_nodes=1 + S * 256, wave_parallel=args.mcts_waves == "schedule")
     orch = FNNMCTSOrchestrator(net, cfg)
     orch.use_graphs = {"auto": None, "on": True, "off": False}[args.graphs]
+    orch.use_ply_graphs = {"auto": None, "on": True, "off": False}[args.ply_graphs]
     orch.game_parts = args.game_parts
     orch.native_waves = args.native_waves == "on"
     ext = orch.ext
@@ -313,10 +316,13 @@ def mcts_leg(args):
         orch.apply_and_rebase(states, tree, r)
         active.logical_and_(ext.check_results_batch(states, G) == 0)
 
+    # counters first: their address is part of a captured ply graph's key, so the
+    # warm-up ply captures the graph the timed plies replay
+    orch.enable_counters()
     for _ in range(args.mcts_warmup):
         ply()
     timed_roots = states.clone()  # the first timed ply's roots (the CPU player searches the same positions)
-    orch.enable_counters()
+    orch._stats.zero_()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.mcts_plies):

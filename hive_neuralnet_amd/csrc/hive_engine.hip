@@ -9,6 +9,7 @@
 #include <stdint.h>
 
 #include "../../include/hive_gpu.h"
+#include "hive_leaf.hpp"
 #include "hive_phases.hpp"
 
 using namespace hw;
@@ -350,45 +351,12 @@ __global__ void k_rows_map(const int32_t* __restrict__ nlegal, const int64_t* __
 }
 
 // k_rows_plan: the offsets, total and map of k_rows_offsets + k_rows_map in
-// one launch, for batches of at most kPlanLeaves leaves.  Block b owns
-// leaves [256 b, 256 b + 256): it adds up the clamped counts before its range
-// itself (at most kPlanLeaves reads, from L2), scans its own counts, writes
-// their offsets and then their rows, each wave one leaf at a time.  Sums stay
-// below kPlanLeaves * 256 (int).
-constexpr int64_t kPlanLeaves = 32768;
-__device__ __forceinline__ int clamp_legal(int n) { return n < 0 ? 0 : (n > kMaxLegal ? kMaxLegal : n); }
+// one launch, for batches of at most kPlanLeaves leaves (rows_plan_block,
+// hive_leaf.hpp).
 __global__ __launch_bounds__(256) void k_rows_plan(const int32_t* __restrict__ nlegal, int64_t T,
                                                    int64_t* __restrict__ offsets, int64_t* __restrict__ total,
                                                    int64_t* __restrict__ a2r, int64_t* __restrict__ mi) {
-    __shared__ int carry_w[4], tot_w[4];
-    __shared__ int cnt_s[256], off_s[256];
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const int lo = (int)blockIdx.x * 256;
-    int before = 0;
-#pragma unroll 8
-    for (int t = tid; t < lo; t += 256) before += clamp_legal(nlegal[t]);
-    const int t = lo + tid;
-    const int v = t < T ? clamp_legal(nlegal[t]) : 0;
-    const int incl = wave_incl_scan(v);
-    const int cw = wave_sum(before);
-    if (lane == 0) carry_w[w] = cw;
-    if (lane == 63) tot_w[w] = incl;
-    __syncthreads();
-    int off = carry_w[0] + carry_w[1] + carry_w[2] + carry_w[3] + incl - v;
-    for (int k = 0; k < w; k++) off += tot_w[k];
-    cnt_s[tid] = v;
-    off_s[tid] = off;
-    if (t < T) offsets[t] = off;
-    if (tid == 255 && lo + 256 >= T) *total = (int64_t)off + v;  // the block holding leaf T - 1
-    __syncthreads();
-    const int nl = T - lo < 256 ? (int)(T - lo) : 256;
-    for (int j = w; j < nl; j += 4) {
-        const int n = cnt_s[j], o = off_s[j];
-        for (int k = lane; k < n; k += 64) {
-            a2r[o + k] = lo + j;
-            mi[o + k] = k;
-        }
-    }
+    rows_plan_block(nlegal, T, offsets, total, a2r, mi, (int)blockIdx.x);
 }
 
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kSuccWaves))) void k_successor_rows(const uint8_t* __restrict__ states,
@@ -522,22 +490,15 @@ int hg_successor_rows(const uint8_t* states, const uint8_t* legal_moves, const i
     if (T <= 0) return 0;
     if (((uintptr_t)workspace & 7)) return (int)hipErrorInvalidValue;
     hipStream_t s = (hipStream_t)stream;
-    int64_t* offsets = reinterpret_cast<int64_t*>(workspace);
-    int64_t* total = offsets + T;
-    int64_t* a2r = total + 1;
-    int64_t* mi = a2r + T * kMaxLegal;
     if (T <= kPlanLeaves) {
-        hipLaunchKernelGGL(k_rows_plan, dim3((unsigned)((T + 255) / 256)), dim3(256), 0, s, num_legal, T, offsets,
-                           total, a2r, mi);
+        const RowsPlan R = rows_plan_of(workspace, T);
+        hipLaunchKernelGGL(k_rows_plan, dim3((unsigned)((T + 255) / 256)), dim3(256), 0, s, num_legal, T, R.offsets,
+                           R.total, R.a2r, R.mi);
     } else {
-        hipLaunchKernelGGL(k_rows_offsets, dim3(1), dim3(1024), 0, s, num_legal, T, offsets, total);
-        hipLaunchKernelGGL(k_rows_map, dim3((unsigned)((T * kMaxLegal + 255) / 256)), dim3(256), 0, s, num_legal,
-                           offsets, T, a2r, mi);
+        int e = successor_rows_plan_large(num_legal, T, workspace, s);
+        if (e) return e;
     }
-    const int64_t pairs = (T * kMaxLegal + kSuccRows * kPosPerWave - 1) / (kSuccRows * kPosPerWave);
-    const unsigned grid = (unsigned)(pairs < kSuccGrid ? pairs : kSuccGrid);
-    hipLaunchKernelGGL(k_successor_rows, dim3(grid), dim3(64), 0, s, states, legal_moves, a2r, mi, total, T, features);
-    return finish();
+    return successor_rows_after_plan(states, legal_moves, T, workspace, features, s);
 }
 
 int hg_fnn_successor_features(const uint8_t* states, const uint8_t* legal_moves, int64_t num_roots,
@@ -565,3 +526,25 @@ int hg_random_play_step(uint8_t* states, const uint8_t* moves, const int32_t* nu
 }
 
 }  // extern "C"
+
+namespace hw {
+
+int successor_rows_plan_large(const int32_t* num_legal, int64_t T, void* workspace, hipStream_t s) {
+    const RowsPlan R = rows_plan_of(workspace, T);
+    hipLaunchKernelGGL(k_rows_offsets, dim3(1), dim3(1024), 0, s, num_legal, T, R.offsets, R.total);
+    hipLaunchKernelGGL(k_rows_map, dim3((unsigned)((T * kMaxLegal + 255) / 256)), dim3(256), 0, s, num_legal,
+                       R.offsets, T, R.a2r, R.mi);
+    return finish();
+}
+
+int successor_rows_after_plan(const uint8_t* states, const uint8_t* legal_moves, int64_t T, void* workspace,
+                              float* features, hipStream_t s) {
+    const RowsPlan R = rows_plan_of(workspace, T);
+    const int64_t pairs = (T * kMaxLegal + kSuccRows * kPosPerWave - 1) / (kSuccRows * kPosPerWave);
+    const unsigned grid = (unsigned)(pairs < kSuccGrid ? pairs : kSuccGrid);
+    hipLaunchKernelGGL(k_successor_rows, dim3(grid), dim3(64), 0, s, states, legal_moves, R.a2r, R.mi, R.total, T,
+                       features);
+    return finish();
+}
+
+}  // namespace hw

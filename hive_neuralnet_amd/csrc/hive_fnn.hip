@@ -46,6 +46,7 @@
 #include <stdint.h>
 
 #include "../../include/hive_gpu.h"
+#include "hive_leaf.hpp"
 
 namespace {
 
@@ -69,8 +70,9 @@ struct MlpLds {
 enum { kB1, kLnW, kLnB, kB2, kWv, kWa2, kBa1 };
 
 // The network laid out once per evaluation in the order the MLP kernels keep
-// in LDS (k_pack_net), so that each of their blocks fills LDS with straight
-// 16-byte copies instead of gathering and permuting the weights itself.
+// in LDS (pack_net_at, in the evaluation's first launch), so that each of
+// their blocks fills LDS with straight 16-byte copies instead of gathering
+// and permuting the weights itself.
 struct PackedNet {
     f4 w1[32][64];
     f4 w2[16][64];
@@ -87,13 +89,14 @@ __device__ __forceinline__ void perm_index(int i, bool first, int& m, int& k) {
     k = first ? 32 * (l >> 4) + s : 16 * (s >> 2) + 4 * (l >> 4) + (s & 3);
 }
 
-__global__ __launch_bounds__(256) void k_pack_net(const float* __restrict__ w1, int F, const float* __restrict__ b1,
-                                                  const float* __restrict__ lnw, const float* __restrict__ lnb,
-                                                  const float* __restrict__ w2, const float* __restrict__ b2,
-                                                  const float* __restrict__ wv, const float* __restrict__ a1w,
-                                                  const float* __restrict__ a1b, const float* __restrict__ a2w,
-                                                  PackedNet* __restrict__ out) {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;  // one float of the packed layout
+// thread i of the packing writes float i of the packed layout (k_leaf_prep's
+// packing blocks)
+__device__ __forceinline__ void pack_net_at(int i, const float* __restrict__ w1, int F, const float* __restrict__ b1,
+                                            const float* __restrict__ lnw, const float* __restrict__ lnb,
+                                            const float* __restrict__ w2, const float* __restrict__ b2,
+                                            const float* __restrict__ wv, const float* __restrict__ a1w,
+                                            const float* __restrict__ a1b, const float* __restrict__ a2w,
+                                            PackedNet* __restrict__ out) {
     constexpr int n1 = 32 * 64 * 4, n2 = 16 * 64 * 4;
     int m, k;
     if (i < n1) {
@@ -118,6 +121,65 @@ __global__ __launch_bounds__(256) void k_pack_net(const float* __restrict__ w1, 
     }
 }
 constexpr int kPackThreads = 32 * 64 * 4 + 3 * 16 * 64 * 4 + kE;
+constexpr int kPackBlocks = (kPackThreads + 255) / 256;
+
+// The first launch of a fused leaf evaluation, three kinds of 256-thread
+// blocks side by side (none waits for another): the successor-row plan of
+// up to kPlanLeaves leaves (plan_blocks blocks, hw::rows_plan_block), the
+// network in the MLP kernels' layout (kPackBlocks blocks, pack_net_at)
+// and, with `stats`, the simulation wave's search counters (one block per
+// 1,024 simulations: leaves reached, their legal counts, their virtual-loss
+// lengths, rows; integer sums added with device atomics).
+__global__ __launch_bounds__(256) void k_leaf_prep(const int32_t* __restrict__ nlegal, int64_t T, int plan_blocks,
+                                                   hw::RowsPlan plan, const float* __restrict__ w1, int F,
+                                                   const float* __restrict__ b1, const float* __restrict__ lnw,
+                                                   const float* __restrict__ lnb, const float* __restrict__ w2,
+                                                   const float* __restrict__ b2, const float* __restrict__ wv,
+                                                   const float* __restrict__ a1w, const float* __restrict__ a1b,
+                                                   const float* __restrict__ a2w, PackedNet* __restrict__ pk,
+                                                   const int32_t* __restrict__ leaf_idx,
+                                                   const int32_t* __restrict__ vl_lens,
+                                                   unsigned long long* __restrict__ stats) {
+    int b = (int)blockIdx.x;
+    if (b < plan_blocks) {
+        hw::rows_plan_block(nlegal, T, plan.offsets, plan.total, plan.a2r, plan.mi, b);
+        return;
+    }
+    b -= plan_blocks;
+    if (b < kPackBlocks) {
+        pack_net_at(b * 256 + (int)threadIdx.x, w1, F, b1, lnw, lnb, w2, b2, wv, a1w, a1b, a2w, pk);
+        return;
+    }
+    b -= kPackBlocks;
+    __shared__ unsigned long long part[3][4];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    unsigned long long a = 0, n = 0, d = 0;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const int64_t i = (int64_t)b * 1024 + k * 256 + tid;
+        if (i < T && leaf_idx[i] >= 0) {
+            a += 1;
+            n += (unsigned long long)(long long)nlegal[i];
+            d += (unsigned long long)(long long)vl_lens[i];
+        }
+    }
+    for (int off = 32; off > 0; off >>= 1) {
+        a += __shfl_xor(a, off);
+        n += __shfl_xor(n, off);
+        d += __shfl_xor(d, off);
+    }
+    if (lane == 0) {
+        part[0][w] = a;
+        part[1][w] = n;
+        part[2][w] = d;
+    }
+    __syncthreads();
+    if (tid < 3) {
+        atomicAdd(&stats[tid], part[tid][0] + part[tid][1] + part[tid][2] + part[tid][3]);
+    } else if (tid == 3 && b == 0) {
+        atomicAdd(&stats[3], (unsigned long long)T);
+    }
+}
 
 // sigmoid from the hardware exp2 and reciprocal (v_exp_f32, v_rcp_f32):
 // ~1e-6 relative against the correctly rounded form, inside the 1e-5
@@ -428,17 +490,31 @@ int hg_fnn_leaf_eval_lists(const uint8_t* leaf_states, const uint8_t* legal_move
                            const float* value_w, float value_b, const float* action1_w, const float* action1_b,
                            const float* action2_w, float action2_b, void* workspace, float* priors,
                            float* root_values, float* child_q, void* stream) {
+    return hw::leaf_eval_lists(leaf_states, legal_moves, num_legal, root_features, T, F, fc1_w, fc1_b, ln_w, ln_b,
+                               fc2_w, fc2_b, value_w, value_b, action1_w, action1_b, action2_w, action2_b, workspace,
+                               priors, root_values, child_q, nullptr, nullptr, nullptr, (hipStream_t)stream);
+}
+
+}  // extern "C"
+
+namespace hw {
+
+int leaf_eval_lists(const uint8_t* leaf_states, const uint8_t* legal_moves, const int32_t* num_legal,
+                    const float* root_features, int64_t T, int F, const float* fc1_w, const float* fc1_b,
+                    const float* ln_w, const float* ln_b, const float* fc2_w, const float* fc2_b,
+                    const float* value_w, float value_b, const float* action1_w, const float* action1_b,
+                    const float* action2_w, float action2_b, void* workspace, float* priors, float* root_values,
+                    float* child_q, const int32_t* leaf_idx, const int32_t* vl_lens, int64_t* stats,
+                    hipStream_t st) {
     if (T < 0 || F <= 0 || F > kFMax || (F & 1)) return (int)hipErrorInvalidValue;
     if (((uintptr_t)root_features & 7) || ((uintptr_t)workspace & 255)) return (int)hipErrorInvalidValue;
     if (F != 122) return (int)hipErrorInvalidValue;  // the successor rows are the engine's 122 features
+    if (stats && (!leaf_idx || !vl_lens)) return (int)hipErrorInvalidValue;
     if (T == 0) return 0;
-    hipStream_t st = (hipStream_t)stream;
     const int64_t cap = T * kSlots;
     uint8_t* base = reinterpret_cast<uint8_t*>(workspace);
     int64_t off = hg_successor_rows_workspace(T);
-    int64_t* offsets = reinterpret_cast<int64_t*>(base);
-    int64_t* total = offsets + T;
-    int64_t* a2r = total + 1;
+    const RowsPlan plan = rows_plan_of(workspace, T);
     off = (off + 255) & ~(int64_t)255;
     float* X = reinterpret_cast<float*>(base + off);
     off += cap * F * (int64_t)sizeof(float);
@@ -449,19 +525,31 @@ int hg_fnn_leaf_eval_lists(const uint8_t* leaf_states, const uint8_t* legal_move
     off += (T * kE + 2 * cap) * (int64_t)sizeof(float);
     off = (off + 255) & ~(int64_t)255;
     PackedNet* pk = reinterpret_cast<PackedNet*>(base + off);
-    hipLaunchKernelGGL(k_pack_net, dim3(grid_for(kPackThreads, 256)), dim3(256), 0, st, fc1_w, F, fc1_b, ln_w, ln_b,
-                       fc2_w, fc2_b, value_w, action1_w, action1_b, action2_w, pk);
-    int e = hg_successor_rows(leaf_states, legal_moves, num_legal, T, workspace, X, stream);
+    // plan, network layout and counters in one launch (the plan of a batch
+    // over kPlanLeaves leaves takes its own two launches first)
+    int plan_blocks = 0;
+    if (T <= kPlanLeaves) {
+        plan_blocks = (int)((T + 255) / 256);
+    } else {
+        int e = successor_rows_plan_large(num_legal, T, workspace, st);
+        if (e) return e;
+    }
+    const int stat_blocks = stats ? (int)((T + 1023) / 1024) : 0;
+    hipLaunchKernelGGL(k_leaf_prep, dim3((unsigned)(plan_blocks + kPackBlocks + stat_blocks)), dim3(256), 0, st,
+                       num_legal, T, plan_blocks, plan, fc1_w, F, fc1_b, ln_w, ln_b, fc2_w, fc2_b, value_w,
+                       action1_w, action1_b, action2_w, pk, leaf_idx, vl_lens,
+                       reinterpret_cast<unsigned long long*>(stats));
+    int e = successor_rows_after_plan(leaf_states, legal_moves, T, workspace, X, st);
     if (e) return e;
     hipLaunchKernelGGL(k_leaf_mlp<true>, dim3(mlp_blocks(T)), dim3(64 * kBlockWaves), 0, st, root_features, T, F,
                        nullptr, T, fc1_w, fc1_b, ln_w, ln_b, fc2_w, fc2_b, value_w, value_b, action1_w, action1_b,
                        action2_w, action2_b, R, root_values, nullptr, nullptr, pk);
-    hipLaunchKernelGGL(k_leaf_mlp<false>, dim3(mlp_blocks(cap)), dim3(64 * kBlockWaves), 0, st, X, cap, F, a2r, T,
-                       fc1_w, fc1_b, ln_w, ln_b, fc2_w, fc2_b, value_w, value_b, action1_w, action1_b, action2_w,
-                       action2_b, R, cval, logit, total, pk);
-    hipLaunchKernelGGL(k_leaf_softmax, dim3(grid_for(T, 4)), dim3(256), 0, st, logit, cval, offsets, num_legal, T,
-                       priors, child_q);
+    hipLaunchKernelGGL(k_leaf_mlp<false>, dim3(mlp_blocks(cap)), dim3(64 * kBlockWaves), 0, st, X, cap, F,
+                       plan.a2r, T, fc1_w, fc1_b, ln_w, ln_b, fc2_w, fc2_b, value_w, value_b, action1_w, action1_b,
+                       action2_w, action2_b, R, cval, logit, plan.total, pk);
+    hipLaunchKernelGGL(k_leaf_softmax, dim3(grid_for(T, 4)), dim3(256), 0, st, logit, cval, plan.offsets,
+                       num_legal, T, priors, child_q);
     return (int)hipGetLastError();
 }
 
-}  // extern "C"
+}  // namespace hw

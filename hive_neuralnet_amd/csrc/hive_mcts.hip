@@ -19,6 +19,7 @@
 #include <stdint.h>
 
 #include "../../include/hive_gpu.h"
+#include "hive_leaf.hpp"
 #include "hive_phases.hpp"
 
 using namespace hw;
@@ -622,6 +623,55 @@ __global__ __launch_bounds__(64) void k_replay(const uint8_t* __restrict__ roots
     uint4* dst = reinterpret_cast<uint4*>(leaves + sim * kStateBytes);
     for (int i = lane; i < kStateBytes / 16; i += 64) dst[i] = row[i];
     if (results && lane == 0) results[sim] = reinterpret_cast<const uint8_t*>(row)[OFF_RESULT];
+}
+
+// The replay (k_replay with its results) and the leaf rows' legal lists +
+// features (k_legal<moves, features>) of a simulation wave in one launch,
+// two simulations per workgroup (lane groups of 32, as k_legal): a group
+// assembles its leaf row in LDS (the root's row, then the path moves applied
+// by one lane), writes the row and its result out (a zero row and 0 for an
+// idle simulation) and, after a barrier, runs the position program on the
+// row it wrote.  The LDS of the row and of the position program's board are
+// the same bytes, used one after the other.
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(6))) void k_replay_legal(
+    const uint8_t* __restrict__ roots, int64_t B, uint8_t* __restrict__ leaves, const uint8_t* __restrict__ paths,
+    const int32_t* __restrict__ plen, const int32_t* __restrict__ leaf_idx, int64_t T, int32_t* __restrict__ results,
+    uint8_t* __restrict__ moves_out, int32_t* __restrict__ n_out, float* __restrict__ feat_out) {
+    __shared__ union LeafLds {
+        Pos P;
+        uint4 row[kStateBytes / 16];
+    } U[kPosPerWave];
+    const int grp = threadIdx.x >> 5, l = threadIdx.x & 31;
+    const int64_t i = (int64_t)blockIdx.x * kPosPerWave + grp;
+    const bool live = i < T;
+    const int64_t sim = live ? i : T - 1;  // a group past the end reads the last row and writes nothing
+    uint4* row = U[grp].row;
+    const bool idle = leaf_idx[sim] < 0;
+    if (!idle) {
+        const uint4* src = reinterpret_cast<const uint4*>(roots + (sim % B) * kStateBytes);
+        for (int k = l; k < kStateBytes / 16; k += 32) row[k] = src[k];
+    }
+    __syncthreads();
+    if (!idle && l == 0) {
+        RowView v{reinterpret_cast<uint8_t*>(row)};
+        const int n = plen[sim];
+        const uint8_t* p = paths + sim * kDepth * 6;
+        for (int d = 0; d < n && d < kDepth; d++, p += 6) v.apply(p[0], p[1], p[2] | (p[3] << 8), p[4] | (p[5] << 8));
+    }
+    __syncthreads();
+    uint8_t* leaf_row = leaves + sim * kStateBytes;
+    if (live) {
+        uint4* dst = reinterpret_cast<uint4*>(leaf_row);
+        const uint4 z = make_uint4(0u, 0u, 0u, 0u);
+        for (int k = l; k < kStateBytes / 16; k += 32) dst[k] = idle ? z : row[k];
+        if (l == 0) results[sim] = idle ? 0 : reinterpret_cast<const uint8_t*>(row)[OFF_RESULT];
+    }
+    // the barrier's workgroup-scope fences order the row's stores before the
+    // reads below (the same workgroup; a device-scope fence would write back
+    // the whole L2 on every workgroup)
+    __syncthreads();
+    run_legal<true, true, false>(U[grp].P, leaf_row, threadIdx.x, live ? moves_out + sim * (kMaxLegal * 6) : nullptr,
+                                 live ? n_out + sim : nullptr, live ? feat_out + sim * kFeat : nullptr, nullptr);
 }
 
 // centroid of a state row (compute_centroid, state_encoder.cuh:889-906)
@@ -1771,20 +1821,18 @@ int hg_mcts_wave_root_slots(const hg_tree* tree, const uint8_t* root_states, con
                                       c_puct, B, W, deterministic_non_root, non_root_sigma, q_penalty, buf->leaf_idx,
                                       buf->move_paths, buf->path_lens, buf->vl_paths, buf->vl_lens, stream);
     if (e) return e;
-    // replay into the leaf rows (idle simulations: zero rows) with each leaf's result
-    hipLaunchKernelGGL(k_replay, dim3((unsigned)T), dim3(64), 0, s, root_states, B, buf->leaf_states,
-                       buf->move_paths, buf->path_lens, buf->leaf_idx, T, 1, buf->results);
+    // replay into the leaf rows (idle simulations: zero rows) with each leaf's
+    // result, and the leaves' legal lists + features, in one launch
+    hipLaunchKernelGGL(k_replay_legal, dim3((unsigned)((T + kPosPerWave - 1) / kPosPerWave)), dim3(64), 0, s,
+                       root_states, B, buf->leaf_states, buf->move_paths, buf->path_lens, buf->leaf_idx, T,
+                       buf->results, buf->legal_moves, buf->num_legal, buf->features);
     if ((e = finish())) return e;
-    if ((e = hg_generate_legal_moves_and_fnn_features(buf->leaf_states, T, buf->legal_moves, buf->num_legal,
-                                                      buf->features, stream)))
-        return e;
-    if ((e = hg_fnn_leaf_eval_lists(buf->leaf_states, buf->legal_moves, buf->num_legal, buf->features, T, net->F,
-                                    net->fc1_w, net->fc1_b, net->ln_w, net->ln_b, net->fc2_w, net->fc2_b,
-                                    net->value_w, net->value_b, net->action1_w, net->action1_b, net->action2_w,
-                                    net->action2_b, buf->leaf_workspace, buf->priors, buf->values, buf->child_q,
-                                    stream)))
-        return e;
-    if (buf->stats && (e = hg_mcts_wave_stats(buf->leaf_idx, buf->num_legal, buf->vl_lens, T, buf->stats, stream)))
+    // the leaf evaluation, the search counters (when asked for) in its first launch
+    if ((e = hw::leaf_eval_lists(buf->leaf_states, buf->legal_moves, buf->num_legal, buf->features, T, net->F,
+                                 net->fc1_w, net->fc1_b, net->ln_w, net->ln_b, net->fc2_w, net->fc2_b,
+                                 net->value_w, net->value_b, net->action1_w, net->action1_b, net->action2_w,
+                                 net->action2_b, buf->leaf_workspace, buf->priors, buf->values, buf->child_q,
+                                 buf->leaf_idx, buf->vl_lens, buf->stats, s)))
         return e;
     return hg_mcts_expand_backprop_dense_ws(tree, buf->child_q, buf->leaf_idx, buf->leaf_states, buf->legal_moves,
                                             buf->num_legal, buf->priors, buf->results, buf->values, buf->vl_paths,

@@ -149,6 +149,15 @@ class FNNMCTSOrchestrator:
         self.graph_rows = 2048
         self.max_graphs = 64
         self._graphs: dict = {}
+        # the search phase of a ply -- every simulation wave of the four
+        # rounds and the halving decisions, whose shapes the configuration
+        # fixes -- replayed from one captured HIP graph: None = whenever every
+        # round runs on one game range (and use_graphs is not False), True /
+        # False = always / never.  The ply's candidates, Gumbel scores and
+        # active games are copied into the graph's buffers before each replay.
+        self.use_ply_graphs: bool | None = None
+        self.max_ply_graphs = 4
+        self._ply_graphs: dict = {}
         # simulation waves of disjoint game ranges on their own streams, so that
         # one range's latency-bound tree walks overlap another's leaf evaluation
         # (games are independent: results are identical to one range); None =
@@ -404,15 +413,18 @@ class FNNMCTSOrchestrator:
         self.ext.mcts_apply_root_noise(*self._tree_args(tree), torch.from_numpy(noise).cuda(), tree["root_node"],
                                        max_nc, cfg.dirichlet_epsilon, 1.0, B, self._max_nodes)
 
+    def _game_parts_for(self, B, C, W):
+        """Game ranges of a round's waves (W simulations per candidate column, C columns)."""
+        if self.game_parts is not None:
+            return self.game_parts
+        return 2 if B >= self.split_min_games and W * C * B >= 2 * self.split_min_rows else 1
+
     def _run_simulations_for_root_slots(self, tree, root_states, game_active, root_slots, B, per_slot, wave_size):
         cfg = self.config
         C = int(root_slots.shape[1])
         W = max(1, int(wave_size))
         q_penalty = float(cfg.virtual_q_penalty) if cfg.deterministic_non_root and W > 1 else 0.0
-        if self.game_parts is not None:
-            parts = self.game_parts
-        else:
-            parts = 2 if B >= self.split_min_games and W * C * B >= 2 * self.split_min_rows else 1
+        parts = self._game_parts_for(B, C, W)
         if parts > 1 and B >= parts:
             self.max_game_parts = max(self.max_game_parts, parts)
             return self._run_split(tree, root_states, game_active, root_slots, B, C, per_slot, W, q_penalty, parts)
@@ -582,6 +594,83 @@ class FNNMCTSOrchestrator:
         graph.replay()
         return outs
 
+    def _round_shapes(self, C):
+        """(C, per_slot, W) of each of the four rounds for C candidate columns."""
+        cfg = self.config
+        per_round = max(1, cfg.num_simulations // _GUMBEL_ROUNDS)
+        out = []
+        for r in range(_GUMBEL_ROUNDS):
+            W = _GUMBEL_WAVE_SCHEDULE[min(r, len(_GUMBEL_WAVE_SCHEDULE) - 1)] if cfg.wave_parallel else 1
+            out.append((C, max(1, per_round // C), W))
+            if C > 1:
+                C //= 2
+        return out
+
+    def _ply_graph_ok(self, B, C) -> bool:
+        if self.use_ply_graphs is False or self.use_graphs is False or self.keep_last_leaves:
+            return False
+        if not (self._native_waves_ok() and self.native_halving and C <= 64):
+            return False
+        single = all(self._game_parts_for(B, c, w) <= 1 or B < self._game_parts_for(B, c, w)
+                     for c, _, w in self._round_shapes(C))
+        return single
+
+    def _ply_graph(self, tree, root_states, game_active, cand, base, B):
+        """_sequential_halving (fnn_mcts_orchestrator.py:650-731) replayed from a
+        captured HIP graph: every wave of the four rounds on one buffer set of its
+        own (hg_mcts_wave_root_slots), the halving decisions (hg_gumbel_halving)
+        and the final choice.  Kept per tree, root-state tensor, network, counters
+        and search configuration; the candidates, Gumbel scores and active games
+        are copied into the graph's buffers before each replay.  Holds only
+        kernel launches (no memset nodes).  Returns (chosen slot [B] int64,
+        simulations)."""
+        cfg = self.config
+        C = int(cand.shape[1])
+        net_key = tuple(p.data_ptr() for p in self.net.parameters()) + tuple(self._head_biases or ())
+        stats = self._stats if self.counters is not None else None
+        key = (tuple(v.data_ptr() for v in tree.values()), B, C, root_states.data_ptr(), net_key,
+               stats.data_ptr() if stats is not None else None, cfg.num_simulations, bool(cfg.wave_parallel),
+               float(cfg.c_puct), bool(cfg.deterministic_non_root), float(cfg.non_root_sigma),
+               float(cfg.virtual_q_penalty), float(cfg.c_visit), float(cfg.c_scale), int(cfg.root_q_min_visits))
+        entry = self._ply_graphs.get(key)
+        if entry is None:
+            if len(self._ply_graphs) >= self.max_ply_graphs:  # oldest first
+                self._ply_graphs.pop(next(iter(self._ply_graphs)))
+            static = {"cand": cand.clone(), "base": base.clone(), "active": game_active.clone()}
+            cap = max(min(w, per) * c * B for c, per, w in self._round_shapes(C))
+            plan = self.ext.prepare_wave_root_slots(*self._tree_args(tree), tree["child_init_q"], B, self._max_nodes,
+                                                    self.net, self._head_biases, capacity=cap)
+            hg_tree = self._packed_tree(tree, B)
+
+            def run_round(c, per_slot, wave):
+                W = max(1, int(wave))
+                q_penalty = float(cfg.virtual_q_penalty) if cfg.deterministic_non_root and W > 1 else 0.0
+                Cc = int(c.shape[1])
+                sims = 0
+                for k in range(math.ceil(per_slot / W)):
+                    w = min(W, per_slot - k * W)
+                    plan.run(root_states, static["active"], tree["root_node"], c, Cc, self._max_legal, cfg.c_puct, w,
+                             cfg.deterministic_non_root, cfg.non_root_sigma, q_penalty, stats=stats)
+                    sims += w * Cc * B
+                return sims
+
+            def decide(c, final):
+                return self.ext.gumbel_halving(hg_tree, tree["root_node"], c, static["base"], cfg.c_visit,
+                                               cfg.c_scale, int(cfg.root_q_min_visits), final)
+
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                chosen, sims = self._sequential_halving(static["cand"], static["base"], run_round, None, decide)
+            entry = (graph, static, chosen, sims, plan, hg_tree)
+            self._ply_graphs[key] = entry
+            # capture records the launches without running them: the replay below runs this ply
+        graph, static, chosen, sims = entry[:4]
+        static["cand"].copy_(cand)
+        static["base"].copy_(base)
+        static["active"].copy_(game_active)
+        graph.replay()
+        return chosen.clone(), sims
+
     def _root_child_stats(self, tree, B, slots):  # _gather_root_candidate_stats / _gather_root_child_stats
         row = torch.arange(B, device="cuda", dtype=torch.long)
         root = tree["root_node"]
@@ -681,11 +770,14 @@ class FNNMCTSOrchestrator:
                 hg_tree = self._packed_tree(tree, B)
                 decide = lambda c, final: self.ext.gumbel_halving(  # noqa: E731
                     hg_tree, tree["root_node"], c, base, cfg.c_visit, cfg.c_scale, int(cfg.root_q_min_visits), final)
-            chosen, sims = self._sequential_halving(
-                cand, base,
-                lambda c, per_slot, wave: self._run_simulations_for_root_slots(tree, states, game_active, c, B,
-                                                                               per_slot, wave),
-                lambda c: self._root_child_stats(tree, B, c), decide)
+            if self._ply_graph_ok(B, int(cand.shape[1])):
+                chosen, sims = self._ply_graph(tree, states, game_active, cand, base, B)
+            else:
+                chosen, sims = self._sequential_halving(
+                    cand, base,
+                    lambda c, per_slot, wave: self._run_simulations_for_root_slots(tree, states, game_active, c, B,
+                                                                                   per_slot, wave),
+                    lambda c: self._root_child_stats(tree, B, c), decide)
             slot_visits, slot_q = self._root_child_stats(tree, B, self._slot_idx.expand(B, -1))
             visited = (slot_visits > 0) & valid_slot
             max_n = slot_visits.float().max(dim=1, keepdim=True).values

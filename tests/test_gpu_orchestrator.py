@@ -364,19 +364,30 @@ def test_reset_trees_equals_full_refill(M):
     assert tree_equal({k: _np(v) for k, v in expect.items()}, {k: _np(v) for k, v in tree.items()}) == []
 
 
-@pytest.mark.parametrize("mask,max_ply,wave_parallel", [(0, 60, True), (7, 90, True), (0, 40, False)])
-def test_graph_waves_equal_eager(mask, max_ply, wave_parallel):
-    """Simulation waves replayed from captured HIP graphs against the same
+@pytest.mark.parametrize("mask,max_ply,wave_parallel,mode", [(0, 60, True, "waves"), (7, 90, True, "waves"),
+                                                             (0, 40, False, "waves"), (0, 60, True, "ply"),
+                                                             (7, 90, False, "ply")])
+def test_graph_waves_equal_eager(mask, max_ply, wave_parallel, mode):
+    """Simulation waves replayed from captured HIP graphs -- one graph per wave
+    shape ("waves"), or the whole search phase of a ply, every wave of the four
+    rounds and the halving decisions, as one graph ("ply") -- against the same
     waves run eagerly: three plies (so each graph is replayed across rounds,
     plies and tree rebases, with eager work and host reads in between), every
-    ply's choice, policy and visits and the final trees bit-identical."""
+    ply's choice, policy and visits, the search counters and the final trees
+    bit-identical."""
     import torch
     from hive_neuralnet_amd import hive_gpu
     outs = []
     for graphs in (False, True):
         B = 16
         orch, _, tree = _setup(B, 64, 8192, mask, max_ply, 71, wave_parallel=wave_parallel)
-        orch.use_graphs = graphs
+        if not graphs:
+            orch.use_graphs, orch.use_ply_graphs = False, False
+        elif mode == "waves":
+            orch.use_graphs, orch.use_ply_graphs = True, False
+        else:
+            orch.use_graphs, orch.use_ply_graphs = None, True
+        orch.enable_counters()
         states, _ = hive_gpu.random_positions(B, mask, max_ply, 72)
         torch.manual_seed(73)
         np.random.seed(73)
@@ -387,14 +398,18 @@ def test_graph_waves_equal_eager(mask, max_ply, wave_parallel):
             rec.append((_np(r.chosen_slot), _np(r.policy), _np(r.slot_visits)))
             orch.apply_and_rebase(states, tree, r)
             active &= orch.ext.check_results_batch(states, B) == 0
+        rec.append(_np(orch._stats).copy())
         rec.append({k: _np(v).copy() for k, v in tree.items()})
         if graphs:
-            assert len(orch._graphs) >= 1
+            assert len(orch._graphs if mode == "waves" else orch._ply_graphs) >= 1
+        else:
+            assert not orch._graphs and not orch._ply_graphs
         outs.append(rec)
-    for a, b in zip(outs[0][:-1], outs[1][:-1]):
+    for a, b in zip(outs[0][:-2], outs[1][:-2]):
         for x, y in zip(a, b):
             assert np.array_equal(x.view(np.uint32) if x.dtype == np.float32 else x,
                                   y.view(np.uint32) if y.dtype == np.float32 else y)
+    assert np.array_equal(outs[0][-2], outs[1][-2])
     assert tree_equal(outs[0][-1], outs[1][-1]) == []
 
 
