@@ -269,6 +269,50 @@ __global__ void k_random_play_step(uint8_t* __restrict__ states, const uint8_t* 
     if (plies_done) plies_done[i] += 1;
 }
 
+// Seeded random play for all its plies in one launch (k_random_play_step
+// with its per-ply k_legal<moves>, fused): a workgroup keeps its two games
+// (lane groups of 32) from their first ply to their last, the grid striding
+// over the games (sized to the workgroups the device holds at once).  Per ply
+// a group lists its game's legal moves into the game's row of `moves`
+// (scratch) and the count into LDS, and one lane applies the Philox choice to
+// the game's state row in place; the rows stay in L2 between plies and the
+// workgroup moves on when both games have stopped (ply >= target or a
+// result).  Same choices, same rows and counts as the per-ply launches.
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(6))) void k_random_play(
+    uint8_t* __restrict__ states, uint8_t* __restrict__ moves, int64_t B, int max_ply, int lockstep, uint32_t seed,
+    int32_t* __restrict__ plies_done) {
+    __shared__ Pos PS[kPosPerWave];
+    __shared__ int32_t NS[kPosPerWave];
+    const int grp = threadIdx.x >> 5, l = threadIdx.x & 31;
+    for (int64_t first = (int64_t)blockIdx.x * kPosPerWave; first < B; first += (int64_t)gridDim.x * kPosPerWave) {
+        const int64_t i = first + grp;
+        const bool live = i < B;
+        const int64_t g = live ? i : B - 1;  // a group past the end mirrors the last game and writes nothing
+        uint8_t* row = states + g * kStateBytes;
+        const int target =
+            lockstep ? max_ply : (int)(philox_word0(seed, 0, (uint32_t)g, 0) % (uint32_t)(max_ply + 1));
+        uint8_t* mrow = moves + g * (kMaxLegal * 6);
+        int done = 0;
+        for (int ply = 0; ply < max_ply; ply++) {
+            const bool act = live && ply < target && row[OFF_RESULT] == 0;
+            if (__ballot(act) == 0ull) break;  // both games of the workgroup have stopped
+            run_legal<true, false, false>(PS[grp], row, threadIdx.x, act ? mrow : nullptr, &NS[grp], nullptr,
+                                          nullptr);
+            __syncthreads();  // the list and its count before they are read
+            if (act && l == 0) {
+                const uint32_t u = philox_word0(seed, 0, (uint32_t)g, (uint32_t)(ply + 1));
+                const int pick = (int)(((uint64_t)u * (uint64_t)NS[grp]) >> 32);
+                const uint8_t* m = mrow + pick * 6;
+                RowView v{row};
+                v.apply(m[0], m[1], m[2] | (m[3] << 8), m[4] | (m[5] << 8));
+                done++;
+            }
+            __syncthreads();  // the row after the move before the next ply reads it
+        }
+        if (live && l == 0 && plies_done) plies_done[g] += done;
+    }
+}
+
 // legal_mask_kernel (state_encoder.cuh:908-976): the [B][85834] float mask is
 // zero-filled (16-byte stores over the whole buffer), then 1.0 is scattered
 // at each legal slot's action index (k_legal's fused action output).
@@ -514,6 +558,22 @@ int hg_fnn_successor_features(const uint8_t* states, const uint8_t* legal_moves,
 int hg_queen_escape_flags(const uint8_t* states, int64_t B, uint8_t* flags, void* stream) {
     if (B <= 0) return 0;
     hipLaunchKernelGGL(k_queen_escape, dim3((unsigned)grid_for(B, kPosPerWave)), dim3(64), 0, (hipStream_t)stream, states, B, flags);
+    return finish();
+}
+
+int hg_random_play(uint8_t* states, uint8_t* moves, int64_t B, int max_ply, int lockstep, uint32_t seed,
+                   int32_t* plies_done, void* stream) {
+    if (B <= 0 || max_ply <= 0) return 0;
+    if (!moves || B > INT32_MAX) return (int)hipErrorInvalidValue;
+    int dev = 0, cus = 0, per_cu = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e == hipSuccess) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_random_play, 64, 0);
+    if (e != hipSuccess) return (int)e;
+    const int64_t pairs = (B + kPosPerWave - 1) / kPosPerWave;
+    const int64_t resident = (int64_t)(cus > 0 ? cus : 1) * (per_cu > 0 ? per_cu : 1);
+    hipLaunchKernelGGL(k_random_play, dim3((unsigned)(pairs < resident ? pairs : resident)), dim3(64), 0,
+                       (hipStream_t)stream, states, moves, B, max_ply, lockstep, seed, plies_done);
     return finish();
 }
 

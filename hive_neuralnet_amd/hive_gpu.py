@@ -75,6 +75,7 @@ _SIGS = {
                          _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, ctypes.c_float,
                          _c_void_p, _c_void_p, _c_void_p, ctypes.c_float, _c_void_p, _c_void_p, _c_void_p,
                          _c_void_p, _c_void_p],
+    "hg_random_play": [_c_void_p, _c_void_p, _c_i64, _c_int, _c_int, ctypes.c_uint32, _c_void_p, _c_void_p],
     "hg_random_play_step": [_c_void_p, _c_void_p, _c_void_p, _c_i64, _c_int, _c_int, _c_int, ctypes.c_uint32,
                             _c_void_p, _c_void_p],
     "hg_mcts_select_root_slots": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, ctypes.c_float, _c_i64,
@@ -678,17 +679,31 @@ class WavePlan:
         return self.leaf_idx[:T], self.leaf_states[:T], self.num_legal[:T], self.vl_lens[:T]
 
 
-def random_positions(batch_size: int, expansion_mask: int, max_ply: int, seed: int, lockstep: bool = False):
+def random_positions(batch_size: int, expansion_mask: int, max_ply: int, seed: int, lockstep: bool = False,
+                     per_ply: bool | None = None):
     """Seeded random-play positions on the GPU (the benchmark configurations'
     generator): position i plays Philox-chosen legal moves from the empty
     board for a Philox-drawn number of plies in [0, max_ply] (or exactly
-    max_ply in lockstep mode), stopping early at a result.
+    max_ply in lockstep mode), stopping early at a result.  per_ply False:
+    one launch for all plies (hg_random_play, each workgroup keeping its two
+    games to their last ply); True: one legal-list launch and one move launch
+    per ply (hg_random_play_step); the same result.  None: the single launch
+    in lockstep mode, where every game runs to the same ply, the per-ply
+    launches otherwise (games stopping at scattered plies keep the whole
+    device busy that way).
     Returns (states [B,3424] u8, plies_done [B] i32)."""
     ext = load_extension()
     B = int(batch_size)
     states = ext.create_initial_states(B, expansion_mask)
     plies = torch.zeros((B,), dtype=torch.int32, device="cuda")
     lib = ext._lib
+    if per_ply is None:
+        per_ply = not lockstep
+    if not per_ply:
+        moves = torch.empty((B, MAX_LEGAL_MOVES, SIZEOF_GPU_MOVE), dtype=torch.uint8, device="cuda")
+        _check(lib.hg_random_play(states.data_ptr(), moves.data_ptr(), B, int(max_ply), 1 if lockstep else 0,
+                                  int(seed) & 0xFFFFFFFF, plies.data_ptr(), _stream()), "random_play")
+        return states, plies
     for ply in range(int(max_ply)):
         moves, n = ext.generate_legal_moves_batch(states, B)
         _check(lib.hg_random_play_step(states.data_ptr(), moves.data_ptr(), n.data_ptr(), B, ply, int(max_ply),

@@ -224,6 +224,15 @@ int hg_queen_escape_flags(const uint8_t* states, int64_t B, uint8_t* flags, void
 int hg_random_play_step(uint8_t* states, const uint8_t* moves, const int32_t* num_legal, int64_t B, int ply,
                         int max_ply, int lockstep, uint32_t seed, int32_t* plies_done, void* stream);
 
+/* The plies 0 .. max_ply - 1 of hg_random_play_step (each after the legal
+ * lists of hg_generate_legal_moves) in one launch, every game's row held on
+ * chip from its first ply to its last: the same states and plies_done.
+ * moves: scratch of B * 256 * 6 bytes (the games' legal lists; its contents
+ * afterwards are unspecified).  No reference counterpart (the generator of
+ * the benchmark configurations, as hg_random_play_step). */
+int hg_random_play(uint8_t* states, uint8_t* moves, int64_t B, int max_ply, int lockstep, uint32_t seed,
+                   int32_t* plies_done, void* stream);
+
 /* ---------------------------------------------------------------- MCTS tree
  * The reference's structure-of-arrays tree (mcts_tree.cuh:31-45), one pool of
  * max_nodes slots per game, arrays [B, max_nodes] (move_bytes [B, max_nodes, 6],

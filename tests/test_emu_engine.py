@@ -141,6 +141,24 @@ def test_emulated_successor_rows_grid_edge(emu, oracle):
     assert np.array_equal(f.view(np.uint32), want.view(np.uint32))
 
 
+def test_emulated_successor_rows_whole_lists(emu, oracle):
+    """Blocked successor rows over every legal move of twelve expansion-piece
+    positions in list order (runs of one root across blocks, placements that
+    grow the hive by a row, moves that empty their origin, beetles that climb,
+    throws), against the oracle's successor features."""
+    g = load_golden("c3")
+    st = np.ascontiguousarray(g["states"][40:52])
+    mv, n, _, _ = oracle.batch_legal_features_actions(st)
+    roots = np.concatenate([np.full(int(k), i, np.int64) for i, k in enumerate(n)])
+    idx = np.concatenate([np.arange(int(k), dtype=np.int64) for k in n])
+    want = oracle.batch_successor_features(st, mv, roots, idx)
+    f = np.full((len(roots), 122), np.nan, np.float32)
+    mv = np.ascontiguousarray(mv)
+    emu.emu_successor_rows(_p(st), _p(mv), _p(roots), _p(idx), ctypes.c_int64(len(roots)),
+                           ctypes.c_int64(st.shape[0]), _p(f))
+    assert np.array_equal(f.view(np.uint32), want.view(np.uint32))
+
+
 @pytest.mark.parametrize("flags,cap", [((1, 1, 1), 0), ((0, 0, 1), 0), ((1, 1, 1), 3)])
 def test_emulated_root_tactical_probe(emu, flags, cap):
     """hive_probe.hpp's group programs, orchestrated as hive_probe.hip's

@@ -322,3 +322,15 @@ def test_mismatched_shapes_rejected(ext):
     assert torch.equal(out.view(-1, 122), want)
     with pytest.raises(ValueError, match="trailing shape"):
         ext.fnn_successor_features_batch(st, legal, a2r, mi, a2r.shape[0], out=out.view(-1, 61))
+
+
+@pytest.mark.parametrize("B,mask,P,lockstep", [(1, 0, 40, True), (777, 7, 90, True), (513, 0, 120, False),
+                                               (300, 7, 150, False)])
+def test_random_play_one_launch_equals_per_ply(B, mask, P, lockstep):
+    """hg_random_play (every ply in one launch, workgroups keeping their games)
+    against hg_random_play_step after each ply's legal lists: the same final
+    rows and ply counts, odd batches (a workgroup with one game) included."""
+    from hive_neuralnet_amd.hive_gpu import random_positions
+    a = random_positions(B, mask, P, 0x5EED + 9, lockstep=lockstep, per_ply=False)
+    b = random_positions(B, mask, P, 0x5EED + 9, lockstep=lockstep, per_ply=True)
+    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
