@@ -20,7 +20,13 @@ EMU = os.path.join(ROOT, "tests", "emu")
 
 @pytest.fixture(scope="module")
 def emu():
-    subprocess.run(["make", "-s", "-C", EMU], check=True)
+    import fcntl
+    # one build at a time when test processes run side by side (the library is
+    # renamed into place, so a loader never sees a partly written file)
+    with open(os.path.join(EMU, ".build.lock"), "w") as lock:
+        fcntl.flock(lock, fcntl.LOCK_EX)
+        subprocess.run(["make", "-s", "-C", EMU], check=True)
+        fcntl.flock(lock, fcntl.LOCK_UN)
     return ctypes.CDLL(os.path.join(EMU, "libwave_emu.so"))
 
 
