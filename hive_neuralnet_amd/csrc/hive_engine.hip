@@ -233,6 +233,217 @@ __global__ __launch_bounds__(64) void k_queen_escape(const uint8_t* __restrict__
     if (live && gl(threadIdx.x) == 0) out[pos] = esc ? 1 : 0;
 }
 
+// Surround count of the queen cell q (0xFFFF: unplaced, count 0; other
+// cells clamped to the board) on the board after a move: occupied on-grid
+// neighbours, the heights read from the LDS board with the move's effect
+// added (dfrom loses a piece, dto gains one; -1: none).
+HW_INL int surround_after(const Pos& P, int q, int dfrom, int dto) {
+    if (q == 0xFFFF) return 0;
+    q = q < 0 ? 0 : (q >= kCells ? kCells - 1 : q);
+    const uint32_t gm = grid6(q);
+    int k = 0;
+    for (int d = 0; d < 6; d++) {
+        if (!((gm >> d) & 1u)) continue;
+        const int nb = step(q, d);
+        k += P.hgt(nb) - (nb == dfrom ? 1 : 0) + (nb == dto ? 1 : 0) > 0 ? 1 : 0;
+    }
+    return k;
+}
+
+// The reserve-slot qualification of the Gumbel root candidates
+// (fnn_mcts_orchestrator.py:338-378): legal child k of root r qualifies when
+// its move raises the surround count of the opponent's queen (the child's
+// side to move) and, with immobile_only, that side then has no queen escape
+// (has_queen_escape_move, move_gen.cuh:771-821).  One lane group per root:
+// its lanes take the slots and work each move's effect on the heights and on
+// the queen's cell out from the root's board, as apply_move makes it; then
+// the qualifying children are built on the board one after another (the
+// root's board restored from registers) for the escape test.  Both groups of
+// a workgroup run as many children as the busier one (barriers); a group's
+// extra turns run a PASS and change nothing.  qual[r][k] = 1 or 0, all 256
+// slots written.
+//
+// With cand: the root's candidate row as well (fnn_mcts_orchestrator.py:
+// 411-444): `reserve` columns of qualifying slots by prior (-1 past the
+// qualifying count), then the other columns of the row from every slot that
+// is legal (and allowed) and not reserved, by prior, the rest (reserved and
+// illegal slots, ranked at -1e30) after them; every ranking stable (ties to
+// the lower slot), one group-wide argmax per column.
+__device__ __forceinline__ void group_argmax(float v, int idx, int lane, float& bv, int& bi) {
+#pragma unroll
+    for (int o = 1; o < kW; o <<= 1) {
+        const float ov = __shfl_xor(v, o, 64);
+        const int oi = __shfl_xor(idx, o, 64);
+        if (ov > v || (ov == v && oi < idx)) {
+            v = ov;
+            idx = oi;
+        }
+    }
+    bv = v;
+    bi = idx;
+}
+HW_INL void candidate_row(const uint32_t* keep, const uint32_t* valid, const float* __restrict__ pr, int k,
+                          int reserve, int lane, int32_t* __restrict__ out) {
+    const int l = gl(lane);
+    const uint32_t bit = 1u << l;
+    float p[kMaxLegal / kW];
+    uint32_t chosen[kMaxLegal / kW];
+    int nq = 0;
+#pragma unroll
+    for (int c = 0; c < kMaxLegal / kW; c++) {
+        p[c] = pr[l + kW * c];
+        chosen[c] = 0u;
+        nq += __popc(keep[c]);
+    }
+    const int rpg = nq < reserve ? nq : reserve;  // reserve columns that hold a slot
+    for (int pass = 0; pass < 2; pass++) {
+        const int cols = pass == 0 ? reserve : k - reserve;
+        uint32_t taken[kMaxLegal / kW];
+#pragma unroll
+        for (int c = 0; c < kMaxLegal / kW; c++) taken[c] = 0u;
+        for (int j = 0; j < cols; j++) {
+            float bv = -INFINITY;
+            int bi = 0x7fffffff;
+#pragma unroll
+            for (int c = 0; c < kMaxLegal / kW; c++) {
+                if (taken[c] & bit) continue;
+                const bool in = (pass == 0 ? keep[c] : (valid[c] & ~chosen[c])) & bit;
+                const float v = in ? p[c] : -1e30f;
+                const int idx = l + kW * c;
+                if (v > bv || (v == bv && idx < bi)) {
+                    bv = v;
+                    bi = idx;
+                }
+            }
+            group_argmax(bv, bi, lane, bv, bi);
+#pragma unroll
+            for (int c = 0; c < kMaxLegal / kW; c++)
+                if (c == bi / kW) {
+                    taken[c] |= 1u << (bi % kW);
+                    if (pass == 0 && j < rpg) chosen[c] |= 1u << (bi % kW);
+                }
+            if (l == 0 && out) out[pass == 0 ? j : reserve + j] = (pass == 0 && j >= rpg) ? -1 : bi;
+        }
+    }
+}
+
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(5))) void k_reserve_qualify(
+    const uint8_t* __restrict__ states, const uint8_t* __restrict__ legal, const int32_t* __restrict__ nlegal,
+    int64_t B, int immobile, uint8_t* __restrict__ qual, const uint8_t* __restrict__ allowed,
+    const float* __restrict__ priors, int k, int reserve, int32_t* __restrict__ cand) {
+    __shared__ Pos PS[kPosPerWave];
+    bool live;
+    const int64_t r = item_of(B, live);
+    Pos& P = PS[threadIdx.x >> 5];
+    const int lane = threadIdx.x, l = gl(lane);
+    const uint8_t* S = states + r * kStateBytes;
+    load_position(P, S, lane);
+    int n = nlegal[r];
+    n = n < 0 ? 0 : (n > kMaxLegal ? kMaxLegal : n);
+    __syncthreads();
+    BaseRegs R;
+    save_base(P, R, lane);
+    const int opp = (P.turn & 1) ^ 1;
+    const int q0 = P.queen[opp];
+    const int before = surround_after(P, q0, -1, -1);
+    const uint8_t* M = legal + r * (kMaxLegal * 6);
+    // keep: the qualifying slots (by the count); pending: those still to be
+    // tested for an escape; both one 32-slot word per chunk, group-uniform
+    uint32_t keep[kMaxLegal / kW], pending[kMaxLegal / kW];
+    int count = 0;
+#pragma unroll
+    for (int c = 0; c < kMaxLegal / kW; c++) {
+        const int k = l + kW * c;
+        bool q = false;
+        if (k < n) {
+            const uint8_t* m = M + 6 * k;
+            const int type = m[0], pt = m[1], from = m[2] | (m[3] << 8), to = m[4] | (m[5] << 8);
+            int dfrom = -1, dto = -1, qc = q0;
+            if (type == MV_PLACE) {
+                if (to < kCells && pt >= PT_Q && pt <= PT_P && P.hgt(to) < 5) dto = to;
+            } else if (type == MV_MOVE) {
+                if (from < kCells && to < kCells && P.hgt(from) > 0 && P.hgt(from) <= 5 && P.hgt(to) < 5) {
+                    dfrom = from;
+                    dto = to;
+                    const int b = P.tp(from);
+                    if ((b & 15) == PT_Q && ((b >> 4) & 1) == opp) qc = to;  // a thrown queen
+                }
+            }
+            q = surround_after(P, qc, dfrom, dto) > before;
+        }
+        keep[c] = grp_ballot(q, lane);
+        pending[c] = immobile ? keep[c] : 0u;
+        count += immobile ? __popc(keep[c]) : 0;
+    }
+    // the workgroup's number of turns: the busier group's
+    const int other = __shfl(count, (lane + kW) & 63, 64);
+    const int turns = count > other ? count : other;
+    for (int j = 0; j < turns; j++) {
+        int slot = -1;
+#pragma unroll
+        for (int c = 0; c < kMaxLegal / kW; c++)
+            if (slot < 0 && pending[c]) slot = kW * c + __ffs(pending[c]) - 1;
+        restore_base(P, R, lane);
+        __syncthreads();
+        if (l == 0) {
+            if (slot >= 0) {
+                const uint8_t* m = M + 6 * slot;
+                apply_on_board(P, S, m[0], m[1], m[2] | (m[3] << 8), m[4] | (m[5] << 8));
+            } else {
+                apply_on_board(P, S, MV_PASS, 0, 0, 0);  // a turn with nothing left to test
+            }
+        }
+        __syncthreads();
+        build_occ_list(P, lane);
+        __syncthreads();
+        build_cell_masks(P, lane);
+        articulation(P, lane);
+        __syncthreads();
+        const bool esc = queen_escape(P, lane);
+        if (slot >= 0) {
+#pragma unroll
+            for (int c = 0; c < kMaxLegal / kW; c++)
+                if (c == slot / kW) {
+                    pending[c] &= ~(1u << (slot % kW));
+                    if (esc) keep[c] &= ~(1u << (slot % kW));
+                }
+        }
+        __syncthreads();
+    }
+    if (live && qual) {
+        uint8_t* out = qual + r * kMaxLegal;
+#pragma unroll
+        for (int c = 0; c < kMaxLegal / kW; c++) out[l + kW * c] = (uint8_t)((keep[c] >> l) & 1u);
+    }
+    if (cand) {
+        uint32_t valid[kMaxLegal / kW];
+#pragma unroll
+        for (int c = 0; c < kMaxLegal / kW; c++) {
+            const int slot = l + kW * c;
+            valid[c] = grp_ballot(slot < n && (!allowed || allowed[r * kMaxLegal + slot] != 0), lane);
+        }
+        candidate_row(keep, valid, priors + r * kMaxLegal, k, reserve, lane, live ? cand + r * k : nullptr);
+    }
+}
+
+// candidate_row from given masks (qualifies, valid: [B][256] uint8), one
+// lane group per root.
+__global__ __launch_bounds__(64) void k_candidate_rows(const uint8_t* __restrict__ qual,
+                                                       const uint8_t* __restrict__ valid,
+                                                       const float* __restrict__ priors, int64_t B, int k,
+                                                       int reserve, int32_t* __restrict__ cand) {
+    bool live;
+    const int64_t r = item_of(B, live);
+    const int lane = threadIdx.x, l = gl(lane);
+    uint32_t keep[kMaxLegal / kW], ok[kMaxLegal / kW];
+#pragma unroll
+    for (int c = 0; c < kMaxLegal / kW; c++) {
+        keep[c] = grp_ballot(qual[r * kMaxLegal + l + kW * c] != 0, lane);
+        ok[c] = grp_ballot(valid[r * kMaxLegal + l + kW * c] != 0, lane);
+    }
+    candidate_row(keep, ok, priors + r * kMaxLegal, k, reserve, lane, live ? cand + r * k : nullptr);
+}
+
 // Philox4x32-10 (Salmon et al., SC'11), first output word.
 __device__ __forceinline__ uint32_t philox_word0(uint32_t k0, uint32_t k1, uint32_t c0, uint32_t c1) {
     uint32_t x0 = c0, x1 = c1, x2 = 0, x3 = 0;
@@ -552,6 +763,27 @@ int hg_fnn_successor_features(const uint8_t* states, const uint8_t* legal_moves,
     const int64_t pairs = (N + kSuccRows * kPosPerWave - 1) / (kSuccRows * kPosPerWave);
     hipLaunchKernelGGL(k_successor_features, dim3((unsigned)(pairs < kSuccGrid ? pairs : kSuccGrid)), dim3(64), 0,
                        (hipStream_t)stream, states, legal_moves, action_to_root, move_indices, N, num_roots, features);
+    return finish();
+}
+
+int hg_reserve_candidates(const uint8_t* states, const uint8_t* legal_moves, const int32_t* num_legal,
+                          const uint8_t* allowed, const float* priors, int64_t B, int k, int reserve,
+                          int immobile_only, uint8_t* qualifies, int32_t* candidates, void* stream) {
+    if (B <= 0) return 0;
+    if (candidates && (!priors || k < 1 || k > kMaxLegal || reserve < 0 || reserve > k))
+        return (int)hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_reserve_qualify, dim3((unsigned)grid_for(B, kPosPerWave)), dim3(64), 0, (hipStream_t)stream,
+                       states, legal_moves, num_legal, B, immobile_only, qualifies, allowed, priors, k, reserve,
+                       candidates);
+    return finish();
+}
+
+int hg_candidate_rows(const uint8_t* qualifies, const uint8_t* valid, const float* priors, int64_t B, int k,
+                      int reserve, int32_t* candidates, void* stream) {
+    if (B <= 0) return 0;
+    if (k < 1 || k > kMaxLegal || reserve < 0 || reserve > k) return (int)hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_candidate_rows, dim3((unsigned)grid_for(B, kPosPerWave)), dim3(64), 0, (hipStream_t)stream,
+                       qualifies, valid, priors, B, k, reserve, candidates);
     return finish();
 }
 

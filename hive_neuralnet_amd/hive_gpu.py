@@ -76,6 +76,9 @@ _SIGS = {
                          _c_void_p, _c_void_p, _c_void_p, ctypes.c_float, _c_void_p, _c_void_p, _c_void_p,
                          _c_void_p, _c_void_p],
     "hg_random_play": [_c_void_p, _c_void_p, _c_i64, _c_int, _c_int, ctypes.c_uint32, _c_void_p, _c_void_p],
+    "hg_reserve_candidates": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_i64, _c_int, _c_int, _c_int,
+                              _c_void_p, _c_void_p, _c_void_p],
+    "hg_candidate_rows": [_c_void_p, _c_void_p, _c_void_p, _c_i64, _c_int, _c_int, _c_void_p, _c_void_p],
     "hg_random_play_step": [_c_void_p, _c_void_p, _c_void_p, _c_i64, _c_int, _c_int, _c_int, ctypes.c_uint32,
                             _c_void_p, _c_void_p],
     "hg_mcts_select_root_slots": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, ctypes.c_float, _c_i64,
@@ -567,6 +570,41 @@ class HiveGpuExtension:
         _check(self._lib.hg_legal_mask(states.data_ptr(), B, moves.data_ptr(), n.data_ptr(), acts.data_ptr(),
                                        masks.data_ptr(), _stream()), "generate_legal_moves_and_mask_batch")
         return moves, n, masks
+
+    def reserve_candidates(self, states, legal_moves, num_legal, batch_size: int, immobile_only: bool = True,
+                           priors=None, k: int = 16, reserve: int = 6, allowed=None, want_qualifies: bool = True):
+        """Reserve-slot qualification and, with priors, the Gumbel root candidate
+        rows in one launch (hg_reserve_candidates; FNNMCTSOrchestrator.
+        _root_candidate_slots with reserve slots, fnn_mcts_orchestrator.py:338-444).
+        Returns (qualifies [B, 256] bool or None, candidates [B, k] int32 or None)."""
+        B = int(batch_size)
+        states = _state_rows(states, B)
+        legal_moves = _dev(legal_moves, "legal_moves", torch.uint8, (MAX_LEGAL_MOVES, SIZEOF_GPU_MOVE), B)
+        num_legal = _dev(num_legal, "num_legal", torch.int32, (), B)
+        qual = torch.empty((B, MAX_LEGAL_MOVES), dtype=torch.uint8, device="cuda") if want_qualifies else None
+        cand = None
+        if priors is not None:
+            priors = _dev(priors, "priors", torch.float32, (MAX_LEGAL_MOVES,), B)
+            cand = torch.empty((B, int(k)), dtype=torch.int32, device="cuda")
+        if allowed is not None:
+            allowed = _dev(allowed.to(torch.uint8).contiguous(), "allowed", torch.uint8, (MAX_LEGAL_MOVES,), B)
+        _check(self._lib.hg_reserve_candidates(
+            states.data_ptr(), legal_moves.data_ptr(), num_legal.data_ptr(),
+            allowed.data_ptr() if allowed is not None else None, priors.data_ptr() if priors is not None else None,
+            B, int(k), int(reserve), 1 if immobile_only else 0, qual.data_ptr() if qual is not None else None,
+            cand.data_ptr() if cand is not None else None, _stream()), "reserve_candidates")
+        return (qual.to(torch.bool) if qual is not None else None), cand
+
+    def candidate_rows(self, qualifies, valid, priors, k: int, reserve: int) -> torch.Tensor:
+        """The candidate rows of reserve_candidates from given [B, 256] masks (hg_candidate_rows)."""
+        B = int(priors.shape[0])
+        q = _dev(qualifies.to(torch.uint8).contiguous(), "qualifies", torch.uint8, (MAX_LEGAL_MOVES,), B)
+        v = _dev(valid.to(torch.uint8).contiguous(), "valid", torch.uint8, (MAX_LEGAL_MOVES,), B)
+        priors = _dev(priors, "priors", torch.float32, (MAX_LEGAL_MOVES,), B)
+        cand = torch.empty((B, int(k)), dtype=torch.int32, device="cuda")
+        _check(self._lib.hg_candidate_rows(q.data_ptr(), v.data_ptr(), priors.data_ptr(), B, int(k), int(reserve),
+                                           cand.data_ptr(), _stream()), "candidate_rows")
+        return cand
 
     def queen_escape_flags_batch(self, states: torch.Tensor, batch_size: int) -> torch.Tensor:
         B = int(batch_size)

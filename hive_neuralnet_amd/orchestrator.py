@@ -127,7 +127,6 @@ class FNNMCTSOrchestrator:
         self._max_nodes = int(self.config.max_tree_nodes)
         self._max_legal = int(self.ext.MAX_LEGAL_MOVES)
         self._slot_idx = torch.arange(self._max_legal, device="cuda", dtype=torch.int64).unsqueeze(0)
-        self._neighbor_cells = self._build_neighbor_cells()
         self.last_policy_temperature_stats: dict[str, float] = {}
         # optional device-side counters (no host sync): simulations run, legal
         # moves at their leaves, virtual-loss path lengths, successor rows
@@ -186,16 +185,6 @@ class FNNMCTSOrchestrator:
         self.counters = {k: self._stats[i] for i, k in enumerate(("sims", "leaf_legal", "vl_len", "rows"))}
 
     # ---- helpers -------------------------------------------------------
-    def _build_neighbor_cells(self) -> torch.Tensor:
-        cells = torch.arange(_NUM_CELLS)
-        row, col = cells // 23, cells % 23
-        out = torch.full((_NUM_CELLS, 6), -1, dtype=torch.int64)
-        for i, (dq, dr) in enumerate(((1, 0), (1, -1), (0, -1), (-1, 0), (-1, 1), (0, 1))):
-            nr, nc = row + dr, col + dq
-            ok = (nr >= 0) & (nr < 23) & (nc >= 0) & (nc < 23)
-            out[:, i] = torch.where(ok, nr * 23 + nc, torch.full_like(nr, -1))
-        return out.cuda()
-
     def _rows(self, n: int) -> torch.Tensor:
         return torch.arange(n, device="cuda", dtype=torch.int64).unsqueeze(1)
 
@@ -288,39 +277,16 @@ class FNNMCTSOrchestrator:
         return prior, root_values, child_q
 
     # ---- root candidates (:318-444) ------------------------------------
-    def _queen_surround_count(self, states, queen_color):
-        rows = torch.arange(states.shape[0], device="cuda", dtype=torch.int64)
-        qbase = (_OFF_QUEEN_CELL + 2 * queen_color).to(torch.int64)
-        qcell = states[rows, qbase].to(torch.int32) | (states[rows, qbase + 1].to(torch.int32) << 8)
-        valid_queen = qcell != 0xFFFF
-        neigh = self._neighbor_cells[qcell.clamp(0, _NUM_CELLS - 1).to(torch.int64)]
-        heights = states[:, _OFF_HEIGHT:_OFF_HEIGHT + _NUM_CELLS].to(torch.int16)
-        nh = heights.gather(1, neigh.clamp(min=0))
-        surround = ((neigh >= 0) & (nh > 0)).sum(dim=1).to(torch.int32)
-        return torch.where(valid_queen, surround, torch.zeros_like(surround)), qcell
-
     def _queen_surround_qualifying_mask(self, states, legal_moves, num_legal, total):
-        valid = self._slot_idx < num_legal.to(torch.int64).unsqueeze(1)
-        if total == 0 or not bool(valid.any().item()):
-            return torch.zeros((total, self._max_legal), dtype=torch.bool, device="cuda")
-        root_rows = self._rows(total).expand_as(valid)[valid]
-        move_indices = self._slot_idx.expand_as(valid)[valid]
-        n_total = int(root_rows.shape[0])
-        child = states[root_rows].clone()
-        self.ext.apply_moves_batch(child, legal_moves[root_rows, move_indices].contiguous(), n_total)
-        parent_turn = states[:, _OFF_TURN].to(torch.int32) | (states[:, _OFF_TURN + 1].to(torch.int32) << 8)
-        before, _ = self._queen_surround_count(states, ((parent_turn + 1) & 1).to(torch.int64))
-        child_turn = child[:, _OFF_TURN].to(torch.int32) | (child[:, _OFF_TURN + 1].to(torch.int32) << 8)
-        after, _ = self._queen_surround_count(child, (child_turn & 1).to(torch.int64))
-        qual_flat = after > before[root_rows]
-        if self.config.queen_surround_reserve_immobile_only and bool(qual_flat.any().item()):
-            qual_flat &= ~self.ext.queen_escape_flags_batch(child, n_total).to(torch.bool)
-        qual = torch.zeros((total, self._max_legal), dtype=torch.bool, device="cuda")
-        qual[valid] = qual_flat
+        """Legal slots whose move raises the surround count of the opponent's
+        queen (and, with queen_surround_reserve_immobile_only, leaves that side
+        no queen escape): [total, 256] bool (hg_reserve_candidates)."""
+        qual, _ = self.ext.reserve_candidates(states, legal_moves, num_legal, total,
+                                              self.config.queen_surround_reserve_immobile_only)
         return qual
 
     def _root_candidate_slots(self, states, legal_moves, num_legal, priors, legal_logits, total,
-                              allowed_slot_mask=None):
+                              allowed_slot_mask=None):  # :384-444
         max_legal = self._max_legal
         k = min(int(self.config.max_num_considered_actions), max_legal)
         valid = self._slot_idx < num_legal.to(torch.int64).unsqueeze(1)
@@ -331,32 +297,18 @@ class FNNMCTSOrchestrator:
             u = torch.rand(total, max_legal, device="cuda").clamp(1e-4, 1 - 1e-4)
             g = torch.where(valid, -torch.log(-torch.log(u)), torch.full_like(u, -1e30))
             return topk_stable(g + legal_logits, k)[1].to(torch.int32)
-        qual = self._queen_surround_qualifying_mask(states, legal_moves, num_legal, total)
-        return self._candidate_row(qual, valid, priors, k, reserve)
+        # qualification and the candidate row in one launch
+        _, cand = self.ext.reserve_candidates(states, legal_moves, num_legal, total,
+                                              self.config.queen_surround_reserve_immobile_only, priors=priors, k=k,
+                                              reserve=reserve, allowed=allowed_slot_mask, want_qualifies=False)
+        return cand
 
     def _candidate_row(self, qual, valid, priors, k, reserve):
-        """The root candidate row (fnn_mcts_orchestrator.py:411-444): `reserve`
-        columns of qualifying slots by prior (-1 padded), then `k` columns of the
-        other legal slots by prior, the concatenation cut to k columns.  The fill
-        ranks every slot (chosen and illegal ones at -1e30), so past the other
-        legal slots it continues with the reserve slots, lowest slot first."""
-        total, max_legal = priors.shape
-        reserve_scores = torch.where(qual, priors, torch.full_like(priors, -1e30))
-        reserve_per_game = qual.sum(dim=1).clamp(max=reserve)
-        _, reserve_order = topk_stable(reserve_scores, reserve)
-        reserve_valid = torch.arange(reserve, device="cuda").unsqueeze(0) < reserve_per_game.unsqueeze(1)
-        reserve_cand = torch.where(reserve_valid, reserve_order.to(torch.int32),
-                                   torch.full_like(reserve_order, -1, dtype=torch.int32))
-        chosen = torch.zeros((total, max_legal), dtype=torch.bool, device="cuda")
-        rows = self._rows(total).expand_as(reserve_valid)[reserve_valid]
-        chosen[rows, reserve_order[reserve_valid]] = True
-        fill_scores = torch.where(valid & ~chosen, priors, torch.full_like(priors, -1e30))
-        _, fill_order = topk_stable(fill_scores, k)
-        fill_keep = (k - reserve_per_game).clamp(min=0)
-        fill_valid = torch.arange(k, device="cuda").unsqueeze(0) < fill_keep.unsqueeze(1)
-        fill_cand = torch.where(fill_valid, fill_order.to(torch.int32), torch.full_like(fill_order, -1,
-                                                                                          dtype=torch.int32))
-        return torch.cat([reserve_cand, fill_cand], dim=1)[:, :k]
+        """The root candidate row (fnn_mcts_orchestrator.py:411-444) from a
+        qualifying mask (hg_candidate_rows): `reserve` columns of qualifying
+        slots by prior (-1 padded), then the other legal slots by prior, then
+        the rest (reserved and illegal slots, lowest slot first), cut to k."""
+        return self.ext.candidate_rows(qual, valid, priors, k, reserve)
 
     def _find_immediate_wins(self, states, legal_moves, num_legal, total):  # :446-493, vectorised
         winners = torch.full((total,), -1, dtype=torch.int64, device="cuda")

@@ -213,6 +213,32 @@ int hg_fnn_leaf_eval_lists(const uint8_t* leaf_states, const uint8_t* legal_move
 /* queen_escape_flags_batch -- game_logic.cu:1538-1554.  flags[B] uint8. */
 int hg_queen_escape_flags(const uint8_t* states, int64_t B, uint8_t* flags, void* stream);
 
+/* The Gumbel root candidates with their reserve slots, in one launch
+ * (FNNMCTSOrchestrator._root_candidate_slots with reserve > 0,
+ * hive_fnn/fnn_mcts_orchestrator.py:338-444, there a chain of torch ops over
+ * a copy of every child state).  Legal slot j of root r qualifies when its
+ * move raises the surround count of the opponent's queen (occupied on-grid
+ * neighbours of its cell, 0 while it is unplaced) and, when immobile_only !=
+ * 0, the child's side to move has no queen escape (queen_escape_flags_batch
+ * on the child).  qualifies (optional): [B][256] uint8, 1 / 0, all 256 slots
+ * written.  candidates (optional, then priors [B][256] f32 required):
+ * [B][k] int32, columns 0 .. reserve-1 the qualifying slots by prior (-1
+ * past their count, at most `reserve`), columns reserve .. k-1 the slots
+ * that are legal, allowed (allowed [B][256] uint8, or NULL: all) and not
+ * reserved, by prior, followed by the others (ranked at -1e30); every ranking
+ * stable (ties to the lower slot).  num_legal is clamped to [0, 256];
+ * 1 <= k <= 256, 0 <= reserve <= k. */
+int hg_reserve_candidates(const uint8_t* states, const uint8_t* legal_moves, const int32_t* num_legal,
+                          const uint8_t* allowed, const float* priors, int64_t B, int k, int reserve,
+                          int immobile_only, uint8_t* qualifies, int32_t* candidates, void* stream);
+
+/* The candidate rows of hg_reserve_candidates from given masks: qualifies and
+ * valid [B][256] uint8 (nonzero = set), priors [B][256] f32 -> candidates
+ * [B][k] int32 (FNNMCTSOrchestrator._root_candidate_slots from its qualifying
+ * mask, fnn_mcts_orchestrator.py:411-444). */
+int hg_candidate_rows(const uint8_t* qualifies, const uint8_t* valid, const float* priors, int64_t B, int k,
+                      int reserve, int32_t* candidates, void* stream);
+
 /* One ply of seeded random play (the position generator of the benchmark
  * configurations; no reference counterpart -- the reference's own pattern is
  * torch.rand x n_legal + apply_moves_batch, hive_gpu/endgame_generator.py:268-276).

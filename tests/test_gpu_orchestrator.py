@@ -678,3 +678,46 @@ def test_candidate_row_short_list():
     qual[0, c["qual"]] = True
     valid = orch._slot_idx < c["n"]
     assert orch._candidate_row(qual, valid, pri, 16, 6)[0].tolist() == c["row"]
+
+
+@pytest.mark.parametrize("mask,max_ply,immobile", [(0, 120, True), (7, 150, True), (7, 150, False)])
+def test_reserve_candidates_match_oracle(mask, max_ply, immobile):
+    """hg_reserve_candidates (qualification + candidate row in one launch)
+    against the numpy restatement (oracle/orchestrator.py: qualifying moves
+    by the C oracle's apply and queen escape, candidate_row) on 768 seeded
+    positions, the half whose opponent queen already has three or more
+    occupied neighbours first (where moves qualify); with and without an
+    allowed mask, and the candidate row from given masks (hg_candidate_rows)."""
+    import torch
+    from hive_neuralnet_amd import hive_gpu
+    from hive_neuralnet_amd.orchestrator import FNNMCTSConfig
+    from oracle.orchestrator import SearchPlyOracle, _surround, _turn, candidate_row
+    ext = hive_gpu.load_extension()
+    st, _ = hive_gpu.random_positions(4096, mask, max_ply, 0x5EED + 21)
+    stn = _np(st)
+    surround = np.array([_surround(s, (_turn(s) + 1) & 1) for s in stn])
+    pick = np.concatenate([np.nonzero(surround >= 3)[0][:384], np.nonzero(surround < 3)[0][:384]])
+    st = st[torch.from_numpy(pick).cuda()].contiguous()
+    B = st.shape[0]
+    legal, nl = ext.generate_legal_moves_batch(st, B)
+    rng = np.random.default_rng(5)
+    pri = rng.random((B, 256)).astype(np.float32)
+    pri[:, ::7] = pri[:, 3::7][:, : pri[:, ::7].shape[1]]  # ties between slots
+    allowed = rng.random((B, 256)) < 0.8
+    cfg = FNNMCTSConfig(queen_surround_reserve_immobile_only=immobile)
+    orc = SearchPlyOracle(cfg)
+    want_q = orc.qualifying(_np(st), _np(legal), _np(nl))
+    assert want_q.any(axis=1).sum() >= 50
+    n = _np(nl)
+    for al in (None, allowed):
+        valid = np.arange(256)[None, :] < n[:, None]
+        if al is not None:
+            valid &= al
+        want_c = candidate_row(want_q, valid, pri, 16, 6)
+        q, c = ext.reserve_candidates(st, legal, nl, B, immobile, priors=torch.from_numpy(pri).cuda(), k=16,
+                                      reserve=6, allowed=None if al is None else torch.from_numpy(al).cuda())
+        assert np.array_equal(_np(q), want_q)
+        assert np.array_equal(_np(c), want_c)
+        c2 = ext.candidate_rows(torch.from_numpy(want_q).cuda(), torch.from_numpy(valid).cuda(),
+                                torch.from_numpy(pri).cuda(), 16, 6)
+        assert np.array_equal(_np(c2), want_c)
