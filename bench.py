@@ -76,6 +76,9 @@ def parse_args():
                     help="C5 search phase of a ply from one HIP graph: auto = when every round runs on one range")
     ap.add_argument("--native-waves", choices=("on", "off"), default="on",
                     help="C5 simulation waves as one library call each (on) or through the step entry points")
+    ap.add_argument("--lib", default=None, metavar="PATH",
+                    help="load this build of the engine instead of the package's own (a build-time alternative "
+                         "made by `python -m hive_neuralnet_amd.build --define ... --out PATH`)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 256 MiB device-to-device copy 3 times (rocprof counter calibration)")
     return ap.parse_args()
@@ -601,6 +604,10 @@ def main():
         sys.exit(2)
     import torch
 
+    if args.lib:
+        from hive_neuralnet_amd import hive_gpu
+
+        hive_gpu.load_library(os.path.abspath(args.lib))
     if args.copy_calibration:
         a = torch.ones(64 * 1024 * 1024, dtype=torch.float32, device="cuda")
         b = torch.empty_like(a)
@@ -633,6 +640,8 @@ def main():
         "data": "synthetic (seeded Philox random-play positions generated on the GPU)",
         **result,
     }
+    if args.lib:
+        result["lib"] = args.lib
     if not args.no_c3:  # configs[2]: the expansion-piece variant, same kernel and bytes per position
         c3 = positions_leg(args, 65536, 7, 150)
         c3["metric"] = "positions/sec (move-gen+encode), expansion pieces"

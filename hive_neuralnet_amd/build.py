@@ -35,18 +35,32 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found: the HIP engine needs ROCm's hipcc to build")
 
 
-def build(verbose: bool = False) -> str:
-    tmp = LIB + ".tmp"
-    cmd = [hipcc(), *FLAGS, "-o", tmp, *SOURCES]
+def build(verbose: bool = False, defines: tuple = (), out: str = LIB) -> str:
+    """Compile the library to `out`.  `defines` ("NAME=VALUE") select
+    build-time alternatives of the engine, e.g. HW_ANT_GROUP=10 (the lane
+    group finishing ant searches after 10 expansions); the package's own
+    library is built without any."""
+    tmp = out + ".tmp"
+    cmd = [hipcc(), *FLAGS, *[f"-D{d}" for d in defines], "-o", tmp, *SOURCES]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         sys.stderr.write(res.stdout + res.stderr)
-        raise RuntimeError("hipcc failed building libhive_gpu.so")
+        raise RuntimeError(f"hipcc failed building {out}")
     if verbose:
         sys.stderr.write(res.stderr)
-    os.replace(tmp, LIB)
-    return LIB
+    os.replace(tmp, out)
+    return out
 
 
 if __name__ == "__main__":
-    print(build(verbose="-v" in sys.argv))
+    import argparse
+
+    ap = argparse.ArgumentParser(description="build the HIP engine library")
+    ap.add_argument("-v", "--verbose", action="store_true")
+    ap.add_argument("--define", action="append", default=[], metavar="NAME=VALUE",
+                    help="a build-time alternative of the engine (e.g. HW_ANT_GROUP=10)")
+    ap.add_argument("--out", default=LIB, help="output path (default: the package's own library)")
+    a = ap.parse_args()
+    if a.define and os.path.abspath(a.out) == LIB:
+        ap.error("a build with --define goes to its own --out path, not the package's library")
+    print(build(verbose=a.verbose, defines=tuple(a.define), out=os.path.abspath(a.out)))

@@ -141,11 +141,14 @@ HW_INL ListInfo generate_legal(Pos& P, int lane, const Gate& G = Gate()) {
         empties = grp_sum(__popc(ew), lane);
     }
     int ub = 0;  // this lane's piece or throw actor, counted toward ub_total
+    bool ant_job = false;  // an ant search left to the group (ant_searches)
+    int c = 0, ant_next = 0, ant_len = 0;
+    RingLift ant_rl{0, 0u, 0u};
     if (l < n_pieces && (off + cap > kPool || set0 + nsets > kSets)) {  // impossible piece counts
         P.piece_off[l] = 0;
         P.piece_cnt[l] = 0;
     } else if (l < n_pieces) {
-        int c = P.piece_cell[l];
+        c = P.piece_cell[l];
         int t = P.piece_type[l];
         uint16_t* out = P.u2.pool + off;
         uint32_t* s0 = P.u1.sets[set0 < kSets ? set0 : 0];
@@ -156,7 +159,16 @@ HW_INL ListInfo generate_legal(Pos& P, int lane, const Gate& G = Gate()) {
         if (run) {
             switch (t) {
                 case PT_Q: case PT_P: m = gen_step(P, c, out); break;
-                case PT_A: m = gen_ant<Gate::kTargeted>(P, c, out, kAntCap, s0, G.stop, &stopped); break;
+                case PT_A:
+                    if (kAntGroup) {
+                        m = gen_ant<Gate::kTargeted, true>(P, c, out, kAntCap, s0, G.stop, &stopped, kAntLaneSteps,
+                                                           &ant_next, &ant_rl);
+                        ant_job = !stopped && ant_next < m && m < kAntCap;
+                        ant_len = m;
+                    } else {
+                        m = gen_ant<Gate::kTargeted>(P, c, out, kAntCap, s0, G.stop, &stopped);
+                    }
+                    break;
                 case PT_G: m = gen_hopper(P, c, out); break;
                 case PT_S: m = gen_spider(P, c, out, s0); break;
                 case PT_B: m = gen_beetle(P, c, out); break;
@@ -172,6 +184,16 @@ HW_INL ListInfo generate_legal(Pos& P, int lane, const Gate& G = Gate()) {
         int j = l - kMaxPieces;
         P.throw_cnt[j] = (uint16_t)gen_throws(P, P.actor_cell[j], P.throw_from[j], P.throw_to[j], P.throw_pt[j]);
         ub = P.throw_cnt[j];
+    }
+    if (kAntGroup) {
+        int m = 0;
+        bool stopped = false;
+        ant_searches<Gate::kTargeted>(P, lane, ant_job, c, off, kAntCap, set0 < kSets ? set0 : 0, ant_len, ant_next,
+                                      ant_rl, G.stop, m, stopped);
+        if (ant_job) {
+            P.piece_cnt[l] = (uint8_t)m;
+            ub = stopped ? dest_bound(PT_A, empties) : m;
+        }
     }
     if (Gate::kTargeted) L.ub_total = n_place + grp_sum(ub, lane);
     __syncthreads();

@@ -48,6 +48,13 @@ constexpr int kMaxPieces = 16;
 // mosquito's union (<= 58 empty cells + 6 neighbours to climb on) plus the
 // sub-list being merged (<= 32) fits in 96.
 constexpr int kAntCap = 60;
+// Ant searches: one lane per ant (gen_ant).  Built with HW_ANT_GROUP = T > 0,
+// a lane makes at most T expansions and the lane group finishes the longer
+// searches together (ant_searches): bit-exact, but slower on the measured
+// workloads, so the default build keeps the lane searches.
+#ifndef HW_ANT_GROUP
+#define HW_ANT_GROUP 0
+#endif
 constexpr int kMosqRoom = 96;
 constexpr int kPool = 3 * kAntCap + kMosqRoom + 2 * 32 + 32 + 8 * 6;
 constexpr int kActors = 2;  // throw actors of one colour: its pillbug and its mosquito
@@ -755,13 +762,18 @@ __device__ __forceinline__ uint32_t exits_ring(const Pos& P, int x, const RingLi
 // Queue entries are cell | (bit of the direction back to the parent) <<
 // kDirShift: that exit leads to a visited cell and is skipped.  kStop: the
 // search ends as soon as cell `stop` is discovered (*stopped set), leaving a
-// prefix of the list that ends with it.
-template <bool kStop = false>
+// prefix of the list that ends with it.  kLimit: the search also ends after
+// `steps` expansions (the origin's own counts as one) with *next = the index
+// of the next entry to expand and *rlo = the origin's lifted exits, so that
+// ant_searches can take it from there; it is unfinished when *stopped is
+// clear and *next < the returned length < cap.
+template <bool kStop = false, bool kLimit = false>
 HW_INL int gen_ant(const Pos& P, int c, uint16_t* out, int cap, uint32_t* seen, int stop = -1,
-                   bool* stopped = nullptr) {
+                   bool* stopped = nullptr, int steps = 0, int* next = nullptr, RingLift* rlo = nullptr) {
     set_clear(seen);
     set_insert(seen, c);
     const RingLift rl = ring_lift(P, c);
+    if (kLimit) *rlo = rl;
     // queue by pointers: q = next free entry, h = next entry to expand
     uint16_t* q = out;
     const uint16_t* h = out;
@@ -800,11 +812,95 @@ HW_INL int gen_ant(const Pos& P, int c, uint16_t* out, int cap, uint32_t* seen, 
             }
         }
         if (h >= q || q >= end) break;
+        if (kLimit && --steps == 0) break;
         const uint32_t e = *h++;
         cur = (int)(e & kCellMask);
         back = e >> kDirShift;
     }
+    if (kLimit) *next = (int)(h - out);
     return (int)(q - out);
+}
+
+// Long ant searches finished by the whole lane group of their position.  A
+// search that gen_ant<kStop, true> left unfinished continues as gen_ant's
+// FIFO taken up to five queued entries at a time, lane 6k + d expanding
+// entry k of the batch in direction d (lanes 30, 31 idle).  A batch's
+// entries are already in the queue, so expanding them together appends what
+// expanding them one by one would, in the same order -- entry, then
+// direction -- provided a cell reached from two entries of the batch is
+// credited to the lower lane only: the lanes insert into the visited set
+// together, and when a cell had two claimants the lower lane is made the
+// winner whichever insert came first.  gen_ant's back-direction mask only
+// skips visited cells, so it is not needed; the entries appended here carry
+// no back bit.
+//
+// Lanes with `job` set hand in their search (origin c, list at
+// P.u2.pool[off] with room cap and `len` entries of which the first `next`
+// are expanded, visited set P.u1.sets[set], lifted exits rl) and get back the
+// final length in m (and, with kStop, whether it stopped at `stop`).  Every
+// lane of the group must call this.
+constexpr bool kAntGroup = HW_ANT_GROUP != 0;
+constexpr int kAntLaneSteps = HW_ANT_GROUP;  // expansions an ant lane makes before the group takes over
+template <bool kStop = false>
+HW_INL void ant_searches(Pos& P, int lane, bool job, int c, int off, int cap, int set, int len, int next,
+                         RingLift rl, int stop, int& m, bool& stopped) {
+    const int l = gl(lane);
+    const int k = l / 6, d = l - 6 * k;
+    const int ofs = (int)dir_byte(kOfsHi, kOfsLo, d) - 23;
+    const uint32_t below = (1u << l) - 1u;
+    uint32_t jobs = grp_ballot(job, lane);
+    while (jobs) {
+        const int j = __ffs(jobs) - 1;
+        jobs &= jobs - 1;
+        const int capj = grp_shfl(cap, j, lane);
+        const RingLift rj{grp_shfl(c, j, lane) - 23, grp_shfl(rl.lo, j, lane), grp_shfl(rl.hi, j, lane)};
+        uint16_t* out = P.u2.pool + grp_shfl(off, j, lane);
+        uint32_t* seen = P.u1.sets[grp_shfl(set, j, lane)];
+        int h = grp_shfl(next, j, lane), q = grp_shfl(len, j, lane);
+        bool hit = false;
+        while (h < q && q < capj && !hit) {
+            const int np = min(5, q - h);
+            bool cand = false;
+            int dest = 0;
+            if (k < np) {
+                const int cur = (int)(out[h + k] & kCellMask);
+                if ((exits_ring(P, cur, rj) >> d) & 1u) {  // open exits lead to on-grid cells
+                    dest = cur + ofs;
+                    cand = !((seen[dest >> 5] >> (dest & 31)) & 1u);
+                }
+            }
+            hw_group_lockstep();  // every read of the set above precedes the inserts
+            bool won = cand && set_insert(seen, dest);
+            uint32_t lost = grp_ballot(cand && !won, lane);
+            while (lost) {  // a cell with two claimants in the batch: the lower lane takes it
+                const int dl = grp_shfl(dest, __ffs(lost) - 1, lane);
+                const uint32_t same = grp_ballot(cand && dest == dl, lane);
+                if (cand && dest == dl) won = l == __ffs(same) - 1;
+                lost &= ~same;
+            }
+            const uint32_t wm = grp_ballot(won, lane);
+            int nw = __popc(wm);
+            const int rank = __popc(wm & below);
+            if (kStop) {  // the list ends with `stop` once it is appended
+                const uint32_t sb = grp_ballot(won && dest == stop, lane);
+                if (sb) {
+                    const int rs = __popc(wm & ((sb & (0u - sb)) - 1u));
+                    if (q + rs < capj) {
+                        nw = rs + 1;
+                        hit = true;
+                    }
+                }
+            }
+            if (won && rank < nw && q + rank < capj) out[q + rank] = (uint16_t)dest;
+            h += np;
+            q = min(capj, q + nw);
+            hw_group_lockstep();  // the next batch reads the entries written here
+        }
+        if (l == j) {
+            m = q;
+            stopped = hit;
+        }
+    }
 }
 
 // gen_spider_moves :397-431 (first occurrence over d1,d2,d3; at most 32)

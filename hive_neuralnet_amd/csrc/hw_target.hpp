@@ -26,6 +26,16 @@ __device__ __forceinline__ int hw_opaque(int v) {
 }
 #endif
 
+// The lanes of a lane group are lanes of one wavefront: they run in lockstep
+// and the wavefront's LDS accesses complete in program order, so what one
+// lane wrote is seen by every lane's later instructions without a barrier.
+// The host emulator runs lanes as threads and synchronises the group here.
+#ifdef HW_HOST_EMU
+inline void hw_group_lockstep() { wave_emu::group_sync(); }
+#else
+__device__ __forceinline__ void hw_group_lockstep() {}
+#endif
+
 // true in every lane of the wavefront when p holds in any of its lanes
 #ifndef HW_HOST_EMU
 __device__ __forceinline__ bool hw_wave_any(bool p) { return __ballot(p) != 0; }

@@ -30,6 +30,12 @@ def emu():
     return ctypes.CDLL(os.path.join(EMU, "libwave_emu.so"))
 
 
+@pytest.fixture(scope="module")
+def emu_antgrp(emu):
+    """The emulator build whose lane groups finish the ant searches (HW_ANT_GROUP=1)."""
+    return ctypes.CDLL(os.path.join(EMU, "libwave_emu_antgrp.so"))
+
+
 def _p(a):
     return a.ctypes.data_as(ctypes.c_void_p)
 
@@ -49,6 +55,34 @@ def test_emulated_legal_features(emu, oracle, name):
     assert np.array_equal(f.view(np.uint32), g["features"][:B].view(np.uint32))
     _, _, _, oa = oracle.batch_legal_features_actions(st)
     assert np.array_equal(a, oa)
+
+
+@pytest.mark.parametrize("mask,max_ply,seed", [(0, 120, 71), (7, 150, 72)])
+def test_emulated_group_ant_searches(emu, emu_antgrp, oracle, mask, max_ply, seed):
+    """The build-time alternative whose lane group finishes each ant search
+    (a batch of queued entries expanded together, one lane per entry and
+    direction) against the oracle's legal lists, features and actions, on
+    random-play and golden positions."""
+    g = load_golden("c2" if mask == 0 else "c3")
+    st, _ = oracle.generate_positions(96, mask, max_ply, seed)
+    st = np.ascontiguousarray(np.concatenate([st, g["states"][:32]]))
+    B = len(st)
+    mv = np.zeros((B, 256, 6), np.uint8)
+    n = np.zeros(B, np.int32)
+    f = np.zeros((B, 122), np.float32)
+    a = np.zeros((B, 256), np.int32)
+    emu_antgrp.emu_legal(_p(st), ctypes.c_int64(B), _p(mv), _p(n), _p(f), _p(a))
+    om, on, of, oa = oracle.batch_legal_features_actions(st)
+    assert np.array_equal(n, on)
+    assert np.array_equal(mv, om)
+    assert np.array_equal(f.view(np.uint32), of.view(np.uint32))
+    assert np.array_equal(a, oa)
+    # ants: a search that ends at a target (the probes' gated lists) stops the same way
+    out0 = np.zeros((B, 5), np.int32)
+    out1 = np.zeros((B, 5), np.int32)
+    emu.emu_gated_win(_p(st), ctypes.c_int64(B), _p(out0))
+    emu_antgrp.emu_gated_win(_p(st), ctypes.c_int64(B), _p(out1))
+    assert np.array_equal(out0, out1)
 
 
 @pytest.mark.parametrize("name", ["c2", "c3"])
