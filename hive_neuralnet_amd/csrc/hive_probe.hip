@@ -238,14 +238,16 @@ constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mu;
 int32_t* g_scratch[kMaxDevices] = {};
 
-// The current device's scratch address, looked up once per device.
-int scratch_of_current_device(int32_t** out) {
+// The current device's scratch address: looked up on the device's first use
+// and kept; `refresh` looks it up again (after a device reset the old address
+// is stale).
+int scratch_of_current_device(int32_t** out, bool refresh) {
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return (int)e;
     if (dev < 0 || dev >= kMaxDevices) return (int)hipErrorInvalidDevice;
     std::lock_guard<std::mutex> lock(g_scratch_mu);
-    if (g_scratch[dev] == nullptr) {
+    if (refresh || g_scratch[dev] == nullptr) {
         void* p = nullptr;
         e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
         if (e != hipSuccess) return (int)e;
@@ -261,7 +263,7 @@ extern "C" {
 
 int hg_probe_scratch_init(void) {
     int32_t* p = nullptr;
-    return scratch_of_current_device(&p);
+    return scratch_of_current_device(&p, true);
 }
 
 int64_t hg_root_tactical_probe_workspace(int64_t B) { return B <= 0 ? 0 : kCounters + kListInts * B * kMaxLegal; }
@@ -306,7 +308,7 @@ int hg_root_tactical_probe_noalloc(const uint8_t* states, const uint8_t* legal_m
     if (B <= 0) return 0;
     if (B > HG_PROBE_NOALLOC_MAX_ROOTS) return (int)hipErrorInvalidValue;
     int32_t* ws = nullptr;
-    const int err = scratch_of_current_device(&ws);
+    const int err = scratch_of_current_device(&ws, false);
     if (err != 0) return err;
     return hg_root_tactical_probe(states, legal_moves, num_legal, priors, B, enable_win_in_one,
                                   enable_check_opponent_wins, enable_win_in_two, winning, allowed, forced, ws, stream);

@@ -199,6 +199,10 @@ def _select_outputs(T: int, whole_rows: bool = False):
 
 _lib = None
 _lib_lock = threading.Lock()
+# root_tactical_probe_batch_noalloc: per device, an event recorded after the
+# last call (the next call's stream waits on it: the calls share the scratch)
+_noalloc_lock = threading.Lock()
+_noalloc_done: dict = {}
 
 
 def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
@@ -531,7 +535,10 @@ class HiveGpuExtension:
         library's per-GPU scratch array, for at most PROBE_NOALLOC_MAX_ROOTS
         roots.  `out` = (winning [B] int64, allowed [B, 256] uint8, forced [B]
         uint8) buffers to write; when None they are allocated here.  Calls
-        that overlap on one GPU share the scratch and race."""
+        on one GPU share the scratch: this method orders its own calls on a
+        device (each waits on an event recorded after the previous one, on
+        whichever stream), except under graph capture, where overlapping
+        replays are the caller's to serialise."""
         B = int(batch_size)
         if B > PROBE_NOALLOC_MAX_ROOTS:
             raise ValueError(f"root_tactical_probe_batch_noalloc: {B} roots, at most {PROBE_NOALLOC_MAX_ROOTS}")
@@ -548,10 +555,21 @@ class HiveGpuExtension:
         legal_moves = _dev(legal_moves, "legal_moves", torch.uint8, (MAX_LEGAL_MOVES, SIZEOF_GPU_MOVE), B)
         num_legal = _dev(num_legal, "num_legal", torch.int32, (), B)
         priors = _dev(priors, "priors", torch.float32, (MAX_LEGAL_MOVES,), B)
-        _check(self._lib.hg_root_tactical_probe_noalloc(
-            states.data_ptr(), legal_moves.data_ptr(), num_legal.data_ptr(), priors.data_ptr(), B,
-            int(bool(enable_win_in_one)), int(bool(enable_check_opponent_wins)), int(bool(enable_win_in_two)),
-            winning.data_ptr(), allowed.data_ptr(), forced.data_ptr(), _stream()), "root_tactical_probe_batch_noalloc")
+        capturing = torch.cuda.is_current_stream_capturing()
+        with _noalloc_lock:
+            dev = torch.cuda.current_device()
+            done = _noalloc_done.get(dev)
+            if done is not None and not capturing:
+                torch.cuda.current_stream().wait_event(done)
+            _check(self._lib.hg_root_tactical_probe_noalloc(
+                states.data_ptr(), legal_moves.data_ptr(), num_legal.data_ptr(), priors.data_ptr(), B,
+                int(bool(enable_win_in_one)), int(bool(enable_check_opponent_wins)), int(bool(enable_win_in_two)),
+                winning.data_ptr(), allowed.data_ptr(), forced.data_ptr(), _stream()),
+                "root_tactical_probe_batch_noalloc")
+            if not capturing:
+                if done is None:
+                    done = _noalloc_done[dev] = torch.cuda.Event()
+                done.record()
         return winning, allowed, forced
 
     def generate_legal_mask_batch(self, states: torch.Tensor, batch_size: int):

@@ -156,6 +156,11 @@ class FNNMCTSOrchestrator:
         # active games are copied into the graph's buffers before each replay.
         self.use_ply_graphs: bool | None = None
         self.max_ply_graphs = 4
+        # game ranges of a captured ply, each range's waves a branch of the
+        # graph (None = one).  At 512 games two branches measured no faster
+        # with the wave schedule and 11 % slower with one simulation per
+        # candidate per wave: the branches' kernels did not overlap.
+        self.ply_graph_parts: int | None = None
         self._ply_graphs: dict = {}
         # simulation waves of disjoint game ranges on their own streams, so that
         # one range's latency-bound tree walks overlap another's leaf evaluation
@@ -563,9 +568,16 @@ class FNNMCTSOrchestrator:
             return False
         if not (self._native_waves_ok() and self.native_halving and C <= 64):
             return False
-        single = all(self._game_parts_for(B, c, w) <= 1 or B < self._game_parts_for(B, c, w)
-                     for c, _, w in self._round_shapes(C))
-        return single
+        if self.ply_graph_parts is not None or self.use_ply_graphs:
+            return True
+        # by default only where every round's waves run on one game range
+        return all(self._game_parts_for(B, c, w) <= 1 or B < self._game_parts_for(B, c, w)
+                   for c, _, w in self._round_shapes(C))
+
+    def _ply_graph_parts(self, B) -> int:
+        """Game ranges of a captured ply (ply_graph_parts, default 1): each
+        range's waves are a branch of the graph of their own."""
+        return max(1, min(int(self.ply_graph_parts or 1), B))
 
     def _ply_graph(self, tree, root_states, game_active, cand, base, B):
         """_sequential_halving (fnn_mcts_orchestrator.py:650-731) replayed from a
@@ -578,9 +590,10 @@ class FNNMCTSOrchestrator:
         simulations)."""
         cfg = self.config
         C = int(cand.shape[1])
+        parts = self._ply_graph_parts(B)
         net_key = tuple(p.data_ptr() for p in self.net.parameters()) + tuple(self._head_biases or ())
         stats = self._stats if self.counters is not None else None
-        key = (tuple(v.data_ptr() for v in tree.values()), B, C, root_states.data_ptr(), net_key,
+        key = (tuple(v.data_ptr() for v in tree.values()), B, C, parts, root_states.data_ptr(), net_key,
                stats.data_ptr() if stats is not None else None, cfg.num_simulations, bool(cfg.wave_parallel),
                float(cfg.c_puct), bool(cfg.deterministic_non_root), float(cfg.non_root_sigma),
                float(cfg.virtual_q_penalty), float(cfg.c_visit), float(cfg.c_scale), int(cfg.root_q_min_visits))
@@ -589,21 +602,43 @@ class FNNMCTSOrchestrator:
             if len(self._ply_graphs) >= self.max_ply_graphs:  # oldest first
                 self._ply_graphs.pop(next(iter(self._ply_graphs)))
             static = {"cand": cand.clone(), "base": base.clone(), "active": game_active.clone()}
-            cap = max(min(w, per) * c * B for c, per, w in self._round_shapes(C))
-            plan = self.ext.prepare_wave_root_slots(*self._tree_args(tree), tree["child_init_q"], B, self._max_nodes,
-                                                    self.net, self._head_biases, capacity=cap)
+            # one buffer set per game range; the ranges' waves are branches of the
+            # graph (forked from the capture stream per round, joined before the
+            # round's halving decision, which reads every game)
+            bounds = [(B * p) // parts for p in range(parts + 1)]
+            ranges = []
+            for p in range(parts):
+                lo, hi = bounds[p], bounds[p + 1]
+                tv = {k: v[lo:hi] for k, v in tree.items()}
+                cap = max(min(w, per) * c * (hi - lo) for c, per, w in self._round_shapes(C))
+                plan = self.ext.prepare_wave_root_slots(*self._tree_args(tv), tv["child_init_q"], hi - lo,
+                                                        self._max_nodes, self.net, self._head_biases, capacity=cap)
+                ranges.append((lo, hi, plan, root_states[lo:hi], static["active"][lo:hi], tv["root_node"]))
+            side = _range_streams(parts)
             hg_tree = self._packed_tree(tree, B)
 
             def run_round(c, per_slot, wave):
                 W = max(1, int(wave))
                 q_penalty = float(cfg.virtual_q_penalty) if cfg.deterministic_non_root and W > 1 else 0.0
                 Cc = int(c.shape[1])
+                main = torch.cuda.current_stream()
+                if parts > 1:
+                    fork = torch.cuda.Event()
+                    fork.record(main)
+                    for p in range(1, parts):
+                        side[p].wait_event(fork)
                 sims = 0
                 for k in range(math.ceil(per_slot / W)):
                     w = min(W, per_slot - k * W)
-                    plan.run(root_states, static["active"], tree["root_node"], c, Cc, self._max_legal, cfg.c_puct, w,
-                             cfg.deterministic_non_root, cfg.non_root_sigma, q_penalty, stats=stats)
+                    for p, (lo, hi, plan, rs, act, rn) in enumerate(ranges):
+                        with torch.cuda.stream(main if p == 0 else side[p]):
+                            plan.run(rs, act, rn, c[lo:hi], Cc, self._max_legal, cfg.c_puct, w,
+                                     cfg.deterministic_non_root, cfg.non_root_sigma, q_penalty, stats=stats)
                     sims += w * Cc * B
+                for p in range(1, parts):
+                    join = torch.cuda.Event()
+                    join.record(side[p])
+                    main.wait_event(join)
                 return sims
 
             def decide(c, final):
@@ -613,7 +648,7 @@ class FNNMCTSOrchestrator:
             graph = torch.cuda.CUDAGraph()
             with torch.cuda.graph(graph):
                 chosen, sims = self._sequential_halving(static["cand"], static["base"], run_round, None, decide)
-            entry = (graph, static, chosen, sims, plan, hg_tree)
+            entry = (graph, static, chosen, sims, ranges, hg_tree)
             self._ply_graphs[key] = entry
             # capture records the launches without running them: the replay below runs this ply
         graph, static, chosen, sims = entry[:4]

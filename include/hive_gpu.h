@@ -166,8 +166,12 @@ int hg_root_tactical_probe(const uint8_t* states, const uint8_t* legal_moves, co
  * (25.2 MB); B above that returns hipErrorInvalidValue and launches nothing.
  * Every call on one GPU shares that GPU's array: calls that overlap on one
  * GPU (other streams, other threads) race and must be serialised by the
- * caller.  Outputs as hg_root_tactical_probe.  hg_probe_scratch_init looks up
- * the current device's array once (the first call on a device does it too). */
+ * caller (the Python binding orders its own calls on one GPU by an event,
+ * outside graph capture).  Outputs as hg_root_tactical_probe.
+ * hg_probe_scratch_init looks up the current device's array address (the
+ * first call on a device does it too) and keeps it for the process; after a
+ * hipDeviceReset that address is stale: call hg_probe_scratch_init again on
+ * that device, with it current, before the next hg_root_tactical_probe_noalloc. */
 #define HG_PROBE_NOALLOC_MAX_ROOTS 4096
 int hg_probe_scratch_init(void);
 int hg_root_tactical_probe_noalloc(const uint8_t* states, const uint8_t* legal_moves, const int32_t* num_legal,

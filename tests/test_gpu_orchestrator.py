@@ -366,15 +366,17 @@ def test_reset_trees_equals_full_refill(M):
 
 @pytest.mark.parametrize("mask,max_ply,wave_parallel,mode", [(0, 60, True, "waves"), (7, 90, True, "waves"),
                                                              (0, 40, False, "waves"), (0, 60, True, "ply"),
-                                                             (7, 90, False, "ply")])
+                                                             (7, 90, False, "ply"), (0, 60, True, "ply2"),
+                                                             (7, 90, False, "ply3")])
 def test_graph_waves_equal_eager(mask, max_ply, wave_parallel, mode):
     """Simulation waves replayed from captured HIP graphs -- one graph per wave
     shape ("waves"), or the whole search phase of a ply, every wave of the four
-    rounds and the halving decisions, as one graph ("ply") -- against the same
-    waves run eagerly: three plies (so each graph is replayed across rounds,
-    plies and tree rebases, with eager work and host reads in between), every
-    ply's choice, policy and visits, the search counters and the final trees
-    bit-identical."""
+    rounds and the halving decisions, as one graph ("ply"; "ply2" / "ply3":
+    the games in two / three ranges whose waves are parallel branches of the
+    graph) -- against the same waves run eagerly: three plies (so each graph
+    is replayed across rounds, plies and tree rebases, with eager work and
+    host reads in between), every ply's choice, policy and visits, the search
+    counters and the final trees bit-identical."""
     import torch
     from hive_neuralnet_amd import hive_gpu
     outs = []
@@ -387,6 +389,7 @@ def test_graph_waves_equal_eager(mask, max_ply, wave_parallel, mode):
             orch.use_graphs, orch.use_ply_graphs = True, False
         else:
             orch.use_graphs, orch.use_ply_graphs = None, True
+            orch.ply_graph_parts = {"ply": 1, "ply2": 2, "ply3": 3}[mode]
         orch.enable_counters()
         states, _ = hive_gpu.random_positions(B, mask, max_ply, 72)
         torch.manual_seed(73)

@@ -71,3 +71,26 @@ def test_noalloc_probe_size_limit():
     for a, b in zip(ext.root_tactical_probe_batch(states, legal, nl, pr, 64),
                     ext.root_tactical_probe_batch_noalloc(states, legal, nl, pr, 64)):
         assert torch.equal(a, b)
+
+
+def test_noalloc_binding_orders_calls_across_streams():
+    """Two binding calls on two streams, enqueued back to back: the second
+    waits for the first (they share the scratch), so both equal the
+    workspace probe; hg_probe_scratch_init (the address looked up again, as
+    after a device reset) leaves later calls correct."""
+    from hive_neuralnet_amd import hive_gpu
+    ext = hive_gpu.load_extension()
+    assert ext._lib.hg_probe_scratch_init() == 0
+    a = _probe_inputs(ext, 4096, 0x61)
+    b = _probe_inputs(ext, 2048, 0x62)
+    want_a = ext.root_tactical_probe_batch(*a, 4096)
+    want_b = ext.root_tactical_probe_batch(*b, 2048)
+    torch.cuda.synchronize()
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    with torch.cuda.stream(s1):
+        got_a = ext.root_tactical_probe_batch_noalloc(*a, 4096)
+    with torch.cuda.stream(s2):
+        got_b = ext.root_tactical_probe_batch_noalloc(*b, 2048)
+    torch.cuda.synchronize()
+    for w, g in zip(want_a + want_b, got_a + got_b):
+        assert torch.equal(w, g)
