@@ -226,15 +226,24 @@ __global__ __launch_bounds__(64 * kBlockWaves) void k_leaf_mlp(const float* __re
     // kBlockWaves * round)): a short batch spreads over all CUs, and a block
     // with no tile leaves before filling LDS
     if ((int64_t)blockIdx.x >= ntiles) return;
-    if (pk) {  // the packed layout: straight 16-byte copies
-        f4* dst = &L.w1[0][0];
+    if (pk) {  // the packed layout: straight 16-byte copies, every load issued before the first store
+        constexpr int kT = 64 * kBlockWaves, k12 = 48 * 64 / kT, k3 = 16 * 64 / kT;
+        static_assert(48 * 64 % kT == 0 && 16 * 64 % kT == 0 && 7 * kE / 4 <= kT, "whole copy rounds");
+        const int tid = threadIdx.x;
         const f4* src = &pk->w1[0][0];
-        for (int i = threadIdx.x; i < 48 * 64; i += blockDim.x) dst[i] = src[i];  // w1, w2
         const f4* s3 = &pk->w3[kRoot ? 0 : 1][0][0];
-        f4* d3 = &L.w3[0][0];
-        for (int i = threadIdx.x; i < 16 * 64; i += blockDim.x) d3[i] = s3[i];
-        if (threadIdx.x < 7 * kE / 4)
-            reinterpret_cast<f4*>(&L.vec[0][0])[threadIdx.x] = reinterpret_cast<const f4*>(&pk->vec[0][0])[threadIdx.x];
+        f4 c12[k12], c3[k3], cv = f4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int k = 0; k < k12; k++) c12[k] = src[tid + k * kT];  // w1, w2
+#pragma unroll
+        for (int k = 0; k < k3; k++) c3[k] = s3[tid + k * kT];
+        if (tid < 7 * kE / 4) cv = reinterpret_cast<const f4*>(&pk->vec[0][0])[tid];
+        f4* dst = &L.w1[0][0];
+#pragma unroll
+        for (int k = 0; k < k12; k++) dst[tid + k * kT] = c12[k];
+#pragma unroll
+        for (int k = 0; k < k3; k++) (&L.w3[0][0])[tid + k * kT] = c3[k];
+        if (tid < 7 * kE / 4) reinterpret_cast<f4*>(&L.vec[0][0])[tid] = cv;
     } else {  // permuted weights gathered into LDS (perm_index)
         int m, k;
         float* l1 = reinterpret_cast<float*>(&L.w1[0][0]);
