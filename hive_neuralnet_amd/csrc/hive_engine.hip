@@ -71,26 +71,39 @@ __device__ __forceinline__ int64_t item_of(int64_t n, bool& live) {
 // two count arrays used in turn: a call counts into the one that is zero
 // and clears the other (the previous call's, whose readers have finished
 // on the same stream), so no launch is spent clearing.
+// A workgroup takes kOrderPer positions (kOrderPer / 256 per thread, their
+// turns loaded together), so the bucket offsets cost one global atomic per
+// bucket per kOrderPer positions.
 constexpr int kOrderBuckets = 32, kOrderShift = 2;  // buckets of 4 turns, turn >= 124 in the last
+constexpr int kOrderPer = 1024, kOrderEach = kOrderPer / 256;
 __global__ __launch_bounds__(256) void k_order_buckets(const uint8_t* __restrict__ states, int64_t B,
                                                        int32_t* __restrict__ counts, int32_t* __restrict__ clear,
                                                        int32_t* __restrict__ lists) {
     __shared__ int cnt[kOrderBuckets], base[kOrderBuckets];
     if (threadIdx.x < kOrderBuckets) cnt[threadIdx.x] = 0;
     if (blockIdx.x == 0 && threadIdx.x < kOrderBuckets) clear[threadIdx.x] = 0;
+    int turn[kOrderEach];
+#pragma unroll
+    for (int k = 0; k < kOrderEach; k++) {
+        const int64_t i = (int64_t)blockIdx.x * kOrderPer + k * 256 + threadIdx.x;
+        turn[k] = i < B ? *reinterpret_cast<const uint16_t*>(states + i * kStateBytes + OFF_TURN) : -1;
+    }
     __syncthreads();
-    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    int b = -1, r = 0;
-    if (i < B) {
-        const int turn = *reinterpret_cast<const uint16_t*>(states + i * kStateBytes + OFF_TURN);
-        b = min(turn >> kOrderShift, kOrderBuckets - 1);
-        r = atomicAdd(&cnt[b], 1);
+    int b[kOrderEach], r[kOrderEach];
+#pragma unroll
+    for (int k = 0; k < kOrderEach; k++) {
+        b[k] = turn[k] < 0 ? -1 : min(turn[k] >> kOrderShift, kOrderBuckets - 1);
+        r[k] = b[k] >= 0 ? atomicAdd(&cnt[b[k]], 1) : 0;
     }
     __syncthreads();
     if (threadIdx.x < kOrderBuckets)
         base[threadIdx.x] = cnt[threadIdx.x] ? atomicAdd(&counts[threadIdx.x], cnt[threadIdx.x]) : 0;
     __syncthreads();
-    if (b >= 0 && base[b] + r < B) lists[(int64_t)b * B + base[b] + r] = (int32_t)i;
+#pragma unroll
+    for (int k = 0; k < kOrderEach; k++) {
+        const int64_t i = (int64_t)blockIdx.x * kOrderPer + k * 256 + threadIdx.x;
+        if (b[k] >= 0 && base[b[k]] + r[k] < B) lists[(int64_t)b[k] * B + base[b[k]] + r[k]] = (int32_t)i;
+    }
 }
 
 // item s of the ordered launch (buckets from the latest turns down): lane
@@ -695,8 +708,8 @@ int hg_legal_features_actions_ordered(const uint8_t* states, int64_t B, uint8_t*
     int32_t* counts = reinterpret_cast<int32_t*>(workspace) + parity * kOrderBuckets;
     int32_t* clear = reinterpret_cast<int32_t*>(workspace) + (parity ^ 1) * kOrderBuckets;
     int32_t* lists = reinterpret_cast<int32_t*>(workspace) + 2 * kOrderBuckets;
-    hipLaunchKernelGGL(k_order_buckets, dim3((unsigned)grid_for(B, 256)), dim3(256), 0, s, states, B, counts, clear,
-                       lists);
+    hipLaunchKernelGGL(k_order_buckets, dim3((unsigned)grid_for(B, kOrderPer)), dim3(256), 0, s, states, B, counts,
+                       clear, lists);
     hipLaunchKernelGGL((k_legal<true, true, true, true>), dim3((unsigned)grid_for(B, kPosPerWave)), dim3(64), 0, s,
                        states, B, moves, num_legal, features, actions, counts, lists);
     return finish();
