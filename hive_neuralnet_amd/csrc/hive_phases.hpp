@@ -725,12 +725,17 @@ HW_INL bool has_ladybug(const Pos& P, int c) {
     return false;
 }
 
-HW_INL bool piece_has_move(const Pos& P, int c, int t) {
+// `climb`: the piece is one high and either has a ground-slide exit (a
+// beetle's move down to the ground is that slide) or stands on a board with
+// no stack and has an occupied neighbour (climbing onto a one-high neighbour
+// is gated only by two flanks higher than one) -- then moving as a beetle
+// succeeds, so has_beetle need not run.
+HW_INL bool piece_has_move(const Pos& P, int c, int t, bool climb = false) {
     switch (t) {
         case PT_Q: case PT_P: case PT_A: return slide_mask(P, c, c) != 0;
         case PT_G: return has_hopper(P, c);
         case PT_S: return has_spider(P, c);
-        case PT_B: return has_beetle(P, c);
+        case PT_B: return climb || has_beetle(P, c);
         case PT_L: return has_ladybug(P, c);
         case PT_M: {
             if (P.hgt(c) > 1) return has_beetle(P, c);
@@ -743,9 +748,9 @@ HW_INL bool piece_has_move(const Pos& P, int c, int t) {
                 if (tt != PT_M) has |= 1u << tt;
             }
             if ((has & ((1u << PT_Q) | (1u << PT_P) | (1u << PT_A))) && slide_mask(P, c, c) != 0) return true;
+            if ((has & (1u << PT_B)) && (climb || has_beetle(P, c))) return true;
             if ((has & (1u << PT_G)) && has_hopper(P, c)) return true;
             if ((has & (1u << PT_S)) && has_spider(P, c)) return true;
-            if ((has & (1u << PT_B)) && has_beetle(P, c)) return true;
             if ((has & (1u << PT_L)) && has_ladybug(P, c)) return true;
             return false;
         }
@@ -807,15 +812,18 @@ HW_INL uint32_t compact_summary(Pos& P, int lane, int* n_place) {
     int npos = grp_sum(__popc(pw), lane);
     *n_place = npos;
     if (!queen_down || npos >= kMaxLegal) return 0;
-    // one lane per occupied cell: own movable pieces and throw actors
+    // one lane per occupied cell (rank l): own movable pieces and throw actors
     uint32_t bucket = 0;
-    if (l < P.n_occ) {
-        int c = P.occ_cells[l];
+    const bool occupied = l < P.n_occ;
+    const int c = occupied ? P.occ_cells[l] : 0;
+    const bool flat = grp_ballot(occupied && P.hgt(c) > 1, lane) == 0;  // no stack on the board
+    if (occupied) {
         int tb = P.tp(c);
         int t = tb & 15;
         if (((tb >> 4) & 1) == me) {
             bool stunned = P.stun != 0xFFFF && (int)P.stun == c;
-            if (!stunned && !pb_get(P.pin, c) && piece_has_move(P, c, t)) bucket |= 1u << ((t - 1) * 2 + me);
+            const bool climb = P.hgt(c) == 1 && (P.sm[c] != 0 || (flat && P.nbd[l] != 0));
+            if (!stunned && !pb_get(P.pin, c) && piece_has_move(P, c, t, climb)) bucket |= 1u << ((t - 1) * 2 + me);
             bool actor = (t == PT_P) || (t == PT_M && P.hgt(c) == 1 && touches_top_pillbug(P, c));
             if (actor) {
                 uint32_t oa = nbo(P, c);
