@@ -730,10 +730,14 @@ HW_INL bool has_ladybug(const Pos& P, int c) {
 // no stack and has an occupied neighbour (climbing onto a one-high neighbour
 // is gated only by two flanks higher than one) -- then moving as a beetle
 // succeeds, so has_beetle need not run.
-HW_INL bool piece_has_move(const Pos& P, int c, int t, bool climb = false) {
+// `jump`: no occupied cell on the grid's border and the piece has an occupied
+// neighbour -- then a jump over it lands inside the grid (the line's last
+// occupied cell lies in the hive, the landing one step beyond), so
+// has_hopper need not run.
+HW_INL bool piece_has_move(const Pos& P, int c, int t, bool climb = false, bool jump = false) {
     switch (t) {
         case PT_Q: case PT_P: case PT_A: return slide_mask(P, c, c) != 0;
-        case PT_G: return has_hopper(P, c);
+        case PT_G: return jump || has_hopper(P, c);
         case PT_S: return has_spider(P, c);
         case PT_B: return climb || has_beetle(P, c);
         case PT_L: return has_ladybug(P, c);
@@ -749,7 +753,7 @@ HW_INL bool piece_has_move(const Pos& P, int c, int t, bool climb = false) {
             }
             if ((has & ((1u << PT_Q) | (1u << PT_P) | (1u << PT_A))) && slide_mask(P, c, c) != 0) return true;
             if ((has & (1u << PT_B)) && (climb || has_beetle(P, c))) return true;
-            if ((has & (1u << PT_G)) && has_hopper(P, c)) return true;
+            if ((has & (1u << PT_G)) && (jump || has_hopper(P, c))) return true;
             if ((has & (1u << PT_S)) && has_spider(P, c)) return true;
             if ((has & (1u << PT_L)) && has_ladybug(P, c)) return true;
             return false;
@@ -817,13 +821,16 @@ HW_INL uint32_t compact_summary(Pos& P, int lane, int* n_place) {
     const bool occupied = l < P.n_occ;
     const int c = occupied ? P.occ_cells[l] : 0;
     const bool flat = grp_ballot(occupied && P.hgt(c) > 1, lane) == 0;  // no stack on the board
+    const bool inner = grp_ballot(l < 18 && (P.occ[l + 1] & kEdgeMask.m[l]) != 0u, lane) == 0;  // none on the border
     if (occupied) {
         int tb = P.tp(c);
         int t = tb & 15;
         if (((tb >> 4) & 1) == me) {
             bool stunned = P.stun != 0xFFFF && (int)P.stun == c;
             const bool climb = P.hgt(c) == 1 && (P.sm[c] != 0 || (flat && P.nbd[l] != 0));
-            if (!stunned && !pb_get(P.pin, c) && piece_has_move(P, c, t, climb)) bucket |= 1u << ((t - 1) * 2 + me);
+            const bool jump = inner && P.nbd[l] != 0;
+            if (!stunned && !pb_get(P.pin, c) && piece_has_move(P, c, t, climb, jump))
+                bucket |= 1u << ((t - 1) * 2 + me);
             bool actor = (t == PT_P) || (t == PT_M && P.hgt(c) == 1 && touches_top_pillbug(P, c));
             if (actor) {
                 uint32_t oa = nbo(P, c);

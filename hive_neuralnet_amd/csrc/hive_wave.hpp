@@ -1102,6 +1102,20 @@ constexpr GridMasks make_grid_masks() {
 }
 static __constant__ GridMasks kGridMask = make_grid_masks();
 
+// kEdgeMask.m[w]: cells of board word w on the grid's border (row or column 0 or 22)
+struct EdgeMask {
+    uint32_t m[18];
+};
+constexpr EdgeMask make_edge_mask() {
+    EdgeMask e{};
+    for (int c = 0; c < kCells; c++) {
+        const int r = c / kGrid, col = c % kGrid;
+        if (r == 0 || r == kGrid - 1 || col == 0 || col == kGrid - 1) e.m[c >> 5] |= 1u << (c & 31);
+    }
+    return e;
+}
+static __constant__ EdgeMask kEdgeMask = make_edge_mask();
+
 // cells of board word w with an on-grid neighbour that is set in pb
 HW_INL uint32_t nbr_union_word(const uint32_t* pb, int w) {
     uint32_t r = 0;
