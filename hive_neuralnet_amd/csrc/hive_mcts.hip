@@ -342,8 +342,71 @@ __device__ __forceinline__ KidRec shfl_kid(const KidRec& r, int src) {
                   __shfl(r.fc, src, 64), __shfl(r.nc, src, 64), (uint32_t)__shfl((int)r.mb01, src, 64),
                   (uint32_t)__shfl((int)r.mb2it, src, 64)};
 }
+// Level 3 of a simulation in select_slot_cached: the children of the level-2
+// node (k2-th child of the root child, record `win` as the simulation found
+// it) scored from an LDS copy when they are at most 64 and all inside the
+// pool.  The copies of the level-2 nodes the wave's simulations pass through
+// are kept in kC3 entries (tag = k2, replaced in turn), loaded on the first
+// visit and updated with the virtual loss as memory is (written through), so
+// a later simulation through the same node scores the same records without
+// a memory round trip.  No other wave touches this subtree during the
+// kernel, and the tree's structure does not change in it.  Then the descent
+// goes on through memory (descend_rec) from level 4.
+constexpr int kC3 = 4;
+HW_INL int descend_level3(const Tree& T, int64_t g0, int node2, int k2, const ChildRec& win, float c_puct,
+                          const SelectOut& O, int64_t sim, int& plen, int& vlen, int lane, KidRec (*c3)[64],
+                          int* tag3, int& next3) {
+    const int cfc = win.fc, cnc = win.nc;
+    const bool cacheable = !(cfc < 0 || win.it || cnc == 0) && cnc <= 64 && (int64_t)cfc + cnc <= T.M;
+    // where the descent through memory starts: level 3 below node2, or level 4
+    // below the cached level's winner (first_iter kDepth: no descent at all)
+    int node = node2, first = 2;
+    ChildRec r = win;
+    if (cacheable) {
+        int e = -1;
+#pragma unroll
+        for (int i = 0; i < kC3; i++)
+            if (tag3[i] == k2) e = i;
+        if (e < 0) {  // first visit: the children's records as memory holds them now
+            e = next3;
+            next3 = next3 == kC3 - 1 ? 0 : next3 + 1;
+            tag3[e] = k2;
+            if (lane < cnc) c3[e][lane] = pack_kid(load_rec(T, g0 + cfc + lane));
+        }
+        KidRec mine = c3[e][lane];
+        float bs = -INFINITY;
+        int bi = 0x7fffffff;
+        if (lane < cnc) {
+            const float sc = puct_kid(mine, win.vc + 1, c_puct);
+            if (sc > -1e30f) {
+                bs = sc;
+                bi = lane;
+            }
+        }
+        const int k3 = wave_argmax_first(bs, bi);
+        first = kDepth;
+        if (k3 >= 0) {
+            r = unpack_kid(shfl_kid(mine, k3));
+            node = cfc + k3;
+            if (lane == k3) {  // the copy takes the virtual loss enter_rec writes to memory
+                mine.vc = r.vc + 1;
+                mine.tv = r.tv + -1.0f;
+                c3[e][lane] = mine;
+            }
+            enter_rec(T, g0, node, r, false, 0.0f, O, sim, plen, vlen, lane);
+            first = 3;
+        }
+    }
+    return descend_rec(T, g0, node, r, r.vc + 1, first, c_puct, false, 0.0f, 0.0f, O, sim, plen, vlen, lane);
+}
+
 HW_INL void select_slot_cached(const Tree& T, int64_t g0, int node1, ChildRec r1, int64_t g, int64_t B, int c,
                                int C, int64_t rounds, float c_puct, const SelectOut& O, int lane) {
+    __shared__ KidRec c3[kC3][64];
+    int tag3[kC3];
+#pragma unroll
+    for (int i = 0; i < kC3; i++) tag3[i] = -1;
+    int next3 = 0;
     const int fc1 = r1.fc, nc1 = r1.nc;
     const bool grown = !(fc1 < 0 || r1.it || nc1 == 0) && !(nc1 <= 0 || nc1 > 1024);
     // the children that descend_rec would score: stop at the first one outside the pool
@@ -414,8 +477,7 @@ HW_INL void select_slot_cached(const Tree& T, int64_t g0, int node1, ChildRec r1
                     dst[2] = win.mb2;
                 }
                 plen = vlen = 2;
-                node = descend_rec(T, g0, node, win, win.vc + 1, 2, c_puct, false, 0.0f, 0.0f, O, sim, plen, vlen,
-                                   lane);
+                node = descend_level3(T, g0, node, k2, win, c_puct, O, sim, plen, vlen, lane, c3, tag3, next3);
             }
         }
         __syncthreads();  // the next simulation reads this one's statistics below level 2
