@@ -24,6 +24,8 @@ Two checks per ply:
 The schedule (2, 4, 8, 16) runs on the default two game ranges (two streams);
 one simulation per candidate per wave runs on one range.
 """
+import os
+
 import numpy as np
 import pytest
 
@@ -307,12 +309,12 @@ def _run(monkeypatch, wave_parallel, roots, plies=1, mask=0):
         got = _np(r.slot_visits).sum(1)
         want = np.where(wins & _np(r.has_actions), SIMS, sims)
         bad = np.nonzero(got != want)[0]
-        if bad.size:
-            import os
-            os.makedirs("gpurun_out", exist_ok=True)
-            np.savez("gpurun_out/c5_diag.npz", bad=bad, got=got, want=want, n=_np(r.num_legal), qual=qual.sum(1),
-                     wins=wins, has=_np(r.has_actions), sv=_np(r.slot_visits)[bad], states=_np(states)[bad],
-                     chosen=_np(r.chosen_slot))
+        diag = os.environ.get("HIVE_TEST_DIAG_DIR")  # where to leave the failing games' data, if anywhere
+        if bad.size and diag:
+            os.makedirs(diag, exist_ok=True)
+            np.savez(os.path.join(diag, "c5_diag.npz"), bad=bad, got=got, want=want, n=_np(r.num_legal),
+                     qual=qual.sum(1), wins=wins, has=_np(r.has_actions), sv=_np(r.slot_visits)[bad],
+                     states=_np(states)[bad], chosen=_np(r.chosen_slot))
         assert bad.size == 0, (f"{bad.size} games: " + "; ".join(
             f"g{g} n={_np(r.num_legal)[g]} reserve={qual.sum(1)[g]} win={wins[g]} got={got[g]} want={want[g]}"
             for g in bad[:12]))
