@@ -875,7 +875,9 @@ HW_INL bool queen_escape(const Pos& P, int lane) {
 // apply_move (hive_state.cuh:497-517) on the LDS board, run by one lane.
 // S is the row the LDS board was loaded from; the piece revealed when a
 // stack's top leaves is read from it (levels under the top are unchanged by
-// a single move).
+// a single move).  With kResult false the surrounded-queen test that sets
+// the result is left to ringed_result, run by the group once the
+// occupied-neighbour masks of the new board are built.
 HW_INL void pb_set(uint32_t* pb, int c) { pb[(c >> 5) + 1] |= 1u << (c & 31); }
 HW_INL void pb_clr(uint32_t* pb, int c) { pb[(c >> 5) + 1] &= ~(1u << (c & 31)); }
 
@@ -891,6 +893,7 @@ HW_INL bool queen_ringed(const Pos& P, int col) {
     return __popc(nbr_bits(P.occ, q)) == 6;
 }
 
+template <bool kResult = true>
 HW_INL void apply_on_board(Pos& P, const uint8_t* __restrict__ S, int type, int pt, int from, int to) {
     const int me = P.turn & 1;
     if (type == MV_PLACE) {
@@ -930,10 +933,29 @@ HW_INL void apply_on_board(Pos& P, const uint8_t* __restrict__ S, int type, int 
         P.stun = 0xFFFF;
     }
     P.turn = (uint16_t)(P.turn + 1);
+    if (!kResult) return;
     bool w = queen_ringed(P, 0), k = queen_ringed(P, 1);
     if (w && k) P.result = 3;
     else if (w) P.result = 2;
     else if (k) P.result = 1;
+}
+
+// The result apply_on_board<true> sets, from the masks build_cell_masks left:
+// a placed queen is surrounded when the occupied-neighbour mask of its cell
+// has all six on-grid directions (queen_ringed's test; off-grid directions
+// are never set).  Every occupied cell is ranked: a board of init/apply
+// holds at most 28 pieces, and a placed queen's cell stays occupied.  Lane 0
+// writes the result before the next barrier.
+HW_INL void ringed_result(Pos& P, int lane) {
+    const int l = gl(lane);
+    bool w = false, k = false;
+    if (l < P.n_occ && P.nbd[l] == 63u) {
+        const int c = P.occ_cells[l];
+        w = (P.qplaced & 1) && c == (int)P.queen[0];
+        k = (P.qplaced & 2) && c == (int)P.queen[1];
+    }
+    const bool W = grp_ballot(w, lane) != 0, K = grp_ballot(k, lane) != 0;
+    if (gl(lane) == 0 && (W || K)) P.result = (uint8_t)(W && K ? 3 : W ? 2 : 1);
 }
 
 // ---------------------------------------------------------------- programs
@@ -990,11 +1012,12 @@ HW_INL void run_extract(Pos& P, ListSets& X, const uint8_t* __restrict__ S, cons
 // the root's row S already on the board
 HW_INL void successor_on_board(Pos& P, const uint8_t* __restrict__ S, const uint8_t* __restrict__ m, int lane,
                                float* __restrict__ feat_row) {
-    if (gl(lane) == 0) apply_on_board(P, S, m[0], m[1], m[2] | (m[3] << 8), m[4] | (m[5] << 8));
+    if (gl(lane) == 0) apply_on_board<false>(P, S, m[0], m[1], m[2] | (m[3] << 8), m[4] | (m[5] << 8));
     __syncthreads();
     build_occ_list(P, lane);
     __syncthreads();
     build_cell_masks(P, lane);
+    ringed_result(P, lane);
     articulation(P, lane);
     __syncthreads();
     int n_place = 0;
