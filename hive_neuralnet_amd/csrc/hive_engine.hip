@@ -398,12 +398,12 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(5))) void k_
             if (slot < 0 && pending[c]) slot = kW * c + __ffs(pending[c]) - 1;
         restore_base(P, R, lane);
         __syncthreads();
-        if (l == 0) {
+        if (l == 0) {  // the escape test reads no result: the apply skips the ring test
             if (slot >= 0) {
                 const uint8_t* m = M + 6 * slot;
-                apply_on_board(P, S, m[0], m[1], m[2] | (m[3] << 8), m[4] | (m[5] << 8));
+                apply_on_board<false>(P, S, m[0], m[1], m[2] | (m[3] << 8), m[4] | (m[5] << 8));
             } else {
-                apply_on_board(P, S, MV_PASS, 0, 0, 0);  // a turn with nothing left to test
+                apply_on_board<false>(P, S, MV_PASS, 0, 0, 0);  // a turn with nothing left to test
             }
         }
         __syncthreads();

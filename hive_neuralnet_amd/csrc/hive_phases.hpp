@@ -1092,15 +1092,20 @@ struct RowView {
         if (col) { set(OFF_BTOP, c); clr(OFF_WTOP, c); }
         else { set(OFF_WTOP, c); clr(OFF_BTOP, c); }
     }
+    // occupancy word w (cells 32w .. 32w + 31) for w >= -1: word -1 is the
+    // four row bytes before the bitboard (heights), whose bits only ever land
+    // on off-grid directions and are masked off
+    __device__ uint32_t occ_word(int w) { return *reinterpret_cast<const uint32_t*>(s + OFF_OCC + 4 * w); }
+    // the queen's six on-grid neighbours all occupied, from one 64-bit window
+    // of the occupancy starting at cell q - 23 (three independent word reads)
     __device__ bool ringed(int col) {
         if (!((s[OFF_QPLACED] >> col) & 1)) return false;
         int q = u16(OFF_QUEEN + 2 * col);
         if (q >= kCells) return false;
-        uint32_t g = grid6(q);
-        int k = 0;
-        for (int d = 0; d < 6; d++)
-            if (((g >> d) & 1u) && get(OFF_OCC, step(q, d))) k++;
-        return k == 6;
+        const int lo = q - 23, w = lo >> 5, sh = lo & 31;
+        uint64_t win = ((uint64_t)occ_word(w) | ((uint64_t)occ_word(w + 1) << 32)) >> sh;
+        if (sh) win |= (uint64_t)occ_word(w + 2) << (64 - sh);
+        return (ring_bits(win) & grid6(q)) == 63u;
     }
     __device__ void apply(int type, int pt, int from, int to) {
         int me = u16(OFF_TURN) & 1;
