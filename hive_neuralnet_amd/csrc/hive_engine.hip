@@ -496,18 +496,21 @@ __global__ void k_random_play_step(uint8_t* __restrict__ states, const uint8_t* 
 // Seeded random play for all its plies in one launch (k_random_play_step
 // with its per-ply k_legal<moves>, fused): a workgroup keeps its two games
 // (lane groups of 32) from their first ply to their last, the grid striding
-// over the games (sized to the workgroups the device holds at once).  Per ply
-// a group lists its game's legal moves into the game's row of `moves`
-// (scratch) and the count into LDS, and one lane applies the Philox choice to
-// the game's state row in place; the rows stay in L2 between plies and the
-// workgroup moves on when both games have stopped (ply >= target or a
-// result).  Same choices, same rows and counts as the per-ply launches.
+// over the games (sized to the workgroups the device holds at once).  A
+// game's board is loaded into LDS once and stays there: per ply the group
+// rebuilds the derived tables (occupied list, slide exits, articulation
+// points), generates the legal list's tables, and one lane decodes the
+// Philox-chosen slot (list_slot; the list itself is never written out) and
+// applies it to the LDS board, writing the bytes that changed into the
+// game's state row (apply_mirrored).  The workgroup moves on when both
+// games have stopped (ply >= target or a result).  Same choices, same rows
+// and counts as the per-ply launches; `moves` is not used.
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(6))) void k_random_play(
-    uint8_t* __restrict__ states, uint8_t* __restrict__ moves, int64_t B, int max_ply, int lockstep, uint32_t seed,
+    uint8_t* __restrict__ states, int64_t B, int max_ply, int lockstep, uint32_t seed,
     int32_t* __restrict__ plies_done) {
     __shared__ Pos PS[kPosPerWave];
-    __shared__ int32_t NS[kPosPerWave];
     const int grp = threadIdx.x >> 5, l = threadIdx.x & 31;
+    Pos& P = PS[grp];
     for (int64_t first = (int64_t)blockIdx.x * kPosPerWave; first < B; first += (int64_t)gridDim.x * kPosPerWave) {
         const int64_t i = first + grp;
         const bool live = i < B;
@@ -515,25 +518,33 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(6))) void k_
         uint8_t* row = states + g * kStateBytes;
         const int target =
             lockstep ? max_ply : (int)(philox_word0(seed, 0, (uint32_t)g, 0) % (uint32_t)(max_ply + 1));
-        uint8_t* mrow = moves + g * (kMaxLegal * 6);
         int done = 0;
+        int result = row[OFF_RESULT];
+        bool loaded = false;  // uniform over the workgroup (one wave)
         for (int ply = 0; ply < max_ply; ply++) {
-            const bool act = live && ply < target && row[OFF_RESULT] == 0;
+            const bool act = live && ply < target && result == 0;
             if (__ballot(act) == 0ull) break;  // both games of the workgroup have stopped
-            run_legal<true, false, false>(PS[grp], row, threadIdx.x, act ? mrow : nullptr, &NS[grp], nullptr,
-                                          nullptr);
-            __syncthreads();  // the list and its count before they are read
+            if (!loaded) {
+                load_position(P, row, threadIdx.x);
+                __syncthreads();
+                loaded = true;
+            }
+            prepare_loaded(P, threadIdx.x);
+            const ListInfo L = generate_legal(P, threadIdx.x);
+            __syncthreads();  // the list's tables before one lane decodes a slot
             if (act && l == 0) {
                 const uint32_t u = philox_word0(seed, 0, (uint32_t)g, (uint32_t)(ply + 1));
-                const int pick = (int)(((uint64_t)u * (uint64_t)NS[grp]) >> 32);
-                const uint8_t* m = mrow + pick * 6;
-                RowView v{row};
-                v.apply(m[0], m[1], m[2] | (m[3] << 8), m[4] | (m[5] << 8));
+                const int pick = (int)(((uint64_t)u * (uint64_t)L.n) >> 32);
+                int tp = MV_PASS, from = 0, to = 0, seg;
+                if (L.total > 0) list_slot(P, L, pick, tp, from, to, seg);
+                apply_mirrored(P, row, tp & 0xFF, tp >> 8, from, to);
                 done++;
             }
-            __syncthreads();  // the row after the move before the next ply reads it
+            __syncthreads();  // the board after the move before the next ply reads it
+            result = P.result;
         }
         if (live && l == 0 && plies_done) plies_done[g] += done;
+        __syncthreads();  // the board's last reads before the next games load
     }
 }
 
@@ -818,7 +829,7 @@ int hg_random_play(uint8_t* states, uint8_t* moves, int64_t B, int max_ply, int 
     const int64_t pairs = (B + kPosPerWave - 1) / kPosPerWave;
     const int64_t resident = (int64_t)(cus > 0 ? cus : 1) * (per_cu > 0 ? per_cu : 1);
     hipLaunchKernelGGL(k_random_play, dim3((unsigned)(pairs < resident ? pairs : resident)), dim3(64), 0,
-                       (hipStream_t)stream, states, moves, B, max_ply, lockstep, seed, plies_done);
+                       (hipStream_t)stream, states, B, max_ply, lockstep, seed, plies_done);
     return finish();
 }
 

@@ -940,6 +940,45 @@ HW_INL void apply_on_board(Pos& P, const uint8_t* __restrict__ S, int type, int 
     else if (k) P.result = 1;
 }
 
+// apply_on_board for a board that is also kept as a state row: the LDS board
+// changes as apply_on_board changes it, and the row (global memory) receives
+// the bytes that changed -- the stack byte, height and bitboard words of the
+// cell the piece left and of the cell it reached, the metadata words -- so
+// that it holds what RowView::apply leaves (states of init/apply: stack bytes
+// fit the board's five top bits, heights stay below 8).  The board is read
+// from LDS; the row is read only for the piece revealed under a leaving top.
+// Run by one lane.
+HW_INL void apply_mirrored(Pos& P, uint8_t* __restrict__ row, int type, int pt, int from, int to) {
+    const int hf0 = from < kCells ? P.hgt(from) : 0;
+    const int ht0 = to < kCells ? P.hgt(to) : 0;
+    apply_on_board<true>(P, row, type, pt, from, to);
+    uint32_t* meta = reinterpret_cast<uint32_t*>(row + OFF_QUEEN);  // queens, hands, turn / flags
+    const uint32_t* hand32 = reinterpret_cast<const uint32_t*>(P.hand);
+    meta[0] = (uint32_t)P.queen[0] | ((uint32_t)P.queen[1] << 16);
+    meta[1] = hand32[0];
+    meta[2] = hand32[1];
+    meta[3] = hand32[2];
+    meta[4] = hand32[3];
+    meta[5] = (uint32_t)P.turn | ((uint32_t)P.qplaced << 16) | ((uint32_t)P.result << 24);
+    *reinterpret_cast<uint16_t*>(row + OFF_STUN) = P.stun;
+    auto words = [&](int c) {
+        const int w = c >> 5;
+        reinterpret_cast<uint32_t*>(row + OFF_OCC)[w] = P.occ[w + 1];
+        reinterpret_cast<uint32_t*>(row + OFF_WTOP)[w] = P.wt[w + 1];
+        reinterpret_cast<uint32_t*>(row + OFF_BTOP)[w] = P.bt[w + 1];
+    };
+    if (type == MV_MOVE && from < kCells && P.hgt(from) != hf0) {  // the piece left: hf0 - 1 high now
+        row[(hf0 - 1) * kCells + from] = 0;
+        row[OFF_HEIGHT + from] = (uint8_t)(hf0 - 1);
+        words(from);
+    }
+    if (to < kCells && P.hgt(to) != ht0) {  // a piece arrived: ht0 + 1 high now
+        row[ht0 * kCells + to] = (uint8_t)P.tp(to);
+        row[OFF_HEIGHT + to] = (uint8_t)(ht0 + 1);
+        words(to);
+    }
+}
+
 // The result apply_on_board<true> sets, from the masks build_cell_masks left:
 // a placed queen is surrounded when the occupied-neighbour mask of its cell
 // has all six on-grid directions (queen_ringed's test; off-grid directions
@@ -962,14 +1001,19 @@ HW_INL void ringed_result(Pos& P, int lane) {
 // Whole-position programs run by all 64 lanes of a wave; the kernels in
 // hive_engine.hip are thin launch wrappers around them.
 
-HW_INL void prepare(Pos& P, const uint8_t* __restrict__ S, int lane) {
-    load_position(P, S, lane);
-    __syncthreads();
+// board prepared for move generation (load_position done, moves applied)
+HW_INL void prepare_loaded(Pos& P, int lane) {
     build_occ_list(P, lane);
     __syncthreads();
     build_cell_masks(P, lane);
     articulation(P, lane);
     __syncthreads();
+}
+
+HW_INL void prepare(Pos& P, const uint8_t* __restrict__ S, int lane) {
+    load_position(P, S, lane);
+    __syncthreads();
+    prepare_loaded(P, lane);
 }
 
 template <bool WithMoves, bool WithFeat, bool WithAct>

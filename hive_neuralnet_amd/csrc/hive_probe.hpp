@@ -185,15 +185,6 @@ HW_INL bool immediate_win(Pos& P, int lane) {
     return hit;
 }
 
-// board prepared for move generation (load_position done, moves applied)
-HW_INL void prepare_loaded(Pos& P, int lane) {
-    build_occ_list(P, lane);
-    __syncthreads();
-    build_cell_masks(P, lane);
-    articulation(P, lane);
-    __syncthreads();
-}
-
 struct RootProbe {
     int win;        // immediate win found (slot), else -1
     int gate;       // kProbeScreen | kProbeWin2: the later stages that run

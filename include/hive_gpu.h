@@ -255,11 +255,12 @@ int hg_random_play_step(uint8_t* states, const uint8_t* moves, const int32_t* nu
                         int max_ply, int lockstep, uint32_t seed, int32_t* plies_done, void* stream);
 
 /* The plies 0 .. max_ply - 1 of hg_random_play_step (each after the legal
- * lists of hg_generate_legal_moves) in one launch, every game's row held on
- * chip from its first ply to its last: the same states and plies_done.
- * moves: scratch of B * 256 * 6 bytes (the games' legal lists; its contents
- * afterwards are unspecified).  No reference counterpart (the generator of
- * the benchmark configurations, as hg_random_play_step). */
+ * lists of hg_generate_legal_moves) in one launch, every game's board held in
+ * LDS from its first ply to its last (the state rows receive each ply's
+ * changed bytes): the same states and plies_done.  moves: scratch of
+ * B * 256 * 6 bytes, required; its contents afterwards are unspecified.  No
+ * reference counterpart (the generator of the benchmark configurations, as
+ * hg_random_play_step). */
 int hg_random_play(uint8_t* states, uint8_t* moves, int64_t B, int max_ply, int lockstep, uint32_t seed,
                    int32_t* plies_done, void* stream);
 

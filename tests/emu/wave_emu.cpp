@@ -80,6 +80,39 @@ void emu_successor_rows(const uint8_t* states, const uint8_t* legal, const int64
         successor_row(g_pos[t / kW], st[t], states, legal, a2r, midx, q * 4 + r % 4, N, num_roots, zero_row, t, feat);
     });
 }
+// k_random_play's ply loop with given choices: game i's board is loaded
+// once, then per ply (while its result is 0) the derived tables are rebuilt,
+// the list's tables generated, slot (u[i][ply] * n) >> 32 decoded by
+// list_slot and applied by apply_mirrored, which also writes the changed
+// bytes into the state row.  done[i]: plies applied.
+void emu_play(uint8_t* states, int64_t B, int plies, const uint32_t* u, int32_t* done) {
+    run_group(64, (B + kPosPerWave - 1) / kPosPerWave, [&](int64_t w, int t) {
+        int64_t i = w * kPosPerWave + t / kW;
+        const bool live = i < B;
+        if (!live) i = B - 1;
+        Pos& P = g_pos[t / kW];
+        uint8_t* row = states + i * kStateBytes;
+        int result = row[OFF_RESULT], d = 0;
+        load_position(P, row, t);
+        __syncthreads();
+        for (int ply = 0; ply < plies; ply++) {
+            const bool act = live && result == 0;
+            prepare_loaded(P, t);
+            const ListInfo L = generate_legal(P, t);
+            __syncthreads();
+            if (act && t % kW == 0) {
+                const int pick = (int)(((uint64_t)u[i * plies + ply] * (uint64_t)L.n) >> 32);
+                int tp = MV_PASS, from = 0, to = 0, seg;
+                if (L.total > 0) list_slot(P, L, pick, tp, from, to, seg);
+                apply_mirrored(P, row, tp & 0xFF, tp >> 8, from, to);
+                d++;
+            }
+            __syncthreads();
+            result = P.result;
+        }
+        if (live && t % kW == 0) done[i] = d;
+    });
+}
 void emu_queen_escape(const uint8_t* states, int64_t B, uint8_t* out) {
     run_group(64, (B + kPosPerWave - 1) / kPosPerWave, [&](int64_t w, int t) {
         int64_t i = w * kPosPerWave + t / kW;

@@ -57,6 +57,36 @@ def test_emulated_legal_features(emu, oracle, name):
     assert np.array_equal(a, oa)
 
 
+@pytest.mark.parametrize("mask,start_ply,seed", [(0, 0, 81), (0, 40, 82), (7, 60, 83)])
+def test_emulated_board_resident_play(emu, oracle, mask, start_ply, seed):
+    """k_random_play's ply loop: the board stays in LDS, each ply's move is
+    decoded from the generated tables (list_slot) rather than read from an
+    emitted list, and the state row only receives the bytes that changed
+    (apply_mirrored).  After 40 plies of given choices the rows and the ply
+    counts equal the oracle's replay: its own legal list, slot
+    (u * n) >> 32, apply_move, stopping at a result."""
+    B, plies = 24, 40
+    states, _ = oracle.generate_positions(B, mask, start_ply, seed, threads=4)
+    states = np.ascontiguousarray(states)
+    u = np.random.default_rng(seed).integers(0, 2**32, size=(B, plies), dtype=np.uint64).astype(np.uint32)
+    want = states.copy()
+    want_done = np.zeros(B, np.int32)
+    for i in range(B):
+        s = want[i]
+        for ply in range(plies):
+            if s[3415] != 0:
+                break
+            mv, n = oracle.legal_moves(s)
+            s = oracle.apply_move(s, mv[(int(u[i, ply]) * n) >> 32])
+            want_done[i] += 1
+        want[i] = s
+    got = states.copy()
+    done = np.zeros(B, np.int32)
+    emu.emu_play(_p(got), ctypes.c_int64(B), ctypes.c_int(plies), _p(u), _p(done))
+    assert np.array_equal(done, want_done)
+    assert np.array_equal(got, want)
+
+
 @pytest.mark.parametrize("mask,max_ply,seed", [(0, 120, 71), (7, 150, 72)])
 def test_emulated_group_ant_searches(emu, emu_antgrp, oracle, mask, max_ply, seed):
     """The build-time alternative whose lane group finishes each ant search
