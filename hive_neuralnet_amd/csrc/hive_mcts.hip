@@ -690,50 +690,62 @@ __global__ __launch_bounds__(64) void k_replay(const uint8_t* __restrict__ roots
 // The replay (k_replay with its results) and the leaf rows' legal lists +
 // features (k_legal<moves, features>) of a simulation wave in one launch,
 // two simulations per workgroup (lane groups of 32, as k_legal): a group
-// assembles its leaf row in LDS (the root's row, then the path moves applied
-// by one lane), writes the row and its result out (a zero row and 0 for an
-// idle simulation) and, after a barrier, runs the position program on the
-// row it wrote.  The LDS of the row and of the position program's board are
-// the same bytes, used one after the other.
+// copies the root's row to the leaf row and loads the root's board into LDS
+// (a zero row and board for an idle simulation), one lane applies the path
+// to the board and writes each move's changed bytes into the leaf row
+// (apply_mirrored; the path's moves staged in LDS 32 at a time), and the
+// position program then runs on the board as it stands -- no second load.
+__device__ __attribute__((aligned(16))) const uint8_t kZeroState[kStateBytes] = {};
+
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(6))) void k_replay_legal(
     const uint8_t* __restrict__ roots, int64_t B, uint8_t* __restrict__ leaves, const uint8_t* __restrict__ paths,
     const int32_t* __restrict__ plen, const int32_t* __restrict__ leaf_idx, int64_t T, int32_t* __restrict__ results,
     uint8_t* __restrict__ moves_out, int32_t* __restrict__ n_out, float* __restrict__ feat_out) {
-    __shared__ union LeafLds {
-        Pos P;
-        uint4 row[kStateBytes / 16];
-    } U[kPosPerWave];
+    __shared__ Pos PS[kPosPerWave];
     const int grp = threadIdx.x >> 5, l = threadIdx.x & 31;
+    Pos& P = PS[grp];
     const int64_t i = (int64_t)blockIdx.x * kPosPerWave + grp;
     const bool live = i < T;
     const int64_t sim = live ? i : T - 1;  // a group past the end reads the last row and writes nothing
-    uint4* row = U[grp].row;
     const bool idle = leaf_idx[sim] < 0;
-    if (!idle) {
-        const uint4* src = reinterpret_cast<const uint4*>(roots + (sim % B) * kStateBytes);
-        for (int k = l; k < kStateBytes / 16; k += 32) row[k] = src[k];
-    }
-    __syncthreads();
-    if (!idle && l == 0) {
-        RowView v{reinterpret_cast<uint8_t*>(row)};
-        const int n = plen[sim];
-        const uint8_t* p = paths + sim * kDepth * 6;
-        for (int d = 0; d < n && d < kDepth; d++, p += 6) v.apply(p[0], p[1], p[2] | (p[3] << 8), p[4] | (p[5] << 8));
-    }
-    __syncthreads();
+    const uint8_t* src = idle ? kZeroState : roots + (sim % B) * kStateBytes;
     uint8_t* leaf_row = leaves + sim * kStateBytes;
     if (live) {
-        uint4* dst = reinterpret_cast<uint4*>(leaf_row);
-        const uint4 z = make_uint4(0u, 0u, 0u, 0u);
-        for (int k = l; k < kStateBytes / 16; k += 32) dst[k] = idle ? z : row[k];
-        if (l == 0) results[sim] = idle ? 0 : reinterpret_cast<const uint8_t*>(row)[OFF_RESULT];
+        const uint4* s4 = reinterpret_cast<const uint4*>(src);
+        uint4* d4 = reinterpret_cast<uint4*>(leaf_row);
+        for (int k = l; k < kStateBytes / 16; k += 32) d4[k] = s4[k];
     }
-    // the barrier's workgroup-scope fences order the row's stores before the
-    // reads below (the same workgroup; a device-scope fence would write back
-    // the whole L2 on every workgroup)
+    load_position(P, src, threadIdx.x);
+    // the board, and the leaf row's copy before the lane applying the path
+    // reads it back (the barrier's workgroup-scope fences; a device-scope
+    // fence would write back the whole L2 on every workgroup)
     __syncthreads();
-    run_legal<true, true, false>(U[grp].P, leaf_row, threadIdx.x, live ? moves_out + sim * (kMaxLegal * 6) : nullptr,
-                                 live ? n_out + sim : nullptr, live ? feat_out + sim * kFeat : nullptr, nullptr);
+    const int n = live && !idle ? min(plen[sim], kDepth) : 0;
+    static_assert(kPool >= 3 * kW, "the pool holds one staged path move per lane");
+    uint16_t* stage = P.u2.pool;  // free until generation: 32 path moves as 3 half-words each
+    for (int d0 = 0; d0 < n; d0 += kW) {
+        if (d0 + l < n) {
+            const uint16_t* m = reinterpret_cast<const uint16_t*>(paths + (sim * kDepth + d0 + l) * 6);
+            const uint16_t a = m[0], b = m[1], c = m[2];
+            stage[3 * l] = a;
+            stage[3 * l + 1] = b;
+            stage[3 * l + 2] = c;
+        }
+        hw_group_lockstep();
+        if (l == 0) {
+            const int e = min(n - d0, kW);
+            for (int k = 0; k < e; k++) {
+                const int a = stage[3 * k];
+                apply_mirrored(P, leaf_row, a & 0xFF, a >> 8, stage[3 * k + 1], stage[3 * k + 2]);
+            }
+        }
+        hw_group_lockstep();
+    }
+    __syncthreads();  // the board after the path; the leaf row's changed bytes
+    if (live && l == 0) results[sim] = idle ? 0 : P.result;
+    run_legal_loaded<true, true, false>(P, leaf_row, threadIdx.x, live ? moves_out + sim * (kMaxLegal * 6) : nullptr,
+                                        live ? n_out + sim : nullptr, live ? feat_out + sim * kFeat : nullptr,
+                                        nullptr);
 }
 
 // centroid of a state row (compute_centroid, state_encoder.cuh:889-906)

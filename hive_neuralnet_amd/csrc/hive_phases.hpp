@@ -1016,10 +1016,13 @@ HW_INL void prepare(Pos& P, const uint8_t* __restrict__ S, int lane) {
     prepare_loaded(P, lane);
 }
 
+// run_legal on a board already loaded (load_position or moves applied since,
+// behind a barrier); S is the state row it stands for (stacked levels).
 template <bool WithMoves, bool WithFeat, bool WithAct>
-HW_INL void run_legal(Pos& P, const uint8_t* __restrict__ S, int lane, uint8_t* __restrict__ moves_row,
-                      int32_t* __restrict__ n_slot, float* __restrict__ feat_row, int32_t* __restrict__ act_row) {
-    prepare(P, S, lane);
+HW_INL void run_legal_loaded(Pos& P, const uint8_t* __restrict__ S, int lane, uint8_t* __restrict__ moves_row,
+                             int32_t* __restrict__ n_slot, float* __restrict__ feat_row,
+                             int32_t* __restrict__ act_row) {
+    prepare_loaded(P, lane);
     ListInfo L = generate_legal(P, lane);
     place_list(P, lane);
     if (WithFeat) sources_clear(P, lane);
@@ -1038,6 +1041,14 @@ HW_INL void run_legal(Pos& P, const uint8_t* __restrict__ S, int lane, uint8_t* 
         int m = L.total > 0 ? min(L.n, L.n_place) : 0;
         features_finish(P, S, feat_row, lane, kFeatGen, 0u, L.ntypes ? (m + L.ntypes - 1) / L.ntypes : 0);
     }
+}
+
+template <bool WithMoves, bool WithFeat, bool WithAct>
+HW_INL void run_legal(Pos& P, const uint8_t* __restrict__ S, int lane, uint8_t* __restrict__ moves_row,
+                      int32_t* __restrict__ n_slot, float* __restrict__ feat_row, int32_t* __restrict__ act_row) {
+    load_position(P, S, lane);
+    __syncthreads();
+    run_legal_loaded<WithMoves, WithFeat, WithAct>(P, S, lane, moves_row, n_slot, feat_row, act_row);
 }
 
 HW_INL void run_extract(Pos& P, ListSets& X, const uint8_t* __restrict__ S, const uint8_t* __restrict__ M, int nl,
