@@ -879,8 +879,8 @@ HW_INL void words_centroid(uint32_t w, int lane, int& cq, int& cr) {
 //
 // kPlanned = false: the game's simulations in order on one wave; `cnt` is the
 //   game's running node counter and the backup walks up to the root.
-// kPlanned = true: one root child's simulations (k_eb_apply): the expansion
-//   decision and node base come from k_eb_plan (`planned` >= 0: expand at that
+// kPlanned = true: one root child's simulations (k_eb_game): the expansion
+//   decision and node base come from the plan (`planned` >= 0: expand at that
 //   node id), the node counter and the root belong to the plan, so the walk
 //   above the path stops below the root; only selection paths get here.
 template <bool kPlanned>
@@ -1049,7 +1049,7 @@ HW_INL void eb_sim(const Tree& T, const LeafIn& L, const float* __restrict__ nn_
             for (int s2 = n; s2 < kDepth + 1 && node >= 0; s2++) {
                 const int64_t ni = g0 + node;
                 const int up = T.pa[ni];
-                if (kPlanned && up < 0) break;  // the root: k_eb_plan's
+                if (kPlanned && up < 0) break;  // the root: the plan's
                 T.vc[ni] += 1;
                 T.tv[ni] += w;
                 w = -w;
@@ -1098,29 +1098,31 @@ __global__ __launch_bounds__(64) void k_expand_backprop(Tree T, LeafIn L, const 
 // The same kernel over root children.  Below the root, a simulation touches
 // only the subtree of the root child it entered: its path, its leaf and the
 // leaf's new children.  So the simulations of different root children are
-// independent except for two things k_eb_plan settles first, in simulation
-// order: node ids (an exclusive prefix sum of the expansion sizes) and the
-// root's statistics.  Then k_eb_apply runs one wave per (game, root child),
-// that child's simulations in order, with the same float operations in the
-// same order per node as the one-wave kernel.  Games where this does not
-// hold -- the node pool could run short, a path that is not a selection path,
-// a leaf at the root -- are flagged, and the first k_eb_apply wave of such a
-// game runs all its simulations in order instead.
-struct EbWork {
-    int32_t* base;        // [total] node id of the simulation's first new child, -1 = none
-    int32_t* group;       // [total] root-child group of the simulation, -1 = idle
-    int32_t* ngroups;     // [B]
-    int32_t* sequential;  // [B] 1 = the game runs in the one-wave order
-};
+// independent except for two things a planning wave settles first, in
+// simulation order: node ids (an exclusive prefix sum of the expansion sizes)
+// and the root's statistics.  Then each root child's simulations are applied
+// in order by one wave, with the same float operations in the same order per
+// node as the one-wave kernel.  Games where this does not hold -- the node
+// pool could run short, a path that is not a selection path, a leaf at the
+// root -- are flagged, and the game's first wave runs all its simulations in
+// order instead.  One workgroup per game (k_eb_game): wave 0 plans into LDS,
+// one workgroup barrier, then wave w applies root-child groups w, w + waves,
+// ...
 constexpr int kPlanMax = 64;  // simulations per game one planning wave takes (one per lane)
+constexpr int kEbWaves = 16;  // waves of a game's workgroup (at most kPlanMax groups, looped)
 
-__global__ __launch_bounds__(64) void k_eb_plan(Tree T, LeafIn L, const float* __restrict__ nn_values,
-                                                const int32_t* __restrict__ vl_paths,
-                                                const int32_t* __restrict__ vl_lens, int64_t B, int64_t total,
-                                                EbWork Wk) {
-    const int64_t g = blockIdx.x;
-    const int lane = threadIdx.x;
-    if (g >= B) return;
+struct EbPlan {
+    int base[kPlanMax];   // node id of simulation k's first new child, -1 = none
+    int group[kPlanMax];  // root-child group of simulation k, -1 = idle
+    int ngroups;
+    int sequential;       // 1 = the game runs in the one-wave order
+};
+
+// The planning wave of game g (its simulations k * B + g, k < K, one per lane).
+HW_INL void eb_plan_game(const Tree& T, const LeafIn& L, const float* __restrict__ nn_values,
+                         const int32_t* __restrict__ vl_paths, const int32_t* __restrict__ vl_lens, int64_t B,
+                         int64_t total, int64_t g, int lane, EbPlan& P) {
+
     const int K = (int)(total / B);  // the host launches this only for total = K * B, K <= kPlanMax
     const int64_t g0 = g * T.M;
     const int64_t sim = (int64_t)lane * B + g;
@@ -1148,7 +1150,7 @@ __global__ __launch_bounds__(64) void k_eb_plan(Tree T, LeafIn L, const float* _
         ltv = T.tval[g0 + leaf];
         n = n < 0 ? 0 : (n > kDepth ? kDepth : n);
         // a selection path: every entry in the pool, each the child of the entry
-        // before, the last one the leaf (eb_sim's chain test, which k_eb_apply relies on)
+        // before, the last one the leaf (eb_sim's chain test, which the planned waves rely on)
         head = n > 0 ? pv[0] : leaf;
         top = leaf;
         x = leaf;
@@ -1212,12 +1214,12 @@ __global__ __launch_bounds__(64) void k_eb_plan(Tree T, LeafIn L, const float* _
     const int gid_own = __popcll(om & ((1ull << lane) - 1ull));
     const int gid = __shfl(gid_own, firstk, 64);
     if (lane < K) {
-        Wk.base[sim] = (!seq && sz > 0) ? cnt0 + pre : -1;
-        Wk.group[sim] = (!seq && live) ? gid : -1;
+        P.base[lane] = (!seq && sz > 0) ? cnt0 + pre : -1;
+        P.group[lane] = (!seq && live) ? gid : -1;
     }
     if (lane == 0) {
-        Wk.ngroups[g] = seq ? 0 : __popcll(om);
-        Wk.sequential[g] = seq ? 1 : 0;
+        P.ngroups = seq ? 0 : __popcll(om);
+        P.sequential = seq ? 1 : 0;
         if (!seq) T.cnt[g] = cnt0 + tot;
     }
     if (seq) return;
@@ -1256,37 +1258,44 @@ __global__ __launch_bounds__(64) void k_eb_plan(Tree T, LeafIn L, const float* _
     }
 }
 
-// One wave per (game, root-child group): blockIdx.x = g + B * j.
-__global__ __launch_bounds__(64) void k_eb_apply(Tree T, LeafIn L, const float* __restrict__ nn_values,
-                                                 const int32_t* __restrict__ vl_paths,
-                                                 const int32_t* __restrict__ vl_lens, float q_penalty, int64_t B,
-                                                 int64_t total, EbWork Wk) {
-    const int64_t g = blockIdx.x % B;
-    const int j = (int)(blockIdx.x / B);
-    const int lane = threadIdx.x;
-    if (Wk.sequential[g]) {  // a game the plan left to the one-wave order: its first wave runs it
-        if (j != 0) return;
+__global__ __launch_bounds__(64 * kEbWaves) void k_eb_game(Tree T, LeafIn L, const float* __restrict__ nn_values,
+                                                          const int32_t* __restrict__ vl_paths,
+                                                          const int32_t* __restrict__ vl_lens, float q_penalty,
+                                                          int64_t B, int64_t total) {
+    __shared__ EbPlan P;
+    const int64_t g = blockIdx.x;  // the grid is B workgroups
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, waves = blockDim.x >> 6;
+    if (wave == 0) eb_plan_game(T, L, nn_values, vl_paths, vl_lens, B, total, g, lane, P);
+    // the plan (LDS) and its tree writes (node count, root statistics) before
+    // any wave applies; the only barrier of the kernel, reached by every wave
+    __syncthreads();
+    // Between two simulations of one wave a workgroup-scope fence orders the
+    // first's stores before the second's loads (the lanes of a wave run in
+    // step; no barrier, the waves' loop counts differ).
+    if (P.sequential) {  // a game the plan left to the one-wave order: its first wave runs it
+        if (wave != 0) return;
         int cnt = T.cnt[g];
         for (int64_t sim = g; sim < total; sim += B) {
             if (L.leaf[sim] < 0) continue;
             eb_sim<false>(T, L, nn_values, vl_paths, vl_lens, q_penalty, g, sim, lane, cnt, -1);
-            __syncthreads();
+            __threadfence_block();
         }
         return;
     }
-    if (j >= Wk.ngroups[g]) return;
     const int K = (int)(total / B);
-    const int64_t mine = lane < K ? (int64_t)lane * B + g : 0;
-    const uint64_t todo = __ballot(lane < K && Wk.group[mine] == j);
-    const int plan = lane < K ? Wk.base[mine] : -1;
-    uint64_t m = todo;
-    int unused = 0;
-    while (m) {
-        const int k = __ffsll((unsigned long long)m) - 1;
-        m &= m - 1;
-        eb_sim<true>(T, L, nn_values, vl_paths, vl_lens, q_penalty, g, (int64_t)k * B + g, lane, unused,
-                     __shfl(plan, k, 64));
-        __syncthreads();  // the next simulation of this root child reads this one's stores
+    const int plan = lane < K ? P.base[lane] : -1;
+    const int grp = lane < K ? P.group[lane] : -1;
+    const int ng = P.ngroups;
+    for (int j = wave; j < ng; j += waves) {
+        uint64_t m = __ballot(grp == j);
+        int unused = 0;
+        while (m) {
+            const int k = __ffsll((unsigned long long)m) - 1;
+            m &= m - 1;
+            eb_sim<true>(T, L, nn_values, vl_paths, vl_lens, q_penalty, g, (int64_t)k * B + g, lane, unused,
+                         __shfl(plan, k, 64));
+            __threadfence_block();  // the next simulation of this root child reads this one's stores
+        }
     }
 }
 
@@ -1719,6 +1728,30 @@ __global__ __launch_bounds__(kHalvThreads) void k_gumbel_halving(Tree T, const i
 
 }  // namespace
 
+// hg_mcts_expand_backprop_dense_ws's launch with at most `groups` waves per
+// game's workgroup (every root child the game's simulations entered gets a
+// wave when there are at most that many; the waves loop otherwise): the
+// simulation wave passes its candidate count, which bounds the root children
+// it enters, so that a small round does not reserve sixteen waves per game.
+static int eb_games(const hg_tree* tree, const float* child_q_values, const int32_t* leaf_idx,
+                    const uint8_t* leaf_states, const uint8_t* legal_moves, const int32_t* num_legal,
+                    const float* priors_per_legal, const int32_t* results, const float* nn_values,
+                    const int32_t* vl_paths, const int32_t* vl_lens, float q_penalty, int64_t B, int64_t total,
+                    int groups, hipStream_t stream) {
+    if (B <= 0 || total <= 0) return 0;
+    const int64_t K = total / B;
+    if (total % B != 0 || K > kPlanMax || B * K > (int64_t)INT32_MAX)  // outside the planner's shape
+        return hg_mcts_expand_backprop_dense(tree, child_q_values, leaf_idx, leaf_states, legal_moves, num_legal,
+                                             priors_per_legal, results, nn_values, vl_paths, vl_lens, q_penalty, B,
+                                             total, stream);
+    LeafIn L{leaf_idx, leaf_states, legal_moves, num_legal, priors_per_legal, child_q_values, results};
+    int64_t waves = K < kEbWaves ? K : kEbWaves;
+    if (groups < waves) waves = groups < 1 ? 1 : groups;
+    hipLaunchKernelGGL(k_eb_game, dim3((unsigned)B), dim3((unsigned)(64 * waves)), 0, stream, to_tree(tree), L,
+                       nn_values, vl_paths, vl_lens, q_penalty, B, total);
+    return finish();
+}
+
 extern "C" {
 
 int hg_mcts_wave_stats(const int32_t* leaf_idx, const int32_t* num_legal, const int32_t* vl_lens, int64_t total,
@@ -1807,22 +1840,9 @@ int hg_mcts_expand_backprop_dense_ws(const hg_tree* tree, const float* child_q_v
                                      const int32_t* num_legal, const float* priors_per_legal, const int32_t* results,
                                      const float* nn_values, const int32_t* vl_paths, const int32_t* vl_lens,
                                      float q_penalty, int64_t B, int64_t total, void* workspace, void* stream) {
-    if (B <= 0 || total <= 0) return 0;
-    const int64_t K = total / B;
-    if (total % B != 0 || K > kPlanMax || B * K > (int64_t)INT32_MAX)  // outside the planner's shape
-        return hg_mcts_expand_backprop_dense(tree, child_q_values, leaf_idx, leaf_states, legal_moves, num_legal,
-                                             priors_per_legal, results, nn_values, vl_paths, vl_lens, q_penalty, B,
-                                             total, stream);
-    LeafIn L{leaf_idx, leaf_states, legal_moves, num_legal, priors_per_legal, child_q_values, results};
-    int32_t* w = static_cast<int32_t*>(workspace);
-    EbWork Wk{w, w + total, w + 2 * total, w + 2 * total + B};
-    hipStream_t s = (hipStream_t)stream;
-    const Tree T = to_tree(tree);
-    hipLaunchKernelGGL(k_eb_plan, dim3((unsigned)B), dim3(64), 0, s, T, L, nn_values, vl_paths, vl_lens, B, total,
-                       Wk);
-    hipLaunchKernelGGL(k_eb_apply, dim3((unsigned)(B * K)), dim3(64), 0, s, T, L, nn_values, vl_paths, vl_lens,
-                       q_penalty, B, total, Wk);
-    return finish();
+    (void)workspace;  // the plan lives in the workgroup's LDS
+    return eb_games(tree, child_q_values, leaf_idx, leaf_states, legal_moves, num_legal, priors_per_legal, results,
+                    nn_values, vl_paths, vl_lens, q_penalty, B, total, kEbWaves, (hipStream_t)stream);
 }
 
 int hg_mcts_select(const hg_tree* tree, const int8_t* game_active, const int32_t* root_nodes, float c_puct, int64_t B,
@@ -1908,9 +1928,9 @@ int hg_mcts_wave_root_slots(const hg_tree* tree, const uint8_t* root_states, con
                                  net->action2_b, buf->leaf_workspace, buf->priors, buf->values, buf->child_q,
                                  buf->leaf_idx, buf->vl_lens, buf->stats, s)))
         return e;
-    return hg_mcts_expand_backprop_dense_ws(tree, buf->child_q, buf->leaf_idx, buf->leaf_states, buf->legal_moves,
-                                            buf->num_legal, buf->priors, buf->results, buf->values, buf->vl_paths,
-                                            buf->vl_lens, q_penalty, B, T, buf->tree_workspace, stream);
+    return eb_games(tree, buf->child_q, buf->leaf_idx, buf->leaf_states, buf->legal_moves, buf->num_legal,
+                    buf->priors, buf->results, buf->values, buf->vl_paths, buf->vl_lens, q_penalty, B, T,
+                    num_candidates, s);
 }
 
 int hg_gumbel_halving(const hg_tree* tree, const int32_t* root_nodes, const int32_t* candidates, int C,

@@ -391,10 +391,12 @@ int hg_mcts_expand_backprop_dense(const hg_tree* tree, const float* child_q_valu
                                   int64_t total, void* stream);
 
 /* hg_mcts_expand_backprop_dense with a workspace of
- * hg_mcts_expand_backprop_dense_workspace(B, total) bytes (4-byte aligned):
- * the same tree, the simulations of different root children applied in
- * parallel (a planning launch settles node ids and the root's statistics in
- * simulation order, then one wave per root child).  Identical results; the
+ * hg_mcts_expand_backprop_dense_workspace(B, total) bytes (4-byte aligned;
+ * accepted and not written: the plan lives in on-chip memory): the same
+ * tree, the simulations of different root children applied in parallel (one
+ * workgroup per game: a planning wave settles node ids and the root's
+ * statistics in simulation order, then one wave per root child).  Identical
+ * results; the
  * one-wave-per-game order is kept for games whose node pool could run short
  * or with a path that is not a selection path (each entry a node of the pool
  * whose parent is the entry before it, the last entry the leaf).  Path
