@@ -413,7 +413,8 @@ __device__ __forceinline__ float wave_max_f(float v) {
 __global__ __launch_bounds__(256) void k_leaf_softmax(const float* __restrict__ logit, const float* __restrict__ cval,
                                                       const int64_t* __restrict__ offsets,
                                                       const int32_t* __restrict__ nlegal, int64_t T,
-                                                      float* __restrict__ priors, float* __restrict__ child_q) {
+                                                      float* __restrict__ priors, float* __restrict__ child_q,
+                                                      int dense) {
     const int lane = threadIdx.x & 63;
     const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (t >= T) return;
@@ -438,8 +439,10 @@ __global__ __launch_bounds__(256) void k_leaf_softmax(const float* __restrict__ 
 #pragma unroll
     for (int k = 0; k < 4; k++) {
         const int i = lane + 64 * k;
-        priors[t * kSlots + i] = i < n ? ex[k] / s : 0.0f;
-        child_q[t * kSlots + i] = i < n ? -cv[k] : 0.0f;
+        if (i < n || dense) {  // `dense`: the rows' tails zeroed, else left as they are
+            priors[t * kSlots + i] = i < n ? ex[k] / s : 0.0f;
+            child_q[t * kSlots + i] = i < n ? -cv[k] : 0.0f;
+        }
     }
 }
 
@@ -476,7 +479,7 @@ int hg_fnn_leaf_eval(const float* features, int64_t T, int64_t N, int F, const i
                            N, F, succ_leaf, T, fc1_w, fc1_b, ln_w, ln_b, fc2_w, fc2_b, value_w, value_b, action1_w,
                            action1_b, action2_w, action2_b, R, cval, logit, nullptr, nullptr);
     hipLaunchKernelGGL(k_leaf_softmax, dim3(grid_for(T, 4)), dim3(256), 0, st, logit, cval, offsets, num_legal, T,
-                       priors, child_q);
+                       priors, child_q, 1);
     return (int)hipGetLastError();
 }
 
@@ -514,7 +517,7 @@ int leaf_eval_lists(const uint8_t* leaf_states, const uint8_t* legal_moves, cons
                     const float* value_w, float value_b, const float* action1_w, const float* action1_b,
                     const float* action2_w, float action2_b, void* workspace, float* priors, float* root_values,
                     float* child_q, const int32_t* leaf_idx, const int32_t* vl_lens, int64_t* stats,
-                    hipStream_t st) {
+                    hipStream_t st, bool dense) {
     if (T < 0 || F <= 0 || F > kFMax || (F & 1)) return (int)hipErrorInvalidValue;
     if (((uintptr_t)root_features & 7) || ((uintptr_t)workspace & 255)) return (int)hipErrorInvalidValue;
     if (F != 122) return (int)hipErrorInvalidValue;  // the successor rows are the engine's 122 features
@@ -557,7 +560,7 @@ int leaf_eval_lists(const uint8_t* leaf_states, const uint8_t* legal_moves, cons
                        plan.a2r, T, fc1_w, fc1_b, ln_w, ln_b, fc2_w, fc2_b, value_w, value_b, action1_w, action1_b,
                        action2_w, action2_b, R, cval, logit, plan.total, pk);
     hipLaunchKernelGGL(k_leaf_softmax, dim3(grid_for(T, 4)), dim3(256), 0, st, logit, cval, plan.offsets,
-                       num_legal, T, priors, child_q);
+                       num_legal, T, priors, child_q, dense ? 1 : 0);
     return (int)hipGetLastError();
 }
 

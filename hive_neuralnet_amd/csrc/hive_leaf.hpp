@@ -81,13 +81,15 @@ int successor_rows_after_plan(const uint8_t* states, const uint8_t* legal_moves,
 
 // hive_fnn.hip: hg_fnn_leaf_eval_lists, and with `stats` (int64[4]) the
 // simulation wave's search counters of hg_mcts_wave_stats over leaf_idx,
-// num_legal and vl_lens added in its first launch
+// num_legal and vl_lens added in its first launch; without `dense` the
+// priors / child-Q rows are written up to each leaf's legal count only (the
+// simulation wave's expansion reads no further)
 int leaf_eval_lists(const uint8_t* leaf_states, const uint8_t* legal_moves, const int32_t* num_legal,
                     const float* root_features, int64_t T, int F, const float* fc1_w, const float* fc1_b,
                     const float* ln_w, const float* ln_b, const float* fc2_w, const float* fc2_b,
                     const float* value_w, float value_b, const float* action1_w, const float* action1_b,
                     const float* action2_w, float action2_b, void* workspace, float* priors, float* root_values,
                     float* child_q, const int32_t* leaf_idx, const int32_t* vl_lens, int64_t* stats,
-                    hipStream_t stream);
+                    hipStream_t stream, bool dense = true);
 
 }  // namespace hw

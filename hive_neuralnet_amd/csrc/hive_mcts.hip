@@ -1926,7 +1926,7 @@ int hg_mcts_wave_root_slots(const hg_tree* tree, const uint8_t* root_states, con
                                  net->fc1_w, net->fc1_b, net->ln_w, net->ln_b, net->fc2_w, net->fc2_b,
                                  net->value_w, net->value_b, net->action1_w, net->action1_b, net->action2_w,
                                  net->action2_b, buf->leaf_workspace, buf->priors, buf->values, buf->child_q,
-                                 buf->leaf_idx, buf->vl_lens, buf->stats, s)))
+                                 buf->leaf_idx, buf->vl_lens, buf->stats, s, false)))
         return e;
     return eb_games(tree, buf->child_q, buf->leaf_idx, buf->leaf_states, buf->legal_moves, buf->num_legal,
                     buf->priors, buf->results, buf->values, buf->vl_paths, buf->vl_lens, q_penalty, B, T,

@@ -477,9 +477,9 @@ typedef struct hg_wave_buffers {  /* rows for T = W * num_candidates * B simulat
     uint8_t* legal_moves;    /* [T][256][6] */
     int32_t* num_legal;      /* [T] */
     float* features;         /* [T][122], 8-byte aligned */
-    float* priors;           /* [T][256] */
+    float* priors;           /* [T][256], each row written up to its leaf's legal count */
     float* values;           /* [T] */
-    float* child_q;          /* [T][256] */
+    float* child_q;          /* [T][256], each row written up to its leaf's legal count */
     void* leaf_workspace;    /* hg_fnn_leaf_eval_lists_workspace(T, 122) bytes, 256-byte aligned */
     void* tree_workspace;    /* hg_mcts_expand_backprop_dense_workspace(B, T) bytes, 4-byte aligned */
     int64_t* stats;          /* NULL, or hg_mcts_wave_stats' int64[4], accumulated */
