@@ -123,12 +123,15 @@ struct SelectOut {
     int32_t* plen;
     int32_t* vl;
     int32_t* vlen;
+    int tails = 1;  // 0: the rows past the recorded entries are left as they are
 };
 
 // Zeros past the recorded entries of a simulation's path rows (move bytes
 // from plen, node ids from vlen), so the dense selects write whole rows and
-// their callers need not clear the outputs.
+// their callers need not clear the outputs.  The simulation wave, whose
+// readers stop at the lengths, leaves the tails (O.tails = 0).
 __device__ __forceinline__ void zero_tails(const SelectOut& O, int64_t sim, int plen, int vlen, int lane) {
+    if (!O.tails) return;
     uint16_t* pw = reinterpret_cast<uint16_t*>(O.paths + sim * kDepth * 6);
     for (int k = 3 * plen + lane; k < 3 * kDepth; k += 64) pw[k] = 0;
     int32_t* vw = O.vl + sim * kDepth;
@@ -1752,6 +1755,21 @@ static int eb_games(const hg_tree* tree, const float* child_q_values, const int3
     return finish();
 }
 
+// hg_mcts_select_root_slots with the path rows' tails zeroed or left
+// (O.tails)
+static int select_root_slots(const hg_tree* tree, const int8_t* game_active, const int32_t* root_nodes,
+                             const int32_t* root_slots, int num_candidates, int max_root_children, float c_puct,
+                             int64_t B, int W, int deterministic_non_root, float non_root_sigma, float q_penalty,
+                             const SelectOut& O, hipStream_t stream) {
+    if (B <= 0 || W <= 0 || num_candidates <= 0) return 0;
+    const int64_t total = (int64_t)W * num_candidates * B;
+    if (B * num_candidates > (int64_t)0x7fffffff) return (int)hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_select_slots, dim3((unsigned)(B * num_candidates)), dim3(64), 0, stream, to_tree(tree),
+                       game_active, root_nodes, root_slots, num_candidates, max_root_children, c_puct, B, total,
+                       deterministic_non_root, non_root_sigma, q_penalty, O);
+    return finish();
+}
+
 extern "C" {
 
 int hg_mcts_wave_stats(const int32_t* leaf_idx, const int32_t* num_legal, const int32_t* vl_lens, int64_t total,
@@ -1767,15 +1785,9 @@ int hg_mcts_select_root_slots(const hg_tree* tree, const int8_t* game_active, co
                               int64_t B, int W, int deterministic_non_root, float non_root_sigma, float q_penalty,
                               int32_t* leaf_idx, uint8_t* move_paths, int32_t* path_lens, int32_t* vl_paths,
                               int32_t* vl_lens, void* stream) {
-    if (B <= 0 || W <= 0 || num_candidates <= 0) return 0;
-    int64_t total = (int64_t)W * num_candidates * B;
-    SelectOut O{leaf_idx, move_paths, path_lens, vl_paths, vl_lens};
-    if (B * num_candidates > (int64_t)0x7fffffff) return (int)hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_select_slots, dim3((unsigned)(B * num_candidates)), dim3(64), 0, (hipStream_t)stream,
-                       to_tree(tree),
-                       game_active, root_nodes, root_slots, num_candidates, max_root_children, c_puct, B, total,
-                       deterministic_non_root, non_root_sigma, q_penalty, O);
-    return finish();
+    return select_root_slots(tree, game_active, root_nodes, root_slots, num_candidates, max_root_children, c_puct, B,
+                             W, deterministic_non_root, non_root_sigma, q_penalty,
+                             SelectOut{leaf_idx, move_paths, path_lens, vl_paths, vl_lens, 1}, (hipStream_t)stream);
 }
 
 int hg_mcts_select_root_mask(const hg_tree* tree, const int8_t* game_active, const int32_t* root_nodes,
@@ -1911,9 +1923,12 @@ int hg_mcts_wave_root_slots(const hg_tree* tree, const uint8_t* root_states, con
     const int64_t T = (int64_t)W * num_candidates * B;
     if (T > buf->capacity || T > (int64_t)INT32_MAX) return (int)hipErrorInvalidValue;
     hipStream_t s = (hipStream_t)stream;
-    int e = hg_mcts_select_root_slots(tree, game_active, root_nodes, root_slots, num_candidates, max_root_children,
-                                      c_puct, B, W, deterministic_non_root, non_root_sigma, q_penalty, buf->leaf_idx,
-                                      buf->move_paths, buf->path_lens, buf->vl_paths, buf->vl_lens, stream);
+    // the wave's readers of the path rows (replay, expansion + backup) stop at
+    // the recorded lengths: the rows' tails are not written
+    int e = select_root_slots(tree, game_active, root_nodes, root_slots, num_candidates, max_root_children, c_puct, B,
+                              W, deterministic_non_root, non_root_sigma, q_penalty,
+                              SelectOut{buf->leaf_idx, buf->move_paths, buf->path_lens, buf->vl_paths, buf->vl_lens, 0},
+                              s);
     if (e) return e;
     // replay into the leaf rows (idle simulations: zero rows) with each leaf's
     // result, and the leaves' legal lists + features, in one launch

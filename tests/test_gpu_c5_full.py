@@ -187,8 +187,15 @@ class SliceShadow:
             b = {k: np.ascontiguousarray(_np(getattr(plan, k)[:T][r])) for k in (
                 "leaf_idx", "move_paths", "path_lens", "vl_paths", "vl_lens", "leaf_states", "results",
                 "legal_moves", "num_legal", "priors", "values", "child_q")}
-            for e, k in zip(exp, ("leaf_idx", "move_paths", "path_lens", "vl_paths", "vl_lens")):
-                assert np.array_equal(e, b[k]), f"native wave: select output {k} differs"
+            exp = dict(zip(("leaf_idx", "move_paths", "path_lens", "vl_paths", "vl_lens"), exp))
+            for k in ("leaf_idx", "path_lens", "vl_lens"):
+                assert np.array_equal(exp[k], b[k]), f"native wave: select output {k} differs"
+            # the wave writes each path row up to its recorded length (its readers stop there)
+            depth = np.arange(exp["vl_paths"].shape[1])[None, :]
+            rec = depth < b["path_lens"][:, None]
+            assert np.array_equal(exp["move_paths"][rec], b["move_paths"][rec]), "native wave: move paths differ"
+            rec = depth < b["vl_lens"][:, None]
+            assert np.array_equal(exp["vl_paths"][rec], b["vl_paths"][rec]), "native wave: node paths differ"
             st = np.zeros((len(r), 3424), np.uint8)
             self.m.replay(np.ascontiguousarray(_np(roots[g])), st, b["move_paths"], b["path_lens"], b["leaf_idx"])
             assert np.array_equal(st, b["leaf_states"]), "native wave: replayed leaf states differ"

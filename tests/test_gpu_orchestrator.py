@@ -116,9 +116,16 @@ class Shadow:
         b = {k: _np(getattr(plan, k)[:T]) for k in (
             "leaf_idx", "move_paths", "path_lens", "vl_paths", "vl_lens", "leaf_states", "results", "legal_moves",
             "num_legal", "priors", "values", "child_q")}
-        exp = self.m.select_slots(self.ot, active, rnodes, slots, max_root, c_puct, W, det, sigma, qp)
-        for e, k in zip(exp, ("leaf_idx", "move_paths", "path_lens", "vl_paths", "vl_lens")):
-            assert np.array_equal(e, b[k]), f"native wave: select output {k} differs"
+        exp = dict(zip(("leaf_idx", "move_paths", "path_lens", "vl_paths", "vl_lens"),
+                       self.m.select_slots(self.ot, active, rnodes, slots, max_root, c_puct, W, det, sigma, qp)))
+        for k in ("leaf_idx", "path_lens", "vl_lens"):
+            assert np.array_equal(exp[k], b[k]), f"native wave: select output {k} differs"
+        # the wave writes each path row up to its recorded length (its readers stop there)
+        depth = np.arange(exp["vl_paths"].shape[1])[None, :]
+        rec = depth < b["path_lens"][:, None]
+        assert np.array_equal(exp["move_paths"][rec], b["move_paths"][rec]), "native wave: move paths differ"
+        rec = depth < b["vl_lens"][:, None]
+        assert np.array_equal(exp["vl_paths"][rec], b["vl_paths"][rec]), "native wave: node paths differ"
         leaves = np.zeros_like(b["leaf_states"])
         self.m.replay(roots, leaves, b["move_paths"], b["path_lens"], b["leaf_idx"])
         assert np.array_equal(leaves, b["leaf_states"]), "native wave: replayed leaf states differ"
