@@ -468,9 +468,9 @@ typedef struct hg_fnn_net {   /* a 64-wide HiveFNN (fnn_network.py:97-140), F = 
 
 typedef struct hg_wave_buffers {  /* rows for T = W * num_candidates * B simulations (or more) */
     int32_t* leaf_idx;       /* [T] */
-    uint8_t* move_paths;     /* [T][128][6] */
+    uint8_t* move_paths;     /* [T][128][6], each row written up to its path_lens entry */
     int32_t* path_lens;      /* [T] */
-    int32_t* vl_paths;       /* [T][128] */
+    int32_t* vl_paths;       /* [T][128], each row written up to its vl_lens entry */
     int32_t* vl_lens;        /* [T] */
     uint8_t* leaf_states;    /* [T][3424] */
     int32_t* results;        /* [T] */
