@@ -746,9 +746,11 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(6))) void k_
     }
     __syncthreads();  // the board after the path; the leaf row's changed bytes
     if (live && l == 0) results[sim] = idle ? 0 : P.result;
+    // legal lists end at their lengths: the wave's readers (successor rows,
+    // expansion) stop there
     run_legal_loaded<true, true, false>(P, leaf_row, threadIdx.x, live ? moves_out + sim * (kMaxLegal * 6) : nullptr,
                                         live ? n_out + sim : nullptr, live ? feat_out + sim * kFeat : nullptr,
-                                        nullptr);
+                                        nullptr, false);
 }
 
 // centroid of a state row (compute_centroid, state_encoder.cuh:889-906)

@@ -565,7 +565,7 @@ HW_INL void place_list(Pos& P, int lane) {
 // index comes from P.piece_win (set after the centroid, behind a barrier).
 template <bool WithMoves, bool WithAct, bool WithFeat>
 HW_INL void emit_list(Pos& P, const ListInfo& L, int lane, uint8_t* __restrict__ moves_row,
-                      int32_t* __restrict__ act_row, int cq, int cr) {
+                      int32_t* __restrict__ act_row, int cq, int cr, bool pad = true) {
     const int me = P.turn & 1;
     const int l = gl(lane);
     if (WithFeat && L.total > 0) {
@@ -624,7 +624,9 @@ HW_INL void emit_list(Pos& P, const ListInfo& L, int lane, uint8_t* __restrict__
         }
     }
     // the rest of the rows: zero moves and -1 action indices, in 16-byte stores
-    // (rows are 16-byte aligned: 1,536 and 1,024 bytes per position)
+    // (rows are 16-byte aligned: 1,536 and 1,024 bytes per position); without
+    // `pad` the rows end at the list's length
+    if (!pad) return;
     if (WithMoves) {
         const int h0 = 3 * L.n, c0 = (h0 + 7) >> 3;  // first padding half-word, first whole 16-byte chunk
         if (l < 8 * c0 - h0) row16[h0 + l] = 0;
@@ -1021,7 +1023,7 @@ HW_INL void prepare(Pos& P, const uint8_t* __restrict__ S, int lane) {
 template <bool WithMoves, bool WithFeat, bool WithAct>
 HW_INL void run_legal_loaded(Pos& P, const uint8_t* __restrict__ S, int lane, uint8_t* __restrict__ moves_row,
                              int32_t* __restrict__ n_slot, float* __restrict__ feat_row,
-                             int32_t* __restrict__ act_row) {
+                             int32_t* __restrict__ act_row, bool pad = true) {
     prepare_loaded(P, lane);
     ListInfo L = generate_legal(P, lane);
     place_list(P, lane);
@@ -1032,7 +1034,7 @@ HW_INL void run_legal_loaded(Pos& P, const uint8_t* __restrict__ S, int lane, ui
         if (gl(lane) < L.n_pieces) P.piece_win[gl(lane)] = (int16_t)window17(P.piece_cell[gl(lane)], cq, cr);
     }
     __syncthreads();
-    if (moves_row) emit_list<WithMoves, WithAct, WithFeat>(P, L, lane, moves_row, act_row, cq, cr);
+    if (moves_row) emit_list<WithMoves, WithAct, WithFeat>(P, L, lane, moves_row, act_row, cq, cr, pad);
     if (gl(lane) == 0 && n_slot) *n_slot = L.n;
     if (WithFeat) {
         __syncthreads();

@@ -474,7 +474,7 @@ typedef struct hg_wave_buffers {  /* rows for T = W * num_candidates * B simulat
     int32_t* vl_lens;        /* [T] */
     uint8_t* leaf_states;    /* [T][3424] */
     int32_t* results;        /* [T] */
-    uint8_t* legal_moves;    /* [T][256][6] */
+    uint8_t* legal_moves;    /* [T][256][6], each row written up to its num_legal entry */
     int32_t* num_legal;      /* [T] */
     float* features;         /* [T][122], 8-byte aligned */
     float* priors;           /* [T][256], each row written up to its leaf's legal count */
