@@ -208,33 +208,42 @@ constexpr int kSuccWaves = 5;
 // batch is bound by the latency of each group's rows in series, not by the
 // board loads that longer runs share).  The loop count is uniform over the
 // workgroup: both groups run while the first group's block is in range.
+template <typename Ix>
 HW_INL void successor_stream(const uint8_t* __restrict__ states, const uint8_t* __restrict__ legal,
-                             const int64_t* __restrict__ a2r, const int64_t* __restrict__ midx, int64_t N,
+                             const int64_t* __restrict__ a2r, const int64_t* __restrict__ midx, Ix N,
                              int64_t num_roots, float* __restrict__ feat_out) {
     __shared__ Pos PS[kPosPerWave];
     const int grp = threadIdx.x >> 5;
-    const int64_t groups = (int64_t)kPosPerWave * gridDim.x;
-    const int64_t per = (N + groups - 1) / groups;
+    const Ix groups = (Ix)kPosPerWave * (Ix)gridDim.x;
+    const Ix per = (N + groups - 1) / groups;
     const int R = per < 1 ? 1 : (per > kSuccRows ? kSuccRows : (int)per);
-    const int64_t blocks = (N + R - 1) / R;
+    const Ix blocks = (N + R - 1) / R;
     SuccessorStream st;
-    for (int64_t p = blockIdx.x; kPosPerWave * p < blocks; p += gridDim.x) {
+    for (Ix p = blockIdx.x; kPosPerWave * p < blocks; p += gridDim.x) {
         for (int k = 0; k < R; k++) {
             const int lane = hw_opaque(threadIdx.x);
-            const int64_t i = (kPosPerWave * p + grp) * R + k;
-            successor_row(PS[grp], st, states, legal, a2r, midx, i, N, num_roots, kZeroRow, lane, feat_out);
+            const Ix i = (kPosPerWave * p + grp) * R + k;
+            successor_row<Ix>(PS[grp], st, states, legal, a2r, midx, i, N, num_roots, kZeroRow, lane, feat_out);
         }
     }
 }
 
+// 32-bit row arithmetic is exact when every state, move and feature offset of
+// the batch (rows < rows_cap, roots < num_roots) stays below 2^32
+inline bool successor_narrow(int64_t rows_cap, int64_t num_roots) {
+    return rows_cap >= 0 && num_roots >= 0 && rows_cap <= ((int64_t)1 << 32) / kFeat &&
+           num_roots <= ((int64_t)1 << 32) / kStateBytes && num_roots <= ((int64_t)1 << 32) / (kMaxLegal * 6);
+}
+
 // fnn_successor_features_kernel (game_logic.cu:182-229): kSuccRows (root, move)
 // rows per lane group, two groups per wave, the grid striding over the rows.
+template <typename Ix>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kSuccWaves))) void k_successor_features(const uint8_t* __restrict__ states,
                                                            const uint8_t* __restrict__ legal,
                                                            const int64_t* __restrict__ a2r,
                                                            const int64_t* __restrict__ midx, int64_t N,
                                                            int64_t num_roots, float* __restrict__ feat_out) {
-    successor_stream(states, legal, a2r, midx, N, num_roots, feat_out);
+    successor_stream<Ix>(states, legal, a2r, midx, (Ix)N, num_roots, feat_out);
 }
 
 __global__ __launch_bounds__(64) void k_queen_escape(const uint8_t* __restrict__ states, int64_t B,
@@ -638,13 +647,14 @@ __global__ __launch_bounds__(256) void k_rows_plan(const int32_t* __restrict__ n
     rows_plan_block(nlegal, T, offsets, total, a2r, mi, (int)blockIdx.x);
 }
 
+template <typename Ix>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kSuccWaves))) void k_successor_rows(const uint8_t* __restrict__ states,
                                                        const uint8_t* __restrict__ legal,
                                                        const int64_t* __restrict__ a2r,
                                                        const int64_t* __restrict__ midx,
                                                        const int64_t* __restrict__ total, int64_t num_roots,
                                                        float* __restrict__ feat_out) {
-    successor_stream(states, legal, a2r, midx, *total, num_roots, feat_out);
+    successor_stream<Ix>(states, legal, a2r, midx, (Ix)*total, num_roots, feat_out);
 }
 
 inline int grid_for(int64_t n, int block) { return (int)((n + block - 1) / block); }
@@ -785,8 +795,13 @@ int hg_fnn_successor_features(const uint8_t* states, const uint8_t* legal_moves,
                               void* stream) {
     if (N <= 0) return 0;
     const int64_t pairs = (N + kSuccRows * kPosPerWave - 1) / (kSuccRows * kPosPerWave);
-    hipLaunchKernelGGL(k_successor_features, dim3((unsigned)(pairs < kSuccGrid ? pairs : kSuccGrid)), dim3(64), 0,
-                       (hipStream_t)stream, states, legal_moves, action_to_root, move_indices, N, num_roots, features);
+    const dim3 grid((unsigned)(pairs < kSuccGrid ? pairs : kSuccGrid));
+    if (successor_narrow(N, num_roots))
+        hipLaunchKernelGGL(k_successor_features<uint32_t>, grid, dim3(64), 0, (hipStream_t)stream, states, legal_moves,
+                           action_to_root, move_indices, N, num_roots, features);
+    else
+        hipLaunchKernelGGL(k_successor_features<int64_t>, grid, dim3(64), 0, (hipStream_t)stream, states, legal_moves,
+                           action_to_root, move_indices, N, num_roots, features);
     return finish();
 }
 
@@ -858,8 +873,12 @@ int successor_rows_after_plan(const uint8_t* states, const uint8_t* legal_moves,
     const RowsPlan R = rows_plan_of(workspace, T);
     const int64_t pairs = (T * kMaxLegal + kSuccRows * kPosPerWave - 1) / (kSuccRows * kPosPerWave);
     const unsigned grid = (unsigned)(pairs < kSuccGrid ? pairs : kSuccGrid);
-    hipLaunchKernelGGL(k_successor_rows, dim3(grid), dim3(64), 0, s, states, legal_moves, R.a2r, R.mi, R.total, T,
-                       features);
+    if (successor_narrow(T * kMaxLegal, T))  // at most 256 rows per leaf
+        hipLaunchKernelGGL(k_successor_rows<uint32_t>, dim3(grid), dim3(64), 0, s, states, legal_moves, R.a2r, R.mi,
+                           R.total, T, features);
+    else
+        hipLaunchKernelGGL(k_successor_rows<int64_t>, dim3(grid), dim3(64), 0, s, states, legal_moves, R.a2r, R.mi,
+                           R.total, T, features);
     return finish();
 }
 

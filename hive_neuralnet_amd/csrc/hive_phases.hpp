@@ -1105,27 +1105,34 @@ struct SuccessorStream {
     int64_t cur = -2;  // root whose base R holds (-1: the zero row)
 };
 
+// Ix: the index type of the rows and roots.  int64_t takes any batch;
+// uint32_t (`narrow`, for batches whose state, move and feature offsets all
+// stay below 2^32 -- the caller's check) does the row's index arithmetic in
+// 32 bits.  The range checks are made on the loaded 64-bit values either way.
+template <typename Ix = int64_t>
 HW_INL void successor_row(Pos& P, SuccessorStream& st, const uint8_t* __restrict__ states,
                           const uint8_t* __restrict__ legal, const int64_t* __restrict__ a2r,
-                          const int64_t* __restrict__ midx, int64_t i, int64_t N, int64_t num_roots,
+                          const int64_t* __restrict__ midx, Ix i, Ix N, int64_t num_roots,
                           const uint8_t* __restrict__ zero_row, int lane, float* __restrict__ feat_out) {
     const bool live = i < N;
-    int64_t root = live ? a2r[i] : -1;
-    const int64_t mi = live ? midx[i] : -1;
-    const bool valid = root >= 0 && root < num_roots && mi >= 0 && mi < kMaxLegal;
-    if (!valid) root = -1;
-    const uint8_t* S = valid ? states + root * kStateBytes : zero_row;
-    const uint8_t* m = valid ? legal + (root * kMaxLegal + mi) * 6 : zero_row;
-    const bool fresh = root != st.cur;
+    const int64_t r64 = live ? a2r[i] : -1;
+    const int64_t m64 = live ? midx[i] : -1;
+    const bool valid = (uint64_t)r64 < (uint64_t)num_roots && (uint64_t)m64 < (uint64_t)kMaxLegal;
+    const Ix root = (Ix)r64, mi = (Ix)m64;
+    const uint8_t* S = valid ? states + (Ix)(root * (Ix)kStateBytes) : zero_row;
+    const uint8_t* m = valid ? legal + (Ix)((root * (Ix)kMaxLegal + mi) * (Ix)6) : zero_row;
+    const int64_t key = valid ? r64 : -1;
+    const bool fresh = key != st.cur;
     if (fresh) load_position(P, S, lane);
     else restore_base(P, st.R, lane);
     __syncthreads();
     if (fresh) save_base(P, st.R, lane);
-    st.cur = root;
+    st.cur = key;
     __syncthreads();
-    successor_on_board(P, S, m, lane, live && valid ? feat_out + i * kFeat : nullptr);
+    float* out = feat_out + (Ix)(i * (Ix)kFeat);
+    successor_on_board(P, S, m, lane, live && valid ? out : nullptr);
     if (live && !valid)
-        for (int k = gl(lane); k < kFeat; k += kW) feat_out[i * kFeat + k] = 0.0f;
+        for (int k = gl(lane); k < kFeat; k += kW) out[k] = 0.0f;
     __syncthreads();
 }
 
