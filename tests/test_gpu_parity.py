@@ -208,6 +208,19 @@ def test_c4_full_lockstep(oracle):
     assert 0 < decided < G  # the run covers finished and unfinished games
 
 
+def test_lockstep_expansion_pieces(oracle):
+    """The one-launch random play with mosquito, ladybug and pillbug (throws
+    move other pieces, mosquitoes climb): 2,048 lockstep games to 300 plies,
+    every final state byte and ply count equal to the oracle's replay."""
+    from hive_neuralnet_amd.hive_gpu import random_positions
+    G, P, seed = 2048, 300, 0x5EED + 11
+    st, plies = random_positions(G, 7, P, seed, lockstep=True)
+    ost, oplies = oracle.lockstep_selfplay(G, 7, P, seed)
+    assert np.array_equal(plies.cpu().numpy(), oplies)
+    assert np.array_equal(st.cpu().numpy(), ost)
+    assert 0 < int((ost[:, 3415] != 0).sum()) < G
+
+
 def test_edge_cases(ext, oracle):
     e = ext.create_initial_states(0)
     m, n = ext.generate_legal_moves_batch(e, 0)
