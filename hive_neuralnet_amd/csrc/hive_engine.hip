@@ -196,9 +196,12 @@ __device__ __attribute__((aligned(16))) const uint8_t kZeroRow[kStateBytes] = {}
 // share the root's load
 constexpr int kSuccRows = 8;
 constexpr int64_t kSuccGrid = 16384;  // workgroups of the successor kernels (they stride beyond)
-// register budget of the successor kernels: 5 waves per SIMD (96 VGPRs, no
-// spills; the LDS board allows 5.5); left alone the row loop takes ~109
-constexpr int kSuccWaves = 5;
+// register budget of the successor kernels, by index type: the 32-bit row
+// arithmetic fits 6 waves per SIMD (80 VGPRs, no spills; the LDS boards of
+// 24 workgroups fill a CU's 160 KB), the 64-bit one 5 (96 VGPRs; at 80 it
+// spills); left alone the row loop takes ~109
+template <typename Ix>
+constexpr int kSuccWaves = sizeof(Ix) == 4 ? 6 : 5;
 
 // Row blocks of R rows: lane group q of the grid takes blocks q,
 // q + 2 * gridDim.x, ... one row after another, as one stream (a root's
@@ -238,7 +241,7 @@ inline bool successor_narrow(int64_t rows_cap, int64_t num_roots) {
 // fnn_successor_features_kernel (game_logic.cu:182-229): kSuccRows (root, move)
 // rows per lane group, two groups per wave, the grid striding over the rows.
 template <typename Ix>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kSuccWaves))) void k_successor_features(const uint8_t* __restrict__ states,
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kSuccWaves<Ix>))) void k_successor_features(const uint8_t* __restrict__ states,
                                                            const uint8_t* __restrict__ legal,
                                                            const int64_t* __restrict__ a2r,
                                                            const int64_t* __restrict__ midx, int64_t N,
@@ -648,7 +651,7 @@ __global__ __launch_bounds__(256) void k_rows_plan(const int32_t* __restrict__ n
 }
 
 template <typename Ix>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kSuccWaves))) void k_successor_rows(const uint8_t* __restrict__ states,
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kSuccWaves<Ix>))) void k_successor_rows(const uint8_t* __restrict__ states,
                                                        const uint8_t* __restrict__ legal,
                                                        const int64_t* __restrict__ a2r,
                                                        const int64_t* __restrict__ midx,
