@@ -515,15 +515,23 @@ __global__ void k_random_play_step(uint8_t* __restrict__ states, const uint8_t* 
 // Philox-chosen slot (list_slot; the list itself is never written out) and
 // applies it to the LDS board, writing the bytes that changed into the
 // game's state row (apply_mirrored).  The workgroup moves on when both
-// games have stopped (ply >= target or a result).  Same choices, same rows
-// and counts as the per-ply launches; `moves` is not used.
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(6))) void k_random_play(
+// games have stopped (ply >= target or a result): games run for different
+// numbers of plies, so after its first pair a workgroup takes the next
+// unstarted pair from a device counter (*pair_ctr, zero at launch; one
+// atomic per pair), and the grid ends together instead of with the
+// workgroups that were dealt a second pair.  Same choices, same rows and
+// counts as the per-ply launches, whichever workgroup plays a game.
+// Register budget: 5 waves per SIMD (96 VGPRs); at 6 the spills cost more
+// than the extra wave.
+__global__ void k_zero_u32(uint32_t* __restrict__ p) { *p = 0u; }
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(5))) void k_random_play(
     uint8_t* __restrict__ states, int64_t B, int max_ply, int lockstep, uint32_t seed,
-    int32_t* __restrict__ plies_done) {
+    int32_t* __restrict__ plies_done, uint32_t* __restrict__ pair_ctr) {
     __shared__ Pos PS[kPosPerWave];
+    __shared__ int64_t next_first;
     const int grp = threadIdx.x >> 5, l = threadIdx.x & 31;
     Pos& P = PS[grp];
-    for (int64_t first = (int64_t)blockIdx.x * kPosPerWave; first < B; first += (int64_t)gridDim.x * kPosPerWave) {
+    for (int64_t first = (int64_t)blockIdx.x * kPosPerWave; first < B;) {
         const int64_t i = first + grp;
         const bool live = i < B;
         const int64_t g = live ? i : B - 1;  // a group past the end mirrors the last game and writes nothing
@@ -557,6 +565,10 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(6))) void k_
         }
         if (live && l == 0 && plies_done) plies_done[g] += done;
         __syncthreads();  // the board's last reads before the next games load
+        // the next pair: the grid's first pairs were dealt by block index
+        if (threadIdx.x == 0) next_first = ((int64_t)gridDim.x + (int64_t)atomicAdd(pair_ctr, 1u)) * kPosPerWave;
+        __syncthreads();
+        first = next_first;
     }
 }
 
@@ -846,8 +858,12 @@ int hg_random_play(uint8_t* states, uint8_t* moves, int64_t B, int max_ply, int 
     if (e != hipSuccess) return (int)e;
     const int64_t pairs = (B + kPosPerWave - 1) / kPosPerWave;
     const int64_t resident = (int64_t)(cus > 0 ? cus : 1) * (per_cu > 0 ? per_cu : 1);
+    // the pair counter in the scratch (its first 4-byte aligned word; the
+    // scratch holds at least 1,536 bytes), zeroed by a kernel
+    uint32_t* ctr = reinterpret_cast<uint32_t*>(((uintptr_t)moves + 3) & ~(uintptr_t)3);
+    hipLaunchKernelGGL(k_zero_u32, dim3(1), dim3(1), 0, (hipStream_t)stream, ctr);
     hipLaunchKernelGGL(k_random_play, dim3((unsigned)(pairs < resident ? pairs : resident)), dim3(64), 0,
-                       (hipStream_t)stream, states, B, max_ply, lockstep, seed, plies_done);
+                       (hipStream_t)stream, states, B, max_ply, lockstep, seed, plies_done, ctr);
     return finish();
 }
 

@@ -258,7 +258,10 @@ int hg_random_play_step(uint8_t* states, const uint8_t* moves, const int32_t* nu
  * lists of hg_generate_legal_moves) in one launch, every game's board held in
  * LDS from its first ply to its last (the state rows receive each ply's
  * changed bytes): the same states and plies_done.  moves: scratch of
- * B * 256 * 6 bytes, required; its contents afterwards are unspecified.  No
+ * B * 256 * 6 bytes, required (its first aligned 4-byte word holds the
+ * launch's counter of game pairs handed out; calls that share a scratch
+ * buffer on different streams race); its contents afterwards are
+ * unspecified.  No
  * reference counterpart (the generator of the benchmark configurations, as
  * hg_random_play_step). */
 int hg_random_play(uint8_t* states, uint8_t* moves, int64_t B, int max_ply, int lockstep, uint32_t seed,

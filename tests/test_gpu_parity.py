@@ -347,3 +347,26 @@ def test_random_play_one_launch_equals_per_ply(B, mask, P, lockstep):
     a = random_positions(B, mask, P, 0x5EED + 9, lockstep=lockstep, per_ply=False)
     b = random_positions(B, mask, P, 0x5EED + 9, lockstep=lockstep, per_ply=True)
     assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+
+
+def test_random_play_pair_counter_scratch(ext):
+    """hg_random_play with more game pairs than the device holds at once
+    (12,001 games: workgroups take the pairs beyond their first from the
+    counter kept in the scratch), on a scratch pointer one byte past an
+    aligned address, reused by a second, smaller call: the rows and ply
+    counts of the per-ply launches both times."""
+    import ctypes
+    from hive_neuralnet_amd.hive_gpu import random_positions
+    lib = ext._lib
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    scratch = torch.empty((12001 * 256 * 6 + 8,), dtype=torch.uint8, device="cuda")
+    for B, P, lockstep in ((12001, 60, False), (999, 40, True)):
+        seed = 0xC0DE + B
+        want_states, want_plies = random_positions(B, 0, P, seed, lockstep=lockstep, per_ply=True)
+        st = ext.create_initial_states(B, 0)
+        plies = torch.zeros((B,), dtype=torch.int32, device="cuda")
+        rc = lib.hg_random_play(st.data_ptr(), scratch.data_ptr() + 1, B, P, 1 if lockstep else 0, seed,
+                                plies.data_ptr(), stream)
+        assert rc == 0
+        torch.cuda.synchronize()
+        assert torch.equal(st, want_states) and torch.equal(plies, want_plies)
