@@ -25,8 +25,8 @@ __device__ __forceinline__ int clamp_legal(int n) { return n < 0 ? 0 : (n > kMax
 // Block b of the one-launch plan (256 threads) owns leaves [256 b, 256 b +
 // 256): it adds up the clamped counts before its range itself (at most
 // kPlanLeaves reads from L2, four counts per load when the counts are 16-byte
-// aligned), scans its own counts and writes their offsets; then each thread
-// writes its own leaf's rows (stores only: no thread waits on another's).
+// aligned), scans its own counts and writes their offsets; then each wave
+// writes its leaves' rows (stores only: no wave waits on another's).
 // Sums stay below kPlanLeaves * 256 (int).
 __device__ __forceinline__ int clamp4_sum(int4 v) {
     return clamp_legal(v.x) + clamp_legal(v.y) + clamp_legal(v.z) + clamp_legal(v.w);
@@ -57,9 +57,16 @@ __device__ __forceinline__ void rows_plan_block(const int32_t* __restrict__ nleg
     for (int k = 0; k < w; k++) off += tot_w[k];
     if (t < T) offsets[t] = off;
     if (tid == 255 && lo + 256 >= T) *total = (int64_t)off + v;  // the block holding leaf T - 1
-    for (int k = 0; k < v; k++) {
-        a2r[off + k] = t;
-        mi[off + k] = k;
+    // each wave writes its 64 leaves' rows one leaf at a time, the lanes over
+    // the leaf's slots (stores of consecutive rows, not one row per lane of
+    // 64 different leaves)
+    for (int k = 0; k < 64; k++) {
+        const int vk = __builtin_amdgcn_readlane(v, k), ok = __builtin_amdgcn_readlane(off, k);
+        const int64_t tk = (int64_t)lo + 64 * w + k;
+        for (int m = lane; m < vk; m += 64) {
+            a2r[ok + m] = tk;
+            mi[ok + m] = m;
+        }
     }
 }
 
